@@ -1,0 +1,150 @@
+"""``torch.autograd.Function`` wrappers over the ``cuda_transformer`` operators.
+
+Same classes, ``apply`` signatures and saved tensors as the reference's cuda_autograd_fns/
+(cuda_flash_attention.py:4-17, cuda_linear_layer.py:4-28, cuda_gelu_layer.py:4-14,
+cuda_softmax_layer.py:4-15, cuda_causal_self_attention.py:4-35), plus ``CudaLayerNorm``.
+
+Deviations, each a fix:
+
+* ``CudaCausalSelfAttention.backward`` scales dq and dk by 1/sqrt(hs).  The reference scales
+  dk and dv (cuda_causal_self_attention.py:34), which gives wrong dq and dv; its own test
+  scales dq and dk (test/test_causal_self_attn.py:67).
+* ``CudaLinearLayer.backward`` allocates its zero bias on dy's device instead of the
+  hard-coded 'cuda' device, and computes dW as one GEMM over the flattened (batch*m) axis
+  instead of a per-batch GEMM followed by ``torch.sum(dim=0)`` (same sum, fewer bytes).
+"""
+import torch
+
+from .ops import (
+    causal_self_attention_bwd, causal_self_attention_fwd, cuda_fma, cuda_softmax,
+    cuda_softmax_bwd, db_calculation, flash_attention_bwd, flash_attention_fwd, gelu_activation,
+    gelu_activation_bwd, layernorm_bwd, layernorm_fwd,
+)
+
+__all__ = [
+    "CudaCausalSelfAttention", "CudaFlashAttention", "CudaGeluLayer", "CudaLinearLayer",
+    "CudaSoftmaxLayer", "CudaLayerNorm",
+]
+
+
+class CudaFlashAttention(torch.autograd.Function):
+    """(q, k, v, causal) -> (o, l); backward ignores grad_l (cuda_flash_attention.py:4-17)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, causal):
+        o, l = flash_attention_fwd(q, k, v, causal)
+        ctx.save_for_backward(q, k, v, o, l)
+        ctx.causal = causal
+        return o, l
+
+    @staticmethod
+    def backward(ctx, grad_output, grad_l=None):
+        q, k, v, o, l = ctx.saved_tensors
+        dq, dk, dv = flash_attention_bwd(q, k, v, o, grad_output, l, ctx.causal)
+        return dq, dk, dv, None
+
+
+class CudaLinearLayer(torch.autograd.Function):
+    """(x, weights (k, n) or (b, k, n), bias (n)) -> x @ W + b (cuda_linear_layer.py:4-28)."""
+
+    @staticmethod
+    def forward(ctx, x, weights, bias):
+        out = cuda_fma(x, weights, bias)
+        ctx.save_for_backward(x, weights, bias, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x, weights, _, _ = ctx.saved_tensors
+        dy = grad_output
+        w = weights.unsqueeze(0) if weights.dim() == 2 else weights
+        k, n = x.shape[-1], dy.shape[-1]
+        dx = cuda_fma(dy, w.transpose(1, 2), torch.zeros(k, dtype=dy.dtype, device=dy.device))
+        zero_n = torch.zeros(n, dtype=dy.dtype, device=dy.device)
+        if weights.dim() == 2:
+            # sum_b x[b]^T dy[b] == (x as (b*m, k))^T (dy as (b*m, n)): one GEMM, K = b*m
+            x2 = x.reshape(1, -1, k)
+            dy2 = dy.reshape(1, -1, n)
+            dw = cuda_fma(x2.transpose(1, 2), dy2, zero_n)[0]
+        else:
+            dw = cuda_fma(x.transpose(1, 2), dy, zero_n)
+        db = db_calculation(dy)
+        return dx, dw, db
+
+
+class CudaGeluLayer(torch.autograd.Function):
+    """Exact GELU (cuda_gelu_layer.py:4-14)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        out = gelu_activation(x)
+        ctx.save_for_backward(x)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (x,) = ctx.saved_tensors
+        return gelu_activation_bwd(x, grad_output.contiguous())
+
+
+class CudaSoftmaxLayer(torch.autograd.Function):
+    """Row softmax over the last dim of a 3-D tensor (cuda_softmax_layer.py:4-15)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        out = cuda_softmax(x)
+        ctx.save_for_backward(out)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (out,) = ctx.saved_tensors
+        return cuda_softmax_bwd(out, grad_output.contiguous())
+
+
+class CudaCausalSelfAttention(torch.autograd.Function):
+    """Materialised attention over packed qkv (cuda_causal_self_attention.py:4-35)."""
+
+    @staticmethod
+    def forward(ctx, qkv, nh, causal):
+        out, probs = causal_self_attention_fwd(qkv, nh, causal)
+        ctx.save_for_backward(qkv, probs)
+        ctx.nh = nh
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        qkv, probs = ctx.saved_tensors
+        nh = ctx.nh
+        q, k, v = qkv.chunk(3, dim=-1)
+        B, T, C = q.shape
+        hs = C // nh
+
+        def heads(t):
+            return t.reshape(B, T, nh, hs).transpose(1, 2).reshape(B * nh, T, hs)
+
+        def unheads(t):
+            return t.reshape(B, nh, T, hs).transpose(1, 2).reshape(B, T, C)
+
+        dq, dk, dv = causal_self_attention_bwd(
+            heads(q), heads(k), heads(v), probs.reshape(B * nh, T, T),
+            heads(grad_output.contiguous()))
+        sm_scale = hs ** 0.5
+        grads = torch.cat([unheads(dq) / sm_scale, unheads(dk) / sm_scale, unheads(dv)], dim=-1)
+        return grads, None, None
+
+
+class CudaLayerNorm(torch.autograd.Function):
+    """LayerNorm over the last dim: (x, gamma, beta, eps) -> y (semantics of gpt.py:47-59)."""
+
+    @staticmethod
+    def forward(ctx, x, gamma, beta, eps=1e-5):
+        y, mean, rstd = layernorm_fwd(x, gamma, beta, eps)
+        ctx.save_for_backward(x, gamma, mean, rstd)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x, gamma, mean, rstd = ctx.saved_tensors
+        dx, dgamma, dbeta = layernorm_bwd(x, gamma, mean, rstd, grad_output.contiguous())
+        return dx, dgamma.reshape(gamma.shape), dbeta.reshape(gamma.shape), None

@@ -1,0 +1,76 @@
+// Shared device helpers and host-side error plumbing for the gfx950 kernels.
+//
+// Every kernel in this library is written for CDNA4 (gfx950): wave64, FP32 MFMA
+// (v_mfma_f32_32x32x2_f32), LDS tiles with padded pitches.  The lane layout of the
+// 32x32x2 MFMA that all attention / GEMM kernels rely on (checked on an MI355X):
+//   A operand (32 x 2):  lane l supplies A[l % 32][l / 32]
+//   B operand (2 x 32):  lane l supplies B[l / 32][l % 32]
+//   D (32 x 32, 16 regs): lane l, register r holds D[R(r, l/32)][l % 32]
+//                         with R(r, h) = 8*(r/4) + 4*h + (r%4)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cmath>
+#include <string>
+
+#include "../../include/cuda_transformer_amd.h"
+
+namespace cta {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Row index inside a 32x32 MFMA output tile held by register r of a lane in half h.
+__device__ __forceinline__ constexpr int mfma_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+__device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+  return z;
+}
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+// Exchange with the lane 32 positions away (the other half of the wave).
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+// 2^x on the hardware transcendental unit (v_exp_f32). Inputs here are <= 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ----------------------------------------------------------------------------------
+// Host-side helpers shared by the C-ABI entry points.
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Attention operands: unit d-stride, (b, h, t) strides divisible by 4, 16-byte aligned base.
+bool attn_layout_ok(const float* p, const int64_t* s);
+// Validates (B, nh, T, hs) for the attention entry points; sets the error message on failure.
+int check_attn_sizes(int64_t B, int64_t nh, int64_t T, int64_t hs);
+
+}  // namespace cta

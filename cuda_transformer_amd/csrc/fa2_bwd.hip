@@ -1,0 +1,572 @@
+// FlashAttention-2 backward, FP32, CDNA4 MFMA: three atomics-free stages.
+//
+// Semantics follow Transformer_kernels/flash_attention.cuh:175-504:
+//   delta_i = sum_d O_id dO_id                                   (:175-213)
+//   P_ij = e^{S_ij - L_i},  dP_ij = dO_i . v_j,  dS_ij = P_ij (dP_ij - delta_i)
+//   dQ_i = s * sum_j dS_ij k_j                                   (:216-354)
+//   dV_j = sum_i P_ij dO_i,  dK_j = s * sum_i dS_ij q_i          (:357-504)
+// with S = s q.k, s = 1/sqrt(hs), and the causal mask j > i.  Each output row is owned by
+// exactly one lane, so there are no atomics and results are deterministic.
+//
+// gfx950 design (same MFMA layout trick as the forward kernel):
+//  * dQ stage: a wave owns 32 query rows and keeps q, dO, L and delta of its rows in
+//    registers.  It computes S^T = K Q^T and dP^T = V dO^T (one query row per lane), forms
+//    dS^T in registers and feeds it straight into dQ^T += K^T dS^T.
+//  * dK/dV stage: a wave owns 32 key rows and keeps k and v in registers.  It computes
+//    S = Q K^T and dP = dO V^T (one key row per lane) and feeds P and dS straight into
+//    dV^T += dO^T P and dK^T += Q^T dS.  Unlike the reference, causal tiles above the
+//    diagonal are skipped here too (the reference computes kvEnd but never uses it).
+//  * Tiles of the streamed operand (K,V for dQ; Q,dO,L,delta for dK/dV) go
+//    global -> registers -> LDS, double buffered, one barrier per tile.
+#include "cta_common.hpp"
+
+namespace cta {
+namespace {
+
+struct RowStrides {
+  int64_t b, h, t;
+};
+struct LStrides {
+  int64_t b, h, t;
+};
+
+// ------------------------------------------------------------------------------------
+// Stage 1: delta.  G = hs/4 lanes share one row (one float4 each).
+template <int HS>
+__global__ __launch_bounds__(256) void fa2_bwd_delta_kernel(const float* __restrict__ O,
+                                                            const float* __restrict__ dO,
+                                                            float* __restrict__ delta, int nh,
+                                                            int T, int64_t rows, RowStrides so,
+                                                            RowStrides sdo) {
+  constexpr int G = HS / 4;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / G;
+  const int c4 = (int)(gid % G);
+  float acc = 0.0f;
+  if (row < rows) {
+    const int64_t bh = row / T;
+    const int t = (int)(row - bh * T);
+    const int64_t b = bh / nh, h = bh - b * nh;
+    const float4 o = ld4(O + b * so.b + h * so.h + (int64_t)t * so.t + 4 * c4);
+    const float4 g = ld4(dO + b * sdo.b + h * sdo.h + (int64_t)t * sdo.t + 4 * c4);
+    acc = o.x * g.x + o.y * g.y + o.z * g.z + o.w * g.w;
+  }
+#pragma unroll
+  for (int off = G / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+  if (row < rows && c4 == 0) delta[row] = acc;
+}
+
+template <int HS>
+struct BwdTile;
+template <> struct BwdTile<32> { static constexpr int BN = 64; static constexpr int MINW = 2; };
+template <> struct BwdTile<64> { static constexpr int BN = 64; static constexpr int MINW = 2; };
+template <> struct BwdTile<128> { static constexpr int BN = 32; static constexpr int MINW = 1; };
+
+// The dK/dV stage keeps k, v and two accumulator sets per lane, so it streams narrower tiles.
+template <int HS>
+struct DkdvTile;
+template <> struct DkdvTile<32> { static constexpr int BN = 64; static constexpr int MINW = 2; };
+template <> struct DkdvTile<64> { static constexpr int BN = 32; static constexpr int MINW = 2; };
+template <> struct DkdvTile<128> { static constexpr int BN = 32; static constexpr int MINW = 1; };
+
+// ------------------------------------------------------------------------------------
+// Stage 2: dQ.  Workgroup = 128 query rows; K/V tiles streamed through LDS.
+template <int HS, bool CAUSAL>
+__global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
+    float* __restrict__ dQ, int nh, int T, int BH, int n_qtiles, RowStrides sq, RowStrides sk,
+    RowStrides sv, RowStrides sdo, LStrides sl, float scale, float scale_log2) {
+  constexpr int BN = BwdTile<HS>::BN;
+  constexpr int BM = 128;
+  constexpr int H2 = HS / 2;
+  constexpr int KP = HS + 4;  // both K and V rows are read as 16-byte row segments
+  constexpr int TILE = BN * KP;
+  constexpr int F4_ROW = HS / 4;
+  constexpr int LOADS = BN * F4_ROW / 256;
+  static_assert(BN * F4_ROW % 256 == 0, "tile must split evenly over 256 threads");
+  __shared__ __attribute__((aligned(16))) float smem[2 * 2 * TILE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, col = lane & 31;
+  const int id = blockIdx.x;
+  const int bh = id % BH;
+  const int qt = CAUSAL ? (n_qtiles - 1 - id / BH) : (id / BH);
+  const int b = bh / nh, h = bh - b * nh;
+
+  const float* Kb = K + b * sk.b + h * sk.h;
+  const float* Vb = V + b * sv.b + h * sv.h;
+
+  const int i0 = qt * BM + wave * 32;
+  const int my_i = i0 + col;
+
+  float qf[H2], dof[H2];
+  float l2 = 0.0f, dl = 0.0f;  // L_i * log2(e) and delta_i of this lane's row
+  if (my_i < T) {
+    const float* qp = Q + b * sq.b + h * sq.h + (int64_t)my_i * sq.t + half * H2;
+    const float* gp = dO + b * sdo.b + h * sdo.h + (int64_t)my_i * sdo.t + half * H2;
+#pragma unroll
+    for (int c = 0; c < H2 / 4; ++c) {
+      const float4 x = ld4(qp + 4 * c);
+      const float4 g = ld4(gp + 4 * c);
+      qf[4 * c + 0] = x.x; qf[4 * c + 1] = x.y; qf[4 * c + 2] = x.z; qf[4 * c + 3] = x.w;
+      dof[4 * c + 0] = g.x; dof[4 * c + 1] = g.y; dof[4 * c + 2] = g.z; dof[4 * c + 3] = g.w;
+    }
+    l2 = Lg[b * sl.b + h * sl.h + (int64_t)my_i * sl.t] * kLog2e;
+    dl = delta[(int64_t)bh * T + my_i];
+  } else {
+#pragma unroll
+    for (int c = 0; c < H2; ++c) { qf[c] = 0.0f; dof[c] = 0.0f; }
+  }
+
+  f32x16 dqacc[HS / 32];
+#pragma unroll
+  for (int d = 0; d < HS / 32; ++d) dqacc[d] = zero16();
+
+  const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
+  const int n_stages = (kv_end + BN - 1) / BN;
+
+  float4 kst[LOADS], vst[LOADS];
+  auto gload = [&](int stage) {
+    const int j0 = stage * BN;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int f = tid + 256 * u;
+      const int r = f / F4_ROW, c4 = f % F4_ROW;
+      const int j = j0 + r;
+      if (j < T) {
+        kst[u] = ld4(Kb + (int64_t)j * sk.t + 4 * c4);
+        vst[u] = ld4(Vb + (int64_t)j * sv.t + 4 * c4);
+      } else {
+        kst[u] = zero4();
+        vst[u] = zero4();
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+    float* ks = smem + buf * 2 * TILE;
+    float* vs = ks + TILE;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int f = tid + 256 * u;
+      const int r = f / F4_ROW, c4 = f % F4_ROW;
+      st4(ks + r * KP + 4 * c4, kst[u]);
+      st4(vs + r * KP + 4 * c4, vst[u]);
+    }
+  };
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+
+  for (int s = 0; s < n_stages; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < n_stages) gload(s + 1);
+    const float* ks = smem + buf * 2 * TILE;
+    const float* vs = ks + TILE;
+
+#pragma unroll
+    for (int sub = 0; sub < BN / 32; ++sub) {
+      const int jj0 = s * BN + sub * 32;
+      if (jj0 >= T) continue;
+      if (CAUSAL && jj0 > i0 + 31) continue;
+
+      f32x16 sacc = zero16(), pacc = zero16();
+      const float* krow = ks + (sub * 32 + col) * KP + half * H2;
+      const float* vrow = vs + (sub * 32 + col) * KP + half * H2;
+#pragma unroll
+      for (int c = 0; c < H2 / 4; ++c) {
+        const float4 kv = ld4(krow + 4 * c);
+        const float4 vv = ld4(vrow + 4 * c);
+        sacc = mfma32(kv.x, qf[4 * c + 0], sacc);
+        pacc = mfma32(vv.x, dof[4 * c + 0], pacc);
+        sacc = mfma32(kv.y, qf[4 * c + 1], sacc);
+        pacc = mfma32(vv.y, dof[4 * c + 1], pacc);
+        sacc = mfma32(kv.z, qf[4 * c + 2], sacc);
+        pacc = mfma32(vv.z, dof[4 * c + 2], pacc);
+        sacc = mfma32(kv.w, qf[4 * c + 3], sacc);
+        pacc = mfma32(vv.w, dof[4 * c + 3], pacc);
+      }
+
+      const bool need_mask = (CAUSAL && jj0 + 31 > i0) || (jj0 + 32 > T);
+      // dS^T (overwrites sacc): P (dP - delta), masked entries give exactly 0.
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = fast_exp2(fmaf(sacc[r], scale_log2, -l2));
+        if (need_mask) {
+          const int j = jj0 + mfma_row(r, half);
+          if ((CAUSAL && j > my_i) || j >= T) p = 0.0f;
+        }
+        sacc[r] = p * (pacc[r] - dl);
+      }
+
+#pragma unroll
+      for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+          const float a = ks[(sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col];
+          dqacc[d] = mfma32(a, sacc[kk], dqacc[d]);
+        }
+      }
+    }
+
+    if (s + 1 < n_stages) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (my_i < T) {
+    float* op = dQ + ((int64_t)bh * T + my_i) * HS;
+#pragma unroll
+    for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dc = d * 32 + 8 * g + 4 * half;
+        st4(op + dc, make_float4(dqacc[d][4 * g + 0] * scale, dqacc[d][4 * g + 1] * scale,
+                                 dqacc[d][4 * g + 2] * scale, dqacc[d][4 * g + 3] * scale));
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Stage 3: dK, dV.  Workgroup = 128 key rows; Q/dO/L/delta tiles streamed through LDS.
+template <int HS, bool CAUSAL>
+__global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
+    float* __restrict__ dK, float* __restrict__ dV, int nh, int T, int BH, int n_ktiles,
+    RowStrides sq, RowStrides sk, RowStrides sv, RowStrides sdo, LStrides sl, float scale,
+    float scale_log2) {
+  constexpr int BN = DkdvTile<HS>::BN;
+  constexpr int BM = 128;
+  constexpr int H2 = HS / 2;
+  constexpr int KP = HS + 4;
+  constexpr int TILE = BN * KP;
+  constexpr int STAGE = 2 * TILE + 2 * BN;  // Q tile, dO tile, L*log2e, delta
+  constexpr int F4_ROW = HS / 4;
+  constexpr int LOADS = BN * F4_ROW / 256;
+  static_assert(BN * F4_ROW % 256 == 0, "tile must split evenly over 256 threads");
+  __shared__ __attribute__((aligned(16))) float smem[2 * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, col = lane & 31;
+  const int id = blockIdx.x;
+  const int bh = id % BH;
+  const int kt = id / BH;  // causal: low key tiles have the most work and go first
+  const int b = bh / nh, h = bh - b * nh;
+
+  const float* Qb = Q + b * sq.b + h * sq.h;
+  const float* dOb = dO + b * sdo.b + h * sdo.h;
+  const float* Lb = Lg + b * sl.b + h * sl.h;
+  const float* Db = delta + (int64_t)bh * T;
+
+  const int j0 = kt * BM + wave * 32;  // first key row of this wave
+  const int my_j = j0 + col;
+
+  float kf[H2], vf[H2];
+  if (my_j < T) {
+    const float* kp = K + b * sk.b + h * sk.h + (int64_t)my_j * sk.t + half * H2;
+    const float* vp = V + b * sv.b + h * sv.h + (int64_t)my_j * sv.t + half * H2;
+#pragma unroll
+    for (int c = 0; c < H2 / 4; ++c) {
+      const float4 x = ld4(kp + 4 * c);
+      const float4 y = ld4(vp + 4 * c);
+      kf[4 * c + 0] = x.x; kf[4 * c + 1] = x.y; kf[4 * c + 2] = x.z; kf[4 * c + 3] = x.w;
+      vf[4 * c + 0] = y.x; vf[4 * c + 1] = y.y; vf[4 * c + 2] = y.z; vf[4 * c + 3] = y.w;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < H2; ++c) { kf[c] = 0.0f; vf[c] = 0.0f; }
+  }
+
+  f32x16 dkacc[HS / 32], dvacc[HS / 32];
+#pragma unroll
+  for (int d = 0; d < HS / 32; ++d) { dkacc[d] = zero16(); dvacc[d] = zero16(); }
+
+  const int q_begin = CAUSAL ? (kt * BM / BN) : 0;  // first query stage that can see these keys
+  const int n_stages_total = (T + BN - 1) / BN;
+
+  float4 qst[LOADS], gst[LOADS];
+  float lst = 0.0f, dst = 0.0f;
+  auto gload = [&](int stage) {
+    const int r0 = stage * BN;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int f = tid + 256 * u;
+      const int r = f / F4_ROW, c4 = f % F4_ROW;
+      const int i = r0 + r;
+      if (i < T) {
+        qst[u] = ld4(Qb + (int64_t)i * sq.t + 4 * c4);
+        gst[u] = ld4(dOb + (int64_t)i * sdo.t + 4 * c4);
+      } else {
+        qst[u] = zero4();
+        gst[u] = zero4();
+      }
+    }
+    if (tid < BN) {
+      const int i = r0 + tid;
+      lst = (i < T) ? Lb[(int64_t)i * sl.t] * kLog2e : 0.0f;
+      dst = (i < T) ? Db[i] : 0.0f;
+    }
+  };
+  auto lstore = [&](int buf) {
+    float* qs = smem + buf * STAGE;
+    float* gs = qs + TILE;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int f = tid + 256 * u;
+      const int r = f / F4_ROW, c4 = f % F4_ROW;
+      st4(qs + r * KP + 4 * c4, qst[u]);
+      st4(gs + r * KP + 4 * c4, gst[u]);
+    }
+    if (tid < BN) {
+      qs[2 * TILE + tid] = lst;
+      qs[2 * TILE + BN + tid] = dst;
+    }
+  };
+
+  if (q_begin < n_stages_total) {
+    gload(q_begin);
+    lstore(0);
+  }
+  __syncthreads();
+
+  for (int s = q_begin; s < n_stages_total; ++s) {
+    const int buf = (s - q_begin) & 1;
+    if (s + 1 < n_stages_total) gload(s + 1);
+    const float* qs = smem + buf * STAGE;
+    const float* gs = qs + TILE;
+    const float* ls = qs + 2 * TILE;
+    const float* ds = ls + BN;
+
+#pragma unroll
+    for (int sub = 0; sub < BN / 32; ++sub) {
+      const int ii0 = s * BN + sub * 32;
+      if (ii0 >= T) continue;
+      if (CAUSAL && ii0 + 31 < j0) continue;  // every query row here precedes every key row
+
+      // S and dP tiles: lane holds column my_j, rows ii0 + R(r, half)
+      f32x16 sacc = zero16(), pacc = zero16();
+      const float* qrow = qs + (sub * 32 + col) * KP + half * H2;
+      const float* grow = gs + (sub * 32 + col) * KP + half * H2;
+#pragma unroll
+      for (int c = 0; c < H2 / 4; ++c) {
+        const float4 qv = ld4(qrow + 4 * c);
+        const float4 gv = ld4(grow + 4 * c);
+        sacc = mfma32(qv.x, kf[4 * c + 0], sacc);
+        pacc = mfma32(gv.x, vf[4 * c + 0], pacc);
+        sacc = mfma32(qv.y, kf[4 * c + 1], sacc);
+        pacc = mfma32(gv.y, vf[4 * c + 1], pacc);
+        sacc = mfma32(qv.z, kf[4 * c + 2], sacc);
+        pacc = mfma32(gv.z, vf[4 * c + 2], pacc);
+        sacc = mfma32(qv.w, kf[4 * c + 3], sacc);
+        pacc = mfma32(gv.w, vf[4 * c + 3], pacc);
+      }
+
+      const bool need_mask = (CAUSAL && ii0 < j0 + 31) || (ii0 + 32 > T);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 lv = ld4(ls + sub * 32 + 8 * g + 4 * half);
+        const float4 dv = ld4(ds + sub * 32 + 8 * g + 4 * half);
+        const float lr[4] = {lv.x, lv.y, lv.z, lv.w};
+        const float dr[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          float p = fast_exp2(fmaf(sacc[r], scale_log2, -lr[e]));
+          if (need_mask) {
+            const int i = ii0 + 8 * g + 4 * half + e;
+            if ((CAUSAL && my_j > i) || i >= T) p = 0.0f;
+          }
+          sacc[r] = p;                       // P
+          pacc[r] = p * (pacc[r] - dr[e]);   // dS
+        }
+      }
+
+#pragma unroll
+      for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+          const int rrow = (sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col;
+          dvacc[d] = mfma32(gs[rrow], sacc[kk], dvacc[d]);
+          dkacc[d] = mfma32(qs[rrow], pacc[kk], dkacc[d]);
+        }
+      }
+    }
+
+    if (s + 1 < n_stages_total) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (my_j < T) {
+    float* kp = dK + ((int64_t)bh * T + my_j) * HS;
+    float* vp = dV + ((int64_t)bh * T + my_j) * HS;
+#pragma unroll
+    for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dc = d * 32 + 8 * g + 4 * half;
+        st4(kp + dc, make_float4(dkacc[d][4 * g + 0] * scale, dkacc[d][4 * g + 1] * scale,
+                                 dkacc[d][4 * g + 2] * scale, dkacc[d][4 * g + 3] * scale));
+        st4(vp + dc, make_float4(dvacc[d][4 * g + 0], dvacc[d][4 * g + 1], dvacc[d][4 * g + 2],
+                                 dvacc[d][4 * g + 3]));
+      }
+    }
+  }
+}
+
+RowStrides rs(const int64_t* s) { return RowStrides{s[0], s[1], s[2]}; }
+
+template <int HS>
+void launch_delta(const float* o, const float* d_o, float* delta, int nh, int T, int64_t rows,
+                  RowStrides so, RowStrides sdo, hipStream_t st) {
+  const int64_t threads = rows * (HS / 4);
+  const unsigned grid = (unsigned)((threads + 255) / 256);
+  hipLaunchKernelGGL((fa2_bwd_delta_kernel<HS>), dim3(grid), dim3(256), 0, st, o, d_o, delta, nh,
+                     T, rows, so, sdo);
+}
+
+template <int HS, bool CAUSAL>
+void launch_dq(const float* q, const float* k, const float* v, const float* d_o, const float* l,
+               const float* delta, float* dq, int nh, int T, int BH, RowStrides sq,
+               RowStrides sk, RowStrides sv, RowStrides sdo, LStrides sl, float scale,
+               hipStream_t st) {
+  const int n_qtiles = (T + 127) / 128;
+  hipLaunchKernelGGL((fa2_bwd_dq_kernel<HS, CAUSAL>), dim3((unsigned)n_qtiles * BH), dim3(256), 0,
+                     st, q, k, v, d_o, l, delta, dq, nh, T, BH, n_qtiles, sq, sk, sv, sdo, sl,
+                     scale, scale * kLog2e);
+}
+
+template <int HS, bool CAUSAL>
+void launch_dkdv(const float* q, const float* k, const float* v, const float* d_o,
+                 const float* l, const float* delta, float* dk, float* dv, int nh, int T, int BH,
+                 RowStrides sq, RowStrides sk, RowStrides sv, RowStrides sdo, LStrides sl,
+                 float scale, hipStream_t st) {
+  const int n_ktiles = (T + 127) / 128;
+  hipLaunchKernelGGL((fa2_bwd_dkdv_kernel<HS, CAUSAL>), dim3((unsigned)n_ktiles * BH), dim3(256),
+                     0, st, q, k, v, d_o, l, delta, dk, dv, nh, T, BH, n_ktiles, sq, sk, sv, sdo,
+                     sl, scale, scale * kLog2e);
+}
+
+bool l_ok(const float* l, const int64_t* s) { return l != nullptr && s != nullptr; }
+
+}  // namespace
+}  // namespace cta
+
+using namespace cta;
+
+extern "C" int cta_flash_attention_bwd_delta(const float* o, const int64_t* o_strides,
+                                             const float* d_o, const int64_t* do_strides,
+                                             int64_t B, int64_t nh, int64_t T, int64_t hs,
+                                             float* delta, void* stream) {
+  if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
+  if (B * nh * T == 0) return CTA_OK;
+  if (!delta) return fail(CTA_ERR_INVALID_ARGUMENT, "null delta pointer");
+  if (!attn_layout_ok(o, o_strides) || !attn_layout_ok(d_o, do_strides))
+    return fail(CTA_ERR_LAYOUT,
+                "flash_attention_bwd needs unit d-stride, strides divisible by 4 and 16-byte "
+                "aligned O/dO");
+  const int64_t rows = B * nh * T;
+  hipStream_t st = as_stream(stream);
+  if (hs == 32) launch_delta<32>(o, d_o, delta, (int)nh, (int)T, rows, rs(o_strides), rs(do_strides), st);
+  else if (hs == 64) launch_delta<64>(o, d_o, delta, (int)nh, (int)T, rows, rs(o_strides), rs(do_strides), st);
+  else launch_delta<128>(o, d_o, delta, (int)nh, (int)T, rows, rs(o_strides), rs(do_strides), st);
+  return check_launch("flash_attention_bwd_delta");
+}
+
+namespace {
+int check_bwd_inputs(const float* q, const int64_t* qs, const float* k, const int64_t* ks,
+                     const float* v, const int64_t* vs, const float* d_o, const int64_t* dos,
+                     const float* l, const int64_t* ls, const float* delta) {
+  if (!attn_layout_ok(q, qs) || !attn_layout_ok(k, ks) || !attn_layout_ok(v, vs) ||
+      !attn_layout_ok(d_o, dos))
+    return fail(CTA_ERR_LAYOUT,
+                "flash_attention_bwd needs unit d-stride, strides divisible by 4 and 16-byte "
+                "aligned Q/K/V/dO");
+  if (!l_ok(l, ls) || !delta) return fail(CTA_ERR_INVALID_ARGUMENT, "null L or delta pointer");
+  return CTA_OK;
+}
+}  // namespace
+
+extern "C" int cta_flash_attention_bwd_dq(const float* q, const int64_t* q_strides,
+                                          const float* k, const int64_t* k_strides,
+                                          const float* v, const int64_t* v_strides,
+                                          const float* d_o, const int64_t* do_strides,
+                                          const float* l, const int64_t* l_strides,
+                                          const float* delta, int64_t B, int64_t nh, int64_t T,
+                                          int64_t hs, int causal, float* dq, void* stream) {
+  if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
+  if (B * nh * T == 0) return CTA_OK;
+  if (int rc = check_bwd_inputs(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l,
+                                l_strides, delta))
+    return rc;
+  if (!dq || !aligned16(dq)) return fail(CTA_ERR_LAYOUT, "dQ must be a 16-byte aligned pointer");
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
+  const int BH = (int)(B * nh);
+  hipStream_t st = as_stream(stream);
+#define CTA_DQ(HS_)                                                                           \
+  if (causal) launch_dq<HS_, true>(q, k, v, d_o, l, delta, dq, (int)nh, (int)T, BH, rs(q_strides), \
+                                   rs(k_strides), rs(v_strides), rs(do_strides), sl, scale, st); \
+  else launch_dq<HS_, false>(q, k, v, d_o, l, delta, dq, (int)nh, (int)T, BH, rs(q_strides),      \
+                             rs(k_strides), rs(v_strides), rs(do_strides), sl, scale, st);
+  if (hs == 32) { CTA_DQ(32) }
+  else if (hs == 64) { CTA_DQ(64) }
+  else { CTA_DQ(128) }
+#undef CTA_DQ
+  return check_launch("flash_attention_bwd_dq");
+}
+
+extern "C" int cta_flash_attention_bwd_dkdv(const float* q, const int64_t* q_strides,
+                                            const float* k, const int64_t* k_strides,
+                                            const float* v, const int64_t* v_strides,
+                                            const float* d_o, const int64_t* do_strides,
+                                            const float* l, const int64_t* l_strides,
+                                            const float* delta, int64_t B, int64_t nh, int64_t T,
+                                            int64_t hs, int causal, float* dk, float* dv,
+                                            void* stream) {
+  if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
+  if (B * nh * T == 0) return CTA_OK;
+  if (int rc = check_bwd_inputs(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l,
+                                l_strides, delta))
+    return rc;
+  if (!dk || !dv || !aligned16(dk) || !aligned16(dv))
+    return fail(CTA_ERR_LAYOUT, "dK/dV must be 16-byte aligned pointers");
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
+  const int BH = (int)(B * nh);
+  hipStream_t st = as_stream(stream);
+#define CTA_DKDV(HS_)                                                                          \
+  if (causal) launch_dkdv<HS_, true>(q, k, v, d_o, l, delta, dk, dv, (int)nh, (int)T, BH,       \
+                                     rs(q_strides), rs(k_strides), rs(v_strides),               \
+                                     rs(do_strides), sl, scale, st);                            \
+  else launch_dkdv<HS_, false>(q, k, v, d_o, l, delta, dk, dv, (int)nh, (int)T, BH,             \
+                               rs(q_strides), rs(k_strides), rs(v_strides), rs(do_strides), sl, \
+                               scale, st);
+  if (hs == 32) { CTA_DKDV(32) }
+  else if (hs == 64) { CTA_DKDV(64) }
+  else { CTA_DKDV(128) }
+#undef CTA_DKDV
+  return check_launch("flash_attention_bwd_dkdv");
+}
+
+extern "C" int cta_flash_attention_bwd(const float* q, const int64_t* q_strides, const float* k,
+                                       const int64_t* k_strides, const float* v,
+                                       const int64_t* v_strides, const float* o,
+                                       const int64_t* o_strides, const float* d_o,
+                                       const int64_t* do_strides, const float* l,
+                                       const int64_t* l_strides, int64_t B, int64_t nh,
+                                       int64_t T, int64_t hs, int causal, float* dq, float* dk,
+                                       float* dv, float* delta, void* stream) {
+  if (int rc = cta_flash_attention_bwd_delta(o, o_strides, d_o, do_strides, B, nh, T, hs, delta,
+                                             stream))
+    return rc;
+  if (int rc = cta_flash_attention_bwd_dq(q, q_strides, k, k_strides, v, v_strides, d_o,
+                                          do_strides, l, l_strides, delta, B, nh, T, hs, causal,
+                                          dq, stream))
+    return rc;
+  return cta_flash_attention_bwd_dkdv(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides,
+                                      l, l_strides, delta, B, nh, T, hs, causal, dk, dv, stream);
+}

@@ -1,0 +1,260 @@
+// FlashAttention-2 forward, FP32, CDNA4 MFMA.
+//
+// Semantics follow Transformer_kernels/flash_attention.cuh:27-170 (online softmax over
+// K/V tiles; O = sum_j e^{S_ij - m_i} v_j / l_i and L_i = m_i + ln l_i with S = q.k/sqrt(hs),
+// causal mask j > i, rows beyond T never written).  The algorithm is re-designed for
+// gfx950:
+//
+//  * A workgroup owns BM = 128 query rows (4 waves x 32 rows).  K/V tiles of BN rows are
+//    staged global -> registers -> LDS, double buffered, one barrier per tile.
+//  * Each wave computes S^T = K Q^T with v_mfma_f32_32x32x2_f32.  In the MFMA output layout
+//    lane l then holds 16 scores of query row (l % 32) — one row per lane — so the row max
+//    needs one in-lane max over 16 registers and one exchange with the other wave half.
+//  * O^T = V^T P^T reuses the score registers directly as the B operand: the K index of the
+//    second MFMA is permuted to match the output layout of the first, and V is read from LDS
+//    in the same permuted order.  P never leaves registers.
+//  * Exponentials use exp2 with log2(e) folded into the scale; L is exported in natural log.
+//  * Workgroup ids are mapped longest-first for causal attention (last query tile first);
+//    consecutive ids walk (batch, head) so the query tiles of one head share an XCD's L2.
+#include "cta_common.hpp"
+
+namespace cta {
+namespace {
+
+struct RowStrides {
+  int64_t b, h, t;  // element strides of the batch, head and time axes (d-stride is 1)
+};
+
+template <int HS>
+struct FwdTile;
+template <> struct FwdTile<32> { static constexpr int BN = 64; static constexpr int MINW = 2; };
+template <> struct FwdTile<64> { static constexpr int BN = 64; static constexpr int MINW = 2; };
+template <> struct FwdTile<128> { static constexpr int BN = 32; static constexpr int MINW = 1; };
+
+template <int HS, bool CAUSAL>
+__global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    float* __restrict__ O, float* __restrict__ L, int nh, int T, int BH, int n_qtiles,
+    RowStrides sq, RowStrides sk, RowStrides sv, float scale, float scale_log2) {
+  constexpr int BN = FwdTile<HS>::BN;
+  constexpr int BM = 128;
+  constexpr int H2 = HS / 2;    // d values per lane half
+  constexpr int KP = HS + 4;    // LDS pitch (floats) of a K row: conflict-free 16-byte row reads
+  constexpr int VP = HS + 8;    // LDS pitch of a V row: the two wave halves read rows 4 apart
+  constexpr int KTILE = BN * KP;
+  constexpr int VTILE = BN * VP;
+  constexpr int F4_ROW = HS / 4;
+  constexpr int LOADS = BN * F4_ROW / 256;
+  static_assert(BN * F4_ROW % 256 == 0, "tile must split evenly over 256 threads");
+  __shared__ __attribute__((aligned(16))) float smem[2 * (KTILE + VTILE)];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, col = lane & 31;
+  const int id = blockIdx.x;
+  const int bh = id % BH;
+  const int qt = CAUSAL ? (n_qtiles - 1 - id / BH) : (id / BH);
+  const int b = bh / nh, h = bh - b * nh;
+
+  const float* Qb = Q + b * sq.b + h * sq.h;
+  const float* Kb = K + b * sk.b + h * sk.h;
+  const float* Vb = V + b * sv.b + h * sv.h;
+
+  const int i0 = qt * BM + wave * 32;  // first query row of this wave
+  const int my_i = i0 + col;           // query row owned by this lane
+
+  float qf[H2];
+  if (my_i < T) {
+    const float* qp = Qb + (int64_t)my_i * sq.t + half * H2;
+#pragma unroll
+    for (int c = 0; c < H2 / 4; ++c) {
+      float4 x = ld4(qp + 4 * c);
+      qf[4 * c + 0] = x.x; qf[4 * c + 1] = x.y; qf[4 * c + 2] = x.z; qf[4 * c + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < H2; ++c) qf[c] = 0.0f;
+  }
+
+  f32x16 oacc[HS / 32];
+#pragma unroll
+  for (int d = 0; d < HS / 32; ++d) oacc[d] = zero16();
+  float m_run = -INFINITY;  // running max of raw q.k for row my_i
+  float l_run = 0.0f;       // this lane's partial row sum (its half of the columns)
+
+  const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
+  const int n_stages = (kv_end + BN - 1) / BN;
+
+  float4 kst[LOADS], vst[LOADS];
+  auto gload = [&](int stage) {
+    const int j0 = stage * BN;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int f = tid + 256 * u;
+      const int r = f / F4_ROW, c4 = f % F4_ROW;
+      const int j = j0 + r;
+      if (j < T) {
+        kst[u] = ld4(Kb + (int64_t)j * sk.t + 4 * c4);
+        vst[u] = ld4(Vb + (int64_t)j * sv.t + 4 * c4);
+      } else {
+        kst[u] = zero4();
+        vst[u] = zero4();
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+    float* ks = smem + buf * (KTILE + VTILE);
+    float* vs = ks + KTILE;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int f = tid + 256 * u;
+      const int r = f / F4_ROW, c4 = f % F4_ROW;
+      st4(ks + r * KP + 4 * c4, kst[u]);
+      st4(vs + r * VP + 4 * c4, vst[u]);
+    }
+  };
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+
+  for (int s = 0; s < n_stages; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < n_stages) gload(s + 1);
+    const float* ks = smem + buf * (KTILE + VTILE);
+    const float* vs = ks + KTILE;
+
+#pragma unroll
+    for (int sub = 0; sub < BN / 32; ++sub) {
+      const int jj0 = s * BN + sub * 32;
+      if (jj0 >= T) continue;                      // ragged tail: nothing left in this stage
+      if (CAUSAL && jj0 > i0 + 31) continue;       // tile entirely above this wave's diagonal
+
+      // S^T tile: sacc[r] = q_{my_i} . k_{jj0 + R(r, half)}
+      f32x16 sacc = zero16();
+      const float* krow = ks + (sub * 32 + col) * KP + half * H2;
+#pragma unroll
+      for (int c = 0; c < H2 / 4; ++c) {
+        const float4 kv = ld4(krow + 4 * c);
+        sacc = mfma32(kv.x, qf[4 * c + 0], sacc);
+        sacc = mfma32(kv.y, qf[4 * c + 1], sacc);
+        sacc = mfma32(kv.z, qf[4 * c + 2], sacc);
+        sacc = mfma32(kv.w, qf[4 * c + 3], sacc);
+      }
+
+      const bool need_mask = (CAUSAL && jj0 + 31 > i0) || (jj0 + 32 > T);
+      if (need_mask) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = jj0 + mfma_row(r, half);
+          if ((CAUSAL && j > my_i) || j >= T) sacc[r] = -INFINITY;
+        }
+      }
+
+      float mt = sacc[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sacc[r]);
+      mt = fmaxf(mt, xor32(mt));
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = fast_exp2((m_run - m_new) * scale_log2);
+      const float mb = m_new * scale_log2;
+      float psum = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(sacc[r], scale_log2, -mb));
+        sacc[r] = p;
+        psum += p;
+      }
+      l_run = fmaf(l_run, alpha, psum);
+      m_run = m_new;
+
+#pragma unroll
+      for (int d = 0; d < HS / 32; ++d) {
+        oacc[d] *= alpha;
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+          const float a = vs[(sub * 32 + mfma_row(kk, half)) * VP + d * 32 + col];
+          oacc[d] = mfma32(a, sacc[kk], oacc[d]);
+        }
+      }
+    }
+
+    if (s + 1 < n_stages) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  const float l_tot = l_run + xor32(l_run);
+  if (my_i < T) {
+    float* op = O + ((int64_t)bh * T + my_i) * HS;
+#pragma unroll
+    for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dc = d * 32 + 8 * g + 4 * half;
+        st4(op + dc, make_float4(oacc[d][4 * g + 0] / l_tot, oacc[d][4 * g + 1] / l_tot,
+                                 oacc[d][4 * g + 2] / l_tot, oacc[d][4 * g + 3] / l_tot));
+      }
+    }
+    if (half == 0) L[(int64_t)bh * T + my_i] = m_run * scale + logf(l_tot);
+  }
+}
+
+template <int HS, bool CAUSAL>
+void launch_fwd(const float* q, const float* k, const float* v, float* o, float* l, int nh,
+                int T, int BH, RowStrides sq, RowStrides sk, RowStrides sv, float scale,
+                hipStream_t stream) {
+  const int n_qtiles = (T + 127) / 128;
+  const unsigned grid = (unsigned)n_qtiles * (unsigned)BH;
+  hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL>), dim3(grid), dim3(256), 0, stream, q, k, v, o,
+                     l, nh, T, BH, n_qtiles, sq, sk, sv, scale, scale * kLog2e);
+}
+
+}  // namespace
+
+bool attn_layout_ok(const float* p, const int64_t* s) {
+  return p != nullptr && s != nullptr && aligned16(p) && s[3] == 1 && s[0] % 4 == 0 &&
+         s[1] % 4 == 0 && s[2] % 4 == 0;
+}
+
+int check_attn_sizes(int64_t B, int64_t nh, int64_t T, int64_t hs) {
+  if (B < 0 || nh < 0 || T < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
+  if (hs != 32 && hs != 64 && hs != 128)
+    return fail(CTA_ERR_UNSUPPORTED_HEAD_DIM,
+                "Unsupported head dimension! Only hs=32, hs=64, and hs=128 are supported.");
+  if (B * nh > (int64_t)1 << 24 || T > (int64_t)1 << 24)
+    return fail(CTA_ERR_INVALID_ARGUMENT, "size too large");
+  return CTA_OK;
+}
+
+}  // namespace cta
+
+using namespace cta;
+
+extern "C" int cta_flash_attention_fwd(const float* q, const int64_t* q_strides, const float* k,
+                                       const int64_t* k_strides, const float* v,
+                                       const int64_t* v_strides, int64_t B, int64_t nh,
+                                       int64_t T, int64_t hs, int causal, float* o, float* l,
+                                       void* stream) {
+  if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
+  if (B * nh * T == 0) return CTA_OK;
+  if (!o || !l) return fail(CTA_ERR_INVALID_ARGUMENT, "null output pointer");
+  if (!attn_layout_ok(q, q_strides) || !attn_layout_ok(k, k_strides) ||
+      !attn_layout_ok(v, v_strides) || !aligned16(o))
+    return fail(CTA_ERR_LAYOUT,
+                "flash_attention_fwd needs unit d-stride, strides divisible by 4 and 16-byte "
+                "aligned Q/K/V/O");
+  const RowStrides sq{q_strides[0], q_strides[1], q_strides[2]};
+  const RowStrides sk{k_strides[0], k_strides[1], k_strides[2]};
+  const RowStrides sv{v_strides[0], v_strides[1], v_strides[2]};
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  const int BH = (int)(B * nh);
+  hipStream_t st = as_stream(stream);
+#define CTA_FWD(HS_)                                                                        \
+  if (causal) launch_fwd<HS_, true>(q, k, v, o, l, (int)nh, (int)T, BH, sq, sk, sv, scale, st); \
+  else launch_fwd<HS_, false>(q, k, v, o, l, (int)nh, (int)T, BH, sq, sk, sv, scale, st);
+  if (hs == 32) { CTA_FWD(32) }
+  else if (hs == 64) { CTA_FWD(64) }
+  else { CTA_FWD(128) }
+#undef CTA_FWD
+  return check_launch("flash_attention_fwd");
+}

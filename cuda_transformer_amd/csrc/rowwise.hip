@@ -1,0 +1,565 @@
+// Bandwidth-bound kernels: exact GELU, row softmax, LayerNorm (forward and backward).
+//
+//  * GELU follows Transformer_kernels/GeLU.cuh:7-29: y = x Phi(x),
+//    dx = dy (Phi(x) + x phi(x)), phi(x) = e^{-x^2/2} / sqrt(2 pi), with HIP's normcdff/expf.
+//  * Softmax follows softmax.cuh:25-159 (row max, sum of e^{x - max}, normalise;
+//    backward dx = p (dp - sum p dp)).
+//  * LayerNorm has no kernel in the reference; its semantics come from gpt/gpt.py:47-59:
+//    y = (x - mean) / sqrt(var + eps) * gamma + beta with the biased variance.
+//
+// gfx950 design: HBM is the bound, so every kernel moves each byte once.  Elementwise kernels
+// use dwordx4 loads/stores.  Row kernels give one wave64 to one row, keep the whole row in
+// registers (up to 2048 columns) and reduce with cross-lane shuffles — a single read and a
+// single write per element, where the reference reads x three times.  Longer rows fall back
+// to a workgroup-per-row path.  Column reductions (dgamma, dbeta) are two-stage and
+// deterministic (no atomics).
+#include "cta_common.hpp"
+
+namespace cta {
+namespace {
+
+constexpr float kInvSqrt2Pi = 0.3989422804014327f;
+
+// ------------------------------------------------------------------------------- GELU
+__device__ __forceinline__ float gelu_f(float x) { return x * normcdff(x); }
+__device__ __forceinline__ float gelu_grad(float x, float g) {
+  const float pdf = kInvSqrt2Pi * expf(-0.5f * x * x);
+  return g * (normcdff(x) + x * pdf);
+}
+
+__global__ __launch_bounds__(256) void gelu_fwd_kernel(const float* __restrict__ x,
+                                                       float* __restrict__ y, int64_t n4,
+                                                       int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+    const float4 v = ld4(x + 4 * i);
+    st4(y + 4 * i, make_float4(gelu_f(v.x), gelu_f(v.y), gelu_f(v.z), gelu_f(v.w)));
+  }
+  // tail (n % 4 elements) handled by the first threads of block 0
+  if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
+    const int64_t i = 4 * n4 + threadIdx.x;
+    y[i] = gelu_f(x[i]);
+  }
+}
+
+__global__ __launch_bounds__(256) void gelu_bwd_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ dy,
+                                                       float* __restrict__ dx, int64_t n4,
+                                                       int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+    const float4 v = ld4(x + 4 * i);
+    const float4 g = ld4(dy + 4 * i);
+    st4(dx + 4 * i, make_float4(gelu_grad(v.x, g.x), gelu_grad(v.y, g.y), gelu_grad(v.z, g.z),
+                                gelu_grad(v.w, g.w)));
+  }
+  if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
+    const int64_t i = 4 * n4 + threadIdx.x;
+    dx[i] = gelu_grad(x[i], dy[i]);
+  }
+}
+
+unsigned elementwise_grid(int64_t n4) {
+  // enough workgroups to fill 256 CUs several times over; grid-stride covers the rest
+  const int64_t want = (n4 + 255) / 256;
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, 256 * 16));
+}
+
+// ------------------------------------------------------------------- row register path
+// A wave owns one row of length n.  VEC: n % 4 == 0 and rows 16-byte aligned, lane loads
+// float4 chunks c = lane + 64*u; otherwise lane loads scalars e = lane + 64*u.
+template <int U, bool VEC>
+struct RowRegs {
+  static constexpr int W = VEC ? 4 : 1;
+  float v[U * W];
+  __device__ __forceinline__ void load(const float* row, int n, int lane, float fill) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = lane + 64 * u;
+      if (VEC) {
+        const float4 t = (4 * c < n) ? ld4(row + 4 * c) : make_float4(fill, fill, fill, fill);
+        v[4 * u + 0] = t.x; v[4 * u + 1] = t.y; v[4 * u + 2] = t.z; v[4 * u + 3] = t.w;
+      } else {
+        v[u] = (c < n) ? row[c] : fill;
+      }
+    }
+  }
+  __device__ __forceinline__ void store(float* row, int n, int lane) const {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = lane + 64 * u;
+      if (VEC) {
+        if (4 * c < n) st4(row + 4 * c, make_float4(v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]));
+      } else {
+        if (c < n) row[c] = v[u];
+      }
+    }
+  }
+  // column index of element e of this lane
+  __device__ __forceinline__ static int colof(int e, int lane) {
+    return VEC ? 4 * (lane + 64 * (e / 4)) + (e % 4) : lane + 64 * e;
+  }
+};
+
+template <int U, bool VEC>
+__global__ __launch_bounds__(256) void softmax_fwd_rows(const float* x,
+                                                        float* y, int64_t rows,
+                                                        int n) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  RowRegs<U, VEC> r;
+  r.load(x + row * n, n, lane, -INFINITY);
+  float mx = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < U * r.W; ++e) mx = fmaxf(mx, r.v[e]);
+  mx = wave_max(mx);
+  float sum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < U * r.W; ++e) {
+    const float p = expf(r.v[e] - mx);
+    r.v[e] = p;
+    sum += p;
+  }
+  sum = wave_sum(sum);
+  const float inv = 1.0f / sum;
+#pragma unroll
+  for (int e = 0; e < U * r.W; ++e) r.v[e] *= inv;
+  r.store(y + row * n, n, lane);
+}
+
+template <int U, bool VEC>
+__global__ __launch_bounds__(256) void softmax_bwd_rows(const float* p,
+                                                        const float* dp,
+                                                        float* dx, int64_t rows,
+                                                        int n) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  RowRegs<U, VEC> a, g;
+  a.load(p + row * n, n, lane, 0.0f);
+  g.load(dp + row * n, n, lane, 0.0f);
+  float dot = 0.0f;
+#pragma unroll
+  for (int e = 0; e < U * a.W; ++e) dot = fmaf(a.v[e], g.v[e], dot);
+  dot = wave_sum(dot);
+#pragma unroll
+  for (int e = 0; e < U * a.W; ++e) a.v[e] = a.v[e] * (g.v[e] - dot);
+  a.store(dx + row * n, n, lane);
+}
+
+// --------------------------------------------------------------- long-row block path
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+  v = is_max ? wave_max(v) : wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();  // red[] may still be read by a previous reduction
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+  return r;
+}
+
+__global__ __launch_bounds__(256) void softmax_fwd_long(const float* x,
+                                                        float* y, int n) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * n;
+  float* yr = y + row * n;
+  // pass 1: online max/sum per thread, then a block-wide merge of the (max, sum) pairs
+  float m = -INFINITY, s = 0.0f;
+  for (int c = threadIdx.x; c < n; c += 256) {
+    const float v = xr[c];
+    const float mn = fmaxf(m, v);
+    s = s * expf(m - mn) + expf(v - mn);
+    m = mn;
+  }
+  const float gm = block_reduce(m, true, red);
+  const float part = (m == -INFINITY) ? 0.0f : s * expf(m - gm);
+  const float gs = block_reduce(part, false, red);
+  const float inv = 1.0f / gs;
+  for (int c = threadIdx.x; c < n; c += 256) yr[c] = expf(xr[c] - gm) * inv;
+}
+
+__global__ __launch_bounds__(256) void softmax_bwd_long(const float* p,
+                                                        const float* dp,
+                                                        float* dx, int n) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float* pr = p + row * n;
+  const float* gr = dp + row * n;
+  float* xr = dx + row * n;
+  float dot = 0.0f;
+  for (int c = threadIdx.x; c < n; c += 256) dot = fmaf(pr[c], gr[c], dot);
+  dot = block_reduce(dot, false, red);
+  __syncthreads();  // every thread has read its p/dp before any in-place write lands
+  for (int c = threadIdx.x; c < n; c += 256) xr[c] = pr[c] * (gr[c] - dot);
+}
+
+// ------------------------------------------------------------------------ LayerNorm
+template <int U, bool VEC>
+__global__ __launch_bounds__(256) void layernorm_fwd_rows(
+    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, int64_t rows,
+    int n, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  using R = RowRegs<U, VEC>;
+  R r, gm, bt;
+  r.load(x + row * n, n, lane, 0.0f);
+  gm.load(gamma, n, lane, 0.0f);
+  bt.load(beta, n, lane, 0.0f);
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < U * R::W; ++e) s += r.v[e];
+  const float mu = wave_sum(s) / (float)n;
+  float q = 0.0f;
+#pragma unroll
+  for (int e = 0; e < U * R::W; ++e) {
+    const float d = (R::colof(e, lane) < n) ? r.v[e] - mu : 0.0f;
+    q = fmaf(d, d, q);
+  }
+  const float var = wave_sum(q) / (float)n;
+  const float rs = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int e = 0; e < U * R::W; ++e) r.v[e] = fmaf((r.v[e] - mu) * rs, gm.v[e], bt.v[e]);
+  r.store(y + row * n, n, lane);
+  if (lane == 0) {
+    mean[row] = mu;
+    rstd[row] = rs;
+  }
+}
+
+// Backward: dx per row in registers; per-block column partials of dgamma/dbeta written to
+// `part` ([blocks][2][n]); a second kernel sums the partials in block order.
+template <int U, bool VEC>
+__global__ __launch_bounds__(256) void layernorm_bwd_rows(
+    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ dy, float* __restrict__ dx,
+    float* __restrict__ part, int64_t rows, int n, int rows_per_wave) {
+  using R = RowRegs<U, VEC>;
+  __shared__ float lds_g[4][U * R::W * 64];
+  __shared__ float lds_b[4][U * R::W * 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  R gm;
+  gm.load(gamma, n, lane, 0.0f);
+  float accg[U * R::W], accb[U * R::W];
+#pragma unroll
+  for (int e = 0; e < U * R::W; ++e) { accg[e] = 0.0f; accb[e] = 0.0f; }
+
+  const int64_t wave_id = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t r0 = wave_id * rows_per_wave;
+  const int64_t r1 = min(rows, r0 + rows_per_wave);
+  const float inv_n = 1.0f / (float)n;
+  for (int64_t row = r0; row < r1; ++row) {
+    R xv, g;
+    xv.load(x + row * n, n, lane, 0.0f);
+    g.load(dy + row * n, n, lane, 0.0f);
+    const float mu = mean[row], rs = rstd[row];
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < U * R::W; ++e) {
+      const float xh = (xv.v[e] - mu) * rs;
+      const float gx = g.v[e] * gm.v[e];
+      accg[e] = fmaf(g.v[e], xh, accg[e]);
+      accb[e] += g.v[e];
+      s1 += gx;
+      s2 = fmaf(gx, xh, s2);
+      xv.v[e] = xh;
+      g.v[e] = gx;
+    }
+    const float m1 = wave_sum(s1) * inv_n, m2 = wave_sum(s2) * inv_n;
+#pragma unroll
+    for (int e = 0; e < U * R::W; ++e) xv.v[e] = rs * (g.v[e] - m1 - xv.v[e] * m2);
+    xv.store(dx + row * n, n, lane);
+  }
+  // combine the 4 waves of this block in a fixed order, then write one partial row
+#pragma unroll
+  for (int e = 0; e < U * R::W; ++e) {
+    lds_g[wave][e * 64 + lane] = accg[e];
+    lds_b[wave][e * 64 + lane] = accb[e];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int e = 0; e < U * R::W; ++e) {
+      const int c = R::colof(e, lane);
+      if (c < n) {
+        float sg = lds_g[0][e * 64 + lane], sb = lds_b[0][e * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+          sg += lds_g[w][e * 64 + lane];
+          sb += lds_b[w][e * 64 + lane];
+        }
+        part[(int64_t)blockIdx.x * 2 * n + c] = sg;
+        part[(int64_t)blockIdx.x * 2 * n + n + c] = sb;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void layernorm_bwd_final(const float* __restrict__ part,
+                                                           float* __restrict__ dgamma,
+                                                           float* __restrict__ dbeta, int n,
+                                                           int blocks) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= n) return;
+  float sg = 0.0f, sb = 0.0f;
+  for (int b = 0; b < blocks; ++b) {
+    sg += part[(int64_t)b * 2 * n + c];
+    sb += part[(int64_t)b * 2 * n + n + c];
+  }
+  dgamma[c] = sg;
+  dbeta[c] = sb;
+}
+
+// Long rows (n > 2048): one workgroup per row, three passes over the row.
+__global__ __launch_bounds__(256) void layernorm_fwd_long(
+    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, int n, float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * n;
+  float s = 0.0f;
+  for (int c = threadIdx.x; c < n; c += 256) s += xr[c];
+  const float mu = block_reduce(s, false, red) / (float)n;
+  float q = 0.0f;
+  for (int c = threadIdx.x; c < n; c += 256) {
+    const float d = xr[c] - mu;
+    q = fmaf(d, d, q);
+  }
+  const float rs = 1.0f / sqrtf(block_reduce(q, false, red) / (float)n + eps);
+  for (int c = threadIdx.x; c < n; c += 256)
+    y[row * n + c] = fmaf((xr[c] - mu) * rs, gamma[c], beta[c]);
+  if (threadIdx.x == 0) {
+    mean[row] = mu;
+    rstd[row] = rs;
+  }
+}
+
+__global__ __launch_bounds__(256) void layernorm_bwd_long(
+    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ dy, float* __restrict__ dx, int n) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float mu = mean[row], rs = rstd[row];
+  float s1 = 0.0f, s2 = 0.0f;
+  for (int c = threadIdx.x; c < n; c += 256) {
+    const float xh = (x[row * n + c] - mu) * rs;
+    const float gx = dy[row * n + c] * gamma[c];
+    s1 += gx;
+    s2 = fmaf(gx, xh, s2);
+  }
+  const float m1 = block_reduce(s1, false, red) / (float)n;
+  const float m2 = block_reduce(s2, false, red) / (float)n;
+  for (int c = threadIdx.x; c < n; c += 256) {
+    const float xh = (x[row * n + c] - mu) * rs;
+    const float gx = dy[row * n + c] * gamma[c];
+    dx[row * n + c] = rs * (gx - m1 - xh * m2);
+  }
+}
+
+// dgamma/dbeta for the long-row path: column partials over row chunks, then the final sum.
+__global__ __launch_bounds__(256) void layernorm_colpart_long(
+    const float* __restrict__ x, const float* __restrict__ mean, const float* __restrict__ rstd,
+    const float* __restrict__ dy, float* __restrict__ part, int64_t rows, int n,
+    int rows_per_block) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= n) return;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_block;
+  const int64_t r1 = min(rows, r0 + rows_per_block);
+  float sg = 0.0f, sb = 0.0f;
+  for (int64_t r = r0; r < r1; ++r) {
+    const float g = dy[r * n + c];
+    sg = fmaf(g, (x[r * n + c] - mean[r]) * rstd[r], sg);
+    sb += g;
+  }
+  part[(int64_t)blockIdx.y * 2 * n + c] = sg;
+  part[(int64_t)blockIdx.y * 2 * n + n + c] = sb;
+}
+
+// ------------------------------------------------------------------ dispatch helpers
+constexpr int kMaxRegCols = 2048;
+constexpr int kLnBwdBlocks = 256;  // partial rows for dgamma/dbeta (row-register path)
+constexpr int kLnLongRowsPerBlock = 64;
+
+int units_for(int n, bool vec) {
+  const int per = vec ? 256 : 64;  // columns covered per unit of U
+  const int u = (n + per - 1) / per;
+  return u <= 1 ? 1 : u <= 2 ? 2 : u <= 4 ? 4 : u <= 8 ? 8 : u <= 16 ? 16 : 32;
+}
+
+bool row_vec_ok(const void* a, const void* b, const void* c, int n) {
+  return n % 4 == 0 && aligned16(a) && (b == nullptr || aligned16(b)) &&
+         (c == nullptr || aligned16(c));
+}
+
+#define CTA_ROW_SWITCH(KERNEL, VEC, U, GRID, ST, ...)                                        \
+  do {                                                                                      \
+    if (VEC) {                                                                              \
+      switch (U) {                                                                          \
+        case 1: hipLaunchKernelGGL((KERNEL<1, true>), GRID, dim3(256), 0, ST, __VA_ARGS__); break; \
+        case 2: hipLaunchKernelGGL((KERNEL<2, true>), GRID, dim3(256), 0, ST, __VA_ARGS__); break; \
+        case 4: hipLaunchKernelGGL((KERNEL<4, true>), GRID, dim3(256), 0, ST, __VA_ARGS__); break; \
+        default: hipLaunchKernelGGL((KERNEL<8, true>), GRID, dim3(256), 0, ST, __VA_ARGS__); break; \
+      }                                                                                     \
+    } else {                                                                                \
+      switch (U) {                                                                          \
+        case 1: hipLaunchKernelGGL((KERNEL<1, false>), GRID, dim3(256), 0, ST, __VA_ARGS__); break; \
+        case 2: hipLaunchKernelGGL((KERNEL<2, false>), GRID, dim3(256), 0, ST, __VA_ARGS__); break; \
+        case 4: hipLaunchKernelGGL((KERNEL<4, false>), GRID, dim3(256), 0, ST, __VA_ARGS__); break; \
+        case 8: hipLaunchKernelGGL((KERNEL<8, false>), GRID, dim3(256), 0, ST, __VA_ARGS__); break; \
+        case 16: hipLaunchKernelGGL((KERNEL<16, false>), GRID, dim3(256), 0, ST, __VA_ARGS__); break; \
+        default: hipLaunchKernelGGL((KERNEL<32, false>), GRID, dim3(256), 0, ST, __VA_ARGS__); break; \
+      }                                                                                     \
+    }                                                                                       \
+  } while (0)
+
+}  // namespace
+
+// Shared with the naive attention: softmax over contiguous rows (in place allowed).
+int softmax_rows(const float* x, float* y, int64_t rows, int64_t n, hipStream_t st) {
+  if (rows == 0 || n == 0) return CTA_OK;
+  if (n > INT32_MAX || rows > ((int64_t)1 << 40)) return fail(CTA_ERR_INVALID_ARGUMENT, "softmax size out of range");
+  if (n <= kMaxRegCols) {
+    const bool vec = row_vec_ok(x, y, nullptr, (int)n);
+    const int u = units_for((int)n, vec);
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    CTA_ROW_SWITCH(softmax_fwd_rows, vec, u, grid, st, x, y, rows, (int)n);
+  } else {
+    hipLaunchKernelGGL(softmax_fwd_long, dim3((unsigned)rows), dim3(256), 0, st, x, y, (int)n);
+  }
+  return check_launch("softmax");
+}
+
+int softmax_bwd_rows_launch(const float* p, const float* dp, float* dx, int64_t rows, int64_t n,
+                            hipStream_t st) {
+  if (rows == 0 || n == 0) return CTA_OK;
+  if (n > INT32_MAX) return fail(CTA_ERR_INVALID_ARGUMENT, "softmax size out of range");
+  if (n <= kMaxRegCols) {
+    const bool vec = row_vec_ok(p, dp, dx, (int)n);
+    const int u = units_for((int)n, vec);
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    CTA_ROW_SWITCH(softmax_bwd_rows, vec, u, grid, st, p, dp, dx, rows, (int)n);
+  } else {
+    hipLaunchKernelGGL(softmax_bwd_long, dim3((unsigned)rows), dim3(256), 0, st, p, dp, dx, (int)n);
+  }
+  return check_launch("softmax_bwd");
+}
+
+int64_t layernorm_bwd_workspace_floats(int64_t rows, int64_t n) {
+  if (rows <= 0 || n <= 0) return 0;
+  if (n <= kMaxRegCols) return (int64_t)kLnBwdBlocks * 2 * n;
+  return ((rows + kLnLongRowsPerBlock - 1) / kLnLongRowsPerBlock) * 2 * n;
+}
+
+}  // namespace cta
+
+using namespace cta;
+
+extern "C" int cta_gelu_fwd(const float* x, float* y, int64_t numel, void* stream) {
+  if (numel < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
+  if (numel == 0) return CTA_OK;
+  if (!x || !y) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (!aligned16(x) || !aligned16(y))
+    return fail(CTA_ERR_LAYOUT, "gelu_activation needs 16-byte aligned buffers");
+  const int64_t n4 = numel / 4;
+  hipLaunchKernelGGL(gelu_fwd_kernel, dim3(elementwise_grid(n4)), dim3(256), 0, as_stream(stream),
+                     x, y, n4, numel);
+  return check_launch("gelu_activation");
+}
+
+extern "C" int cta_gelu_bwd(const float* x, const float* dy, float* dx, int64_t numel,
+                            void* stream) {
+  if (numel < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
+  if (numel == 0) return CTA_OK;
+  if (!x || !dy || !dx) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (!aligned16(x) || !aligned16(dy) || !aligned16(dx))
+    return fail(CTA_ERR_LAYOUT, "gelu_activation_bwd needs 16-byte aligned buffers");
+  const int64_t n4 = numel / 4;
+  hipLaunchKernelGGL(gelu_bwd_kernel, dim3(elementwise_grid(n4)), dim3(256), 0, as_stream(stream),
+                     x, dy, dx, n4, numel);
+  return check_launch("gelu_activation_bwd");
+}
+
+extern "C" int cta_softmax_fwd(const float* x, float* y, int64_t rows, int64_t n, void* stream) {
+  if (rows < 0 || n < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
+  if (rows * n > 0 && (!x || !y)) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  return softmax_rows(x, y, rows, n, as_stream(stream));
+}
+
+extern "C" int cta_softmax_bwd(const float* probs, const float* dp, float* dx, int64_t rows,
+                               int64_t n, void* stream) {
+  if (rows < 0 || n < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
+  if (rows * n > 0 && (!probs || !dp || !dx)) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  return softmax_bwd_rows_launch(probs, dp, dx, rows, n, as_stream(stream));
+}
+
+extern "C" int cta_layernorm_fwd(const float* x, const float* gamma, const float* beta,
+                                 int64_t rows, int64_t n, float eps, float* y, float* mean,
+                                 float* rstd, void* stream) {
+  if (rows < 0 || n < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
+  if (rows == 0) return CTA_OK;
+  if (n == 0) return fail(CTA_ERR_INVALID_ARGUMENT, "layernorm over an empty dimension");
+  if (n > INT32_MAX) return fail(CTA_ERR_INVALID_ARGUMENT, "layernorm size out of range");
+  if (!x || !gamma || !beta || !y || !mean || !rstd)
+    return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  hipStream_t st = as_stream(stream);
+  if (n <= kMaxRegCols) {
+    const bool vec = row_vec_ok(x, y, gamma, (int)n) && aligned16(beta);
+    const int u = units_for((int)n, vec);
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    CTA_ROW_SWITCH(layernorm_fwd_rows, vec, u, grid, st, x, gamma, beta, y, mean, rstd, rows,
+                   (int)n, eps);
+  } else {
+    hipLaunchKernelGGL(layernorm_fwd_long, dim3((unsigned)rows), dim3(256), 0, st, x, gamma, beta,
+                       y, mean, rstd, (int)n, eps);
+  }
+  return check_launch("layernorm_fwd");
+}
+
+extern "C" int64_t cta_layernorm_bwd_workspace(int64_t rows, int64_t n) {
+  return layernorm_bwd_workspace_floats(rows, n) * (int64_t)sizeof(float);
+}
+
+extern "C" int cta_layernorm_bwd(const float* x, const float* gamma, const float* mean,
+                                 const float* rstd, const float* dy, int64_t rows, int64_t n,
+                                 float* dx, float* dgamma, float* dbeta, float* workspace,
+                                 void* stream) {
+  if (rows < 0 || n < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
+  if (n == 0) return CTA_OK;
+  if (n > INT32_MAX) return fail(CTA_ERR_INVALID_ARGUMENT, "layernorm size out of range");
+  if (!dgamma || !dbeta) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  hipStream_t st = as_stream(stream);
+  if (rows == 0) {
+    if (hipMemsetAsync(dgamma, 0, n * sizeof(float), st) != hipSuccess ||
+        hipMemsetAsync(dbeta, 0, n * sizeof(float), st) != hipSuccess)
+      return fail(CTA_ERR_LAUNCH, "hipMemsetAsync failed");
+    return CTA_OK;
+  }
+  if (!x || !gamma || !mean || !rstd || !dy || !dx || !workspace)
+    return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (n <= kMaxRegCols) {
+    const bool vec = row_vec_ok(x, dy, dx, (int)n) && aligned16(gamma);
+    const int u = units_for((int)n, vec);
+    const int64_t waves = (int64_t)kLnBwdBlocks * 4;
+    const int rows_per_wave = (int)((rows + waves - 1) / waves);
+    CTA_ROW_SWITCH(layernorm_bwd_rows, vec, u, dim3(kLnBwdBlocks), st, x, gamma, mean, rstd, dy,
+                   dx, workspace, rows, (int)n, rows_per_wave);
+    hipLaunchKernelGGL(layernorm_bwd_final, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       workspace, dgamma, dbeta, (int)n, kLnBwdBlocks);
+  } else {
+    hipLaunchKernelGGL(layernorm_bwd_long, dim3((unsigned)rows), dim3(256), 0, st, x, gamma, mean,
+                       rstd, dy, dx, (int)n);
+    const int64_t chunks = (rows + kLnLongRowsPerBlock - 1) / kLnLongRowsPerBlock;
+    if (chunks > 65535) return fail(CTA_ERR_INVALID_ARGUMENT, "too many rows for layernorm_bwd");
+    hipLaunchKernelGGL(layernorm_colpart_long, dim3((unsigned)((n + 255) / 256), (unsigned)chunks),
+                       dim3(256), 0, st, x, mean, rstd, dy, workspace, rows, (int)n,
+                       kLnLongRowsPerBlock);
+    hipLaunchKernelGGL(layernorm_bwd_final, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       workspace, dgamma, dbeta, (int)n, (int)chunks);
+  }
+  return check_launch("layernorm_bwd");
+}

@@ -1,0 +1,394 @@
+// torch operator library `cuda_transformer` on top of the C ABI.
+//
+// Same operator names, schemas, argument meaning and error messages as the reference's
+// launchers (Transformer_launchers/*.cu registered through bindings.cpp:3-7).  Each op:
+// validates its inputs with TORCH_CHECK (surfacing as a Python RuntimeError), allocates
+// dense outputs on the input's device, and calls the gfx950 kernels through the C ABI on
+// torch's current HIP stream.  Two schemas are added for LayerNorm, which the reference
+// implements in plain torch only (gpt/gpt.py:47-59).
+//
+// This file is host-only C++; every kernel lives in libcuda_transformer_amd.so.
+#include <Python.h>
+
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <array>
+#include <cstdint>
+#include <tuple>
+
+#include "cuda_transformer_amd.h"
+
+namespace cuda_transformer {
+namespace {
+
+void* stream_of(const at::Tensor& t) {
+  return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.get_device()).stream());
+}
+
+void check_rc(int rc) { TORCH_CHECK(rc == CTA_OK, cta_last_error()); }
+
+void check_f32(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.scalar_type() == at::kFloat, name, " must be a float32 tensor, got ",
+              t.scalar_type());
+}
+
+template <size_t N>
+std::array<int64_t, N> strides_of(const at::Tensor& t) {
+  std::array<int64_t, N> s{};
+  for (size_t d = 0; d < N; ++d) s[d] = t.size(d) == 1 ? 0 : t.stride(d);  // size-1 dims: unused
+  return s;
+}
+
+// The attention kernels read 16-byte row segments: unit d-stride, strides divisible by 4,
+// 16-byte aligned base.  Anything else is passed as a dense copy.
+bool attn_layout_ok(const at::Tensor& t) {
+  const auto s = strides_of<4>(t);
+  return (t.size(3) == 1 || t.stride(3) == 1) && s[0] % 4 == 0 && s[1] % 4 == 0 &&
+         s[2] % 4 == 0 && (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) == 0;
+}
+
+at::Tensor attn_operand(const at::Tensor& t) {
+  if (attn_layout_ok(t)) return t;
+  at::Tensor c = t.contiguous();
+  if (!attn_layout_ok(c)) c = t.clone(at::MemoryFormat::Contiguous);
+  return c;
+}
+
+at::Tensor dense(const at::Tensor& t) {
+  at::Tensor c = t.contiguous();
+  if ((reinterpret_cast<uintptr_t>(c.data_ptr()) & 15u) != 0) c = t.clone(at::MemoryFormat::Contiguous);
+  return c;
+}
+
+// ------------------------------------------------------------------ linear layer
+// cf. Transformer_launchers/linear_layer.cu:28-70
+at::Tensor cuda_fma(at::Tensor x, at::Tensor weights, at::Tensor bias) {
+  if (weights.dim() == 2) weights = weights.unsqueeze(0);
+  TORCH_CHECK(x.dim() == 3, "x must be a 3D tensor (batch, m, k)");
+  TORCH_CHECK(weights.dim() == 3, "weights must be a 2D or 3D tensor");
+  TORCH_CHECK(bias.dim() == 1, "bias must be a 1D tensor");
+  const int64_t x_batch = x.size(0), m = x.size(1), k = x.size(2), n = weights.size(2);
+  TORCH_CHECK(weights.size(1) == k, "weights.size(1) must match x.size(2)");
+  TORCH_CHECK(bias.size(0) == n, "bias.size(0) must match weights.size(2)");
+  TORCH_CHECK(x.is_cuda(), "x must be a CUDA tensor");
+  TORCH_CHECK(weights.is_cuda(), "weights must be a CUDA tensor");
+  TORCH_CHECK(bias.is_cuda(), "bias must be a CUDA tensor");
+  check_f32(x, "x");
+  check_f32(weights, "weights");
+  check_f32(bias, "bias");
+  TORCH_CHECK(weights.size(0) == 1 || weights.size(0) == x_batch,
+              "weights.size(0) must be 1 or match x.size(0)");
+  c10::OptionalDeviceGuard guard(x.device());
+  at::Tensor out = at::empty({x_batch, m, n}, x.options());
+  const auto xs = strides_of<3>(x);
+  const auto ws = strides_of<3>(weights);
+  check_rc(cta_cuda_fma(x.data_ptr<float>(), xs.data(), weights.data_ptr<float>(), ws.data(),
+                        bias.data_ptr<float>(), bias.stride(0), x_batch, m, k, n,
+                        weights.size(0), out.data_ptr<float>(), stream_of(x)));
+  return out;
+}
+
+// cf. linear_layer.cu:74-97
+at::Tensor db_calculation(at::Tensor dy) {
+  TORCH_CHECK(dy.dim() == 3, "dy must be a 3D tensor (batch, m, n)");
+  TORCH_CHECK(dy.is_cuda(), "dy must be a CUDA tensor");
+  check_f32(dy, "dy");
+  const int64_t batch = dy.size(0), m = dy.size(1), n = dy.size(2);
+  c10::OptionalDeviceGuard guard(dy.device());
+  at::Tensor db = at::empty({n}, dy.options());
+  const int64_t ws_bytes = cta_db_calculation_workspace(batch, m, n);
+  at::Tensor ws = at::empty({std::max<int64_t>(1, ws_bytes / 4)}, dy.options());
+  const auto s = strides_of<3>(dy);
+  check_rc(cta_db_calculation(dy.data_ptr<float>(), s.data(), batch, m, n, db.data_ptr<float>(),
+                              ws.data_ptr<float>(), stream_of(dy)));
+  return db;
+}
+
+// ------------------------------------------------------------------ GELU
+// cf. Transformer_launchers/gelu_activation.cu:22-77
+at::Tensor gelu_activation(at::Tensor x) {
+  TORCH_CHECK(x.is_cuda(), "x must be a CUDA tensor");
+  TORCH_CHECK(x.is_contiguous(), "x must be contiguous");
+  check_f32(x, "x");
+  c10::OptionalDeviceGuard guard(x.device());
+  const at::Tensor xd = dense(x);
+  at::Tensor out = at::empty(x.sizes(), x.options());
+  check_rc(cta_gelu_fwd(xd.data_ptr<float>(), out.data_ptr<float>(), x.numel(), stream_of(x)));
+  return out;
+}
+
+at::Tensor gelu_activation_bwd(at::Tensor x, at::Tensor dy) {
+  TORCH_CHECK(x.is_cuda(), "x must be a CUDA tensor");
+  TORCH_CHECK(x.is_contiguous(), "x must be contiguous");
+  TORCH_CHECK(dy.is_cuda(), "dy must be a CUDA tensor");
+  TORCH_CHECK(dy.is_contiguous(), "dy must be contiguous");
+  check_f32(x, "x");
+  check_f32(dy, "dy");
+  TORCH_CHECK(x.numel() == dy.numel(), "x and dy must have the same number of elements");
+  c10::OptionalDeviceGuard guard(x.device());
+  const at::Tensor xd = dense(x), gd = dense(dy);
+  at::Tensor out = at::empty(x.sizes(), x.options());
+  check_rc(cta_gelu_bwd(xd.data_ptr<float>(), gd.data_ptr<float>(), out.data_ptr<float>(),
+                        x.numel(), stream_of(x)));
+  return out;
+}
+
+// ------------------------------------------------------------------ softmax
+// cf. Transformer_launchers/softmax_layer.cu:22-78
+at::Tensor cuda_softmax(at::Tensor x) {
+  TORCH_CHECK(x.dim() == 3, "x must be a 3D tensor");
+  TORCH_CHECK(x.is_cuda(), "x must be a CUDA tensor");
+  TORCH_CHECK(x.is_contiguous(), "x must be contiguous");
+  check_f32(x, "x");
+  c10::OptionalDeviceGuard guard(x.device());
+  const at::Tensor xd = dense(x);
+  at::Tensor out = at::empty(x.sizes(), x.options());
+  check_rc(cta_softmax_fwd(xd.data_ptr<float>(), out.data_ptr<float>(), x.size(0) * x.size(1),
+                           x.size(2), stream_of(x)));
+  return out;
+}
+
+at::Tensor cuda_softmax_bwd(at::Tensor probs, at::Tensor dp) {
+  TORCH_CHECK(probs.dim() == 3, "probs must be a 3D tensor");
+  TORCH_CHECK(probs.is_cuda(), "probs must be a CUDA tensor");
+  TORCH_CHECK(probs.is_contiguous(), "probs must be contiguous");
+  TORCH_CHECK(dp.dim() == 3, "dp must be a 3D tensor");
+  TORCH_CHECK(dp.is_cuda(), "dp must be a CUDA tensor");
+  TORCH_CHECK(dp.is_contiguous(), "dp must be contiguous");
+  check_f32(probs, "probs");
+  check_f32(dp, "dp");
+  TORCH_CHECK(probs.sizes() == dp.sizes(), "probs and dp must have the same shape");
+  c10::OptionalDeviceGuard guard(probs.device());
+  const at::Tensor pd = dense(probs), gd = dense(dp);
+  at::Tensor out = at::empty(probs.sizes(), probs.options());
+  check_rc(cta_softmax_bwd(pd.data_ptr<float>(), gd.data_ptr<float>(), out.data_ptr<float>(),
+                           probs.size(0) * probs.size(1), probs.size(2), stream_of(probs)));
+  return out;
+}
+
+// ------------------------------------------------------------------ LayerNorm (new)
+std::tuple<at::Tensor, at::Tensor, at::Tensor> layernorm_fwd(at::Tensor x, at::Tensor gamma,
+                                                             at::Tensor beta, double eps) {
+  TORCH_CHECK(x.dim() >= 1, "x must have at least one dimension");
+  TORCH_CHECK(x.is_cuda(), "x must be a CUDA tensor");
+  TORCH_CHECK(gamma.is_cuda(), "gamma must be a CUDA tensor");
+  TORCH_CHECK(beta.is_cuda(), "beta must be a CUDA tensor");
+  check_f32(x, "x");
+  check_f32(gamma, "gamma");
+  check_f32(beta, "beta");
+  const int64_t n = x.size(-1);
+  TORCH_CHECK(gamma.numel() == n && beta.numel() == n,
+              "gamma and beta must have x.size(-1) elements");
+  c10::OptionalDeviceGuard guard(x.device());
+  const at::Tensor xd = dense(x), gd = dense(gamma), bd = dense(beta);
+  const int64_t rows = n == 0 ? 0 : x.numel() / n;
+  at::Tensor y = at::empty(x.sizes(), x.options());
+  auto stat_shape = x.sizes().vec();
+  stat_shape.pop_back();
+  at::Tensor mean = at::empty(stat_shape, x.options());
+  at::Tensor rstd = at::empty(stat_shape, x.options());
+  check_rc(cta_layernorm_fwd(xd.data_ptr<float>(), gd.data_ptr<float>(), bd.data_ptr<float>(),
+                             rows, n, static_cast<float>(eps), y.data_ptr<float>(),
+                             mean.data_ptr<float>(), rstd.data_ptr<float>(), stream_of(x)));
+  return {y, mean, rstd};
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> layernorm_bwd(at::Tensor x, at::Tensor gamma,
+                                                             at::Tensor mean, at::Tensor rstd,
+                                                             at::Tensor dy) {
+  TORCH_CHECK(x.is_cuda() && gamma.is_cuda() && mean.is_cuda() && rstd.is_cuda() && dy.is_cuda(),
+              "layernorm_bwd inputs must be CUDA tensors");
+  check_f32(x, "x");
+  check_f32(gamma, "gamma");
+  check_f32(mean, "mean");
+  check_f32(rstd, "rstd");
+  check_f32(dy, "dy");
+  const int64_t n = x.size(-1);
+  TORCH_CHECK(dy.sizes() == x.sizes(), "dy must have the shape of x");
+  TORCH_CHECK(gamma.numel() == n, "gamma must have x.size(-1) elements");
+  const int64_t rows = n == 0 ? 0 : x.numel() / n;
+  TORCH_CHECK(mean.numel() == rows && rstd.numel() == rows, "mean/rstd must have one value per row");
+  c10::OptionalDeviceGuard guard(x.device());
+  const at::Tensor xd = dense(x), gd = dense(gamma), md = dense(mean), rd = dense(rstd),
+                   dd = dense(dy);
+  at::Tensor dx = at::empty(x.sizes(), x.options());
+  at::Tensor dgamma = at::empty({n}, x.options());
+  at::Tensor dbeta = at::empty({n}, x.options());
+  const int64_t ws_bytes = cta_layernorm_bwd_workspace(rows, n);
+  at::Tensor ws = at::empty({std::max<int64_t>(1, ws_bytes / 4)}, x.options());
+  check_rc(cta_layernorm_bwd(xd.data_ptr<float>(), gd.data_ptr<float>(), md.data_ptr<float>(),
+                             rd.data_ptr<float>(), dd.data_ptr<float>(), rows, n,
+                             dx.data_ptr<float>(), dgamma.data_ptr<float>(),
+                             dbeta.data_ptr<float>(), ws.data_ptr<float>(), stream_of(x)));
+  return {dx, dgamma, dbeta};
+}
+
+// ------------------------------------------------------------------ naive attention
+// cf. Transformer_launchers/causal_self_attn_layer.cu:24-67
+std::tuple<at::Tensor, at::Tensor> causal_self_attention_fwd(at::Tensor qkv, int64_t nh,
+                                                             bool causal) {
+  TORCH_CHECK(qkv.dim() == 3, "qkv must be a 3D tensor (B, T, 3C)");
+  TORCH_CHECK(qkv.is_cuda(), "qkv must be a CUDA tensor");
+  TORCH_CHECK(qkv.is_contiguous(), "qkv must be contiguous");
+  check_f32(qkv, "qkv");
+  const int64_t B = qkv.size(0), T = qkv.size(1), C = qkv.size(2) / 3;
+  TORCH_CHECK(nh > 0 && C % nh == 0, "C must be divisible by nh");
+  c10::OptionalDeviceGuard guard(qkv.device());
+  const at::Tensor qd = dense(qkv);
+  at::Tensor s = at::empty({B, nh, T, T}, qkv.options());
+  at::Tensor out = at::empty({B, T, C}, qkv.options());
+  check_rc(cta_causal_self_attention_fwd(qd.data_ptr<float>(), B, T, C, nh, causal ? 1 : 0,
+                                         out.data_ptr<float>(), s.data_ptr<float>(),
+                                         stream_of(qkv)));
+  return {out, s};
+}
+
+// cf. causal_self_attn_layer.cu:70-132; inputs (B*nh, T, hs), probs (B*nh, T, T)
+std::tuple<at::Tensor, at::Tensor, at::Tensor> causal_self_attention_bwd(
+    at::Tensor Q, at::Tensor K, at::Tensor V, at::Tensor probs, at::Tensor dO) {
+  TORCH_CHECK(Q.is_cuda(), "q must be a CUDA tensor");
+  TORCH_CHECK(K.is_cuda(), "k must be a CUDA tensor");
+  TORCH_CHECK(V.is_cuda(), "v must be a CUDA tensor");
+  TORCH_CHECK(probs.is_cuda(), "probs must be a CUDA tensor");
+  TORCH_CHECK(dO.is_cuda(), "dO must be a CUDA tensor");
+  for (const auto* t : {&Q, &K, &V, &probs, &dO}) check_f32(*t, "input");
+  TORCH_CHECK(Q.dim() == 3, "Q must be (B*nh, T, hs)");
+  const int64_t BH = Q.size(0), T = Q.size(1), hs = Q.size(2);
+  TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes() && dO.sizes() == Q.sizes(),
+              "Q, K, V and dO must have the same shape");
+  TORCH_CHECK(probs.dim() == 3 && probs.size(0) == BH && probs.size(1) == T && probs.size(2) == T,
+              "probs must be (B*nh, T, T)");
+  c10::OptionalDeviceGuard guard(Q.device());
+  const at::Tensor pd = dense(probs);
+  at::Tensor dq = at::empty({BH, T, hs}, Q.options());
+  at::Tensor dk = at::empty({BH, T, hs}, Q.options());
+  at::Tensor dv = at::empty({BH, T, hs}, Q.options());
+  const int64_t ws_bytes = cta_causal_self_attention_bwd_workspace(BH, T);
+  at::Tensor ws = at::empty({std::max<int64_t>(1, ws_bytes / 4)}, Q.options());
+  const auto qs = strides_of<3>(Q), ks = strides_of<3>(K), vs = strides_of<3>(V),
+             gs = strides_of<3>(dO);
+  check_rc(cta_causal_self_attention_bwd(
+      Q.data_ptr<float>(), qs.data(), K.data_ptr<float>(), ks.data(), V.data_ptr<float>(),
+      vs.data(), pd.data_ptr<float>(), dO.data_ptr<float>(), gs.data(), BH, T, hs,
+      dq.data_ptr<float>(), dk.data_ptr<float>(), dv.data_ptr<float>(), ws.data_ptr<float>(),
+      stream_of(Q)));
+  return {dq, dk, dv};
+}
+
+// ------------------------------------------------------------------ FlashAttention-2
+// cf. Transformer_launchers/flash_attn_launcher.cu:22-65
+std::tuple<at::Tensor, at::Tensor> flash_attention_fwd(at::Tensor Q, at::Tensor K, at::Tensor V,
+                                                       bool causal) {
+  TORCH_CHECK(Q.dim() == 4, "Q must be a 4D tensor (B, nh, T, hs)");
+  const int64_t B = Q.size(0), nh = Q.size(1), T = Q.size(2), hs = Q.size(3);
+  TORCH_CHECK(Q.is_cuda(), "Q must be a CUDA tensor");
+  TORCH_CHECK(K.is_cuda(), "K must be a CUDA tensor");
+  TORCH_CHECK(V.is_cuda(), "V must be a CUDA tensor");
+  check_f32(Q, "Q");
+  check_f32(K, "K");
+  check_f32(V, "V");
+  TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes(), "Q, K and V must have the same shape");
+  c10::OptionalDeviceGuard guard(Q.device());
+  at::Tensor O = at::empty({B, nh, T, hs}, Q.options());
+  at::Tensor L = at::empty({B, nh, T}, Q.options());
+  if (hs != 32 && hs != 64 && hs != 128)
+    TORCH_CHECK(false, "Unsupported head dimension! Only hs=32, hs=64, and hs=128 are supported.");
+  const at::Tensor q = attn_operand(Q), k = attn_operand(K), v = attn_operand(V);
+  const auto qs = strides_of<4>(q), ks = strides_of<4>(k), vs = strides_of<4>(v);
+  check_rc(cta_flash_attention_fwd(q.data_ptr<float>(), qs.data(), k.data_ptr<float>(), ks.data(),
+                                   v.data_ptr<float>(), vs.data(), B, nh, T, hs, causal ? 1 : 0,
+                                   O.data_ptr<float>(), L.data_ptr<float>(), stream_of(Q)));
+  return {O, L};
+}
+
+// cf. flash_attn_launcher.cu:67-142
+std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd(at::Tensor Q, at::Tensor K,
+                                                                   at::Tensor V, at::Tensor O,
+                                                                   at::Tensor dO, at::Tensor L,
+                                                                   bool causal) {
+  TORCH_CHECK(Q.dim() == 4, "Q must be a 4D tensor (B, nh, T, hs)");
+  const int64_t B = Q.size(0), nh = Q.size(1), T = Q.size(2), hs = Q.size(3);
+  TORCH_CHECK(Q.is_cuda(), "Q must be a CUDA tensor");
+  TORCH_CHECK(K.is_cuda(), "K must be a CUDA tensor");
+  TORCH_CHECK(V.is_cuda(), "V must be a CUDA tensor");
+  TORCH_CHECK(O.is_cuda(), "O must be a CUDA tensor");
+  TORCH_CHECK(dO.is_cuda(), "dO must be a CUDA tensor");
+  TORCH_CHECK(L.is_cuda(), "L must be a CUDA tensor");
+  for (const auto* t : {&Q, &K, &V, &O, &dO, &L}) check_f32(*t, "input");
+  TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes() && O.sizes() == Q.sizes() &&
+                  dO.sizes() == Q.sizes(),
+              "Q, K, V, O and dO must have the same shape");
+  TORCH_CHECK(L.dim() == 3 && L.size(0) == B && L.size(1) == nh && L.size(2) == T,
+              "L must be (B, nh, T)");
+  c10::OptionalDeviceGuard guard(Q.device());
+  at::Tensor dQ = at::empty({B, nh, T, hs}, Q.options());
+  at::Tensor dK = at::empty({B, nh, T, hs}, Q.options());
+  at::Tensor dV = at::empty({B, nh, T, hs}, Q.options());
+  at::Tensor delta = at::empty({B, nh, T}, Q.options());
+  if (hs != 32 && hs != 64 && hs != 128)
+    TORCH_CHECK(false, "Unsupported head dimension! Only hs=32, hs=64, and hs=128 are supported.");
+  const at::Tensor q = attn_operand(Q), k = attn_operand(K), v = attn_operand(V),
+                   o = attn_operand(O), g = attn_operand(dO);
+  const auto qs = strides_of<4>(q), ks = strides_of<4>(k), vs = strides_of<4>(v),
+             os = strides_of<4>(o), gs = strides_of<4>(g);
+  const auto ls = strides_of<3>(L);
+  check_rc(cta_flash_attention_bwd(q.data_ptr<float>(), qs.data(), k.data_ptr<float>(), ks.data(),
+                                   v.data_ptr<float>(), vs.data(), o.data_ptr<float>(), os.data(),
+                                   g.data_ptr<float>(), gs.data(), L.data_ptr<float>(), ls.data(),
+                                   B, nh, T, hs, causal ? 1 : 0, dQ.data_ptr<float>(),
+                                   dK.data_ptr<float>(), dV.data_ptr<float>(),
+                                   delta.data_ptr<float>(), stream_of(Q)));
+  return {dQ, dK, dV};
+}
+
+}  // namespace
+
+TORCH_LIBRARY(cuda_transformer, m) {
+  m.def("cuda_fma(Tensor x, Tensor weights, Tensor bias) -> Tensor");
+  m.def("db_calculation(Tensor dy) -> Tensor");
+  m.def("gelu_activation(Tensor x) -> Tensor");
+  m.def("gelu_activation_bwd(Tensor x, Tensor dy) -> Tensor");
+  m.def("cuda_softmax(Tensor x) -> Tensor");
+  m.def("cuda_softmax_bwd(Tensor probs, Tensor dp) -> Tensor");
+  m.def("causal_self_attention_fwd(Tensor qkv, int nh, bool causal) -> (Tensor, Tensor)");
+  m.def(
+      "causal_self_attention_bwd(Tensor Q, Tensor K, Tensor V, Tensor probs, Tensor dO) -> "
+      "(Tensor, Tensor, Tensor)");
+  m.def("flash_attention_fwd(Tensor Q, Tensor K, Tensor V, bool causal) -> (Tensor, Tensor)");
+  m.def(
+      "flash_attention_bwd(Tensor Q, Tensor K, Tensor V, Tensor O, Tensor dO, Tensor L, bool "
+      "causal) -> (Tensor, Tensor, Tensor)");
+  m.def("layernorm_fwd(Tensor x, Tensor gamma, Tensor beta, float eps) -> (Tensor, Tensor, Tensor)");
+  m.def(
+      "layernorm_bwd(Tensor x, Tensor gamma, Tensor mean, Tensor rstd, Tensor dy) -> "
+      "(Tensor, Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(cuda_transformer, CUDA, m) {
+  m.impl("cuda_fma", &cuda_fma);
+  m.impl("db_calculation", &db_calculation);
+  m.impl("gelu_activation", &gelu_activation);
+  m.impl("gelu_activation_bwd", &gelu_activation_bwd);
+  m.impl("cuda_softmax", &cuda_softmax);
+  m.impl("cuda_softmax_bwd", &cuda_softmax_bwd);
+  m.impl("causal_self_attention_fwd", &causal_self_attention_fwd);
+  m.impl("causal_self_attention_bwd", &causal_self_attention_bwd);
+  m.impl("flash_attention_fwd", &flash_attention_fwd);
+  m.impl("flash_attention_bwd", &flash_attention_bwd);
+  m.impl("layernorm_fwd", &layernorm_fwd);
+  m.impl("layernorm_bwd", &layernorm_bwd);
+}
+
+}  // namespace cuda_transformer
+
+// Importable as cuda_transformer_amd._C (the reference imports cuda_transformer._C); importing
+// it runs the static registrations above.
+extern "C" PyObject* PyInit__C(void) {
+  static struct PyModuleDef def = {PyModuleDef_HEAD_INIT, "_C",
+                                   "gfx950 FP32 transformer kernels: torch operator library",
+                                   -1, nullptr, nullptr, nullptr, nullptr, nullptr};
+  return PyModule_Create(&def);
+}

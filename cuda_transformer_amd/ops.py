@@ -1,0 +1,193 @@
+"""Python wrappers of the ``cuda_transformer`` operators, with fake (meta) kernels.
+
+Mirrors the reference's cuda_transformer/ops.py:1-138: the same ten functions, calling
+``torch.ops.cuda_transformer.<op>.default`` and registering ``torch.library.register_fake``
+shape functions for FakeTensor / ``torch.compile`` tracing.  Two deviations, both fixes:
+
+* the fake of ``gelu_activation_bwd`` checks ``dy.dtype`` (ops.py:73 reads ``dy.type``, which
+  is a method and never equals ``torch.float32``);
+* the fake of ``causal_self_attention_fwd`` returns probs of shape (B, nh, T, T) — the real
+  operator's shape (causal_self_attn_layer.cu:36) — where ops.py:81-89 says (B, T, T).
+
+Added: ``layernorm_fwd`` / ``layernorm_bwd`` (the reference's LayerNorm is plain torch,
+gpt/gpt.py:47-59).
+"""
+import torch
+from torch import Tensor
+
+__all__ = [
+    "cuda_fma", "db_calculation",
+    "cuda_softmax", "cuda_softmax_bwd",
+    "gelu_activation", "gelu_activation_bwd",
+    "causal_self_attention_fwd", "causal_self_attention_bwd",
+    "flash_attention_fwd", "flash_attention_bwd",
+    "layernorm_fwd", "layernorm_bwd",
+]
+
+_ops = torch.ops.cuda_transformer
+
+
+def _f32(*ts):
+    for t in ts:
+        torch._check(t.dtype == torch.float32)
+
+
+def _same_device(*ts):
+    torch._check(all(t.device == ts[0].device for t in ts))
+
+
+# ----------------------------------------------------------------- linear layer
+def cuda_fma(x: Tensor, weights: Tensor, bias: Tensor) -> Tensor:
+    """out[b] = x[b] @ weights[b or 0] + bias  (reference ops.py:13-15)."""
+    return _ops.cuda_fma.default(x, weights, bias)
+
+
+@torch.library.register_fake("cuda_transformer::cuda_fma")
+def _(x, weights, bias):
+    _f32(x, weights, bias)
+    _same_device(x, weights, bias)
+    w = weights if weights.dim() == 3 else weights.unsqueeze(0)
+    return torch.empty(x.size(0), x.size(1), w.size(2), dtype=x.dtype, device=x.device)
+
+
+def db_calculation(dy: Tensor) -> Tensor:
+    """Bias gradient: sum of dy over (batch, rows)  (reference ops.py:26-28)."""
+    return _ops.db_calculation.default(dy)
+
+
+@torch.library.register_fake("cuda_transformer::db_calculation")
+def _(dy):
+    _f32(dy)
+    return torch.empty(dy.size(-1), dtype=dy.dtype, device=dy.device)
+
+
+# ----------------------------------------------------------------- softmax
+def cuda_softmax(x: Tensor) -> Tensor:
+    """Row softmax over the last dim of a 3-D tensor  (reference ops.py:36-38)."""
+    return _ops.cuda_softmax.default(x)
+
+
+@torch.library.register_fake("cuda_transformer::cuda_softmax")
+def _(x):
+    _f32(x)
+    return torch.empty_like(x)
+
+
+def cuda_softmax_bwd(probs: Tensor, dp: Tensor) -> Tensor:
+    """dx = probs * (dp - sum(probs * dp))  (reference ops.py:45-47)."""
+    return _ops.cuda_softmax_bwd.default(probs, dp)
+
+
+@torch.library.register_fake("cuda_transformer::cuda_softmax_bwd")
+def _(probs, dp):
+    _f32(probs, dp)
+    _same_device(probs, dp)
+    return torch.empty_like(probs)
+
+
+# ----------------------------------------------------------------- GELU
+def gelu_activation(x: Tensor) -> Tensor:
+    """Exact (erf) GELU  (reference ops.py:56-58)."""
+    return _ops.gelu_activation.default(x)
+
+
+@torch.library.register_fake("cuda_transformer::gelu_activation")
+def _(x):
+    _f32(x)
+    return torch.empty_like(x)
+
+
+def gelu_activation_bwd(x: Tensor, dy: Tensor) -> Tensor:
+    """GELU input gradient  (reference ops.py:66-68)."""
+    return _ops.gelu_activation_bwd.default(x, dy)
+
+
+@torch.library.register_fake("cuda_transformer::gelu_activation_bwd")
+def _(x, dy):
+    _f32(x, dy)
+    _same_device(x, dy)
+    return torch.empty_like(x)
+
+
+# ----------------------------------------------------------------- naive attention
+def causal_self_attention_fwd(qkv: Tensor, nh: int, causal: bool) -> tuple[Tensor, Tensor]:
+    """Materialised attention over packed qkv (B, T, 3C) -> (out, probs)  (ops.py:78-80)."""
+    return _ops.causal_self_attention_fwd.default(qkv, nh, causal)
+
+
+@torch.library.register_fake("cuda_transformer::causal_self_attention_fwd")
+def _(qkv, nh, causal):
+    _f32(qkv)
+    b, t, three_c = qkv.shape
+    c = three_c // 3
+    out = torch.empty((b, t, c), dtype=qkv.dtype, device=qkv.device)
+    probs = torch.empty((b, nh, t, t), dtype=qkv.dtype, device=qkv.device)
+    return out, probs
+
+
+def causal_self_attention_bwd(Q: Tensor, K: Tensor, V: Tensor, probs: Tensor, dO: Tensor):
+    """Naive attention backward on (B*nh, T, hs); dq, dk unscaled  (ops.py:91-93)."""
+    return _ops.causal_self_attention_bwd.default(Q, K, V, probs, dO)
+
+
+@torch.library.register_fake("cuda_transformer::causal_self_attention_bwd")
+def _(Q, K, V, probs, dO):
+    _f32(Q, K, V, probs, dO)
+    _same_device(Q, K, V, probs, dO)
+    return torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
+
+
+# ----------------------------------------------------------------- FlashAttention-2
+def flash_attention_fwd(Q: Tensor, K: Tensor, V: Tensor, causal: bool) -> tuple[Tensor, Tensor]:
+    """FA2 forward -> (O, L), L = rowmax + ln(rowsum)  (reference ops.py:109-111)."""
+    return _ops.flash_attention_fwd.default(Q, K, V, causal)
+
+
+@torch.library.register_fake("cuda_transformer::flash_attention_fwd")
+def _(Q, K, V, causal):
+    _f32(Q, K, V)
+    _same_device(Q, K, V)
+    O = torch.empty((Q.size(0), Q.size(1), Q.size(2), Q.size(3)), dtype=Q.dtype, device=Q.device)
+    L = torch.empty((Q.size(0), Q.size(1), Q.size(2)), dtype=Q.dtype, device=Q.device)
+    return O, L
+
+
+def flash_attention_bwd(Q: Tensor, K: Tensor, V: Tensor, O: Tensor, dO: Tensor, L: Tensor,
+                        causal: bool):
+    """FA2 backward -> (dQ, dK, dV)  (reference ops.py:123-125)."""
+    return _ops.flash_attention_bwd.default(Q, K, V, O, dO, L, causal)
+
+
+@torch.library.register_fake("cuda_transformer::flash_attention_bwd")
+def _(Q, K, V, O, dO, L, causal):
+    _f32(Q, K, V, O, dO, L)
+    _same_device(Q, K, V, O, dO, L)
+    return torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
+
+
+# ----------------------------------------------------------------- LayerNorm (added)
+def layernorm_fwd(x: Tensor, gamma: Tensor, beta: Tensor, eps: float = 1e-5):
+    """LayerNorm over the last dim -> (y, mean, rstd); semantics of gpt/gpt.py:47-59."""
+    return _ops.layernorm_fwd.default(x, gamma, beta, eps)
+
+
+@torch.library.register_fake("cuda_transformer::layernorm_fwd")
+def _(x, gamma, beta, eps):
+    _f32(x, gamma, beta)
+    _same_device(x, gamma, beta)
+    stat = torch.empty(x.shape[:-1], dtype=x.dtype, device=x.device)
+    return torch.empty_like(x), stat, torch.empty_like(stat)
+
+
+def layernorm_bwd(x: Tensor, gamma: Tensor, mean: Tensor, rstd: Tensor, dy: Tensor):
+    """LayerNorm backward -> (dx, dgamma, dbeta)."""
+    return _ops.layernorm_bwd.default(x, gamma, mean, rstd, dy)
+
+
+@torch.library.register_fake("cuda_transformer::layernorm_bwd")
+def _(x, gamma, mean, rstd, dy):
+    _f32(x, gamma, mean, rstd, dy)
+    _same_device(x, gamma, mean, rstd, dy)
+    n = x.size(-1)
+    return (torch.empty_like(x), torch.empty(n, dtype=x.dtype, device=x.device),
+            torch.empty(n, dtype=x.dtype, device=x.device))

@@ -1,0 +1,192 @@
+/*
+ * cuda_transformer_amd — C ABI of the MI355X (gfx950) FP32 transformer kernels.
+ *
+ * This is the drop-in boundary.  Each entry point replaces one launcher of the
+ * reference's PyTorch extension (the .cu files of Transformer_launchers/) with plain
+ * pointers, sizes and strides; no torch type appears here, so any FFI (ctypes, cgo, JNI,
+ * N-API) can bind it.  The torch operator layer (cuda_transformer::* schemas) sits
+ * on top of these functions.
+ *
+ * Conventions shared by every entry point
+ *  - Tensors are FP32, device-resident (HIP device pointers).
+ *  - Strides are in elements, outermost first.  Outputs are always dense
+ *    row-major ("contiguous"), exactly as the reference launchers allocate them.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).  Every
+ *    call is asynchronous on that stream; nothing synchronises the host.
+ *  - Return value: CTA_OK (0) or one of the CTA_ERR_* codes; cta_last_error()
+ *    then returns a message for the calling thread.  Messages for conditions the
+ *    reference checks use the reference's wording.
+ */
+#ifndef CUDA_TRANSFORMER_AMD_H
+#define CUDA_TRANSFORMER_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  CTA_OK = 0,
+  CTA_ERR_INVALID_ARGUMENT = 1,     /* bad size / null pointer / mismatched shapes          */
+  CTA_ERR_UNSUPPORTED_HEAD_DIM = 2, /* head size outside {32, 64, 128}                      */
+  CTA_ERR_LAYOUT = 3,               /* stride or alignment the kernel cannot read directly   */
+  CTA_ERR_LAUNCH = 4                /* the HIP runtime rejected a kernel launch              */
+};
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* cta_last_error(void);
+
+/* Library version string. */
+const char* cta_version(void);
+
+/* ------------------------------------------------------------------------------
+ * FlashAttention-2, FP32.  Shapes (B, nh, T, hs); hs in {32, 64, 128}.
+ * softmax scale = 1/sqrt(hs) (the reference launcher passes sqrt(hs) and the
+ * kernel inverts it: flash_attn_launcher.cu:27, flash_attention.cuh:45).
+ * Q/K/V/O/dO strides: 4 entries (b, h, t, d).  The kernels need d-stride 1, other
+ * strides divisible by 4 and 16-byte aligned base pointers (CTA_ERR_LAYOUT
+ * otherwise; the torch layer passes a dense copy in that case).
+ * L strides: 3 entries (b, h, t), any values.
+ * ---------------------------------------------------------------------------- */
+
+/* Forward: O (B,nh,T,hs) dense, L (B,nh,T) dense with L = rowmax + ln(rowsum).
+ * Replaces cuda_transformer::flash_attention_fwd
+ * (Transformer_launchers/flash_attn_launcher.cu:22-65). */
+int cta_flash_attention_fwd(const float* q, const int64_t* q_strides,
+                            const float* k, const int64_t* k_strides,
+                            const float* v, const int64_t* v_strides,
+                            int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                            float* o, float* l, void* stream);
+
+/* Backward, all three stages in stream order: delta, then dQ and dK/dV.
+ * `delta` is caller-provided scratch of B*nh*T floats (the reference allocates it
+ * inside the launcher).  dq/dk/dv are dense (B,nh,T,hs).
+ * Replaces cuda_transformer::flash_attention_bwd (flash_attn_launcher.cu:67-142). */
+int cta_flash_attention_bwd(const float* q, const int64_t* q_strides,
+                            const float* k, const int64_t* k_strides,
+                            const float* v, const int64_t* v_strides,
+                            const float* o, const int64_t* o_strides,
+                            const float* d_o, const int64_t* do_strides,
+                            const float* l, const int64_t* l_strides,
+                            int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                            float* dq, float* dk, float* dv, float* delta, void* stream);
+
+/* Stage 1 of the backward: delta[b,h,t] = sum_d O*dO, dense (B,nh,T).
+ * Replaces the flash_attention_bwd_delta launch (flash_attn_launcher.cu:107-108). */
+int cta_flash_attention_bwd_delta(const float* o, const int64_t* o_strides,
+                                  const float* d_o, const int64_t* do_strides,
+                                  int64_t B, int64_t nh, int64_t T, int64_t hs,
+                                  float* delta, void* stream);
+
+/* Stage 2: dQ.  Replaces the flash_attention_bwd_dq launch (flash_attn_launcher.cu:111,118,125). */
+int cta_flash_attention_bwd_dq(const float* q, const int64_t* q_strides,
+                               const float* k, const int64_t* k_strides,
+                               const float* v, const int64_t* v_strides,
+                               const float* d_o, const int64_t* do_strides,
+                               const float* l, const int64_t* l_strides,
+                               const float* delta,
+                               int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                               float* dq, void* stream);
+
+/* Stage 3: dK and dV.  Replaces the flash_attention_bwd_dk_dv launch
+ * (flash_attn_launcher.cu:114,121,131). */
+int cta_flash_attention_bwd_dkdv(const float* q, const int64_t* q_strides,
+                                 const float* k, const int64_t* k_strides,
+                                 const float* v, const int64_t* v_strides,
+                                 const float* d_o, const int64_t* do_strides,
+                                 const float* l, const int64_t* l_strides,
+                                 const float* delta,
+                                 int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                                 float* dk, float* dv, void* stream);
+
+/* ------------------------------------------------------------------------------
+ * Linear layer.
+ * ---------------------------------------------------------------------------- */
+
+/* out[b] = x[b] . W[b or 0] + bias, out dense (batch, m, n).
+ * x strides: 3 entries (batch, m, k).  W strides: 3 entries (batch, k, n); w_batch is 1
+ * (broadcast, batch stride ignored) or `batch`.  Any strides: transposed views are read
+ * in place.  Replaces cuda_transformer::cuda_fma (Transformer_launchers/linear_layer.cu:28-70). */
+int cta_cuda_fma(const float* x, const int64_t* x_strides,
+                 const float* w, const int64_t* w_strides,
+                 const float* bias, int64_t bias_stride,
+                 int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
+                 float* out, void* stream);
+
+/* Bytes of scratch cta_db_calculation needs for a (batch, m, n) gradient. */
+int64_t cta_db_calculation_workspace(int64_t batch, int64_t m, int64_t n);
+
+/* db[n] = sum over (batch, m) of dy; dy strides: 3 entries.  Deterministic (no atomics).
+ * Replaces cuda_transformer::db_calculation (linear_layer.cu:74-97). */
+int cta_db_calculation(const float* dy, const int64_t* dy_strides,
+                       int64_t batch, int64_t m, int64_t n,
+                       float* db, float* workspace, void* stream);
+
+/* ------------------------------------------------------------------------------
+ * Elementwise / row kernels (dense inputs, as the reference launchers require).
+ * ---------------------------------------------------------------------------- */
+
+/* y = x * Phi(x) (exact erf GELU).  Replaces cuda_transformer::gelu_activation
+ * (Transformer_launchers/gelu_activation.cu:22-47). */
+int cta_gelu_fwd(const float* x, float* y, int64_t numel, void* stream);
+
+/* dx = dy * (Phi(x) + x * phi(x)).  Replaces cuda_transformer::gelu_activation_bwd
+ * (gelu_activation.cu:49-77). */
+int cta_gelu_bwd(const float* x, const float* dy, float* dx, int64_t numel, void* stream);
+
+/* Row softmax over `rows` rows of length n.  Replaces cuda_transformer::cuda_softmax
+ * (Transformer_launchers/softmax_layer.cu:22-47). */
+int cta_softmax_fwd(const float* x, float* y, int64_t rows, int64_t n, void* stream);
+
+/* dx = p * (dp - sum(p * dp)) per row.  Replaces cuda_transformer::cuda_softmax_bwd
+ * (softmax_layer.cu:50-78). */
+int cta_softmax_bwd(const float* probs, const float* dp, float* dx,
+                    int64_t rows, int64_t n, void* stream);
+
+/* LayerNorm over the last dimension (no reference kernel; semantics of gpt/gpt.py:47-59):
+ * y = (x - mean) * rstd * gamma + beta, rstd = 1/sqrt(biased var + eps).
+ * Also writes mean and rstd (rows floats each) for the backward. */
+int cta_layernorm_fwd(const float* x, const float* gamma, const float* beta,
+                      int64_t rows, int64_t n, float eps,
+                      float* y, float* mean, float* rstd, void* stream);
+
+/* Bytes of scratch cta_layernorm_bwd needs. */
+int64_t cta_layernorm_bwd_workspace(int64_t rows, int64_t n);
+
+/* dx, dgamma, dbeta of the LayerNorm above.  Deterministic (no atomics). */
+int cta_layernorm_bwd(const float* x, const float* gamma, const float* mean,
+                      const float* rstd, const float* dy, int64_t rows, int64_t n,
+                      float* dx, float* dgamma, float* dbeta, float* workspace, void* stream);
+
+/* ------------------------------------------------------------------------------
+ * Materialised causal self-attention (API parity with the reference's naive path).
+ * ---------------------------------------------------------------------------- */
+
+/* qkv dense (B, T, 3C); returns out dense (B, T, C) and probs dense (B, nh, T, T).
+ * Replaces cuda_transformer::causal_self_attention_fwd
+ * (Transformer_launchers/causal_self_attn_layer.cu:24-67). */
+int cta_causal_self_attention_fwd(const float* qkv, int64_t B, int64_t T, int64_t C,
+                                  int64_t nh, int causal, float* out, float* probs,
+                                  void* stream);
+
+/* Bytes of scratch cta_causal_self_attention_bwd needs (one (BH, T, T) buffer). */
+int64_t cta_causal_self_attention_bwd_workspace(int64_t BH, int64_t T);
+
+/* Q, K, V, dO: (BH, T, hs) with 3 strides each; probs dense (BH, T, T).  Returns dense
+ * dq, dk (unscaled: the caller divides by sqrt(hs)) and dv.
+ * Replaces cuda_transformer::causal_self_attention_bwd (causal_self_attn_layer.cu:70-132). */
+int cta_causal_self_attention_bwd(const float* q, const int64_t* q_strides,
+                                  const float* k, const int64_t* k_strides,
+                                  const float* v, const int64_t* v_strides,
+                                  const float* probs,
+                                  const float* d_o, const int64_t* do_strides,
+                                  int64_t BH, int64_t T, int64_t hs,
+                                  float* dq, float* dk, float* dv, float* workspace,
+                                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUDA_TRANSFORMER_AMD_H */

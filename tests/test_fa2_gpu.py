@@ -1,0 +1,187 @@
+"""FlashAttention-2 forward/backward on the GPU vs the CPU oracle (float64).
+
+Shapes: the reference's own parametrisation (test/test_flash_attention.py:52-60, including
+ragged T and hs in {32, 64, 128}) and BASELINE config 1 (B1 H4 N256 D64).  Tolerances: the
+reference suite's allclose (O, L atol 1e-5; grads atol 1e-4, rtol 1e-5) and BASELINE's bar
+(O max-abs <= 1e-4, dQ/dK/dV relative L2 error <= 1e-3).  Like the reference test, the
+backward is fed the oracle's L and the kernel's own O (test_flash_attention.py:48).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_rel_err, f64, seeded
+from oracle import attention as ora
+
+pytestmark = pytest.mark.gpu
+
+REF_SHAPES = [
+    (1, 1, 64, 128, False),
+    (1, 1, 64, 128, True),
+    (1, 1, 65, 64, True),
+    (2, 4, 128, 32, False),
+    (2, 4, 128, 64, True),
+    (2, 4, 257, 64, True),
+    (1, 2, 512, 128, True),
+    (1, 4, 256, 64, True),
+    (1, 4, 256, 64, False),
+    (1, 3, 1, 64, True),     # single row
+    (2, 2, 129, 32, True),
+    (1, 2, 200, 128, False),
+]
+
+
+def _inputs(B, nh, T, hs, seed):
+    q = seeded((B, nh, T, hs), seed)
+    k = seeded((B, nh, T, hs), seed + 1)
+    v = seeded((B, nh, T, hs), seed + 2)
+    do = seeded((B, nh, T, hs), seed + 3, kind="rand")  # dO ~ U[0,1), as the reference test
+    return q, k, v, do
+
+
+@pytest.mark.parametrize("B,nh,T,hs,causal", REF_SHAPES)
+def test_fa2_matches_oracle(cuda, B, nh, T, hs, causal):
+    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+
+    q, k, v, do = _inputs(B, nh, T, hs, seed=1000 + T + hs)
+    O, L = flash_attention_fwd(q.to(cuda), k.to(cuda), v.to(cuda), causal)
+    O_ref, L_ref = ora.reference_attention(f64(q), f64(k), f64(v), causal)
+    np.testing.assert_allclose(f64(O), O_ref, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(f64(L), L_ref, rtol=1e-5, atol=1e-5)
+    assert np.abs(f64(O) - O_ref).max() <= 1e-4
+
+    L_in = torch.from_numpy(L_ref.astype(np.float32))
+    dq, dk, dv = flash_attention_bwd(q.to(cuda), k.to(cuda), v.to(cuda), O, do.to(cuda),
+                                     L_in.to(cuda), causal)
+    dq_r, dk_r, dv_r = ora.fa2_backward(f64(q), f64(k), f64(v), O_ref, f64(do), L_ref, causal,
+                                        br=64, bc=64)
+    for got, ref in ((dq, dq_r), (dk, dk_r), (dv, dv_r)):
+        np.testing.assert_allclose(f64(got), ref, rtol=1e-5, atol=1e-4)
+        assert_rel_err(f64(got), ref, 1e-3)
+
+
+def test_fa2_strided_views_match_dense(cuda):
+    """q, k, v as head views of a packed (B, T, 3C) projection (gpt/gpt.py:104-107), dO as a
+    transposed view: read in place through strides, bitwise equal to dense copies."""
+    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+
+    B, T, nh, hs = 2, 193, 4, 64
+    C = nh * hs
+    qkv = seeded((B, T, 3 * C), 7).to(cuda)
+    q, k, v = (t.reshape(B, T, nh, hs).transpose(1, 2) for t in qkv.chunk(3, dim=-1))
+    assert not q.is_contiguous()
+    O, L = flash_attention_fwd(q, k, v, True)
+    Oc, Lc = flash_attention_fwd(q.contiguous(), k.contiguous(), v.contiguous(), True)
+    assert torch.equal(O, Oc) and torch.equal(L, Lc)
+    do = seeded((B, T, nh, hs), 8).to(cuda).transpose(1, 2)
+    g1 = flash_attention_bwd(q, k, v, O, do, L, True)
+    g2 = flash_attention_bwd(q.contiguous(), k.contiguous(), v.contiguous(), O, do.contiguous(),
+                             L, True)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+def test_fa2_misaligned_view_falls_back_to_copy(cuda):
+    from cuda_transformer.ops import flash_attention_fwd
+
+    base = seeded((1 * 2 * 70 * 64 + 1,), 3).to(cuda)
+    q = base[1:].reshape(1, 2, 70, 64)  # 4-byte offset: not 16-byte aligned
+    O, L = flash_attention_fwd(q, q, q, False)
+    O2, L2 = flash_attention_fwd(q.clone(), q.clone(), q.clone(), False)
+    assert torch.equal(O, O2) and torch.equal(L, L2)
+
+
+def test_fa2_deterministic(cuda):
+    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+
+    q, k, v, do = (t.to(cuda) for t in _inputs(2, 3, 300, 64, seed=5))
+    r1 = flash_attention_fwd(q, k, v, True)
+    r2 = flash_attention_fwd(q, k, v, True)
+    assert all(torch.equal(a, b) for a, b in zip(r1, r2))
+    g1 = flash_attention_bwd(q, k, v, r1[0], do, r1[1], True)
+    g2 = flash_attention_bwd(q, k, v, r1[0], do, r1[1], True)
+    assert all(torch.equal(a, b) for a, b in zip(g1, g2))
+
+
+def test_fa2_unsupported_head_dim(cuda):
+    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+
+    q = torch.randn(1, 1, 16, 48, device=cuda)
+    with pytest.raises(RuntimeError, match="Unsupported head dimension"):
+        flash_attention_fwd(q, q, q, True)
+    L = torch.zeros(1, 1, 16, device=cuda)
+    with pytest.raises(RuntimeError, match="Unsupported head dimension"):
+        flash_attention_bwd(q, q, q, q, q, L, True)
+
+
+def test_fa2_autograd_function(cuda):
+    """CudaFlashAttention.apply + .backward, as gpt.py and the benchmark drive it."""
+    from cuda_autograd_fns import CudaFlashAttention
+
+    q, k, v, do = _inputs(1, 2, 130, 64, seed=11)
+    qg, kg, vg = (t.to(cuda).requires_grad_() for t in (q, k, v))
+    o, l = CudaFlashAttention.apply(qg, kg, vg, True)
+    o.backward(do.to(cuda))
+    O_ref, L_ref = ora.reference_attention(f64(q), f64(k), f64(v), True)
+    dq_r, dk_r, dv_r = ora.fa2_backward(f64(q), f64(k), f64(v), O_ref, f64(do), L_ref, True)
+    np.testing.assert_allclose(f64(o), O_ref, atol=1e-5, rtol=1e-5)
+    for got, ref in ((qg.grad, dq_r), (kg.grad, dk_r), (vg.grad, dv_r)):
+        np.testing.assert_allclose(f64(got), ref, atol=1e-4, rtol=1e-5)
+
+
+def test_fa2_through_c_abi(cuda):
+    """Call the C entry points directly (ctypes) and compare bitwise with the torch op."""
+    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+    from cuda_transformer_amd import capi
+
+    B, nh, T, hs = 1, 2, 97, 64
+    q, k, v, do = (t.to(cuda) for t in _inputs(B, nh, T, hs, seed=21))
+    O = torch.empty_like(q)
+    L = torch.empty(B, nh, T, device=cuda)
+    st = torch.cuda.current_stream().cuda_stream
+    s4 = capi.strides(q.stride())
+    capi.call("cta_flash_attention_fwd", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(), s4,
+              B, nh, T, hs, 1, O.data_ptr(), L.data_ptr(), st)
+    O2, L2 = flash_attention_fwd(q, k, v, True)
+    torch.cuda.synchronize()
+    assert torch.equal(O, O2) and torch.equal(L, L2)
+    dq, dk, dv, delta = (torch.empty_like(q), torch.empty_like(q), torch.empty_like(q),
+                         torch.empty(B, nh, T, device=cuda))
+    s3 = capi.strides(L.stride())
+    capi.call("cta_flash_attention_bwd", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(), s4,
+              O.data_ptr(), s4, do.data_ptr(), s4, L.data_ptr(), s3, B, nh, T, hs, 1,
+              dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), st)
+    g = flash_attention_bwd(q, k, v, O, do, L, True)
+    torch.cuda.synchronize()
+    assert torch.equal(dq, g[0]) and torch.equal(dk, g[1]) and torch.equal(dv, g[2])
+    np.testing.assert_allclose(f64(delta), (f64(O) * f64(do)).sum(-1), rtol=1e-5, atol=1e-5)
+    with pytest.raises(capi.CtaError, match="Unsupported head dimension"):
+        capi.call("cta_flash_attention_fwd", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(),
+                  s4, B, nh, T, 96, 1, O.data_ptr(), L.data_ptr(), st)
+
+
+def test_fa2_config2_full_size(cuda):
+    """BASELINE config 2 (B4 H32 N4096 D64, causal) at full size: two heads against the
+    float64 oracle, and on every head the size-independent invariants of the backward:
+    sum_j dK_j = 0 (rows of dS sum to zero) and sum_j dV_j = sum_i dO_i (rows of P sum to 1)."""
+    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+
+    B, nh, T, hs = 4, 32, 4096, 64
+    q, k, v, do = (t.to(cuda) for t in _inputs(B, nh, T, hs, seed=2024))
+    O, L = flash_attention_fwd(q, k, v, True)
+    dq, dk, dv = flash_attention_bwd(q, k, v, O, do, L, True)
+    torch.cuda.synchronize()
+    for t in (O, L, dq, dk, dv):
+        assert torch.isfinite(t).all()
+    for (b, h) in ((0, 0), (3, 31)):
+        qh, kh, vh, doh = (f64(t[b:b + 1, h:h + 1]) for t in (q, k, v, do))
+        O_ref, L_ref = ora.reference_attention(qh, kh, vh, True)
+        assert np.abs(f64(O[b:b + 1, h:h + 1]) - O_ref).max() <= 1e-4
+        np.testing.assert_allclose(f64(L[b:b + 1, h:h + 1]), L_ref, atol=1e-4, rtol=1e-5)
+        g_ref = ora.fa2_backward(qh, kh, vh, O_ref, doh, L_ref, True, br=512, bc=512)
+        for got, ref in zip((dq, dk, dv), g_ref):
+            assert_rel_err(f64(got[b:b + 1, h:h + 1]), ref, 1e-3)
+    sum_dk = dk.double().sum(dim=2)
+    assert sum_dk.abs().max().item() <= 1e-3 * dk.double().abs().sum(dim=2).max().item()
+    torch.testing.assert_close(dv.double().sum(dim=2), do.double().sum(dim=2), rtol=1e-6,
+                               atol=1e-2)

@@ -1,0 +1,192 @@
+"""Linear, db, GELU, softmax, LayerNorm and naive attention on the GPU vs the CPU oracle.
+
+Shapes follow the reference suite (test/test_linear.py:53-59, test_gelu.py:36-42,
+test_softmax.py:33-39, test_causal_self_attn.py:69-77) plus BASELINE config 4 (GPT-2-small
+widths).  Tolerances: the reference's allclose atol 1e-5 (rtol 1e-5) on U[0,1) inputs; for
+config 4 the GEMM is checked by relative error (K = 768/3072 FP32 sums).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import f64, rel_err, seeded
+from oracle import attention as ora
+from oracle import elementwise as ew
+from oracle import linear as lin
+
+pytestmark = pytest.mark.gpu
+
+LINEAR_SHAPES = [(1, 32, 64, 32), (1, 32, 65, 32), (2, 64, 32, 64), (2, 128, 32, 64),
+                 (1, 512, 70, 120), (3, 33, 129, 257)]
+ROW_SHAPES = [(1, 64, 32), (1, 65, 32), (2, 32, 64), (4, 128, 64), (1, 70, 120), (2, 5, 1000),
+              (1, 3, 2049), (1, 2, 5000), (3, 7, 4096)]
+
+
+@pytest.mark.parametrize("B,T,fin,fout", LINEAR_SHAPES)
+def test_linear_forward_backward(cuda, B, T, fin, fout):
+    from cuda_autograd_fns import CudaLinearLayer
+    from cuda_transformer.ops import cuda_fma, db_calculation
+
+    x = seeded((B, T, fin), 1, kind="rand")
+    w = seeded((fin, fout), 2) * 0.1
+    b = seeded((fout,), 3) * 0.1
+    dy = seeded((B, T, fout), 4, kind="rand")
+    out = cuda_fma(x.to(cuda), w.to(cuda), b.to(cuda))
+    np.testing.assert_allclose(f64(out), lin.fma_forward(f64(x), f64(w), f64(b)), atol=1e-5,
+                               rtol=1e-5)
+    # the reference test's own backward composition (test_linear.py:33-51)
+    w3 = w.to(cuda).unsqueeze(0).transpose(1, 2)
+    dx = cuda_fma(dy.to(cuda), w3, torch.zeros(fin, device=cuda))
+    dw = cuda_fma(dy.to(cuda).transpose(1, 2), x.to(cuda), torch.zeros(fin, device=cuda)).sum(0)
+    db = db_calculation(dy.to(cuda))
+    dx_r, dw_r, db_r = lin.linear_backward(f64(x), f64(w), f64(dy))
+    np.testing.assert_allclose(f64(dx), dx_r, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(f64(dw), dw_r.T, atol=1e-4, rtol=1e-5)
+    np.testing.assert_allclose(f64(db), db_r, atol=1e-4, rtol=1e-5)
+    # autograd wrapper
+    xg = x.to(cuda).requires_grad_()
+    wg = w.to(cuda).requires_grad_()
+    bg = b.to(cuda).requires_grad_()
+    CudaLinearLayer.apply(xg, wg, bg).backward(dy.to(cuda))
+    np.testing.assert_allclose(f64(xg.grad), dx_r, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(f64(wg.grad), dw_r, atol=1e-4, rtol=1e-5)
+    np.testing.assert_allclose(f64(bg.grad), db_r, atol=1e-4, rtol=1e-5)
+
+
+def test_linear_batched_weights_and_errors(cuda):
+    from cuda_transformer.ops import cuda_fma
+
+    x = seeded((3, 40, 24), 1).to(cuda)
+    w = seeded((3, 24, 36), 2).to(cuda)
+    b = seeded((36,), 3).to(cuda)
+    out = cuda_fma(x, w, b)
+    np.testing.assert_allclose(f64(out), lin.fma_forward(f64(x), f64(w), f64(b)), atol=1e-4,
+                               rtol=1e-5)
+    with pytest.raises(RuntimeError, match="weights.size\\(1\\) must match x.size\\(2\\)"):
+        cuda_fma(x, w[:, :20], b)
+    with pytest.raises(RuntimeError, match="bias.size\\(0\\) must match weights.size\\(2\\)"):
+        cuda_fma(x, w, b[:30])
+
+
+def test_linear_config4(cuda):
+    """X[8192,768] . W[768,3072] + b, X and W ~ N(0, 0.02^2)."""
+    from cuda_autograd_fns import CudaLinearLayer
+
+    x = seeded((1, 8192, 768), 40, scale=0.02)
+    w = seeded((768, 3072), 41, scale=0.02)
+    b = seeded((3072,), 42, scale=0.02)
+    dy = seeded((1, 8192, 3072), 43, scale=0.02)
+    xg, wg, bg = (t.to(cuda).requires_grad_() for t in (x, w, b))
+    out = CudaLinearLayer.apply(xg, wg, bg)
+    out.backward(dy.to(cuda))
+    ref = lin.fma_forward(f64(x), f64(w), f64(b))
+    assert rel_err(f64(out), ref) <= 1e-5
+    dx_r, dw_r, db_r = lin.linear_backward(f64(x), f64(w), f64(dy))
+    assert rel_err(f64(xg.grad), dx_r) <= 1e-5
+    assert rel_err(f64(wg.grad), dw_r) <= 1e-5
+    assert rel_err(f64(bg.grad), db_r) <= 1e-5
+
+
+@pytest.mark.parametrize("batch,m,n", ROW_SHAPES[:5] + [(1, 8192, 3072)])
+def test_gelu(cuda, batch, m, n):
+    from cuda_autograd_fns import CudaGeluLayer
+    from cuda_transformer.ops import gelu_activation, gelu_activation_bwd
+
+    x = seeded((batch, m, n), 5, kind="rand") * 6 - 3  # covers the negative tail too
+    dy = seeded((batch, m, n), 6, kind="rand")
+    y = gelu_activation(x.to(cuda))
+    np.testing.assert_allclose(f64(y), ew.gelu_forward(f64(x)), atol=1e-5, rtol=1e-5)
+    dx = gelu_activation_bwd(x.to(cuda), dy.to(cuda))
+    np.testing.assert_allclose(f64(dx), ew.gelu_backward(f64(x), f64(dy)), atol=1e-5, rtol=1e-5)
+    xg = x.to(cuda).requires_grad_()
+    CudaGeluLayer.apply(xg).backward(dy.to(cuda))
+    assert torch.equal(xg.grad, dx)
+
+
+def test_gelu_ragged_numel(cuda):
+    from cuda_transformer.ops import gelu_activation
+
+    for numel in (1, 3, 5, 1027):
+        x = seeded((1, 1, numel), numel, kind="randn")
+        np.testing.assert_allclose(f64(gelu_activation(x.to(cuda))), ew.gelu_forward(f64(x)),
+                                   atol=1e-6, rtol=1e-5)
+
+
+@pytest.mark.parametrize("batch,m,n", ROW_SHAPES + [(48, 1024, 1024)])
+def test_softmax(cuda, batch, m, n):
+    from cuda_autograd_fns import CudaSoftmaxLayer
+    from cuda_transformer.ops import cuda_softmax, cuda_softmax_bwd
+
+    scale = 2.0 if n == 1024 else 1.0  # config 4 logits ~ N(0, 4)
+    x = seeded((batch, m, n), 7) * scale
+    dp = seeded((batch, m, n), 8, kind="rand")
+    p = cuda_softmax(x.to(cuda))
+    p_ref = ew.softmax_forward(f64(x))
+    np.testing.assert_allclose(f64(p), p_ref, atol=1e-5, rtol=1e-5)
+    dx = cuda_softmax_bwd(p, dp.to(cuda))
+    np.testing.assert_allclose(f64(dx), ew.softmax_backward(f64(p), f64(dp)), atol=1e-5,
+                               rtol=1e-5)
+    xg = x.to(cuda).requires_grad_()
+    CudaSoftmaxLayer.apply(xg).backward(dp.to(cuda))
+    assert torch.equal(xg.grad, dx)
+
+
+@pytest.mark.parametrize("rows,n", [(64, 32), (65, 32), (70, 120), (8192, 768), (33, 384),
+                                    (5, 2048), (3, 3000), (7, 65)])
+def test_layernorm(cuda, rows, n):
+    from cuda_autograd_fns import CudaLayerNorm
+
+    x = seeded((rows, n), 9) * 3 + 1
+    gamma = 1 + 0.1 * seeded((n,), 10)
+    beta = 0.1 * seeded((n,), 11)
+    dy = seeded((rows, n), 12)
+    xg, gg, bg = (t.to(cuda).requires_grad_() for t in (x, gamma, beta))
+    y = CudaLayerNorm.apply(xg, gg, bg, 1e-5)
+    y.backward(dy.to(cuda))
+    y_ref, mean, rstd = ew.layernorm_forward(f64(x), f64(gamma), f64(beta), 1e-5)
+    np.testing.assert_allclose(f64(y), y_ref, atol=1e-5, rtol=1e-5)
+    dx_r, dg_r, db_r = ew.layernorm_backward(f64(x), f64(gamma), mean, rstd, f64(dy))
+    np.testing.assert_allclose(f64(xg.grad), dx_r, atol=1e-4, rtol=1e-5)
+    assert rel_err(f64(gg.grad), dg_r) <= 1e-5
+    assert rel_err(f64(bg.grad), db_r) <= 1e-5
+
+
+NAIVE_SHAPES = [(1, 64, 1, 32, False), (1, 64, 1, 32, True), (1, 65, 1, 32, True),
+                (2, 128, 4, 64, False), (2, 128, 4, 64, True), (2, 257, 4, 64, True),
+                (1, 512, 2, 128, True)]
+
+
+@pytest.mark.parametrize("B,T,nh,hs,causal", NAIVE_SHAPES)
+def test_causal_self_attention(cuda, B, T, nh, hs, causal):
+    from cuda_autograd_fns import CudaCausalSelfAttention
+    from cuda_transformer.ops import causal_self_attention_bwd, causal_self_attention_fwd
+
+    C = nh * hs
+    qkv = seeded((B, T, 3 * C), 13, kind="rand")
+    dO = seeded((B, T, C), 14, kind="rand")
+    out, probs = causal_self_attention_fwd(qkv.to(cuda), nh, causal)
+    out_r, probs_r = ora.causal_self_attention_forward(f64(qkv), nh, causal)
+    assert probs.shape == (B, nh, T, T)
+    np.testing.assert_allclose(f64(out), out_r, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(f64(probs), probs_r, atol=1e-5, rtol=1e-5)
+
+    def heads(t):
+        return t.reshape(B, T, nh, hs).transpose(1, 2).reshape(B * nh, T, hs)
+
+    q, k, v = (heads(t) for t in qkv.to(cuda).chunk(3, dim=-1))
+    dq, dk, dv = causal_self_attention_bwd(q, k, v, probs.reshape(B * nh, T, T),
+                                           heads(dO.to(cuda)))
+    g_r = ora.causal_self_attention_backward(f64(q), f64(k), f64(v),
+                                             probs_r.reshape(B * nh, T, T), f64(heads(dO)))
+    for got, ref in zip((dq, dk, dv), g_r):
+        np.testing.assert_allclose(f64(got), ref, atol=1e-4, rtol=1e-5)
+    # autograd wrapper: grads of the packed qkv against the float64 oracle
+    qg = qkv.to(cuda).requires_grad_()
+    CudaCausalSelfAttention.apply(qg, nh, causal).backward(dO.to(cuda))
+    sm = hs ** 0.5
+
+    def unheads(a):
+        return a.reshape(B, nh, T, hs).transpose(0, 2, 1, 3).reshape(B, T, C)
+
+    ref_grad = np.concatenate([unheads(g_r[0]) / sm, unheads(g_r[1]) / sm, unheads(g_r[2])], -1)
+    np.testing.assert_allclose(f64(qg.grad), ref_grad, atol=1e-4, rtol=1e-5)
