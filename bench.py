@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Headline benchmark: FlashAttention-2 forward + backward, FP32, on one MI355X.
+
+Workload: B=4, H=32, N=4096, D=64, causal; Q, K, V, dO ~ N(0, 1) from fixed
+seeds; softmax scale 1/sqrt(64).  One step = the forward kernel then the three backward
+stages (delta, dQ, dK/dV), launched through the C ABI on torch's current stream with all
+inputs and outputs already resident in HBM.
+
+Reported:
+  value          whole-step TFLOPS by the reference's formula (benchmark/cuda_bench.py:63-68):
+                 fwd 4*B*H*N^2*D, halved for causal; bwd 2.5x fwd; divided by the wall time of
+                 exactly --steps steps bracketed by device synchronisation.
+  per_kernel_ms  HIP-event durations of each kernel on its launch stream, averaged over the
+                 timed steps.
+  roofline       the dominant kernel's algorithmic FLOPs per launch / its mean duration, vs the
+                 157.3 TFLOP/s dense FP32 MFMA peak; traffic from the committed rocprofv3 PMC
+                 summary (profiles/) when present.
+  cpu_baseline   the CPU oracle (numpy port of the reference algorithm, float32) timed on this
+                 host's cores on a bounded sample of whole heads of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+MFMA_FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBPS = 8000.0
+METRIC = "FA2 fwd+bwd FP32 TFLOPS @B4 H32 N4096 D64 causal; % of FP32 MFMA peak"
+# The reference's own numbers for this exact configuration (RTX 5070, README.md:60-67,197):
+# forward 212.73 ms + backward 1259.32 ms.  Different hardware: reported for context only.
+REFERENCE_RTX5070_MS = {"fwd": 212.73, "bwd": 1259.32}
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--batch", type=int, default=4)
+    p.add_argument("--heads", type=int, default=32)
+    p.add_argument("--seq", type=int, default=4096)
+    p.add_argument("--head-dim", type=int, default=64)
+    p.add_argument("--non-causal", action="store_true")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="target CPU time of the bounded CPU-baseline sample")
+    p.add_argument("--no-autograd", action="store_true",
+                   help="skip the extra autograd-path timing (CudaFlashAttention fwd + backward)")
+    p.add_argument("--copy-calibration-mib", type=int, default=0,
+                   help="only run a plain device copy of this many MiB (3 times): the known-size "
+                        "reference that scales the FETCH_SIZE / WRITE_SIZE counters")
+    return p.parse_args()
+
+
+def copy_calibration(mib):
+    import torch
+
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4,
+                      "launches": 3}), flush=True)
+    return 0
+
+
+def attn_flops(B, H, N, D, causal):
+    fwd = 4.0 * B * H * N * N * D * (0.5 if causal else 1.0)
+    return fwd, 2.5 * fwd
+
+
+def kernel_algorithmic(name, B, H, N, D, causal):
+    """(amount, unit, bound) of algorithmic work per launch of one kernel.
+
+    Attention kernels: 2*D FLOPs per (query, key) pair for each N x N x D product the kernel
+    must form — forward 2 products (S, PV), dQ 3 (S, dP, dQ), dK/dV 4 (S, dP, dV, dK) — over
+    B*H*N^2 pairs, halved when causal.  delta: bytes of O and dO read plus delta written."""
+    pairs = B * H * N * N * (0.5 if causal else 1.0)
+    products = {"fwd": 2, "dq": 3, "dkdv": 4}
+    if name in products:
+        return 2.0 * D * pairs * products[name], "TFLOP/s", "mfma"
+    return float(2 * B * H * N * D * 4 + B * H * N * 4), "GB/s", "hbm"
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed PMC summary, or None."""
+    path = ROOT / "profiles" / "fa2_config2_traffic.md"
+    if not path.exists():
+        return None
+    m = re.search(rf"traffic_bytes_per_launch\[{re.escape(kernel)}\]\s*=\s*([0-9.eE+]+)",
+                  path.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(B, H, N, D, causal, target_s):
+    """Time the CPU oracle (float32 numpy, BLAS-threaded) on whole heads until target_s."""
+    import numpy as np
+    from threadpoolctl import threadpool_info, threadpool_limits
+
+    from oracle import attention as ora
+
+    cores = min(16, os.cpu_count() or 1)  # the GPU box's CPU share is 16 cores
+    with threadpool_limits(limits=cores, user_api="blas"):
+        threads = max([i["num_threads"] for i in threadpool_info()
+                       if i.get("user_api") == "blas"] or [1])
+        rng = np.random.default_rng(0)
+        chunk = 4  # heads per chunk
+        shape = (1, chunk, N, D)
+        q, k, v, do = (rng.standard_normal(shape, dtype=np.float32) for _ in range(4))
+        heads = 0
+        t0 = time.perf_counter()
+        while heads < B * H:
+            O, L = ora.fa2_forward(q, k, v, causal, br=512, bc=512)
+            ora.fa2_backward(q, k, v, O, do, L, causal, br=512, bc=512)
+            heads += chunk
+            if time.perf_counter() - t0 >= target_s:
+                break
+        elapsed = time.perf_counter() - t0
+    fwd, bwd = attn_flops(1, heads, N, D, causal)
+    return {
+        "value": (fwd + bwd) / elapsed / 1e12,
+        "unit": "TFLOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{heads} of {B * H} heads (N={N}, D={D}, {'causal' if causal else 'full'}) "
+                   f"fwd+bwd, float32 numpy oracle (oracle/attention.py), 512x512 tiles, "
+                   f"{elapsed:.1f} s on {threads} BLAS threads"),
+        "seconds": elapsed,
+    }
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): "
+              "this build is single-GPU; multi-GPU sharding is a design note, not a benchmark.",
+              file=sys.stderr)
+        return 2
+
+    if args.copy_calibration_mib:
+        return copy_calibration(args.copy_calibration_mib)
+
+    import torch
+
+    import cuda_transformer_amd  # noqa: F401  (fails loudly if the native library is missing)
+    from cuda_transformer_amd import capi
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    B, H, N, D = args.batch, args.heads, args.seq, args.head_dim
+    causal = not args.non_causal
+
+    gen = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(B, H, N, D, generator=gen).to(dev) for _ in range(3))
+    do = torch.randn(B, H, N, D, generator=torch.Generator().manual_seed(1)).to(dev)
+    O = torch.empty_like(q)
+    L = torch.empty(B, H, N, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    delta = torch.empty(B, H, N, device=dev)
+
+    stream = torch.cuda.current_stream(dev)
+    st = ctypes.c_void_p(stream.cuda_stream)
+    s4 = capi.strides(q.stride())
+    s3 = capi.strides(L.stride())
+    P = {name: ctypes.c_void_p(t.data_ptr()) for name, t in
+         dict(q=q, k=k, v=v, do=do, O=O, L=L, dq=dq, dk=dk, dv=dv, delta=delta).items()}
+    lib = capi.lib()
+    c = int(causal)
+
+    def launch(kernel):
+        if kernel == "fwd":
+            rc = lib.cta_flash_attention_fwd(P["q"], s4, P["k"], s4, P["v"], s4, B, H, N, D, c,
+                                             P["O"], P["L"], st)
+        elif kernel == "delta":
+            rc = lib.cta_flash_attention_bwd_delta(P["O"], s4, P["do"], s4, B, H, N, D,
+                                                   P["delta"], st)
+        elif kernel == "dq":
+            rc = lib.cta_flash_attention_bwd_dq(P["q"], s4, P["k"], s4, P["v"], s4, P["do"], s4,
+                                                P["L"], s3, P["delta"], B, H, N, D, c, P["dq"],
+                                                st)
+        else:
+            rc = lib.cta_flash_attention_bwd_dkdv(P["q"], s4, P["k"], s4, P["v"], s4, P["do"],
+                                                  s4, P["L"], s3, P["delta"], B, H, N, D, c,
+                                                  P["dk"], P["dv"], st)
+        if rc != 0:
+            raise RuntimeError(f"{kernel}: {lib.cta_last_error().decode()}")
+
+    kernels = ["fwd", "delta", "dq", "dkdv"]
+
+    def step(events=None):
+        for i, kname in enumerate(kernels):
+            if events is not None:
+                events[i].record(stream)
+            launch(kname)
+        if events is not None:
+            events[len(kernels)].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(kernels) + 1)]
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    per_kernel = {kname: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / args.steps
+                  for j, kname in enumerate(kernels)}
+
+    fwd_fl, bwd_fl = attn_flops(B, H, N, D, causal)
+    value = (fwd_fl + bwd_fl) / (ms_step * 1e-3) / 1e12
+    fwd_tf = fwd_fl / (per_kernel["fwd"] * 1e-3) / 1e12
+    bwd_ms = per_kernel["delta"] + per_kernel["dq"] + per_kernel["dkdv"]
+    bwd_tf = bwd_fl / (bwd_ms * 1e-3) / 1e12
+
+    dom = max(per_kernel, key=per_kernel.get)
+    amount, unit, bound = kernel_algorithmic(dom, B, H, N, D, causal)
+    if unit == "TFLOP/s":
+        achieved, peak = amount / (per_kernel[dom] * 1e-3) / 1e12, MFMA_FP32_PEAK_TFLOPS
+    else:
+        achieved, peak = amount / (per_kernel[dom] * 1e-3) / 1e9, HBM_PEAK_GBPS
+    kernel_symbols = {"fwd": "fa2_fwd_kernel", "delta": "fa2_bwd_delta_kernel",
+                      "dq": "fa2_bwd_dq_kernel", "dkdv": "fa2_bwd_dkdv_kernel"}
+    roofline = {"kernel": kernel_symbols[dom], "bound": bound, "achieved": round(achieved, 3),
+                "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
+                "traffic": load_traffic(kernel_symbols[dom]),
+                "algorithmic_per_launch": amount}
+
+    extra = {}
+    if not args.no_autograd:
+        # The reference's benchmark path: CudaFlashAttention.apply, then o.backward(dO)
+        # (benchmark/cuda_bench.py:44-48), through the torch operator layer and autograd.
+        from cuda_autograd_fns import CudaFlashAttention
+
+        qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+        for _ in range(2):
+            o, _l = CudaFlashAttention.apply(qg, kg, vg, causal)
+            o.backward(do)
+        torch.cuda.synchronize()
+        reps = max(3, args.steps // 2)
+        ta = time.perf_counter()
+        for _ in range(reps):
+            o, _l = CudaFlashAttention.apply(qg, kg, vg, causal)
+            o.backward(do)
+        torch.cuda.synchronize()
+        extra["autograd_ms_per_step"] = round((time.perf_counter() - ta) * 1e3 / reps, 4)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (N(0,1) Q/K/V/dO from fixed seeds)",
+        "config": {"workload": f"FA2 fwd+bwd B{B} H{H} N{N} D{D} {'causal' if causal else 'non-causal'}",
+                   "B": B, "H": H, "N": N, "D": D, "causal": causal},
+        "fwd_tflops": round(fwd_tf, 3),
+        "bwd_tflops": round(bwd_tf, 3),
+        "fwd_frac_of_peak": round(fwd_tf / MFMA_FP32_PEAK_TFLOPS, 4),
+        "bwd_frac_of_peak": round(bwd_tf / MFMA_FP32_PEAK_TFLOPS, 4),
+        "per_kernel_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
+        "roofline": roofline,
+        "reference_rtx5070_ms": REFERENCE_RTX5070_MS,
+        "device": torch.cuda.get_device_name(0),
+        "torch": torch.__version__,
+        **extra,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(B, H, N, D, causal, args.cpu_seconds)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,73 @@
+"""The C ABI on the CPU: the shared library loads, exports every symbol the public header
+declares, and its host-side validation rejects bad arguments before any launch (these
+calls never touch a GPU, so they run anywhere)."""
+import ctypes
+
+import pytest
+
+from cuda_transformer_amd import capi
+
+OK, INVALID, HEADDIM, LAYOUT = 0, 1, 2, 3
+
+
+def test_library_exports_every_declared_symbol():
+    lib = capi.lib()
+    declared = capi.declared_symbols()
+    assert len(declared) >= 20
+    missing = [name for name in declared if not hasattr(lib, name)]
+    assert missing == []
+    assert set(declared) == set(capi.SIGNATURES), "ctypes prototypes out of sync with the header"
+
+
+def test_version_and_last_error():
+    lib = capi.lib()
+    assert lib.cta_version().decode().startswith("cuda_transformer_amd")
+    assert isinstance(lib.cta_last_error(), bytes)
+
+
+def _fwd(hs=64, B=1, nh=1, T=8, q=16, s=(512, 512, 64, 1), o=16, l=16):
+    st = capi.strides(s)
+    return capi.lib().cta_flash_attention_fwd(q, st, q, st, q, st, B, nh, T, hs, 1, o, l, None)
+
+
+def test_unsupported_head_dim_message_matches_reference():
+    lib = capi.lib()
+    assert _fwd(hs=48) == HEADDIM
+    assert lib.cta_last_error().decode() == (
+        "Unsupported head dimension! Only hs=32, hs=64, and hs=128 are supported.")
+
+
+def test_empty_and_invalid_sizes():
+    assert _fwd(T=0) == OK           # nothing to do, no launch
+    assert _fwd(B=0) == OK
+    assert _fwd(T=-1) == INVALID
+
+
+def test_layout_checks_run_before_launch():
+    # misaligned pointer / non-unit d-stride / stride not divisible by 4 -> CTA_ERR_LAYOUT
+    assert _fwd(q=20) == LAYOUT
+    assert _fwd(s=(512, 512, 64, 2)) == LAYOUT
+    assert _fwd(s=(512, 512, 66, 1)) == LAYOUT
+    assert b"16-byte" in capi.lib().cta_last_error()
+
+
+def test_workspace_queries():
+    lib = capi.lib()
+    assert lib.cta_db_calculation_workspace(1, 8192, 3072) == 128 * 3072 * 4
+    assert lib.cta_db_calculation_workspace(0, 5, 5) == 0
+    assert lib.cta_layernorm_bwd_workspace(8192, 768) > 0
+    assert lib.cta_causal_self_attention_bwd_workspace(8, 33) == 8 * 33 * 33 * 4
+
+
+def test_other_entry_points_validate_arguments():
+    lib = capi.lib()
+    s3 = capi.strides((1, 1, 1))
+    assert lib.cta_cuda_fma(16, s3, 16, s3, 16, 1, 2, 3, 4, 5, 3, 16, None) == INVALID  # w_batch
+    assert lib.cta_gelu_fwd(16, 16, -1, None) == INVALID
+    assert lib.cta_gelu_fwd(20, 16, 8, None) == LAYOUT
+    assert lib.cta_softmax_fwd(16, 16, -1, 4, None) == INVALID
+    assert lib.cta_layernorm_fwd(16, 16, 16, 4, 0, ctypes.c_float(1e-5), 16, 16, 16, None) == INVALID
+    assert lib.cta_causal_self_attention_fwd(16, 1, 4, 10, 3, 1, 16, 16, None) == INVALID  # C % nh
+    with pytest.raises(capi.CtaError, match="Unsupported head dimension"):
+        st = capi.strides((512, 512, 64, 1))
+        capi.call("cta_flash_attention_bwd_delta", 16, st, 16, st, 1, 1, 8, 96, 16, None)
