@@ -45,6 +45,9 @@ REFERENCE_RTX5070_MS = {"fwd": 212.73, "bwd": 1259.32}
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--workload", choices=["fa2", "fa2-sweep", "ops"], default="fa2",
+                   help="fa2: the headline step (default, one JSON line); fa2-sweep: BASELINE "
+                        "config 3; ops: BASELINE config 4 (one JSON line per op)")
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--batch", type=int, default=4)
@@ -142,30 +145,14 @@ def cpu_baseline(B, H, N, D, causal, target_s):
     }
 
 
-def main():
-    args = parse_args()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): "
-              "this build is single-GPU; multi-GPU sharding is a design note, not a benchmark.",
-              file=sys.stderr)
-        return 2
-
-    if args.copy_calibration_mib:
-        return copy_calibration(args.copy_calibration_mib)
-
+def fa2_timings(B, H, N, D, causal, steps, warmup):
+    """Time `steps` FA2 steps [fwd, delta, dQ, dK/dV] through the C ABI on torch's current
+    stream.  Returns (wall ms per step, {kernel: mean HIP-event ms}, (q, k, v, dO))."""
     import torch
 
-    import cuda_transformer_amd  # noqa: F401  (fails loudly if the native library is missing)
     from cuda_transformer_amd import capi
 
-    if not torch.cuda.is_available():
-        print("bench.py needs a GPU", file=sys.stderr)
-        return 1
     dev = torch.device("cuda", 0)
-    B, H, N, D = args.batch, args.heads, args.seq, args.head_dim
-    causal = not args.non_causal
-
     gen = torch.Generator().manual_seed(0)
     q, k, v = (torch.randn(B, H, N, D, generator=gen).to(dev) for _ in range(3))
     do = torch.randn(B, H, N, D, generator=torch.Generator().manual_seed(1)).to(dev)
@@ -211,21 +198,238 @@ def main():
         if events is not None:
             events[len(kernels)].record(stream)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
 
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(kernels) + 1)]
-           for _ in range(args.steps)]
+           for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
+    for i in range(steps):
         step(evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_step = wall * 1e3 / args.steps
-    per_kernel = {kname: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / args.steps
+    per_kernel = {kname: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps
                   for j, kname in enumerate(kernels)}
+    return wall * 1e3 / steps, per_kernel, (q, k, v, do)
+
+
+def fa2_sweep(args):
+    """non-causal B4 H32 D64, N in {1024 ... 16384}; one JSON line per N."""
+    import torch
+
+    for N in (1024, 2048, 4096, 8192, 16384):
+        steps = max(2, args.steps // (N // 1024))
+        ms, per_kernel, _ = fa2_timings(4, 32, N, 64, False, steps, 1)
+        fwd_fl, bwd_fl = attn_flops(4, 32, N, 64, False)
+        bwd_ms = per_kernel["delta"] + per_kernel["dq"] + per_kernel["dkdv"]
+        print(json.dumps({
+            "workload": f"FA2 B4 H32 N{N} D64 non-causal", "N": N, "steps": steps,
+            "fwd_ms": round(per_kernel["fwd"], 4), "bwd_ms": round(bwd_ms, 4),
+            "fwd_tflops": round(fwd_fl / per_kernel["fwd"] / 1e9, 3),
+            "bwd_tflops": round(bwd_fl / bwd_ms / 1e9, 3),
+            "fwd_frac_of_peak": round(fwd_fl / per_kernel["fwd"] / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
+            "bwd_frac_of_peak": round(bwd_fl / bwd_ms / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
+            "per_kernel_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
+        }), flush=True)
+        torch.cuda.empty_cache()
+    return 0
+
+
+def _time_kernel(fn, reps):
+    """Mean HIP-event duration (ms) of fn's launches on torch's current stream."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    for a, b in evs:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / reps
+
+
+def _cpu_time(fn, target_s=2.0):
+    """Seconds per call of a CPU function, repeated until about target_s."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= target_s or n >= 50:
+            return el / n
+
+
+def ops_workload(args):
+    """BASELINE config 4 (GPT-2-small widths, FP32): linear GEMM fwd/bwd, db, exact GELU,
+    LayerNorm and row softmax, each launched through the C ABI.  One JSON line per op with
+    the kernel's roofline (MFMA TFLOP/s for GEMMs, HBM GB/s otherwise) and the CPU oracle
+    (float32 numpy) timed on a bounded sample of the same op."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+
+    from cuda_transformer_amd import capi
+    from oracle import elementwise as ew
+    from oracle import linear as lin
+
+    lib = capi.lib()
+    dev = torch.device("cuda", 0)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    reps = max(5, args.steps)
+    g = torch.Generator().manual_seed(0)
+    cores = min(16, os.cpu_count() or 1)
+
+    def emit(name, shape, ms, amount, unit, cpu_s, cpu_amount, sample):
+        if unit == "TFLOP/s":
+            achieved, peak = amount / (ms * 1e-3) / 1e12, MFMA_FP32_PEAK_TFLOPS
+            cpu_val = cpu_amount / cpu_s / 1e12
+        else:
+            achieved, peak = amount / (ms * 1e-3) / 1e9, HBM_PEAK_GBPS
+            cpu_val = cpu_amount / cpu_s / 1e9
+        print(json.dumps({
+            "workload": name, "shape": shape, "ms": round(ms, 5), "value": round(achieved, 3),
+            "unit": unit,
+            "roofline": {"bound": "mfma" if unit == "TFLOP/s" else "hbm",
+                         "achieved": round(achieved, 3), "peak": peak,
+                         "frac": round(achieved / peak, 4), "algorithmic_per_launch": amount},
+            "cpu_baseline": {"value": round(cpu_val, 4), "unit": unit, "cores": cores,
+                             "kind": "port", "sample": sample},
+        }), flush=True)
+
+    with threadpool_limits(limits=cores, user_api="blas"):
+        # ---- linear layer: X[8192,768] . W[768,3072] + b, X, W ~ N(0, 0.02^2)
+        M, K, Nn = 8192, 768, 3072
+        x = (torch.randn(1, M, K, generator=g) * 0.02).to(dev)
+        w = (torch.randn(K, Nn, generator=g) * 0.02).to(dev)
+        b = (torch.randn(Nn, generator=g) * 0.02).to(dev)
+        dy = (torch.randn(1, M, Nn, generator=g) * 0.02).to(dev)
+        out = torch.empty(1, M, Nn, device=dev)
+        dx = torch.empty(1, M, K, device=dev)
+        dw = torch.empty(1, K, Nn, device=dev)
+        zk, zn = torch.zeros(K, device=dev), torch.zeros(Nn, device=dev)
+        xs, ws = capi.strides(x.stride()), capi.strides((0, Nn, 1))
+        wts = capi.strides((0, 1, Nn))              # W^T view (1, n=3072 -> k, 768)
+        dys = capi.strides(dy.stride())
+        xts = capi.strides((M * K, 1, K))           # x^T view (1, 768, 8192)
+        fl = 2.0 * M * K * Nn
+        xc, wc, dyc = (t.cpu().numpy().reshape(t.shape[-2:]) for t in (x, w, dy))
+        rows = M // 8
+        sample = f"rows 0..{rows} of {M} (1/8), float32 numpy BLAS"
+
+        def gemm_fwd():
+            assert lib.cta_cuda_fma(vp(x), xs, vp(w), ws, vp(b), 1, 1, M, K, Nn, 1, vp(out), st) == 0
+        emit("linear_fwd (cuda_fma)", [M, K, Nn], _time_kernel(gemm_fwd, reps), fl, "TFLOP/s",
+             _cpu_time(lambda: xc[:rows] @ wc + b.cpu().numpy()), fl / 8, sample)
+
+        def gemm_dx():
+            assert lib.cta_cuda_fma(vp(dy), dys, vp(w), wts, vp(zk), 1, 1, M, Nn, K, 1, vp(dx), st) == 0
+        emit("linear_bwd_dx (cuda_fma, W^T view)", [M, Nn, K], _time_kernel(gemm_dx, reps), fl,
+             "TFLOP/s", _cpu_time(lambda: dyc[:rows] @ wc.T), fl / 8, sample)
+
+        def gemm_dw():
+            assert lib.cta_cuda_fma(vp(x), xts, vp(dy), dys, vp(zn), 1, 1, K, M, Nn, 1, vp(dw), st) == 0
+        emit("linear_bwd_dw (cuda_fma, x^T view)", [K, M, Nn], _time_kernel(gemm_dw, reps), fl,
+             "TFLOP/s", _cpu_time(lambda: xc[:rows].T @ dyc[:rows]), fl / 8, sample)
+
+        db = torch.empty(Nn, device=dev)
+        ws_db = torch.empty(lib.cta_db_calculation_workspace(1, M, Nn) // 4, device=dev)
+
+        def dbk():
+            assert lib.cta_db_calculation(vp(dy), dys, 1, M, Nn, vp(db), vp(ws_db), st) == 0
+        emit("db_calculation", [M, Nn], _time_kernel(dbk, reps), 4.0 * M * Nn + 4 * Nn, "GB/s",
+             _cpu_time(lambda: lin.db_calculation(dyc[None, :rows])), 4.0 * rows * Nn, sample)
+        del x, w, dy, out, dx, dw
+
+        # ---- exact GELU on [8192, 3072]
+        n = M * Nn
+        xg = torch.randn(n, generator=g).to(dev)
+        yg, gg = torch.empty_like(xg), torch.randn(n, generator=g).to(dev)
+        xgc, ggc = xg[: n // 8].cpu().numpy(), gg[: n // 8].cpu().numpy()
+        sample8 = "1/8 of the elements, float32 numpy oracle"
+        emit("gelu_fwd", [M, Nn], _time_kernel(lambda: lib.cta_gelu_fwd(vp(xg), vp(yg), n, st), reps),
+             8.0 * n, "GB/s", _cpu_time(lambda: ew.gelu_forward(xgc)), 8.0 * n / 8, sample8)
+        emit("gelu_bwd", [M, Nn],
+             _time_kernel(lambda: lib.cta_gelu_bwd(vp(xg), vp(gg), vp(yg), n, st), reps),
+             12.0 * n, "GB/s", _cpu_time(lambda: ew.gelu_backward(xgc, ggc)), 12.0 * n / 8, sample8)
+        del xg, yg, gg
+
+        # ---- LayerNorm over 768 on [8192, 768], gamma = 1, beta = 0
+        R, C = 8192, 768
+        xl = torch.randn(R, C, generator=g).to(dev)
+        gam, bet = torch.ones(C, device=dev), torch.zeros(C, device=dev)
+        yl, mean, rstd = torch.empty_like(xl), torch.empty(R, device=dev), torch.empty(R, device=dev)
+        dyl, dxl = torch.randn(R, C, generator=g).to(dev), torch.empty_like(xl)
+        dgam, dbet = torch.empty(C, device=dev), torch.empty(C, device=dev)
+        ws_ln = torch.empty(lib.cta_layernorm_bwd_workspace(R, C) // 4, device=dev)
+        xlc, dylc = xl[: R // 8].cpu().numpy(), dyl[: R // 8].cpu().numpy()
+        onec, zeroc = np.ones(C, np.float32), np.zeros(C, np.float32)
+        eps = ctypes.c_float(1e-5)
+        emit("layernorm_fwd", [R, C], _time_kernel(
+            lambda: lib.cta_layernorm_fwd(vp(xl), vp(gam), vp(bet), R, C, eps, vp(yl), vp(mean),
+                                          vp(rstd), st), reps),
+             8.0 * R * C + 8 * R, "GB/s",
+             _cpu_time(lambda: ew.layernorm_forward(xlc, onec, zeroc)), (8.0 * R * C + 8 * R) / 8,
+             sample8.replace("elements", "rows"))
+        _, mc, rc_ = ew.layernorm_forward(xlc, onec, zeroc)
+        emit("layernorm_bwd", [R, C], _time_kernel(
+            lambda: lib.cta_layernorm_bwd(vp(xl), vp(gam), vp(mean), vp(rstd), vp(dyl), R, C,
+                                          vp(dxl), vp(dgam), vp(dbet), vp(ws_ln), st), reps),
+             12.0 * R * C + 8 * R + 8 * C, "GB/s",
+             _cpu_time(lambda: ew.layernorm_backward(xlc, onec, mc, rc_, dylc)),
+             (12.0 * R * C + 8 * R) / 8, sample8.replace("elements", "rows"))
+        del xl, yl, dyl, dxl
+
+        # ---- row softmax on [4*12*1024, 1024], logits ~ N(0, 4)
+        R, C = 4 * 12 * 1024, 1024
+        xs_ = (torch.randn(R, C, generator=g) * 2).to(dev)
+        ps_, dps, dxs = torch.empty_like(xs_), torch.rand(R, C, generator=g).to(dev), torch.empty_like(xs_)
+        xsc, dpsc = xs_[: R // 8].cpu().numpy(), dps[: R // 8].cpu().numpy()
+        emit("softmax_fwd", [R, C],
+             _time_kernel(lambda: lib.cta_softmax_fwd(vp(xs_), vp(ps_), R, C, st), reps),
+             8.0 * R * C, "GB/s", _cpu_time(lambda: ew.softmax_forward(xsc)), 8.0 * R * C / 8,
+             sample8.replace("elements", "rows"))
+        psc = ew.softmax_forward(xsc).astype(np.float32)
+        emit("softmax_bwd", [R, C],
+             _time_kernel(lambda: lib.cta_softmax_bwd(vp(ps_), vp(dps), vp(dxs), R, C, st), reps),
+             12.0 * R * C, "GB/s", _cpu_time(lambda: ew.softmax_backward(psc, dpsc)),
+             12.0 * R * C / 8, sample8.replace("elements", "rows"))
+    return 0
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): "
+              "this build is single-GPU; multi-GPU sharding is a design note, not a benchmark.",
+              file=sys.stderr)
+        return 2
+
+    if args.copy_calibration_mib:
+        return copy_calibration(args.copy_calibration_mib)
+
+    import torch
+
+    import cuda_transformer_amd  # noqa: F401  (fails loudly if the native library is missing)
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    if args.workload == "ops":
+        return ops_workload(args)
+    if args.workload == "fa2-sweep":
+        return fa2_sweep(args)
+    B, H, N, D = args.batch, args.heads, args.seq, args.head_dim
+    causal = not args.non_causal
+    ms_step, per_kernel, (q, k, v, do) = fa2_timings(B, H, N, D, causal, args.steps, args.warmup)
 
     fwd_fl, bwd_fl = attn_flops(B, H, N, D, causal)
     value = (fwd_fl + bwd_fl) / (ms_step * 1e-3) / 1e12

@@ -55,6 +55,20 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// MI355X dispatches workgroup ids round-robin over its 8 XCDs, each with a private 4 MB L2.
+// Remap the hardware id so that XCD x walks the contiguous run [x*per, (x+1)*per) of a
+// work list: when that list is ordered head-major, the workgroups resident on one XCD share
+// one or two heads' K/V instead of sixteen.  Launch 8*per workgroups; ids mapped past
+// `total` have no work and exit.
+constexpr int kNumXcds = 8;
+__device__ __forceinline__ int xcd_work_item(int hw_id, int total) {
+  const int per = (total + kNumXcds - 1) / kNumXcds;
+  return (hw_id % kNumXcds) * per + hw_id / kNumXcds;
+}
+inline unsigned xcd_grid(int64_t total) {
+  return (unsigned)(kNumXcds * ((total + kNumXcds - 1) / kNumXcds));
+}
+
 // 2^x on the hardware transcendental unit (v_exp_f32). Inputs here are <= 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

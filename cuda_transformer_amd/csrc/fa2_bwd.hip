@@ -90,14 +90,20 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, col = lane & 31;
-  const int id = blockIdx.x;
-  const int bh = id % BH;
-  const int qt = CAUSAL ? (n_qtiles - 1 - id / BH) : (id / BH);
+  // Head-major items over XCDs; causal items are query-tile pairs (n-1-p, p) of equal cost.
+  const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+  const int w = xcd_work_item(blockIdx.x, BH * per_head);
+  if (w >= BH * per_head) return;
+  const int bh = w / per_head;
+  const int p = w - bh * per_head;
   const int b = bh / nh, h = bh - b * nh;
 
   const float* Kb = K + b * sk.b + h * sk.h;
   const float* Vb = V + b * sv.b + h * sv.h;
 
+  const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
+  for (int pass = 0; pass < n_pass; ++pass) {
+  const int qt = CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p;
   const int i0 = qt * BM + wave * 32;
   const int my_i = i0 + col;
 
@@ -227,6 +233,7 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
       }
     }
   }
+  }  // pass
 }
 
 // ------------------------------------------------------------------------------------
@@ -252,9 +259,12 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, col = lane & 31;
-  const int id = blockIdx.x;
-  const int bh = id % BH;
-  const int kt = id / BH;  // causal: low key tiles have the most work and go first
+  // Head-major items over XCDs; causal items are key-tile pairs (p, n-1-p) of equal cost.
+  const int per_head = CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles;
+  const int w = xcd_work_item(blockIdx.x, BH * per_head);
+  if (w >= BH * per_head) return;
+  const int bh = w / per_head;
+  const int p = w - bh * per_head;
   const int b = bh / nh, h = bh - b * nh;
 
   const float* Qb = Q + b * sq.b + h * sq.h;
@@ -262,6 +272,9 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
   const float* Lb = Lg + b * sl.b + h * sl.h;
   const float* Db = delta + (int64_t)bh * T;
 
+  const int n_pass = (CAUSAL && n_ktiles - 1 - p != p) ? 2 : 1;
+  for (int pass = 0; pass < n_pass; ++pass) {
+  const int kt = CAUSAL ? (pass == 0 ? p : n_ktiles - 1 - p) : p;
   const int j0 = kt * BM + wave * 32;  // first key row of this wave
   const int my_j = j0 + col;
 
@@ -415,6 +428,7 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
       }
     }
   }
+  }  // pass
 }
 
 RowStrides rs(const int64_t* s) { return RowStrides{s[0], s[1], s[2]}; }
@@ -434,7 +448,8 @@ void launch_dq(const float* q, const float* k, const float* v, const float* d_o,
                RowStrides sk, RowStrides sv, RowStrides sdo, LStrides sl, float scale,
                hipStream_t st) {
   const int n_qtiles = (T + 127) / 128;
-  hipLaunchKernelGGL((fa2_bwd_dq_kernel<HS, CAUSAL>), dim3((unsigned)n_qtiles * BH), dim3(256), 0,
+  const int64_t items = (int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH;
+  hipLaunchKernelGGL((fa2_bwd_dq_kernel<HS, CAUSAL>), dim3(xcd_grid(items)), dim3(256), 0,
                      st, q, k, v, d_o, l, delta, dq, nh, T, BH, n_qtiles, sq, sk, sv, sdo, sl,
                      scale, scale * kLog2e);
 }
@@ -445,7 +460,8 @@ void launch_dkdv(const float* q, const float* k, const float* v, const float* d_
                  RowStrides sq, RowStrides sk, RowStrides sv, RowStrides sdo, LStrides sl,
                  float scale, hipStream_t st) {
   const int n_ktiles = (T + 127) / 128;
-  hipLaunchKernelGGL((fa2_bwd_dkdv_kernel<HS, CAUSAL>), dim3((unsigned)n_ktiles * BH), dim3(256),
+  const int64_t items = (int64_t)(CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles) * BH;
+  hipLaunchKernelGGL((fa2_bwd_dkdv_kernel<HS, CAUSAL>), dim3(xcd_grid(items)), dim3(256),
                      0, st, q, k, v, d_o, l, delta, dk, dv, nh, T, BH, n_ktiles, sq, sk, sv, sdo,
                      sl, scale, scale * kLog2e);
 }

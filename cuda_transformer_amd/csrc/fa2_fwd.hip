@@ -14,8 +14,10 @@
 //    second MFMA is permuted to match the output layout of the first, and V is read from LDS
 //    in the same permuted order.  P never leaves registers.
 //  * Exponentials use exp2 with log2(e) folded into the scale; L is exported in natural log.
-//  * Workgroup ids are mapped longest-first for causal attention (last query tile first);
-//    consecutive ids walk (batch, head) so the query tiles of one head share an XCD's L2.
+//  * Workgroup ids are remapped so each XCD walks a contiguous run of a head-major work list:
+//    the workgroups resident on one XCD share a few heads' K/V in its L2.  With a causal mask a
+//    workgroup takes the query-tile pair (n-1-p, p), so all workgroups cost the same and the
+//    head-major order leaves no long tiles for the end.
 #include "cta_common.hpp"
 
 namespace cta {
@@ -51,15 +53,22 @@ __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, col = lane & 31;
-  const int id = blockIdx.x;
-  const int bh = id % BH;
-  const int qt = CAUSAL ? (n_qtiles - 1 - id / BH) : (id / BH);
+  // Work items are head-major and spread over XCDs.  Causal: one item = the query-tile pair
+  // (n-1-p, p), so every item costs n+1 tile units and the dynamic dispatch has no tail.
+  const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+  const int w = xcd_work_item(blockIdx.x, BH * per_head);
+  if (w >= BH * per_head) return;
+  const int bh = w / per_head;
+  const int p = w - bh * per_head;
   const int b = bh / nh, h = bh - b * nh;
 
   const float* Qb = Q + b * sq.b + h * sq.h;
   const float* Kb = K + b * sk.b + h * sk.h;
   const float* Vb = V + b * sv.b + h * sv.h;
 
+  const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
+  for (int pass = 0; pass < n_pass; ++pass) {
+  const int qt = CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p;
   const int i0 = qt * BM + wave * 32;  // first query row of this wave
   const int my_i = i0 + col;           // query row owned by this lane
 
@@ -197,6 +206,7 @@ __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
     }
     if (half == 0) L[(int64_t)bh * T + my_i] = m_run * scale + logf(l_tot);
   }
+  }  // pass: the K/V loop ended on a barrier, so the next pass may refill LDS
 }
 
 template <int HS, bool CAUSAL>
@@ -204,7 +214,7 @@ void launch_fwd(const float* q, const float* k, const float* v, float* o, float*
                 int T, int BH, RowStrides sq, RowStrides sk, RowStrides sv, float scale,
                 hipStream_t stream) {
   const int n_qtiles = (T + 127) / 128;
-  const unsigned grid = (unsigned)n_qtiles * (unsigned)BH;
+  const unsigned grid = xcd_grid((int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH);
   hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL>), dim3(grid), dim3(256), 0, stream, q, k, v, o,
                      l, nh, T, BH, n_qtiles, sq, sk, sv, scale, scale * kLog2e);
 }
