@@ -324,18 +324,28 @@ def ops_workload(args):
         rows = M // 8
         sample = f"rows 0..{rows} of {M} (1/8), float32 numpy BLAS"
 
+        def scratch(m_, k_, n_):
+            nbytes = lib.cta_cuda_fma_workspace(1, m_, k_, n_)
+            return torch.empty(max(1, nbytes // 4), device=dev) if nbytes else None
+
+        ws_f, ws_dx, ws_dw = scratch(M, K, Nn), scratch(M, Nn, K), scratch(K, M, Nn)
+        vpo = lambda t: None if t is None else vp(t)  # noqa: E731
+
         def gemm_fwd():
-            assert lib.cta_cuda_fma(vp(x), xs, vp(w), ws, vp(b), 1, 1, M, K, Nn, 1, vp(out), st) == 0
+            assert lib.cta_cuda_fma(vp(x), xs, vp(w), ws, vp(b), 1, 1, M, K, Nn, 1, vp(out),
+                                    vpo(ws_f), st) == 0
         emit("linear_fwd (cuda_fma)", [M, K, Nn], _time_kernel(gemm_fwd, reps), fl, "TFLOP/s",
              _cpu_time(lambda: xc[:rows] @ wc + b.cpu().numpy()), fl / 8, sample)
 
         def gemm_dx():
-            assert lib.cta_cuda_fma(vp(dy), dys, vp(w), wts, vp(zk), 1, 1, M, Nn, K, 1, vp(dx), st) == 0
+            assert lib.cta_cuda_fma(vp(dy), dys, vp(w), wts, vp(zk), 1, 1, M, Nn, K, 1, vp(dx),
+                                    vpo(ws_dx), st) == 0
         emit("linear_bwd_dx (cuda_fma, W^T view)", [M, Nn, K], _time_kernel(gemm_dx, reps), fl,
              "TFLOP/s", _cpu_time(lambda: dyc[:rows] @ wc.T), fl / 8, sample)
 
         def gemm_dw():
-            assert lib.cta_cuda_fma(vp(x), xts, vp(dy), dys, vp(zn), 1, 1, K, M, Nn, 1, vp(dw), st) == 0
+            assert lib.cta_cuda_fma(vp(x), xts, vp(dy), dys, vp(zn), 1, 1, K, M, Nn, 1, vp(dw),
+                                    vpo(ws_dw), st) == 0
         emit("linear_bwd_dw (cuda_fma, x^T view)", [K, M, Nn], _time_kernel(gemm_dw, reps), fl,
              "TFLOP/s", _cpu_time(lambda: xc[:rows].T @ dyc[:rows]), fl / 8, sample)
 

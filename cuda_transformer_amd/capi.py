@@ -36,8 +36,9 @@ SIGNATURES = {
     "cta_flash_attention_bwd_dkdv": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p,
                                             _i64p, _p, _i64, _i64, _i64, _i64, _int, _p, _p,
                                             _p]),
+    "cta_cuda_fma_workspace": (_i64, [_i64, _i64, _i64, _i64]),
     "cta_cuda_fma": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p,
-                            _p]),
+                            _p, _p]),
     "cta_db_calculation_workspace": (_i64, [_i64, _i64, _i64]),
     "cta_db_calculation": (_int, [_p, _i64p, _i64, _i64, _i64, _p, _p, _p]),
     "cta_gelu_fwd": (_int, [_p, _p, _i64, _p]),
@@ -90,7 +91,7 @@ def strides(values) -> ctypes.Array:
 def call(name: str, *args) -> int:
     """Call an entry point; raise CtaError with the library's message on a non-zero status."""
     rc = getattr(lib(), name)(*args)
-    if isinstance(rc, int) and name not in ("cta_db_calculation_workspace",
+    if isinstance(rc, int) and name not in ("cta_db_calculation_workspace", "cta_cuda_fma_workspace",
                                              "cta_layernorm_bwd_workspace",
                                              "cta_causal_self_attention_bwd_workspace") and rc != 0:
         raise CtaError(f"{name} failed ({rc}): {lib().cta_last_error().decode()}")

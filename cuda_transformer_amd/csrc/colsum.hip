@@ -1,0 +1,140 @@
+// Deterministic column reductions (no atomics) on gfx950.
+//
+//  * colsum_rows: per-chunk column sums of a strided (batch, m, n) tensor — the first stage of
+//    the bias gradient db[n] = sum over (batch, m) of dy (the reference reduces one column per
+//    1024-thread block with strided reads: warp_sum_kernel.cuh:13-51).  Each thread owns 4
+//    adjacent columns (dwordx4) or 1 column, walks 32 rows of its chunk with four independent
+//    accumulators, and writes one partial row.  Row pointers advance incrementally, so there is
+//    no division in the loop.
+//  * colsum_partials: sums a [chunks][ncols] partial matrix over its rows with a fixed-order
+//    tree (8 row groups per column, combined in LDS), so results are bitwise reproducible.
+#include "cta_common.hpp"
+#include "gemm.hpp"
+
+namespace cta {
+namespace {
+
+constexpr int kRowsPerChunk = 32;
+constexpr int kTreeCols = 32;    // columns per workgroup in the final sum
+constexpr int kTreeGroups = 8;   // row groups per column
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void colsum_rows_kernel(const float* __restrict__ x,
+                                                          float* __restrict__ part, int64_t M,
+                                                          int64_t N, int64_t sb, int64_t sm,
+                                                          int64_t sn, int64_t rows, int rpc) {
+  constexpr int W = VEC ? 4 : 1;
+  const int64_t col0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * W;
+  if (col0 >= N) return;
+  const int64_t r0 = (int64_t)blockIdx.y * rpc;
+  const int64_t r1 = min(rows, r0 + rpc);
+  int64_t b = r0 / M, m = r0 - b * M;
+  const float* p = x + b * sb + m * sm + col0 * sn;
+  auto advance = [&]() {
+    p += sm;
+    if (++m == M) {
+      m = 0;
+      ++b;
+      p = x + b * sb + col0 * sn;
+    }
+  };
+  float4 acc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) acc[u] = zero4();
+  auto load = [&](const float* q) -> float4 {
+    if (VEC) return ld4(q);
+    return make_float4(q[0], 0.f, 0.f, 0.f);
+  };
+  int64_t r = r0;
+  for (; r + 4 <= r1; r += 4) {
+    const float* q0 = p; advance();
+    const float* q1 = p; advance();
+    const float* q2 = p; advance();
+    const float* q3 = p; advance();
+    const float4 v0 = load(q0), v1 = load(q1), v2 = load(q2), v3 = load(q3);
+    acc[0].x += v0.x; acc[0].y += v0.y; acc[0].z += v0.z; acc[0].w += v0.w;
+    acc[1].x += v1.x; acc[1].y += v1.y; acc[1].z += v1.z; acc[1].w += v1.w;
+    acc[2].x += v2.x; acc[2].y += v2.y; acc[2].z += v2.z; acc[2].w += v2.w;
+    acc[3].x += v3.x; acc[3].y += v3.y; acc[3].z += v3.z; acc[3].w += v3.w;
+  }
+  for (; r < r1; ++r) {
+    const float4 v = load(p);
+    advance();
+    acc[0].x += v.x; acc[0].y += v.y; acc[0].z += v.z; acc[0].w += v.w;
+  }
+  const float4 s = make_float4((acc[0].x + acc[1].x) + (acc[2].x + acc[3].x),
+                               (acc[0].y + acc[1].y) + (acc[2].y + acc[3].y),
+                               (acc[0].z + acc[1].z) + (acc[2].z + acc[3].z),
+                               (acc[0].w + acc[1].w) + (acc[2].w + acc[3].w));
+  float* out = part + (int64_t)blockIdx.y * N + col0;
+  if (VEC) st4(out, s);
+  else out[0] = s.x;
+}
+
+__global__ __launch_bounds__(256) void colsum_tree_kernel(const float* __restrict__ part,
+                                                          int64_t chunks, int64_t ncols,
+                                                          float* __restrict__ out0,
+                                                          float* __restrict__ out1,
+                                                          int64_t split) {
+  __shared__ float red[kTreeGroups][kTreeCols];
+  const int c = threadIdx.x % kTreeCols, g = threadIdx.x / kTreeCols;
+  const int64_t col = (int64_t)blockIdx.x * kTreeCols + c;
+  float a0 = 0.f, a1 = 0.f;
+  if (col < ncols) {
+    int64_t k = g;
+    for (; k + kTreeGroups < chunks; k += 2 * kTreeGroups) {
+      a0 += part[k * ncols + col];
+      a1 += part[(k + kTreeGroups) * ncols + col];
+    }
+    if (k < chunks) a0 += part[k * ncols + col];
+  }
+  red[g][c] = a0 + a1;
+  __syncthreads();
+  if (g == 0 && col < ncols) {
+    float s = red[0][c];
+#pragma unroll
+    for (int i = 1; i < kTreeGroups; ++i) s += red[i][c];
+    if (col < split) out0[col] = s;
+    else out1[col - split] = s;
+  }
+}
+
+int64_t rows_per_chunk(int64_t rows) {
+  return std::max<int64_t>(kRowsPerChunk, (rows + 65534) / 65535);
+}
+
+}  // namespace
+
+int colsum_partials_launch(const float* part, int64_t chunks, int64_t ncols, float* out0,
+                           float* out1, int64_t split, hipStream_t st) {
+  const unsigned grid = (unsigned)((ncols + kTreeCols - 1) / kTreeCols);
+  hipLaunchKernelGGL(colsum_tree_kernel, dim3(grid), dim3(256), 0, st, part, chunks, ncols, out0,
+                     out1, split);
+  return check_launch("column sum");
+}
+
+int64_t colsum_chunks(int64_t rows) {
+  return rows <= 0 ? 0 : (rows + rows_per_chunk(rows) - 1) / rows_per_chunk(rows);
+}
+
+int colsum_launch(const float* x, int64_t batch, int64_t M, int64_t N, int64_t sb, int64_t sm,
+                  int64_t sn, float* out, float* workspace, hipStream_t st) {
+  const int64_t rows = batch * M;
+  const int64_t rpc = rows_per_chunk(rows);
+  const int64_t chunks = colsum_chunks(rows);
+  if (chunks > 65535 || N > INT32_MAX) return fail(CTA_ERR_INVALID_ARGUMENT, "column sum too large");
+  if (batch == 1) sb = 0;  // the batch stride of a single batch is never used
+  const bool vec = sn == 1 && N % 4 == 0 && aligned16(x) && sm % 4 == 0 && sb % 4 == 0;
+  const int64_t per_block = vec ? 1024 : 256;
+  const dim3 grid((unsigned)((N + per_block - 1) / per_block), (unsigned)chunks);
+  if (vec)
+    hipLaunchKernelGGL((colsum_rows_kernel<true>), grid, dim3(256), 0, st, x, workspace, M, N, sb,
+                       sm, sn, rows, (int)rpc);
+  else
+    hipLaunchKernelGGL((colsum_rows_kernel<false>), grid, dim3(256), 0, st, x, workspace, M, N, sb,
+                       sm, sn, rows, (int)rpc);
+  if (int rc = check_launch("db_calculation")) return rc;
+  return colsum_partials_launch(workspace, chunks, N, out, out, N, st);
+}
+
+}  // namespace cta

@@ -1,4 +1,4 @@
-// Strided, batched FP32 GEMM on CDNA4 MFMA, plus the bias-gradient column reduction.
+// Strided, batched FP32 GEMM on CDNA4 MFMA, and the linear layer's C entry points.
 //
 //   out[z][m][n] = alpha * sum_k A[z][m][k] * B[z][k][n]  (+ bias[n])  (causal: -inf for n > m)
 //
@@ -94,10 +94,14 @@ struct TileLoader {
   }
 };
 
+// split_ws == nullptr: out = alpha * A B (+ bias, mask) written through C.
+// split_ws != nullptr: blockIdx.z = s * Z + z covers K range [s*kchunk, (s+1)*kchunk) and the raw
+// partial sum goes to split_ws[s][z][m][n] (dense); gemm_splitk_reduce finishes the epilogue.
 template <int AMODE, int BMODE>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmOperand A, GemmOperand B, GemmOut C,
                                                       GemmEpilogue ep, int M, int N, int K,
-                                                      int zin) {
+                                                      int zin, int Z, int kchunk,
+                                                      float* __restrict__ split_ws) {
   __shared__ __attribute__((aligned(16))) float smem[2 * (GBM + GBN) * GKP];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -105,15 +109,17 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmOperand A, GemmOperand
   const int wm = wave >> 1, wn = wave & 1;
 
   const int n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM;
-  const int z = blockIdx.z;
+  const int z = blockIdx.z % Z, split = blockIdx.z / Z;
   const int zo = z / zin, zi = z - zo * zin;
   const float* Ab = A.p + zo * A.s_outer + zi * A.s_inner;
   const float* Bb = B.p + zo * B.s_outer + zi * B.s_inner;
+  const int kb = split * kchunk;
+  const int ke = min(K, kb + kchunk);
 
   // A rows are m with (s_row, s_col) = (m, k); B "rows" are n with (n, k) = (s_col, s_row).
   TileLoader<AMODE> la;
   TileLoader<BMODE> lb;
-  const int nk = (K + GBK - 1) / GBK;
+  const int nk = (ke - kb + GBK - 1) / GBK;
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -121,8 +127,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmOperand A, GemmOperand
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
 
-  la.load(Ab, A.s_row, A.s_col, m0, 0, M, K, tid);
-  lb.load(Bb, B.s_col, B.s_row, n0, 0, N, K, tid);
+  la.load(Ab, A.s_row, A.s_col, m0, kb, M, ke, tid);
+  lb.load(Bb, B.s_col, B.s_row, n0, kb, N, ke, tid);
   la.store(smem, tid);
   lb.store(smem + GBM * GKP, tid);
   __syncthreads();
@@ -130,8 +136,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmOperand A, GemmOperand
   for (int t = 0; t < nk; ++t) {
     const int buf = t & 1;
     if (t + 1 < nk) {
-      la.load(Ab, A.s_row, A.s_col, m0, (t + 1) * GBK, M, K, tid);
-      lb.load(Bb, B.s_col, B.s_row, n0, (t + 1) * GBK, N, K, tid);
+      la.load(Ab, A.s_row, A.s_col, m0, kb + (t + 1) * GBK, M, ke, tid);
+      lb.load(Bb, B.s_col, B.s_row, n0, kb + (t + 1) * GBK, N, ke, tid);
     }
     const float* as = smem + buf * (GBM + GBN) * GKP;
     const float* bs = as + GBM * GKP;
@@ -165,6 +171,22 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmOperand A, GemmOperand
     __syncthreads();
   }
 
+  if (split_ws != nullptr) {
+    float* Pb = split_ws + ((int64_t)split * Z + z) * M * N;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn * 64 + j * 32 + col;
+      if (n >= N) continue;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * 64 + i * 32 + mfma_row(r, half);
+          if (m < M) Pb[(int64_t)m * N + n] = acc[i][j][r];
+        }
+    }
+    return;
+  }
   float* Cb = C.p + zo * C.s_outer + zi * C.s_inner;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -186,6 +208,26 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmOperand A, GemmOperand
   }
 }
 
+// Fixed-order sum of the split-K partials plus the epilogue of gemm_kernel.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(const float* __restrict__ ws, int S,
+                                                          int Z, int M, int N, GemmOut C,
+                                                          GemmEpilogue ep, int zin) {
+  const int64_t total = (int64_t)Z * M * N;
+  const int64_t plane = total;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * 256) {
+    float acc = ws[e];
+    for (int s = 1; s < S; ++s) acc += ws[(int64_t)s * plane + e];
+    const int64_t z = e / ((int64_t)M * N);
+    const int64_t mn = e - z * M * N;
+    const int m = (int)(mn / N), n = (int)(mn - (int64_t)m * N);
+    const int64_t zo = z / zin, zi = z - zo * zin;
+    float val = fmaf(ep.alpha, acc, ep.bias ? ep.bias[(int64_t)n * ep.bias_stride] : 0.0f);
+    if (ep.causal_mask && n > m) val = -INFINITY;
+    C.p[zo * C.s_outer + zi * C.s_inner + (int64_t)m * C.s_row + n] = val;
+  }
+}
+
 bool vec_ok(const GemmOperand& op, bool contig_is_col) {
   // dwordx4 loads along the contiguous dimension need 16-byte aligned rows.
   const int64_t s_other = contig_is_col ? op.s_row : op.s_col;
@@ -204,79 +246,80 @@ int pick_mode(const GemmOperand& op, bool is_a) {
 
 template <int AM>
 void dispatch_b(int bm, dim3 grid, hipStream_t st, const GemmOperand& A, const GemmOperand& B,
-                const GemmOut& C, const GemmEpilogue& ep, int M, int N, int K, int zin) {
+                const GemmOut& C, const GemmEpilogue& ep, int M, int N, int K, int zin, int Z,
+                int kchunk, float* ws) {
   if (bm == kVecK)
-    hipLaunchKernelGGL((gemm_kernel<AM, kVecK>), grid, dim3(256), 0, st, A, B, C, ep, M, N, K, zin);
+    hipLaunchKernelGGL((gemm_kernel<AM, kVecK>), grid, dim3(256), 0, st, A, B, C, ep, M, N, K, zin,
+                       Z, kchunk, ws);
   else if (bm == kVecMN)
-    hipLaunchKernelGGL((gemm_kernel<AM, kVecMN>), grid, dim3(256), 0, st, A, B, C, ep, M, N, K, zin);
+    hipLaunchKernelGGL((gemm_kernel<AM, kVecMN>), grid, dim3(256), 0, st, A, B, C, ep, M, N, K,
+                       zin, Z, kchunk, ws);
   else
-    hipLaunchKernelGGL((gemm_kernel<AM, kScalar>), grid, dim3(256), 0, st, A, B, C, ep, M, N, K, zin);
+    hipLaunchKernelGGL((gemm_kernel<AM, kScalar>), grid, dim3(256), 0, st, A, B, C, ep, M, N, K,
+                       zin, Z, kchunk, ws);
+}
+
+// K splits for a GEMM whose output tiles alone cannot fill the 256 CUs: enough splits for
+// ~512 workgroups, each keeping at least 512 of K; 1 = no split.
+int64_t splitk_factor(int64_t M, int64_t N, int64_t K, int64_t Z) {
+  const int64_t tiles = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN) * Z;
+  if (tiles >= 256 || K < 1024) return 1;
+  const int64_t s = std::min<int64_t>({(512 + tiles - 1) / tiles, K / 512, 8});
+  return s >= 2 ? s : 1;
 }
 
 }  // namespace
 
-// Launch the strided batched GEMM.  Z = number of batches, zin = inner batch extent.
+int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, int64_t Z) {
+  const int64_t S = splitk_factor(M, N, K, Z);
+  return S > 1 ? S * Z * M * N : 0;
+}
+
+// Launch the strided batched GEMM.  Z = number of batches, zin = inner batch extent.  With a
+// workspace of gemm_workspace_floats() floats, low-parallelism shapes are split along K.
 int gemm_launch(const GemmOperand& A, const GemmOperand& B, const GemmOut& C,
                 const GemmEpilogue& ep, int64_t M, int64_t N, int64_t K, int64_t Z, int64_t zin,
-                hipStream_t st) {
+                hipStream_t st, float* workspace, int64_t workspace_floats) {
   if (M <= 0 || N <= 0 || Z <= 0) return CTA_OK;
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || Z > 65535 || zin <= 0)
     return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM size out of range");
-  const dim3 grid((unsigned)((N + GBN - 1) / GBN), (unsigned)((M + GBM - 1) / GBM), (unsigned)Z);
-  if (grid.y > 65535) return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM M too large");
-  // The B operand is loaded as [n][k]: swap its roles so the loader sees (row=n, k).
+  int64_t S = splitk_factor(M, N, K, Z);
+  if (S > 1 && (workspace == nullptr || workspace_floats < S * Z * M * N)) S = 1;
+  const int64_t kchunk = S > 1 ? ((K + S - 1) / S + GBK - 1) / GBK * GBK : std::max<int64_t>(K, 1);
+  const dim3 grid((unsigned)((N + GBN - 1) / GBN), (unsigned)((M + GBM - 1) / GBM),
+                  (unsigned)(Z * S));
+  if (grid.y > 65535 || grid.z > 65535) return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM grid too large");
+  float* ws = S > 1 ? workspace : nullptr;
   const int am = pick_mode(A, true);
   const int bm = pick_mode(B, false);
-  // B's loader treats s_row as the n stride and s_col as the k stride, see gemm_kernel.
-  if (am == kVecK) dispatch_b<kVecK>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin);
-  else if (am == kVecMN) dispatch_b<kVecMN>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin);
-  else dispatch_b<kScalar>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin);
+  if (am == kVecK)
+    dispatch_b<kVecK>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin, (int)Z, (int)kchunk, ws);
+  else if (am == kVecMN)
+    dispatch_b<kVecMN>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin, (int)Z, (int)kchunk, ws);
+  else
+    dispatch_b<kScalar>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin, (int)Z, (int)kchunk, ws);
+  if (S > 1) {
+    const int64_t total = Z * M * N;
+    const unsigned rgrid = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(rgrid), dim3(256), 0, st, ws, (int)S, (int)Z,
+                       (int)M, (int)N, C, ep, (int)zin);
+  }
   return check_launch("gemm");
 }
-
-// ----------------------------------------------------------------------------------
-// Bias gradient: db[n] = sum over (batch, m) of dy[batch][m][n].  Deterministic two-stage
-// column reduction: coalesced partial sums over row chunks, then one ordered sum per column.
-namespace {
-constexpr int DB_ROWS_PER_CHUNK = 64;
-
-__global__ __launch_bounds__(256) void colsum_partial_kernel(const float* __restrict__ dy,
-                                                             float* __restrict__ part, int M,
-                                                             int N, int64_t rows, int64_t sb,
-                                                             int64_t sm, int64_t sn) {
-  const int n = blockIdx.x * 256 + threadIdx.x;
-  const int64_t r0 = (int64_t)blockIdx.y * DB_ROWS_PER_CHUNK;
-  if (n >= N) return;
-  const int64_t r1 = min(rows, r0 + DB_ROWS_PER_CHUNK);
-  float acc = 0.0f;
-  for (int64_t r = r0; r < r1; ++r) {
-    const int64_t b = r / M, m = r - b * M;
-    acc += dy[b * sb + m * sm + (int64_t)n * sn];
-  }
-  part[(int64_t)blockIdx.y * N + n] = acc;
-}
-
-__global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restrict__ part,
-                                                           float* __restrict__ out, int N,
-                                                           int chunks) {
-  const int n = blockIdx.x * 256 + threadIdx.x;
-  if (n >= N) return;
-  float acc = 0.0f;
-  for (int c = 0; c < chunks; ++c) acc += part[(int64_t)c * N + n];
-  out[n] = acc;
-}
-}  // namespace
-
-int64_t db_chunks(int64_t rows) { return (rows + DB_ROWS_PER_CHUNK - 1) / DB_ROWS_PER_CHUNK; }
 
 }  // namespace cta
 
 using namespace cta;
 
+extern "C" int64_t cta_cuda_fma_workspace(int64_t batch, int64_t m, int64_t k, int64_t n) {
+  if (batch <= 0 || m <= 0 || n <= 0 || k <= 0) return 0;
+  return gemm_workspace_floats(m, n, k, batch) * (int64_t)sizeof(float);
+}
+
 extern "C" int cta_cuda_fma(const float* x, const int64_t* x_strides, const float* w,
                             const int64_t* w_strides, const float* bias, int64_t bias_stride,
                             int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
-                            float* out, void* stream) {
+                            float* out, float* workspace, void* stream) {
   if (batch < 0 || m < 0 || k < 0 || n < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
   if (w_batch != 1 && w_batch != batch)
     return fail(CTA_ERR_INVALID_ARGUMENT, "weights batch must be 1 or equal to x batch");
@@ -288,12 +331,13 @@ extern "C" int cta_cuda_fma(const float* x, const int64_t* x_strides, const floa
   const GemmOperand B{w, w_batch == 1 ? 0 : w_strides[0], 0, w_strides[1], w_strides[2]};
   const GemmOut C{out, m * n, 0, n};
   const GemmEpilogue ep{1.0f, bias, bias_stride, 0};
-  return gemm_launch(A, B, C, ep, m, n, k, batch, 1, as_stream(stream));
+  return gemm_launch(A, B, C, ep, m, n, k, batch, 1, as_stream(stream), workspace,
+                     workspace ? gemm_workspace_floats(m, n, k, batch) : 0);
 }
 
 extern "C" int64_t cta_db_calculation_workspace(int64_t batch, int64_t m, int64_t n) {
   if (batch <= 0 || m <= 0 || n <= 0) return 0;
-  return db_chunks(batch * m) * n * (int64_t)sizeof(float);
+  return colsum_chunks(batch * m) * n * (int64_t)sizeof(float);
 }
 
 extern "C" int cta_db_calculation(const float* dy, const int64_t* dy_strides, int64_t batch,
@@ -303,20 +347,12 @@ extern "C" int cta_db_calculation(const float* dy, const int64_t* dy_strides, in
   if (n == 0) return CTA_OK;
   if (!db) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
   hipStream_t st = as_stream(stream);
-  const int64_t rows = batch * m;
-  if (rows == 0) {
+  if (batch * m == 0) {
     if (hipMemsetAsync(db, 0, n * sizeof(float), st) != hipSuccess)
       return fail(CTA_ERR_LAUNCH, "hipMemsetAsync failed");
     return CTA_OK;
   }
   if (!dy || !dy_strides || !workspace) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
-  if (n > INT32_MAX || m > INT32_MAX) return fail(CTA_ERR_INVALID_ARGUMENT, "size out of range");
-  const int64_t chunks = db_chunks(rows);
-  if (chunks > 65535) return fail(CTA_ERR_INVALID_ARGUMENT, "too many rows for db_calculation");
-  const unsigned gx = (unsigned)((n + 255) / 256);
-  hipLaunchKernelGGL(colsum_partial_kernel, dim3(gx, (unsigned)chunks), dim3(256), 0, st, dy,
-                     workspace, (int)m, (int)n, rows, dy_strides[0], dy_strides[1], dy_strides[2]);
-  hipLaunchKernelGGL(colsum_final_kernel, dim3(gx), dim3(256), 0, st, workspace, db, (int)n,
-                     (int)chunks);
-  return check_launch("db_calculation");
+  return colsum_launch(dy, batch, m, n, dy_strides[0], dy_strides[1], dy_strides[2], db,
+                       workspace, st);
 }

@@ -25,14 +25,27 @@ struct GemmEpilogue {
 };
 
 // out[z] = alpha * A[z] B[z] (+ bias) for z in [0, Z); batch index split as (z / zin, z % zin).
+// With a workspace of gemm_workspace_floats(M, N, K, Z) floats, shapes with too few output
+// tiles to fill the GPU are split along K (deterministic fixed-order reduction).
 int gemm_launch(const GemmOperand& A, const GemmOperand& B, const GemmOut& C,
                 const GemmEpilogue& ep, int64_t M, int64_t N, int64_t K, int64_t Z, int64_t zin,
-                hipStream_t st);
+                hipStream_t st, float* workspace = nullptr, int64_t workspace_floats = 0);
+int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, int64_t Z);
 
 // Row softmax over `rows` dense rows of length n (x == y allowed).
 int softmax_rows(const float* x, float* y, int64_t rows, int64_t n, hipStream_t st);
 // dx = p * (dp - rowsum(p * dp)) over dense rows (dx may alias dp or p).
 int softmax_bwd_rows_launch(const float* p, const float* dp, float* dx, int64_t rows, int64_t n,
                             hipStream_t st);
+
+// Column sums of a strided (batch, M, N) tensor into out[N]; workspace holds
+// colsum_chunks(batch * M) * N floats.  Deterministic.
+int colsum_launch(const float* x, int64_t batch, int64_t M, int64_t N, int64_t sb, int64_t sm,
+                  int64_t sn, float* out, float* workspace, hipStream_t st);
+int64_t colsum_chunks(int64_t rows);
+// Fixed-order sum over the rows of part[chunks][ncols]: column c goes to out0[c] (c < split)
+// or out1[c - split].
+int colsum_partials_launch(const float* part, int64_t chunks, int64_t ncols, float* out0,
+                           float* out1, int64_t split, hipStream_t st);
 
 }  // namespace cta

@@ -14,6 +14,7 @@
 // to a workgroup-per-row path.  Column reductions (dgamma, dbeta) are two-stage and
 // deterministic (no atomics).
 #include "cta_common.hpp"
+#include "gemm.hpp"
 
 namespace cta {
 namespace {
@@ -27,13 +28,25 @@ __device__ __forceinline__ float gelu_grad(float x, float g) {
   return g * (normcdff(x) + x * pdf);
 }
 
+// Each thread handles four independent float4 per iteration (index i + 256*u within a chunk of
+// 1024 float4) so that four loads are in flight before the math starts.
 __global__ __launch_bounds__(256) void gelu_fwd_kernel(const float* __restrict__ x,
                                                        float* __restrict__ y, int64_t n4,
                                                        int64_t n) {
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
-    const float4 v = ld4(x + 4 * i);
-    st4(y + 4 * i, make_float4(gelu_f(v.x), gelu_f(v.y), gelu_f(v.z), gelu_f(v.w)));
+  const int64_t stride = (int64_t)gridDim.x * 1024;
+  for (int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x; base < n4; base += stride) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = base + 256 * u;
+      v[u] = (i < n4) ? ld4(x + 4 * i) : zero4();
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = base + 256 * u;
+      if (i < n4)
+        st4(y + 4 * i, make_float4(gelu_f(v[u].x), gelu_f(v[u].y), gelu_f(v[u].z), gelu_f(v[u].w)));
+    }
   }
   // tail (n % 4 elements) handled by the first threads of block 0
   if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
@@ -46,12 +59,22 @@ __global__ __launch_bounds__(256) void gelu_bwd_kernel(const float* __restrict__
                                                        const float* __restrict__ dy,
                                                        float* __restrict__ dx, int64_t n4,
                                                        int64_t n) {
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
-    const float4 v = ld4(x + 4 * i);
-    const float4 g = ld4(dy + 4 * i);
-    st4(dx + 4 * i, make_float4(gelu_grad(v.x, g.x), gelu_grad(v.y, g.y), gelu_grad(v.z, g.z),
-                                gelu_grad(v.w, g.w)));
+  const int64_t stride = (int64_t)gridDim.x * 1024;
+  for (int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x; base < n4; base += stride) {
+    float4 v[4], g[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = base + 256 * u;
+      v[u] = (i < n4) ? ld4(x + 4 * i) : zero4();
+      g[u] = (i < n4) ? ld4(dy + 4 * i) : zero4();
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = base + 256 * u;
+      if (i < n4)
+        st4(dx + 4 * i, make_float4(gelu_grad(v[u].x, g[u].x), gelu_grad(v[u].y, g[u].y),
+                                    gelu_grad(v[u].z, g[u].z), gelu_grad(v[u].w, g[u].w)));
+    }
   }
   if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
     const int64_t i = 4 * n4 + threadIdx.x;
@@ -61,7 +84,7 @@ __global__ __launch_bounds__(256) void gelu_bwd_kernel(const float* __restrict__
 
 unsigned elementwise_grid(int64_t n4) {
   // enough workgroups to fill 256 CUs several times over; grid-stride covers the rest
-  const int64_t want = (n4 + 255) / 256;
+  const int64_t want = (n4 + 1023) / 1024;
   return (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, 256 * 16));
 }
 
@@ -300,21 +323,6 @@ __global__ __launch_bounds__(256) void layernorm_bwd_rows(
   }
 }
 
-__global__ __launch_bounds__(256) void layernorm_bwd_final(const float* __restrict__ part,
-                                                           float* __restrict__ dgamma,
-                                                           float* __restrict__ dbeta, int n,
-                                                           int blocks) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= n) return;
-  float sg = 0.0f, sb = 0.0f;
-  for (int b = 0; b < blocks; ++b) {
-    sg += part[(int64_t)b * 2 * n + c];
-    sb += part[(int64_t)b * 2 * n + n + c];
-  }
-  dgamma[c] = sg;
-  dbeta[c] = sb;
-}
-
 // Long rows (n > 2048): one workgroup per row, three passes over the row.
 __global__ __launch_bounds__(256) void layernorm_fwd_long(
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
@@ -382,7 +390,7 @@ __global__ __launch_bounds__(256) void layernorm_colpart_long(
 
 // ------------------------------------------------------------------ dispatch helpers
 constexpr int kMaxRegCols = 2048;
-constexpr int kLnBwdBlocks = 256;  // partial rows for dgamma/dbeta (row-register path)
+constexpr int kLnBwdMaxBlocks = 512;  // partial rows for dgamma/dbeta (row-register path)
 constexpr int kLnLongRowsPerBlock = 64;
 
 int units_for(int n, bool vec) {
@@ -449,9 +457,14 @@ int softmax_bwd_rows_launch(const float* p, const float* dp, float* dx, int64_t 
   return check_launch("softmax_bwd");
 }
 
+// Workgroups of the row-register backward: 4 waves each, about 4 rows per wave.
+int64_t ln_bwd_blocks(int64_t rows) {
+  return std::max<int64_t>(1, std::min<int64_t>(kLnBwdMaxBlocks, (rows + 15) / 16));
+}
+
 int64_t layernorm_bwd_workspace_floats(int64_t rows, int64_t n) {
   if (rows <= 0 || n <= 0) return 0;
-  if (n <= kMaxRegCols) return (int64_t)kLnBwdBlocks * 2 * n;
+  if (n <= kMaxRegCols) return ln_bwd_blocks(rows) * 2 * n;
   return ((rows + kLnLongRowsPerBlock - 1) / kLnLongRowsPerBlock) * 2 * n;
 }
 
@@ -544,12 +557,12 @@ extern "C" int cta_layernorm_bwd(const float* x, const float* gamma, const float
   if (n <= kMaxRegCols) {
     const bool vec = row_vec_ok(x, dy, dx, (int)n) && aligned16(gamma);
     const int u = units_for((int)n, vec);
-    const int64_t waves = (int64_t)kLnBwdBlocks * 4;
-    const int rows_per_wave = (int)((rows + waves - 1) / waves);
-    CTA_ROW_SWITCH(layernorm_bwd_rows, vec, u, dim3(kLnBwdBlocks), st, x, gamma, mean, rstd, dy,
-                   dx, workspace, rows, (int)n, rows_per_wave);
-    hipLaunchKernelGGL(layernorm_bwd_final, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                       workspace, dgamma, dbeta, (int)n, kLnBwdBlocks);
+    const int64_t blocks = ln_bwd_blocks(rows);
+    const int rows_per_wave = (int)((rows + blocks * 4 - 1) / (blocks * 4));
+    CTA_ROW_SWITCH(layernorm_bwd_rows, vec, u, dim3((unsigned)blocks), st, x, gamma, mean, rstd,
+                   dy, dx, workspace, rows, (int)n, rows_per_wave);
+    if (int rc = check_launch("layernorm_bwd")) return rc;
+    return colsum_partials_launch(workspace, blocks, 2 * n, dgamma, dbeta, n, st);
   } else {
     hipLaunchKernelGGL(layernorm_bwd_long, dim3((unsigned)rows), dim3(256), 0, st, x, gamma, mean,
                        rstd, dy, dx, (int)n);
@@ -558,8 +571,8 @@ extern "C" int cta_layernorm_bwd(const float* x, const float* gamma, const float
     hipLaunchKernelGGL(layernorm_colpart_long, dim3((unsigned)((n + 255) / 256), (unsigned)chunks),
                        dim3(256), 0, st, x, mean, rstd, dy, workspace, rows, (int)n,
                        kLnLongRowsPerBlock);
-    hipLaunchKernelGGL(layernorm_bwd_final, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                       workspace, dgamma, dbeta, (int)n, (int)chunks);
+    if (int rc = check_launch("layernorm_bwd")) return rc;
+    return colsum_partials_launch(workspace, chunks, 2 * n, dgamma, dbeta, n, st);
   }
   return check_launch("layernorm_bwd");
 }

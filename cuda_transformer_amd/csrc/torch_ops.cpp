@@ -85,9 +85,13 @@ at::Tensor cuda_fma(at::Tensor x, at::Tensor weights, at::Tensor bias) {
   at::Tensor out = at::empty({x_batch, m, n}, x.options());
   const auto xs = strides_of<3>(x);
   const auto ws = strides_of<3>(weights);
+  const int64_t ws_bytes = cta_cuda_fma_workspace(x_batch, m, k, n);
+  at::Tensor scratch;
+  if (ws_bytes > 0) scratch = at::empty({ws_bytes / 4}, x.options());
   check_rc(cta_cuda_fma(x.data_ptr<float>(), xs.data(), weights.data_ptr<float>(), ws.data(),
                         bias.data_ptr<float>(), bias.stride(0), x_batch, m, k, n,
-                        weights.size(0), out.data_ptr<float>(), stream_of(x)));
+                        weights.size(0), out.data_ptr<float>(),
+                        ws_bytes > 0 ? scratch.data_ptr<float>() : nullptr, stream_of(x)));
   return out;
 }
 

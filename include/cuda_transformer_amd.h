@@ -104,15 +104,21 @@ int cta_flash_attention_bwd_dkdv(const float* q, const int64_t* q_strides,
  * Linear layer.
  * ---------------------------------------------------------------------------- */
 
+/* Bytes of optional scratch for cta_cuda_fma (0 when the shape fills the GPU without a
+ * K split). */
+int64_t cta_cuda_fma_workspace(int64_t batch, int64_t m, int64_t k, int64_t n);
+
 /* out[b] = x[b] . W[b or 0] + bias, out dense (batch, m, n).
  * x strides: 3 entries (batch, m, k).  W strides: 3 entries (batch, k, n); w_batch is 1
  * (broadcast, batch stride ignored) or `batch`.  Any strides: transposed views are read
- * in place.  Replaces cuda_transformer::cuda_fma (Transformer_launchers/linear_layer.cu:28-70). */
+ * in place.  `workspace` may be NULL; given cta_cuda_fma_workspace() bytes, shapes with few
+ * output tiles and a long K are split along K with a deterministic reduction.
+ * Replaces cuda_transformer::cuda_fma (Transformer_launchers/linear_layer.cu:28-70). */
 int cta_cuda_fma(const float* x, const int64_t* x_strides,
                  const float* w, const int64_t* w_strides,
                  const float* bias, int64_t bias_stride,
                  int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
-                 float* out, void* stream);
+                 float* out, float* workspace, void* stream);
 
 /* Bytes of scratch cta_db_calculation needs for a (batch, m, n) gradient. */
 int64_t cta_db_calculation_workspace(int64_t batch, int64_t m, int64_t n);

@@ -53,16 +53,18 @@ def test_layout_checks_run_before_launch():
 
 def test_workspace_queries():
     lib = capi.lib()
-    assert lib.cta_db_calculation_workspace(1, 8192, 3072) == 128 * 3072 * 4
+    assert lib.cta_db_calculation_workspace(1, 8192, 3072) == 256 * 3072 * 4
     assert lib.cta_db_calculation_workspace(0, 5, 5) == 0
     assert lib.cta_layernorm_bwd_workspace(8192, 768) > 0
     assert lib.cta_causal_self_attention_bwd_workspace(8, 33) == 8 * 33 * 33 * 4
+    assert lib.cta_cuda_fma_workspace(1, 8192, 768, 3072) == 0          # fills the GPU: no split
+    assert lib.cta_cuda_fma_workspace(1, 768, 8192, 3072) > 0           # 144 tiles, K = 8192
 
 
 def test_other_entry_points_validate_arguments():
     lib = capi.lib()
     s3 = capi.strides((1, 1, 1))
-    assert lib.cta_cuda_fma(16, s3, 16, s3, 16, 1, 2, 3, 4, 5, 3, 16, None) == INVALID  # w_batch
+    assert lib.cta_cuda_fma(16, s3, 16, s3, 16, 1, 2, 3, 4, 5, 3, 16, None, None) == INVALID  # w_batch
     assert lib.cta_gelu_fwd(16, 16, -1, None) == INVALID
     assert lib.cta_gelu_fwd(20, 16, 8, None) == LAYOUT
     assert lib.cta_softmax_fwd(16, 16, -1, 4, None) == INVALID

@@ -190,3 +190,37 @@ def test_causal_self_attention(cuda, B, T, nh, hs, causal):
 
     ref_grad = np.concatenate([unheads(g_r[0]) / sm, unheads(g_r[1]) / sm, unheads(g_r[2])], -1)
     np.testing.assert_allclose(f64(qg.grad), ref_grad, atol=1e-4, rtol=1e-5)
+
+
+@pytest.mark.parametrize("B,M,K,N", [(1, 100, 3000, 130), (2, 64, 4096, 96), (1, 768, 8192, 256)])
+def test_linear_split_k(cuda, B, M, K, N):
+    """Few output tiles and a long K: the GEMM splits K across workgroups (deterministic)."""
+    from cuda_transformer.ops import cuda_fma
+    from cuda_transformer_amd import capi
+
+    assert capi.lib().cta_cuda_fma_workspace(B, M, K, N) > 0
+    x = seeded((B, M, K), 31, kind="rand")
+    w = seeded((K, N), 32) * 0.05
+    b = seeded((N,), 33)
+    out = cuda_fma(x.to(cuda), w.to(cuda), b.to(cuda))
+    ref = lin.fma_forward(f64(x), f64(w), f64(b))
+    assert rel_err(f64(out), ref) <= 1e-6
+    out2 = cuda_fma(x.to(cuda), w.to(cuda), b.to(cuda))
+    assert torch.equal(out, out2)
+    # transposed operand view (the linear backward's x^T): (B, K, M) . (B, M, N)
+    dyt = seeded((B, M, N), 34).to(cuda)
+    out3 = cuda_fma(x.to(cuda).transpose(1, 2), dyt, torch.zeros(N, device=cuda))
+    assert rel_err(f64(out3), np.swapaxes(f64(x), 1, 2) @ f64(dyt)) <= 1e-6
+
+
+def test_db_strided_views(cuda):
+    from cuda_transformer.ops import db_calculation
+
+    base = seeded((3, 50, 70), 35).to(cuda)
+    for dy in (base, base[:, 5:45, :], base.transpose(1, 2), base[:, :, 3:67]):
+        got = db_calculation(dy)
+        np.testing.assert_allclose(f64(got), f64(dy).sum(axis=(0, 1)), rtol=1e-5, atol=1e-4)
+    big = seeded((2, 4100, 1030), 36).to(cuda)
+    np.testing.assert_allclose(f64(db_calculation(big)), f64(big).sum(axis=(0, 1)), rtol=1e-5,
+                               atol=1e-3)
+    assert torch.equal(db_calculation(big), db_calculation(big))
