@@ -45,9 +45,10 @@ REFERENCE_RTX5070_MS = {"fwd": 212.73, "bwd": 1259.32}
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--workload", choices=["fa2", "fa2-sweep", "ops"], default="fa2",
+    p.add_argument("--workload", choices=["fa2", "fa2-sweep", "ops", "gpt"], default="fa2",
                    help="fa2: the headline step (default, one JSON line); fa2-sweep: BASELINE "
-                        "config 3; ops: BASELINE config 4 (one JSON line per op)")
+                        "config 3; ops: BASELINE config 4 (one JSON line per op); gpt: BASELINE "
+                        "config 5 training step")
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--batch", type=int, default=4)
@@ -414,6 +415,75 @@ def ops_workload(args):
     return 0
 
 
+def gpt_workload(args):
+    """one training step (fwd + bwd + AdamW) of the small GPT on the HIP
+    kernels (cuda_transformer_amd/gpt.py), batch 64 x context 256; tokens/s.  CPU baseline: the
+    plain-torch model (oracle/gpt.py) on this host, batch 8, same step."""
+    import torch
+
+    from cuda_transformer_amd.gpt import GPT, GPTConfig, init_weights_, synthetic_batch
+    from oracle import gpt as ogpt
+
+    cfg, batch = GPTConfig(), 64
+    model = GPT(cfg)
+    init_weights_(model, seed=0)
+    model.cuda()
+    opt = torch.optim.AdamW(model.parameters(), lr=6e-4)
+    batches = [synthetic_batch(cfg, batch, seed=s, device="cuda") for s in range(4)]
+
+    def step(i, optimize=True):
+        opt.zero_grad(set_to_none=True)
+        _, loss = model(*batches[i % 4])
+        loss.backward()
+        if optimize:
+            opt.step()
+        return loss
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i, optimize=False)
+    torch.cuda.synchronize()
+    ms_fb = (time.perf_counter() - t0) * 1e3 / args.steps
+    tokens = batch * cfg.block_size
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cores = min(16, os.cpu_count() or 1)
+        torch.set_num_threads(cores)
+        ref = ogpt.GPT(cfg)
+        ref.load_state_dict({k: v.cpu() for k, v in model.state_dict().items()})
+        ropt = torch.optim.AdamW(ref.parameters(), lr=6e-4)
+        cb = 8
+        idx, tgt = synthetic_batch(cfg, cb, seed=0)
+
+        def cpu_step():
+            ropt.zero_grad(set_to_none=True)
+            _, l_ = ref(idx, tgt)
+            l_.backward()
+            ropt.step()
+
+        cpu_s = _cpu_time(cpu_step, target_s=args.cpu_seconds)
+        cpu = {"value": round(cb * cfg.block_size / cpu_s, 1), "unit": "tokens/s", "cores": cores,
+               "kind": "port", "sample": f"batch {cb} x {cfg.block_size} tokens, plain-torch model "
+                                         f"(oracle/gpt.py), fwd+bwd+AdamW, float32, "
+                                         f"{torch.get_num_threads()} threads"}
+    print(json.dumps({
+        "workload": "small-GPT training step (6L 6H d384 ctx256 vocab65, batch 64), FP32",
+        "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 3),
+        "fwd_bwd_ms": round(ms_fb, 3), "fwd_bwd_tokens_per_s": round(tokens / (ms_fb * 1e-3), 1),
+        "steps": args.steps, "cpu_baseline": cpu,
+    }), flush=True)
+    return 0
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -437,6 +507,8 @@ def main():
         return ops_workload(args)
     if args.workload == "fa2-sweep":
         return fa2_sweep(args)
+    if args.workload == "gpt":
+        return gpt_workload(args)
     B, H, N, D = args.batch, args.heads, args.seq, args.head_dim
     causal = not args.non_causal
     ms_step, per_kernel, (q, k, v, do) = fa2_timings(B, H, N, D, causal, args.steps, args.warmup)
