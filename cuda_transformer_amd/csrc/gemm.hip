@@ -25,70 +25,94 @@ enum LoadMode { kVecK = 0, kVecMN = 1, kScalar = 2 };
 
 namespace {
 
-constexpr int GBM = 128, GBN = 128, GBK = 16;
-constexpr int GKP = GBK + 4;  // LDS pitch (floats) of one m (or n) row of a k-slice
+// Workgroup tile BM x BN, K-slice BK, WM x WN waves; each wave owns a (BM/WM) x (BN/WN) block of
+// 32x32 MFMA tiles.  LDS rows hold one k-slice of one m (or n) index, pitch BK + 4 floats.
+template <int BM_, int BN_, int BK_, int WM_, int WN_>
+struct GemmTile {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+  static constexpr int THREADS = 64 * WM * WN;
+  static constexpr int MB = BM / WM / 32;  // MFMA tiles per wave along m
+  static constexpr int NB = BN / WN / 32;  // ... along n
+  static constexpr int KP = BK + 4;
+  static constexpr int LDS_FLOATS = 2 * (BM + BN) * KP;  // double buffered
+  static_assert(MB >= 1 && NB >= 1 && BK % 8 == 0, "bad GEMM tile");
+};
 
-// Loads one 128 x 16 slice of an operand into registers.  `rows` indexes m (A) or n (B);
-// the operand is row-major in (row, k) when kVecK, (k, row) when kVecMN.
-template <int MODE>
+// Row and k offset of float4 number f of a k-contiguous slice.  Four lanes read one row's 64
+// contiguous bytes.  With BK = 16 (LDS pitch 20 floats) a 16-byte LDS write serves 8 lanes =
+// 2 rows at once, and rows r and r+4 start 4 bank groups apart: pairing them keeps the 8
+// writes on 8 distinct bank groups.
+template <int BK>
+__device__ __forceinline__ void veck_coords(int f, int& r, int& k4) {
+  if (BK == 16) {
+    const int g = f >> 3, l = f & 7;
+    r = ((g >> 2) << 3) + (g & 3) + ((l >> 2) << 2);
+    k4 = (l & 3) * 4;
+  } else {
+    r = f / (BK / 4);
+    k4 = (f % (BK / 4)) * 4;
+  }
+}
+
+// Loads one ROWS x BK slice of an operand into registers.  `rows` indexes m (A) or n (B); the
+// operand is row-major in (row, k) when kVecK, (k, row) when kVecMN.
+template <int MODE, int ROWS, int BK, int THREADS>
 struct TileLoader {
-  float4 v[2];
+  static constexpr int LOADS = ROWS * BK / 4 / THREADS;
+  static_assert(ROWS * BK % (4 * THREADS) == 0, "tile must split evenly over the workgroup");
+  float4 v[LOADS];
+  bool kin[LOADS];  // vector modes: the float4 lies inside K (zeroed at store time otherwise)
   __device__ __forceinline__ void load(const float* base, int64_t s_row, int64_t s_k, int row0,
                                        int k0, int R, int K, int tid) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int f = tid + 256 * u;
-      if (MODE == kVecK) {
-        const int r = f >> 2, k4 = (f & 3) * 4;
-        const int gr = row0 + r, gk = k0 + k4;
-        const float* p = base + (int64_t)gr * s_row + gk;
-        if (gr < R && gk + 3 < K) {
-          v[u] = ld4(p);
-        } else {
-          float t[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) t[e] = (gr < R && gk + e < K) ? p[e] : 0.0f;
-          v[u] = make_float4(t[0], t[1], t[2], t[3]);
-        }
-      } else if (MODE == kVecMN) {
-        const int k = f >> 5, r4 = (f & 31) * 4;
+    for (int u = 0; u < LOADS; ++u) {
+      const int f = tid + THREADS * u;
+      if (MODE == kVecMN) {
+        // k varies fastest across lanes: each 16-lane group reads 64 contiguous bytes of one k
+        // row and the LDS transpose below writes 16 consecutive words (no bank conflicts).
+        // Branch-free: always one dwordx4 from a clamped in-bounds address (R % 4 == 0), so the
+        // wait counters stay exact.  Rows past R only feed output rows/columns that are never
+        // stored; k past K must contribute zero and is masked when the slice is stored to LDS.
+        const int k = f % BK, r4 = (f / BK) * 4;
         const int gr = row0 + r4, gk = k0 + k;
-        const float* p = base + (int64_t)gk * s_k + gr;
-        if (gk < K && gr + 3 < R) {
-          v[u] = ld4(p);
-        } else {
-          float t[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) t[e] = (gk < K && gr + e < R) ? p[e] : 0.0f;
-          v[u] = make_float4(t[0], t[1], t[2], t[3]);
-        }
+        v[u] = ld4(base + (int64_t)min(gk, K - 1) * s_k + min(gr, R - 4));
+        kin[u] = gk < K;
+      } else if (MODE == kVecK) {
+        int r, k4;
+        veck_coords<BK>(f, r, k4);
+        const int gr = row0 + r, gk = k0 + k4;
+        v[u] = ld4(base + (int64_t)min(gr, R - 1) * s_row + min(gk, K - 4));
+        kin[u] = gk < K;  // K % 4 == 0: a float4 is wholly inside or outside
       } else {
-        const int r = f >> 2, k4 = (f & 3) * 4;
-        const int gr = row0 + r;
+        int r, k4;
+        veck_coords<BK>(f, r, k4);
+        const int gr = row0 + r, gk = k0 + k4;
         float t[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int gk = k0 + k4 + e;
-          t[e] = (gr < R && gk < K) ? base[(int64_t)gr * s_row + (int64_t)gk * s_k] : 0.0f;
-        }
+        for (int e = 0; e < 4; ++e)
+          t[e] = (gr < R && gk + e < K) ? base[(int64_t)gr * s_row + (int64_t)(gk + e) * s_k] : 0.0f;
         v[u] = make_float4(t[0], t[1], t[2], t[3]);
+        kin[u] = true;
       }
     }
   }
-  // LDS image: [row][k], pitch GKP.
+  // LDS image: [row][k], pitch BK + 4.
   __device__ __forceinline__ void store(float* lds, int tid) const {
+    constexpr int KP = BK + 4;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int f = tid + 256 * u;
+    for (int u = 0; u < LOADS; ++u) {
+      const int f = tid + THREADS * u;
+      const float4 w = kin[u] ? v[u] : zero4();
       if (MODE == kVecMN) {
-        const int k = f >> 5, r4 = (f & 31) * 4;
-        lds[(r4 + 0) * GKP + k] = v[u].x;
-        lds[(r4 + 1) * GKP + k] = v[u].y;
-        lds[(r4 + 2) * GKP + k] = v[u].z;
-        lds[(r4 + 3) * GKP + k] = v[u].w;
+        const int k = f % BK, r4 = (f / BK) * 4;
+        lds[(r4 + 0) * KP + k] = w.x;
+        lds[(r4 + 1) * KP + k] = w.y;
+        lds[(r4 + 2) * KP + k] = w.z;
+        lds[(r4 + 3) * KP + k] = w.w;
       } else {
-        const int r = f >> 2, k4 = (f & 3) * 4;
-        st4(lds + r * GKP + k4, v[u]);
+        int r, k4;
+        veck_coords<BK>(f, r, k4);
+        st4(lds + r * KP + k4, w);
       }
     }
   }
@@ -97,18 +121,21 @@ struct TileLoader {
 // split_ws == nullptr: out = alpha * A B (+ bias, mask) written through C.
 // split_ws != nullptr: blockIdx.z = s * Z + z covers K range [s*kchunk, (s+1)*kchunk) and the raw
 // partial sum goes to split_ws[s][z][m][n] (dense); gemm_splitk_reduce finishes the epilogue.
-template <int AMODE, int BMODE>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmOperand A, GemmOperand B, GemmOut C,
-                                                      GemmEpilogue ep, int M, int N, int K,
-                                                      int zin, int Z, int kchunk,
-                                                      float* __restrict__ split_ws) {
-  __shared__ __attribute__((aligned(16))) float smem[2 * (GBM + GBN) * GKP];
+template <class TL, int AMODE, int BMODE>
+__global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOperand B,
+                                                           GemmOut C, GemmEpilogue ep, int M,
+                                                           int N, int K, int zin, int Z,
+                                                           int kchunk,
+                                                           float* __restrict__ split_ws) {
+  constexpr int BM = TL::BM, BN = TL::BN, BK = TL::BK, KP = TL::KP;
+  constexpr int MB = TL::MB, NB = TL::NB, KC = BK / 8;  // KC: 16-byte chunks per lane half
+  __shared__ __attribute__((aligned(16))) float smem[TL::LDS_FLOATS];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, col = lane & 31;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / TL::WN, wn = wave % TL::WN;
 
-  const int n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM;
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
   const int z = blockIdx.z % Z, split = blockIdx.z / Z;
   const int zo = z / zin, zi = z - zo * zin;
   const float* Ab = A.p + zo * A.s_outer + zi * A.s_inner;
@@ -117,71 +144,95 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmOperand A, GemmOperand
   const int ke = min(K, kb + kchunk);
 
   // A rows are m with (s_row, s_col) = (m, k); B "rows" are n with (n, k) = (s_col, s_row).
-  TileLoader<AMODE> la;
-  TileLoader<BMODE> lb;
-  const int nk = (ke - kb + GBK - 1) / GBK;
+  // Global loads run two K-slices ahead of the MFMAs (two register sets, alternating), so a
+  // slice's loads have two slices of MFMA work to arrive; LDS is double buffered.  Vector-mode
+  // loads clamp their addresses into the operand, so reads past K stay in bounds.
+  using LA = TileLoader<AMODE, BM, BK, TL::THREADS>;
+  using LB = TileLoader<BMODE, BN, BK, TL::THREADS>;
+  LA la0, la1;
+  LB lb0, lb1;
+  const int nk = (ke - kb + BK - 1) / BK;
 
-  f32x16 acc[2][2];
+  f32x16 acc[MB][NB];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
+    for (int j = 0; j < NB; ++j) acc[i][j] = zero16();
 
-  la.load(Ab, A.s_row, A.s_col, m0, kb, M, ke, tid);
-  lb.load(Bb, B.s_col, B.s_row, n0, kb, N, ke, tid);
-  la.store(smem, tid);
-  lb.store(smem + GBM * GKP, tid);
+  // Slice count rounded up to even: slices past the end load clamped addresses whose k lies
+  // beyond ke, so they are stored as zeros and add nothing.  The loop then has no conditional
+  // loads or stores, which keeps the compiler's wait counts exact (a load issued two slices
+  // ahead is not waited for until its LDS store).
+  const int nk2 = (nk + 1) & ~1;
+  la0.load(Ab, A.s_row, A.s_col, m0, kb, M, ke, tid);
+  lb0.load(Bb, B.s_col, B.s_row, n0, kb, N, ke, tid);
+  la1.load(Ab, A.s_row, A.s_col, m0, kb + BK, M, ke, tid);
+  lb1.load(Bb, B.s_col, B.s_row, n0, kb + BK, N, ke, tid);
+  la0.store(smem, tid);
+  lb0.store(smem + BM * KP, tid);
   __syncthreads();
 
-  for (int t = 0; t < nk; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < nk) {
-      la.load(Ab, A.s_row, A.s_col, m0, kb + (t + 1) * GBK, M, ke, tid);
-      lb.load(Bb, B.s_col, B.s_row, n0, kb + (t + 1) * GBK, N, ke, tid);
-    }
-    const float* as = smem + buf * (GBM + GBN) * GKP;
-    const float* bs = as + GBM * GKP;
-    float4 af[2][2], bf[2][2];
+  auto mma = [&](const float* as) {
+    const float* bs = as + BM * KP;
+    float4 af[MB][KC], bf[NB][KC];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const float* ap = as + (wm * 64 + i * 32 + col) * GKP + half * (GBK / 2);
-      const float* bp = bs + (wn * 64 + i * 32 + col) * GKP + half * (GBK / 2);
-      af[i][0] = ld4(ap);
-      af[i][1] = ld4(ap + 4);
-      bf[i][0] = ld4(bp);
-      bf[i][1] = ld4(bp + 4);
+    for (int i = 0; i < MB; ++i) {
+      const float* ap = as + (wm * (BM / TL::WM) + i * 32 + col) * KP + half * (BK / 2);
+#pragma unroll
+      for (int c = 0; c < KC; ++c) af[i][c] = ld4(ap + 4 * c);
     }
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
+    for (int j = 0; j < NB; ++j) {
+      const float* bp = bs + (wn * (BN / TL::WN) + j * 32 + col) * KP + half * (BK / 2);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int c = 0; c < KC; ++c) bf[j][c] = ld4(bp + 4 * c);
+    }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          acc[i][j] = mfma32(af[i][c].x, bf[j][c].x, acc[i][j]);
-          acc[i][j] = mfma32(af[i][c].y, bf[j][c].y, acc[i][j]);
-          acc[i][j] = mfma32(af[i][c].z, bf[j][c].z, acc[i][j]);
-          acc[i][j] = mfma32(af[i][c].w, bf[j][c].w, acc[i][j]);
-        }
+    for (int c = 0; c < KC; ++c) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j) {
+            const float a = e == 0 ? af[i][c].x : e == 1 ? af[i][c].y : e == 2 ? af[i][c].z : af[i][c].w;
+            const float b = e == 0 ? bf[j][c].x : e == 1 ? bf[j][c].y : e == 2 ? bf[j][c].z : bf[j][c].w;
+            acc[i][j] = mfma32(a, b, acc[i][j]);
+          }
     }
-    if (t + 1 < nk) {
-      float* nas = smem + (buf ^ 1) * (GBM + GBN) * GKP;
-      la.store(nas, tid);
-      lb.store(nas + GBM * GKP, tid);
-    }
+  };
+  float* const buf0 = smem;
+  float* const buf1 = smem + (BM + BN) * KP;
+  for (int t = 0; t < nk2; t += 2) {
+    // slice t from buf0; slices t+2 (set 0) and t+1 (set 1, stored below) in flight
+    la0.load(Ab, A.s_row, A.s_col, m0, kb + (t + 2) * BK, M, ke, tid);
+    lb0.load(Bb, B.s_col, B.s_row, n0, kb + (t + 2) * BK, N, ke, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(buf0);
+    la1.store(buf1, tid);
+    lb1.store(buf1 + BM * KP, tid);
+    __syncthreads();
+    // slice t+1 from buf1
+    la1.load(Ab, A.s_row, A.s_col, m0, kb + (t + 3) * BK, M, ke, tid);
+    lb1.load(Bb, B.s_col, B.s_row, n0, kb + (t + 3) * BK, N, ke, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(buf1);
+    la0.store(buf0, tid);
+    lb0.store(buf0 + BM * KP, tid);
     __syncthreads();
   }
 
   if (split_ws != nullptr) {
     float* Pb = split_ws + ((int64_t)split * Z + z) * M * N;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + wn * 64 + j * 32 + col;
+    for (int j = 0; j < NB; ++j) {
+      const int n = n0 + wn * (BN / TL::WN) + j * 32 + col;
       if (n >= N) continue;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm * 64 + i * 32 + mfma_row(r, half);
+          const int m = m0 + wm * (BM / TL::WM) + i * 32 + mfma_row(r, half);
           if (m < M) Pb[(int64_t)m * N + n] = acc[i][j][r];
         }
     }
@@ -189,15 +240,15 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmOperand A, GemmOperand
   }
   float* Cb = C.p + zo * C.s_outer + zi * C.s_inner;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + wn * 64 + j * 32 + col;
+  for (int j = 0; j < NB; ++j) {
+    const int n = n0 + wn * (BN / TL::WN) + j * 32 + col;
     if (n >= N) continue;
     const float bv = ep.bias ? ep.bias[(int64_t)n * ep.bias_stride] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < MB; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 64 + i * 32 + mfma_row(r, half);
+        const int m = m0 + wm * (BM / TL::WM) + i * 32 + mfma_row(r, half);
         if (m < M) {
           float val = fmaf(ep.alpha, acc[i][j][r], bv);
           if (ep.causal_mask && n > m) val = -INFINITY;
@@ -234,44 +285,89 @@ bool vec_ok(const GemmOperand& op, bool contig_is_col) {
   return aligned16(op.p) && s_other % 4 == 0 && op.s_outer % 4 == 0 && op.s_inner % 4 == 0;
 }
 
-int pick_mode(const GemmOperand& op, bool is_a) {
-  // For A: (s_row, s_col) = (m, k) -> kVecK when k is contiguous.
-  // For B: (s_row, s_col) = (k, n) -> kVecK (n-major, k contiguous) when s_row == 1.
+// Load mode of an operand.  A: (s_row, s_col) = (m, k); B: (k, n).  `rows` is M for A and N for
+// B.  The vector modes also need the contiguous extent to be a multiple of 4 (the branch-free
+// loads clamp whole float4s) and at least 4.
+int pick_mode(const GemmOperand& op, bool is_a, int64_t rows, int64_t K) {
   const int64_t s_k = is_a ? op.s_col : op.s_row;
   const int64_t s_mn = is_a ? op.s_row : op.s_col;
-  if (s_k == 1 && vec_ok(op, is_a)) return kVecK;
-  if (s_mn == 1 && vec_ok(op, !is_a)) return kVecMN;
+  if (s_k == 1 && K % 4 == 0 && K >= 4 && vec_ok(op, is_a)) return kVecK;
+  if (s_mn == 1 && rows % 4 == 0 && rows >= 4 && vec_ok(op, !is_a)) return kVecMN;
   return kScalar;
 }
 
-template <int AM>
+template <class TL, int AM>
 void dispatch_b(int bm, dim3 grid, hipStream_t st, const GemmOperand& A, const GemmOperand& B,
                 const GemmOut& C, const GemmEpilogue& ep, int M, int N, int K, int zin, int Z,
                 int kchunk, float* ws) {
+  const dim3 block(TL::THREADS);
   if (bm == kVecK)
-    hipLaunchKernelGGL((gemm_kernel<AM, kVecK>), grid, dim3(256), 0, st, A, B, C, ep, M, N, K, zin,
-                       Z, kchunk, ws);
+    hipLaunchKernelGGL((gemm_kernel<TL, AM, kVecK>), grid, block, 0, st, A, B, C, ep, M, N, K,
+                       zin, Z, kchunk, ws);
   else if (bm == kVecMN)
-    hipLaunchKernelGGL((gemm_kernel<AM, kVecMN>), grid, dim3(256), 0, st, A, B, C, ep, M, N, K,
+    hipLaunchKernelGGL((gemm_kernel<TL, AM, kVecMN>), grid, block, 0, st, A, B, C, ep, M, N, K,
                        zin, Z, kchunk, ws);
   else
-    hipLaunchKernelGGL((gemm_kernel<AM, kScalar>), grid, dim3(256), 0, st, A, B, C, ep, M, N, K,
+    hipLaunchKernelGGL((gemm_kernel<TL, AM, kScalar>), grid, block, 0, st, A, B, C, ep, M, N, K,
                        zin, Z, kchunk, ws);
 }
 
 // K splits for a GEMM whose output tiles alone cannot fill the 256 CUs: enough splits for
 // ~512 workgroups, each keeping at least 512 of K; 1 = no split.
+template <class TL>
 int64_t splitk_factor(int64_t M, int64_t N, int64_t K, int64_t Z) {
-  const int64_t tiles = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN) * Z;
+  const int64_t tiles = ((M + TL::BM - 1) / TL::BM) * ((N + TL::BN - 1) / TL::BN) * Z;
   if (tiles >= 256 || K < 1024) return 1;
-  const int64_t s = std::min<int64_t>({(512 + tiles - 1) / tiles, K / 512, 8});
+  const int64_t s = std::min<int64_t>({(512 + tiles - 1) / tiles, K / 512, 16});
   return s >= 2 ? s : 1;
 }
+
+template <class TL>
+int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& C,
+                     const GemmEpilogue& ep, int64_t M, int64_t N, int64_t K, int64_t Z,
+                     int64_t zin, hipStream_t st, float* workspace, int64_t workspace_floats) {
+  if (M <= 0 || N <= 0 || Z <= 0) return CTA_OK;
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || Z > 65535 || zin <= 0)
+    return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM size out of range");
+  int64_t S = splitk_factor<TL>(M, N, K, Z);
+  if (S > 1 && (workspace == nullptr || workspace_floats < S * Z * M * N)) S = 1;
+  const int64_t kchunk =
+      S > 1 ? ((K + S - 1) / S + TL::BK - 1) / TL::BK * TL::BK : std::max<int64_t>(K, 1);
+  const dim3 grid((unsigned)((N + TL::BN - 1) / TL::BN), (unsigned)((M + TL::BM - 1) / TL::BM),
+                  (unsigned)(Z * S));
+  if (grid.y > 65535 || grid.z > 65535) return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM grid too large");
+  float* ws = S > 1 ? workspace : nullptr;
+  const int am = pick_mode(A, true, M, K);
+  const int bm = pick_mode(B, false, N, K);
+  if (am == kVecK)
+    dispatch_b<TL, kVecK>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin, (int)Z,
+                          (int)kchunk, ws);
+  else if (am == kVecMN)
+    dispatch_b<TL, kVecMN>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin, (int)Z,
+                           (int)kchunk, ws);
+  else
+    dispatch_b<TL, kScalar>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin, (int)Z,
+                            (int)kchunk, ws);
+  if (S > 1) {
+    const int64_t total = Z * M * N;
+    const unsigned rgrid = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(rgrid), dim3(256), 0, st, ws, (int)S, (int)Z,
+                       (int)M, (int)N, C, ep, (int)zin);
+  }
+  return check_launch("gemm");
+}
+
+// Tile choice, from measured sweeps of the config-4 and small-GPT shapes on an MI355X:
+// shapes split along K run best with eight 32x64 waves, narrow outputs (N <= 768) with a
+// 128x64 tile, everything else with four 64x64 waves.
+using SplitTile = GemmTile<128, 128, 16, 4, 2>;
+using NarrowTile = GemmTile<128, 64, 16, 2, 2>;
+using WideTile = GemmTile<128, 128, 16, 2, 2>;
 
 }  // namespace
 
 int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, int64_t Z) {
-  const int64_t S = splitk_factor(M, N, K, Z);
+  const int64_t S = splitk_factor<SplitTile>(M, N, K, Z);
   return S > 1 ? S * Z * M * N : 0;
 }
 
@@ -280,31 +376,13 @@ int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, int64_t Z) {
 int gemm_launch(const GemmOperand& A, const GemmOperand& B, const GemmOut& C,
                 const GemmEpilogue& ep, int64_t M, int64_t N, int64_t K, int64_t Z, int64_t zin,
                 hipStream_t st, float* workspace, int64_t workspace_floats) {
-  if (M <= 0 || N <= 0 || Z <= 0) return CTA_OK;
-  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || Z > 65535 || zin <= 0)
-    return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM size out of range");
-  int64_t S = splitk_factor(M, N, K, Z);
-  if (S > 1 && (workspace == nullptr || workspace_floats < S * Z * M * N)) S = 1;
-  const int64_t kchunk = S > 1 ? ((K + S - 1) / S + GBK - 1) / GBK * GBK : std::max<int64_t>(K, 1);
-  const dim3 grid((unsigned)((N + GBN - 1) / GBN), (unsigned)((M + GBM - 1) / GBM),
-                  (unsigned)(Z * S));
-  if (grid.y > 65535 || grid.z > 65535) return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM grid too large");
-  float* ws = S > 1 ? workspace : nullptr;
-  const int am = pick_mode(A, true);
-  const int bm = pick_mode(B, false);
-  if (am == kVecK)
-    dispatch_b<kVecK>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin, (int)Z, (int)kchunk, ws);
-  else if (am == kVecMN)
-    dispatch_b<kVecMN>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin, (int)Z, (int)kchunk, ws);
-  else
-    dispatch_b<kScalar>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin, (int)Z, (int)kchunk, ws);
-  if (S > 1) {
-    const int64_t total = Z * M * N;
-    const unsigned rgrid = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
-    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(rgrid), dim3(256), 0, st, ws, (int)S, (int)Z,
-                       (int)M, (int)N, C, ep, (int)zin);
-  }
-  return check_launch("gemm");
+  const int64_t S = splitk_factor<SplitTile>(M, N, K, Z);
+  if (S > 1 && workspace != nullptr && workspace_floats >= S * Z * M * N)
+    return gemm_launch_tile<SplitTile>(A, B, C, ep, M, N, K, Z, zin, st, workspace,
+                                       workspace_floats);
+  if (N <= 768)
+    return gemm_launch_tile<NarrowTile>(A, B, C, ep, M, N, K, Z, zin, st, nullptr, 0);
+  return gemm_launch_tile<WideTile>(A, B, C, ep, M, N, K, Z, zin, st, nullptr, 0);
 }
 
 }  // namespace cta
