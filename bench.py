@@ -3,8 +3,10 @@
 
 Workload: B=4, H=32, N=4096, D=64, causal; Q, K, V, dO ~ N(0, 1) from fixed
 seeds; softmax scale 1/sqrt(64).  One step = the forward kernel then the three backward
-stages (delta, dQ, dK/dV), launched through the C ABI on torch's current stream with all
-inputs and outputs already resident in HBM.
+stages, launched through the C ABI on torch's current stream with all inputs and outputs
+already resident in HBM.  The backward runs the schedule the flash_attention_bwd operator
+uses: delta, dK/dV storing dS, dQ from the stored dS (--bwd-schedule stored, default); or the
+reference's schedule, delta, dQ recomputing S and dP, dK/dV (--bwd-schedule recompute).
 
 Reported:
   value          whole-step TFLOPS by the reference's formula (benchmark/cuda_bench.py:63-68):
@@ -56,6 +58,9 @@ def parse_args():
     p.add_argument("--seq", type=int, default=4096)
     p.add_argument("--head-dim", type=int, default=64)
     p.add_argument("--non-causal", action="store_true")
+    p.add_argument("--bwd-schedule", choices=["stored", "recompute"], default="stored",
+                   help="stored: dK/dV writes dS and dQ reads it (what the operator runs); "
+                        "recompute: the reference's delta / dQ / dK/dV schedule")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="target CPU time of the bounded CPU-baseline sample")
@@ -90,10 +95,11 @@ def kernel_algorithmic(name, B, H, N, D, causal):
     """(amount, unit, bound) of algorithmic work per launch of one kernel.
 
     Attention kernels: 2*D FLOPs per (query, key) pair for each N x N x D product the kernel
-    must form — forward 2 products (S, PV), dQ 3 (S, dP, dQ), dK/dV 4 (S, dP, dV, dK) — over
-    B*H*N^2 pairs, halved when causal.  delta: bytes of O and dO read plus delta written."""
+    must form — forward 2 products (S, PV), dQ 3 (S, dP, dQ), dK/dV 4 (S, dP, dV, dK), dQ from
+    stored dS 1 — over B*H*N^2 pairs, halved when causal.  delta: bytes of O and dO read plus
+    delta written."""
     pairs = B * H * N * N * (0.5 if causal else 1.0)
-    products = {"fwd": 2, "dq": 3, "dkdv": 4}
+    products = {"fwd": 2, "dq": 3, "dkdv": 4, "dq_ds": 1}
     if name in products:
         return 2.0 * D * pairs * products[name], "TFLOP/s", "mfma"
     return float(2 * B * H * N * D * 4 + B * H * N * 4), "GB/s", "hbm"
@@ -146,9 +152,15 @@ def cpu_baseline(B, H, N, D, causal, target_s):
     }
 
 
-def fa2_timings(B, H, N, D, causal, steps, warmup):
-    """Time `steps` FA2 steps [fwd, delta, dQ, dK/dV] through the C ABI on torch's current
-    stream.  Returns (wall ms per step, {kernel: mean HIP-event ms}, (q, k, v, dO))."""
+# Largest dS workspace the flash_attention_bwd operator allocates (torch_ops.cpp).
+BWD_WORKSPACE_CAP = 8 << 30
+
+
+def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored"):
+    """Time `steps` FA2 steps through the C ABI on torch's current stream: fwd, then the
+    backward stages of `schedule` ([delta, dkdv, dq_ds] stored; [delta, dq, dkdv] recompute;
+    one combined [bwd] launch when the stored schedule needs head chunks, as the operator
+    runs it).  Returns (wall ms per step, {kernel: mean HIP-event ms}, (q, k, v, dO))."""
     import torch
 
     from cuda_transformer_amd import capi
@@ -161,13 +173,16 @@ def fa2_timings(B, H, N, D, causal, steps, warmup):
     L = torch.empty(B, H, N, device=dev)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
     delta = torch.empty(B, H, N, device=dev)
+    ws_full = capi.lib().cta_flash_attention_bwd_workspace(B, H, N, D, int(causal))
+    ws_bytes = min(ws_full, BWD_WORKSPACE_CAP) if schedule == "stored" else 0
+    ws = torch.empty(max(1, ws_bytes // 4), device=dev)
 
     stream = torch.cuda.current_stream(dev)
     st = ctypes.c_void_p(stream.cuda_stream)
     s4 = capi.strides(q.stride())
     s3 = capi.strides(L.stride())
     P = {name: ctypes.c_void_p(t.data_ptr()) for name, t in
-         dict(q=q, k=k, v=v, do=do, O=O, L=L, dq=dq, dk=dk, dv=dv, delta=delta).items()}
+         dict(q=q, k=k, v=v, do=do, O=O, L=L, dq=dq, dk=dk, dv=dv, delta=delta, ws=ws).items()}
     lib = capi.lib()
     c = int(causal)
 
@@ -182,14 +197,30 @@ def fa2_timings(B, H, N, D, causal, steps, warmup):
             rc = lib.cta_flash_attention_bwd_dq(P["q"], s4, P["k"], s4, P["v"], s4, P["do"], s4,
                                                 P["L"], s3, P["delta"], B, H, N, D, c, P["dq"],
                                                 st)
-        else:
+        elif kernel == "dkdv" and schedule == "recompute":
             rc = lib.cta_flash_attention_bwd_dkdv(P["q"], s4, P["k"], s4, P["v"], s4, P["do"],
                                                   s4, P["L"], s3, P["delta"], B, H, N, D, c,
                                                   P["dk"], P["dv"], st)
+        elif kernel == "dkdv":
+            rc = lib.cta_flash_attention_bwd_dkdv_store_ds(
+                P["q"], s4, P["k"], s4, P["v"], s4, P["do"], s4, P["L"], s3, P["delta"], B, H,
+                N, D, c, P["dk"], P["dv"], P["ws"], st)
+        elif kernel == "dq_ds":
+            rc = lib.cta_flash_attention_bwd_dq_from_ds(P["k"], s4, P["ws"], B, H, N, D, c,
+                                                        P["dq"], st)
+        else:  # "bwd": the combined entry point, chunked over heads
+            rc = lib.cta_flash_attention_bwd(P["q"], s4, P["k"], s4, P["v"], s4, P["O"], s4,
+                                             P["do"], s4, P["L"], s3, B, H, N, D, c, P["dq"],
+                                             P["dk"], P["dv"], P["delta"], P["ws"], ws_bytes, st)
         if rc != 0:
             raise RuntimeError(f"{kernel}: {lib.cta_last_error().decode()}")
 
-    kernels = ["fwd", "delta", "dq", "dkdv"]
+    if schedule == "recompute":
+        kernels = ["fwd", "delta", "dq", "dkdv"]
+    elif ws_full <= ws_bytes:
+        kernels = ["fwd", "delta", "dkdv", "dq_ds"]
+    else:
+        kernels = ["fwd", "bwd"]
 
     def step(events=None):
         for i, kname in enumerate(kernels):
@@ -222,11 +253,12 @@ def fa2_sweep(args):
 
     for N in (1024, 2048, 4096, 8192, 16384):
         steps = max(2, args.steps // (N // 1024))
-        ms, per_kernel, _ = fa2_timings(4, 32, N, 64, False, steps, 1)
+        ms, per_kernel, _ = fa2_timings(4, 32, N, 64, False, steps, 1, args.bwd_schedule)
         fwd_fl, bwd_fl = attn_flops(4, 32, N, 64, False)
-        bwd_ms = per_kernel["delta"] + per_kernel["dq"] + per_kernel["dkdv"]
+        bwd_ms = sum(v_ for k_, v_ in per_kernel.items() if k_ != "fwd")
         print(json.dumps({
             "workload": f"FA2 B4 H32 N{N} D64 non-causal", "N": N, "steps": steps,
+            "bwd_schedule": args.bwd_schedule,
             "fwd_ms": round(per_kernel["fwd"], 4), "bwd_ms": round(bwd_ms, 4),
             "fwd_tflops": round(fwd_fl / per_kernel["fwd"] / 1e9, 3),
             "bwd_tflops": round(bwd_fl / bwd_ms / 1e9, 3),
@@ -511,22 +543,24 @@ def main():
         return gpt_workload(args)
     B, H, N, D = args.batch, args.heads, args.seq, args.head_dim
     causal = not args.non_causal
-    ms_step, per_kernel, (q, k, v, do) = fa2_timings(B, H, N, D, causal, args.steps, args.warmup)
+    ms_step, per_kernel, (q, k, v, do) = fa2_timings(B, H, N, D, causal, args.steps, args.warmup,
+                                                     args.bwd_schedule)
 
     fwd_fl, bwd_fl = attn_flops(B, H, N, D, causal)
     value = (fwd_fl + bwd_fl) / (ms_step * 1e-3) / 1e12
     fwd_tf = fwd_fl / (per_kernel["fwd"] * 1e-3) / 1e12
-    bwd_ms = per_kernel["delta"] + per_kernel["dq"] + per_kernel["dkdv"]
+    bwd_ms = sum(v_ for k_, v_ in per_kernel.items() if k_ != "fwd")
     bwd_tf = bwd_fl / (bwd_ms * 1e-3) / 1e12
 
-    dom = max(per_kernel, key=per_kernel.get)
+    dom = max((k_ for k_ in per_kernel if k_ != "bwd"), key=per_kernel.get)
     amount, unit, bound = kernel_algorithmic(dom, B, H, N, D, causal)
     if unit == "TFLOP/s":
         achieved, peak = amount / (per_kernel[dom] * 1e-3) / 1e12, MFMA_FP32_PEAK_TFLOPS
     else:
         achieved, peak = amount / (per_kernel[dom] * 1e-3) / 1e9, HBM_PEAK_GBPS
     kernel_symbols = {"fwd": "fa2_fwd_kernel", "delta": "fa2_bwd_delta_kernel",
-                      "dq": "fa2_bwd_dq_kernel", "dkdv": "fa2_bwd_dkdv_kernel"}
+                      "dq": "fa2_bwd_dq_kernel", "dkdv": "fa2_bwd_dkdv_kernel",
+                      "dq_ds": "fa2_bwd_dq_ds_kernel"}
     roofline = {"kernel": kernel_symbols[dom], "bound": bound, "achieved": round(achieved, 3),
                 "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
                 "traffic": load_traffic(kernel_symbols[dom]),
@@ -565,7 +599,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic (N(0,1) Q/K/V/dO from fixed seeds)",
         "config": {"workload": f"FA2 fwd+bwd B{B} H{H} N{N} D{D} {'causal' if causal else 'non-causal'}",
-                   "B": B, "H": H, "N": N, "D": D, "causal": causal},
+                   "B": B, "H": H, "N": N, "D": D, "causal": causal,
+                   "bwd_schedule": args.bwd_schedule},
         "fwd_tflops": round(fwd_tf, 3),
         "bwd_tflops": round(bwd_tf, 3),
         "fwd_frac_of_peak": round(fwd_tf / MFMA_FP32_PEAK_TFLOPS, 4),

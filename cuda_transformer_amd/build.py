@@ -35,7 +35,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
-    "-std=c++17",
+    "-std=c++20",
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
@@ -90,7 +90,7 @@ def build_binding() -> Path:
     py_inc = sysconfig.get_paths()["include"]
     cxx = os.environ.get("CXX", "g++")
     cmd = [
-        cxx, "-O2", "-std=c++17", "-fPIC", "-shared",
+        cxx, "-O2", "-std=c++20", "-fPIC", "-shared",
         f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
         "-DUSE_ROCM", "-D__HIP_PLATFORM_AMD__",
         *[f"-I{p}" for p in incs], f"-I{ROCM / 'include'}", f"-I{py_inc}", f"-I{INCLUDE}",

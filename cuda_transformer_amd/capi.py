@@ -26,9 +26,10 @@ SIGNATURES = {
     "cta_version": (ctypes.c_char_p, []),
     "cta_flash_attention_fwd": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64,
                                        _int, _p, _p, _p]),
+    "cta_flash_attention_bwd_workspace": (_i64, [_i64, _i64, _i64, _i64, _int]),
     "cta_flash_attention_bwd": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
                                        _p, _i64p, _i64, _i64, _i64, _i64, _int, _p, _p, _p, _p,
-                                       _p]),
+                                       _p, _i64, _p]),
     "cta_flash_attention_bwd_delta": (_int, [_p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _p,
                                              _p]),
     "cta_flash_attention_bwd_dq": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
@@ -36,6 +37,11 @@ SIGNATURES = {
     "cta_flash_attention_bwd_dkdv": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p,
                                             _i64p, _p, _i64, _i64, _i64, _i64, _int, _p, _p,
                                             _p]),
+    "cta_flash_attention_bwd_dkdv_store_ds": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p,
+                                                     _i64p, _p, _i64p, _p, _i64, _i64, _i64,
+                                                     _i64, _int, _p, _p, _p, _p]),
+    "cta_flash_attention_bwd_dq_from_ds": (_int, [_p, _i64p, _p, _i64, _i64, _i64, _i64, _int,
+                                                  _p, _p]),
     "cta_cuda_fma_workspace": (_i64, [_i64, _i64, _i64, _i64]),
     "cta_cuda_fma": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p,
                             _p, _p]),
@@ -91,8 +97,6 @@ def strides(values) -> ctypes.Array:
 def call(name: str, *args) -> int:
     """Call an entry point; raise CtaError with the library's message on a non-zero status."""
     rc = getattr(lib(), name)(*args)
-    if isinstance(rc, int) and name not in ("cta_db_calculation_workspace", "cta_cuda_fma_workspace",
-                                             "cta_layernorm_bwd_workspace",
-                                             "cta_causal_self_attention_bwd_workspace") and rc != 0:
+    if isinstance(rc, int) and not name.endswith("_workspace") and rc != 0:
         raise CtaError(f"{name} failed ({rc}): {lib().cta_last_error().decode()}")
     return rc

@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <algorithm>
 #include <cmath>
 #include <string>
 
@@ -44,6 +45,19 @@ __device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.
 // Exchange with the lane 32 positions away (the other half of the wave).
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
 
+// Combine the two wave halves with v_permlane32_swap (gfx950): a VALU lane swap with no LDS
+// round trip.  Swapping a register with itself leaves r[0] = v of lane (l % 32) and
+// r[1] = v of lane (l % 32) + 32 in every lane, so both halves compute the same operands in
+// the same order and get bitwise identical results.
+__device__ __forceinline__ float max_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
@@ -67,6 +81,28 @@ __device__ __forceinline__ int xcd_work_item(int hw_id, int total) {
 }
 inline unsigned xcd_grid(int64_t total) {
   return (unsigned)(kNumXcds * ((total + kNumXcds - 1) / kNumXcds));
+}
+
+// Asynchronous copy global -> LDS without registers (global_load_lds_dwordx4 / _dword on
+// gfx950): lane l's 16 (4) bytes land at lds + 16*l (4*l), so `lds` must be the same for the
+// whole wave and the wave's 64 lanes fill 1 KiB (256 B) of LDS contiguously.  Completion is
+// counted by vmcnt: vm_wait_all() before the barrier that publishes the data.
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __forceinline__ void async_copy16(const float* g, float* lds) {
+  __builtin_amdgcn_global_load_lds(static_cast<const void*>(g), (lds_void_t*)(lds), 16, 0, 0);
+}
+__device__ __forceinline__ void async_copy4(const float* g, float* lds) {
+  __builtin_amdgcn_global_load_lds(static_cast<const void*>(g), (lds_void_t*)(lds), 4, 0, 0);
+}
+// s_waitcnt vmcnt(0): all of this wave's vector memory operations have completed.
+__device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Orders one wave's LDS accesses around a cross-lane exchange through LDS.  The hardware
+// executes a wave's LDS instructions in order; the fence keeps the compiler from moving
+// them across this point.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
 }
 
 // 2^x on the hardware transcendental unit (v_exp_f32). Inputs here are <= 0.

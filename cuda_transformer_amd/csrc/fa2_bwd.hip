@@ -18,6 +18,14 @@
 //    diagonal are skipped here too (the reference computes kvEnd but never uses it).
 //  * Tiles of the streamed operand (K,V for dQ; Q,dO,L,delta for dK/dV) go
 //    global -> registers -> LDS, double buffered, one barrier per tile.
+//
+// Stored-dS schedule (cta_flash_attention_bwd given a workspace): the reference's dQ stage
+// recomputes S and dP, so the three stages run seven tile GEMMs.  With HBM to spare, the
+// dK/dV kernel also writes every 32x32 dS tile it forms to a workspace, transposed through
+// LDS into the order the dQ kernel reads, and a lean dQ kernel computes dQ = s * dS K from
+// it: five GEMMs, still without atomics and bitwise deterministic.  The workspace holds
+// whole heads (the lower-triangular tiles only when causal); heads are processed in chunks
+// when the caller's workspace cannot hold them all.
 #include "cta_common.hpp"
 
 namespace cta {
@@ -237,24 +245,57 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
 }
 
 // ------------------------------------------------------------------------------------
-// Stage 3: dK, dV.  Workgroup = 128 key rows; Q/dO/L/delta tiles streamed through LDS.
-template <int HS, bool CAUSAL>
+// Stored dS tiles.  Tile (ib, jb) covers query rows 32*ib.. and key rows 32*jb.. of one head
+// in 1024 floats, ordered for the wave that consumes it: lane l = 32*h + c reads float4 g
+// at offset 256*g + 4*l, which holds dS[32*ib + c][32*jb + 8*g + 4*h + e] for e = 0..3 —
+// the B operand of the 32x32x2 MFMA for contraction steps kk = 4*g + e.  Causal heads keep
+// the tiles with jb <= ib only, packed row by row.
+__host__ __device__ inline int64_t ds_tile_index(int ib, int jb, int nb, bool causal) {
+  return causal ? (int64_t)ib * (ib + 1) / 2 + jb : (int64_t)ib * nb + jb;
+}
+__host__ __device__ inline int64_t ds_tiles_per_head(int64_t T, bool causal) {
+  const int64_t nb = (T + 31) / 32;
+  return causal ? nb * (nb + 1) / 2 : nb * nb;
+}
+constexpr int kDsTileFloats = 1024;
+constexpr int kDsPitch = 40;  // LDS pitch of the per-wave transpose: halves 4 rows apart hit disjoint banks
+
+// ------------------------------------------------------------------------------------
+// Stage 3: dK, dV.  Workgroup = 128 key rows (4 waves x 32), each lane owning one key row's
+// k and v in registers.  Q, dO, L and delta stream through LDS in stages of BN query rows,
+// copied global -> LDS directly (global_load_lds: no staging registers), double buffered,
+// one barrier per stage.  Query rows past T are read clamped to row T-1 and masked to P = 0.
+//
+// The Q and dO tiles keep the padded pitch HS + 4, under which both access patterns are
+// free of bank conflicts: the row-segment reads of the S / dP products and the column reads
+// of the dV / dK products.  The async copies fill whole 1 KiB pieces of LDS per wave, so the
+// lanes that land on pad words (or past the dO tile) copy a harmless in-bounds chunk there.
+//
+// Heads [bh_base, bh_base + BH) are processed; with STORE_DS every dS tile is also written
+// to dsw (heads indexed from bh_base).  A dS tile goes to a per-wave LDS transpose buffer when
+// it is formed and out to HBM at the start of the next stage, so its stores drain behind a
+// stage of MFMAs rather than in front of the stage's vmcnt wait.
+template <int HS, bool CAUSAL, bool STORE_DS>
 __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
-    float* __restrict__ dK, float* __restrict__ dV, int nh, int T, int BH, int n_ktiles,
-    RowStrides sq, RowStrides sk, RowStrides sv, RowStrides sdo, LStrides sl, float scale,
-    float scale_log2) {
+    float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ dsw, int nh, int T,
+    int bh_base, int BH, int n_ktiles, RowStrides sq, RowStrides sk, RowStrides sv,
+    RowStrides sdo, LStrides sl, float scale, float scale_log2) {
   constexpr int BN = DkdvTile<HS>::BN;
+  constexpr int NSUB = BN / 32;
   constexpr int BM = 128;
   constexpr int H2 = HS / 2;
-  constexpr int KP = HS + 4;
+  constexpr int KP = HS + 4;                // LDS pitch of a Q / dO row
   constexpr int TILE = BN * KP;
-  constexpr int STAGE = 2 * TILE + 2 * BN;  // Q tile, dO tile, L*log2e, delta
-  constexpr int F4_ROW = HS / 4;
-  constexpr int LOADS = BN * F4_ROW / 256;
-  static_assert(BN * F4_ROW % 256 == 0, "tile must split evenly over 256 threads");
-  __shared__ __attribute__((aligned(16))) float smem[2 * STAGE];
+  constexpr int PIECES = (2 * TILE + 255) / 256;  // 1 KiB async copies covering Q and dO
+  constexpr int QG = PIECES * 256;          // Q tile, dO tile, tail of the last piece
+  constexpr int RVEC = 64;                  // L and delta of a stage, padded to one wave
+  constexpr int STAGE = QG + 2 * RVEC;
+  constexpr int PER_WAVE = (PIECES + 3) / 4;
+  static_assert(BN <= RVEC, "one wave copies a stage's L and delta");
+  constexpr int XPOSE = STORE_DS ? 4 * NSUB * 32 * kDsPitch : 0;
+  __shared__ __attribute__((aligned(16))) float smem[2 * STAGE + XPOSE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -263,14 +304,19 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
   const int per_head = CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles;
   const int w = xcd_work_item(blockIdx.x, BH * per_head);
   if (w >= BH * per_head) return;
-  const int bh = w / per_head;
-  const int p = w - bh * per_head;
+  const int bh_local = w / per_head;
+  const int p = w - bh_local * per_head;
+  const int bh = bh_base + bh_local;
   const int b = bh / nh, h = bh - b * nh;
 
   const float* Qb = Q + b * sq.b + h * sq.h;
   const float* dOb = dO + b * sdo.b + h * sdo.h;
   const float* Lb = Lg + b * sl.b + h * sl.h;
   const float* Db = delta + (int64_t)bh * T;
+  const int nb = (T + 31) / 32;
+  float* xpose = smem + 2 * STAGE + wave * NSUB * 32 * kDsPitch;  // this wave's dS buffers
+  float* dsh = STORE_DS ? dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileFloats
+                        : nullptr;
 
   const int n_pass = (CAUSAL && n_ktiles - 1 - p != p) ? 2 : 1;
   for (int pass = 0; pass < n_pass; ++pass) {
@@ -299,66 +345,69 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
   for (int d = 0; d < HS / 32; ++d) { dkacc[d] = zero16(); dvacc[d] = zero16(); }
 
   const int q_begin = CAUSAL ? (kt * BM / BN) : 0;  // first query stage that can see these keys
-  const int n_stages_total = (T + BN - 1) / BN;
+  const int n_stages = (T + BN - 1) / BN;
+  const bool wave_stores = STORE_DS && j0 < T;
 
-  float4 qst[LOADS], gst[LOADS];
-  float lst = 0.0f, dst = 0.0f;
-  auto gload = [&](int stage) {
+  // Async copies of stage `stage` into buffer `buf`.  Piece pc covers floats
+  // [256 pc, 256 pc + 256) of the Q|dO region; wave w copies pieces w, w + 4, ...
+  auto issue = [&](int stage, int buf) {
+    float* qs = smem + buf * STAGE;
     const int r0 = stage * BN;
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int f = tid + 256 * u;
-      const int r = f / F4_ROW, c4 = f % F4_ROW;
-      const int i = r0 + r;
-      if (i < T) {
-        qst[u] = ld4(Qb + (int64_t)i * sq.t + 4 * c4);
-        gst[u] = ld4(dOb + (int64_t)i * sdo.t + 4 * c4);
-      } else {
-        qst[u] = zero4();
-        gst[u] = zero4();
+    for (int u = 0; u < PER_WAVE; ++u) {
+      const int pc = wave + 4 * u;
+      if (pc < PIECES) {
+        const int f = pc * 256 + lane * 4;  // float offset this lane fills
+        const int which = f / TILE;         // 0: Q, 1: dO, 2: tail
+        const int rem = f - which * TILE;
+        const int r = rem / KP, c = rem - r * KP;
+        const int64_t i = min(r0 + r, T - 1);
+        const float* src = which == 0 ? Qb + i * sq.t : dOb + i * sdo.t;
+        // pad words and the tail take the row's first chunk: in bounds and never read
+        async_copy16(which < 2 && c < HS ? src + c : Qb + i * sq.t, qs + pc * 256);
       }
     }
-    if (tid < BN) {
-      const int i = r0 + tid;
-      lst = (i < T) ? Lb[(int64_t)i * sl.t] * kLog2e : 0.0f;
-      dst = (i < T) ? Db[i] : 0.0f;
+    if (wave == 0) {  // lanes past BN fill the padding
+      const int64_t i = min(r0 + lane, T - 1);
+      async_copy4(Lb + i * sl.t, qs + QG);
+      async_copy4(Db + i, qs + QG + RVEC);
     }
   };
-  auto lstore = [&](int buf) {
-    float* qs = smem + buf * STAGE;
-    float* gs = qs + TILE;
+  // Tiles whose every query row precedes every key row are skipped (dS = 0, nothing stored).
+  auto live = [&](int ii0) { return ii0 < T && !(CAUSAL && ii0 + 31 < j0); };
+  // Copy the dS tiles of `stage` from the transpose buffers to the workspace.
+  auto flush = [&](int stage) {
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int f = tid + 256 * u;
-      const int r = f / F4_ROW, c4 = f % F4_ROW;
-      st4(qs + r * KP + 4 * c4, qst[u]);
-      st4(gs + r * KP + 4 * c4, gst[u]);
-    }
-    if (tid < BN) {
-      qs[2 * TILE + tid] = lst;
-      qs[2 * TILE + BN + tid] = dst;
+    for (int sub = 0; sub < NSUB; ++sub) {
+      const int ii0 = stage * BN + sub * 32;
+      if (!live(ii0)) continue;
+      const float* xw = xpose + sub * 32 * kDsPitch;
+      float* gt = dsh + ds_tile_index(ii0 / 32, j0 / 32, nb, CAUSAL) * kDsTileFloats;
+      wave_lds_fence();
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        st4(gt + 256 * g + 4 * lane, ld4(xw + col * kDsPitch + 8 * g + 4 * half));
+      wave_lds_fence();
     }
   };
 
-  if (q_begin < n_stages_total) {
-    gload(q_begin);
-    lstore(0);
-  }
+  if (q_begin < n_stages) issue(q_begin, 0);
+  vm_wait_all();
   __syncthreads();
 
-  for (int s = q_begin; s < n_stages_total; ++s) {
+  for (int s = q_begin; s < n_stages; ++s) {
     const int buf = (s - q_begin) & 1;
-    if (s + 1 < n_stages_total) gload(s + 1);
+    if (s + 1 < n_stages) issue(s + 1, buf ^ 1);
+    if (wave_stores && s > q_begin) flush(s - 1);
     const float* qs = smem + buf * STAGE;
     const float* gs = qs + TILE;
-    const float* ls = qs + 2 * TILE;
-    const float* ds = ls + BN;
+    const float* ls = qs + QG;
+    const float* ds = ls + RVEC;
 
 #pragma unroll
-    for (int sub = 0; sub < BN / 32; ++sub) {
+    for (int sub = 0; sub < NSUB; ++sub) {
       const int ii0 = s * BN + sub * 32;
-      if (ii0 >= T) continue;
-      if (CAUSAL && ii0 + 31 < j0) continue;  // every query row here precedes every key row
+      if (!live(ii0)) continue;
 
       // S and dP tiles: lane holds column my_j, rows ii0 + R(r, half)
       f32x16 sacc = zero16(), pacc = zero16();
@@ -378,7 +427,9 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
         pacc = mfma32(gv.w, vf[4 * c + 3], pacc);
       }
 
-      const bool need_mask = (CAUSAL && ii0 < j0 + 31) || (ii0 + 32 > T);
+      // When storing dS, key rows past T are masked too, so a stored tile is exactly 0 there.
+      const bool need_mask =
+          (CAUSAL && ii0 < j0 + 31) || (ii0 + 32 > T) || (STORE_DS && j0 + 32 > T);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const float4 lv = ld4(ls + sub * 32 + 8 * g + 4 * half);
@@ -388,30 +439,49 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
-          float p = fast_exp2(fmaf(sacc[r], scale_log2, -lr[e]));
+          float pr = fast_exp2(fmaf(sacc[r], scale_log2, -lr[e] * kLog2e));
           if (need_mask) {
             const int i = ii0 + 8 * g + 4 * half + e;
-            if ((CAUSAL && my_j > i) || i >= T) p = 0.0f;
+            if ((CAUSAL && my_j > i) || i >= T || (STORE_DS && my_j >= T)) pr = 0.0f;
           }
-          sacc[r] = p;                       // P
-          pacc[r] = p * (pacc[r] - dr[e]);   // dS
+          sacc[r] = pr;                       // P
+          pacc[r] = pr * (pacc[r] - dr[e]);   // dS
         }
       }
 
+      // Lane (col, half) holds dS[ii0 + R(r, half)][j0 + col]: into the transpose buffer as
+      // [query][key]; flush() reads it back one query row per lane.  A wave's LDS operations
+      // complete in order, so no barrier separates the write, the read and the next write.
+      if (wave_stores) {
+        float* xw = xpose + sub * 32 * kDsPitch;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xw[mfma_row(r, half) * kDsPitch + col] = pacc[r];
+      }
+
+      // dV^T += dO^T P, then dK^T += Q^T dS: one product at a time keeps at most one set of
+      // LDS operands in flight.
 #pragma unroll
       for (int d = 0; d < HS / 32; ++d) {
 #pragma unroll
         for (int kk = 0; kk < 16; ++kk) {
-          const int rrow = (sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col;
-          dvacc[d] = mfma32(gs[rrow], sacc[kk], dvacc[d]);
-          dkacc[d] = mfma32(qs[rrow], pacc[kk], dkacc[d]);
+          const int off = (sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col;
+          dvacc[d] = mfma32(gs[off], sacc[kk], dvacc[d]);
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+          const int off = (sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col;
+          dkacc[d] = mfma32(qs[off], pacc[kk], dkacc[d]);
         }
       }
     }
 
-    if (s + 1 < n_stages_total) lstore(buf ^ 1);
+    vm_wait_all();
     __syncthreads();
   }
+  if (wave_stores && n_stages > q_begin) flush(n_stages - 1);
 
   if (my_j < T) {
     float* kp = dK + ((int64_t)bh * T + my_j) * HS;
@@ -428,7 +498,147 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
       }
     }
   }
-  }  // pass
+  }  // pass: the stage loop ended on a barrier, so the next pass may refill LDS
+}
+
+// ------------------------------------------------------------------------------------
+// dQ from stored dS tiles: dQ^T += K^T dS^T, one 32x32 tile per MFMA chain.  Workgroup =
+// 128 query rows (4 waves x 32).  K tiles of 64 rows go global -> registers -> LDS, double
+// buffered; each wave streams its own dS tiles from the workspace straight into registers,
+// one stage ahead, as the B operand.  Heads [bh_base, bh_base + BH).
+__device__ __forceinline__ float f4_at(const float4& v, int e) {
+  return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+}
+
+template <int HS, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void fa2_bwd_dq_ds_kernel(
+    const float* __restrict__ K, const float* __restrict__ dsw, float* __restrict__ dQ, int nh,
+    int T, int bh_base, int BH, int n_qtiles, RowStrides sk, float scale) {
+  constexpr int BN = 64;
+  constexpr int NSUB = BN / 32;
+  constexpr int BM = 128;
+  constexpr int KP = HS + 8;  // column reads of rows R(kk, 0) and R(kk, 1) = +4: disjoint banks
+  constexpr int TILE = BN * KP;
+  constexpr int F4_ROW = HS / 4;
+  constexpr int LOADS = BN * F4_ROW / 256;
+  static_assert(BN * F4_ROW % 256 == 0, "tile must split evenly over 256 threads");
+  __shared__ __attribute__((aligned(16))) float smem[2 * TILE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, col = lane & 31;
+  // Head-major items over XCDs; causal items are query-tile pairs (n-1-p, p) of equal cost.
+  const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+  const int w = xcd_work_item(blockIdx.x, BH * per_head);
+  if (w >= BH * per_head) return;
+  const int bh_local = w / per_head;
+  const int p = w - bh_local * per_head;
+  const int bh = bh_base + bh_local;
+  const int b = bh / nh, h = bh - b * nh;
+  const float* Kb = K + b * sk.b + h * sk.h;
+  const int nb = (T + 31) / 32;
+  const float* dsh = dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileFloats;
+
+  const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
+  for (int pass = 0; pass < n_pass; ++pass) {
+  const int qt = CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p;
+  const int i0 = qt * BM + wave * 32;
+  const int my_i = i0 + col;
+  const int ib = i0 / 32;  // query block of this wave
+
+  f32x16 acc[HS / 32];
+#pragma unroll
+  for (int d = 0; d < HS / 32; ++d) acc[d] = zero16();
+
+  const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
+  const int n_stages = (kv_end + BN - 1) / BN;
+
+  float4 kst[LOADS];
+  auto gload = [&](int stage) {
+    const int j0 = stage * BN;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int f = tid + 256 * u;
+      const int r = f / F4_ROW, c4 = f % F4_ROW;
+      const int j = j0 + r;
+      kst[u] = j < T ? ld4(Kb + (int64_t)j * sk.t + 4 * c4) : zero4();
+    }
+  };
+  auto lstore = [&](int buf) {
+    float* ks = smem + buf * TILE;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int f = tid + 256 * u;
+      const int r = f / F4_ROW, c4 = f % F4_ROW;
+      st4(ks + r * KP + 4 * c4, kst[u]);
+    }
+  };
+  // A stored tile exists for query block ib and key block jb iff both lie inside the head and,
+  // with a causal mask, jb <= ib (the wave-uniform skip of the dK/dV stage).
+  auto has_tile = [&](int jb) { return ib < nb && jb < nb && (!CAUSAL || jb <= ib); };
+  auto dsload = [&](int stage, float4 (&dr)[NSUB][4]) {
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub) {
+      const int jb = stage * NSUB + sub;
+      if (has_tile(jb)) {
+        const float* src = dsh + ds_tile_index(ib, jb, nb, CAUSAL) * kDsTileFloats + 4 * lane;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) dr[sub][g] = ld4(src + 256 * g);
+      } else {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) dr[sub][g] = zero4();
+      }
+    }
+  };
+  auto compute = [&](int stage, const float* ks, const float4 (&dr)[NSUB][4]) {
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub) {
+      if (!has_tile(stage * NSUB + sub)) continue;
+#pragma unroll
+      for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+          const float a = ks[(sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col];
+          acc[d] = mfma32(a, f4_at(dr[sub][kk >> 2], kk & 3), acc[d]);
+        }
+      }
+    }
+  };
+  auto step = [&](int s, const float4 (&cur)[NSUB][4], float4 (&nxt)[NSUB][4]) {
+    const int buf = s & 1;
+    if (s + 1 < n_stages) {
+      gload(s + 1);
+      dsload(s + 1, nxt);
+    }
+    compute(s, smem + buf * TILE, cur);
+    if (s + 1 < n_stages) lstore(buf ^ 1);
+    __syncthreads();
+  };
+
+  float4 dA[NSUB][4], dB[NSUB][4];
+  dsload(0, dA);
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  // Unrolled by two so the two dS register sets swap roles without copies.
+  for (int s = 0; s < n_stages; s += 2) {
+    step(s, dA, dB);
+    if (s + 1 < n_stages) step(s + 1, dB, dA);
+  }
+
+  if (my_i < T) {
+    float* op = dQ + ((int64_t)bh * T + my_i) * HS;
+#pragma unroll
+    for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dc = d * 32 + 8 * g + 4 * half;
+        st4(op + dc, make_float4(acc[d][4 * g + 0] * scale, acc[d][4 * g + 1] * scale,
+                                 acc[d][4 * g + 2] * scale, acc[d][4 * g + 3] * scale));
+      }
+    }
+  }
+  }  // pass: the stage loop ended on a barrier, so the next pass may refill LDS
 }
 
 RowStrides rs(const int64_t* s) { return RowStrides{s[0], s[1], s[2]}; }
@@ -454,16 +664,34 @@ void launch_dq(const float* q, const float* k, const float* v, const float* d_o,
                      scale, scale * kLog2e);
 }
 
-template <int HS, bool CAUSAL>
+// dK/dV for heads [bh_base, bh_base + n_heads); with STORE_DS the dS tiles go to dsw.
+template <int HS, bool CAUSAL, bool STORE_DS>
 void launch_dkdv(const float* q, const float* k, const float* v, const float* d_o,
-                 const float* l, const float* delta, float* dk, float* dv, int nh, int T, int BH,
-                 RowStrides sq, RowStrides sk, RowStrides sv, RowStrides sdo, LStrides sl,
-                 float scale, hipStream_t st) {
+                 const float* l, const float* delta, float* dk, float* dv, float* dsw, int nh,
+                 int T, int bh_base, int n_heads, RowStrides sq, RowStrides sk, RowStrides sv,
+                 RowStrides sdo, LStrides sl, float scale, hipStream_t st) {
   const int n_ktiles = (T + 127) / 128;
-  const int64_t items = (int64_t)(CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles) * BH;
-  hipLaunchKernelGGL((fa2_bwd_dkdv_kernel<HS, CAUSAL>), dim3(xcd_grid(items)), dim3(256),
-                     0, st, q, k, v, d_o, l, delta, dk, dv, nh, T, BH, n_ktiles, sq, sk, sv, sdo,
-                     sl, scale, scale * kLog2e);
+  const int64_t items = (int64_t)(CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles) * n_heads;
+  hipLaunchKernelGGL((fa2_bwd_dkdv_kernel<HS, CAUSAL, STORE_DS>), dim3(xcd_grid(items)),
+                     dim3(256), 0, st, q, k, v, d_o, l, delta, dk, dv, dsw, nh, T, bh_base,
+                     n_heads, n_ktiles, sq, sk, sv, sdo, sl, scale, scale * kLog2e);
+}
+
+template <int HS, bool CAUSAL>
+void launch_dq_ds(const float* k, const float* dsw, float* dq, int nh, int T, int bh_base,
+                  int n_heads, RowStrides sk, float scale, hipStream_t st) {
+  const int n_qtiles = (T + 127) / 128;
+  const int64_t items = (int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * n_heads;
+  hipLaunchKernelGGL((fa2_bwd_dq_ds_kernel<HS, CAUSAL>), dim3(xcd_grid(items)), dim3(256), 0,
+                     st, k, dsw, dq, nh, T, bh_base, n_heads, n_qtiles, sk, scale);
+}
+
+// Runs f.template operator()<HS, CAUSAL>() for the runtime head size and mask flag.
+template <typename F>
+void dispatch_hs_causal(int64_t hs, int causal, F&& f) {
+  if (hs == 32) { if (causal) f.template operator()<32, true>(); else f.template operator()<32, false>(); }
+  else if (hs == 64) { if (causal) f.template operator()<64, true>(); else f.template operator()<64, false>(); }
+  else { if (causal) f.template operator()<128, true>(); else f.template operator()<128, false>(); }
 }
 
 bool l_ok(const float* l, const int64_t* s) { return l != nullptr && s != nullptr; }
@@ -554,18 +782,63 @@ extern "C" int cta_flash_attention_bwd_dkdv(const float* q, const int64_t* q_str
   const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
   const int BH = (int)(B * nh);
   hipStream_t st = as_stream(stream);
-#define CTA_DKDV(HS_)                                                                          \
-  if (causal) launch_dkdv<HS_, true>(q, k, v, d_o, l, delta, dk, dv, (int)nh, (int)T, BH,       \
-                                     rs(q_strides), rs(k_strides), rs(v_strides),               \
-                                     rs(do_strides), sl, scale, st);                            \
-  else launch_dkdv<HS_, false>(q, k, v, d_o, l, delta, dk, dv, (int)nh, (int)T, BH,             \
-                               rs(q_strides), rs(k_strides), rs(v_strides), rs(do_strides), sl, \
-                               scale, st);
-  if (hs == 32) { CTA_DKDV(32) }
-  else if (hs == 64) { CTA_DKDV(64) }
-  else { CTA_DKDV(128) }
-#undef CTA_DKDV
+  dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
+    launch_dkdv<HS, C, false>(q, k, v, d_o, l, delta, dk, dv, nullptr, (int)nh, (int)T, 0, BH,
+                              rs(q_strides), rs(k_strides), rs(v_strides), rs(do_strides), sl,
+                              scale, st);
+  });
   return check_launch("flash_attention_bwd_dkdv");
+}
+
+extern "C" int64_t cta_flash_attention_bwd_workspace(int64_t B, int64_t nh, int64_t T,
+                                                     int64_t hs, int causal) {
+  if (B <= 0 || nh <= 0 || T <= 0 || (hs != 32 && hs != 64 && hs != 128)) return 0;
+  return B * nh * ds_tiles_per_head(T, causal != 0) * kDsTileFloats * (int64_t)sizeof(float);
+}
+
+extern "C" int cta_flash_attention_bwd_dkdv_store_ds(
+    const float* q, const int64_t* q_strides, const float* k, const int64_t* k_strides,
+    const float* v, const int64_t* v_strides, const float* d_o, const int64_t* do_strides,
+    const float* l, const int64_t* l_strides, const float* delta, int64_t B, int64_t nh,
+    int64_t T, int64_t hs, int causal, float* dk, float* dv, float* ds_workspace,
+    void* stream) {
+  if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
+  if (B * nh * T == 0) return CTA_OK;
+  if (int rc = check_bwd_inputs(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l,
+                                l_strides, delta))
+    return rc;
+  if (!dk || !dv || !aligned16(dk) || !aligned16(dv) || !ds_workspace || !aligned16(ds_workspace))
+    return fail(CTA_ERR_LAYOUT, "dK/dV and the dS workspace must be 16-byte aligned pointers");
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
+  hipStream_t st = as_stream(stream);
+  dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
+    launch_dkdv<HS, C, true>(q, k, v, d_o, l, delta, dk, dv, ds_workspace, (int)nh, (int)T, 0,
+                             (int)(B * nh), rs(q_strides), rs(k_strides), rs(v_strides),
+                             rs(do_strides), sl, scale, st);
+  });
+  return check_launch("flash_attention_bwd_dkdv_store_ds");
+}
+
+extern "C" int cta_flash_attention_bwd_dq_from_ds(const float* k, const int64_t* k_strides,
+                                                  const float* ds_workspace, int64_t B,
+                                                  int64_t nh, int64_t T, int64_t hs, int causal,
+                                                  float* dq, void* stream) {
+  if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
+  if (B * nh * T == 0) return CTA_OK;
+  if (!attn_layout_ok(k, k_strides))
+    return fail(CTA_ERR_LAYOUT,
+                "flash_attention_bwd needs unit d-stride, strides divisible by 4 and 16-byte "
+                "aligned K");
+  if (!dq || !aligned16(dq) || !ds_workspace || !aligned16(ds_workspace))
+    return fail(CTA_ERR_LAYOUT, "dQ and the dS workspace must be 16-byte aligned pointers");
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  hipStream_t st = as_stream(stream);
+  dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
+    launch_dq_ds<HS, C>(k, ds_workspace, dq, (int)nh, (int)T, 0, (int)(B * nh), rs(k_strides),
+                        scale, st);
+  });
+  return check_launch("flash_attention_bwd_dq_from_ds");
 }
 
 extern "C" int cta_flash_attention_bwd(const float* q, const int64_t* q_strides, const float* k,
@@ -575,14 +848,46 @@ extern "C" int cta_flash_attention_bwd(const float* q, const int64_t* q_strides,
                                        const int64_t* do_strides, const float* l,
                                        const int64_t* l_strides, int64_t B, int64_t nh,
                                        int64_t T, int64_t hs, int causal, float* dq, float* dk,
-                                       float* dv, float* delta, void* stream) {
+                                       float* dv, float* delta, float* workspace,
+                                       int64_t workspace_bytes, void* stream) {
   if (int rc = cta_flash_attention_bwd_delta(o, o_strides, d_o, do_strides, B, nh, T, hs, delta,
                                              stream))
     return rc;
-  if (int rc = cta_flash_attention_bwd_dq(q, q_strides, k, k_strides, v, v_strides, d_o,
-                                          do_strides, l, l_strides, delta, B, nh, T, hs, causal,
-                                          dq, stream))
+  const int64_t head_bytes = cta_flash_attention_bwd_workspace(1, 1, T, hs, causal);
+  if (workspace == nullptr || head_bytes == 0 || workspace_bytes < head_bytes) {
+    // The reference's schedule: dQ recomputes S and dP.
+    if (int rc = cta_flash_attention_bwd_dq(q, q_strides, k, k_strides, v, v_strides, d_o,
+                                            do_strides, l, l_strides, delta, B, nh, T, hs,
+                                            causal, dq, stream))
+      return rc;
+    return cta_flash_attention_bwd_dkdv(q, q_strides, k, k_strides, v, v_strides, d_o,
+                                        do_strides, l, l_strides, delta, B, nh, T, hs, causal, dk,
+                                        dv, stream);
+  }
+  if (B * nh * T == 0) return CTA_OK;
+  if (int rc = check_bwd_inputs(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l,
+                                l_strides, delta))
     return rc;
-  return cta_flash_attention_bwd_dkdv(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides,
-                                      l, l_strides, delta, B, nh, T, hs, causal, dk, dv, stream);
+  if (!dq || !dk || !dv || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
+      !aligned16(workspace))
+    return fail(CTA_ERR_LAYOUT, "dQ/dK/dV and the workspace must be 16-byte aligned pointers");
+  // Stored-dS schedule over chunks of equal head counts that fit the workspace.
+  const int BH = (int)(B * nh);
+  const int64_t fit = std::min<int64_t>(BH, workspace_bytes / head_bytes);
+  const int64_t n_chunks = (BH + fit - 1) / fit;
+  const int chunk = (int)((BH + n_chunks - 1) / n_chunks);
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
+  hipStream_t st = as_stream(stream);
+  for (int h0 = 0; h0 < BH; h0 += chunk) {
+    const int n = std::min(chunk, BH - h0);
+    dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
+      launch_dkdv<HS, C, true>(q, k, v, d_o, l, delta, dk, dv, workspace, (int)nh, (int)T, h0, n,
+                               rs(q_strides), rs(k_strides), rs(v_strides), rs(do_strides), sl,
+                               scale, st);
+      launch_dq_ds<HS, C>(k, workspace, dq, (int)nh, (int)T, h0, n, rs(k_strides), scale, st);
+    });
+    if (int rc = check_launch("flash_attention_bwd")) return rc;
+  }
+  return CTA_OK;
 }

@@ -14,6 +14,12 @@
 //    second MFMA is permuted to match the output layout of the first, and V is read from LDS
 //    in the same permuted order.  P never leaves registers.
 //  * Exponentials use exp2 with log2(e) folded into the scale; L is exported in natural log.
+//  * Lazy rescaling: the running max m used as the exponent offset only moves when some row
+//    of the wave sees a tile max more than 2^8 above it (a wave-uniform vote).  Otherwise the
+//    tile is exponentiated against the stale m, so every p <= 2^8 and the O accumulator and
+//    row sum stay exact multiples of the same e^{-m}; O = acc / l and L = m + ln l are
+//    unchanged.  This removes the per-tile rescale of the O registers from the common path.
+//  * The max / sum across the two wave halves use v_permlane32_swap (no LDS round trip).
 //  * Workgroup ids are remapped so each XCD walks a contiguous run of a head-major work list:
 //    the workgroups resident on one XCD share a few heads' K/V in its L2.  With a causal mask a
 //    workgroup takes the query-tile pair (n-1-p, p), so all workgroups cost the same and the
@@ -29,15 +35,16 @@ struct RowStrides {
 
 template <int HS>
 struct FwdTile;
-template <> struct FwdTile<32> { static constexpr int BN = 64; static constexpr int MINW = 2; };
-template <> struct FwdTile<64> { static constexpr int BN = 64; static constexpr int MINW = 2; };
+template <> struct FwdTile<32> { static constexpr int BN = 32; static constexpr int MINW = 2; };
+template <> struct FwdTile<64> { static constexpr int BN = 32; static constexpr int MINW = 2; };
 template <> struct FwdTile<128> { static constexpr int BN = 32; static constexpr int MINW = 1; };
 
 template <int HS, bool CAUSAL>
 __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ L, int nh, int T, int BH, int n_qtiles,
-    RowStrides sq, RowStrides sk, RowStrides sv, float scale, float scale_log2) {
+    RowStrides sq, RowStrides sk, RowStrides sv, float scale, float scale_log2,
+    float rescale_gap) {
   constexpr int BN = FwdTile<HS>::BN;
   constexpr int BM = 128;
   constexpr int H2 = HS / 2;    // d values per lane half
@@ -88,7 +95,7 @@ __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   f32x16 oacc[HS / 32];
 #pragma unroll
   for (int d = 0; d < HS / 32; ++d) oacc[d] = zero16();
-  float m_run = -INFINITY;  // running max of raw q.k for row my_i
+  float m_run = -INFINITY;  // exponent offset of row my_i (raw q.k units), lazily updated
   float l_run = 0.0f;       // this lane's partial row sum (its half of the columns)
 
   const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
@@ -163,10 +170,18 @@ __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
       float mt = sacc[0];
 #pragma unroll
       for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sacc[r]);
-      mt = fmaxf(mt, xor32(mt));
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = fast_exp2((m_run - m_new) * scale_log2);
-      const float mb = m_new * scale_log2;
+      mt = max_halves(mt);
+      // rescale_gap = 8 / scale_log2: a tile max within 2^8 of m keeps the old offset.
+      // The first tile always rescales (m_run = -inf), with alpha = 0 on zero accumulators.
+      if (__any(mt > m_run + rescale_gap)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = fast_exp2((m_run - m_new) * scale_log2);
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < HS / 32; ++d) oacc[d] *= alpha;
+        m_run = m_new;
+      }
+      const float mb = m_run * scale_log2;
       float psum = 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -174,12 +189,10 @@ __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
         sacc[r] = p;
         psum += p;
       }
-      l_run = fmaf(l_run, alpha, psum);
-      m_run = m_new;
+      l_run += psum;
 
 #pragma unroll
       for (int d = 0; d < HS / 32; ++d) {
-        oacc[d] *= alpha;
 #pragma unroll
         for (int kk = 0; kk < 16; ++kk) {
           const float a = vs[(sub * 32 + mfma_row(kk, half)) * VP + d * 32 + col];
@@ -192,7 +205,7 @@ __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
     __syncthreads();
   }
 
-  const float l_tot = l_run + xor32(l_run);
+  const float l_tot = sum_halves(l_run);
   if (my_i < T) {
     float* op = O + ((int64_t)bh * T + my_i) * HS;
 #pragma unroll
@@ -216,7 +229,8 @@ void launch_fwd(const float* q, const float* k, const float* v, float* o, float*
   const int n_qtiles = (T + 127) / 128;
   const unsigned grid = xcd_grid((int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH);
   hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL>), dim3(grid), dim3(256), 0, stream, q, k, v, o,
-                     l, nh, T, BH, n_qtiles, sq, sk, sv, scale, scale * kLog2e);
+                     l, nh, T, BH, n_qtiles, sq, sk, sv, scale, scale * kLog2e,
+                     8.0f / (scale * kLog2e));
 }
 
 }  // namespace

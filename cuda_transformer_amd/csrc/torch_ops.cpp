@@ -15,6 +15,7 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <algorithm>
 #include <array>
 #include <cstdint>
 #include <tuple>
@@ -23,6 +24,10 @@
 
 namespace cuda_transformer {
 namespace {
+
+// Largest dS workspace the flash_attention_bwd op allocates (8 GiB of the MI355X's 288 GB);
+// longer sequences run the stored-dS schedule in chunks of heads.
+constexpr int64_t kBwdWorkspaceCap = int64_t{8} << 30;
 
 void* stream_of(const at::Tensor& t) {
   return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.get_device()).stream());
@@ -339,12 +344,27 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd(at::Tensor Q,
   const auto qs = strides_of<4>(q), ks = strides_of<4>(k), vs = strides_of<4>(v),
              os = strides_of<4>(o), gs = strides_of<4>(g);
   const auto ls = strides_of<3>(L);
+  // Workspace for the stored-dS schedule: every head's dS tiles up to kBwdWorkspaceCap
+  // (chunked over heads beyond that).  If the allocator cannot supply it, the kernels run
+  // the recompute schedule, which needs no workspace.
+  int64_t ws_bytes = std::min(cta_flash_attention_bwd_workspace(B, nh, T, hs, causal ? 1 : 0),
+                              kBwdWorkspaceCap);
+  at::Tensor ws;
+  if (ws_bytes > 0) {
+    try {
+      ws = at::empty({ws_bytes / static_cast<int64_t>(sizeof(float))}, Q.options());
+    } catch (const c10::OutOfMemoryError&) {
+      ws_bytes = 0;
+    }
+  }
   check_rc(cta_flash_attention_bwd(q.data_ptr<float>(), qs.data(), k.data_ptr<float>(), ks.data(),
                                    v.data_ptr<float>(), vs.data(), o.data_ptr<float>(), os.data(),
                                    g.data_ptr<float>(), gs.data(), L.data_ptr<float>(), ls.data(),
                                    B, nh, T, hs, causal ? 1 : 0, dQ.data_ptr<float>(),
                                    dK.data_ptr<float>(), dV.data_ptr<float>(),
-                                   delta.data_ptr<float>(), stream_of(Q)));
+                                   delta.data_ptr<float>(),
+                                   ws_bytes > 0 ? ws.data_ptr<float>() : nullptr, ws_bytes,
+                                   stream_of(Q)));
   return {dQ, dK, dV};
 }
 

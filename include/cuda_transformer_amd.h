@@ -59,9 +59,20 @@ int cta_flash_attention_fwd(const float* q, const int64_t* q_strides,
                             int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
                             float* o, float* l, void* stream);
 
-/* Backward, all three stages in stream order: delta, then dQ and dK/dV.
- * `delta` is caller-provided scratch of B*nh*T floats (the reference allocates it
- * inside the launcher).  dq/dk/dv are dense (B,nh,T,hs).
+/* Bytes of dS workspace that let cta_flash_attention_bwd keep every head's dS tiles
+ * (the lower-triangular 32x32 tiles only when causal): B*nh*ceil(T/32)^2*4 KiB, or about
+ * half of that when causal.  0 for empty or unsupported shapes. */
+int64_t cta_flash_attention_bwd_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs,
+                                          int causal);
+
+/* Backward: delta, then dQ and dK/dV.  dq/dk/dv are dense (B,nh,T,hs); `delta` is
+ * caller-provided scratch of B*nh*T floats (the reference allocates it inside the launcher).
+ * `workspace` may be NULL: the three stages then run as the reference schedules them, the
+ * dQ stage recomputing S and dP.  Given at least one head's share of
+ * cta_flash_attention_bwd_workspace() bytes, the dK/dV stage stores dS and dQ is computed
+ * from it (cta_flash_attention_bwd_dkdv_store_ds + cta_flash_attention_bwd_dq_from_ds),
+ * chunked over heads to fit workspace_bytes: fewer FLOPs, same results to rounding.
+ * Both schedules are deterministic.
  * Replaces cuda_transformer::flash_attention_bwd (flash_attn_launcher.cu:67-142). */
 int cta_flash_attention_bwd(const float* q, const int64_t* q_strides,
                             const float* k, const int64_t* k_strides,
@@ -70,7 +81,8 @@ int cta_flash_attention_bwd(const float* q, const int64_t* q_strides,
                             const float* d_o, const int64_t* do_strides,
                             const float* l, const int64_t* l_strides,
                             int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
-                            float* dq, float* dk, float* dv, float* delta, void* stream);
+                            float* dq, float* dk, float* dv, float* delta,
+                            float* workspace, int64_t workspace_bytes, void* stream);
 
 /* Stage 1 of the backward: delta[b,h,t] = sum_d O*dO, dense (B,nh,T).
  * Replaces the flash_attention_bwd_delta launch (flash_attn_launcher.cu:107-108). */
@@ -99,6 +111,28 @@ int cta_flash_attention_bwd_dkdv(const float* q, const int64_t* q_strides,
                                  const float* delta,
                                  int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
                                  float* dk, float* dv, void* stream);
+
+/* Stage 3 of the stored-dS schedule: dK and dV as cta_flash_attention_bwd_dkdv, and every
+ * dS tile written to ds_workspace (cta_flash_attention_bwd_workspace(B, nh, T, hs, causal)
+ * bytes, 16-byte aligned).  Same launch slot as the reference's flash_attention_bwd_dk_dv
+ * (flash_attn_launcher.cu:114,121,131), run before the dQ stage. */
+int cta_flash_attention_bwd_dkdv_store_ds(const float* q, const int64_t* q_strides,
+                                          const float* k, const int64_t* k_strides,
+                                          const float* v, const int64_t* v_strides,
+                                          const float* d_o, const int64_t* do_strides,
+                                          const float* l, const int64_t* l_strides,
+                                          const float* delta,
+                                          int64_t B, int64_t nh, int64_t T, int64_t hs,
+                                          int causal, float* dk, float* dv,
+                                          float* ds_workspace, void* stream);
+
+/* dQ = s * dS K from the tiles cta_flash_attention_bwd_dkdv_store_ds wrote.  Replaces the
+ * flash_attention_bwd_dq launch (flash_attn_launcher.cu:111,118,125) in the stored-dS
+ * schedule. */
+int cta_flash_attention_bwd_dq_from_ds(const float* k, const int64_t* k_strides,
+                                       const float* ds_workspace,
+                                       int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                                       float* dq, void* stream);
 
 /* ------------------------------------------------------------------------------
  * Linear layer.

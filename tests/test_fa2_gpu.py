@@ -60,6 +60,33 @@ def test_fa2_matches_oracle(cuda, B, nh, T, hs, causal):
         assert_rel_err(f64(got), ref, 1e-3)
 
 
+RECOMPUTE_SHAPES = [REF_SHAPES[i] for i in (0, 2, 3, 5, 6, 9, 11)]
+
+
+@pytest.mark.parametrize("B,nh,T,hs,causal", RECOMPUTE_SHAPES)
+def test_fa2_recompute_schedule_matches_oracle(cuda, B, nh, T, hs, causal):
+    """The reference's schedule (dQ recomputes S and dP), selected by passing no workspace
+    through the C ABI; the torch op runs the stored-dS schedule checked above."""
+    from cuda_transformer_amd import capi
+
+    q, k, v, do = (t.to(cuda) for t in _inputs(B, nh, T, hs, seed=2000 + T + hs))
+    O_ref, L_ref = ora.reference_attention(f64(q), f64(k), f64(v), causal)
+    O = torch.from_numpy(O_ref.astype(np.float32)).to(cuda)
+    L = torch.from_numpy(L_ref.astype(np.float32)).to(cuda)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    delta = torch.empty(B, nh, T, device=cuda)
+    s4, s3 = capi.strides(q.stride()), capi.strides(L.stride())
+    capi.call("cta_flash_attention_bwd", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(), s4,
+              O.data_ptr(), s4, do.data_ptr(), s4, L.data_ptr(), s3, B, nh, T, hs, int(causal),
+              dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), None, 0,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    g_ref = ora.fa2_backward(f64(q), f64(k), f64(v), O_ref, f64(do), L_ref, causal, br=64, bc=64)
+    for got, ref in zip((dq, dk, dv), g_ref):
+        np.testing.assert_allclose(f64(got), ref, rtol=1e-5, atol=1e-4)
+        assert_rel_err(f64(got), ref, 1e-3)
+
+
 def test_fa2_strided_views_match_dense(cuda):
     """q, k, v as head views of a packed (B, T, 3C) projection (gpt/gpt.py:104-107), dO as a
     transposed view: read in place through strides, bitwise equal to dense copies."""
@@ -145,15 +172,42 @@ def test_fa2_through_c_abi(cuda):
     O2, L2 = flash_attention_fwd(q, k, v, True)
     torch.cuda.synchronize()
     assert torch.equal(O, O2) and torch.equal(L, L2)
+    s3 = capi.strides(L.stride())
+    ws_bytes = capi.call("cta_flash_attention_bwd_workspace", B, nh, T, hs, 1)
+    nb = (T + 31) // 32
+    assert ws_bytes == B * nh * nb * (nb + 1) // 2 * 4096
+    assert capi.call("cta_flash_attention_bwd_workspace", B, nh, T, hs, 0) == B * nh * nb * nb * 4096
+    ws = torch.empty(ws_bytes // 4, device=cuda)
+
+    def bwd(workspace, nbytes):
+        out = [torch.empty_like(q) for _ in range(3)] + [torch.empty(B, nh, T, device=cuda)]
+        capi.call("cta_flash_attention_bwd", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(),
+                  s4, O.data_ptr(), s4, do.data_ptr(), s4, L.data_ptr(), s3, B, nh, T, hs, 1,
+                  *(t.data_ptr() for t in out), workspace, nbytes, st)
+        return out
+
+    stored = bwd(ws.data_ptr(), ws_bytes)            # every head's dS fits
+    chunked = bwd(ws.data_ptr(), ws_bytes // 2)      # one head per chunk
+    recompute = bwd(None, 0)                         # the reference's schedule
+    g = flash_attention_bwd(q, k, v, O, do, L, True)
+    # The stages of the stored-dS schedule called one by one.
     dq, dk, dv, delta = (torch.empty_like(q), torch.empty_like(q), torch.empty_like(q),
                          torch.empty(B, nh, T, device=cuda))
-    s3 = capi.strides(L.stride())
-    capi.call("cta_flash_attention_bwd", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(), s4,
-              O.data_ptr(), s4, do.data_ptr(), s4, L.data_ptr(), s3, B, nh, T, hs, 1,
-              dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), st)
-    g = flash_attention_bwd(q, k, v, O, do, L, True)
+    capi.call("cta_flash_attention_bwd_delta", O.data_ptr(), s4, do.data_ptr(), s4, B, nh, T, hs,
+              delta.data_ptr(), st)
+    capi.call("cta_flash_attention_bwd_dkdv_store_ds", q.data_ptr(), s4, k.data_ptr(), s4,
+              v.data_ptr(), s4, do.data_ptr(), s4, L.data_ptr(), s3, delta.data_ptr(), B, nh, T,
+              hs, 1, dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), st)
+    capi.call("cta_flash_attention_bwd_dq_from_ds", k.data_ptr(), s4, ws.data_ptr(), B, nh, T,
+              hs, 1, dq.data_ptr(), st)
     torch.cuda.synchronize()
-    assert torch.equal(dq, g[0]) and torch.equal(dk, g[1]) and torch.equal(dv, g[2])
+    for i in range(3):
+        assert torch.equal(stored[i], g[i])
+        assert torch.equal(chunked[i], g[i])
+        assert torch.equal((dq, dk, dv)[i], g[i])
+    # dK/dV come from the same kernel in both schedules; dQ differs only in summation order.
+    assert torch.equal(recompute[1], g[1]) and torch.equal(recompute[2], g[2])
+    torch.testing.assert_close(recompute[0], g[0], rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(f64(delta), (f64(O) * f64(do)).sum(-1), rtol=1e-5, atol=1e-5)
     with pytest.raises(capi.CtaError, match="Unsupported head dimension"):
         capi.call("cta_flash_attention_fwd", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(),
