@@ -430,12 +430,11 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
       // When storing dS, key rows past T are masked too, so a stored tile is exactly 0 there.
       const bool need_mask =
           (CAUSAL && ii0 < j0 + 31) || (ii0 + 32 > T) || (STORE_DS && j0 + 32 > T);
+      // P = e^{S - L}; masked entries are exactly 0.
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const float4 lv = ld4(ls + sub * 32 + 8 * g + 4 * half);
-        const float4 dv = ld4(ds + sub * 32 + 8 * g + 4 * half);
         const float lr[4] = {lv.x, lv.y, lv.z, lv.w};
-        const float dr[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
@@ -444,9 +443,27 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
             const int i = ii0 + 8 * g + 4 * half + e;
             if ((CAUSAL && my_j > i) || i >= T || (STORE_DS && my_j >= T)) pr = 0.0f;
           }
-          sacc[r] = pr;                       // P
-          pacc[r] = pr * (pacc[r] - dr[e]);   // dS
+          sacc[r] = pr;
         }
+      }
+
+      // dV^T += dO^T P is issued before dS is formed, so the dS arithmetic and its transpose
+      // writes overlap these MFMAs; then dK^T += Q^T dS.  One product at a time keeps at most
+      // one set of LDS operands in flight.
+#pragma unroll
+      for (int kk = 0; kk < 16; ++kk) {
+#pragma unroll
+        for (int d = 0; d < HS / 32; ++d) {
+          const int off = (sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col;
+          dvacc[d] = mfma32(gs[off], sacc[kk], dvacc[d]);
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 dv = ld4(ds + sub * 32 + 8 * g + 4 * half);
+        const float dr[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pacc[4 * g + e] = sacc[4 * g + e] * (pacc[4 * g + e] - dr[e]);
       }
 
       // Lane (col, half) holds dS[ii0 + R(r, half)][j0 + col]: into the transpose buffer as
@@ -458,20 +475,10 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
         for (int r = 0; r < 16; ++r) xw[mfma_row(r, half) * kDsPitch + col] = pacc[r];
       }
 
-      // dV^T += dO^T P, then dK^T += Q^T dS: one product at a time keeps at most one set of
-      // LDS operands in flight.
 #pragma unroll
-      for (int d = 0; d < HS / 32; ++d) {
+      for (int kk = 0; kk < 16; ++kk) {
 #pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
-          const int off = (sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col;
-          dvacc[d] = mfma32(gs[off], sacc[kk], dvacc[d]);
-        }
-      }
-#pragma unroll
-      for (int d = 0; d < HS / 32; ++d) {
-#pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
+        for (int d = 0; d < HS / 32; ++d) {
           const int off = (sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col;
           dkacc[d] = mfma32(qs[off], pacc[kk], dkacc[d]);
         }
@@ -594,10 +601,11 @@ __global__ __launch_bounds__(256, 2) void fa2_bwd_dq_ds_kernel(
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub) {
       if (!has_tile(stage * NSUB + sub)) continue;
+      // kk-major: the HS/32 accumulator chains alternate, so no MFMA waits on its predecessor
 #pragma unroll
-      for (int d = 0; d < HS / 32; ++d) {
+      for (int kk = 0; kk < 16; ++kk) {
 #pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
+        for (int d = 0; d < HS / 32; ++d) {
           const float a = ks[(sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col];
           acc[d] = mfma32(a, f4_at(dr[sub][kk >> 2], kk & 3), acc[d]);
         }
