@@ -15,8 +15,8 @@ Reported:
   per_kernel_ms  HIP-event durations of each kernel on its launch stream, averaged over the
                  timed steps.
   roofline       the dominant kernel's algorithmic FLOPs per launch / its mean duration, vs the
-                 157.3 TFLOP/s dense FP32 MFMA peak; traffic from the committed rocprofv3 PMC
-                 summary (profiles/) when present.
+                 157.3 TFLOP/s dense FP32 MFMA peak; traffic (HBM bytes per launch) from the
+                 committed rocprofv3 counter summary profiles/fa2_config2_counters.md.
   cpu_baseline   the CPU oracle (numpy port of the reference algorithm, float32) timed on this
                  host's cores on a bounded sample of whole heads of the same workload.
 
@@ -107,7 +107,7 @@ def kernel_algorithmic(name, B, H, N, D, causal):
 
 def load_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed PMC summary, or None."""
-    path = ROOT / "profiles" / "fa2_config2_traffic.md"
+    path = ROOT / "profiles" / "fa2_config2_counters.md"
     if not path.exists():
         return None
     m = re.search(rf"traffic_bytes_per_launch\[{re.escape(kernel)}\]\s*=\s*([0-9.eE+]+)",
@@ -270,21 +270,30 @@ def fa2_sweep(args):
     return 0
 
 
-def _time_kernel(fn, reps):
-    """Mean HIP-event duration (ms) of fn's launches on torch's current stream."""
+def _time_kernel(fn, reps, warm_s=0.02):
+    """Median HIP-event duration (ms) of fn's launches on torch's current stream, over at least
+    20 launches, after at least warm_s of back-to-back launches: the CPU-baseline timings between
+    ops leave the GPU idle long enough for its clocks to drop."""
+    import statistics
+
     import torch
 
-    fn()
-    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= warm_s:
+            break
     stream = torch.cuda.current_stream()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(reps)]
+           for _ in range(max(20, reps))]
     for a, b in evs:
         a.record(stream)
         fn()
         b.record(stream)
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in evs) / reps
+    return statistics.median(a.elapsed_time(b) for a, b in evs)
 
 
 def _cpu_time(fn, target_s=2.0):

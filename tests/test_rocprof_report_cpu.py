@@ -1,0 +1,122 @@
+"""The rocprofv3 counter report (cuda_transformer_amd/rocprof_report.py) on synthetic CSVs whose
+derived figures are known in closed form: MFMA utilisation, clock, executed FLOPs, HBM bytes
+through the copy calibration, arithmetic intensity and LDS conflict rate."""
+import csv
+
+import pytest
+
+from cuda_transformer_amd import rocprof_report as rr
+
+PMC_HEADER = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id", "Thread_Id",
+              "Grid_Size", "Kernel_Id", "Kernel_Name", "Workgroup_Size", "LDS_Block_Size",
+              "Scratch_Size", "VGPR_Count", "Accum_VGPR_Count", "SGPR_Count", "Counter_Name",
+              "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+AGENT = {"Agent_Type": "GPU", "Name": "gfx950", "Cu_Count": "256", "Simd_Count": "1024",
+         "Num_Xcc": "8", "Max_Engine_Clk_Fcompute": "2400"}
+
+
+def _pmc(d, name, rows):
+    """rows: [(kernel, counter, value), ...] -> d/<name>_counter_collection.csv + agent info."""
+    d.mkdir(parents=True, exist_ok=True)
+    with open(d / f"{name}_counter_collection.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(PMC_HEADER)
+        for i, (k, c, v) in enumerate(rows):
+            # every dispatch lasts 2 ms (its timestamps), the span the clock is measured over
+            w.writerow([i, i, "Agent 1", 1, 1, 1, 1024, 7, k, 256, 4096, 0, 128, 0, 32, c, v,
+                        10_000_000 * i, 10_000_000 * i + 2_000_000])
+    with open(d / f"{name}_agent_info.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(AGENT))
+        w.writeheader()
+        w.writerow({**AGENT, "Agent_Type": "CPU", "Name": "host"})
+        w.writerow(AGENT)
+    return d
+
+
+def _trace(d, kernels):
+    d.mkdir(parents=True, exist_ok=True)
+    with open(d / "t_kernel_stats.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs",
+                    "StdDev"])
+        for k, calls, avg in kernels:
+            w.writerow([k, calls, calls * avg, avg, 50.0, avg, avg, 0])
+    return d
+
+
+def test_derived_figures(tmp_path):
+    ms = 2.0
+    xcds, simds, clock = 8, 1024, 2.25e9
+    cycles = clock * ms * 1e-3                       # per XCD
+    mops = 4.0e8                                     # -> 2.048e11 FLOP
+    busy = 0.75 * cycles * simds
+    trace = _trace(tmp_path / "trace", [("k_mfma", 3, ms * 1e6), ("k_copyish", 3, 1e6)])
+    mf = _pmc(tmp_path / "mfma", "m", [
+        ("k_mfma", "GRBM_GUI_ACTIVE", cycles * xcds), ("k_mfma", "GRBM_GUI_ACTIVE", cycles * xcds),
+        ("k_mfma", "SQ_VALU_MFMA_BUSY_CYCLES", busy), ("k_mfma", "SQ_INSTS_VALU_MFMA_MOPS_F32", mops),
+        ("k_mfma", "SQ_LDS_BANK_CONFLICT", 5.0), ("k_mfma", "SQ_LDS_IDX_ACTIVE", 100.0)])
+    fe = _pmc(tmp_path / "fetch", "f", [("k_mfma", "FETCH_SIZE", 1000.0), ("k_copyish", "FETCH_SIZE", 10.0)])
+    wr = _pmc(tmp_path / "write", "w", [("k_mfma", "WRITE_SIZE", 500.0), ("k_copyish", "WRITE_SIZE", 10.0)])
+    cf = _pmc(tmp_path / "cf", "c", [("__amd_rocclr_copyBuffer", "FETCH_SIZE", 512.0)])
+    cw = _pmc(tmp_path / "cw", "c", [("__amd_rocclr_copyBuffer", "WRITE_SIZE", 1024.0)])
+    calib = rr.calibration(cf, cw, 1 << 20)          # 1024 KiB moved each way
+    assert calib[0] == pytest.approx(2.0) and calib[1] == pytest.approx(1.0)
+    agent = rr.read_agent(mf)
+    assert agent["xcds"] == 8 and agent["simds"] == 1024
+    rows = {r.name: r for r in rr.build_rows(trace, [mf, fe, wr], calib, agent)}
+    r = rows["k_mfma"]
+    assert r.calls == 3 and r.avg_ms == pytest.approx(ms)
+    assert r.mfma_flop == pytest.approx(mops * 512)
+    assert r.tflops == pytest.approx(mops * 512 / (ms * 1e-3) / 1e12)
+    assert r.mfma_util == pytest.approx(0.75)
+    assert r.clock_ghz == pytest.approx(2.25)
+    assert r.hbm_bytes == pytest.approx(1024 * (1000 * 2.0 + 500 * 1.0))
+    assert r.intensity == pytest.approx(r.mfma_flop / r.hbm_bytes)
+    assert r.lds_conflict_rate == pytest.approx(0.05)
+    assert rows["k_copyish"].mfma_flop is None and rows["k_copyish"].mfma_util is None
+
+    text = rr.render(list(rows.values()), "T", ["cmd"], calib, agent)
+    assert "traffic_bytes_per_launch[k_mfma] = 2.560000e+06" in text
+    assert "mfma_util[k_mfma] = 0.7500" in text
+    assert "| k_mfma | 3 | 2.0000 |" in text
+
+
+def test_cli_writes_report(tmp_path):
+    trace = _trace(tmp_path / "trace", [("k", 1, 1e6)])
+    pmc = _pmc(tmp_path / "p", "p", [("k", "SQ_INSTS_VALU_MFMA_MOPS_F32", 1.0)])
+    out = tmp_path / "r.md"
+    assert rr.main(["--title", "X", "--trace", str(trace), "--pmc", str(pmc), "--out", str(out),
+                    "--command", "rocprofv3 ..."]) == 0
+    text = out.read_text()
+    assert text.startswith("# X") and "mfma_flop_per_launch[k] = 5.120000e+02" in text
+
+
+def test_missing_inputs_raise(tmp_path):
+    with pytest.raises(FileNotFoundError):
+        rr.read_kernel_stats(tmp_path)
+    no_copy = _pmc(tmp_path / "n", "n", [("k", "FETCH_SIZE", 1.0)])
+    with pytest.raises(ValueError):
+        rr.calibration(no_copy, no_copy, 1024)
+
+
+def test_trace_window(tmp_path):
+    d = tmp_path / "tr"
+    d.mkdir()
+    with open(d / "x_kernel_trace.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        # dispatches of k in launch order: 9, 1, 2, 3, 9 (ms); written out of order
+        for i, dur in reversed(list(enumerate([9, 1, 2, 3, 9]))):
+            w.writerow(["k", i * 100_000_000, i * 100_000_000 + dur * 1_000_000])
+    with open(d / "x_kernel_stats.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs",
+                    "StdDev"])
+        w.writerow(["k", 5, 24e6, 4.8e6, 100.0, 1e6, 9e6, 0])
+    win = rr.read_trace_window(d, 1, 3)
+    assert win["k"]["calls"] == 3 and win["k"]["avg_ns"] == pytest.approx(2e6)
+    assert win["k"]["all_calls"] == 5 and win["k"]["all_avg_ns"] == pytest.approx(4.8e6)
+    (row,) = rr.build_rows(d, window=(1, 3))
+    assert row.avg_ms == pytest.approx(2.0) and row.calls == 3
+    text = rr.render([row], "T", window=(1, 3))
+    assert "dispatches 1..3" in text and "| k | 5 | 4.8000 |" in text
