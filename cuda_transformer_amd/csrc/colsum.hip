@@ -6,8 +6,10 @@
 //    adjacent columns (dwordx4) or 1 column, walks 32 rows of its chunk with four independent
 //    accumulators, and writes one partial row.  Row pointers advance incrementally, so there is
 //    no division in the loop.
-//  * colsum_partials: sums a [chunks][ncols] partial matrix over its rows with a fixed-order
-//    tree (8 row groups per column, combined in LDS), so results are bitwise reproducible.
+//  * colsum_partials: sums a [chunks][ncols] partial matrix over its rows in a fixed order, so
+//    results are bitwise reproducible.  Given scratch, in two stages: up to 16 row groups of
+//    64-column blocks in parallel (four row phases per column, combined in LDS), then one pass
+//    over the group sums; without scratch, one workgroup per 32 columns walks every row.
 #include "cta_common.hpp"
 #include "gemm.hpp"
 
@@ -99,22 +101,88 @@ __global__ __launch_bounds__(256) void colsum_tree_kernel(const float* __restric
   }
 }
 
+constexpr int kGroupCols = 64;      // columns per workgroup in the grouped first stage
+constexpr int kGroupPhases = 4;     // row phases per column (256 threads = 64 x 4)
+constexpr int kRowsPerGroup = 32;   // target rows per group
+constexpr int kMaxGroups = 16;
+
+// Stage 1: group g of rows [g*rpg, min(chunks, (g+1)*rpg)) for 64 columns -> scratch[g][col].
+__global__ __launch_bounds__(256) void colsum_group_kernel(const float* __restrict__ part,
+                                                           int64_t chunks, int64_t ncols,
+                                                           int64_t rpg,
+                                                           float* __restrict__ scratch) {
+  __shared__ float red[kGroupPhases][kGroupCols];
+  const int c = threadIdx.x % kGroupCols, ph = threadIdx.x / kGroupCols;
+  const int64_t col = (int64_t)blockIdx.x * kGroupCols + c;
+  const int64_t r0 = (int64_t)blockIdx.y * rpg, r1 = min(chunks, r0 + rpg);
+  float a0 = 0.f, a1 = 0.f;
+  if (col < ncols) {
+    int64_t r = r0 + ph;
+    for (; r + kGroupPhases < r1; r += 2 * kGroupPhases) {
+      a0 += part[r * ncols + col];
+      a1 += part[(r + kGroupPhases) * ncols + col];
+    }
+    if (r < r1) a0 += part[r * ncols + col];
+  }
+  red[ph][c] = a0 + a1;
+  __syncthreads();
+  if (ph == 0 && col < ncols)
+    scratch[(int64_t)blockIdx.y * ncols + col] = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
+}
+
+// Stage 2: out[col] = sum over groups, in group order.
+__global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restrict__ scratch,
+                                                           int groups, int64_t ncols,
+                                                           float* __restrict__ out0,
+                                                           float* __restrict__ out1,
+                                                           int64_t split) {
+  const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (col >= ncols) return;
+  float s = scratch[col];
+  for (int g = 1; g < groups; ++g) s += scratch[(int64_t)g * ncols + col];
+  if (col < split) out0[col] = s;
+  else out1[col - split] = s;
+}
+
 int64_t rows_per_chunk(int64_t rows) {
   return std::max<int64_t>(kRowsPerChunk, (rows + 65534) / 65535);
 }
 
+int64_t colsum_groups(int64_t chunks) {
+  return std::min<int64_t>(kMaxGroups, std::max<int64_t>(1, (chunks + kRowsPerGroup - 1) / kRowsPerGroup));
+}
+
 }  // namespace
 
+int64_t colsum_partials_scratch_floats(int64_t chunks, int64_t ncols) {
+  return colsum_groups(chunks) * ncols;
+}
+
 int colsum_partials_launch(const float* part, int64_t chunks, int64_t ncols, float* out0,
-                           float* out1, int64_t split, hipStream_t st) {
-  const unsigned grid = (unsigned)((ncols + kTreeCols - 1) / kTreeCols);
-  hipLaunchKernelGGL(colsum_tree_kernel, dim3(grid), dim3(256), 0, st, part, chunks, ncols, out0,
-                     out1, split);
+                           float* out1, int64_t split, hipStream_t st, float* scratch) {
+  if (scratch == nullptr) {
+    const unsigned grid = (unsigned)((ncols + kTreeCols - 1) / kTreeCols);
+    hipLaunchKernelGGL(colsum_tree_kernel, dim3(grid), dim3(256), 0, st, part, chunks, ncols,
+                       out0, out1, split);
+    return check_launch("column sum");
+  }
+  const int64_t groups = colsum_groups(chunks);
+  const int64_t rpg = (chunks + groups - 1) / groups;
+  hipLaunchKernelGGL(colsum_group_kernel,
+                     dim3((unsigned)((ncols + kGroupCols - 1) / kGroupCols), (unsigned)groups),
+                     dim3(256), 0, st, part, chunks, ncols, rpg, scratch);
+  hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((ncols + 255) / 256)), dim3(256), 0, st,
+                     scratch, (int)groups, ncols, out0, out1, split);
   return check_launch("column sum");
 }
 
 int64_t colsum_chunks(int64_t rows) {
   return rows <= 0 ? 0 : (rows + rows_per_chunk(rows) - 1) / rows_per_chunk(rows);
+}
+
+int64_t colsum_workspace_floats(int64_t rows, int64_t N) {
+  const int64_t chunks = colsum_chunks(rows);
+  return chunks * N + colsum_partials_scratch_floats(chunks, N);
 }
 
 int colsum_launch(const float* x, int64_t batch, int64_t M, int64_t N, int64_t sb, int64_t sm,
@@ -134,7 +202,7 @@ int colsum_launch(const float* x, int64_t batch, int64_t M, int64_t N, int64_t s
     hipLaunchKernelGGL((colsum_rows_kernel<false>), grid, dim3(256), 0, st, x, workspace, M, N, sb,
                        sm, sn, rows, (int)rpc);
   if (int rc = check_launch("db_calculation")) return rc;
-  return colsum_partials_launch(workspace, chunks, N, out, out, N, st);
+  return colsum_partials_launch(workspace, chunks, N, out, out, N, st, workspace + chunks * N);
 }
 
 }  // namespace cta

@@ -10,9 +10,9 @@
 // The batch index z is split as (z / zin, z % zin) with a stride per level, which lets
 // the naive attention address heads inside a packed (B, T, 3C) tensor directly.
 //
-// gfx950 design: 256 threads = 4 waves in a 2x2 arrangement; workgroup tile 128x128, wave
-// tile 64x64 = 2x2 v_mfma_f32_32x32x2_f32 blocks.  A and B tiles are staged through LDS as
-// [m][k] and [n][k] (k contiguous, pitch BK+4), so each MFMA operand fragment is a pair of
+// gfx950 design: workgroup tile 128x128 of eight 32x64 waves (4x2) or 128x64 of four 64x32
+// waves, each wave owning a block of v_mfma_f32_32x32x2_f32 tiles.  A and B tiles are staged
+// through LDS as [m][k] and [n][k] (k contiguous, pitch BK+4), so each MFMA operand fragment is a pair of
 // conflict-free 16-byte LDS reads whatever the operand's memory order.  Global loads are
 // dwordx4 along whichever dimension is contiguous in memory (template mode), with scalar
 // loads for ragged edges and irregular strides.
@@ -358,11 +358,11 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
 }
 
 // Tile choice, from measured sweeps of the config-4 and small-GPT shapes on an MI355X:
-// shapes split along K run best with eight 32x64 waves, narrow outputs (N <= 768) with a
-// 128x64 tile, everything else with four 64x64 waves.
+// narrow outputs (N <= 768) run best with a 128x64 tile of four 64x32 waves, everything else
+// (including shapes split along K) with a 128x128 tile of eight 32x64 waves.
 using SplitTile = GemmTile<128, 128, 16, 4, 2>;
 using NarrowTile = GemmTile<128, 64, 16, 2, 2>;
-using WideTile = GemmTile<128, 128, 16, 2, 2>;
+using WideTile = GemmTile<128, 128, 16, 4, 2>;
 
 }  // namespace
 
@@ -415,7 +415,7 @@ extern "C" int cta_cuda_fma(const float* x, const int64_t* x_strides, const floa
 
 extern "C" int64_t cta_db_calculation_workspace(int64_t batch, int64_t m, int64_t n) {
   if (batch <= 0 || m <= 0 || n <= 0) return 0;
-  return colsum_chunks(batch * m) * n * (int64_t)sizeof(float);
+  return colsum_workspace_floats(batch * m, n) * (int64_t)sizeof(float);
 }
 
 extern "C" int cta_db_calculation(const float* dy, const int64_t* dy_strides, int64_t batch,

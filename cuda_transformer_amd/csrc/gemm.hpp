@@ -39,13 +39,16 @@ int softmax_bwd_rows_launch(const float* p, const float* dp, float* dx, int64_t 
                             hipStream_t st);
 
 // Column sums of a strided (batch, M, N) tensor into out[N]; workspace holds
-// colsum_chunks(batch * M) * N floats.  Deterministic.
+// colsum_workspace_floats(batch * M, N) floats.  Deterministic.
 int colsum_launch(const float* x, int64_t batch, int64_t M, int64_t N, int64_t sb, int64_t sm,
                   int64_t sn, float* out, float* workspace, hipStream_t st);
 int64_t colsum_chunks(int64_t rows);
+int64_t colsum_workspace_floats(int64_t rows, int64_t N);
 // Fixed-order sum over the rows of part[chunks][ncols]: column c goes to out0[c] (c < split)
-// or out1[c - split].
+// or out1[c - split].  `scratch` (colsum_partials_scratch_floats floats, may be null) lets the
+// sum run in two parallel stages.
 int colsum_partials_launch(const float* part, int64_t chunks, int64_t ncols, float* out0,
-                           float* out1, int64_t split, hipStream_t st);
+                           float* out1, int64_t split, hipStream_t st, float* scratch);
+int64_t colsum_partials_scratch_floats(int64_t chunks, int64_t ncols);
 
 }  // namespace cta

@@ -464,8 +464,10 @@ int64_t ln_bwd_blocks(int64_t rows) {
 
 int64_t layernorm_bwd_workspace_floats(int64_t rows, int64_t n) {
   if (rows <= 0 || n <= 0) return 0;
-  if (n <= kMaxRegCols) return ln_bwd_blocks(rows) * 2 * n;
-  return ((rows + kLnLongRowsPerBlock - 1) / kLnLongRowsPerBlock) * 2 * n;
+  const int64_t chunks = n <= kMaxRegCols
+                            ? ln_bwd_blocks(rows)
+                            : (rows + kLnLongRowsPerBlock - 1) / kLnLongRowsPerBlock;
+  return chunks * 2 * n + colsum_partials_scratch_floats(chunks, 2 * n);
 }
 
 }  // namespace cta
@@ -562,7 +564,8 @@ extern "C" int cta_layernorm_bwd(const float* x, const float* gamma, const float
     CTA_ROW_SWITCH(layernorm_bwd_rows, vec, u, dim3((unsigned)blocks), st, x, gamma, mean, rstd,
                    dy, dx, workspace, rows, (int)n, rows_per_wave);
     if (int rc = check_launch("layernorm_bwd")) return rc;
-    return colsum_partials_launch(workspace, blocks, 2 * n, dgamma, dbeta, n, st);
+    return colsum_partials_launch(workspace, blocks, 2 * n, dgamma, dbeta, n, st,
+                                  workspace + blocks * 2 * n);
   } else {
     hipLaunchKernelGGL(layernorm_bwd_long, dim3((unsigned)rows), dim3(256), 0, st, x, gamma, mean,
                        rstd, dy, dx, (int)n);
@@ -572,7 +575,8 @@ extern "C" int cta_layernorm_bwd(const float* x, const float* gamma, const float
                        dim3(256), 0, st, x, mean, rstd, dy, workspace, rows, (int)n,
                        kLnLongRowsPerBlock);
     if (int rc = check_launch("layernorm_bwd")) return rc;
-    return colsum_partials_launch(workspace, chunks, 2 * n, dgamma, dbeta, n, st);
+    return colsum_partials_launch(workspace, chunks, 2 * n, dgamma, dbeta, n, st,
+                                  workspace + chunks * 2 * n);
   }
   return check_launch("layernorm_bwd");
 }

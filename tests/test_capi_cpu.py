@@ -53,7 +53,7 @@ def test_layout_checks_run_before_launch():
 
 def test_workspace_queries():
     lib = capi.lib()
-    assert lib.cta_db_calculation_workspace(1, 8192, 3072) == 256 * 3072 * 4
+    assert lib.cta_db_calculation_workspace(1, 8192, 3072) == (256 + 8) * 3072 * 4  # partials + group sums
     assert lib.cta_db_calculation_workspace(0, 5, 5) == 0
     assert lib.cta_layernorm_bwd_workspace(8192, 768) > 0
     assert lib.cta_causal_self_attention_bwd_workspace(8, 33) == 8 * 33 * 33 * 4
