@@ -130,18 +130,26 @@ __global__ __launch_bounds__(256) void colsum_group_kernel(const float* __restri
     scratch[(int64_t)blockIdx.y * ncols + col] = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
 }
 
-// Stage 2: out[col] = sum over groups, in group order.
+// Stage 2: out[col] = sum over the group sums: each of four phases adds every fourth group in
+// order, then the phases are combined in order.
 __global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restrict__ scratch,
                                                            int groups, int64_t ncols,
                                                            float* __restrict__ out0,
                                                            float* __restrict__ out1,
                                                            int64_t split) {
-  const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (col >= ncols) return;
-  float s = scratch[col];
-  for (int g = 1; g < groups; ++g) s += scratch[(int64_t)g * ncols + col];
-  if (col < split) out0[col] = s;
-  else out1[col - split] = s;
+  __shared__ float red[kGroupPhases][kGroupCols];
+  const int c = threadIdx.x % kGroupCols, ph = threadIdx.x / kGroupCols;
+  const int64_t col = (int64_t)blockIdx.x * kGroupCols + c;
+  float a = 0.f;
+  if (col < ncols)
+    for (int g = ph; g < groups; g += kGroupPhases) a += scratch[(int64_t)g * ncols + col];
+  red[ph][c] = a;
+  __syncthreads();
+  if (ph == 0 && col < ncols) {
+    const float s = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
+    if (col < split) out0[col] = s;
+    else out1[col - split] = s;
+  }
 }
 
 int64_t rows_per_chunk(int64_t rows) {
@@ -171,8 +179,8 @@ int colsum_partials_launch(const float* part, int64_t chunks, int64_t ncols, flo
   hipLaunchKernelGGL(colsum_group_kernel,
                      dim3((unsigned)((ncols + kGroupCols - 1) / kGroupCols), (unsigned)groups),
                      dim3(256), 0, st, part, chunks, ncols, rpg, scratch);
-  hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((ncols + 255) / 256)), dim3(256), 0, st,
-                     scratch, (int)groups, ncols, out0, out1, split);
+  hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((ncols + kGroupCols - 1) / kGroupCols)),
+                     dim3(256), 0, st, scratch, (int)groups, ncols, out0, out1, split);
   return check_launch("column sum");
 }
 
