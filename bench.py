@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Headline benchmark: FlashAttention-2 forward + backward, FP32, on one MI355X.
 
-Workload: B=4, H=32, N=4096, D=64, causal; Q, K, V, dO ~ N(0, 1) from fixed
+Workload (benchmark config 2): B=4, H=32, N=4096, D=64, causal; Q, K, V, dO ~ N(0, 1) from fixed
 seeds; softmax scale 1/sqrt(64).  One step = the forward kernel then the three backward
 stages, launched through the C ABI on torch's current stream with all inputs and outputs
 already resident in HBM.  The backward runs the schedule the flash_attention_bwd operator
@@ -48,8 +48,8 @@ def parse_args():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--workload", choices=["fa2", "fa2-sweep", "ops", "gpt"], default="fa2",
-                   help="fa2: the headline step (default, one JSON line); fa2-sweep: BASELINE "
-                        "config 3; ops: BASELINE config 4 (one JSON line per op); gpt: BASELINE "
+                   help="fa2: the headline step (default, one JSON line); fa2-sweep: benchmark "
+                        "config 3; ops: benchmark config 4 (one JSON line per op); gpt: benchmark "
                         "config 5 training step")
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
@@ -248,7 +248,7 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored"):
 
 
 def fa2_sweep(args):
-    """non-causal B4 H32 D64, N in {1024 ... 16384}; one JSON line per N."""
+    """Benchmark config 3: non-causal B4 H32 D64, N in {1024 ... 16384}; one JSON line per N."""
     import torch
 
     for N in (1024, 2048, 4096, 8192, 16384):
@@ -309,7 +309,7 @@ def _cpu_time(fn, target_s=2.0):
 
 
 def ops_workload(args):
-    """BASELINE config 4 (GPT-2-small widths, FP32): linear GEMM fwd/bwd, db, exact GELU,
+    """Benchmark config 4 (GPT-2-small widths, FP32): linear GEMM fwd/bwd, db, exact GELU,
     LayerNorm and row softmax, each launched through the C ABI.  One JSON line per op with
     the kernel's roofline (MFMA TFLOP/s for GEMMs, HBM GB/s otherwise) and the CPU oracle
     (float32 numpy) timed on a bounded sample of the same op."""
@@ -457,7 +457,7 @@ def ops_workload(args):
 
 
 def gpt_workload(args):
-    """one training step (fwd + bwd + AdamW) of the small GPT on the HIP
+    """Benchmark config 5: one training step (fwd + bwd + AdamW) of the small GPT on the HIP
     kernels (cuda_transformer_amd/gpt.py), batch 64 x context 256; tokens/s.  CPU baseline: the
     plain-torch model (oracle/gpt.py) on this host, batch 8, same step."""
     import torch

@@ -1,7 +1,7 @@
 """ctypes binding of the C ABI in ``include/cuda_transformer_amd.h``.
 
-This is the binding a non-torch caller would use (see INTEGRATION.md for the same in other
-FFIs).  The tests use it to call the kernels through the C boundary directly and to check
+This is the binding a non-torch caller would use; other FFIs (cgo, JNI, N-API) bind the same
+symbols.  The tests use it to call the kernels through the C boundary directly and to check
 that the shared library exports every declared symbol.  Loading it needs no GPU.
 """
 from __future__ import annotations

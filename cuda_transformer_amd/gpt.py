@@ -1,4 +1,4 @@
-"""Small GPT on the gfx950 kernels: the training-step harness of BASELINE config 5.
+"""Small GPT on the gfx950 kernels: the training-step harness of benchmark config 5.
 
 A parametrised counterpart of the reference's gpt/gpt.py:47-187, whose model reads module
 globals (d_model, vocab_size, block_size: gpt.py:17-29,50-51,64-65) and trains at import time.

@@ -55,7 +55,7 @@ def rel_err(a, b):
 
 
 def assert_rel_err(a, b, tol=1e-3, floor=1e-6):
-    """Relative L2 error <= tol (BASELINE's gradient bar).  When the reference is exactly zero
+    """Relative L2 error <= tol (the acceptance bar for gradients).  When the reference is exactly zero
     up to rounding (norm below floor * sqrt(size), e.g. dQ for T = 1) a relative error is
     meaningless and the absolute bar floor * sqrt(size) applies instead."""
     a = np.asarray(a, dtype=np.float64)

@@ -1,8 +1,8 @@
 """FlashAttention-2 forward/backward on the GPU vs the CPU oracle (float64).
 
 Shapes: the reference's own parametrisation (test/test_flash_attention.py:52-60, including
-ragged T and hs in {32, 64, 128}) and BASELINE config 1 (B1 H4 N256 D64).  Tolerances: the
-reference suite's allclose (O, L atol 1e-5; grads atol 1e-4, rtol 1e-5) and BASELINE's bar
+ragged T and hs in {32, 64, 128}) and benchmark config 1 (B1 H4 N256 D64).  Tolerances: the
+reference suite's allclose (O, L atol 1e-5; grads atol 1e-4, rtol 1e-5) and the acceptance bar
 (O max-abs <= 1e-4, dQ/dK/dV relative L2 error <= 1e-3).  Like the reference test, the
 backward is fed the oracle's L and the kernel's own O (test_flash_attention.py:48).
 """
@@ -23,8 +23,8 @@ REF_SHAPES = [
     (2, 4, 128, 64, True),
     (2, 4, 257, 64, True),
     (1, 2, 512, 128, True),
-    (1, 4, 256, 64, True),
-    (1, 4, 256, 64, False),
+    (1, 4, 256, 64, True),   # benchmark config 1
+    (1, 4, 256, 64, False),  # benchmark config 1
     (1, 3, 1, 64, True),     # single row
     (2, 2, 129, 32, True),
     (1, 2, 200, 128, False),
@@ -215,7 +215,7 @@ def test_fa2_through_c_abi(cuda):
 
 
 def test_fa2_config2_full_size(cuda):
-    """BASELINE config 2 (B4 H32 N4096 D64, causal) at full size: two heads against the
+    """Benchmark config 2 (B4 H32 N4096 D64, causal) at full size: two heads against the
     float64 oracle, and on every head the size-independent invariants of the backward:
     sum_j dK_j = 0 (rows of dS sum to zero) and sum_j dV_j = sum_i dO_i (rows of P sum to 1)."""
     from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd

@@ -1,4 +1,4 @@
-"""the small GPT (6 layers, 6 heads, d_model 384, context 256, vocab 65,
+"""Benchmark config 5: the small GPT (6 layers, 6 heads, d_model 384, context 256, vocab 65,
 batch 64) trained for 5 AdamW steps on the HIP kernels, against the same model in plain torch
 on the CPU from identical weights and token ids.  Loss must match at every step."""
 import pytest

@@ -1,7 +1,7 @@
 """Linear, db, GELU, softmax, LayerNorm and naive attention on the GPU vs the CPU oracle.
 
 Shapes follow the reference suite (test/test_linear.py:53-59, test_gelu.py:36-42,
-test_softmax.py:33-39, test_causal_self_attn.py:69-77) plus BASELINE config 4 (GPT-2-small
+test_softmax.py:33-39, test_causal_self_attn.py:69-77) plus benchmark config 4 (GPT-2-small
 widths).  Tolerances: the reference's allclose atol 1e-5 (rtol 1e-5) on U[0,1) inputs; for
 config 4 the GEMM is checked by relative error (K = 768/3072 FP32 sums).
 """
@@ -69,7 +69,7 @@ def test_linear_batched_weights_and_errors(cuda):
 
 
 def test_linear_config4(cuda):
-    """X[8192,768] . W[768,3072] + b, X and W ~ N(0, 0.02^2)."""
+    """X[8192,768] . W[768,3072] + b, X and W ~ N(0, 0.02^2) (benchmark config 4)."""
     from cuda_autograd_fns import CudaLinearLayer
 
     x = seeded((1, 8192, 768), 40, scale=0.02)
