@@ -58,6 +58,9 @@ def parse_args():
     p.add_argument("--seq", type=int, default=4096)
     p.add_argument("--head-dim", type=int, default=64)
     p.add_argument("--non-causal", action="store_true")
+    p.add_argument("--gpt-mlp", choices=["fused", "reference"], default="fused",
+                   help="gpt workload: fused: CudaMLP (GELU in the GEMM epilogues, the model's "
+                        "default); reference: CudaLinearLayer -> CudaGeluLayer -> CudaLinearLayer")
     p.add_argument("--bwd-schedule", choices=["stored", "recompute"], default="stored",
                    help="stored: dK/dV writes dS and dQ reads it (what the operator runs); "
                         "recompute: the reference's delta / dQ / dK/dV schedule")
@@ -465,7 +468,7 @@ def gpt_workload(args):
     from cuda_transformer_amd.gpt import GPT, GPTConfig, init_weights_, synthetic_batch
     from oracle import gpt as ogpt
 
-    cfg, batch = GPTConfig(), 64
+    cfg, batch = GPTConfig(fused_mlp=args.gpt_mlp == "fused"), 64
     model = GPT(cfg)
     init_weights_(model, seed=0)
     model.cuda()
@@ -520,7 +523,7 @@ def gpt_workload(args):
         "workload": "small-GPT training step (6L 6H d384 ctx256 vocab65, batch 64), FP32",
         "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 3),
         "fwd_bwd_ms": round(ms_fb, 3), "fwd_bwd_tokens_per_s": round(tokens / (ms_fb * 1e-3), 1),
-        "steps": args.steps, "cpu_baseline": cpu,
+        "steps": args.steps, "mlp": args.gpt_mlp, "cpu_baseline": cpu,
     }), flush=True)
     return 0
 

@@ -14,7 +14,7 @@ _MISSING = [p.name for p in (_PKG / "_C.so", _PKG / "libcuda_transformer_amd.so"
 if _MISSING:
     raise ImportError(
         f"cuda_transformer_amd native libraries not built ({', '.join(_MISSING)}); "
-        "run `python -m cuda_transformer_amd.build`"
+        "run `python cuda_transformer_amd/build.py`"
     )
 
 from . import _C  # noqa: E402,F401  registers torch.ops.cuda_transformer.*

@@ -2,7 +2,8 @@
 
 Same classes, ``apply`` signatures and saved tensors as the reference's cuda_autograd_fns/
 (cuda_flash_attention.py:4-17, cuda_linear_layer.py:4-28, cuda_gelu_layer.py:4-14,
-cuda_softmax_layer.py:4-15, cuda_causal_self_attention.py:4-35), plus ``CudaLayerNorm``.
+cuda_softmax_layer.py:4-15, cuda_causal_self_attention.py:4-35), plus ``CudaLayerNorm`` and
+``CudaMLP`` (the GPT MLP with its GELU folded into the GEMM epilogues).
 
 Deviations, each a fix:
 
@@ -16,14 +17,14 @@ Deviations, each a fix:
 import torch
 
 from .ops import (
-    causal_self_attention_bwd, causal_self_attention_fwd, cuda_fma, cuda_softmax,
-    cuda_softmax_bwd, db_calculation, flash_attention_bwd, flash_attention_fwd, gelu_activation,
+    causal_self_attention_bwd, causal_self_attention_fwd, cuda_fma, cuda_fma_gelu,
+    cuda_fma_gelu_grad, cuda_softmax, cuda_softmax_bwd, db_calculation, flash_attention_bwd, flash_attention_fwd, gelu_activation,
     gelu_activation_bwd, layernorm_bwd, layernorm_fwd,
 )
 
 __all__ = [
     "CudaCausalSelfAttention", "CudaFlashAttention", "CudaGeluLayer", "CudaLinearLayer",
-    "CudaSoftmaxLayer", "CudaLayerNorm",
+    "CudaSoftmaxLayer", "CudaLayerNorm", "CudaMLP",
 ]
 
 
@@ -58,18 +59,24 @@ class CudaLinearLayer(torch.autograd.Function):
         x, weights, _, _ = ctx.saved_tensors
         dy = grad_output
         w = weights.unsqueeze(0) if weights.dim() == 2 else weights
-        k, n = x.shape[-1], dy.shape[-1]
-        dx = cuda_fma(dy, w.transpose(1, 2), torch.zeros(k, dtype=dy.dtype, device=dy.device))
-        zero_n = torch.zeros(n, dtype=dy.dtype, device=dy.device)
-        if weights.dim() == 2:
-            # sum_b x[b]^T dy[b] == (x as (b*m, k))^T (dy as (b*m, n)): one GEMM, K = b*m
-            x2 = x.reshape(1, -1, k)
-            dy2 = dy.reshape(1, -1, n)
-            dw = cuda_fma(x2.transpose(1, 2), dy2, zero_n)[0]
-        else:
-            dw = cuda_fma(x.transpose(1, 2), dy, zero_n)
-        db = db_calculation(dy)
+        dx = cuda_fma(dy, w.transpose(1, 2),
+                      torch.zeros(x.shape[-1], dtype=dy.dtype, device=dy.device))
+        dw, db = _weight_and_bias_grads(x, weights, dy)
         return dx, dw, db
+
+
+def _weight_and_bias_grads(x, weights, dy):
+    """dW = sum_b x[b]^T dy[b] and db = sum of dy over (batch, rows) (cuda_linear_layer.py:21-27)."""
+    k, n = x.shape[-1], dy.shape[-1]
+    zero_n = torch.zeros(n, dtype=dy.dtype, device=dy.device)
+    if weights.dim() == 2:
+        # sum_b x[b]^T dy[b] == (x as (b*m, k))^T (dy as (b*m, n)): one GEMM, K = b*m
+        x2 = x.reshape(1, -1, k)
+        dy2 = dy.reshape(1, -1, n)
+        dw = cuda_fma(x2.transpose(1, 2), dy2, zero_n)[0]
+    else:
+        dw = cuda_fma(x.transpose(1, 2), dy, zero_n)
+    return dw, db_calculation(dy)
 
 
 class CudaGeluLayer(torch.autograd.Function):
@@ -85,6 +92,36 @@ class CudaGeluLayer(torch.autograd.Function):
     def backward(ctx, grad_output):
         (x,) = ctx.saved_tensors
         return gelu_activation_bwd(x, grad_output.contiguous())
+
+
+class CudaMLP(torch.autograd.Function):
+    """(x, w1, b1, w2, b2) -> gelu(x @ w1 + b1) @ w2 + b2, the GPT MLP (gpt/gpt.py:133-136).
+
+    Same values, bit for bit, as CudaLinearLayer, CudaGeluLayer and CudaLinearLayer applied in
+    turn (2-D weights), in fewer passes over the (batch, m, 4 d_model) hidden tensor: the
+    forward's fc1 GEMM writes the pre-activation and its GELU together (``cuda_fma_gelu``), and
+    the backward's fc2 dx GEMM applies the GELU derivative before its store
+    (``cuda_fma_gelu_grad``), so neither GELU pass re-reads the hidden tensor.
+    """
+
+    @staticmethod
+    def forward(ctx, x, w1, b1, w2, b2):
+        torch._check(w1.dim() == 2 and w2.dim() == 2, lambda: "CudaMLP takes 2-D weights")
+        pre, h = cuda_fma_gelu(x, w1, b1)
+        out = cuda_fma(h, w2, b2)
+        ctx.save_for_backward(x, w1, w2, pre, h)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x, w1, w2, pre, h = ctx.saved_tensors
+        dz = grad_output
+        dw2, db2 = _weight_and_bias_grads(h, w2, dz)
+        dpre = cuda_fma_gelu_grad(dz, w2.unsqueeze(0).transpose(1, 2), pre)
+        dw1, db1 = _weight_and_bias_grads(x, w1, dpre)
+        dx = cuda_fma(dpre, w1.unsqueeze(0).transpose(1, 2),
+                      torch.zeros(x.shape[-1], dtype=dz.dtype, device=dz.device))
+        return dx, dw1, db1, dw2, db2
 
 
 class CudaSoftmaxLayer(torch.autograd.Function):

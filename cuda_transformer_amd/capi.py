@@ -45,6 +45,10 @@ SIGNATURES = {
     "cta_cuda_fma_workspace": (_i64, [_i64, _i64, _i64, _i64]),
     "cta_cuda_fma": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p,
                             _p, _p]),
+    "cta_cuda_fma_gelu": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                                 _p, _p, _p, _p]),
+    "cta_cuda_fma_gelu_grad": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64, _i64,
+                                      _p, _p, _p]),
     "cta_db_calculation_workspace": (_i64, [_i64, _i64, _i64]),
     "cta_db_calculation": (_int, [_p, _i64p, _i64, _i64, _i64, _p, _p, _p]),
     "cta_gelu_fwd": (_int, [_p, _p, _i64, _p]),
@@ -79,7 +83,7 @@ def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
-            raise ImportError(f"{LIB_PATH.name} is not built; run `python -m cuda_transformer_amd.build`")
+            raise ImportError(f"{LIB_PATH.name} is not built; run `python cuda_transformer_amd/build.py`")
         handle = ctypes.CDLL(str(LIB_PATH))
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(handle, name)

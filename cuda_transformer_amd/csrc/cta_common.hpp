@@ -108,6 +108,17 @@ __device__ __forceinline__ void wave_lds_fence() {
 // 2^x on the hardware transcendental unit (v_exp_f32). Inputs here are <= 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Exact (erf) GELU as Transformer_kernels/GeLU.cuh:7-29 defines it: y = x Phi(x) and
+// dx = dy (Phi(x) + x phi(x)), phi(x) = e^{-x^2/2} / sqrt(2 pi), with HIP's normcdff/expf.
+// The standalone GELU kernels and the GEMM epilogue share these two functions, so a fused
+// linear+GELU gives the same bits as the two ops run one after the other.
+constexpr float kInvSqrt2Pi = 0.3989422804014327f;
+__device__ __forceinline__ float gelu_f(float x) { return x * normcdff(x); }
+__device__ __forceinline__ float gelu_grad(float x, float g) {
+  const float pdf = kInvSqrt2Pi * expf(-0.5f * x * x);
+  return g * (normcdff(x) + x * pdf);
+}
+
 // ----------------------------------------------------------------------------------
 // Host-side helpers shared by the C-ABI entry points.
 void set_error(const std::string& msg);

@@ -2,6 +2,9 @@
 //
 //   out[z][m][n] = alpha * sum_k A[z][m][k] * B[z][k][n]  (+ bias[n])  (causal: -inf for n > m)
 //
+// optionally followed by a GELU stage in the epilogue (the GPT MLP's fc1 -> GELU forward and
+// fc2 -> GELU backward products, each one pass over the output instead of two).
+//
 // This one kernel backs the reference's fused_multiply_add (Transformer_kernels/
 // fused_multiply_add.cuh:10-92, launched from Transformer_launchers/linear_layer.cu:28-70),
 // its strided batched cuda_bmm (batched_matrix_multiply.cuh:9-75) and the two GEMM stages of
@@ -121,7 +124,7 @@ struct TileLoader {
 // split_ws == nullptr: out = alpha * A B (+ bias, mask) written through C.
 // split_ws != nullptr: blockIdx.z = s * Z + z covers K range [s*kchunk, (s+1)*kchunk) and the raw
 // partial sum goes to split_ws[s][z][m][n] (dense); gemm_splitk_reduce finishes the epilogue.
-template <class TL, int AMODE, int BMODE>
+template <class TL, int AMODE, int BMODE, int ACT>
 __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOperand B,
                                                            GemmOut C, GemmEpilogue ep, int M,
                                                            int N, int K, int zin, int Z,
@@ -239,6 +242,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
     return;
   }
   float* Cb = C.p + zo * C.s_outer + zi * C.s_inner;
+  float* Xb = ep.aux ? ep.aux + zo * C.s_outer + zi * C.s_inner : nullptr;
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int n = n0 + wn * (BN / TL::WN) + j * 32 + col;
@@ -252,7 +256,10 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
         if (m < M) {
           float val = fmaf(ep.alpha, acc[i][j][r], bv);
           if (ep.causal_mask && n > m) val = -INFINITY;
-          Cb[(int64_t)m * C.s_row + n] = val;
+          const int64_t off = (int64_t)m * C.s_row + n;
+          if (ACT == kActGeluGrad) val = gelu_grad(Xb[off], val);
+          Cb[off] = val;
+          if (ACT == kActGelu) Xb[off] = gelu_f(val);
         }
       }
     }
@@ -275,7 +282,10 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float* __restric
     const int64_t zo = z / zin, zi = z - zo * zin;
     float val = fmaf(ep.alpha, acc, ep.bias ? ep.bias[(int64_t)n * ep.bias_stride] : 0.0f);
     if (ep.causal_mask && n > m) val = -INFINITY;
-    C.p[zo * C.s_outer + zi * C.s_inner + (int64_t)m * C.s_row + n] = val;
+    const int64_t off = zo * C.s_outer + zi * C.s_inner + (int64_t)m * C.s_row + n;
+    if (ep.act == kActGeluGrad) val = gelu_grad(ep.aux[off], val);
+    C.p[off] = val;
+    if (ep.act == kActGelu) ep.aux[off] = gelu_f(val);
   }
 }
 
@@ -296,20 +306,32 @@ int pick_mode(const GemmOperand& op, bool is_a, int64_t rows, int64_t K) {
   return kScalar;
 }
 
-template <class TL, int AM>
+template <class TL, int AM, int ACT>
 void dispatch_b(int bm, dim3 grid, hipStream_t st, const GemmOperand& A, const GemmOperand& B,
                 const GemmOut& C, const GemmEpilogue& ep, int M, int N, int K, int zin, int Z,
                 int kchunk, float* ws) {
   const dim3 block(TL::THREADS);
   if (bm == kVecK)
-    hipLaunchKernelGGL((gemm_kernel<TL, AM, kVecK>), grid, block, 0, st, A, B, C, ep, M, N, K,
-                       zin, Z, kchunk, ws);
+    hipLaunchKernelGGL((gemm_kernel<TL, AM, kVecK, ACT>), grid, block, 0, st, A, B, C, ep, M, N,
+                       K, zin, Z, kchunk, ws);
   else if (bm == kVecMN)
-    hipLaunchKernelGGL((gemm_kernel<TL, AM, kVecMN>), grid, block, 0, st, A, B, C, ep, M, N, K,
-                       zin, Z, kchunk, ws);
+    hipLaunchKernelGGL((gemm_kernel<TL, AM, kVecMN, ACT>), grid, block, 0, st, A, B, C, ep, M, N,
+                       K, zin, Z, kchunk, ws);
   else
-    hipLaunchKernelGGL((gemm_kernel<TL, AM, kScalar>), grid, block, 0, st, A, B, C, ep, M, N, K,
-                       zin, Z, kchunk, ws);
+    hipLaunchKernelGGL((gemm_kernel<TL, AM, kScalar, ACT>), grid, block, 0, st, A, B, C, ep, M,
+                       N, K, zin, Z, kchunk, ws);
+}
+
+template <class TL, int ACT>
+void dispatch_a(int am, int bm, dim3 grid, hipStream_t st, const GemmOperand& A,
+                const GemmOperand& B, const GemmOut& C, const GemmEpilogue& ep, int M, int N,
+                int K, int zin, int Z, int kchunk, float* ws) {
+  if (am == kVecK)
+    dispatch_b<TL, kVecK, ACT>(bm, grid, st, A, B, C, ep, M, N, K, zin, Z, kchunk, ws);
+  else if (am == kVecMN)
+    dispatch_b<TL, kVecMN, ACT>(bm, grid, st, A, B, C, ep, M, N, K, zin, Z, kchunk, ws);
+  else
+    dispatch_b<TL, kScalar, ACT>(bm, grid, st, A, B, C, ep, M, N, K, zin, Z, kchunk, ws);
 }
 
 // K splits for a GEMM whose output tiles alone cannot fill the 256 CUs: enough splits for
@@ -339,15 +361,15 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
   float* ws = S > 1 ? workspace : nullptr;
   const int am = pick_mode(A, true, M, K);
   const int bm = pick_mode(B, false, N, K);
-  if (am == kVecK)
-    dispatch_b<TL, kVecK>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin, (int)Z,
-                          (int)kchunk, ws);
-  else if (am == kVecMN)
-    dispatch_b<TL, kVecMN>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin, (int)Z,
-                           (int)kchunk, ws);
+  // Split-K partials are stored raw; the reduction applies the epilogue's pointwise stage.
+  const int act = S > 1 ? kActNone : ep.act;
+  const int iM = (int)M, iN = (int)N, iK = (int)K, izin = (int)zin, iZ = (int)Z, ikc = (int)kchunk;
+  if (act == kActGelu)
+    dispatch_a<TL, kActGelu>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
+  else if (act == kActGeluGrad)
+    dispatch_a<TL, kActGeluGrad>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
   else
-    dispatch_b<TL, kScalar>(bm, grid, st, A, B, C, ep, (int)M, (int)N, (int)K, (int)zin, (int)Z,
-                            (int)kchunk, ws);
+    dispatch_a<TL, kActNone>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
   if (S > 1) {
     const int64_t total = Z * M * N;
     const unsigned rgrid = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
@@ -394,23 +416,62 @@ extern "C" int64_t cta_cuda_fma_workspace(int64_t batch, int64_t m, int64_t k, i
   return gemm_workspace_floats(m, n, k, batch) * (int64_t)sizeof(float);
 }
 
-extern "C" int cta_cuda_fma(const float* x, const int64_t* x_strides, const float* w,
-                            const int64_t* w_strides, const float* bias, int64_t bias_stride,
-                            int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
-                            float* out, float* workspace, void* stream) {
+namespace {
+// out[b] = x[b] . W[b or 0] with epilogue `ep`, out dense (batch, m, n): the shared body of the
+// linear-layer entry points.  Weights broadcast over the batch with batch stride 0 when
+// w_batch == 1, as linear_layer.cu:30-34 does.
+int linear_launch(const float* x, const int64_t* x_strides, const float* w,
+                  const int64_t* w_strides, int64_t batch, int64_t m, int64_t k, int64_t n,
+                  int64_t w_batch, float* out, const GemmEpilogue& ep, float* workspace,
+                  void* stream) {
   if (batch < 0 || m < 0 || k < 0 || n < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
   if (w_batch != 1 && w_batch != batch)
     return fail(CTA_ERR_INVALID_ARGUMENT, "weights batch must be 1 or equal to x batch");
   if (batch * m * n == 0) return CTA_OK;
-  if (!x || !w || !bias || !out || !x_strides || !w_strides)
+  if (!x || !w || !out || !x_strides || !w_strides)
     return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
   const GemmOperand A{x, x_strides[0], 0, x_strides[1], x_strides[2]};
-  // Broadcast weights use batch stride 0, as linear_layer.cu:30-34 does.
   const GemmOperand B{w, w_batch == 1 ? 0 : w_strides[0], 0, w_strides[1], w_strides[2]};
   const GemmOut C{out, m * n, 0, n};
-  const GemmEpilogue ep{1.0f, bias, bias_stride, 0};
   return gemm_launch(A, B, C, ep, m, n, k, batch, 1, as_stream(stream), workspace,
                      workspace ? gemm_workspace_floats(m, n, k, batch) : 0);
+}
+}  // namespace
+
+extern "C" int cta_cuda_fma(const float* x, const int64_t* x_strides, const float* w,
+                            const int64_t* w_strides, const float* bias, int64_t bias_stride,
+                            int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
+                            float* out, float* workspace, void* stream) {
+  if (!bias && batch > 0 && m > 0 && n > 0) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  const GemmEpilogue ep{1.0f, bias, bias_stride, 0};
+  return linear_launch(x, x_strides, w, w_strides, batch, m, k, n, w_batch, out, ep, workspace,
+                       stream);
+}
+
+extern "C" int cta_cuda_fma_gelu(const float* x, const int64_t* x_strides, const float* w,
+                                 const int64_t* w_strides, const float* bias,
+                                 int64_t bias_stride, int64_t batch, int64_t m, int64_t k,
+                                 int64_t n, int64_t w_batch, float* pre, float* out,
+                                 float* workspace, void* stream) {
+  if (batch > 0 && m > 0 && n > 0) {
+    if (!bias || !out) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+    if (pre == out) return fail(CTA_ERR_INVALID_ARGUMENT, "pre and out must be distinct buffers");
+  }
+  const GemmEpilogue ep{1.0f, bias, bias_stride, 0, kActGelu, out};
+  return linear_launch(x, x_strides, w, w_strides, batch, m, k, n, w_batch, pre, ep, workspace,
+                       stream);
+}
+
+extern "C" int cta_cuda_fma_gelu_grad(const float* dy, const int64_t* dy_strides, const float* w,
+                                      const int64_t* w_strides, const float* pre, int64_t batch,
+                                      int64_t m, int64_t k, int64_t n, int64_t w_batch,
+                                      float* dx, float* workspace, void* stream) {
+  if (!pre && batch > 0 && m > 0 && n > 0) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  // Each output element reads its own pre-activation just before it is stored, so dx may
+  // alias pre.
+  const GemmEpilogue ep{1.0f, nullptr, 0, 0, kActGeluGrad, const_cast<float*>(pre)};
+  return linear_launch(dy, dy_strides, w, w_strides, batch, m, k, n, w_batch, dx, ep, workspace,
+                       stream);
 }
 
 extern "C" int64_t cta_db_calculation_workspace(int64_t batch, int64_t m, int64_t n) {

@@ -17,11 +17,20 @@ struct GemmOut {
   int64_t s_outer, s_inner, s_row;  // column stride is 1
 };
 
+// Pointwise stage applied to v = alpha * acc + bias before the store.
+enum GemmAct {
+  kActNone = 0,
+  kActGelu = 1,      // C = v (the pre-activation) and aux = gelu(v)
+  kActGeluGrad = 2,  // C = v * gelu'(aux): aux holds the pre-activation
+};
+
 struct GemmEpilogue {
   float alpha;
   const float* bias;  // nullable, indexed by n
   int64_t bias_stride;
   int causal_mask;    // set entries with n > m to -inf
+  int act = kActNone;
+  float* aux = nullptr;  // same (batch, m, n) layout as the output; read-only for kActGeluGrad
 };
 
 // out[z] = alpha * A[z] B[z] (+ bias) for z in [0, Z); batch index split as (z / zin, z % zin).

@@ -19,14 +19,8 @@
 namespace cta {
 namespace {
 
-constexpr float kInvSqrt2Pi = 0.3989422804014327f;
-
 // ------------------------------------------------------------------------------- GELU
-__device__ __forceinline__ float gelu_f(float x) { return x * normcdff(x); }
-__device__ __forceinline__ float gelu_grad(float x, float g) {
-  const float pdf = kInvSqrt2Pi * expf(-0.5f * x * x);
-  return g * (normcdff(x) + x * pdf);
-}
+// (gelu_f / gelu_grad live in cta_common.hpp, shared with the GEMM epilogue.)
 
 // Each thread handles four independent float4 per iteration (index i + 256*u within a chunk of
 // 1024 float4) so that four loads are in flight before the math starts.

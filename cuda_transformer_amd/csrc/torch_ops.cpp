@@ -5,7 +5,8 @@
 // validates its inputs with TORCH_CHECK (surfacing as a Python RuntimeError), allocates
 // dense outputs on the input's device, and calls the gfx950 kernels through the C ABI on
 // torch's current HIP stream.  Two schemas are added for LayerNorm, which the reference
-// implements in plain torch only (gpt/gpt.py:47-59).
+// implements in plain torch only (gpt/gpt.py:47-59), and two for the fused linear+GELU products
+// of the GPT MLP.
 //
 // This file is host-only C++; every kernel lives in libcuda_transformer_amd.so.
 #include <Python.h>
@@ -98,6 +99,72 @@ at::Tensor cuda_fma(at::Tensor x, at::Tensor weights, at::Tensor bias) {
                         weights.size(0), out.data_ptr<float>(),
                         ws_bytes > 0 ? scratch.data_ptr<float>() : nullptr, stream_of(x)));
   return out;
+}
+
+// Shared checks of the fused linear+GELU ops: x (batch, m, k), weights (k, n) or (1|batch, k, n),
+// same messages as cuda_fma.  Returns weights as 3-D.
+at::Tensor check_linear(const at::Tensor& x, at::Tensor weights) {
+  if (weights.dim() == 2) weights = weights.unsqueeze(0);
+  TORCH_CHECK(x.dim() == 3, "x must be a 3D tensor (batch, m, k)");
+  TORCH_CHECK(weights.dim() == 3, "weights must be a 2D or 3D tensor");
+  TORCH_CHECK(weights.size(1) == x.size(2), "weights.size(1) must match x.size(2)");
+  TORCH_CHECK(x.is_cuda(), "x must be a CUDA tensor");
+  TORCH_CHECK(weights.is_cuda(), "weights must be a CUDA tensor");
+  check_f32(x, "x");
+  check_f32(weights, "weights");
+  TORCH_CHECK(weights.size(0) == 1 || weights.size(0) == x.size(0),
+              "weights.size(0) must be 1 or match x.size(0)");
+  return weights;
+}
+
+// (pre, out) = (x W + b, GELU(x W + b)) from one GEMM whose epilogue writes both.  New op: the
+// GPT MLP's fc1 -> GELU (gpt/gpt.py:134-135) without the second pass over pre.
+std::tuple<at::Tensor, at::Tensor> cuda_fma_gelu(at::Tensor x, at::Tensor weights,
+                                                 at::Tensor bias) {
+  weights = check_linear(x, weights);
+  TORCH_CHECK(bias.dim() == 1, "bias must be a 1D tensor");
+  TORCH_CHECK(bias.size(0) == weights.size(2), "bias.size(0) must match weights.size(2)");
+  TORCH_CHECK(bias.is_cuda(), "bias must be a CUDA tensor");
+  check_f32(bias, "bias");
+  const int64_t batch = x.size(0), m = x.size(1), k = x.size(2), n = weights.size(2);
+  c10::OptionalDeviceGuard guard(x.device());
+  at::Tensor pre = at::empty({batch, m, n}, x.options());
+  at::Tensor out = at::empty({batch, m, n}, x.options());
+  const auto xs = strides_of<3>(x);
+  const auto wst = strides_of<3>(weights);
+  const int64_t ws_bytes = cta_cuda_fma_workspace(batch, m, k, n);
+  at::Tensor scratch;
+  if (ws_bytes > 0) scratch = at::empty({ws_bytes / 4}, x.options());
+  check_rc(cta_cuda_fma_gelu(x.data_ptr<float>(), xs.data(), weights.data_ptr<float>(),
+                             wst.data(), bias.data_ptr<float>(), bias.stride(0), batch, m, k, n,
+                             weights.size(0), pre.data_ptr<float>(), out.data_ptr<float>(),
+                             ws_bytes > 0 ? scratch.data_ptr<float>() : nullptr, stream_of(x)));
+  return {pre, out};
+}
+
+// dx = (dy W) * GELU'(pre).  New op: CudaLinearLayer.backward's dx product of fc2 followed by
+// CudaGeluLayer.backward (cuda_linear_layer.py:19-23, cuda_gelu_layer.py:12-14) in one pass.
+at::Tensor cuda_fma_gelu_grad(at::Tensor dy, at::Tensor weights, at::Tensor pre) {
+  weights = check_linear(dy, weights);
+  const int64_t batch = dy.size(0), m = dy.size(1), k = dy.size(2), n = weights.size(2);
+  TORCH_CHECK(pre.dim() == 3 && pre.size(0) == batch && pre.size(1) == m && pre.size(2) == n,
+              "pre must have shape (dy.size(0), dy.size(1), weights.size(-1))");
+  TORCH_CHECK(pre.is_cuda(), "pre must be a CUDA tensor");
+  check_f32(pre, "pre");
+  c10::OptionalDeviceGuard guard(dy.device());
+  const at::Tensor pd = pre.contiguous();
+  at::Tensor dx = at::empty({batch, m, n}, dy.options());
+  const auto ds = strides_of<3>(dy);
+  const auto wst = strides_of<3>(weights);
+  const int64_t ws_bytes = cta_cuda_fma_workspace(batch, m, k, n);
+  at::Tensor scratch;
+  if (ws_bytes > 0) scratch = at::empty({ws_bytes / 4}, dy.options());
+  check_rc(cta_cuda_fma_gelu_grad(dy.data_ptr<float>(), ds.data(), weights.data_ptr<float>(),
+                                  wst.data(), pd.data_ptr<float>(), batch, m, k, n,
+                                  weights.size(0), dx.data_ptr<float>(),
+                                  ws_bytes > 0 ? scratch.data_ptr<float>() : nullptr,
+                                  stream_of(dy)));
+  return dx;
 }
 
 // cf. linear_layer.cu:74-97
@@ -373,6 +440,8 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd(at::Tensor Q,
 TORCH_LIBRARY(cuda_transformer, m) {
   m.def("cuda_fma(Tensor x, Tensor weights, Tensor bias) -> Tensor");
   m.def("db_calculation(Tensor dy) -> Tensor");
+  m.def("cuda_fma_gelu(Tensor x, Tensor weights, Tensor bias) -> (Tensor, Tensor)");
+  m.def("cuda_fma_gelu_grad(Tensor dy, Tensor weights, Tensor pre) -> Tensor");
   m.def("gelu_activation(Tensor x) -> Tensor");
   m.def("gelu_activation_bwd(Tensor x, Tensor dy) -> Tensor");
   m.def("cuda_softmax(Tensor x) -> Tensor");
@@ -394,6 +463,8 @@ TORCH_LIBRARY(cuda_transformer, m) {
 TORCH_LIBRARY_IMPL(cuda_transformer, CUDA, m) {
   m.impl("cuda_fma", &cuda_fma);
   m.impl("db_calculation", &db_calculation);
+  m.impl("cuda_fma_gelu", &cuda_fma_gelu);
+  m.impl("cuda_fma_gelu_grad", &cuda_fma_gelu_grad);
   m.impl("gelu_activation", &gelu_activation);
   m.impl("gelu_activation_bwd", &gelu_activation_bwd);
   m.impl("cuda_softmax", &cuda_softmax);

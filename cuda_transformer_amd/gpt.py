@@ -18,7 +18,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .autograd_fns import (CudaFlashAttention, CudaGeluLayer, CudaLayerNorm, CudaLinearLayer)
+from .autograd_fns import (CudaFlashAttention, CudaGeluLayer, CudaLayerNorm, CudaLinearLayer,
+                           CudaMLP)
 
 
 @dataclass
@@ -31,6 +32,9 @@ class GPTConfig:
     mlp_ratio: int = 4
     eps: float = 1e-5
     init_std: float = 0.02
+    # MLP as one CudaMLP (GELU folded into the fc1 forward and fc2 dx GEMM epilogues; same
+    # bits) instead of the reference's CudaLinearLayer -> CudaGeluLayer -> CudaLinearLayer.
+    fused_mlp: bool = True
 
 
 class LayerNorm(nn.Module):
@@ -90,8 +94,12 @@ class MLP(nn.Module):
         self.fc2_bias = nn.Parameter(torch.zeros(d))
         nn.init.normal_(self.fc1_weights, mean=0.0, std=cfg.init_std)
         nn.init.normal_(self.fc2_weights, mean=0.0, std=cfg.init_std)
+        self.fused = cfg.fused_mlp
 
     def forward(self, x):
+        if self.fused:
+            return CudaMLP.apply(x, self.fc1_weights, self.fc1_bias, self.fc2_weights,
+                                 self.fc2_bias)
         x = CudaLinearLayer.apply(x, self.fc1_weights, self.fc1_bias)
         x = CudaGeluLayer.apply(x)
         return CudaLinearLayer.apply(x, self.fc2_weights, self.fc2_bias)

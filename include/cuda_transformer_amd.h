@@ -154,6 +154,28 @@ int cta_cuda_fma(const float* x, const int64_t* x_strides,
                  int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
                  float* out, float* workspace, void* stream);
 
+/* pre = x . W + bias and out = GELU(pre) (exact erf GELU) from one GEMM: the epilogue writes
+ * both, so the activation costs no second pass over pre.  Arguments as cta_cuda_fma; pre and
+ * out dense (batch, m, n), distinct; workspace sized by cta_cuda_fma_workspace().  Bitwise
+ * equal to cta_cuda_fma followed by cta_gelu_fwd.  No single reference counterpart: it fuses
+ * cuda_transformer::cuda_fma (linear_layer.cu:28-70) with gelu_activation
+ * (gelu_activation.cu:22-47) as the GPT MLP composes them (gpt/gpt.py:133-136). */
+int cta_cuda_fma_gelu(const float* x, const int64_t* x_strides,
+                      const float* w, const int64_t* w_strides,
+                      const float* bias, int64_t bias_stride,
+                      int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
+                      float* pre, float* out, float* workspace, void* stream);
+
+/* dx = (dy . W) * GELU'(pre), dx dense (batch, m, n); pre dense (batch, m, n), may alias dx.
+ * dy and W as x and W of cta_cuda_fma (the GPT MLP passes fc2's W^T view).  Bitwise equal to
+ * cta_cuda_fma with a zero bias followed by cta_gelu_bwd.  No single reference counterpart:
+ * it fuses the dx product of CudaLinearLayer.backward (cuda_autograd_fns/
+ * cuda_linear_layer.py:19-23) with gelu_activation_bwd (gelu_activation.cu:49-77). */
+int cta_cuda_fma_gelu_grad(const float* dy, const int64_t* dy_strides,
+                           const float* w, const int64_t* w_strides, const float* pre,
+                           int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
+                           float* dx, float* workspace, void* stream);
+
 /* Bytes of scratch cta_db_calculation needs for a (batch, m, n) gradient. */
 int64_t cta_db_calculation_workspace(int64_t batch, int64_t m, int64_t n);
 

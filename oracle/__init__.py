@@ -11,7 +11,9 @@ Pinning (tests/test_oracle.py, all CPU):
     float64 (the reference's own test oracle, test/test_flash_attention.py:10-50), the committed
     golden fixtures, closed forms (causal row 0, K = 0, constant V, T = 1), invariants
     (sum_j dK_j = 0, sum_j dV_j = sum_i dO_i) and central finite differences.
-  * linear — numpy matmul in float64, identity/one-hot closed forms, finite differences.
+  * linear — numpy matmul in float64, identity/one-hot closed forms, finite differences;
+    linear.mlp_forward / mlp_backward (fc1 -> GELU -> fc2) against torch float64 autograd and a
+    finite difference through both layers.
   * gelu — erf closed form at known points, finite differences for the gradient.
   * softmax — row sums, shift invariance, torch autograd, finite differences.
   * layernorm — torch.nn.functional.layer_norm + autograd, normalisation invariants.

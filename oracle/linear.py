@@ -33,3 +33,25 @@ def linear_backward(x, weights, dy):
     if w.ndim == 2:
         dw = dw.sum(axis=0)
     return dx, dw, db_calculation(dy)
+
+
+def mlp_forward(x, w1, b1, w2, b2):
+    """The GPT MLP, fc1 -> exact GELU -> fc2 (gpt/gpt.py:133-136).  Returns (pre, h, out):
+    fc1's pre-activation, its GELU and the fc2 output."""
+    from .elementwise import gelu_forward
+
+    pre = fma_forward(x, w1, b1)
+    h = gelu_forward(pre)
+    return pre, h, fma_forward(h, w2, b2)
+
+
+def mlp_backward(x, w1, w2, pre, h, dz):
+    """(dx, dW1, db1, dW2, db2): CudaLinearLayer.backward of fc2, CudaGeluLayer.backward and
+    CudaLinearLayer.backward of fc1 in turn (cuda_linear_layer.py:14-29,
+    cuda_gelu_layer.py:12-15)."""
+    from .elementwise import gelu_backward
+
+    dh, dw2, db2 = linear_backward(h, w2, dz)
+    dpre = gelu_backward(pre, dh)
+    dx, dw1, db1 = linear_backward(x, w1, dpre)
+    return dx, dw1, db1, dw2, db2

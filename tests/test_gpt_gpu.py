@@ -40,3 +40,26 @@ def test_gpt_training_steps_match_cpu_reference(cuda):
     # parameters stay close after 5 updates
     for (name, p), q in zip(model.named_parameters(), ref.parameters()):
         torch.testing.assert_close(p.detach().cpu(), q.detach(), rtol=1e-3, atol=1e-4, msg=name)
+
+
+def test_gpt_fused_mlp_matches_reference_composition(cuda):
+    """GPTConfig.fused_mlp (CudaMLP) against the reference's Linear -> GELU -> Linear modules:
+    the same loss and gradients, bit for bit (the embedding gradients, accumulated by torch's
+    own embedding backward, to FP32 rounding)."""
+    cfg = GPTConfig(n_layers=2)
+    idx, tgt = synthetic_batch(cfg, 8, seed=7)
+    runs = []
+    for fused in (True, False):
+        model = GPT(GPTConfig(n_layers=2, fused_mlp=fused))
+        init_weights_(model, seed=3)
+        model.to(cuda)
+        _, loss = model(idx.to(cuda), tgt.to(cuda))
+        loss.backward()
+        runs.append((loss.detach(), {n: p.grad for n, p in model.named_parameters()}))
+    (loss_f, g_f), (loss_u, g_u) = runs
+    assert torch.equal(loss_f, loss_u)
+    for name, g in g_f.items():
+        if "embedding" in name or "positional" in name:
+            torch.testing.assert_close(g, g_u[name], rtol=1e-6, atol=1e-7, msg=name)
+        else:
+            assert torch.equal(g, g_u[name]), name

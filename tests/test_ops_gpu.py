@@ -224,3 +224,101 @@ def test_db_strided_views(cuda):
     np.testing.assert_allclose(f64(db_calculation(big)), f64(big).sum(axis=(0, 1)), rtol=1e-5,
                                atol=1e-3)
     assert torch.equal(db_calculation(big), db_calculation(big))
+
+
+# ------------------------------------------------------------ fused linear + GELU (GPT MLP)
+# (batch, rows, d, hidden); the last shape has 1 output tile and K = 4096, so it runs split-K.
+FUSED_SHAPES = [(1, 32, 64, 96), (2, 33, 17, 65), (3, 70, 129, 257), (2, 256, 384, 1536),
+                (1, 64, 4096, 96)]
+
+
+@pytest.mark.parametrize("B,T,d,hid", FUSED_SHAPES)
+def test_fused_linear_gelu(cuda, B, T, d, hid):
+    """cuda_fma_gelu and cuda_fma_gelu_grad: the same bits as the unfused ops, and the oracle."""
+    from cuda_transformer.ops import (cuda_fma, cuda_fma_gelu, cuda_fma_gelu_grad,
+                                      gelu_activation, gelu_activation_bwd)
+
+    x = seeded((B, T, d), 50, kind="rand")
+    w1 = seeded((d, hid), 51) * 0.2
+    b1 = seeded((hid,), 52) * 0.2
+    w2 = seeded((hid, d), 53) * 0.2
+    dz = seeded((B, T, d), 54)
+    xc, w1c, b1c, w2c, dzc = (t.to(cuda) for t in (x, w1, b1, w2, dz))
+    pre, h = cuda_fma_gelu(xc, w1c, b1c)
+    assert torch.equal(pre, cuda_fma(xc, w1c, b1c))
+    assert torch.equal(h, gelu_activation(pre))
+    # FP32 sums of up to K = 4096 terms: relative error in norm, and a looser elementwise bound
+    pre_r, h_r, _ = lin.mlp_forward(f64(x), f64(w1), f64(b1), f64(w2), np.zeros(d))
+    w2t = w2c.unsqueeze(0).transpose(1, 2)
+    dpre = cuda_fma_gelu_grad(dzc, w2t, pre)
+    unfused = gelu_activation_bwd(pre, cuda_fma(dzc, w2t, torch.zeros(hid, device=cuda)))
+    assert torch.equal(dpre, unfused)
+    dpre_r = ew.gelu_backward(f64(pre), f64(dz) @ f64(w2).T)
+    for got, ref in ((pre, pre_r), (h, h_r), (dpre, dpre_r)):
+        assert rel_err(f64(got), ref) <= 1e-6
+        np.testing.assert_allclose(f64(got), ref, atol=1e-4, rtol=1e-4)
+
+
+def test_fused_linear_gelu_through_c_abi(cuda):
+    """The C entry points: both outputs, the in-place gradient (dx aliasing pre), the error on
+    pre == out."""
+    from cuda_transformer.ops import cuda_fma_gelu, cuda_fma_gelu_grad
+    from cuda_transformer_amd import capi
+
+    B, T, d, hid = 2, 40, 48, 80
+    x = seeded((B, T, d), 55).to(cuda)
+    w1 = seeded((d, hid), 56).to(cuda) * 0.2
+    b1 = seeded((hid,), 57).to(cuda)
+    w2t = (seeded((hid, d), 58).to(cuda) * 0.2).t()      # (d, hid) view, strides (1, d)
+    dz = seeded((B, T, d), 59).to(cuda)
+    stream = torch.cuda.current_stream().cuda_stream
+    pre = torch.empty(B, T, hid, device=cuda)
+    out = torch.empty_like(pre)
+    capi.call("cta_cuda_fma_gelu", x.data_ptr(), capi.strides(x.stride()), w1.data_ptr(),
+              capi.strides((0,) + w1.stride()), b1.data_ptr(), 1, B, T, d, hid, 1,
+              pre.data_ptr(), out.data_ptr(), None, stream)
+    dx = pre.clone()
+    capi.call("cta_cuda_fma_gelu_grad", dz.data_ptr(), capi.strides(dz.stride()), w2t.data_ptr(),
+              capi.strides((0,) + w2t.stride()), dx.data_ptr(), B, T, d, hid, 1, dx.data_ptr(),
+              None, stream)
+    torch.cuda.synchronize()
+    pre_t, out_t = cuda_fma_gelu(x, w1, b1)
+    assert torch.equal(pre, pre_t) and torch.equal(out, out_t)
+    assert torch.equal(dx, cuda_fma_gelu_grad(dz, w2t, pre_t))
+    with pytest.raises(capi.CtaError, match="distinct"):
+        capi.call("cta_cuda_fma_gelu", x.data_ptr(), capi.strides(x.stride()), w1.data_ptr(),
+                  capi.strides((0,) + w1.stride()), b1.data_ptr(), 1, B, T, d, hid, 1,
+                  pre.data_ptr(), pre.data_ptr(), None, stream)
+
+
+@pytest.mark.parametrize("B,T,d", [(2, 33, 48), (4, 256, 384)])
+def test_cuda_mlp_matches_composition(cuda, B, T, d):
+    """CudaMLP: output and all five gradients bitwise equal to CudaLinearLayer -> CudaGeluLayer
+    -> CudaLinearLayer, and within FP32 rounding of the oracle."""
+    from cuda_autograd_fns import CudaGeluLayer, CudaLinearLayer, CudaMLP
+
+    hid = 4 * d
+    params = [seeded(s, 60 + i) * 0.1 for i, s in enumerate([(d, hid), (hid,), (hid, d), (d,)])]
+    x = seeded((B, T, d), 66)
+    dz = seeded((B, T, d), 67)
+
+    def run(fused):
+        xg = x.to(cuda).requires_grad_()
+        ps = [p.to(cuda).requires_grad_() for p in params]
+        if fused:
+            out = CudaMLP.apply(xg, *ps)
+        else:
+            h = CudaGeluLayer.apply(CudaLinearLayer.apply(xg, ps[0], ps[1]))
+            out = CudaLinearLayer.apply(h, ps[2], ps[3])
+        out.backward(dz.to(cuda))
+        return [out.detach(), xg.grad] + [p.grad for p in ps]
+
+    fused, plain = run(True), run(False)
+    for a, b in zip(fused, plain):
+        assert torch.equal(a, b)
+    p64 = [f64(p) for p in params]
+    pre, h, out = lin.mlp_forward(f64(x), *p64)
+    grads = lin.mlp_backward(f64(x), p64[0], p64[2], pre, h, f64(dz))
+    assert rel_err(f64(fused[0]), out) <= 1e-5
+    for g, r in zip(fused[1:], grads):
+        assert rel_err(f64(g), r) <= 1e-5

@@ -265,6 +265,33 @@ def test_linear_closed_forms():
         assert abs(dw[idx] - fd) < 1e-6
 
 
+def test_mlp_matches_torch_autograd_and_finite_differences():
+    """fc1 -> GELU -> fc2 composition against torch float64 autograd (F.gelu, erf form) and a
+    finite difference through both layers."""
+    import torch
+    import torch.nn.functional as F
+
+    x = RNG.standard_normal((2, 7, 5))
+    w1, b1 = RNG.standard_normal((5, 12)), RNG.standard_normal(12)
+    w2, b2 = RNG.standard_normal((12, 5)), RNG.standard_normal(5)
+    dz = RNG.standard_normal((2, 7, 5))
+    pre, h, out = lin.mlp_forward(x, w1, b1, w2, b2)
+    grads = lin.mlp_backward(x, w1, w2, pre, h, dz)
+    ts = [torch.tensor(a, requires_grad=True) for a in (x, w1, b1, w2, b2)]
+    ref = F.gelu(ts[0] @ ts[1] + ts[2], approximate="none") @ ts[3] + ts[4]
+    ref.backward(torch.tensor(dz))
+    np.testing.assert_allclose(out, ref.detach().numpy(), rtol=1e-12, atol=1e-12)
+    for g, t in zip(grads, ts):
+        np.testing.assert_allclose(g, t.grad.numpy(), rtol=1e-11, atol=1e-11)
+    eps = 1e-6
+    w1p, w1m = w1.copy(), w1.copy()
+    w1p[3, 7] += eps
+    w1m[3, 7] -= eps
+    fd = ((lin.mlp_forward(x, w1p, b1, w2, b2)[2] - lin.mlp_forward(x, w1m, b1, w2, b2)[2])
+          * dz).sum() / (2 * eps)
+    assert abs(grads[1][3, 7] - fd) < 1e-6
+
+
 # ------------------------------------------------------------------ GELU
 def test_gelu_matches_golden_and_closed_forms():
     f = load("gelu_1x65x32")
