@@ -1,7 +1,8 @@
 // Bandwidth-bound kernels: exact GELU, row softmax, LayerNorm (forward and backward).
 //
 //  * GELU follows Transformer_kernels/GeLU.cuh:7-29: y = x Phi(x),
-//    dx = dy (Phi(x) + x phi(x)), phi(x) = e^{-x^2/2} / sqrt(2 pi), with HIP's normcdff/expf.
+//    dx = dy (Phi(x) + x phi(x)), phi(x) = e^{-x^2/2} / sqrt(2 pi); Phi from a Chebyshev-fitted
+//    erfc (cta_common.hpp), short enough that the kernels stay HBM-bound.
 //  * Softmax follows softmax.cuh:25-159 (row max, sum of e^{x - max}, normalise;
 //    backward dx = p (dp - sum p dp)).
 //  * LayerNorm has no kernel in the reference; its semantics come from gpt/gpt.py:47-59:
