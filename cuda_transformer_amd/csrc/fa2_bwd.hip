@@ -560,6 +560,10 @@ __global__ __launch_bounds__(256, 2) void fa2_bwd_dq_ds_kernel(
   const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
   const int n_stages = (kv_end + BN - 1) / BN;
 
+  // Every stage issues the same loads, unconditionally, from clamped in-bounds addresses, and
+  // the stage count is padded to even (padded stages compute nothing).  The compiler can then
+  // count the loads in flight exactly: the MFMAs of stage s wait only for stage s's dS, not
+  // for the stage s+1 loads issued ahead of them.
   float4 kst[LOADS];
   auto gload = [&](int stage) {
     const int j0 = stage * BN;
@@ -568,7 +572,8 @@ __global__ __launch_bounds__(256, 2) void fa2_bwd_dq_ds_kernel(
       const int f = tid + 256 * u;
       const int r = f / F4_ROW, c4 = f % F4_ROW;
       const int j = j0 + r;
-      kst[u] = j < T ? ld4(Kb + (int64_t)j * sk.t + 4 * c4) : zero4();
+      const float4 kv = ld4(Kb + (int64_t)min(j, T - 1) * sk.t + 4 * c4);
+      kst[u] = j < T ? kv : zero4();  // keys past T meet finite dS columns: K must be 0 there
     }
   };
   auto lstore = [&](int buf) {
@@ -583,18 +588,16 @@ __global__ __launch_bounds__(256, 2) void fa2_bwd_dq_ds_kernel(
   // A stored tile exists for query block ib and key block jb iff both lie inside the head and,
   // with a causal mask, jb <= ib (the wave-uniform skip of the dK/dV stage).
   auto has_tile = [&](int jb) { return ib < nb && jb < nb && (!CAUSAL || jb <= ib); };
+  // Tiles that do not exist are read from the row's last stored tile (clamped block indices,
+  // equal to (ib, jb) whenever has_tile(jb)); compute() skips them.
+  const int ibc = min(ib, nb - 1);
   auto dsload = [&](int stage, float4 (&dr)[NSUB][4]) {
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub) {
-      const int jb = stage * NSUB + sub;
-      if (has_tile(jb)) {
-        const float* src = dsh + ds_tile_index(ib, jb, nb, CAUSAL) * kDsTileFloats + 4 * lane;
+      const int jbc = min(stage * NSUB + sub, CAUSAL ? ibc : nb - 1);
+      const float* src = dsh + ds_tile_index(ibc, jbc, nb, CAUSAL) * kDsTileFloats + 4 * lane;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) dr[sub][g] = ld4(src + 256 * g);
-      } else {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) dr[sub][g] = zero4();
-      }
+      for (int g = 0; g < 4; ++g) dr[sub][g] = ld4(src + 256 * g);
     }
   };
   auto compute = [&](int stage, const float* ks, const float4 (&dr)[NSUB][4]) {
@@ -614,12 +617,10 @@ __global__ __launch_bounds__(256, 2) void fa2_bwd_dq_ds_kernel(
   };
   auto step = [&](int s, const float4 (&cur)[NSUB][4], float4 (&nxt)[NSUB][4]) {
     const int buf = s & 1;
-    if (s + 1 < n_stages) {
-      gload(s + 1);
-      dsload(s + 1, nxt);
-    }
+    gload(s + 1);
+    dsload(s + 1, nxt);
     compute(s, smem + buf * TILE, cur);
-    if (s + 1 < n_stages) lstore(buf ^ 1);
+    lstore(buf ^ 1);
     __syncthreads();
   };
 
@@ -629,9 +630,10 @@ __global__ __launch_bounds__(256, 2) void fa2_bwd_dq_ds_kernel(
   lstore(0);
   __syncthreads();
   // Unrolled by two so the two dS register sets swap roles without copies.
-  for (int s = 0; s < n_stages; s += 2) {
+  const int n_stages2 = (n_stages + 1) & ~1;
+  for (int s = 0; s < n_stages2; s += 2) {
     step(s, dA, dB);
-    if (s + 1 < n_stages) step(s + 1, dB, dA);
+    step(s + 1, dB, dA);
   }
 
   if (my_i < T) {
