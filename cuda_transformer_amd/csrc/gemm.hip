@@ -121,6 +121,73 @@ struct TileLoader {
   }
 };
 
+// The MFMAs of one K-slice: A rows [BM][KP] then B rows [BN][KP] in LDS at `as`.
+template <class TL>
+__device__ __forceinline__ void slice_mma(const float* as, f32x16 (&acc)[TL::MB][TL::NB], int wm,
+                                          int wn, int half, int col) {
+  constexpr int BM = TL::BM, BN = TL::BN, BK = TL::BK, KP = TL::KP;
+  constexpr int MB = TL::MB, NB = TL::NB, KC = BK / 8;  // KC: 16-byte chunks per lane half
+  const float* bs = as + BM * KP;
+  float4 af[MB][KC], bf[NB][KC];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    const float* ap = as + (wm * (BM / TL::WM) + i * 32 + col) * KP + half * (BK / 2);
+#pragma unroll
+    for (int c = 0; c < KC; ++c) af[i][c] = ld4(ap + 4 * c);
+  }
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const float* bp = bs + (wn * (BN / TL::WN) + j * 32 + col) * KP + half * (BK / 2);
+#pragma unroll
+    for (int c = 0; c < KC; ++c) bf[j][c] = ld4(bp + 4 * c);
+  }
+#pragma unroll
+  for (int c = 0; c < KC; ++c) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const float a = e == 0 ? af[i][c].x : e == 1 ? af[i][c].y : e == 2 ? af[i][c].z : af[i][c].w;
+          const float b = e == 0 ? bf[j][c].x : e == 1 ? bf[j][c].y : e == 2 ? bf[j][c].z : bf[j][c].w;
+          acc[i][j] = mfma32(a, b, acc[i][j]);
+        }
+  }
+}
+
+// The epilogue of one output tile (origin m0, n0 of batch (zo, zi)): alpha, bias, causal mask
+// and the pointwise stage ACT, stored through C.
+template <class TL, int ACT>
+__device__ __forceinline__ void tile_store(const f32x16 (&acc)[TL::MB][TL::NB], const GemmOut& C,
+                                           const GemmEpilogue& ep, int M, int N, int m0, int n0,
+                                           int zo, int zi, int wm, int wn, int half, int col) {
+  constexpr int BM = TL::BM, BN = TL::BN, MB = TL::MB, NB = TL::NB;
+  float* Cb = C.p + zo * C.s_outer + zi * C.s_inner;
+  float* Xb = ep.aux ? ep.aux + zo * C.s_outer + zi * C.s_inner : nullptr;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int n = n0 + wn * (BN / TL::WN) + j * 32 + col;
+    if (n >= N) continue;
+    const float bv = ep.bias ? ep.bias[(int64_t)n * ep.bias_stride] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * (BM / TL::WM) + i * 32 + mfma_row(r, half);
+        if (m < M) {
+          float val = fmaf(ep.alpha, acc[i][j][r], bv);
+          if (ep.causal_mask && n > m) val = -INFINITY;
+          const int64_t off = (int64_t)m * C.s_row + n;
+          if (ACT == kActGeluGrad) val = gelu_grad(Xb[off], val);
+          Cb[off] = val;
+          if (ACT == kActGelu) Xb[off] = gelu_f(val);
+        }
+      }
+    }
+  }
+}
+
 // split_ws == nullptr: out = alpha * A B (+ bias, mask) written through C.
 // split_ws != nullptr: blockIdx.z = s * Z + z covers K range [s*kchunk, (s+1)*kchunk) and the raw
 // partial sum goes to split_ws[s][z][m][n] (dense); gemm_splitk_reduce finishes the epilogue.
@@ -131,7 +198,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
                                                            int kchunk,
                                                            float* __restrict__ split_ws) {
   constexpr int BM = TL::BM, BN = TL::BN, BK = TL::BK, KP = TL::KP;
-  constexpr int MB = TL::MB, NB = TL::NB, KC = BK / 8;  // KC: 16-byte chunks per lane half
+  constexpr int MB = TL::MB, NB = TL::NB;
   __shared__ __attribute__((aligned(16))) float smem[TL::LDS_FLOATS];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -175,35 +242,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
   lb0.store(smem + BM * KP, tid);
   __syncthreads();
 
-  auto mma = [&](const float* as) {
-    const float* bs = as + BM * KP;
-    float4 af[MB][KC], bf[NB][KC];
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-      const float* ap = as + (wm * (BM / TL::WM) + i * 32 + col) * KP + half * (BK / 2);
-#pragma unroll
-      for (int c = 0; c < KC; ++c) af[i][c] = ld4(ap + 4 * c);
-    }
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const float* bp = bs + (wn * (BN / TL::WN) + j * 32 + col) * KP + half * (BK / 2);
-#pragma unroll
-      for (int c = 0; c < KC; ++c) bf[j][c] = ld4(bp + 4 * c);
-    }
-#pragma unroll
-    for (int c = 0; c < KC; ++c) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-#pragma unroll
-          for (int j = 0; j < NB; ++j) {
-            const float a = e == 0 ? af[i][c].x : e == 1 ? af[i][c].y : e == 2 ? af[i][c].z : af[i][c].w;
-            const float b = e == 0 ? bf[j][c].x : e == 1 ? bf[j][c].y : e == 2 ? bf[j][c].z : bf[j][c].w;
-            acc[i][j] = mfma32(a, b, acc[i][j]);
-          }
-    }
-  };
+  auto mma = [&](const float* as) { slice_mma<TL>(as, acc, wm, wn, half, col); };
   float* const buf0 = smem;
   float* const buf1 = smem + (BM + BN) * KP;
   for (int t = 0; t < nk2; t += 2) {
@@ -241,29 +280,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
     }
     return;
   }
-  float* Cb = C.p + zo * C.s_outer + zi * C.s_inner;
-  float* Xb = ep.aux ? ep.aux + zo * C.s_outer + zi * C.s_inner : nullptr;
-#pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    const int n = n0 + wn * (BN / TL::WN) + j * 32 + col;
-    if (n >= N) continue;
-    const float bv = ep.bias ? ep.bias[(int64_t)n * ep.bias_stride] : 0.0f;
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * (BM / TL::WM) + i * 32 + mfma_row(r, half);
-        if (m < M) {
-          float val = fmaf(ep.alpha, acc[i][j][r], bv);
-          if (ep.causal_mask && n > m) val = -INFINITY;
-          const int64_t off = (int64_t)m * C.s_row + n;
-          if (ACT == kActGeluGrad) val = gelu_grad(Xb[off], val);
-          Cb[off] = val;
-          if (ACT == kActGelu) Xb[off] = gelu_f(val);
-        }
-      }
-    }
-  }
+  tile_store<TL, ACT>(acc, C, ep, M, N, m0, n0, zo, zi, wm, wn, half, col);
 }
 
 // Fixed-order sum of the split-K partials plus the epilogue of gemm_kernel.
