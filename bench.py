@@ -19,6 +19,10 @@ Reported:
                  committed rocprofv3 counter summary profiles/fa2_config2_counters.md.
   cpu_baseline   the CPU oracle (numpy port of the reference algorithm, float32) timed on this
                  host's cores on a bounded sample of whole heads of the same workload.
+  cpu_reference_path
+                 the reference's own CPU comparison path, torch FP32 SDPA forward + autograd
+                 backward, timed on the same host cores on 16 whole heads, with the backend torch
+                 chose and the estimated time of the full step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -152,6 +156,55 @@ def cpu_baseline(B, H, N, D, causal, target_s):
                    f"fwd+bwd, float32 numpy oracle (oracle/attention.py), 512x512 tiles, "
                    f"{elapsed:.1f} s on {threads} BLAS threads"),
         "seconds": elapsed,
+    }
+
+
+def cpu_reference_path(B, H, N, D, causal, heads=16):
+    """The reference's own CPU path, as its test suite and benchmark define correctness and the
+    comparison point (test/test_flash_attention.py:10-21, benchmark/cuda_bench.py:44-68): torch
+    FP32 scaled_dot_product_attention forward + autograd backward on this host's cores, on
+    `heads` whole heads of the workload.  One warm-up step, then the median of three."""
+    import statistics
+
+    import torch
+    import torch.nn.functional as F
+
+    threads = min(16, os.cpu_count() or 1)  # the GPU box's CPU share is 16 cores
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        heads = min(heads, B * H)
+        gen = torch.Generator().manual_seed(0)
+        q, k, v = (torch.randn(1, heads, N, D, generator=gen).requires_grad_() for _ in range(3))
+        do = torch.randn(1, heads, N, D, generator=torch.Generator().manual_seed(1))
+        backend = torch.nn.attention.SDPBackend(torch._fused_sdp_choice(q, k, v, is_causal=causal))
+
+        def step():
+            o = F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+            o.backward(do)
+            q.grad = k.grad = v.grad = None
+
+        step()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            step()
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+    finally:
+        torch.set_num_threads(prev)
+    fwd, bwd = attn_flops(1, heads, N, D, causal)
+    return {
+        "value": (fwd + bwd) / med / 1e12,
+        "unit": "TFLOPS",
+        "cores": threads,
+        "cpu_count": os.cpu_count(),
+        "kind": "torch-sdpa",
+        "backend": backend.name,
+        "sample": (f"{heads} of {B * H} heads (N={N}, D={D}, {'causal' if causal else 'full'}), "
+                   f"torch {torch.__version__} F.scaled_dot_product_attention + backward, FP32, "
+                   f"{threads} threads, median of 3 steps of {med:.3f} s"),
+        "est_ms_per_full_step": round(med * 1e3 * B * H / heads, 1),
     }
 
 
@@ -626,6 +679,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(B, H, N, D, causal, args.cpu_seconds)
+        line["cpu_reference_path"] = cpu_reference_path(B, H, N, D, causal)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

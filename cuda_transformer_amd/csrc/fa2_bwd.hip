@@ -391,14 +391,23 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
     }
   };
 
-  if (q_begin < n_stages) issue(q_begin, 0);
+  // Stage order.  With a causal mask the first (long) pass walks its query stages downward
+  // from the last and the second (short) pass upward from its first, so every workgroup of a
+  // head in its first pass reads query stage n-1-t at step t and every one in its second pass
+  // reads stage t - 4 (t counted from the item's start): the workgroups of a head share each
+  // streamed Q / dO stage in L2 instead of each reading it at a different time.
+  const int n_steps = n_stages - q_begin;
+  const bool down = CAUSAL && pass == 0;
+  auto stage_at = [&](int i) { return down ? n_stages - 1 - i : q_begin + i; };
+  if (n_steps > 0) issue(stage_at(0), 0);
   vm_wait_all();
   __syncthreads();
 
-  for (int s = q_begin; s < n_stages; ++s) {
-    const int buf = (s - q_begin) & 1;
-    if (s + 1 < n_stages) issue(s + 1, buf ^ 1);
-    if (wave_stores && s > q_begin) flush(s - 1);
+  for (int i = 0; i < n_steps; ++i) {
+    const int s = stage_at(i);
+    const int buf = i & 1;
+    if (i + 1 < n_steps) issue(stage_at(i + 1), buf ^ 1);
+    if (wave_stores && i > 0) flush(stage_at(i - 1));
     const float* qs = smem + buf * STAGE;
     const float* gs = qs + TILE;
     const float* ls = qs + QG;
@@ -488,7 +497,7 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
     vm_wait_all();
     __syncthreads();
   }
-  if (wave_stores && n_stages > q_begin) flush(n_stages - 1);
+  if (wave_stores && n_steps > 0) flush(stage_at(n_steps - 1));
 
   if (my_j < T) {
     float* kp = dK + ((int64_t)bh * T + my_j) * HS;

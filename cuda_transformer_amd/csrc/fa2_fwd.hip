@@ -130,13 +130,20 @@ __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
     }
   };
 
-  gload(0);
+  // Stage order.  With a causal mask the second (short) pass walks the K/V stages downward
+  // from its last: every workgroup of a head in its first pass reads stage t at step t, and
+  // every one in its second pass reads stage 4n+3-t (n query tiles; t counted from the item's
+  // start), so the workgroups of a head share each K/V stage in L2.
+  const bool down = CAUSAL && pass == 1;
+  auto stage_at = [&](int i) { return down ? n_stages - 1 - i : i; };
+  gload(stage_at(0));
   lstore(0);
   __syncthreads();
 
-  for (int s = 0; s < n_stages; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < n_stages) gload(s + 1);
+  for (int i = 0; i < n_stages; ++i) {
+    const int s = stage_at(i);
+    const int buf = i & 1;
+    if (i + 1 < n_stages) gload(stage_at(i + 1));
     const float* ks = smem + buf * (KTILE + VTILE);
     const float* vs = ks + KTILE;
 
@@ -201,7 +208,7 @@ __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
       }
     }
 
-    if (s + 1 < n_stages) lstore(buf ^ 1);
+    if (i + 1 < n_stages) lstore(buf ^ 1);
     __syncthreads();
   }
 
