@@ -41,6 +41,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense
 HBM_PEAK_GBPS = 8000.0
 METRIC = "FA2 fwd+bwd FP32 TFLOPS @B4 H32 N4096 D64 causal; % of FP32 MFMA peak"
 # The reference's own numbers for this exact configuration (RTX 5070, README.md:60-67,197):
@@ -51,10 +52,12 @@ REFERENCE_RTX5070_MS = {"fwd": 212.73, "bwd": 1259.32}
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--workload", choices=["fa2", "fa2-sweep", "ops", "gpt"], default="fa2",
+    p.add_argument("--workload", choices=["fa2", "fa2-sweep", "ops", "gpt", "fa2-bf16"],
+                   default="fa2",
                    help="fa2: the headline step (default, one JSON line); fa2-sweep: benchmark "
                         "config 3; ops: benchmark config 4 (one JSON line per op); gpt: benchmark "
-                        "config 5 training step")
+                        "config 5 training step; fa2-bf16: the BF16 forward at the config-2 "
+                        "shape, causal and full (an extension beyond the FP32 metric)")
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--batch", type=int, default=4)
@@ -323,6 +326,45 @@ def fa2_sweep(args):
             "per_kernel_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
         }), flush=True)
         torch.cuda.empty_cache()
+    return 0
+
+
+def fa2_bf16_workload(args):
+    """The BF16 FlashAttention-2 forward (cta_flash_attention_fwd_bf16) at the config-2 shape,
+    causal and non-causal: HIP-event time per launch on torch's current stream with inputs in
+    HBM, TFLOPS by the reference's formula (4*B*H*N^2*D, halved when causal) and the fraction
+    of the 2.5 PFLOP/s dense BF16 MFMA peak.  One JSON line per mask."""
+    import torch
+
+    from cuda_transformer_amd import capi
+
+    B, H, N, D = args.batch, args.heads, args.seq, args.head_dim
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(B, H, N, D, generator=gen).to(torch.bfloat16).to(dev) for _ in range(3))
+    O = torch.empty_like(q)
+    L = torch.empty(B, H, N, device=dev)
+    lib = capi.lib()
+    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    s4 = capi.strides(q.stride())
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    for causal in (True, False):
+        def fwd():
+            rc = lib.cta_flash_attention_fwd_bf16(vp(q), s4, vp(k), s4, vp(v), s4, B, H, N, D,
+                                                  int(causal), vp(O), vp(L), st)
+            if rc != 0:
+                raise RuntimeError(lib.cta_last_error().decode())
+        ms = _time_kernel(fwd, max(10, args.steps), warm_s=0.2)
+        fl, _ = attn_flops(B, H, N, D, causal)
+        tf = fl / (ms * 1e-3) / 1e12
+        print(json.dumps({
+            "workload": f"FA2 forward BF16 B{B} H{H} N{N} D{D} {'causal' if causal else 'non-causal'}",
+            "metric": "FA2 BF16 forward TFLOPS", "value": round(tf, 2), "unit": "TFLOPS",
+            "ms": round(ms, 4), "dtype": "bf16 inputs, fp32 accumulation",
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                         "algorithmic_per_launch": fl},
+        }), flush=True)
     return 0
 
 
@@ -606,6 +648,8 @@ def main():
         return fa2_sweep(args)
     if args.workload == "gpt":
         return gpt_workload(args)
+    if args.workload == "fa2-bf16":
+        return fa2_bf16_workload(args)
     B, H, N, D = args.batch, args.heads, args.seq, args.head_dim
     causal = not args.non_causal
     ms_step, per_kernel, (q, k, v, do) = fa2_timings(B, H, N, D, causal, args.steps, args.warmup,

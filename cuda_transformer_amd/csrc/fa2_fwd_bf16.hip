@@ -1,0 +1,284 @@
+// FlashAttention-2 forward with BF16 Q, K, V and FP32 accumulation, CDNA4 MFMA
+// (v_mfma_f32_32x32x16_bf16).
+//
+// The reduced-precision variant the reference lists on its roadmap (README.md:277); the
+// semantics are those of the FP32 forward (Transformer_kernels/flash_attention.cuh:27-170):
+// O = softmax(s Q K^T) V with s = 1/sqrt(hs), the causal mask j > i, and L = m + ln l in FP32.
+// O is written in BF16, L in FP32.  Scores, the online-softmax statistics and the O
+// accumulator are FP32; the probabilities are rounded to BF16 as the P V operand, as in every
+// BF16 FlashAttention.
+//
+// gfx950 design (the FP32 kernel's layout trick carried to the 16-deep BF16 MFMA):
+//  * Workgroup = 128 query rows (4 waves x 32), K/V stages of 64 keys (two 32-key tiles),
+//    global -> registers -> LDS, double buffered, one barrier per stage.  Causal workgroups
+//    take query-tile pairs (n-1-p, p), head-major and XCD-contiguous, and the second pass walks
+//    its stages downward, exactly as the FP32 forward.
+//  * S^T = K Q^T: lane l supplies K[key l%32][8 (l/32) + 16 s + 0..7] (one 16-byte LDS read of
+//    a [key][d] image) and its own query row's q values from registers.  The 32x32 output puts
+//    one query per lane: lane l holds the scores of query l%32 for keys R(r, l/32),
+//    R(r, h) = 8 (r/4) + 4 h + r%4.
+//  * O^T += V^T P^T: for MFMA step s the B operand is the lane's registers r = 8s .. 8s+7,
+//    rounded to BF16, i.e. keys 16 s + 8 (j/4) + 4 h + j%4 for element j.  V is stored in LDS
+//    transposed, [d][key], with bits 2 and 3 of the key index swapped inside each 16-key
+//    group, so those eight keys are adjacent and the A operand is one 16-byte read.
+//  * Online softmax, lazy rescaling and the two-half max / sum exchange are the FP32 kernel's.
+#include "cta_common.hpp"
+
+namespace cta {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+struct RowStridesB {
+  int64_t b, h, t;  // element strides of the batch, head and time axes (d-stride is 1)
+};
+
+__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Position of key k (0..63 of a stage) in a V^T row: bits 2 and 3 swapped.
+__device__ __forceinline__ constexpr int vt_pos(int k) {
+  return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
+template <int HS, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
+    const __bf16* __restrict__ Q, const __bf16* __restrict__ K, const __bf16* __restrict__ V,
+    __bf16* __restrict__ O, float* __restrict__ L, int nh, int T, int BH, int n_qtiles,
+    RowStridesB sq, RowStridesB sk, RowStridesB sv, float scale, float scale_log2,
+    float rescale_gap) {
+  constexpr int BN = 64;             // keys per stage
+  constexpr int NSUB = BN / 32;      // 32-key score tiles per stage
+  constexpr int BM = 128;
+  constexpr int KP = HS + 8;         // bf16 pitch of a K row: conflict-free 16-byte row reads
+  constexpr int VP = BN + 8;         // bf16 pitch of a V^T row (one d, every key of the stage)
+  constexpr int KTILE = BN * KP;
+  constexpr int VTILE = HS * VP;
+  constexpr int CH = HS / 8;         // 16-byte chunks per K / V row
+  constexpr int LOADS = BN * CH / 256;
+  constexpr int QS = HS / 16;        // MFMA steps of S over d
+  static_assert(BN * CH % 256 == 0, "stage must split evenly over 256 threads");
+  __shared__ __attribute__((aligned(16))) __bf16 smem[2 * (KTILE + VTILE)];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, col = lane & 31;
+  const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+  const int w = xcd_work_item(blockIdx.x, BH * per_head);
+  if (w >= BH * per_head) return;
+  const int bh = w / per_head;
+  const int p = w - bh * per_head;
+  const int b = bh / nh, h = bh - b * nh;
+
+  const __bf16* Qb = Q + b * sq.b + h * sq.h;
+  const __bf16* Kb = K + b * sk.b + h * sk.h;
+  const __bf16* Vb = V + b * sv.b + h * sv.h;
+
+  const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
+  for (int pass = 0; pass < n_pass; ++pass) {
+  const int qt = CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p;
+  const int i0 = qt * BM + wave * 32;
+  const int my_i = i0 + col;
+
+  // This lane's query row, d = 16 s + 8 half + 0..7 for step s.
+  bf16x8 qf[QS];
+  if (my_i < T) {
+    const __bf16* qp = Qb + (int64_t)my_i * sq.t + 8 * half;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qp + 16 * s);
+  } else {
+#pragma unroll
+    for (int s = 0; s < QS; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qf[s][j] = (__bf16)0.0f;
+  }
+
+  f32x16 oacc[HS / 32];
+#pragma unroll
+  for (int d = 0; d < HS / 32; ++d) oacc[d] = zero16();
+  float m_run = -INFINITY;  // exponent offset of row my_i (raw q.k units), lazily updated
+  float l_run = 0.0f;       // this lane's partial row sum
+
+  const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
+  const int n_stages = (kv_end + BN - 1) / BN;
+
+  uint4 kst[LOADS], vst[LOADS];
+  auto gload = [&](int stage) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int c = tid + 256 * u;
+      const int r = c / CH, ch = c % CH;
+      const int j = stage * BN + r;
+      if (j < T) {
+        kst[u] = *reinterpret_cast<const uint4*>(Kb + (int64_t)j * sk.t + 8 * ch);
+        vst[u] = *reinterpret_cast<const uint4*>(Vb + (int64_t)j * sv.t + 8 * ch);
+      } else {
+        kst[u] = make_uint4(0, 0, 0, 0);
+        vst[u] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+    __bf16* ks = smem + buf * (KTILE + VTILE);
+    __bf16* vt = ks + KTILE;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int c = tid + 256 * u;
+      const int r = c / CH, ch = c % CH;
+      *reinterpret_cast<uint4*>(ks + r * KP + 8 * ch) = kst[u];
+      const __bf16* e = reinterpret_cast<const __bf16*>(&vst[u]);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) vt[(8 * ch + t) * VP + vt_pos(r)] = e[t];
+    }
+  };
+
+  const bool down = CAUSAL && pass == 1;
+  auto stage_at = [&](int i) { return down ? n_stages - 1 - i : i; };
+  gload(stage_at(0));
+  lstore(0);
+  __syncthreads();
+
+  for (int i = 0; i < n_stages; ++i) {
+    const int s_idx = stage_at(i);
+    const int buf = i & 1;
+    if (i + 1 < n_stages) gload(stage_at(i + 1));
+    const __bf16* ks = smem + buf * (KTILE + VTILE);
+    const __bf16* vt = ks + KTILE;
+
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub) {
+      const int jj0 = s_idx * BN + sub * 32;
+      if (jj0 >= T) continue;                 // ragged tail
+      if (CAUSAL && jj0 > i0 + 31) continue;  // tile entirely above this wave's diagonal
+
+      // S^T tile: sacc[r] = q_{my_i} . k_{jj0 + R(r, half)}
+      f32x16 sacc = zero16();
+      const __bf16* krow = ks + (sub * 32 + col) * KP + 8 * half;
+#pragma unroll
+      for (int s = 0; s < QS; ++s)
+        sacc = mfma_bf16(*reinterpret_cast<const bf16x8*>(krow + 16 * s), qf[s], sacc);
+
+      const bool need_mask = (CAUSAL && jj0 + 31 > i0) || (jj0 + 32 > T);
+      if (need_mask) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = jj0 + mfma_row(r, half);
+          if ((CAUSAL && j > my_i) || j >= T) sacc[r] = -INFINITY;
+        }
+      }
+
+      float mt = sacc[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sacc[r]);
+      mt = max_halves(mt);
+      if (__any(mt > m_run + rescale_gap)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = fast_exp2((m_run - m_new) * scale_log2);
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < HS / 32; ++d) oacc[d] *= alpha;
+        m_run = m_new;
+      }
+      const float mb = m_run * scale_log2;
+      float psum = 0.0f;
+      bf16x8 pf[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = fast_exp2(fmaf(sacc[r], scale_log2, -mb));
+        psum += pr;
+        pf[r >> 3][r & 7] = (__bf16)pr;
+      }
+      l_run += psum;
+
+      // O^T += V^T P^T over the tile's 32 keys, two 16-key MFMA steps per d block.
+#pragma unroll
+      for (int d = 0; d < HS / 32; ++d) {
+        const __bf16* vrow = vt + (d * 32 + col) * VP + sub * 32 + 8 * half;
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          oacc[d] = mfma_bf16(*reinterpret_cast<const bf16x8*>(vrow + 16 * s), pf[s], oacc[d]);
+      }
+    }
+
+    if (i + 1 < n_stages) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  const float l_tot = sum_halves(l_run);
+  if (my_i < T) {
+    __bf16* op = O + ((int64_t)bh * T + my_i) * HS;
+    const float inv = 1.0f / l_tot;
+#pragma unroll
+    for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        __bf16 o4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(oacc[d][4 * g + e] * inv);
+        *reinterpret_cast<uint2*>(op + d * 32 + 8 * g + 4 * half) =
+            *reinterpret_cast<const uint2*>(o4);
+      }
+    }
+    if (half == 0) L[(int64_t)bh * T + my_i] = m_run * scale + logf(l_tot);
+  }
+  }  // pass: the K/V loop ended on a barrier, so the next pass may refill LDS
+}
+
+template <int HS, bool CAUSAL>
+void launch_fwd_bf16(const __bf16* q, const __bf16* k, const __bf16* v, __bf16* o, float* l,
+                     int nh, int T, int BH, RowStridesB sq, RowStridesB sk, RowStridesB sv,
+                     float scale, hipStream_t stream) {
+  const int n_qtiles = (T + 127) / 128;
+  const unsigned grid = xcd_grid((int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH);
+  hipLaunchKernelGGL((fa2_fwd_bf16_kernel<HS, CAUSAL>), dim3(grid), dim3(256), 0, stream, q, k,
+                     v, o, l, nh, T, BH, n_qtiles, sq, sk, sv, scale, scale * kLog2e,
+                     8.0f / (scale * kLog2e));
+}
+
+// BF16 operands: unit d-stride, (b, h, t) strides divisible by 8 elements, 16-byte aligned.
+bool attn_layout_bf16_ok(const void* p, const int64_t* s) {
+  return p != nullptr && s != nullptr && aligned16(p) && s[3] == 1 && s[0] % 8 == 0 &&
+         s[1] % 8 == 0 && s[2] % 8 == 0;
+}
+
+}  // namespace
+}  // namespace cta
+
+using namespace cta;
+
+extern "C" int cta_flash_attention_fwd_bf16(const uint16_t* q, const int64_t* q_strides,
+                                            const uint16_t* k, const int64_t* k_strides,
+                                            const uint16_t* v, const int64_t* v_strides,
+                                            int64_t B, int64_t nh, int64_t T, int64_t hs,
+                                            int causal, uint16_t* o, float* l, void* stream) {
+  if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
+  if (hs == 32)
+    return fail(CTA_ERR_UNSUPPORTED_HEAD_DIM,
+                "flash_attention_fwd with bfloat16 inputs supports hs=64 and hs=128");
+  if (B * nh * T == 0) return CTA_OK;
+  if (!o || !l) return fail(CTA_ERR_INVALID_ARGUMENT, "null output pointer");
+  if (!attn_layout_bf16_ok(q, q_strides) || !attn_layout_bf16_ok(k, k_strides) ||
+      !attn_layout_bf16_ok(v, v_strides) || !aligned16(o))
+    return fail(CTA_ERR_LAYOUT,
+                "flash_attention_fwd (bfloat16) needs unit d-stride, strides divisible by 8 and "
+                "16-byte aligned Q/K/V/O");
+  const RowStridesB sq{q_strides[0], q_strides[1], q_strides[2]};
+  const RowStridesB sk{k_strides[0], k_strides[1], k_strides[2]};
+  const RowStridesB sv{v_strides[0], v_strides[1], v_strides[2]};
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  const int BH = (int)(B * nh);
+  hipStream_t st = as_stream(stream);
+  const auto* qb = reinterpret_cast<const __bf16*>(q);
+  const auto* kb = reinterpret_cast<const __bf16*>(k);
+  const auto* vb = reinterpret_cast<const __bf16*>(v);
+  auto* ob = reinterpret_cast<__bf16*>(o);
+#define CTA_FWD_BF16(HS_)                                                                     \
+  if (causal) launch_fwd_bf16<HS_, true>(qb, kb, vb, ob, l, (int)nh, (int)T, BH, sq, sk, sv,  \
+                                         scale, st);                                          \
+  else launch_fwd_bf16<HS_, false>(qb, kb, vb, ob, l, (int)nh, (int)T, BH, sq, sk, sv, scale, st);
+  if (hs == 64) { CTA_FWD_BF16(64) }
+  else { CTA_FWD_BF16(128) }
+#undef CTA_FWD_BF16
+  return check_launch("flash_attention_fwd_bf16");
+}

@@ -355,6 +355,41 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> causal_self_attention_bwd(
 }
 
 // ------------------------------------------------------------------ FlashAttention-2
+// BF16 inputs (an extension: the reference's kernels are FP32 only): O in BF16, L in FP32.
+bool attn_layout_bf16_ok(const at::Tensor& t) {
+  const auto s = strides_of<4>(t);
+  return (t.size(3) == 1 || t.stride(3) == 1) && s[0] % 8 == 0 && s[1] % 8 == 0 &&
+         s[2] % 8 == 0 && (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) == 0;
+}
+
+at::Tensor attn_operand_bf16(const at::Tensor& t) {
+  if (attn_layout_bf16_ok(t)) return t;
+  at::Tensor c = t.contiguous();
+  if (!attn_layout_bf16_ok(c)) c = t.clone(at::MemoryFormat::Contiguous);
+  return c;
+}
+
+std::tuple<at::Tensor, at::Tensor> flash_attention_fwd_bf16(const at::Tensor& Q,
+                                                            const at::Tensor& K,
+                                                            const at::Tensor& V, bool causal) {
+  const int64_t B = Q.size(0), nh = Q.size(1), T = Q.size(2), hs = Q.size(3);
+  TORCH_CHECK(K.scalar_type() == at::kBFloat16 && V.scalar_type() == at::kBFloat16,
+              "Q, K and V must all be bfloat16 (or all float32)");
+  TORCH_CHECK(hs == 64 || hs == 128,
+              "Unsupported head dimension for bfloat16! Only hs=64 and hs=128 are supported.");
+  c10::OptionalDeviceGuard guard(Q.device());
+  at::Tensor O = at::empty({B, nh, T, hs}, Q.options());
+  at::Tensor L = at::empty({B, nh, T}, Q.options().dtype(at::kFloat));
+  const at::Tensor q = attn_operand_bf16(Q), k = attn_operand_bf16(K), v = attn_operand_bf16(V);
+  const auto qs = strides_of<4>(q), ks = strides_of<4>(k), vs = strides_of<4>(v);
+  check_rc(cta_flash_attention_fwd_bf16(
+      reinterpret_cast<const uint16_t*>(q.data_ptr()), qs.data(),
+      reinterpret_cast<const uint16_t*>(k.data_ptr()), ks.data(),
+      reinterpret_cast<const uint16_t*>(v.data_ptr()), vs.data(), B, nh, T, hs, causal ? 1 : 0,
+      reinterpret_cast<uint16_t*>(O.data_ptr()), L.data_ptr<float>(), stream_of(Q)));
+  return {O, L};
+}
+
 // cf. Transformer_launchers/flash_attn_launcher.cu:22-65
 std::tuple<at::Tensor, at::Tensor> flash_attention_fwd(at::Tensor Q, at::Tensor K, at::Tensor V,
                                                        bool causal) {
@@ -363,10 +398,11 @@ std::tuple<at::Tensor, at::Tensor> flash_attention_fwd(at::Tensor Q, at::Tensor 
   TORCH_CHECK(Q.is_cuda(), "Q must be a CUDA tensor");
   TORCH_CHECK(K.is_cuda(), "K must be a CUDA tensor");
   TORCH_CHECK(V.is_cuda(), "V must be a CUDA tensor");
+  TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes(), "Q, K and V must have the same shape");
+  if (Q.scalar_type() == at::kBFloat16) return flash_attention_fwd_bf16(Q, K, V, causal);
   check_f32(Q, "Q");
   check_f32(K, "K");
   check_f32(V, "V");
-  TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes(), "Q, K and V must have the same shape");
   c10::OptionalDeviceGuard guard(Q.device());
   at::Tensor O = at::empty({B, nh, T, hs}, Q.options());
   at::Tensor L = at::empty({B, nh, T}, Q.options());

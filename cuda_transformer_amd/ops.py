@@ -171,16 +171,23 @@ def _(Q, K, V, probs, dO):
 
 # ----------------------------------------------------------------- FlashAttention-2
 def flash_attention_fwd(Q: Tensor, K: Tensor, V: Tensor, causal: bool) -> tuple[Tensor, Tensor]:
-    """FA2 forward -> (O, L), L = rowmax + ln(rowsum)  (reference ops.py:109-111)."""
+    """FA2 forward -> (O, L), L = rowmax + ln(rowsum)  (reference ops.py:109-111).
+
+    Extension: bfloat16 Q, K, V (hs 64 or 128) run the BF16 kernel, which returns O in
+    bfloat16 and L in float32; the reference's kernels are float32 only."""
     return _ops.flash_attention_fwd.default(Q, K, V, causal)
 
 
 @torch.library.register_fake("cuda_transformer::flash_attention_fwd")
 def _(Q, K, V, causal):
-    _f32(Q, K, V)
+    if Q.dtype == torch.bfloat16:
+        torch._check(K.dtype == torch.bfloat16 and V.dtype == torch.bfloat16,
+                     lambda: "Q, K and V must all be bfloat16 (or all float32)")
+    else:
+        _f32(Q, K, V)
     _same_device(Q, K, V)
     O = torch.empty((Q.size(0), Q.size(1), Q.size(2), Q.size(3)), dtype=Q.dtype, device=Q.device)
-    L = torch.empty((Q.size(0), Q.size(1), Q.size(2)), dtype=Q.dtype, device=Q.device)
+    L = torch.empty((Q.size(0), Q.size(1), Q.size(2)), dtype=torch.float32, device=Q.device)
     return O, L
 
 

@@ -59,6 +59,19 @@ int cta_flash_attention_fwd(const float* q, const int64_t* q_strides,
                             int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
                             float* o, float* l, void* stream);
 
+/* Forward with BF16 Q, K, V (stored as uint16_t bit patterns) and FP32 accumulation: O dense
+ * (B,nh,T,hs) in BF16, L dense (B,nh,T) in FP32, L = rowmax + ln(rowsum) as above.  hs in
+ * {64, 128}.  Q/K/V strides: unit d-stride, other strides divisible by 8, 16-byte aligned
+ * base pointers (CTA_ERR_LAYOUT otherwise).  The probabilities are rounded to BF16 as the
+ * P.V operand.  No counterpart in the reference's launchers: its roadmap lists reduced
+ * precision (README.md:277); the semantics are those of flash_attention_fwd
+ * (flash_attn_launcher.cu:22-65). */
+int cta_flash_attention_fwd_bf16(const uint16_t* q, const int64_t* q_strides,
+                                 const uint16_t* k, const int64_t* k_strides,
+                                 const uint16_t* v, const int64_t* v_strides,
+                                 int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                                 uint16_t* o, float* l, void* stream);
+
 /* Bytes of dS workspace that let cta_flash_attention_bwd keep every head's dS tiles
  * (the lower-triangular 32x32 tiles only when causal): B*nh*ceil(T/32)^2*4 KiB, or about
  * half of that when causal.  0 for empty or unsupported shapes. */
