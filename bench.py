@@ -56,8 +56,8 @@ def parse_args():
                    default="fa2",
                    help="fa2: the headline step (default, one JSON line); fa2-sweep: benchmark "
                         "config 3; ops: benchmark config 4 (one JSON line per op); gpt: benchmark "
-                        "config 5 training step; fa2-bf16: the BF16 forward at the config-2 "
-                        "shape, causal and full (an extension beyond the FP32 metric)")
+                        "config 5 training step; fa2-bf16: the BF16 forward and backward at the "
+                        "config-2 shape, causal and full (an extension beyond the FP32 metric)")
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--batch", type=int, default=4)
@@ -65,6 +65,8 @@ def parse_args():
     p.add_argument("--seq", type=int, default=4096)
     p.add_argument("--head-dim", type=int, default=64)
     p.add_argument("--non-causal", action="store_true")
+    p.add_argument("--masks", choices=["both", "causal", "full"], default="both",
+                   help="fa2-bf16 workload: which masks to time")
     p.add_argument("--gpt-mlp", choices=["fused", "reference"], default="fused",
                    help="gpt workload: fused: CudaMLP (GELU in the GEMM epilogues, the model's "
                         "default); reference: CudaLinearLayer -> CudaGeluLayer -> CudaLinearLayer")
@@ -330,10 +332,11 @@ def fa2_sweep(args):
 
 
 def fa2_bf16_workload(args):
-    """The BF16 FlashAttention-2 forward (cta_flash_attention_fwd_bf16) at the config-2 shape,
-    causal and non-causal: HIP-event time per launch on torch's current stream with inputs in
-    HBM, TFLOPS by the reference's formula (4*B*H*N^2*D, halved when causal) and the fraction
-    of the 2.5 PFLOP/s dense BF16 MFMA peak.  One JSON line per mask."""
+    """The BF16 FlashAttention-2 step at the config-2 shape, causal and non-causal: forward
+    (cta_flash_attention_fwd_bf16) and backward (cta_flash_attention_bwd_bf16: delta, dK/dV
+    storing BF16 dS, dQ from dS), each timed with HIP events on torch's current stream with
+    inputs in HBM.  TFLOPS by the reference's formula (forward 4*B*H*N^2*D, halved when causal;
+    backward 2.5x), against the 2.5 PFLOP/s dense BF16 MFMA peak.  One JSON line per mask."""
     import torch
 
     from cuda_transformer_amd import capi
@@ -342,29 +345,48 @@ def fa2_bf16_workload(args):
     dev = torch.device("cuda", 0)
     gen = torch.Generator().manual_seed(0)
     q, k, v = (torch.randn(B, H, N, D, generator=gen).to(torch.bfloat16).to(dev) for _ in range(3))
+    do = torch.randn(B, H, N, D, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
     O = torch.empty_like(q)
     L = torch.empty(B, H, N, device=dev)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    delta = torch.empty(B, H, N, device=dev)
     lib = capi.lib()
     st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-    s4 = capi.strides(q.stride())
+    s4, s3 = capi.strides(q.stride()), capi.strides(L.stride())
     vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-    for causal in (True, False):
+    masks = {"both": (True, False), "causal": (True,), "full": (False,)}[args.masks]
+    for causal in masks:
+        ws_bytes = lib.cta_flash_attention_bwd_bf16_workspace(B, H, N, D, int(causal))
+        ws = torch.empty(ws_bytes // 4 + 4, device=dev)
+
         def fwd():
-            rc = lib.cta_flash_attention_fwd_bf16(vp(q), s4, vp(k), s4, vp(v), s4, B, H, N, D,
-                                                  int(causal), vp(O), vp(L), st)
-            if rc != 0:
+            if lib.cta_flash_attention_fwd_bf16(vp(q), s4, vp(k), s4, vp(v), s4, B, H, N, D,
+                                                int(causal), vp(O), vp(L), st) != 0:
                 raise RuntimeError(lib.cta_last_error().decode())
-        ms = _time_kernel(fwd, max(10, args.steps), warm_s=0.2)
-        fl, _ = attn_flops(B, H, N, D, causal)
-        tf = fl / (ms * 1e-3) / 1e12
+
+        def bwd():
+            if lib.cta_flash_attention_bwd_bf16(vp(q), s4, vp(k), s4, vp(v), s4, vp(O), s4,
+                                                vp(do), s4, vp(L), s3, B, H, N, D, int(causal),
+                                                vp(dq), vp(dk), vp(dv), vp(delta), vp(ws),
+                                                ws_bytes, st) != 0:
+                raise RuntimeError(lib.cta_last_error().decode())
+        fwd_ms = _time_kernel(fwd, max(10, args.steps), warm_s=0.2)
+        fwd()
+        bwd_ms = _time_kernel(bwd, max(10, args.steps), warm_s=0.2)
+        fl, bfl = attn_flops(B, H, N, D, causal)
+        ftf, btf = fl / (fwd_ms * 1e-3) / 1e12, bfl / (bwd_ms * 1e-3) / 1e12
+        stf = (fl + bfl) / ((fwd_ms + bwd_ms) * 1e-3) / 1e12
         print(json.dumps({
-            "workload": f"FA2 forward BF16 B{B} H{H} N{N} D{D} {'causal' if causal else 'non-causal'}",
-            "metric": "FA2 BF16 forward TFLOPS", "value": round(tf, 2), "unit": "TFLOPS",
-            "ms": round(ms, 4), "dtype": "bf16 inputs, fp32 accumulation",
-            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                         "algorithmic_per_launch": fl},
+            "workload": f"FA2 BF16 fwd+bwd B{B} H{H} N{N} D{D} {'causal' if causal else 'non-causal'}",
+            "metric": "FA2 BF16 fwd+bwd TFLOPS", "value": round(stf, 2), "unit": "TFLOPS",
+            "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
+            "fwd_tflops": round(ftf, 2), "bwd_tflops": round(btf, 2),
+            "dtype": "bf16 inputs, fp32 accumulation",
+            "roofline": {"bound": "mfma", "achieved": round(stf, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(stf / MFMA_BF16_PEAK_TFLOPS, 4),
+                         "algorithmic_per_launch": fl + bfl},
         }), flush=True)
+        del ws
     return 0
 
 

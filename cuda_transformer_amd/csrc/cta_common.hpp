@@ -42,6 +42,25 @@ __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast
 __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
 __device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
 
+// BF16 MFMA (gfx950 v_mfma_f32_32x32x16_bf16), checked on an MI355X:
+//   A (32 x 16): lane l supplies A[l % 32][8 (l/32) + j], j = 0..7
+//   B (16 x 32): lane l supplies B[8 (l/32) + j][l % 32]
+//   D: the 32x32 layout of the FP32 MFMA above.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// A 32x32 score tile in registers (lane l: rows R(r, l/32)) is the B operand of two 16-deep
+// BF16 MFMA steps: step s takes registers 8s .. 8s+7, i.e. rows 16 s + 8 (j/4) + 4 h + j%4 of
+// element j.  A matching A operand read from a transposed [col][row] image in LDS needs those
+// rows adjacent: store row k of the image at position kt_pos(k), bits 2 and 3 of k swapped.
+__device__ __forceinline__ constexpr int kt_pos(int k) {
+  return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+__device__ __forceinline__ bf16x8 ld_bf16x8(const __bf16* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+
 // Exchange with the lane 32 positions away (the other half of the wave).
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
 
@@ -81,6 +100,17 @@ __device__ __forceinline__ int xcd_work_item(int hw_id, int total) {
 }
 inline unsigned xcd_grid(int64_t total) {
   return (unsigned)(kNumXcds * ((total + kNumXcds - 1) / kNumXcds));
+}
+
+// Stored dS tiles of the backward (FA2, FP32 and BF16).  Tile (ib, jb) covers query rows
+// 32*ib.. and key rows 32*jb.. of one head; causal heads keep the tiles with jb <= ib only,
+// packed row by row.
+__host__ __device__ inline int64_t ds_tile_index(int ib, int jb, int nb, bool causal) {
+  return causal ? (int64_t)ib * (ib + 1) / 2 + jb : (int64_t)ib * nb + jb;
+}
+__host__ __device__ inline int64_t ds_tiles_per_head(int64_t T, bool causal) {
+  const int64_t nb = (T + 31) / 32;
+  return causal ? nb * (nb + 1) / 2 : nb * nb;
 }
 
 // Asynchronous copy global -> LDS without registers (global_load_lds_dwordx4 / _dword on

@@ -245,18 +245,10 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
 }
 
 // ------------------------------------------------------------------------------------
-// Stored dS tiles.  Tile (ib, jb) covers query rows 32*ib.. and key rows 32*jb.. of one head
-// in 1024 floats, ordered for the wave that consumes it: lane l = 32*h + c reads float4 g
-// at offset 256*g + 4*l, which holds dS[32*ib + c][32*jb + 8*g + 4*h + e] for e = 0..3 —
-// the B operand of the 32x32x2 MFMA for contraction steps kk = 4*g + e.  Causal heads keep
-// the tiles with jb <= ib only, packed row by row.
-__host__ __device__ inline int64_t ds_tile_index(int ib, int jb, int nb, bool causal) {
-  return causal ? (int64_t)ib * (ib + 1) / 2 + jb : (int64_t)ib * nb + jb;
-}
-__host__ __device__ inline int64_t ds_tiles_per_head(int64_t T, bool causal) {
-  const int64_t nb = (T + 31) / 32;
-  return causal ? nb * (nb + 1) / 2 : nb * nb;
-}
+// Stored dS tiles (ds_tile_index, cta_common.hpp).  An FP32 tile holds its 1024 floats in the
+// order of the wave that consumes it: lane l = 32*h + c reads float4 g at offset 256*g + 4*l,
+// which holds dS[32*ib + c][32*jb + 8*g + 4*h + e] for e = 0..3 — the B operand of the
+// 32x32x2 MFMA for contraction steps kk = 4*g + e.
 constexpr int kDsTileFloats = 1024;
 constexpr int kDsPitch = 40;  // LDS pitch of the per-wave transpose: halves 4 rows apart hit disjoint banks
 

@@ -1,0 +1,554 @@
+// FlashAttention-2 backward with BF16 Q, K, V, O, dO (FP32 L), FP32 accumulation, CDNA4 MFMA
+// (v_mfma_f32_32x32x16_bf16).  dQ, dK, dV are written in BF16.
+//
+// The semantics are those of the FP32 backward (Transformer_kernels/flash_attention.cuh:175-504):
+//   delta_i = sum_d O_id dO_id,  P_ij = e^{S_ij - L_i},  dP_ij = dO_i . v_j,
+//   dS_ij = P_ij (dP_ij - delta_i),  dV_j = sum_i P_ij dO_i,  dK_j = s sum_i dS_ij q_i,
+//   dQ_i = s sum_j dS_ij k_j,  S = s q.k, s = 1/sqrt(hs), causal mask j > i.
+// S, dP, delta and dS are FP32; P and dS are rounded to BF16 as MFMA operands, and dS is stored
+// in BF16 for the dQ stage.  The schedule is the FP32 kernels' stored-dS one: delta, then a
+// dK/dV stage that also writes every dS tile, then dQ = s dS K from the stored tiles; both
+// stages are atomics-free and deterministic.
+//
+// gfx950 layout (the BF16 forward's trick, see fa2_fwd_bf16.hip):
+//  * dK/dV: a wave owns 32 key rows and keeps k, v of its key row in registers as the B
+//    operands of S = Q K^T and dP = dO V^T, read row-wise from [query][d] images of the Q and
+//    dO tiles.  S and dP then hold one key per lane; P and dS, rounded to BF16, are the B
+//    operands of dV^T += dO^T P and dK^T += Q^T dS, whose A operands come from transposed
+//    [d][query] images with bits 2 and 3 of the query index swapped (kt_pos).  Each stage's
+//    Q / dO tile therefore goes to LDS twice, row-wise and transposed.
+//  * dS tiles go through a per-wave LDS transpose and out to HBM in the dQ stage's operand
+//    order: in tile (ib, jb), lane l = 32 h + c of step s reads 8 consecutive keys
+//    16 s + 8 h .. +7 of query c at offset 8 (32 (2 s + h) + c), one 16-byte load.
+//  * dQ: a wave owns 32 query rows; K tiles go to LDS transposed ([d][key]) and the stored dS
+//    tiles straight into registers as the B operand of dQ^T += K^T dS^T.
+#include "cta_common.hpp"
+
+namespace cta {
+namespace {
+
+struct RowStridesH {
+  int64_t b, h, t;  // element strides of the batch, head and time axes (d-stride is 1)
+};
+
+constexpr int kDsTileBf16 = 1024;  // bf16 elements of one stored 32x32 dS tile
+
+// ------------------------------------------------------------------------------------
+// delta = rowsum(O * dO), FP32 from BF16 rows; G = hs/8 lanes per row, 16 bytes each.
+template <int HS>
+__global__ __launch_bounds__(256) void fa2_bwd_delta_bf16_kernel(const __bf16* __restrict__ O,
+                                                                 const __bf16* __restrict__ dO,
+                                                                 float* __restrict__ delta,
+                                                                 int nh, int T, int64_t rows,
+                                                                 RowStridesH so,
+                                                                 RowStridesH sdo) {
+  constexpr int G = HS / 8;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / G;
+  const int c8 = (int)(gid % G);
+  float acc = 0.0f;
+  if (row < rows) {
+    const int64_t bh = row / T;
+    const int t = (int)(row - bh * T);
+    const int64_t b = bh / nh, h = bh - b * nh;
+    const bf16x8 o = ld_bf16x8(O + b * so.b + h * so.h + (int64_t)t * so.t + 8 * c8);
+    const bf16x8 g = ld_bf16x8(dO + b * sdo.b + h * sdo.h + (int64_t)t * sdo.t + 8 * c8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf((float)o[e], (float)g[e], acc);
+  }
+#pragma unroll
+  for (int off = G / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+  if (row < rows && c8 == 0) delta[row] = acc;
+}
+
+// ------------------------------------------------------------------------------------
+// dK, dV and the stored dS tiles.  Workgroup = 128 key rows (4 waves x 32); query stages of 32
+// rows, global -> registers -> LDS, double buffered, one barrier per stage.  Heads
+// [bh_base, bh_base + BH); the dS tiles go to dsw, heads indexed from bh_base.
+template <int HS, bool CAUSAL>
+__global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kernel(
+    const __bf16* __restrict__ Q, const __bf16* __restrict__ K, const __bf16* __restrict__ V,
+    const __bf16* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
+    __bf16* __restrict__ dK, __bf16* __restrict__ dV, __bf16* __restrict__ dsw, int nh, int T,
+    int bh_base, int BH, int n_ktiles, RowStridesH sq, RowStridesH sk, RowStridesH sv,
+    RowStridesH sdo, RowStridesH sl, float scale, float scale_log2) {
+  constexpr int BN = 32;             // query rows per stage
+  constexpr int BM = 128;            // key rows per workgroup
+  constexpr int RP = HS + 8;         // bf16 pitch of a row image: conflict-free 16-byte reads
+  constexpr int TP = BN + 8;         // bf16 pitch of a transposed image row (one d)
+  constexpr int XP = 32 + 8;         // bf16 pitch of the dS transpose
+  constexpr int CH = HS / 8;         // 16-byte chunks per row
+  constexpr int LOADS = BN * CH / 256;
+  constexpr int QS = HS / 16;        // MFMA steps over d
+  static_assert(BN * CH % 256 == 0, "stage must split evenly over 256 threads");
+  // Stage image, in bytes: Q rows, dO rows, Q^T, dO^T, L, delta.
+  constexpr int B_ROWS = BN * RP * 2, B_TRS = HS * TP * 2;
+  constexpr int OFF_GR = B_ROWS, OFF_QT = 2 * B_ROWS, OFF_GT = 2 * B_ROWS + B_TRS;
+  constexpr int OFF_L = 2 * B_ROWS + 2 * B_TRS, OFF_D = OFF_L + BN * 4;
+  constexpr int STAGE = OFF_D + BN * 4;
+  constexpr int XPOSE = 32 * XP * 2;  // per wave
+  static_assert(STAGE % 16 == 0 && OFF_QT % 16 == 0 && OFF_L % 16 == 0, "16-byte aligned images");
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * STAGE + 4 * XPOSE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, col = lane & 31;
+  const int per_head = CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles;
+  const int w = xcd_work_item(blockIdx.x, BH * per_head);
+  if (w >= BH * per_head) return;
+  const int bh_local = w / per_head;
+  const int p = w - bh_local * per_head;
+  const int bh = bh_base + bh_local;
+  const int b = bh / nh, h = bh - b * nh;
+
+  const __bf16* Qb = Q + b * sq.b + h * sq.h;
+  const __bf16* dOb = dO + b * sdo.b + h * sdo.h;
+  const float* Lb = Lg + b * sl.b + h * sl.h;
+  const float* Db = delta + (int64_t)bh * T;
+  const int nb = (T + 31) / 32;
+  __bf16* xw = reinterpret_cast<__bf16*>(smem + 2 * STAGE + wave * XPOSE);
+  __bf16* dsh = dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileBf16;
+
+  const int n_pass = (CAUSAL && n_ktiles - 1 - p != p) ? 2 : 1;
+  for (int pass = 0; pass < n_pass; ++pass) {
+  const int kt = CAUSAL ? (pass == 0 ? p : n_ktiles - 1 - p) : p;
+  const int j0 = kt * BM + wave * 32;  // first key row of this wave
+  const int my_j = j0 + col;
+
+  // k and v of this lane's key row, d = 16 s + 8 half + 0..7 for step s.
+  bf16x8 kf[QS], vf[QS];
+  if (my_j < T) {
+    const __bf16* kp = K + b * sk.b + h * sk.h + (int64_t)my_j * sk.t + 8 * half;
+    const __bf16* vp = V + b * sv.b + h * sv.h + (int64_t)my_j * sv.t + 8 * half;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      kf[s] = ld_bf16x8(kp + 16 * s);
+      vf[s] = ld_bf16x8(vp + 16 * s);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < QS; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { kf[s][j] = (__bf16)0.0f; vf[s][j] = (__bf16)0.0f; }
+  }
+
+  f32x16 dkacc[HS / 32], dvacc[HS / 32];
+#pragma unroll
+  for (int d = 0; d < HS / 32; ++d) { dkacc[d] = zero16(); dvacc[d] = zero16(); }
+
+  const int q_begin = CAUSAL ? (kt * BM / BN) : 0;  // first query stage that can see these keys
+  const int n_stages = (T + BN - 1) / BN;
+  const bool wave_stores = j0 < T;
+
+  // Register-staged loads of one query stage: Q and dO rows (rows past T are zero), L, delta.
+  uint4 qst[LOADS], gst[LOADS];
+  float lst = 0.0f, dst = 0.0f;
+  auto gload = [&](int stage) {
+    const int r0 = stage * BN;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int c = tid + 256 * u;
+      const int r = c / CH, ch = c % CH;
+      const int i = r0 + r;
+      if (i < T) {
+        qst[u] = *reinterpret_cast<const uint4*>(Qb + (int64_t)i * sq.t + 8 * ch);
+        gst[u] = *reinterpret_cast<const uint4*>(dOb + (int64_t)i * sdo.t + 8 * ch);
+      } else {
+        qst[u] = make_uint4(0, 0, 0, 0);
+        gst[u] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    if (tid < BN) {
+      const int i = r0 + tid;
+      lst = i < T ? Lb[(int64_t)i * sl.t] : 0.0f;
+      dst = i < T ? Db[i] : 0.0f;
+    }
+  };
+  auto lstore = [&](int buf) {
+    unsigned char* base = smem + buf * STAGE;
+    __bf16* qr = reinterpret_cast<__bf16*>(base);
+    __bf16* gr = reinterpret_cast<__bf16*>(base + OFF_GR);
+    __bf16* qt = reinterpret_cast<__bf16*>(base + OFF_QT);
+    __bf16* gt = reinterpret_cast<__bf16*>(base + OFF_GT);
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int c = tid + 256 * u;
+      const int r = c / CH, ch = c % CH;
+      *reinterpret_cast<uint4*>(qr + r * RP + 8 * ch) = qst[u];
+      *reinterpret_cast<uint4*>(gr + r * RP + 8 * ch) = gst[u];
+      const __bf16* qe = reinterpret_cast<const __bf16*>(&qst[u]);
+      const __bf16* ge = reinterpret_cast<const __bf16*>(&gst[u]);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        qt[(8 * ch + t) * TP + kt_pos(r)] = qe[t];
+        gt[(8 * ch + t) * TP + kt_pos(r)] = ge[t];
+      }
+    }
+    if (tid < BN) {
+      reinterpret_cast<float*>(base + OFF_L)[tid] = lst;
+      reinterpret_cast<float*>(base + OFF_D)[tid] = dst;
+    }
+  };
+
+  // Tiles whose every query row precedes every key row are skipped (dS = 0, nothing stored).
+  auto live = [&](int ii0) { return ii0 < T && !(CAUSAL && ii0 + 31 < j0); };
+  // The dS tile of query stage `stage`, from the transpose buffer to the workspace.
+  auto flush = [&](int stage) {
+    const int ii0 = stage * BN;
+    if (!live(ii0)) return;
+    __bf16* gtile = dsh + ds_tile_index(ii0 / 32, j0 / 32, nb, CAUSAL) * kDsTileBf16;
+    wave_lds_fence();
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+      *reinterpret_cast<bf16x8*>(gtile + 8 * (32 * (2 * s + half) + col)) =
+          ld_bf16x8(xw + col * XP + 16 * s + 8 * half);
+    wave_lds_fence();
+  };
+
+  // Stage order: with a causal mask the first (long) pass walks its query stages downward and
+  // the second (short) pass upward, so a head's workgroups share each streamed stage in L2.
+  const int n_steps = n_stages - q_begin;
+  const bool down = CAUSAL && pass == 0;
+  auto stage_at = [&](int i) { return down ? n_stages - 1 - i : q_begin + i; };
+  if (n_steps > 0) {
+    gload(stage_at(0));
+    lstore(0);
+  }
+  __syncthreads();
+
+  for (int i = 0; i < n_steps; ++i) {
+    const int s_idx = stage_at(i);
+    const int buf = i & 1;
+    if (i + 1 < n_steps) gload(stage_at(i + 1));
+    if (wave_stores && i > 0) flush(stage_at(i - 1));
+    const unsigned char* base = smem + buf * STAGE;
+    const __bf16* qr = reinterpret_cast<const __bf16*>(base);
+    const __bf16* gr = reinterpret_cast<const __bf16*>(base + OFF_GR);
+    const __bf16* qt = reinterpret_cast<const __bf16*>(base + OFF_QT);
+    const __bf16* gt = reinterpret_cast<const __bf16*>(base + OFF_GT);
+    const float* ls = reinterpret_cast<const float*>(base + OFF_L);
+    const float* ds = reinterpret_cast<const float*>(base + OFF_D);
+    const int ii0 = s_idx * BN;
+
+    if (live(ii0)) {
+      // S = Q K^T and dP = dO V^T: lane holds column my_j, rows ii0 + R(r, half).
+      f32x16 sacc = zero16(), pacc = zero16();
+#pragma unroll
+      for (int s = 0; s < QS; ++s)
+        sacc = mfma_bf16(ld_bf16x8(qr + col * RP + 16 * s + 8 * half), kf[s], sacc);
+#pragma unroll
+      for (int s = 0; s < QS; ++s)
+        pacc = mfma_bf16(ld_bf16x8(gr + col * RP + 16 * s + 8 * half), vf[s], pacc);
+
+      // P = e^{S - L}; masked entries (and, for the stored dS, key rows past T) are exactly 0.
+      const bool need_mask = (CAUSAL && ii0 < j0 + 31) || (ii0 + 32 > T) || (j0 + 32 > T);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 lv = ld4(ls + 8 * g + 4 * half);
+        const float lr[4] = {lv.x, lv.y, lv.z, lv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          float pr = fast_exp2(fmaf(sacc[r], scale_log2, -lr[e] * kLog2e));
+          if (need_mask) {
+            const int qi = ii0 + 8 * g + 4 * half + e;
+            if ((CAUSAL && my_j > qi) || qi >= T || my_j >= T) pr = 0.0f;
+          }
+          sacc[r] = pr;
+        }
+      }
+      bf16x8 pb[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pb[r >> 3][r & 7] = (__bf16)sacc[r];
+
+      // dV^T += dO^T P
+#pragma unroll
+      for (int d = 0; d < HS / 32; ++d)
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          dvacc[d] = mfma_bf16(ld_bf16x8(gt + (d * 32 + col) * TP + 16 * s + 8 * half), pb[s],
+                               dvacc[d]);
+
+      // dS = P (dP - delta)
+      bf16x8 db[2];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 dv = ld4(ds + 8 * g + 4 * half);
+        const float dr[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          db[r >> 3][r & 7] = (__bf16)(sacc[r] * (pacc[r] - dr[e]));
+        }
+      }
+
+      // dS tile into the transpose buffer as [query][key]: lane (col, half) holds
+      // dS[ii0 + R(r, half)][j0 + col].  A wave's LDS operations complete in order, so no
+      // barrier separates the write, the read in flush() and the next write.
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xw[mfma_row(r, half) * XP + col] = db[r >> 3][r & 7];
+
+      // dK^T += Q^T dS
+#pragma unroll
+      for (int d = 0; d < HS / 32; ++d)
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          dkacc[d] = mfma_bf16(ld_bf16x8(qt + (d * 32 + col) * TP + 16 * s + 8 * half), db[s],
+                               dkacc[d]);
+    }
+
+    if (i + 1 < n_steps) lstore(buf ^ 1);
+    __syncthreads();
+  }
+  if (wave_stores && n_steps > 0) flush(stage_at(n_steps - 1));
+
+  if (my_j < T) {
+    __bf16* kp = dK + ((int64_t)bh * T + my_j) * HS;
+    __bf16* vp = dV + ((int64_t)bh * T + my_j) * HS;
+#pragma unroll
+    for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        __bf16 k4[4], v4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          k4[e] = (__bf16)(dkacc[d][4 * g + e] * scale);
+          v4[e] = (__bf16)dvacc[d][4 * g + e];
+        }
+        const int dc = d * 32 + 8 * g + 4 * half;
+        *reinterpret_cast<uint2*>(kp + dc) = *reinterpret_cast<const uint2*>(k4);
+        *reinterpret_cast<uint2*>(vp + dc) = *reinterpret_cast<const uint2*>(v4);
+      }
+    }
+  }
+  }  // pass: the stage loop ended on a barrier, so the next pass may refill LDS
+}
+
+// ------------------------------------------------------------------------------------
+// dQ from the stored BF16 dS tiles: dQ^T += K^T dS^T.  Workgroup = 128 query rows (4 waves x
+// 32); key stages of 64 rows go to LDS transposed ([d][key]); each wave loads its own dS tiles
+// from the workspace straight into registers, one stage ahead.
+template <int HS, bool CAUSAL>
+__global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_bf16_kernel(
+    const __bf16* __restrict__ K, const __bf16* __restrict__ dsw, __bf16* __restrict__ dQ,
+    int nh, int T, int bh_base, int BH, int n_qtiles, RowStridesH sk, float scale) {
+  constexpr int BN = 64;
+  constexpr int NSUB = BN / 32;
+  constexpr int BM = 128;
+  constexpr int KTP = BN + 8;  // bf16 pitch of a K^T row (one d, every key of the stage)
+  constexpr int TILE = HS * KTP;
+  constexpr int CH = HS / 8;
+  constexpr int LOADS = BN * CH / 256;
+  static_assert(BN * CH % 256 == 0, "stage must split evenly over 256 threads");
+  __shared__ __attribute__((aligned(16))) __bf16 smem[2 * TILE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, col = lane & 31;
+  const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+  const int w = xcd_work_item(blockIdx.x, BH * per_head);
+  if (w >= BH * per_head) return;
+  const int bh_local = w / per_head;
+  const int p = w - bh_local * per_head;
+  const int bh = bh_base + bh_local;
+  const int b = bh / nh, h = bh - b * nh;
+  const __bf16* Kb = K + b * sk.b + h * sk.h;
+  const int nb = (T + 31) / 32;
+  const __bf16* dsh = dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileBf16;
+
+  const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
+  for (int pass = 0; pass < n_pass; ++pass) {
+  const int qt = CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p;
+  const int i0 = qt * BM + wave * 32;
+  const int my_i = i0 + col;
+  const int ib = i0 / 32;
+
+  f32x16 acc[HS / 32];
+#pragma unroll
+  for (int d = 0; d < HS / 32; ++d) acc[d] = zero16();
+
+  const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
+  const int n_stages = (kv_end + BN - 1) / BN;
+
+  // Branch-free clamped loads: every stage issues the same loads, so the compiler counts them
+  // exactly and a stage's MFMAs wait only for that stage's dS.
+  uint4 kst[LOADS];
+  auto gload = [&](int stage) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int c = tid + 256 * u;
+      const int r = c / CH, ch = c % CH;
+      const int j = stage * BN + r;
+      const uint4 kv = *reinterpret_cast<const uint4*>(Kb + (int64_t)min(j, T - 1) * sk.t + 8 * ch);
+      kst[u] = j < T ? kv : make_uint4(0, 0, 0, 0);  // keys past T meet finite dS: K must be 0
+    }
+  };
+  auto lstore = [&](int buf) {
+    __bf16* kt = smem + buf * TILE;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int c = tid + 256 * u;
+      const int r = c / CH, ch = c % CH;
+      const __bf16* e = reinterpret_cast<const __bf16*>(&kst[u]);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) kt[(8 * ch + t) * KTP + r] = e[t];
+    }
+  };
+  auto has_tile = [&](int jb) { return ib < nb && jb < nb && (!CAUSAL || jb <= ib); };
+  const int ibc = min(ib, nb - 1);
+  auto dsload = [&](int stage, bf16x8 (&dr)[NSUB][2]) {
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub) {
+      const int jbc = min(stage * NSUB + sub, CAUSAL ? ibc : nb - 1);
+      const __bf16* src = dsh + ds_tile_index(ibc, jbc, nb, CAUSAL) * kDsTileBf16;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) dr[sub][s] = ld_bf16x8(src + 8 * (32 * (2 * s + half) + col));
+    }
+  };
+  auto compute = [&](int stage, const __bf16* kt, const bf16x8 (&dr)[NSUB][2]) {
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub) {
+      if (!has_tile(stage * NSUB + sub)) continue;
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int d = 0; d < HS / 32; ++d)
+          acc[d] = mfma_bf16(ld_bf16x8(kt + (d * 32 + col) * KTP + sub * 32 + 16 * s + 8 * half),
+                             dr[sub][s], acc[d]);
+    }
+  };
+  auto step = [&](int s, const bf16x8 (&cur)[NSUB][2], bf16x8 (&nxt)[NSUB][2]) {
+    const int buf = s & 1;
+    gload(s + 1);
+    dsload(s + 1, nxt);
+    compute(s, smem + buf * TILE, cur);
+    lstore(buf ^ 1);
+    __syncthreads();
+  };
+
+  bf16x8 dA[NSUB][2], dB[NSUB][2];
+  dsload(0, dA);
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int n_stages2 = (n_stages + 1) & ~1;
+  for (int s = 0; s < n_stages2; s += 2) {
+    step(s, dA, dB);
+    step(s + 1, dB, dA);
+  }
+
+  if (my_i < T) {
+    __bf16* op = dQ + ((int64_t)bh * T + my_i) * HS;
+#pragma unroll
+    for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        __bf16 q4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q4[e] = (__bf16)(acc[d][4 * g + e] * scale);
+        *reinterpret_cast<uint2*>(op + d * 32 + 8 * g + 4 * half) =
+            *reinterpret_cast<const uint2*>(q4);
+      }
+    }
+  }
+  }  // pass: the stage loop ended on a barrier, so the next pass may refill LDS
+}
+
+RowStridesH rsh(const int64_t* s) { return RowStridesH{s[0], s[1], s[2]}; }
+
+bool layout_bf16_ok(const void* p, const int64_t* s) {
+  return p != nullptr && s != nullptr && aligned16(p) && s[3] == 1 && s[0] % 8 == 0 &&
+         s[1] % 8 == 0 && s[2] % 8 == 0;
+}
+
+template <typename F>
+void dispatch_bf16(int64_t hs, int causal, F&& f) {
+  if (hs == 64) {
+    if (causal) f.template operator()<64, true>();
+    else f.template operator()<64, false>();
+  } else {
+    if (causal) f.template operator()<128, true>();
+    else f.template operator()<128, false>();
+  }
+}
+
+}  // namespace
+}  // namespace cta
+
+using namespace cta;
+
+extern "C" int64_t cta_flash_attention_bwd_bf16_workspace(int64_t B, int64_t nh, int64_t T,
+                                                          int64_t hs, int causal) {
+  if (B <= 0 || nh <= 0 || T <= 0 || (hs != 64 && hs != 128)) return 0;
+  return B * nh * ds_tiles_per_head(T, causal != 0) * kDsTileBf16 * 2;
+}
+
+extern "C" int cta_flash_attention_bwd_bf16(
+    const uint16_t* q, const int64_t* q_strides, const uint16_t* k, const int64_t* k_strides,
+    const uint16_t* v, const int64_t* v_strides, const uint16_t* o, const int64_t* o_strides,
+    const uint16_t* d_o, const int64_t* do_strides, const float* l, const int64_t* l_strides,
+    int64_t B, int64_t nh, int64_t T, int64_t hs, int causal, uint16_t* dq, uint16_t* dk,
+    uint16_t* dv, float* delta, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
+  if (hs == 32)
+    return fail(CTA_ERR_UNSUPPORTED_HEAD_DIM,
+                "flash_attention_bwd with bfloat16 inputs supports hs=64 and hs=128");
+  if (B * nh * T == 0) return CTA_OK;
+  if (!layout_bf16_ok(q, q_strides) || !layout_bf16_ok(k, k_strides) ||
+      !layout_bf16_ok(v, v_strides) || !layout_bf16_ok(o, o_strides) ||
+      !layout_bf16_ok(d_o, do_strides))
+    return fail(CTA_ERR_LAYOUT,
+                "flash_attention_bwd (bfloat16) needs unit d-stride, strides divisible by 8 and "
+                "16-byte aligned Q/K/V/O/dO");
+  if (!l || !l_strides || !delta) return fail(CTA_ERR_INVALID_ARGUMENT, "null L or delta pointer");
+  if (!dq || !dk || !dv || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
+      !aligned16(workspace))
+    return fail(CTA_ERR_LAYOUT, "dQ/dK/dV and the workspace must be 16-byte aligned pointers");
+  const int64_t head_bytes = cta_flash_attention_bwd_bf16_workspace(1, 1, T, hs, causal);
+  if (workspace == nullptr || workspace_bytes < head_bytes)
+    return fail(CTA_ERR_INVALID_ARGUMENT,
+                "flash_attention_bwd (bfloat16) needs a dS workspace of at least one head");
+  const auto* qb = reinterpret_cast<const __bf16*>(q);
+  const auto* kb = reinterpret_cast<const __bf16*>(k);
+  const auto* vb = reinterpret_cast<const __bf16*>(v);
+  const auto* ob = reinterpret_cast<const __bf16*>(o);
+  const auto* gb = reinterpret_cast<const __bf16*>(d_o);
+  auto* dqb = reinterpret_cast<__bf16*>(dq);
+  auto* dkb = reinterpret_cast<__bf16*>(dk);
+  auto* dvb = reinterpret_cast<__bf16*>(dv);
+  auto* wsb = reinterpret_cast<__bf16*>(workspace);
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  const RowStridesH sl{l_strides[0], l_strides[1], l_strides[2]};
+  const int BH = (int)(B * nh);
+  hipStream_t st = as_stream(stream);
+
+  const int64_t rows = B * nh * T;
+  const unsigned dgrid = (unsigned)((rows * (hs / 8) + 255) / 256);
+  if (hs == 64)
+    hipLaunchKernelGGL(fa2_bwd_delta_bf16_kernel<64>, dim3(dgrid), dim3(256), 0, st, ob, gb, delta,
+                       (int)nh, (int)T, rows, rsh(o_strides), rsh(do_strides));
+  else
+    hipLaunchKernelGGL(fa2_bwd_delta_bf16_kernel<128>, dim3(dgrid), dim3(256), 0, st, ob, gb,
+                       delta, (int)nh, (int)T, rows, rsh(o_strides), rsh(do_strides));
+  if (int rc = check_launch("flash_attention_bwd_bf16 delta")) return rc;
+
+  // Chunks of equal head counts that fit the workspace.
+  const int64_t fit = std::min<int64_t>(BH, workspace_bytes / head_bytes);
+  const int64_t n_chunks = (BH + fit - 1) / fit;
+  const int chunk = (int)((BH + n_chunks - 1) / n_chunks);
+  const int n_tiles = (int)((T + 127) / 128);
+  for (int h0 = 0; h0 < BH; h0 += chunk) {
+    const int n = std::min(chunk, BH - h0);
+    dispatch_bf16(hs, causal, [&]<int HS, bool C>() {
+      const int64_t items = (int64_t)(C ? (n_tiles + 1) / 2 : n_tiles) * n;
+      hipLaunchKernelGGL((fa2_bwd_dkdv_bf16_kernel<HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
+                         st, qb, kb, vb, gb, l, delta, dkb, dvb, wsb, (int)nh, (int)T, h0, n,
+                         n_tiles, rsh(q_strides), rsh(k_strides), rsh(v_strides),
+                         rsh(do_strides), sl, scale, scale * kLog2e);
+      hipLaunchKernelGGL((fa2_bwd_dq_ds_bf16_kernel<HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
+                         st, kb, wsb, dqb, (int)nh, (int)T, h0, n, n_tiles, rsh(k_strides), scale);
+    });
+    if (int rc = check_launch("flash_attention_bwd_bf16")) return rc;
+  }
+  return CTA_OK;
+}

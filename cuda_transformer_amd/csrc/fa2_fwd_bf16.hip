@@ -19,28 +19,17 @@
 //    R(r, h) = 8 (r/4) + 4 h + r%4.
 //  * O^T += V^T P^T: for MFMA step s the B operand is the lane's registers r = 8s .. 8s+7,
 //    rounded to BF16, i.e. keys 16 s + 8 (j/4) + 4 h + j%4 for element j.  V is stored in LDS
-//    transposed, [d][key], with bits 2 and 3 of the key index swapped inside each 16-key
-//    group, so those eight keys are adjacent and the A operand is one 16-byte read.
+//    transposed, [d][key], with bits 2 and 3 of the key index swapped (kt_pos), so those eight
+//    keys are adjacent and the A operand is one 16-byte read.
 //  * Online softmax, lazy rescaling and the two-half max / sum exchange are the FP32 kernel's.
 #include "cta_common.hpp"
 
 namespace cta {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
 struct RowStridesB {
   int64_t b, h, t;  // element strides of the batch, head and time axes (d-stride is 1)
 };
-
-__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-// Position of key k (0..63 of a stage) in a V^T row: bits 2 and 3 swapped.
-__device__ __forceinline__ constexpr int vt_pos(int k) {
-  return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
-}
 
 template <int HS, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
@@ -129,7 +118,7 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
       *reinterpret_cast<uint4*>(ks + r * KP + 8 * ch) = kst[u];
       const __bf16* e = reinterpret_cast<const __bf16*>(&vst[u]);
 #pragma unroll
-      for (int t = 0; t < 8; ++t) vt[(8 * ch + t) * VP + vt_pos(r)] = e[t];
+      for (int t = 0; t < 8; ++t) vt[(8 * ch + t) * VP + kt_pos(r)] = e[t];
     }
   };
 

@@ -416,6 +416,49 @@ std::tuple<at::Tensor, at::Tensor> flash_attention_fwd(at::Tensor Q, at::Tensor 
   return {O, L};
 }
 
+// BF16 backward (extension): stored-dS schedule with a BF16 dS workspace from torch's caching
+// allocator (the same 8 GiB cap as the FP32 op; chunked over heads beyond it).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd_bf16(
+    const at::Tensor& Q, const at::Tensor& K, const at::Tensor& V, const at::Tensor& O,
+    const at::Tensor& dO, const at::Tensor& L, bool causal) {
+  const int64_t B = Q.size(0), nh = Q.size(1), T = Q.size(2), hs = Q.size(3);
+  for (const auto* t : {&K, &V, &O, &dO})
+    TORCH_CHECK(t->scalar_type() == at::kBFloat16,
+                "Q, K, V, O and dO must all be bfloat16 (or all float32)");
+  TORCH_CHECK(L.scalar_type() == at::kFloat, "L must be a float32 tensor");
+  TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes() && O.sizes() == Q.sizes() &&
+                  dO.sizes() == Q.sizes(),
+              "Q, K, V, O and dO must have the same shape");
+  TORCH_CHECK(L.dim() == 3 && L.size(0) == B && L.size(1) == nh && L.size(2) == T,
+              "L must have shape (B, nh, T)");
+  TORCH_CHECK(hs == 64 || hs == 128,
+              "Unsupported head dimension for bfloat16! Only hs=64 and hs=128 are supported.");
+  c10::OptionalDeviceGuard guard(Q.device());
+  at::Tensor dQ = at::empty({B, nh, T, hs}, Q.options());
+  at::Tensor dK = at::empty({B, nh, T, hs}, Q.options());
+  at::Tensor dV = at::empty({B, nh, T, hs}, Q.options());
+  if (B * nh * T == 0) return {dQ, dK, dV};
+  at::Tensor delta = at::empty({B, nh, T}, Q.options().dtype(at::kFloat));
+  const int64_t full = cta_flash_attention_bwd_bf16_workspace(B, nh, T, hs, causal ? 1 : 0);
+  const int64_t head = cta_flash_attention_bwd_bf16_workspace(1, 1, T, hs, causal ? 1 : 0);
+  const int64_t ws_bytes = std::max(head, std::min(full, kBwdWorkspaceCap));
+  at::Tensor ws = at::empty({(ws_bytes + 15) / 16 * 4}, Q.options().dtype(at::kFloat));
+  const at::Tensor q = attn_operand_bf16(Q), k = attn_operand_bf16(K), v = attn_operand_bf16(V),
+                   o = attn_operand_bf16(O), g = attn_operand_bf16(dO);
+  const auto qs = strides_of<4>(q), ks = strides_of<4>(k), vs = strides_of<4>(v),
+             os = strides_of<4>(o), gs = strides_of<4>(g);
+  const auto ls = strides_of<3>(L);
+  auto u16 = [](const at::Tensor& t) { return reinterpret_cast<const uint16_t*>(t.data_ptr()); };
+  auto w16 = [](at::Tensor& t) { return reinterpret_cast<uint16_t*>(t.data_ptr()); };
+  check_rc(cta_flash_attention_bwd_bf16(u16(q), qs.data(), u16(k), ks.data(), u16(v), vs.data(),
+                                        u16(o), os.data(), u16(g), gs.data(),
+                                        L.data_ptr<float>(), ls.data(), B, nh, T, hs,
+                                        causal ? 1 : 0, w16(dQ), w16(dK), w16(dV),
+                                        delta.data_ptr<float>(), ws.data_ptr(), ws_bytes,
+                                        stream_of(Q)));
+  return {dQ, dK, dV};
+}
+
 // cf. flash_attn_launcher.cu:67-142
 std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd(at::Tensor Q, at::Tensor K,
                                                                    at::Tensor V, at::Tensor O,
@@ -429,6 +472,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd(at::Tensor Q,
   TORCH_CHECK(O.is_cuda(), "O must be a CUDA tensor");
   TORCH_CHECK(dO.is_cuda(), "dO must be a CUDA tensor");
   TORCH_CHECK(L.is_cuda(), "L must be a CUDA tensor");
+  if (Q.scalar_type() == at::kBFloat16) return flash_attention_bwd_bf16(Q, K, V, O, dO, L, causal);
   for (const auto* t : {&Q, &K, &V, &O, &dO, &L}) check_f32(*t, "input");
   TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes() && O.sizes() == Q.sizes() &&
                   dO.sizes() == Q.sizes(),

@@ -193,13 +193,21 @@ def _(Q, K, V, causal):
 
 def flash_attention_bwd(Q: Tensor, K: Tensor, V: Tensor, O: Tensor, dO: Tensor, L: Tensor,
                         causal: bool):
-    """FA2 backward -> (dQ, dK, dV)  (reference ops.py:123-125)."""
+    """FA2 backward -> (dQ, dK, dV)  (reference ops.py:123-125).
+
+    Extension: bfloat16 Q, K, V, O, dO with float32 L (hs 64 or 128) run the BF16 kernels and
+    return bfloat16 gradients."""
     return _ops.flash_attention_bwd.default(Q, K, V, O, dO, L, causal)
 
 
 @torch.library.register_fake("cuda_transformer::flash_attention_bwd")
 def _(Q, K, V, O, dO, L, causal):
-    _f32(Q, K, V, O, dO, L)
+    if Q.dtype == torch.bfloat16:
+        torch._check(all(t.dtype == torch.bfloat16 for t in (K, V, O, dO)),
+                     lambda: "Q, K, V, O and dO must all be bfloat16 (or all float32)")
+        _f32(L)
+    else:
+        _f32(Q, K, V, O, dO, L)
     _same_device(Q, K, V, O, dO, L)
     return torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
 

@@ -60,14 +60,36 @@ def _one(directory: Path, suffix: str) -> Path:
     return hits[0]
 
 
+def short_name(name: str) -> str:
+    """The function name of a kernel.  rocprofv3's truncated names (-T) are already short, but
+    it leaves names it cannot demangle (e.g. templates over __bf16, "DF16b") mangled; for those
+    the last identifier of the Itanium nested name is taken, so template instances merge into
+    one row as they do for demangled names."""
+    if not name.startswith("_Z"):
+        return name
+    i = 3 if name.startswith("_ZN") else 2
+    last = name
+    while i < len(name) and name[i].isdigit():
+        j = i
+        while j < len(name) and name[j].isdigit():
+            j += 1
+        n = int(name[i:j])
+        last = name[j:j + n]
+        i = j + n
+    return last
+
+
 def read_kernel_stats(directory) -> dict[str, dict]:
     """{kernel: {calls, avg_ns, total_ns, share}} from a --kernel-trace --stats run."""
-    out = {}
+    out: dict[str, dict] = {}
     with open(_one(directory, "_kernel_stats.csv")) as f:
         for r in csv.DictReader(f):
-            out[r["Name"]] = {"calls": int(r["Calls"]), "avg_ns": float(r["AverageNs"]),
-                              "total_ns": float(r["TotalDurationNs"]),
-                              "share": float(r["Percentage"])}
+            k = short_name(r["Name"])
+            o = out.setdefault(k, {"calls": 0, "total_ns": 0.0, "share": 0.0})
+            o["calls"] += int(r["Calls"])
+            o["total_ns"] += float(r["TotalDurationNs"])
+            o["share"] += float(r["Percentage"])
+            o["avg_ns"] = o["total_ns"] / o["calls"]
     return out
 
 
@@ -78,7 +100,7 @@ def read_trace_window(directory, skip: int, count: int) -> dict[str, dict]:
     per: dict[str, list[tuple[int, int]]] = {}
     with open(_one(directory, "_kernel_trace.csv")) as f:
         for r in csv.DictReader(f):
-            per.setdefault(r["Kernel_Name"], []).append(
+            per.setdefault(short_name(r["Kernel_Name"]), []).append(
                 (int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
     out = {}
     for k, ds in per.items():
@@ -98,7 +120,7 @@ def read_counters(directory) -> tuple[dict[str, dict[str, float]], dict[str, dic
     spans: dict[str, dict[str, int]] = {}  # kernel -> dispatch id -> duration (ns)
     with open(_one(directory, "_counter_collection.csv")) as f:
         for r in csv.DictReader(f):
-            k = r["Kernel_Name"]
+            k = short_name(r["Kernel_Name"])
             vals.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
             info.setdefault(k, {"lds": int(r["LDS_Block_Size"]), "scratch": int(r["Scratch_Size"]),
                                 "workgroup": int(r["Workgroup_Size"]), "grid": int(r["Grid_Size"])})

@@ -97,6 +97,29 @@ int cta_flash_attention_bwd(const float* q, const int64_t* q_strides,
                             float* dq, float* dk, float* dv, float* delta,
                             float* workspace, int64_t workspace_bytes, void* stream);
 
+/* Bytes of BF16 dS workspace for cta_flash_attention_bwd_bf16: B*nh*ceil(T/32)^2*2 KiB, or
+ * about half of that when causal.  0 for empty or unsupported shapes (hs not in {64, 128}). */
+int64_t cta_flash_attention_bwd_bf16_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs,
+                                               int causal);
+
+/* Backward with BF16 Q, K, V, O, dO (uint16_t bit patterns) and FP32 L: delta (FP32, caller
+ * scratch of B*nh*T floats), then dK/dV storing BF16 dS tiles and dQ from them, chunked over
+ * heads to fit workspace_bytes (at least one head's share of
+ * cta_flash_attention_bwd_bf16_workspace(), else CTA_ERR_INVALID_ARGUMENT).  dq/dk/dv dense
+ * (B,nh,T,hs) BF16.  hs in {64, 128}; strides as for cta_flash_attention_fwd_bf16.  P and dS
+ * are rounded to BF16 as MFMA operands; accumulation is FP32; deterministic.  No counterpart
+ * in the reference's launchers (reduced precision is on its roadmap, README.md:277); the
+ * semantics are those of flash_attention_bwd (flash_attn_launcher.cu:67-142). */
+int cta_flash_attention_bwd_bf16(const uint16_t* q, const int64_t* q_strides,
+                                 const uint16_t* k, const int64_t* k_strides,
+                                 const uint16_t* v, const int64_t* v_strides,
+                                 const uint16_t* o, const int64_t* o_strides,
+                                 const uint16_t* d_o, const int64_t* do_strides,
+                                 const float* l, const int64_t* l_strides,
+                                 int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                                 uint16_t* dq, uint16_t* dk, uint16_t* dv, float* delta,
+                                 void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Stage 1 of the backward: delta[b,h,t] = sum_d O*dO, dense (B,nh,T).
  * Replaces the flash_attention_bwd_delta launch (flash_attn_launcher.cu:107-108). */
 int cta_flash_attention_bwd_delta(const float* o, const int64_t* o_strides,

@@ -102,3 +102,110 @@ def test_fa2_bf16_errors(cuda):
     q = torch.randn(1, 2, 16, 64, device=cuda, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="all be bfloat16"):
         flash_attention_fwd(q, q.float(), q, False)
+
+
+# ---------------------------------------------------------------- backward
+# The oracle backward runs in float64 on the bf16-rounded q, k, v, dO with the exact O and L.
+# The kernel rounds P and dS to bf16 as MFMA operands (2^-9 relative each), forms delta from
+# its bf16 O, and rounds the gradients to bf16 on output.  dV carries only the P rounding and
+# its own output rounding; dQ and dK also the dS rounding, where dP - delta can cancel.  Bounds
+# on the relative L2 error: 1.5e-2 for dV, 3e-2 for dQ and dK.
+BWD_SHAPES = [
+    (1, 4, 256, 64, True),   # benchmark config 1
+    (1, 4, 256, 64, False),  # benchmark config 1
+    (1, 1, 65, 64, True),
+    (2, 4, 257, 64, True),
+    (1, 2, 200, 128, False),
+    (1, 2, 512, 128, True),
+    (1, 3, 1, 64, True),
+    (2, 2, 1000, 64, False),
+]
+
+
+def _bwd_check(grads, q, k, v, do, causal):
+    from conftest import rel_err
+
+    O_ref, L_ref = ora.reference_attention(f64(q), f64(k), f64(v), causal)
+    refs = ora.fa2_backward(f64(q), f64(k), f64(v), O_ref, f64(do), L_ref, causal, br=64, bc=64)
+    errs = []
+    for got, ref, tol in zip(grads, refs, (3e-2, 3e-2, 1.5e-2)):
+        assert got.dtype == torch.bfloat16
+        scale = 1e-6 * np.sqrt(ref.size)
+        if np.linalg.norm(ref) <= scale:  # e.g. dQ for T = 1 is exactly zero
+            assert np.linalg.norm(f64(got) - ref) <= 1e-3 * np.sqrt(ref.size)
+            errs.append(0.0)
+            continue
+        e = rel_err(f64(got), ref)
+        assert e <= tol, (e, tol)
+        errs.append(e)
+    return errs
+
+
+@pytest.mark.parametrize("B,nh,T,hs,causal", BWD_SHAPES)
+def test_fa2_bf16_backward_matches_oracle(cuda, B, nh, T, hs, causal):
+    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+
+    q, k, v = _bf16_inputs(B, nh, T, hs, seed=5000 + T + hs)
+    do = seeded((B, nh, T, hs), 9000 + T, kind="rand").to(torch.bfloat16)
+    qg, kg, vg = q.to(cuda), k.to(cuda), v.to(cuda)
+    O, L = flash_attention_fwd(qg, kg, vg, causal)
+    grads = flash_attention_bwd(qg, kg, vg, O, do.to(cuda), L, causal)
+    torch.cuda.synchronize()
+    _bwd_check([g.cpu() for g in grads], q, k, v, do, causal)
+
+
+def test_fa2_bf16_autograd_and_torch_bf16_error(cuda):
+    """CudaFlashAttention with bf16 leaves: bf16 gradients within the bounds above, and no
+    more than twice the error of torch's own bf16 SDPA backward (CPU) on the same inputs."""
+    import torch.nn.functional as F
+
+    from cuda_autograd_fns import CudaFlashAttention
+    from conftest import rel_err
+
+    B, nh, T, hs, causal = 1, 4, 256, 64, True
+    q, k, v = _bf16_inputs(B, nh, T, hs, seed=41)
+    do = seeded((B, nh, T, hs), 42, kind="rand").to(torch.bfloat16)
+    leaves = [t.to(cuda).requires_grad_() for t in (q, k, v)]
+    o, _l = CudaFlashAttention.apply(*leaves, causal)
+    o.backward(do.to(cuda))
+    ours = _bwd_check([t.grad.cpu() for t in leaves], q, k, v, do, causal)
+
+    tq, tk, tv = (t.clone().requires_grad_() for t in (q, k, v))
+    F.scaled_dot_product_attention(tq, tk, tv, is_causal=causal).backward(do)
+    O_ref, L_ref = ora.reference_attention(f64(q), f64(k), f64(v), causal)
+    refs = ora.fa2_backward(f64(q), f64(k), f64(v), O_ref, f64(do), L_ref, causal, br=64, bc=64)
+    theirs = [rel_err(f64(t.grad), r) for t, r in zip((tq, tk, tv), refs)]
+    for a, b in zip(ours, theirs):
+        assert a <= 2.0 * b + 1e-3, (ours, theirs)
+
+
+def test_fa2_bf16_backward_chunked_matches_full(cuda):
+    """The head-chunked stored-dS schedule (a workspace of one head) gives the same bits as the
+    full workspace."""
+    import ctypes
+
+    from cuda_transformer_amd import capi
+
+    B, nh, T, hs = 2, 3, 300, 64
+    q, k, v = (t.to(cuda) for t in _bf16_inputs(B, nh, T, hs, seed=61))
+    from cuda_transformer.ops import flash_attention_fwd
+    O, L = flash_attention_fwd(q, k, v, True)
+    do = torch.rand(B, nh, T, hs, device=cuda).to(torch.bfloat16)
+    lib = capi.lib()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    s4, s3 = capi.strides(q.stride()), capi.strides(L.stride())
+    outs = []
+    for heads in (B * nh, 1):
+        ws_bytes = lib.cta_flash_attention_bwd_bf16_workspace(1, 1, T, hs, 1) * heads
+        ws = torch.empty(ws_bytes // 4 + 4, device=cuda)
+        dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+        delta = torch.empty(B, nh, T, device=cuda)
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = lib.cta_flash_attention_bwd_bf16(P(q), s4, P(k), s4, P(v), s4, P(O), s4, P(do), s4,
+                                              P(L), s3, B, nh, T, hs, 1, P(dq), P(dk), P(dv),
+                                              P(delta), P(ws), ws_bytes, st)
+        assert rc == 0, lib.cta_last_error()
+        outs.append((dq, dk, dv))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)

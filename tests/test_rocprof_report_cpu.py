@@ -120,3 +120,15 @@ def test_trace_window(tmp_path):
     assert row.avg_ms == pytest.approx(2.0) and row.calls == 3
     text = rr.render([row], "T", window=(1, 3))
     assert "dispatches 1..3" in text and "| k | 5 | 4.8000 |" in text
+
+
+def test_short_name_of_mangled_kernels():
+    """rocprofv3 leaves kernels over __bf16 mangled; the report shortens them like the rest."""
+    from cuda_transformer_amd.rocprof_report import short_name
+
+    mangled = ("_ZN3cta12_GLOBAL__N_119fa2_fwd_bf16_kernelILi64ELb0EEEvPKDF16bS3_S3_PDF16bPfiiii"
+               "NS0_11RowStridesBES6_S6_fff")
+    assert short_name(mangled) == "fa2_fwd_bf16_kernel"
+    assert short_name("_Z6foobarv") == "foobar"
+    assert short_name("fa2_fwd_kernel") == "fa2_fwd_kernel"
+    assert short_name("__amd_rocclr_copyBuffer") == "__amd_rocclr_copyBuffer"
