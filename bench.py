@@ -41,7 +41,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
-MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense; FP16 is the same
 HBM_PEAK_GBPS = 8000.0
 METRIC = "FA2 fwd+bwd FP32 TFLOPS @B4 H32 N4096 D64 causal; % of FP32 MFMA peak"
 # The reference's own numbers for this exact configuration (RTX 5070, README.md:60-67,197):
@@ -52,12 +52,13 @@ REFERENCE_RTX5070_MS = {"fwd": 212.73, "bwd": 1259.32}
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--workload", choices=["fa2", "fa2-sweep", "ops", "gpt", "fa2-bf16"],
+    p.add_argument("--workload", choices=["fa2", "fa2-sweep", "ops", "gpt", "fa2-bf16", "fa2-f16"],
                    default="fa2",
                    help="fa2: the headline step (default, one JSON line); fa2-sweep: benchmark "
                         "config 3; ops: benchmark config 4 (one JSON line per op); gpt: benchmark "
-                        "config 5 training step; fa2-bf16: the BF16 forward and backward at the "
-                        "config-2 shape, causal and full (an extension beyond the FP32 metric)")
+                        "config 5 training step; fa2-bf16 / fa2-f16: the BF16 / FP16 forward and "
+                        "backward at the config-2 shape, causal and full (an extension beyond "
+                        "the FP32 metric)")
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--batch", type=int, default=4)
@@ -331,12 +332,13 @@ def fa2_sweep(args):
     return 0
 
 
-def fa2_bf16_workload(args):
-    """The BF16 FlashAttention-2 step at the config-2 shape, causal and non-causal: forward
-    (cta_flash_attention_fwd_bf16) and backward (cta_flash_attention_bwd_bf16: delta, dK/dV
-    storing BF16 dS, dQ from dS), each timed with HIP events on torch's current stream with
-    inputs in HBM.  TFLOPS by the reference's formula (forward 4*B*H*N^2*D, halved when causal;
-    backward 2.5x), against the 2.5 PFLOP/s dense BF16 MFMA peak.  One JSON line per mask."""
+def fa2_half_workload(args, kind):
+    """The 16-bit FlashAttention-2 step (kind "bf16" or "f16") at the config-2 shape, causal and
+    non-causal: forward (cta_flash_attention_fwd_<kind>) and backward
+    (cta_flash_attention_bwd_<kind>: delta, dK/dV storing 16-bit dS, dQ from dS), each timed
+    with HIP events on torch's current stream with inputs in HBM.  TFLOPS by the reference's
+    formula (forward 4*B*H*N^2*D, halved when causal; backward 2.5x), against the 2.5 PFLOP/s
+    dense BF16/FP16 MFMA peak.  One JSON line per mask."""
     import torch
 
     from cuda_transformer_amd import capi
@@ -344,31 +346,34 @@ def fa2_bf16_workload(args):
     B, H, N, D = args.batch, args.heads, args.seq, args.head_dim
     dev = torch.device("cuda", 0)
     gen = torch.Generator().manual_seed(0)
-    q, k, v = (torch.randn(B, H, N, D, generator=gen).to(torch.bfloat16).to(dev) for _ in range(3))
-    do = torch.randn(B, H, N, D, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+    dt = torch.bfloat16 if kind == "bf16" else torch.float16
+    q, k, v = (torch.randn(B, H, N, D, generator=gen).to(dt).to(dev) for _ in range(3))
+    do = torch.randn(B, H, N, D, generator=torch.Generator().manual_seed(1)).to(dt).to(dev)
     O = torch.empty_like(q)
     L = torch.empty(B, H, N, device=dev)
     dq, dk, dv = (torch.empty_like(q) for _ in range(3))
     delta = torch.empty(B, H, N, device=dev)
     lib = capi.lib()
+    fwd_fn = getattr(lib, f"cta_flash_attention_fwd_{kind}")
+    bwd_fn = getattr(lib, f"cta_flash_attention_bwd_{kind}")
+    ws_fn = getattr(lib, f"cta_flash_attention_bwd_{kind}_workspace")
     st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     s4, s3 = capi.strides(q.stride()), capi.strides(L.stride())
     vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     masks = {"both": (True, False), "causal": (True,), "full": (False,)}[args.masks]
     for causal in masks:
-        ws_bytes = lib.cta_flash_attention_bwd_bf16_workspace(B, H, N, D, int(causal))
+        ws_bytes = ws_fn(B, H, N, D, int(causal))
         ws = torch.empty(ws_bytes // 4 + 4, device=dev)
 
         def fwd():
-            if lib.cta_flash_attention_fwd_bf16(vp(q), s4, vp(k), s4, vp(v), s4, B, H, N, D,
-                                                int(causal), vp(O), vp(L), st) != 0:
+            if fwd_fn(vp(q), s4, vp(k), s4, vp(v), s4, B, H, N, D, int(causal), vp(O), vp(L),
+                      st) != 0:
                 raise RuntimeError(lib.cta_last_error().decode())
 
         def bwd():
-            if lib.cta_flash_attention_bwd_bf16(vp(q), s4, vp(k), s4, vp(v), s4, vp(O), s4,
-                                                vp(do), s4, vp(L), s3, B, H, N, D, int(causal),
-                                                vp(dq), vp(dk), vp(dv), vp(delta), vp(ws),
-                                                ws_bytes, st) != 0:
+            if bwd_fn(vp(q), s4, vp(k), s4, vp(v), s4, vp(O), s4, vp(do), s4, vp(L), s3, B, H,
+                      N, D, int(causal), vp(dq), vp(dk), vp(dv), vp(delta), vp(ws), ws_bytes,
+                      st) != 0:
                 raise RuntimeError(lib.cta_last_error().decode())
         fwd_ms = _time_kernel(fwd, max(10, args.steps), warm_s=0.2)
         fwd()
@@ -377,11 +382,12 @@ def fa2_bf16_workload(args):
         ftf, btf = fl / (fwd_ms * 1e-3) / 1e12, bfl / (bwd_ms * 1e-3) / 1e12
         stf = (fl + bfl) / ((fwd_ms + bwd_ms) * 1e-3) / 1e12
         print(json.dumps({
-            "workload": f"FA2 BF16 fwd+bwd B{B} H{H} N{N} D{D} {'causal' if causal else 'non-causal'}",
-            "metric": "FA2 BF16 fwd+bwd TFLOPS", "value": round(stf, 2), "unit": "TFLOPS",
+            "workload": f"FA2 {kind.upper()} fwd+bwd B{B} H{H} N{N} D{D} "
+                        f"{'causal' if causal else 'non-causal'}",
+            "metric": f"FA2 {kind.upper()} fwd+bwd TFLOPS", "value": round(stf, 2), "unit": "TFLOPS",
             "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
             "fwd_tflops": round(ftf, 2), "bwd_tflops": round(btf, 2),
-            "dtype": "bf16 inputs, fp32 accumulation",
+            "dtype": f"{kind} inputs, fp32 accumulation",
             "roofline": {"bound": "mfma", "achieved": round(stf, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(stf / MFMA_BF16_PEAK_TFLOPS, 4),
                          "algorithmic_per_launch": fl + bfl},
@@ -670,8 +676,8 @@ def main():
         return fa2_sweep(args)
     if args.workload == "gpt":
         return gpt_workload(args)
-    if args.workload == "fa2-bf16":
-        return fa2_bf16_workload(args)
+    if args.workload in ("fa2-bf16", "fa2-f16"):
+        return fa2_half_workload(args, args.workload[4:])
     B, H, N, D = args.batch, args.heads, args.seq, args.head_dim
     causal = not args.non_causal
     ms_step, per_kernel, (q, k, v, do) = fa2_timings(B, H, N, D, causal, args.steps, args.warmup,

@@ -42,13 +42,33 @@ __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast
 __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
 __device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
 
-// BF16 MFMA (gfx950 v_mfma_f32_32x32x16_bf16), checked on an MI355X:
+// 16-bit MFMA (gfx950 v_mfma_f32_32x32x16_bf16 / _f16), checked on an MI355X for BF16 and
+// shared by the FP16 form:
 //   A (32 x 16): lane l supplies A[l % 32][8 (l/32) + j], j = 0..7
 //   B (16 x 32): lane l supplies B[8 (l/32) + j][l % 32]
 //   D: the 32x32 layout of the FP32 MFMA above.
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+// Half16<E> carries the 8-element operand type and the MFMA for E = __bf16 or _Float16.
+template <class E>
+struct Half16;
+template <>
+struct Half16<__bf16> {
+  typedef __bf16 vec8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16 mfma(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Half16<_Float16> {
+  typedef _Float16 vec8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16 mfma(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <class E>
+using vec8_t = typename Half16<E>::vec8;
+template <class E>
+__device__ __forceinline__ vec8_t<E> ld8(const E* p) {
+  return *reinterpret_cast<const vec8_t<E>*>(p);
 }
 // A 32x32 score tile in registers (lane l: rows R(r, l/32)) is the B operand of two 16-deep
 // BF16 MFMA steps: step s takes registers 8s .. 8s+7, i.e. rows 16 s + 8 (j/4) + 4 h + j%4 of
@@ -56,9 +76,6 @@ __device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
 // rows adjacent: store row k of the image at position kt_pos(k), bits 2 and 3 of k swapped.
 __device__ __forceinline__ constexpr int kt_pos(int k) {
   return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
-}
-__device__ __forceinline__ bf16x8 ld_bf16x8(const __bf16* p) {
-  return *reinterpret_cast<const bf16x8*>(p);
 }
 
 // Exchange with the lane 32 positions away (the other half of the wave).

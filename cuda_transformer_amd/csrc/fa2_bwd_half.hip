@@ -1,5 +1,7 @@
-// FlashAttention-2 backward with BF16 Q, K, V, O, dO (FP32 L), FP32 accumulation, CDNA4 MFMA
-// (v_mfma_f32_32x32x16_bf16).  dQ, dK, dV are written in BF16.
+// FlashAttention-2 backward with 16-bit (BF16 or FP16) Q, K, V, O, dO (FP32 L), FP32
+// accumulation, CDNA4 MFMA (v_mfma_f32_32x32x16_bf16 / _f16).  dQ, dK, dV are written in the
+// input type.  Written for BF16; the FP16 instance differs only in the element type and the
+// MFMA (Half16<E>), and stores dS in FP16.
 //
 // The semantics are those of the FP32 backward (Transformer_kernels/flash_attention.cuh:175-504):
 //   delta_i = sum_d O_id dO_id,  P_ij = e^{S_ij - L_i},  dP_ij = dO_i . v_j,
@@ -10,7 +12,7 @@
 // dK/dV stage that also writes every dS tile, then dQ = s dS K from the stored tiles; both
 // stages are atomics-free and deterministic.
 //
-// gfx950 layout (the BF16 forward's trick, see fa2_fwd_bf16.hip):
+// gfx950 layout (the 16-bit forward's trick, see fa2_fwd_half.hip):
 //  * dK/dV: a wave owns 32 key rows and keeps k, v of its key row in registers as the B
 //    operands of S = Q K^T and dP = dO V^T, read row-wise from [query][d] images of the Q and
 //    dO tiles.  S and dP then hold one key per lane; P and dS, rounded to BF16, are the B
@@ -31,13 +33,13 @@ struct RowStridesH {
   int64_t b, h, t;  // element strides of the batch, head and time axes (d-stride is 1)
 };
 
-constexpr int kDsTileBf16 = 1024;  // bf16 elements of one stored 32x32 dS tile
+constexpr int kDsTileHalf = 1024;  // 16-bit elements of one stored 32x32 dS tile
 
 // ------------------------------------------------------------------------------------
 // delta = rowsum(O * dO), FP32 from BF16 rows; G = hs/8 lanes per row, 16 bytes each.
-template <int HS>
-__global__ __launch_bounds__(256) void fa2_bwd_delta_bf16_kernel(const __bf16* __restrict__ O,
-                                                                 const __bf16* __restrict__ dO,
+template <class E, int HS>
+__global__ __launch_bounds__(256) void fa2_bwd_delta_half_kernel(const E* __restrict__ O,
+                                                                 const E* __restrict__ dO,
                                                                  float* __restrict__ delta,
                                                                  int nh, int T, int64_t rows,
                                                                  RowStridesH so,
@@ -51,8 +53,8 @@ __global__ __launch_bounds__(256) void fa2_bwd_delta_bf16_kernel(const __bf16* _
     const int64_t bh = row / T;
     const int t = (int)(row - bh * T);
     const int64_t b = bh / nh, h = bh - b * nh;
-    const bf16x8 o = ld_bf16x8(O + b * so.b + h * so.h + (int64_t)t * so.t + 8 * c8);
-    const bf16x8 g = ld_bf16x8(dO + b * sdo.b + h * sdo.h + (int64_t)t * sdo.t + 8 * c8);
+    const vec8_t<E> o = ld8<E>(O + b * so.b + h * so.h + (int64_t)t * so.t + 8 * c8);
+    const vec8_t<E> g = ld8<E>(dO + b * sdo.b + h * sdo.h + (int64_t)t * sdo.t + 8 * c8);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc = fmaf((float)o[e], (float)g[e], acc);
   }
@@ -65,18 +67,18 @@ __global__ __launch_bounds__(256) void fa2_bwd_delta_bf16_kernel(const __bf16* _
 // dK, dV and the stored dS tiles.  Workgroup = 128 key rows (4 waves x 32); query stages of 32
 // rows, global -> registers -> LDS, double buffered, one barrier per stage.  Heads
 // [bh_base, bh_base + BH); the dS tiles go to dsw, heads indexed from bh_base.
-template <int HS, bool CAUSAL>
-__global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kernel(
-    const __bf16* __restrict__ Q, const __bf16* __restrict__ K, const __bf16* __restrict__ V,
-    const __bf16* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
-    __bf16* __restrict__ dK, __bf16* __restrict__ dV, __bf16* __restrict__ dsw, int nh, int T,
+template <class E, int HS, bool CAUSAL>
+__global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_half_kernel(
+    const E* __restrict__ Q, const E* __restrict__ K, const E* __restrict__ V,
+    const E* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
+    E* __restrict__ dK, E* __restrict__ dV, E* __restrict__ dsw, int nh, int T,
     int bh_base, int BH, int n_ktiles, RowStridesH sq, RowStridesH sk, RowStridesH sv,
     RowStridesH sdo, RowStridesH sl, float scale, float scale_log2) {
   constexpr int BN = 32;             // query rows per stage
   constexpr int BM = 128;            // key rows per workgroup
-  constexpr int RP = HS + 8;         // bf16 pitch of a row image: conflict-free 16-byte reads
-  constexpr int TP = BN + 8;         // bf16 pitch of a transposed image row (one d)
-  constexpr int XP = 32 + 8;         // bf16 pitch of the dS transpose
+  constexpr int RP = HS + 8;         // 16-bit pitch of a row image: conflict-free 16-byte reads
+  constexpr int TP = BN + 8;         // 16-bit pitch of a transposed image row (one d)
+  constexpr int XP = 32 + 8;         // 16-bit pitch of the dS transpose
   constexpr int CH = HS / 8;         // 16-byte chunks per row
   constexpr int LOADS = BN * CH / 256;
   constexpr int QS = HS / 16;        // MFMA steps over d
@@ -101,13 +103,13 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kerne
   const int bh = bh_base + bh_local;
   const int b = bh / nh, h = bh - b * nh;
 
-  const __bf16* Qb = Q + b * sq.b + h * sq.h;
-  const __bf16* dOb = dO + b * sdo.b + h * sdo.h;
+  const E* Qb = Q + b * sq.b + h * sq.h;
+  const E* dOb = dO + b * sdo.b + h * sdo.h;
   const float* Lb = Lg + b * sl.b + h * sl.h;
   const float* Db = delta + (int64_t)bh * T;
   const int nb = (T + 31) / 32;
-  __bf16* xw = reinterpret_cast<__bf16*>(smem + 2 * STAGE + wave * XPOSE);
-  __bf16* dsh = dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileBf16;
+  E* xw = reinterpret_cast<E*>(smem + 2 * STAGE + wave * XPOSE);
+  E* dsh = dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileHalf;
 
   const int n_pass = (CAUSAL && n_ktiles - 1 - p != p) ? 2 : 1;
   for (int pass = 0; pass < n_pass; ++pass) {
@@ -116,20 +118,20 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kerne
   const int my_j = j0 + col;
 
   // k and v of this lane's key row, d = 16 s + 8 half + 0..7 for step s.
-  bf16x8 kf[QS], vf[QS];
+  vec8_t<E> kf[QS], vf[QS];
   if (my_j < T) {
-    const __bf16* kp = K + b * sk.b + h * sk.h + (int64_t)my_j * sk.t + 8 * half;
-    const __bf16* vp = V + b * sv.b + h * sv.h + (int64_t)my_j * sv.t + 8 * half;
+    const E* kp = K + b * sk.b + h * sk.h + (int64_t)my_j * sk.t + 8 * half;
+    const E* vp = V + b * sv.b + h * sv.h + (int64_t)my_j * sv.t + 8 * half;
 #pragma unroll
     for (int s = 0; s < QS; ++s) {
-      kf[s] = ld_bf16x8(kp + 16 * s);
-      vf[s] = ld_bf16x8(vp + 16 * s);
+      kf[s] = ld8<E>(kp + 16 * s);
+      vf[s] = ld8<E>(vp + 16 * s);
     }
   } else {
 #pragma unroll
     for (int s = 0; s < QS; ++s)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) { kf[s][j] = (__bf16)0.0f; vf[s][j] = (__bf16)0.0f; }
+      for (int j = 0; j < 8; ++j) { kf[s][j] = (E)0.0f; vf[s][j] = (E)0.0f; }
   }
 
   f32x16 dkacc[HS / 32], dvacc[HS / 32];
@@ -166,18 +168,18 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kerne
   };
   auto lstore = [&](int buf) {
     unsigned char* base = smem + buf * STAGE;
-    __bf16* qr = reinterpret_cast<__bf16*>(base);
-    __bf16* gr = reinterpret_cast<__bf16*>(base + OFF_GR);
-    __bf16* qt = reinterpret_cast<__bf16*>(base + OFF_QT);
-    __bf16* gt = reinterpret_cast<__bf16*>(base + OFF_GT);
+    E* qr = reinterpret_cast<E*>(base);
+    E* gr = reinterpret_cast<E*>(base + OFF_GR);
+    E* qt = reinterpret_cast<E*>(base + OFF_QT);
+    E* gt = reinterpret_cast<E*>(base + OFF_GT);
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int c = tid + 256 * u;
       const int r = c / CH, ch = c % CH;
       *reinterpret_cast<uint4*>(qr + r * RP + 8 * ch) = qst[u];
       *reinterpret_cast<uint4*>(gr + r * RP + 8 * ch) = gst[u];
-      const __bf16* qe = reinterpret_cast<const __bf16*>(&qst[u]);
-      const __bf16* ge = reinterpret_cast<const __bf16*>(&gst[u]);
+      const E* qe = reinterpret_cast<const E*>(&qst[u]);
+      const E* ge = reinterpret_cast<const E*>(&gst[u]);
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         qt[(8 * ch + t) * TP + kt_pos(r)] = qe[t];
@@ -196,12 +198,12 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kerne
   auto flush = [&](int stage) {
     const int ii0 = stage * BN;
     if (!live(ii0)) return;
-    __bf16* gtile = dsh + ds_tile_index(ii0 / 32, j0 / 32, nb, CAUSAL) * kDsTileBf16;
+    E* gtile = dsh + ds_tile_index(ii0 / 32, j0 / 32, nb, CAUSAL) * kDsTileHalf;
     wave_lds_fence();
 #pragma unroll
     for (int s = 0; s < 2; ++s)
-      *reinterpret_cast<bf16x8*>(gtile + 8 * (32 * (2 * s + half) + col)) =
-          ld_bf16x8(xw + col * XP + 16 * s + 8 * half);
+      *reinterpret_cast<vec8_t<E>*>(gtile + 8 * (32 * (2 * s + half) + col)) =
+          ld8<E>(xw + col * XP + 16 * s + 8 * half);
     wave_lds_fence();
   };
 
@@ -222,10 +224,10 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kerne
     if (i + 1 < n_steps) gload(stage_at(i + 1));
     if (wave_stores && i > 0) flush(stage_at(i - 1));
     const unsigned char* base = smem + buf * STAGE;
-    const __bf16* qr = reinterpret_cast<const __bf16*>(base);
-    const __bf16* gr = reinterpret_cast<const __bf16*>(base + OFF_GR);
-    const __bf16* qt = reinterpret_cast<const __bf16*>(base + OFF_QT);
-    const __bf16* gt = reinterpret_cast<const __bf16*>(base + OFF_GT);
+    const E* qr = reinterpret_cast<const E*>(base);
+    const E* gr = reinterpret_cast<const E*>(base + OFF_GR);
+    const E* qt = reinterpret_cast<const E*>(base + OFF_QT);
+    const E* gt = reinterpret_cast<const E*>(base + OFF_GT);
     const float* ls = reinterpret_cast<const float*>(base + OFF_L);
     const float* ds = reinterpret_cast<const float*>(base + OFF_D);
     const int ii0 = s_idx * BN;
@@ -235,10 +237,10 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kerne
       f32x16 sacc = zero16(), pacc = zero16();
 #pragma unroll
       for (int s = 0; s < QS; ++s)
-        sacc = mfma_bf16(ld_bf16x8(qr + col * RP + 16 * s + 8 * half), kf[s], sacc);
+        sacc = Half16<E>::mfma(ld8<E>(qr + col * RP + 16 * s + 8 * half), kf[s], sacc);
 #pragma unroll
       for (int s = 0; s < QS; ++s)
-        pacc = mfma_bf16(ld_bf16x8(gr + col * RP + 16 * s + 8 * half), vf[s], pacc);
+        pacc = Half16<E>::mfma(ld8<E>(gr + col * RP + 16 * s + 8 * half), vf[s], pacc);
 
       // P = e^{S - L}; masked entries (and, for the stored dS, key rows past T) are exactly 0.
       const bool need_mask = (CAUSAL && ii0 < j0 + 31) || (ii0 + 32 > T) || (j0 + 32 > T);
@@ -257,20 +259,20 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kerne
           sacc[r] = pr;
         }
       }
-      bf16x8 pb[2];
+      vec8_t<E> pb[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pb[r >> 3][r & 7] = (__bf16)sacc[r];
+      for (int r = 0; r < 16; ++r) pb[r >> 3][r & 7] = (E)sacc[r];
 
       // dV^T += dO^T P
 #pragma unroll
       for (int d = 0; d < HS / 32; ++d)
 #pragma unroll
         for (int s = 0; s < 2; ++s)
-          dvacc[d] = mfma_bf16(ld_bf16x8(gt + (d * 32 + col) * TP + 16 * s + 8 * half), pb[s],
+          dvacc[d] = Half16<E>::mfma(ld8<E>(gt + (d * 32 + col) * TP + 16 * s + 8 * half), pb[s],
                                dvacc[d]);
 
       // dS = P (dP - delta)
-      bf16x8 db[2];
+      vec8_t<E> db[2];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const float4 dv = ld4(ds + 8 * g + 4 * half);
@@ -278,7 +280,7 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kerne
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
-          db[r >> 3][r & 7] = (__bf16)(sacc[r] * (pacc[r] - dr[e]));
+          db[r >> 3][r & 7] = (E)(sacc[r] * (pacc[r] - dr[e]));
         }
       }
 
@@ -293,7 +295,7 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kerne
       for (int d = 0; d < HS / 32; ++d)
 #pragma unroll
         for (int s = 0; s < 2; ++s)
-          dkacc[d] = mfma_bf16(ld_bf16x8(qt + (d * 32 + col) * TP + 16 * s + 8 * half), db[s],
+          dkacc[d] = Half16<E>::mfma(ld8<E>(qt + (d * 32 + col) * TP + 16 * s + 8 * half), db[s],
                                dkacc[d]);
     }
 
@@ -303,17 +305,17 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kerne
   if (wave_stores && n_steps > 0) flush(stage_at(n_steps - 1));
 
   if (my_j < T) {
-    __bf16* kp = dK + ((int64_t)bh * T + my_j) * HS;
-    __bf16* vp = dV + ((int64_t)bh * T + my_j) * HS;
+    E* kp = dK + ((int64_t)bh * T + my_j) * HS;
+    E* vp = dV + ((int64_t)bh * T + my_j) * HS;
 #pragma unroll
     for (int d = 0; d < HS / 32; ++d) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        __bf16 k4[4], v4[4];
+        E k4[4], v4[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          k4[e] = (__bf16)(dkacc[d][4 * g + e] * scale);
-          v4[e] = (__bf16)dvacc[d][4 * g + e];
+          k4[e] = (E)(dkacc[d][4 * g + e] * scale);
+          v4[e] = (E)dvacc[d][4 * g + e];
         }
         const int dc = d * 32 + 8 * g + 4 * half;
         *reinterpret_cast<uint2*>(kp + dc) = *reinterpret_cast<const uint2*>(k4);
@@ -328,19 +330,19 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_bf16_kerne
 // dQ from the stored BF16 dS tiles: dQ^T += K^T dS^T.  Workgroup = 128 query rows (4 waves x
 // 32); key stages of 64 rows go to LDS transposed ([d][key]); each wave loads its own dS tiles
 // from the workspace straight into registers, one stage ahead.
-template <int HS, bool CAUSAL>
-__global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_bf16_kernel(
-    const __bf16* __restrict__ K, const __bf16* __restrict__ dsw, __bf16* __restrict__ dQ,
+template <class E, int HS, bool CAUSAL>
+__global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_half_kernel(
+    const E* __restrict__ K, const E* __restrict__ dsw, E* __restrict__ dQ,
     int nh, int T, int bh_base, int BH, int n_qtiles, RowStridesH sk, float scale) {
   constexpr int BN = 64;
   constexpr int NSUB = BN / 32;
   constexpr int BM = 128;
-  constexpr int KTP = BN + 8;  // bf16 pitch of a K^T row (one d, every key of the stage)
+  constexpr int KTP = BN + 8;  // 16-bit pitch of a K^T row (one d, every key of the stage)
   constexpr int TILE = HS * KTP;
   constexpr int CH = HS / 8;
   constexpr int LOADS = BN * CH / 256;
   static_assert(BN * CH % 256 == 0, "stage must split evenly over 256 threads");
-  __shared__ __attribute__((aligned(16))) __bf16 smem[2 * TILE];
+  __shared__ __attribute__((aligned(16))) E smem[2 * TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -352,9 +354,9 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_bf16_kern
   const int p = w - bh_local * per_head;
   const int bh = bh_base + bh_local;
   const int b = bh / nh, h = bh - b * nh;
-  const __bf16* Kb = K + b * sk.b + h * sk.h;
+  const E* Kb = K + b * sk.b + h * sk.h;
   const int nb = (T + 31) / 32;
-  const __bf16* dsh = dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileBf16;
+  const E* dsh = dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileHalf;
 
   const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
   for (int pass = 0; pass < n_pass; ++pass) {
@@ -384,28 +386,28 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_bf16_kern
     }
   };
   auto lstore = [&](int buf) {
-    __bf16* kt = smem + buf * TILE;
+    E* kt = smem + buf * TILE;
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int c = tid + 256 * u;
       const int r = c / CH, ch = c % CH;
-      const __bf16* e = reinterpret_cast<const __bf16*>(&kst[u]);
+      const E* e = reinterpret_cast<const E*>(&kst[u]);
 #pragma unroll
       for (int t = 0; t < 8; ++t) kt[(8 * ch + t) * KTP + r] = e[t];
     }
   };
   auto has_tile = [&](int jb) { return ib < nb && jb < nb && (!CAUSAL || jb <= ib); };
   const int ibc = min(ib, nb - 1);
-  auto dsload = [&](int stage, bf16x8 (&dr)[NSUB][2]) {
+  auto dsload = [&](int stage, vec8_t<E> (&dr)[NSUB][2]) {
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub) {
       const int jbc = min(stage * NSUB + sub, CAUSAL ? ibc : nb - 1);
-      const __bf16* src = dsh + ds_tile_index(ibc, jbc, nb, CAUSAL) * kDsTileBf16;
+      const E* src = dsh + ds_tile_index(ibc, jbc, nb, CAUSAL) * kDsTileHalf;
 #pragma unroll
-      for (int s = 0; s < 2; ++s) dr[sub][s] = ld_bf16x8(src + 8 * (32 * (2 * s + half) + col));
+      for (int s = 0; s < 2; ++s) dr[sub][s] = ld8<E>(src + 8 * (32 * (2 * s + half) + col));
     }
   };
-  auto compute = [&](int stage, const __bf16* kt, const bf16x8 (&dr)[NSUB][2]) {
+  auto compute = [&](int stage, const E* kt, const vec8_t<E> (&dr)[NSUB][2]) {
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub) {
       if (!has_tile(stage * NSUB + sub)) continue;
@@ -413,11 +415,11 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_bf16_kern
       for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int d = 0; d < HS / 32; ++d)
-          acc[d] = mfma_bf16(ld_bf16x8(kt + (d * 32 + col) * KTP + sub * 32 + 16 * s + 8 * half),
+          acc[d] = Half16<E>::mfma(ld8<E>(kt + (d * 32 + col) * KTP + sub * 32 + 16 * s + 8 * half),
                              dr[sub][s], acc[d]);
     }
   };
-  auto step = [&](int s, const bf16x8 (&cur)[NSUB][2], bf16x8 (&nxt)[NSUB][2]) {
+  auto step = [&](int s, const vec8_t<E> (&cur)[NSUB][2], vec8_t<E> (&nxt)[NSUB][2]) {
     const int buf = s & 1;
     gload(s + 1);
     dsload(s + 1, nxt);
@@ -426,7 +428,7 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_bf16_kern
     __syncthreads();
   };
 
-  bf16x8 dA[NSUB][2], dB[NSUB][2];
+  vec8_t<E> dA[NSUB][2], dB[NSUB][2];
   dsload(0, dA);
   gload(0);
   lstore(0);
@@ -438,14 +440,14 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_bf16_kern
   }
 
   if (my_i < T) {
-    __bf16* op = dQ + ((int64_t)bh * T + my_i) * HS;
+    E* op = dQ + ((int64_t)bh * T + my_i) * HS;
 #pragma unroll
     for (int d = 0; d < HS / 32; ++d) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        __bf16 q4[4];
+        E q4[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) q4[e] = (__bf16)(acc[d][4 * g + e] * scale);
+        for (int e = 0; e < 4; ++e) q4[e] = (E)(acc[d][4 * g + e] * scale);
         *reinterpret_cast<uint2*>(op + d * 32 + 8 * g + 4 * half) =
             *reinterpret_cast<const uint2*>(q4);
       }
@@ -456,13 +458,13 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_bf16_kern
 
 RowStridesH rsh(const int64_t* s) { return RowStridesH{s[0], s[1], s[2]}; }
 
-bool layout_bf16_ok(const void* p, const int64_t* s) {
+bool layout_half_ok(const void* p, const int64_t* s) {
   return p != nullptr && s != nullptr && aligned16(p) && s[3] == 1 && s[0] % 8 == 0 &&
          s[1] % 8 == 0 && s[2] % 8 == 0;
 }
 
 template <typename F>
-void dispatch_bf16(int64_t hs, int causal, F&& f) {
+void dispatch_half(int64_t hs, int causal, F&& f) {
   if (hs == 64) {
     if (causal) f.template operator()<64, true>();
     else f.template operator()<64, false>();
@@ -472,51 +474,48 @@ void dispatch_bf16(int64_t hs, int causal, F&& f) {
   }
 }
 
-}  // namespace
-}  // namespace cta
-
-using namespace cta;
-
-extern "C" int64_t cta_flash_attention_bwd_bf16_workspace(int64_t B, int64_t nh, int64_t T,
-                                                          int64_t hs, int causal) {
+int64_t bwd_half_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs, int causal) {
   if (B <= 0 || nh <= 0 || T <= 0 || (hs != 64 && hs != 128)) return 0;
-  return B * nh * ds_tiles_per_head(T, causal != 0) * kDsTileBf16 * 2;
+  return B * nh * ds_tiles_per_head(T, causal != 0) * kDsTileHalf * 2;
 }
 
-extern "C" int cta_flash_attention_bwd_bf16(
-    const uint16_t* q, const int64_t* q_strides, const uint16_t* k, const int64_t* k_strides,
-    const uint16_t* v, const int64_t* v_strides, const uint16_t* o, const int64_t* o_strides,
-    const uint16_t* d_o, const int64_t* do_strides, const float* l, const int64_t* l_strides,
-    int64_t B, int64_t nh, int64_t T, int64_t hs, int causal, uint16_t* dq, uint16_t* dk,
-    uint16_t* dv, float* delta, void* workspace, int64_t workspace_bytes, void* stream) {
+// The entry points' shared body; `what` names the element type in error messages.
+template <class E>
+int bwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
+             const int64_t* k_strides, const uint16_t* v, const int64_t* v_strides,
+             const uint16_t* o, const int64_t* o_strides, const uint16_t* d_o,
+             const int64_t* do_strides, const float* l, const int64_t* l_strides, int64_t B,
+             int64_t nh, int64_t T, int64_t hs, int causal, uint16_t* dq, uint16_t* dk,
+             uint16_t* dv, float* delta, void* workspace, int64_t workspace_bytes, void* stream,
+             const char* what) {
   if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
   if (hs == 32)
-    return fail(CTA_ERR_UNSUPPORTED_HEAD_DIM,
-                "flash_attention_bwd with bfloat16 inputs supports hs=64 and hs=128");
+    return fail(CTA_ERR_UNSUPPORTED_HEAD_DIM, std::string("flash_attention_bwd with ") + what +
+                                                  " inputs supports hs=64 and hs=128");
   if (B * nh * T == 0) return CTA_OK;
-  if (!layout_bf16_ok(q, q_strides) || !layout_bf16_ok(k, k_strides) ||
-      !layout_bf16_ok(v, v_strides) || !layout_bf16_ok(o, o_strides) ||
-      !layout_bf16_ok(d_o, do_strides))
-    return fail(CTA_ERR_LAYOUT,
-                "flash_attention_bwd (bfloat16) needs unit d-stride, strides divisible by 8 and "
-                "16-byte aligned Q/K/V/O/dO");
+  if (!layout_half_ok(q, q_strides) || !layout_half_ok(k, k_strides) ||
+      !layout_half_ok(v, v_strides) || !layout_half_ok(o, o_strides) ||
+      !layout_half_ok(d_o, do_strides))
+    return fail(CTA_ERR_LAYOUT, std::string("flash_attention_bwd (") + what +
+                                    ") needs unit d-stride, strides divisible by 8 and 16-byte "
+                                    "aligned Q/K/V/O/dO");
   if (!l || !l_strides || !delta) return fail(CTA_ERR_INVALID_ARGUMENT, "null L or delta pointer");
   if (!dq || !dk || !dv || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
       !aligned16(workspace))
     return fail(CTA_ERR_LAYOUT, "dQ/dK/dV and the workspace must be 16-byte aligned pointers");
-  const int64_t head_bytes = cta_flash_attention_bwd_bf16_workspace(1, 1, T, hs, causal);
+  const int64_t head_bytes = bwd_half_workspace(1, 1, T, hs, causal);
   if (workspace == nullptr || workspace_bytes < head_bytes)
-    return fail(CTA_ERR_INVALID_ARGUMENT,
-                "flash_attention_bwd (bfloat16) needs a dS workspace of at least one head");
-  const auto* qb = reinterpret_cast<const __bf16*>(q);
-  const auto* kb = reinterpret_cast<const __bf16*>(k);
-  const auto* vb = reinterpret_cast<const __bf16*>(v);
-  const auto* ob = reinterpret_cast<const __bf16*>(o);
-  const auto* gb = reinterpret_cast<const __bf16*>(d_o);
-  auto* dqb = reinterpret_cast<__bf16*>(dq);
-  auto* dkb = reinterpret_cast<__bf16*>(dk);
-  auto* dvb = reinterpret_cast<__bf16*>(dv);
-  auto* wsb = reinterpret_cast<__bf16*>(workspace);
+    return fail(CTA_ERR_INVALID_ARGUMENT, std::string("flash_attention_bwd (") + what +
+                                              ") needs a dS workspace of at least one head");
+  const auto* qb = reinterpret_cast<const E*>(q);
+  const auto* kb = reinterpret_cast<const E*>(k);
+  const auto* vb = reinterpret_cast<const E*>(v);
+  const auto* ob = reinterpret_cast<const E*>(o);
+  const auto* gb = reinterpret_cast<const E*>(d_o);
+  auto* dqb = reinterpret_cast<E*>(dq);
+  auto* dkb = reinterpret_cast<E*>(dk);
+  auto* dvb = reinterpret_cast<E*>(dv);
+  auto* wsb = reinterpret_cast<E*>(workspace);
   const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
   const RowStridesH sl{l_strides[0], l_strides[1], l_strides[2]};
   const int BH = (int)(B * nh);
@@ -525,12 +524,12 @@ extern "C" int cta_flash_attention_bwd_bf16(
   const int64_t rows = B * nh * T;
   const unsigned dgrid = (unsigned)((rows * (hs / 8) + 255) / 256);
   if (hs == 64)
-    hipLaunchKernelGGL(fa2_bwd_delta_bf16_kernel<64>, dim3(dgrid), dim3(256), 0, st, ob, gb, delta,
-                       (int)nh, (int)T, rows, rsh(o_strides), rsh(do_strides));
-  else
-    hipLaunchKernelGGL(fa2_bwd_delta_bf16_kernel<128>, dim3(dgrid), dim3(256), 0, st, ob, gb,
+    hipLaunchKernelGGL((fa2_bwd_delta_half_kernel<E, 64>), dim3(dgrid), dim3(256), 0, st, ob, gb,
                        delta, (int)nh, (int)T, rows, rsh(o_strides), rsh(do_strides));
-  if (int rc = check_launch("flash_attention_bwd_bf16 delta")) return rc;
+  else
+    hipLaunchKernelGGL((fa2_bwd_delta_half_kernel<E, 128>), dim3(dgrid), dim3(256), 0, st, ob, gb,
+                       delta, (int)nh, (int)T, rows, rsh(o_strides), rsh(do_strides));
+  if (int rc = check_launch("flash_attention_bwd (16-bit) delta")) return rc;
 
   // Chunks of equal head counts that fit the workspace.
   const int64_t fit = std::min<int64_t>(BH, workspace_bytes / head_bytes);
@@ -539,16 +538,53 @@ extern "C" int cta_flash_attention_bwd_bf16(
   const int n_tiles = (int)((T + 127) / 128);
   for (int h0 = 0; h0 < BH; h0 += chunk) {
     const int n = std::min(chunk, BH - h0);
-    dispatch_bf16(hs, causal, [&]<int HS, bool C>() {
+    dispatch_half(hs, causal, [&]<int HS, bool C>() {
       const int64_t items = (int64_t)(C ? (n_tiles + 1) / 2 : n_tiles) * n;
-      hipLaunchKernelGGL((fa2_bwd_dkdv_bf16_kernel<HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
+      hipLaunchKernelGGL((fa2_bwd_dkdv_half_kernel<E, HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
                          st, qb, kb, vb, gb, l, delta, dkb, dvb, wsb, (int)nh, (int)T, h0, n,
                          n_tiles, rsh(q_strides), rsh(k_strides), rsh(v_strides),
                          rsh(do_strides), sl, scale, scale * kLog2e);
-      hipLaunchKernelGGL((fa2_bwd_dq_ds_bf16_kernel<HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
+      hipLaunchKernelGGL((fa2_bwd_dq_ds_half_kernel<E, HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
                          st, kb, wsb, dqb, (int)nh, (int)T, h0, n, n_tiles, rsh(k_strides), scale);
     });
-    if (int rc = check_launch("flash_attention_bwd_bf16")) return rc;
+    if (int rc = check_launch("flash_attention_bwd (16-bit)")) return rc;
   }
   return CTA_OK;
+}
+
+}  // namespace
+}  // namespace cta
+
+using namespace cta;
+
+extern "C" int64_t cta_flash_attention_bwd_bf16_workspace(int64_t B, int64_t nh, int64_t T,
+                                                          int64_t hs, int causal) {
+  return bwd_half_workspace(B, nh, T, hs, causal);
+}
+
+extern "C" int cta_flash_attention_bwd_bf16(
+    const uint16_t* q, const int64_t* q_strides, const uint16_t* k, const int64_t* k_strides,
+    const uint16_t* v, const int64_t* v_strides, const uint16_t* o, const int64_t* o_strides,
+    const uint16_t* d_o, const int64_t* do_strides, const float* l, const int64_t* l_strides,
+    int64_t B, int64_t nh, int64_t T, int64_t hs, int causal, uint16_t* dq, uint16_t* dk,
+    uint16_t* dv, float* delta, void* workspace, int64_t workspace_bytes, void* stream) {
+  return bwd_half<__bf16>(q, q_strides, k, k_strides, v, v_strides, o, o_strides, d_o,
+                          do_strides, l, l_strides, B, nh, T, hs, causal, dq, dk, dv, delta,
+                          workspace, workspace_bytes, stream, "bfloat16");
+}
+
+extern "C" int64_t cta_flash_attention_bwd_f16_workspace(int64_t B, int64_t nh, int64_t T,
+                                                         int64_t hs, int causal) {
+  return bwd_half_workspace(B, nh, T, hs, causal);
+}
+
+extern "C" int cta_flash_attention_bwd_f16(
+    const uint16_t* q, const int64_t* q_strides, const uint16_t* k, const int64_t* k_strides,
+    const uint16_t* v, const int64_t* v_strides, const uint16_t* o, const int64_t* o_strides,
+    const uint16_t* d_o, const int64_t* do_strides, const float* l, const int64_t* l_strides,
+    int64_t B, int64_t nh, int64_t T, int64_t hs, int causal, uint16_t* dq, uint16_t* dk,
+    uint16_t* dv, float* delta, void* workspace, int64_t workspace_bytes, void* stream) {
+  return bwd_half<_Float16>(q, q_strides, k, k_strides, v, v_strides, o, o_strides, d_o,
+                            do_strides, l, l_strides, B, nh, T, hs, causal, dq, dk, dv, delta,
+                            workspace, workspace_bytes, stream, "float16");
 }

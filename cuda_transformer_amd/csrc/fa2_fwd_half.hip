@@ -1,14 +1,15 @@
-// FlashAttention-2 forward with BF16 Q, K, V and FP32 accumulation, CDNA4 MFMA
-// (v_mfma_f32_32x32x16_bf16).
+// FlashAttention-2 forward with 16-bit (BF16 or FP16) Q, K, V and FP32 accumulation, CDNA4
+// MFMA (v_mfma_f32_32x32x16_bf16 / _f16).  Written for BF16; the FP16 instance differs only in
+// the element type and the MFMA (Half16<E>).
 //
 // The reduced-precision variant the reference lists on its roadmap (README.md:277); the
 // semantics are those of the FP32 forward (Transformer_kernels/flash_attention.cuh:27-170):
 // O = softmax(s Q K^T) V with s = 1/sqrt(hs), the causal mask j > i, and L = m + ln l in FP32.
-// O is written in BF16, L in FP32.  Scores, the online-softmax statistics and the O
-// accumulator are FP32; the probabilities are rounded to BF16 as the P V operand, as in every
-// BF16 FlashAttention.
+// O is written in the input type, L in FP32.  Scores, the online-softmax statistics and the O
+// accumulator are FP32; the probabilities are rounded to the input type as the P V operand, as
+// in every 16-bit FlashAttention.
 //
-// gfx950 design (the FP32 kernel's layout trick carried to the 16-deep BF16 MFMA):
+// gfx950 design (the FP32 kernel's layout trick carried to the 16-deep 16-bit MFMA):
 //  * Workgroup = 128 query rows (4 waves x 32), K/V stages of 64 keys (two 32-key tiles),
 //    global -> registers -> LDS, double buffered, one barrier per stage.  Causal workgroups
 //    take query-tile pairs (n-1-p, p), head-major and XCD-contiguous, and the second pass walks
@@ -18,7 +19,7 @@
 //    one query per lane: lane l holds the scores of query l%32 for keys R(r, l/32),
 //    R(r, h) = 8 (r/4) + 4 h + r%4.
 //  * O^T += V^T P^T: for MFMA step s the B operand is the lane's registers r = 8s .. 8s+7,
-//    rounded to BF16, i.e. keys 16 s + 8 (j/4) + 4 h + j%4 for element j.  V is stored in LDS
+//    rounded to 16 bits, i.e. keys 16 s + 8 (j/4) + 4 h + j%4 for element j.  V is stored in LDS
 //    transposed, [d][key], with bits 2 and 3 of the key index swapped (kt_pos), so those eight
 //    keys are adjacent and the A operand is one 16-byte read.
 //  * Online softmax, lazy rescaling and the two-half max / sum exchange are the FP32 kernel's.
@@ -31,10 +32,10 @@ struct RowStridesB {
   int64_t b, h, t;  // element strides of the batch, head and time axes (d-stride is 1)
 };
 
-template <int HS, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
-    const __bf16* __restrict__ Q, const __bf16* __restrict__ K, const __bf16* __restrict__ V,
-    __bf16* __restrict__ O, float* __restrict__ L, int nh, int T, int BH, int n_qtiles,
+template <class E, int HS, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
+    const E* __restrict__ Q, const E* __restrict__ K, const E* __restrict__ V,
+    E* __restrict__ O, float* __restrict__ L, int nh, int T, int BH, int n_qtiles,
     RowStridesB sq, RowStridesB sk, RowStridesB sv, float scale, float scale_log2,
     float rescale_gap) {
   constexpr int BN = 64;             // keys per stage
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
   constexpr int LOADS = BN * CH / 256;
   constexpr int QS = HS / 16;        // MFMA steps of S over d
   static_assert(BN * CH % 256 == 0, "stage must split evenly over 256 threads");
-  __shared__ __attribute__((aligned(16))) __bf16 smem[2 * (KTILE + VTILE)];
+  __shared__ __attribute__((aligned(16))) E smem[2 * (KTILE + VTILE)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -60,9 +61,9 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
   const int p = w - bh * per_head;
   const int b = bh / nh, h = bh - b * nh;
 
-  const __bf16* Qb = Q + b * sq.b + h * sq.h;
-  const __bf16* Kb = K + b * sk.b + h * sk.h;
-  const __bf16* Vb = V + b * sv.b + h * sv.h;
+  const E* Qb = Q + b * sq.b + h * sq.h;
+  const E* Kb = K + b * sk.b + h * sk.h;
+  const E* Vb = V + b * sv.b + h * sv.h;
 
   const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
   for (int pass = 0; pass < n_pass; ++pass) {
@@ -71,16 +72,16 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
   const int my_i = i0 + col;
 
   // This lane's query row, d = 16 s + 8 half + 0..7 for step s.
-  bf16x8 qf[QS];
+  vec8_t<E> qf[QS];
   if (my_i < T) {
-    const __bf16* qp = Qb + (int64_t)my_i * sq.t + 8 * half;
+    const E* qp = Qb + (int64_t)my_i * sq.t + 8 * half;
 #pragma unroll
-    for (int s = 0; s < QS; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qp + 16 * s);
+    for (int s = 0; s < QS; ++s) qf[s] = *reinterpret_cast<const vec8_t<E>*>(qp + 16 * s);
   } else {
 #pragma unroll
     for (int s = 0; s < QS; ++s)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) qf[s][j] = (__bf16)0.0f;
+      for (int j = 0; j < 8; ++j) qf[s][j] = (E)0.0f;
   }
 
   f32x16 oacc[HS / 32];
@@ -109,14 +110,14 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
     }
   };
   auto lstore = [&](int buf) {
-    __bf16* ks = smem + buf * (KTILE + VTILE);
-    __bf16* vt = ks + KTILE;
+    E* ks = smem + buf * (KTILE + VTILE);
+    E* vt = ks + KTILE;
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int c = tid + 256 * u;
       const int r = c / CH, ch = c % CH;
       *reinterpret_cast<uint4*>(ks + r * KP + 8 * ch) = kst[u];
-      const __bf16* e = reinterpret_cast<const __bf16*>(&vst[u]);
+      const E* e = reinterpret_cast<const E*>(&vst[u]);
 #pragma unroll
       for (int t = 0; t < 8; ++t) vt[(8 * ch + t) * VP + kt_pos(r)] = e[t];
     }
@@ -132,8 +133,8 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
     const int s_idx = stage_at(i);
     const int buf = i & 1;
     if (i + 1 < n_stages) gload(stage_at(i + 1));
-    const __bf16* ks = smem + buf * (KTILE + VTILE);
-    const __bf16* vt = ks + KTILE;
+    const E* ks = smem + buf * (KTILE + VTILE);
+    const E* vt = ks + KTILE;
 
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub) {
@@ -143,10 +144,10 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
 
       // S^T tile: sacc[r] = q_{my_i} . k_{jj0 + R(r, half)}
       f32x16 sacc = zero16();
-      const __bf16* krow = ks + (sub * 32 + col) * KP + 8 * half;
+      const E* krow = ks + (sub * 32 + col) * KP + 8 * half;
 #pragma unroll
       for (int s = 0; s < QS; ++s)
-        sacc = mfma_bf16(*reinterpret_cast<const bf16x8*>(krow + 16 * s), qf[s], sacc);
+        sacc = Half16<E>::mfma(*reinterpret_cast<const vec8_t<E>*>(krow + 16 * s), qf[s], sacc);
 
       const bool need_mask = (CAUSAL && jj0 + 31 > i0) || (jj0 + 32 > T);
       if (need_mask) {
@@ -171,22 +172,22 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
       }
       const float mb = m_run * scale_log2;
       float psum = 0.0f;
-      bf16x8 pf[2];
+      vec8_t<E> pf[2];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float pr = fast_exp2(fmaf(sacc[r], scale_log2, -mb));
         psum += pr;
-        pf[r >> 3][r & 7] = (__bf16)pr;
+        pf[r >> 3][r & 7] = (E)pr;
       }
       l_run += psum;
 
       // O^T += V^T P^T over the tile's 32 keys, two 16-key MFMA steps per d block.
 #pragma unroll
       for (int d = 0; d < HS / 32; ++d) {
-        const __bf16* vrow = vt + (d * 32 + col) * VP + sub * 32 + 8 * half;
+        const E* vrow = vt + (d * 32 + col) * VP + sub * 32 + 8 * half;
 #pragma unroll
         for (int s = 0; s < 2; ++s)
-          oacc[d] = mfma_bf16(*reinterpret_cast<const bf16x8*>(vrow + 16 * s), pf[s], oacc[d]);
+          oacc[d] = Half16<E>::mfma(*reinterpret_cast<const vec8_t<E>*>(vrow + 16 * s), pf[s], oacc[d]);
       }
     }
 
@@ -196,15 +197,15 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
 
   const float l_tot = sum_halves(l_run);
   if (my_i < T) {
-    __bf16* op = O + ((int64_t)bh * T + my_i) * HS;
+    E* op = O + ((int64_t)bh * T + my_i) * HS;
     const float inv = 1.0f / l_tot;
 #pragma unroll
     for (int d = 0; d < HS / 32; ++d) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        __bf16 o4[4];
+        E o4[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(oacc[d][4 * g + e] * inv);
+        for (int e = 0; e < 4; ++e) o4[e] = (E)(oacc[d][4 * g + e] * inv);
         *reinterpret_cast<uint2*>(op + d * 32 + 8 * g + 4 * half) =
             *reinterpret_cast<const uint2*>(o4);
       }
@@ -214,21 +215,59 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_bf16_kernel(
   }  // pass: the K/V loop ended on a barrier, so the next pass may refill LDS
 }
 
-template <int HS, bool CAUSAL>
-void launch_fwd_bf16(const __bf16* q, const __bf16* k, const __bf16* v, __bf16* o, float* l,
-                     int nh, int T, int BH, RowStridesB sq, RowStridesB sk, RowStridesB sv,
-                     float scale, hipStream_t stream) {
+template <class E, int HS, bool CAUSAL>
+void launch_fwd_half(const E* q, const E* k, const E* v, E* o, float* l, int nh, int T, int BH,
+                     RowStridesB sq, RowStridesB sk, RowStridesB sv, float scale,
+                     hipStream_t stream) {
   const int n_qtiles = (T + 127) / 128;
   const unsigned grid = xcd_grid((int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH);
-  hipLaunchKernelGGL((fa2_fwd_bf16_kernel<HS, CAUSAL>), dim3(grid), dim3(256), 0, stream, q, k,
-                     v, o, l, nh, T, BH, n_qtiles, sq, sk, sv, scale, scale * kLog2e,
+  hipLaunchKernelGGL((fa2_fwd_half_kernel<E, HS, CAUSAL>), dim3(grid), dim3(256), 0, stream, q,
+                     k, v, o, l, nh, T, BH, n_qtiles, sq, sk, sv, scale, scale * kLog2e,
                      8.0f / (scale * kLog2e));
 }
 
-// BF16 operands: unit d-stride, (b, h, t) strides divisible by 8 elements, 16-byte aligned.
-bool attn_layout_bf16_ok(const void* p, const int64_t* s) {
+// 16-bit operands: unit d-stride, (b, h, t) strides divisible by 8 elements, 16-byte aligned.
+bool attn_layout_half_ok(const void* p, const int64_t* s) {
   return p != nullptr && s != nullptr && aligned16(p) && s[3] == 1 && s[0] % 8 == 0 &&
          s[1] % 8 == 0 && s[2] % 8 == 0;
+}
+
+// The entry points' shared body; `what` names the element type in error messages.
+template <class E>
+int fwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
+             const int64_t* k_strides, const uint16_t* v, const int64_t* v_strides, int64_t B,
+             int64_t nh, int64_t T, int64_t hs, int causal, uint16_t* o, float* l, void* stream,
+             const char* what) {
+  if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
+  if (hs == 32)
+    return fail(CTA_ERR_UNSUPPORTED_HEAD_DIM, std::string("flash_attention_fwd with ") + what +
+                                                  " inputs supports hs=64 and hs=128");
+  if (B * nh * T == 0) return CTA_OK;
+  if (!o || !l) return fail(CTA_ERR_INVALID_ARGUMENT, "null output pointer");
+  if (!attn_layout_half_ok(q, q_strides) || !attn_layout_half_ok(k, k_strides) ||
+      !attn_layout_half_ok(v, v_strides) || !aligned16(o))
+    return fail(CTA_ERR_LAYOUT, std::string("flash_attention_fwd (") + what +
+                                    ") needs unit d-stride, strides divisible by 8 and 16-byte "
+                                    "aligned Q/K/V/O");
+  const RowStridesB sq{q_strides[0], q_strides[1], q_strides[2]};
+  const RowStridesB sk{k_strides[0], k_strides[1], k_strides[2]};
+  const RowStridesB sv{v_strides[0], v_strides[1], v_strides[2]};
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  const int BH = (int)(B * nh);
+  hipStream_t st = as_stream(stream);
+  const auto* qb = reinterpret_cast<const E*>(q);
+  const auto* kb = reinterpret_cast<const E*>(k);
+  const auto* vb = reinterpret_cast<const E*>(v);
+  auto* ob = reinterpret_cast<E*>(o);
+#define CTA_FWD_HALF(HS_)                                                                     \
+  if (causal) launch_fwd_half<E, HS_, true>(qb, kb, vb, ob, l, (int)nh, (int)T, BH, sq, sk,   \
+                                            sv, scale, st);                                   \
+  else launch_fwd_half<E, HS_, false>(qb, kb, vb, ob, l, (int)nh, (int)T, BH, sq, sk, sv,     \
+                                      scale, st);
+  if (hs == 64) { CTA_FWD_HALF(64) }
+  else { CTA_FWD_HALF(128) }
+#undef CTA_FWD_HALF
+  return check_launch("flash_attention_fwd (16-bit)");
 }
 
 }  // namespace
@@ -241,33 +280,15 @@ extern "C" int cta_flash_attention_fwd_bf16(const uint16_t* q, const int64_t* q_
                                             const uint16_t* v, const int64_t* v_strides,
                                             int64_t B, int64_t nh, int64_t T, int64_t hs,
                                             int causal, uint16_t* o, float* l, void* stream) {
-  if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
-  if (hs == 32)
-    return fail(CTA_ERR_UNSUPPORTED_HEAD_DIM,
-                "flash_attention_fwd with bfloat16 inputs supports hs=64 and hs=128");
-  if (B * nh * T == 0) return CTA_OK;
-  if (!o || !l) return fail(CTA_ERR_INVALID_ARGUMENT, "null output pointer");
-  if (!attn_layout_bf16_ok(q, q_strides) || !attn_layout_bf16_ok(k, k_strides) ||
-      !attn_layout_bf16_ok(v, v_strides) || !aligned16(o))
-    return fail(CTA_ERR_LAYOUT,
-                "flash_attention_fwd (bfloat16) needs unit d-stride, strides divisible by 8 and "
-                "16-byte aligned Q/K/V/O");
-  const RowStridesB sq{q_strides[0], q_strides[1], q_strides[2]};
-  const RowStridesB sk{k_strides[0], k_strides[1], k_strides[2]};
-  const RowStridesB sv{v_strides[0], v_strides[1], v_strides[2]};
-  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
-  const int BH = (int)(B * nh);
-  hipStream_t st = as_stream(stream);
-  const auto* qb = reinterpret_cast<const __bf16*>(q);
-  const auto* kb = reinterpret_cast<const __bf16*>(k);
-  const auto* vb = reinterpret_cast<const __bf16*>(v);
-  auto* ob = reinterpret_cast<__bf16*>(o);
-#define CTA_FWD_BF16(HS_)                                                                     \
-  if (causal) launch_fwd_bf16<HS_, true>(qb, kb, vb, ob, l, (int)nh, (int)T, BH, sq, sk, sv,  \
-                                         scale, st);                                          \
-  else launch_fwd_bf16<HS_, false>(qb, kb, vb, ob, l, (int)nh, (int)T, BH, sq, sk, sv, scale, st);
-  if (hs == 64) { CTA_FWD_BF16(64) }
-  else { CTA_FWD_BF16(128) }
-#undef CTA_FWD_BF16
-  return check_launch("flash_attention_fwd_bf16");
+  return fwd_half<__bf16>(q, q_strides, k, k_strides, v, v_strides, B, nh, T, hs, causal, o, l,
+                          stream, "bfloat16");
+}
+
+extern "C" int cta_flash_attention_fwd_f16(const uint16_t* q, const int64_t* q_strides,
+                                           const uint16_t* k, const int64_t* k_strides,
+                                           const uint16_t* v, const int64_t* v_strides,
+                                           int64_t B, int64_t nh, int64_t T, int64_t hs,
+                                           int causal, uint16_t* o, float* l, void* stream) {
+  return fwd_half<_Float16>(q, q_strides, k, k_strides, v, v_strides, B, nh, T, hs, causal, o,
+                            l, stream, "float16");
 }

@@ -355,34 +355,40 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> causal_self_attention_bwd(
 }
 
 // ------------------------------------------------------------------ FlashAttention-2
-// BF16 inputs (an extension: the reference's kernels are FP32 only): O in BF16, L in FP32.
-bool attn_layout_bf16_ok(const at::Tensor& t) {
+// 16-bit inputs, bfloat16 or float16 (an extension: the reference's kernels are FP32 only):
+// O in the input type, L in FP32.
+bool is_half16(const at::Tensor& t) {
+  return t.scalar_type() == at::kBFloat16 || t.scalar_type() == at::kHalf;
+}
+
+bool attn_layout_half_ok(const at::Tensor& t) {
   const auto s = strides_of<4>(t);
   return (t.size(3) == 1 || t.stride(3) == 1) && s[0] % 8 == 0 && s[1] % 8 == 0 &&
          s[2] % 8 == 0 && (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) == 0;
 }
 
-at::Tensor attn_operand_bf16(const at::Tensor& t) {
-  if (attn_layout_bf16_ok(t)) return t;
+at::Tensor attn_operand_half(const at::Tensor& t) {
+  if (attn_layout_half_ok(t)) return t;
   at::Tensor c = t.contiguous();
-  if (!attn_layout_bf16_ok(c)) c = t.clone(at::MemoryFormat::Contiguous);
+  if (!attn_layout_half_ok(c)) c = t.clone(at::MemoryFormat::Contiguous);
   return c;
 }
 
-std::tuple<at::Tensor, at::Tensor> flash_attention_fwd_bf16(const at::Tensor& Q,
+std::tuple<at::Tensor, at::Tensor> flash_attention_fwd_half(const at::Tensor& Q,
                                                             const at::Tensor& K,
                                                             const at::Tensor& V, bool causal) {
   const int64_t B = Q.size(0), nh = Q.size(1), T = Q.size(2), hs = Q.size(3);
-  TORCH_CHECK(K.scalar_type() == at::kBFloat16 && V.scalar_type() == at::kBFloat16,
-              "Q, K and V must all be bfloat16 (or all float32)");
+  const bool bf = Q.scalar_type() == at::kBFloat16;
+  TORCH_CHECK(K.scalar_type() == Q.scalar_type() && V.scalar_type() == Q.scalar_type(),
+              "Q, K and V must have the same dtype (float32, bfloat16 or float16)");
   TORCH_CHECK(hs == 64 || hs == 128,
-              "Unsupported head dimension for bfloat16! Only hs=64 and hs=128 are supported.");
+              "Unsupported head dimension for 16-bit inputs! Only hs=64 and hs=128 are supported.");
   c10::OptionalDeviceGuard guard(Q.device());
   at::Tensor O = at::empty({B, nh, T, hs}, Q.options());
   at::Tensor L = at::empty({B, nh, T}, Q.options().dtype(at::kFloat));
-  const at::Tensor q = attn_operand_bf16(Q), k = attn_operand_bf16(K), v = attn_operand_bf16(V);
+  const at::Tensor q = attn_operand_half(Q), k = attn_operand_half(K), v = attn_operand_half(V);
   const auto qs = strides_of<4>(q), ks = strides_of<4>(k), vs = strides_of<4>(v);
-  check_rc(cta_flash_attention_fwd_bf16(
+  check_rc((bf ? cta_flash_attention_fwd_bf16 : cta_flash_attention_fwd_f16)(
       reinterpret_cast<const uint16_t*>(q.data_ptr()), qs.data(),
       reinterpret_cast<const uint16_t*>(k.data_ptr()), ks.data(),
       reinterpret_cast<const uint16_t*>(v.data_ptr()), vs.data(), B, nh, T, hs, causal ? 1 : 0,
@@ -399,7 +405,7 @@ std::tuple<at::Tensor, at::Tensor> flash_attention_fwd(at::Tensor Q, at::Tensor 
   TORCH_CHECK(K.is_cuda(), "K must be a CUDA tensor");
   TORCH_CHECK(V.is_cuda(), "V must be a CUDA tensor");
   TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes(), "Q, K and V must have the same shape");
-  if (Q.scalar_type() == at::kBFloat16) return flash_attention_fwd_bf16(Q, K, V, causal);
+  if (is_half16(Q)) return flash_attention_fwd_half(Q, K, V, causal);
   check_f32(Q, "Q");
   check_f32(K, "K");
   check_f32(V, "V");
@@ -416,15 +422,16 @@ std::tuple<at::Tensor, at::Tensor> flash_attention_fwd(at::Tensor Q, at::Tensor 
   return {O, L};
 }
 
-// BF16 backward (extension): stored-dS schedule with a BF16 dS workspace from torch's caching
+// 16-bit backward (extension): stored-dS schedule with a 16-bit dS workspace from torch's caching
 // allocator (the same 8 GiB cap as the FP32 op; chunked over heads beyond it).
-std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd_bf16(
+std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd_half(
     const at::Tensor& Q, const at::Tensor& K, const at::Tensor& V, const at::Tensor& O,
     const at::Tensor& dO, const at::Tensor& L, bool causal) {
   const int64_t B = Q.size(0), nh = Q.size(1), T = Q.size(2), hs = Q.size(3);
+  const bool bf = Q.scalar_type() == at::kBFloat16;
   for (const auto* t : {&K, &V, &O, &dO})
-    TORCH_CHECK(t->scalar_type() == at::kBFloat16,
-                "Q, K, V, O and dO must all be bfloat16 (or all float32)");
+    TORCH_CHECK(t->scalar_type() == Q.scalar_type(),
+                "Q, K, V, O and dO must have the same dtype (float32, bfloat16 or float16)");
   TORCH_CHECK(L.scalar_type() == at::kFloat, "L must be a float32 tensor");
   TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes() && O.sizes() == Q.sizes() &&
                   dO.sizes() == Q.sizes(),
@@ -432,7 +439,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd_bf16(
   TORCH_CHECK(L.dim() == 3 && L.size(0) == B && L.size(1) == nh && L.size(2) == T,
               "L must have shape (B, nh, T)");
   TORCH_CHECK(hs == 64 || hs == 128,
-              "Unsupported head dimension for bfloat16! Only hs=64 and hs=128 are supported.");
+              "Unsupported head dimension for 16-bit inputs! Only hs=64 and hs=128 are supported.");
   c10::OptionalDeviceGuard guard(Q.device());
   at::Tensor dQ = at::empty({B, nh, T, hs}, Q.options());
   at::Tensor dK = at::empty({B, nh, T, hs}, Q.options());
@@ -443,14 +450,14 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd_bf16(
   const int64_t head = cta_flash_attention_bwd_bf16_workspace(1, 1, T, hs, causal ? 1 : 0);
   const int64_t ws_bytes = std::max(head, std::min(full, kBwdWorkspaceCap));
   at::Tensor ws = at::empty({(ws_bytes + 15) / 16 * 4}, Q.options().dtype(at::kFloat));
-  const at::Tensor q = attn_operand_bf16(Q), k = attn_operand_bf16(K), v = attn_operand_bf16(V),
-                   o = attn_operand_bf16(O), g = attn_operand_bf16(dO);
+  const at::Tensor q = attn_operand_half(Q), k = attn_operand_half(K), v = attn_operand_half(V),
+                   o = attn_operand_half(O), g = attn_operand_half(dO);
   const auto qs = strides_of<4>(q), ks = strides_of<4>(k), vs = strides_of<4>(v),
              os = strides_of<4>(o), gs = strides_of<4>(g);
   const auto ls = strides_of<3>(L);
   auto u16 = [](const at::Tensor& t) { return reinterpret_cast<const uint16_t*>(t.data_ptr()); };
   auto w16 = [](at::Tensor& t) { return reinterpret_cast<uint16_t*>(t.data_ptr()); };
-  check_rc(cta_flash_attention_bwd_bf16(u16(q), qs.data(), u16(k), ks.data(), u16(v), vs.data(),
+  check_rc((bf ? cta_flash_attention_bwd_bf16 : cta_flash_attention_bwd_f16)(u16(q), qs.data(), u16(k), ks.data(), u16(v), vs.data(),
                                         u16(o), os.data(), u16(g), gs.data(),
                                         L.data_ptr<float>(), ls.data(), B, nh, T, hs,
                                         causal ? 1 : 0, w16(dQ), w16(dK), w16(dV),
@@ -472,7 +479,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd(at::Tensor Q,
   TORCH_CHECK(O.is_cuda(), "O must be a CUDA tensor");
   TORCH_CHECK(dO.is_cuda(), "dO must be a CUDA tensor");
   TORCH_CHECK(L.is_cuda(), "L must be a CUDA tensor");
-  if (Q.scalar_type() == at::kBFloat16) return flash_attention_bwd_bf16(Q, K, V, O, dO, L, causal);
+  if (is_half16(Q)) return flash_attention_bwd_half(Q, K, V, O, dO, L, causal);
   for (const auto* t : {&Q, &K, &V, &O, &dO, &L}) check_f32(*t, "input");
   TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes() && O.sizes() == Q.sizes() &&
                   dO.sizes() == Q.sizes(),

@@ -173,16 +173,16 @@ def _(Q, K, V, probs, dO):
 def flash_attention_fwd(Q: Tensor, K: Tensor, V: Tensor, causal: bool) -> tuple[Tensor, Tensor]:
     """FA2 forward -> (O, L), L = rowmax + ln(rowsum)  (reference ops.py:109-111).
 
-    Extension: bfloat16 Q, K, V (hs 64 or 128) run the BF16 kernel, which returns O in
-    bfloat16 and L in float32; the reference's kernels are float32 only."""
+    Extension: bfloat16 or float16 Q, K, V (hs 64 or 128) run the 16-bit kernel, which returns
+    O in the input dtype and L in float32; the reference's kernels are float32 only."""
     return _ops.flash_attention_fwd.default(Q, K, V, causal)
 
 
 @torch.library.register_fake("cuda_transformer::flash_attention_fwd")
 def _(Q, K, V, causal):
-    if Q.dtype == torch.bfloat16:
-        torch._check(K.dtype == torch.bfloat16 and V.dtype == torch.bfloat16,
-                     lambda: "Q, K and V must all be bfloat16 (or all float32)")
+    if Q.dtype in (torch.bfloat16, torch.float16):
+        torch._check(K.dtype == Q.dtype and V.dtype == Q.dtype,
+                     lambda: "Q, K and V must have the same dtype")
     else:
         _f32(Q, K, V)
     _same_device(Q, K, V)
@@ -195,16 +195,16 @@ def flash_attention_bwd(Q: Tensor, K: Tensor, V: Tensor, O: Tensor, dO: Tensor, 
                         causal: bool):
     """FA2 backward -> (dQ, dK, dV)  (reference ops.py:123-125).
 
-    Extension: bfloat16 Q, K, V, O, dO with float32 L (hs 64 or 128) run the BF16 kernels and
-    return bfloat16 gradients."""
+    Extension: bfloat16 or float16 Q, K, V, O, dO with float32 L (hs 64 or 128) run the 16-bit
+    kernels and return gradients in the input dtype."""
     return _ops.flash_attention_bwd.default(Q, K, V, O, dO, L, causal)
 
 
 @torch.library.register_fake("cuda_transformer::flash_attention_bwd")
 def _(Q, K, V, O, dO, L, causal):
-    if Q.dtype == torch.bfloat16:
-        torch._check(all(t.dtype == torch.bfloat16 for t in (K, V, O, dO)),
-                     lambda: "Q, K, V, O and dO must all be bfloat16 (or all float32)")
+    if Q.dtype in (torch.bfloat16, torch.float16):
+        torch._check(all(t.dtype == Q.dtype for t in (K, V, O, dO)),
+                     lambda: "Q, K, V, O and dO must have the same dtype")
         _f32(L)
     else:
         _f32(Q, K, V, O, dO, L)

@@ -72,6 +72,13 @@ int cta_flash_attention_fwd_bf16(const uint16_t* q, const int64_t* q_strides,
                                  int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
                                  uint16_t* o, float* l, void* stream);
 
+/* The same with FP16 Q, K, V (O in FP16, L in FP32; P rounded to FP16). */
+int cta_flash_attention_fwd_f16(const uint16_t* q, const int64_t* q_strides,
+                                const uint16_t* k, const int64_t* k_strides,
+                                const uint16_t* v, const int64_t* v_strides,
+                                int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                                uint16_t* o, float* l, void* stream);
+
 /* Bytes of dS workspace that let cta_flash_attention_bwd keep every head's dS tiles
  * (the lower-triangular 32x32 tiles only when causal): B*nh*ceil(T/32)^2*4 KiB, or about
  * half of that when causal.  0 for empty or unsupported shapes. */
@@ -119,6 +126,19 @@ int cta_flash_attention_bwd_bf16(const uint16_t* q, const int64_t* q_strides,
                                  int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
                                  uint16_t* dq, uint16_t* dk, uint16_t* dv, float* delta,
                                  void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The same with FP16 Q, K, V, O, dO (FP32 L): FP16 gradients, dS stored and rounded in FP16. */
+int64_t cta_flash_attention_bwd_f16_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs,
+                                              int causal);
+int cta_flash_attention_bwd_f16(const uint16_t* q, const int64_t* q_strides,
+                                const uint16_t* k, const int64_t* k_strides,
+                                const uint16_t* v, const int64_t* v_strides,
+                                const uint16_t* o, const int64_t* o_strides,
+                                const uint16_t* d_o, const int64_t* do_strides,
+                                const float* l, const int64_t* l_strides,
+                                int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                                uint16_t* dq, uint16_t* dk, uint16_t* dv, float* delta,
+                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Stage 1 of the backward: delta[b,h,t] = sum_d O*dO, dense (B,nh,T).
  * Replaces the flash_attention_bwd_delta launch (flash_attn_launcher.cu:107-108). */

@@ -1,12 +1,14 @@
-"""FlashAttention-2 forward with bfloat16 Q, K, V on the GPU vs the CPU oracle (float64).
+"""FlashAttention-2 with 16-bit (bfloat16 and float16) Q, K, V on the GPU vs the CPU oracle
+(float64).
 
-The oracle is evaluated on the bf16-rounded inputs, so input rounding is not counted as kernel
-error.  The kernel accumulates in FP32 and rounds twice: the probabilities to bf16 as the P.V
-operand, and O to bf16 on output, each a relative error of at most 2^-9.  Hence per element
+The oracle is evaluated on the 16-bit-rounded inputs, so input rounding is not counted as kernel
+error.  The kernel accumulates in FP32 and rounds twice: the probabilities to 16 bits as the
+P.V operand, and O on output, each a relative error of at most 2^-9 for bfloat16 (2^-12 for
+float16).  Hence per element
     |O - O_ref| <= 2^-9 |O_ref| + 2^-9 max_j |v_j| (+ FP32 accumulation),
-bounded here by 2^-8 (|O_ref| + max|V|); L comes from FP32 scores of exact bf16 products and
-keeps an FP32-level bound of 1e-4.  Shapes follow the FP32 suite (ragged T, causal and full,
-hs 64 and 128, benchmark config 1).
+bounded here by 2^-8 (|O_ref| + max|V|) for both types; L comes from FP32 scores of exact
+16-bit products and keeps an FP32-level bound of 1e-4.  Shapes follow the FP32 suite (ragged T,
+causal and full, hs 64 and 128, benchmark config 1).
 """
 import numpy as np
 import pytest
@@ -16,6 +18,8 @@ from conftest import f64, seeded
 from oracle import attention as ora
 
 pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.bfloat16, torch.float16]
 
 SHAPES = [
     (1, 4, 256, 64, True),   # benchmark config 1
@@ -31,13 +35,13 @@ SHAPES = [
 ]
 
 
-def _bf16_inputs(B, nh, T, hs, seed):
-    return [seeded((B, nh, T, hs), seed + i).to(torch.bfloat16) for i in range(3)]
+def _half_inputs(B, nh, T, hs, seed, dtype=torch.bfloat16):
+    return [seeded((B, nh, T, hs), seed + i).to(dtype) for i in range(3)]
 
 
 def _check(O, L, q, k, v, causal):
     O_ref, L_ref = ora.reference_attention(f64(q), f64(k), f64(v), causal)
-    assert O.dtype == torch.bfloat16 and L.dtype == torch.float32
+    assert O.dtype == q.dtype and L.dtype == torch.float32
     bound = 2.0 ** -8 * (np.abs(O_ref) + np.abs(f64(v)).max())
     err = np.abs(f64(O) - O_ref)
     assert (err <= bound).all(), f"O error {err.max():.3e} exceeds the bf16 bound"
@@ -45,24 +49,26 @@ def _check(O, L, q, k, v, causal):
     return err.max()
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("B,nh,T,hs,causal", SHAPES)
-def test_fa2_bf16_forward_matches_oracle(cuda, B, nh, T, hs, causal):
+def test_fa2_half_forward_matches_oracle(cuda, B, nh, T, hs, causal, dtype):
     from cuda_transformer.ops import flash_attention_fwd
 
-    q, k, v = _bf16_inputs(B, nh, T, hs, seed=3000 + T + hs)
+    q, k, v = _half_inputs(B, nh, T, hs, seed=3000 + T + hs, dtype=dtype)
     O, L = flash_attention_fwd(q.to(cuda), k.to(cuda), v.to(cuda), causal)
     torch.cuda.synchronize()
     _check(O.cpu(), L.cpu(), q, k, v, causal)
 
 
-def test_fa2_bf16_forward_error_like_torch_bf16(cuda):
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_fa2_half_forward_error_like_torch(cuda, dtype):
     """The kernel's error against the float64 oracle is no larger than that of torch's own
-    bf16 attention (CPU SDPA on the same bf16 inputs) plus the bf16 output rounding."""
+    16-bit attention (CPU SDPA on the same inputs)."""
     import torch.nn.functional as F
 
     from cuda_transformer.ops import flash_attention_fwd
 
-    q, k, v = _bf16_inputs(1, 4, 256, 64, seed=77)
+    q, k, v = _half_inputs(1, 4, 256, 64, seed=77, dtype=dtype)
     O, _ = flash_attention_fwd(q.to(cuda), k.to(cuda), v.to(cuda), True)
     O_ref, _ = ora.reference_attention(f64(q), f64(k), f64(v), True)
     ours = np.abs(f64(O) - O_ref).mean()
@@ -70,7 +76,7 @@ def test_fa2_bf16_forward_error_like_torch_bf16(cuda):
     assert ours <= 1.5 * torch_bf16 + 1e-4, (ours, torch_bf16)
 
 
-def test_fa2_bf16_strided_views(cuda):
+def test_fa2_half_strided_views(cuda):
     """Head views of a packed (B, T, 3C) bf16 projection are read in place, as in gpt.py."""
     from cuda_transformer.ops import flash_attention_fwd
 
@@ -84,30 +90,32 @@ def test_fa2_bf16_strided_views(cuda):
     _check(O.cpu(), L.cpu(), q.contiguous(), k.contiguous(), v.contiguous(), True)
 
 
-def test_fa2_bf16_deterministic(cuda):
+def test_fa2_half_deterministic(cuda):
     from cuda_transformer.ops import flash_attention_fwd
 
-    q, k, v = (t.to(cuda) for t in _bf16_inputs(2, 4, 300, 128, seed=11))
+    q, k, v = (t.to(cuda) for t in _half_inputs(2, 4, 300, 128, seed=11))
     O1, L1 = flash_attention_fwd(q, k, v, True)
     O2, L2 = flash_attention_fwd(q, k, v, True)
     assert torch.equal(O1, O2) and torch.equal(L1, L2)
 
 
-def test_fa2_bf16_errors(cuda):
+def test_fa2_half_errors(cuda):
     from cuda_transformer.ops import flash_attention_fwd
 
     q = torch.randn(1, 2, 16, 32, device=cuda, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="hs=64 and hs=128"):
         flash_attention_fwd(q, q, q, False)
     q = torch.randn(1, 2, 16, 64, device=cuda, dtype=torch.bfloat16)
-    with pytest.raises(RuntimeError, match="all be bfloat16"):
+    with pytest.raises(RuntimeError, match="same dtype"):
         flash_attention_fwd(q, q.float(), q, False)
+    with pytest.raises(RuntimeError, match="same dtype"):
+        flash_attention_fwd(q, q.half(), q, False)
 
 
 # ---------------------------------------------------------------- backward
-# The oracle backward runs in float64 on the bf16-rounded q, k, v, dO with the exact O and L.
-# The kernel rounds P and dS to bf16 as MFMA operands (2^-9 relative each), forms delta from
-# its bf16 O, and rounds the gradients to bf16 on output.  dV carries only the P rounding and
+# The oracle backward runs in float64 on the 16-bit-rounded q, k, v, dO with the exact O and L.
+# The kernel rounds P and dS to 16 bits as MFMA operands (2^-9 relative each for bfloat16),
+# forms delta from its 16-bit O, and rounds the gradients on output.  dV carries only the P rounding and
 # its own output rounding; dQ and dK also the dS rounding, where dP - delta can cancel.  Bounds
 # on the relative L2 error: 1.5e-2 for dV, 3e-2 for dQ and dK.
 BWD_SHAPES = [
@@ -129,7 +137,7 @@ def _bwd_check(grads, q, k, v, do, causal):
     refs = ora.fa2_backward(f64(q), f64(k), f64(v), O_ref, f64(do), L_ref, causal, br=64, bc=64)
     errs = []
     for got, ref, tol in zip(grads, refs, (3e-2, 3e-2, 1.5e-2)):
-        assert got.dtype == torch.bfloat16
+        assert got.dtype == q.dtype
         scale = 1e-6 * np.sqrt(ref.size)
         if np.linalg.norm(ref) <= scale:  # e.g. dQ for T = 1 is exactly zero
             assert np.linalg.norm(f64(got) - ref) <= 1e-3 * np.sqrt(ref.size)
@@ -141,12 +149,13 @@ def _bwd_check(grads, q, k, v, do, causal):
     return errs
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("B,nh,T,hs,causal", BWD_SHAPES)
-def test_fa2_bf16_backward_matches_oracle(cuda, B, nh, T, hs, causal):
+def test_fa2_half_backward_matches_oracle(cuda, B, nh, T, hs, causal, dtype):
     from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
 
-    q, k, v = _bf16_inputs(B, nh, T, hs, seed=5000 + T + hs)
-    do = seeded((B, nh, T, hs), 9000 + T, kind="rand").to(torch.bfloat16)
+    q, k, v = _half_inputs(B, nh, T, hs, seed=5000 + T + hs, dtype=dtype)
+    do = seeded((B, nh, T, hs), 9000 + T, kind="rand").to(dtype)
     qg, kg, vg = q.to(cuda), k.to(cuda), v.to(cuda)
     O, L = flash_attention_fwd(qg, kg, vg, causal)
     grads = flash_attention_bwd(qg, kg, vg, O, do.to(cuda), L, causal)
@@ -154,17 +163,19 @@ def test_fa2_bf16_backward_matches_oracle(cuda, B, nh, T, hs, causal):
     _bwd_check([g.cpu() for g in grads], q, k, v, do, causal)
 
 
-def test_fa2_bf16_autograd_and_torch_bf16_error(cuda):
-    """CudaFlashAttention with bf16 leaves: bf16 gradients within the bounds above, and no
-    more than twice the error of torch's own bf16 SDPA backward (CPU) on the same inputs."""
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_fa2_half_autograd_and_torch_error(cuda, dtype):
+    """CudaFlashAttention with 16-bit leaves: gradients in the input dtype within the bounds
+    above, and no more than twice the error of torch's own 16-bit SDPA backward (CPU) on the
+    same inputs."""
     import torch.nn.functional as F
 
     from cuda_autograd_fns import CudaFlashAttention
     from conftest import rel_err
 
     B, nh, T, hs, causal = 1, 4, 256, 64, True
-    q, k, v = _bf16_inputs(B, nh, T, hs, seed=41)
-    do = seeded((B, nh, T, hs), 42, kind="rand").to(torch.bfloat16)
+    q, k, v = _half_inputs(B, nh, T, hs, seed=41, dtype=dtype)
+    do = seeded((B, nh, T, hs), 42, kind="rand").to(dtype)
     leaves = [t.to(cuda).requires_grad_() for t in (q, k, v)]
     o, _l = CudaFlashAttention.apply(*leaves, causal)
     o.backward(do.to(cuda))
@@ -179,7 +190,7 @@ def test_fa2_bf16_autograd_and_torch_bf16_error(cuda):
         assert a <= 2.0 * b + 1e-3, (ours, theirs)
 
 
-def test_fa2_bf16_backward_chunked_matches_full(cuda):
+def test_fa2_half_backward_chunked_matches_full(cuda):
     """The head-chunked stored-dS schedule (a workspace of one head) gives the same bits as the
     full workspace."""
     import ctypes
@@ -187,7 +198,7 @@ def test_fa2_bf16_backward_chunked_matches_full(cuda):
     from cuda_transformer_amd import capi
 
     B, nh, T, hs = 2, 3, 300, 64
-    q, k, v = (t.to(cuda) for t in _bf16_inputs(B, nh, T, hs, seed=61))
+    q, k, v = (t.to(cuda) for t in _half_inputs(B, nh, T, hs, seed=61))
     from cuda_transformer.ops import flash_attention_fwd
     O, L = flash_attention_fwd(q, k, v, True)
     do = torch.rand(B, nh, T, hs, device=cuda).to(torch.bfloat16)
