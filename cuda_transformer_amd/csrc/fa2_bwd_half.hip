@@ -143,21 +143,32 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_half_kerne
   const bool wave_stores = j0 < T;
 
   // Register-staged loads of one query stage: Q and dO rows (rows past T are zero), L, delta.
-  uint4 qst[LOADS], gst[LOADS];
+  // A load task is rows 2 rp and 2 rp + 1 of one 16-byte chunk ch of Q or of dO; it goes to LDS
+  // row-wise and transposed, the two rows' values for one d as one 32-bit store (kt_pos keeps
+  // rows 2 rp and 2 rp + 1 adjacent).  Tasks [0, BN/2 * CH) are Q, the rest dO.
+  constexpr int PAIRS = BN / 2 * CH;
+  uint4 st2[LOADS][2];
   float lst = 0.0f, dst = 0.0f;
+  auto task_of = [&](int u, int& tensor, int& rp, int& ch) {
+    const int c = tid + 256 * u;
+    tensor = c / PAIRS;
+    const int rem = c - tensor * PAIRS;
+    rp = rem / CH;
+    ch = rem % CH;
+  };
   auto gload = [&](int stage) {
     const int r0 = stage * BN;
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int r = c / CH, ch = c % CH;
-      const int i = r0 + r;
-      if (i < T) {
-        qst[u] = *reinterpret_cast<const uint4*>(Qb + (int64_t)i * sq.t + 8 * ch);
-        gst[u] = *reinterpret_cast<const uint4*>(dOb + (int64_t)i * sdo.t + 8 * ch);
-      } else {
-        qst[u] = make_uint4(0, 0, 0, 0);
-        gst[u] = make_uint4(0, 0, 0, 0);
+      int tensor, rp, ch;
+      task_of(u, tensor, rp, ch);
+      const E* base = tensor == 0 ? Qb : dOb;
+      const int64_t st_t = tensor == 0 ? sq.t : sdo.t;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int i = r0 + 2 * rp + e;
+        st2[u][e] = i < T ? *reinterpret_cast<const uint4*>(base + (int64_t)i * st_t + 8 * ch)
+                          : make_uint4(0, 0, 0, 0);
       }
     }
     if (tid < BN) {
@@ -168,22 +179,21 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_half_kerne
   };
   auto lstore = [&](int buf) {
     unsigned char* base = smem + buf * STAGE;
-    E* qr = reinterpret_cast<E*>(base);
-    E* gr = reinterpret_cast<E*>(base + OFF_GR);
-    E* qt = reinterpret_cast<E*>(base + OFF_QT);
-    E* gt = reinterpret_cast<E*>(base + OFF_GT);
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int r = c / CH, ch = c % CH;
-      *reinterpret_cast<uint4*>(qr + r * RP + 8 * ch) = qst[u];
-      *reinterpret_cast<uint4*>(gr + r * RP + 8 * ch) = gst[u];
-      const E* qe = reinterpret_cast<const E*>(&qst[u]);
-      const E* ge = reinterpret_cast<const E*>(&gst[u]);
+      int tensor, rp, ch;
+      task_of(u, tensor, rp, ch);
+      E* rows = reinterpret_cast<E*>(base + (tensor == 0 ? 0 : OFF_GR));
+      E* trs = reinterpret_cast<E*>(base + (tensor == 0 ? OFF_QT : OFF_GT));
+      *reinterpret_cast<uint4*>(rows + (2 * rp) * RP + 8 * ch) = st2[u][0];
+      *reinterpret_cast<uint4*>(rows + (2 * rp + 1) * RP + 8 * ch) = st2[u][1];
+      const uint32_t* e0 = reinterpret_cast<const uint32_t*>(&st2[u][0]);
+      const uint32_t* e1 = reinterpret_cast<const uint32_t*>(&st2[u][1]);
+      uint32_t* col2 = reinterpret_cast<uint32_t*>(trs + kt_pos(2 * rp));
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        qt[(8 * ch + t) * TP + kt_pos(r)] = qe[t];
-        gt[(8 * ch + t) * TP + kt_pos(r)] = ge[t];
+      for (int t = 0; t < 4; ++t) {
+        col2[(8 * ch + 2 * t) * (TP / 2)] = (e0[t] & 0xFFFFu) | (e1[t] << 16);
+        col2[(8 * ch + 2 * t + 1) * (TP / 2)] = (e0[t] >> 16) | (e1[t] & 0xFFFF0000u);
       }
     }
     if (tid < BN) {
@@ -373,27 +383,43 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_half_kern
   const int n_stages = (kv_end + BN - 1) / BN;
 
   // Branch-free clamped loads: every stage issues the same loads, so the compiler counts them
-  // exactly and a stage's MFMAs wait only for that stage's dS.
+  // exactly and a stage's MFMAs wait only for that stage's dS.  A thread loads rows 2 rp and
+  // 2 rp + 1 of chunk ch and stores each d's pair as one 32-bit word of the K^T image.
+  static_assert(LOADS % 2 == 0, "row pairs");
   uint4 kst[LOADS];
+  auto pair_of = [&](int u2, int& rp, int& ch) {
+    const int c = tid + 256 * u2;
+    rp = c / CH;
+    ch = c % CH;
+  };
   auto gload = [&](int stage) {
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int r = c / CH, ch = c % CH;
-      const int j = stage * BN + r;
-      const uint4 kv = *reinterpret_cast<const uint4*>(Kb + (int64_t)min(j, T - 1) * sk.t + 8 * ch);
-      kst[u] = j < T ? kv : make_uint4(0, 0, 0, 0);  // keys past T meet finite dS: K must be 0
+    for (int u2 = 0; u2 < LOADS / 2; ++u2) {
+      int rp, ch;
+      pair_of(u2, rp, ch);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int j = stage * BN + 2 * rp + e;
+        const uint4 kv =
+            *reinterpret_cast<const uint4*>(Kb + (int64_t)min(j, T - 1) * sk.t + 8 * ch);
+        kst[2 * u2 + e] = j < T ? kv : make_uint4(0, 0, 0, 0);  // keys past T: K must be 0
+      }
     }
   };
   auto lstore = [&](int buf) {
     E* kt = smem + buf * TILE;
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int r = c / CH, ch = c % CH;
-      const E* e = reinterpret_cast<const E*>(&kst[u]);
+    for (int u2 = 0; u2 < LOADS / 2; ++u2) {
+      int rp, ch;
+      pair_of(u2, rp, ch);
+      const uint32_t* e0 = reinterpret_cast<const uint32_t*>(&kst[2 * u2]);
+      const uint32_t* e1 = reinterpret_cast<const uint32_t*>(&kst[2 * u2 + 1]);
+      uint32_t* col2 = reinterpret_cast<uint32_t*>(kt + 2 * rp);
 #pragma unroll
-      for (int t = 0; t < 8; ++t) kt[(8 * ch + t) * KTP + r] = e[t];
+      for (int t = 0; t < 4; ++t) {
+        col2[(8 * ch + 2 * t) * (KTP / 2)] = (e0[t] & 0xFFFFu) | (e1[t] << 16);
+        col2[(8 * ch + 2 * t + 1) * (KTP / 2)] = (e0[t] >> 16) | (e1[t] & 0xFFFF0000u);
+      }
     }
   };
   auto has_tile = [&](int jb) { return ib < nb && jb < nb && (!CAUSAL || jb <= ib); };

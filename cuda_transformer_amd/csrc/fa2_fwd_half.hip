@@ -93,19 +93,31 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
   const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
   const int n_stages = (kv_end + BN - 1) / BN;
 
+  // Each thread loads rows 2 rp and 2 rp + 1 (LOADS / 2 row pairs) of one 16-byte chunk ch of
+  // K and V.  K goes to LDS row-wise; V goes transposed, the two rows' values for one d as one
+  // 32-bit store (kt_pos keeps rows 2 rp and 2 rp + 1 adjacent).
+  static_assert(LOADS % 2 == 0, "row pairs");
   uint4 kst[LOADS], vst[LOADS];
+  auto pair_of = [&](int u2, int& rp, int& ch) {
+    const int c = tid + 256 * u2;
+    rp = c / CH;
+    ch = c % CH;
+  };
   auto gload = [&](int stage) {
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int r = c / CH, ch = c % CH;
-      const int j = stage * BN + r;
-      if (j < T) {
-        kst[u] = *reinterpret_cast<const uint4*>(Kb + (int64_t)j * sk.t + 8 * ch);
-        vst[u] = *reinterpret_cast<const uint4*>(Vb + (int64_t)j * sv.t + 8 * ch);
-      } else {
-        kst[u] = make_uint4(0, 0, 0, 0);
-        vst[u] = make_uint4(0, 0, 0, 0);
+    for (int u2 = 0; u2 < LOADS / 2; ++u2) {
+      int rp, ch;
+      pair_of(u2, rp, ch);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int j = stage * BN + 2 * rp + e;
+        if (j < T) {
+          kst[2 * u2 + e] = *reinterpret_cast<const uint4*>(Kb + (int64_t)j * sk.t + 8 * ch);
+          vst[2 * u2 + e] = *reinterpret_cast<const uint4*>(Vb + (int64_t)j * sv.t + 8 * ch);
+        } else {
+          kst[2 * u2 + e] = make_uint4(0, 0, 0, 0);
+          vst[2 * u2 + e] = make_uint4(0, 0, 0, 0);
+        }
       }
     }
   };
@@ -113,13 +125,20 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
     E* ks = smem + buf * (KTILE + VTILE);
     E* vt = ks + KTILE;
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int r = c / CH, ch = c % CH;
-      *reinterpret_cast<uint4*>(ks + r * KP + 8 * ch) = kst[u];
-      const E* e = reinterpret_cast<const E*>(&vst[u]);
+    for (int u2 = 0; u2 < LOADS / 2; ++u2) {
+      int rp, ch;
+      pair_of(u2, rp, ch);
+      *reinterpret_cast<uint4*>(ks + (2 * rp) * KP + 8 * ch) = kst[2 * u2];
+      *reinterpret_cast<uint4*>(ks + (2 * rp + 1) * KP + 8 * ch) = kst[2 * u2 + 1];
+      const uint32_t* e0 = reinterpret_cast<const uint32_t*>(&vst[2 * u2]);
+      const uint32_t* e1 = reinterpret_cast<const uint32_t*>(&vst[2 * u2 + 1]);
+      uint32_t* col2 = reinterpret_cast<uint32_t*>(vt + kt_pos(2 * rp));
 #pragma unroll
-      for (int t = 0; t < 8; ++t) vt[(8 * ch + t) * VP + kt_pos(r)] = e[t];
+      for (int t = 0; t < 4; ++t) {
+        // d = 8 ch + 2t and 8 ch + 2t + 1: low halves of e0/e1 hold the even d
+        col2[(8 * ch + 2 * t) * (VP / 2)] = (e0[t] & 0xFFFFu) | (e1[t] << 16);
+        col2[(8 * ch + 2 * t + 1) * (VP / 2)] = (e0[t] >> 16) | (e1[t] & 0xFFFF0000u);
+      }
     }
   };
 
