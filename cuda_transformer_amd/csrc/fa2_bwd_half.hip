@@ -149,12 +149,14 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dkdv_half_kerne
   constexpr int PAIRS = BN / 2 * CH;
   uint4 st2[LOADS][2];
   float lst = 0.0f, dst = 0.0f;
+  // Sixteen consecutive lanes take the 16 row pairs of one chunk, so a transposed store
+  // instruction spreads over 32 pair positions x 2 chunk parities (2-way at worst).
   auto task_of = [&](int u, int& tensor, int& rp, int& ch) {
     const int c = tid + 256 * u;
     tensor = c / PAIRS;
     const int rem = c - tensor * PAIRS;
-    rp = rem / CH;
-    ch = rem % CH;
+    rp = rem % (BN / 2);
+    ch = rem / (BN / 2);
   };
   auto gload = [&](int stage) {
     const int r0 = stage * BN;
@@ -387,10 +389,12 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_half_kern
   // 2 rp + 1 of chunk ch and stores each d's pair as one 32-bit word of the K^T image.
   static_assert(LOADS % 2 == 0, "row pairs");
   uint4 kst[LOADS];
+  // A wave's 64 tasks are 32 row pairs x 2 chunks: each transposed store instruction hits 64
+  // distinct banks (the 32 pair positions, and the two chunks' d rows 32 banks apart).
+  static_assert(BN == 64, "32 row pairs per stage");
   auto pair_of = [&](int u2, int& rp, int& ch) {
-    const int c = tid + 256 * u2;
-    rp = c / CH;
-    ch = c % CH;
+    rp = lane & 31;
+    ch = 2 * (wave + 4 * u2) + (lane >> 5);
   };
   auto gload = [&](int stage) {
 #pragma unroll

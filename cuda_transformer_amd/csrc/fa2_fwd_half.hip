@@ -93,31 +93,34 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
   const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
   const int n_stages = (kv_end + BN - 1) / BN;
 
-  // Each thread loads rows 2 rp and 2 rp + 1 (LOADS / 2 row pairs) of one 16-byte chunk ch of
-  // K and V.  K goes to LDS row-wise; V goes transposed, the two rows' values for one d as one
-  // 32-bit store (kt_pos keeps rows 2 rp and 2 rp + 1 adjacent).
-  static_assert(LOADS % 2 == 0, "row pairs");
+  // K: thread task c = tid + 256 u is row c / CH, 16-byte chunk c % CH, stored row-wise (eight
+  // lanes fill one 128-byte row).  V: a task is rows 2 rp and 2 rp + 1 of one chunk, stored
+  // transposed, the two rows' values for one d as one 32-bit word (kt_pos keeps them adjacent).
+  // A wave's 64 V tasks are 32 row pairs x 2 chunks, so each transposed store instruction hits
+  // 64 distinct banks: the 32 pair positions, and the two chunks' d rows 16 rows (32 banks) apart.
+  static_assert(LOADS % 2 == 0 && BN == 64, "32 row pairs per stage");
   uint4 kst[LOADS], vst[LOADS];
-  auto pair_of = [&](int u2, int& rp, int& ch) {
-    const int c = tid + 256 * u2;
-    rp = c / CH;
-    ch = c % CH;
+  auto vtask = [&](int u2, int& rp, int& ch) {
+    rp = lane & 31;
+    ch = 2 * (wave + 4 * u2) + (lane >> 5);
   };
   auto gload = [&](int stage) {
 #pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int c = tid + 256 * u;
+      const int j = stage * BN + c / CH;
+      kst[u] = j < T ? *reinterpret_cast<const uint4*>(Kb + (int64_t)j * sk.t + 8 * (c % CH))
+                     : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
     for (int u2 = 0; u2 < LOADS / 2; ++u2) {
       int rp, ch;
-      pair_of(u2, rp, ch);
+      vtask(u2, rp, ch);
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int j = stage * BN + 2 * rp + e;
-        if (j < T) {
-          kst[2 * u2 + e] = *reinterpret_cast<const uint4*>(Kb + (int64_t)j * sk.t + 8 * ch);
-          vst[2 * u2 + e] = *reinterpret_cast<const uint4*>(Vb + (int64_t)j * sv.t + 8 * ch);
-        } else {
-          kst[2 * u2 + e] = make_uint4(0, 0, 0, 0);
-          vst[2 * u2 + e] = make_uint4(0, 0, 0, 0);
-        }
+        vst[2 * u2 + e] = j < T ? *reinterpret_cast<const uint4*>(Vb + (int64_t)j * sv.t + 8 * ch)
+                                : make_uint4(0, 0, 0, 0);
       }
     }
   };
@@ -125,11 +128,14 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
     E* ks = smem + buf * (KTILE + VTILE);
     E* vt = ks + KTILE;
 #pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int c = tid + 256 * u;
+      *reinterpret_cast<uint4*>(ks + (c / CH) * KP + 8 * (c % CH)) = kst[u];
+    }
+#pragma unroll
     for (int u2 = 0; u2 < LOADS / 2; ++u2) {
       int rp, ch;
-      pair_of(u2, rp, ch);
-      *reinterpret_cast<uint4*>(ks + (2 * rp) * KP + 8 * ch) = kst[2 * u2];
-      *reinterpret_cast<uint4*>(ks + (2 * rp + 1) * KP + 8 * ch) = kst[2 * u2 + 1];
+      vtask(u2, rp, ch);
       const uint32_t* e0 = reinterpret_cast<const uint32_t*>(&vst[2 * u2]);
       const uint32_t* e1 = reinterpret_cast<const uint32_t*>(&vst[2 * u2 + 1]);
       uint32_t* col2 = reinterpret_cast<uint32_t*>(vt + kt_pos(2 * rp));
