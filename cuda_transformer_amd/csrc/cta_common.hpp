@@ -21,8 +21,10 @@ namespace cta {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16 bytes of 16-bit elements
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 
 // Row index inside a 32x32 MFMA output tile held by register r of a lane in half h.
 __device__ __forceinline__ constexpr int mfma_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
@@ -76,6 +78,36 @@ __device__ __forceinline__ vec8_t<E> ld8(const E* p) {
 // rows adjacent: store row k of the image at position kt_pos(k), bits 2 and 3 of k swapped.
 __device__ __forceinline__ constexpr int kt_pos(int k) {
   return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
+// Interleave the 16-bit halves of two words with one v_perm_b32: pack_lo16(a, b) holds the low
+// halves (a's in bits 0-15, b's in bits 16-31), pack_hi16(a, b) the high halves.
+__device__ __forceinline__ uint32_t pack_lo16(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// Index of this thread's wave in a 256-thread workgroup, marked wave-uniform for the compiler
+// (through readfirstlane), so that branches on it are scalar branches.
+__device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Maximum of v[0 .. N) as a tree of three-input maxima, depth log3(N): the form v_max3_f32
+// implements.  Overwrites v.
+template <int N>
+__device__ __forceinline__ float max3_tree(float (&v)[N]) {
+  constexpr int M = (N + 2) / 3;
+  float w[M];
+#pragma unroll
+  for (int k = 0; k < M; ++k) {
+    float a = v[3 * k];
+    if (3 * k + 1 < N) a = fmaxf(a, v[3 * k + 1]);
+    if (3 * k + 2 < N) a = fmaxf(a, v[3 * k + 2]);
+    w[k] = a;
+  }
+  if constexpr (M == 1) return w[0];
+  else return max3_tree(w);
 }
 
 // Exchange with the lane 32 positions away (the other half of the wave).

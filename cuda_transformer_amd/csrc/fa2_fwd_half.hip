@@ -36,8 +36,8 @@ template <class E, int HS, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
     const E* __restrict__ Q, const E* __restrict__ K, const E* __restrict__ V,
     E* __restrict__ O, float* __restrict__ L, int nh, int T, int BH, int n_qtiles,
-    RowStridesB sq, RowStridesB sk, RowStridesB sv, float scale, float scale_log2,
-    float rescale_gap) {
+    RowStridesB sq, RowStridesB sk, RowStridesB sv, float scale_log2) {
+  constexpr float kRescaleGap = 8.0f;  // log2 units: probabilities stay below 2^8
   constexpr int BN = 64;             // keys per stage
   constexpr int NSUB = BN / 32;      // 32-key score tiles per stage
   constexpr int BM = 128;
@@ -87,8 +87,11 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
   f32x16 oacc[HS / 32];
 #pragma unroll
   for (int d = 0; d < HS / 32; ++d) oacc[d] = zero16();
-  float m_run = -INFINITY;  // exponent offset of row my_i (raw q.k units), lazily updated
-  float l_run = 0.0f;       // this lane's partial row sum
+  // Exponent offset of row my_i in log2 units (scores times s log2(e)), lazily updated: it only
+  // moves when some row of the wave sees a score more than kRescaleGap above it, so every
+  // probability stays below 2^kRescaleGap against the offset in use.
+  float mb = -INFINITY;
+  float l_run = 0.0f;  // this lane's partial row sum
 
   const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
   const int n_stages = (kv_end + BN - 1) / BN;
@@ -99,18 +102,20 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
   // A wave's 64 V tasks are 32 row pairs x 2 chunks, so each transposed store instruction hits
   // 64 distinct banks: the 32 pair positions, and the two chunks' d rows 16 rows (32 banks) apart.
   static_assert(LOADS % 2 == 0 && BN == 64, "32 row pairs per stage");
-  uint4 kst[LOADS], vst[LOADS];
+  u32x4 kst[LOADS], vst[LOADS];
   auto vtask = [&](int u2, int& rp, int& ch) {
     rp = lane & 31;
     ch = 2 * (wave + 4 * u2) + (lane >> 5);
   };
+  // Rows past T are read clamped to row T - 1: those keys are masked to P = 0, so their finite
+  // values never reach O.  Row strides are below 2^31 (checked on the host), so an address is
+  // one 32 x 32 -> 64-bit multiply-add.
   auto gload = [&](int stage) {
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int c = tid + 256 * u;
-      const int j = stage * BN + c / CH;
-      kst[u] = j < T ? *reinterpret_cast<const uint4*>(Kb + (int64_t)j * sk.t + 8 * (c % CH))
-                     : make_uint4(0, 0, 0, 0);
+      const uint32_t j = min(stage * BN + c / CH, T - 1);
+      kst[u] = *reinterpret_cast<const u32x4*>(Kb + 8 * (c % CH) + (uint64_t)j * (uint32_t)sk.t);
     }
 #pragma unroll
     for (int u2 = 0; u2 < LOADS / 2; ++u2) {
@@ -118,9 +123,9 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
       vtask(u2, rp, ch);
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        const int j = stage * BN + 2 * rp + e;
-        vst[2 * u2 + e] = j < T ? *reinterpret_cast<const uint4*>(Vb + (int64_t)j * sv.t + 8 * ch)
-                                : make_uint4(0, 0, 0, 0);
+        const uint32_t j = min(stage * BN + 2 * rp + e, T - 1);
+        vst[2 * u2 + e] =
+            *reinterpret_cast<const u32x4*>(Vb + 8 * ch + (uint64_t)j * (uint32_t)sv.t);
       }
     }
   };
@@ -130,22 +135,69 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int c = tid + 256 * u;
-      *reinterpret_cast<uint4*>(ks + (c / CH) * KP + 8 * (c % CH)) = kst[u];
+      *reinterpret_cast<u32x4*>(ks + (c / CH) * KP + 8 * (c % CH)) = kst[u];
     }
 #pragma unroll
     for (int u2 = 0; u2 < LOADS / 2; ++u2) {
       int rp, ch;
       vtask(u2, rp, ch);
-      const uint32_t* e0 = reinterpret_cast<const uint32_t*>(&vst[2 * u2]);
-      const uint32_t* e1 = reinterpret_cast<const uint32_t*>(&vst[2 * u2 + 1]);
+      const u32x4 e0 = vst[2 * u2], e1 = vst[2 * u2 + 1];
       uint32_t* col2 = reinterpret_cast<uint32_t*>(vt + kt_pos(2 * rp));
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         // d = 8 ch + 2t and 8 ch + 2t + 1: low halves of e0/e1 hold the even d
-        col2[(8 * ch + 2 * t) * (VP / 2)] = (e0[t] & 0xFFFFu) | (e1[t] << 16);
-        col2[(8 * ch + 2 * t + 1) * (VP / 2)] = (e0[t] >> 16) | (e1[t] & 0xFFFF0000u);
+        col2[(8 * ch + 2 * t) * (VP / 2)] = pack_lo16(e0[t], e1[t]);
+        col2[(8 * ch + 2 * t + 1) * (VP / 2)] = pack_hi16(e0[t], e1[t]);
       }
     }
+  };
+
+  // One online-softmax step over score tile x0, and x1 too when `two`:
+  // replaces the raw scores by their probabilities against the row's offset and adds them to
+  // l_run, rescaling l_run and O when the offset moves.  The max is taken over the exponent
+  // arguments fma(x, s log2(e), -offset), which the exponentials need anyway; as results of
+  // arithmetic they are canonical, so the compiler forms v_max3 trees without canonicalising
+  // every MFMA output first.  The first tile of a row (offset -inf) always sets the offset;
+  // every processed tile holds at least one unmasked key per row, so it ends finite.
+  auto softmax_step = [&]<bool two>(f32x16& x0, f32x16& x1) {
+    const float mb0 = mb == -INFINITY ? 0.0f : mb;
+    constexpr int NT = two ? 32 : 16;
+    float t[NT];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      x0[r] = fmaf(x0[r], scale_log2, -mb0);
+      t[r] = x0[r];
+      if constexpr (two) {
+        x1[r] = fmaf(x1[r], scale_log2, -mb0);
+        t[16 + r] = x1[r];
+      }
+    }
+    const float my = max_halves(max3_tree(t));
+    if (__any(mb == -INFINITY || my > kRescaleGap)) {
+      const float mb_new = fmaxf(mb, mb0 + my);
+      const float alpha = fast_exp2(mb - mb_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < HS / 32; ++d) oacc[d] *= alpha;
+      const float shift = mb_new - mb0;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        x0[r] -= shift;
+        if (two) x1[r] -= shift;
+      }
+      mb = mb_new;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      x0[r] = fast_exp2(x0[r]);
+      if (two) x1[r] = fast_exp2(x1[r]);
+      t[r] = two ? x0[r] + x1[r] : x0[r];
+    }
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int r = 0; r < w; ++r) t[r] += t[r + w];
+    l_run += t[0];
   };
 
   const bool down = CAUSAL && pass == 1;
@@ -161,6 +213,38 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
     const E* ks = smem + buf * (KTILE + VTILE);
     const E* vt = ks + KTILE;
 
+    // Causal, hs = 64, and all 64 keys of the stage exist and lie at or below every row of
+    // this wave: both 32-key tiles go through one softmax step (one max exchange and one
+    // rescale check per 64 keys, two independent MFMA chains in every phase).  It needs ~160
+    // VGPRs, which the causal kernel's 3 waves per SIMD allow.  The non-causal kernel fits in
+    // 128 VGPRs with one tile at a time, and the fourth wave per SIMD is worth more (measured
+    // 869 against 803 TFLOP/s at B4 H32 N4096); so is hs = 128's register budget.
+    const bool joint = CAUSAL && HS == 64 && s_idx * BN + BN <= T && s_idx * BN + BN - 1 <= i0;
+    if (joint) {
+      f32x16 sa = zero16(), sb = zero16();
+      const E* krow = ks + col * KP + 8 * half;
+#pragma unroll
+      for (int s = 0; s < QS; ++s) {
+        sa = Half16<E>::mfma(ld8<E>(krow + 16 * s), qf[s], sa);
+        sb = Half16<E>::mfma(ld8<E>(krow + 32 * KP + 16 * s), qf[s], sb);
+      }
+      softmax_step.template operator()<true>(sa, sb);
+      vec8_t<E> pa[2], pb[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        pa[r >> 3][r & 7] = (E)sa[r];
+        pb[r >> 3][r & 7] = (E)sb[r];
+      }
+#pragma unroll
+      for (int d = 0; d < HS / 32; ++d) {
+        const E* vrow = vt + (d * 32 + col) * VP + 8 * half;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) oacc[d] = Half16<E>::mfma(ld8<E>(vrow + 16 * s), pa[s], oacc[d]);
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          oacc[d] = Half16<E>::mfma(ld8<E>(vrow + 32 + 16 * s), pb[s], oacc[d]);
+      }
+    } else {
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub) {
       const int jj0 = s_idx * BN + sub * 32;
@@ -183,28 +267,10 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
         }
       }
 
-      float mt = sacc[0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sacc[r]);
-      mt = max_halves(mt);
-      if (__any(mt > m_run + rescale_gap)) {
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = fast_exp2((m_run - m_new) * scale_log2);
-        l_run *= alpha;
-#pragma unroll
-        for (int d = 0; d < HS / 32; ++d) oacc[d] *= alpha;
-        m_run = m_new;
-      }
-      const float mb = m_run * scale_log2;
-      float psum = 0.0f;
+      softmax_step.template operator()<false>(sacc, sacc);
       vec8_t<E> pf[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pr = fast_exp2(fmaf(sacc[r], scale_log2, -mb));
-        psum += pr;
-        pf[r >> 3][r & 7] = (E)pr;
-      }
-      l_run += psum;
+      for (int r = 0; r < 16; ++r) pf[r >> 3][r & 7] = (E)sacc[r];
 
       // O^T += V^T P^T over the tile's 32 keys, two 16-key MFMA steps per d block.
 #pragma unroll
@@ -214,6 +280,7 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
         for (int s = 0; s < 2; ++s)
           oacc[d] = Half16<E>::mfma(*reinterpret_cast<const vec8_t<E>*>(vrow + 16 * s), pf[s], oacc[d]);
       }
+    }
     }
 
     if (i + 1 < n_stages) lstore(buf ^ 1);
@@ -235,7 +302,7 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
             *reinterpret_cast<const uint2*>(o4);
       }
     }
-    if (half == 0) L[(int64_t)bh * T + my_i] = m_run * scale + logf(l_tot);
+    if (half == 0) L[(int64_t)bh * T + my_i] = mb * kLn2 + logf(l_tot);
   }
   }  // pass: the K/V loop ended on a barrier, so the next pass may refill LDS
 }
@@ -247,8 +314,7 @@ void launch_fwd_half(const E* q, const E* k, const E* v, E* o, float* l, int nh,
   const int n_qtiles = (T + 127) / 128;
   const unsigned grid = xcd_grid((int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH);
   hipLaunchKernelGGL((fa2_fwd_half_kernel<E, HS, CAUSAL>), dim3(grid), dim3(256), 0, stream, q,
-                     k, v, o, l, nh, T, BH, n_qtiles, sq, sk, sv, scale, scale * kLog2e,
-                     8.0f / (scale * kLog2e));
+                     k, v, o, l, nh, T, BH, n_qtiles, sq, sk, sv, scale * kLog2e);
 }
 
 // 16-bit operands: unit d-stride, (b, h, t) strides divisible by 8 elements, 16-byte aligned.
@@ -274,6 +340,10 @@ int fwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
     return fail(CTA_ERR_LAYOUT, std::string("flash_attention_fwd (") + what +
                                     ") needs unit d-stride, strides divisible by 8 and 16-byte "
                                     "aligned Q/K/V/O");
+  for (const int64_t* st : {q_strides, k_strides, v_strides})
+    if (st[2] >= (int64_t(1) << 31))
+      return fail(CTA_ERR_LAYOUT, std::string("flash_attention_fwd (") + what +
+                                      ") needs row strides below 2^31 elements");
   const RowStridesB sq{q_strides[0], q_strides[1], q_strides[2]};
   const RowStridesB sk{k_strides[0], k_strides[1], k_strides[2]};
   const RowStridesB sv{v_strides[0], v_strides[1], v_strides[2]};
