@@ -290,7 +290,7 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
   __shared__ __attribute__((aligned(16))) float smem[2 * STAGE + XPOSE];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_index();
   const int half = lane >> 5, col = lane & 31;
   // Head-major items over XCDs; causal items are key-tile pairs (p, n-1-p) of equal cost.
   const int per_head = CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles;
@@ -428,9 +428,18 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
         pacc = mfma32(gv.w, vf[4 * c + 3], pacc);
       }
 
-      // When storing dS, key rows past T are masked too, so a stored tile is exactly 0 there.
-      const bool need_mask =
-          (CAUSAL && ii0 < j0 + 31) || (ii0 + 32 > T) || (STORE_DS && j0 + 32 > T);
+      // Masked entries (and, when storing dS, key rows past T, so a stored tile is exactly 0
+      // there) become -inf, so P = 2^-inf = 0 below.  A separate block behind a wave-uniform
+      // branch: inside the exponential loop the test is if-converted into per-element
+      // predication that every tile pays for.
+      if ((CAUSAL && ii0 < j0 + 31) || (ii0 + 32 > T) || (STORE_DS && j0 + 32 > T)) {
+        asm volatile("");  // a side effect keeps the block from being speculated into selects
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = ii0 + mfma_row(r, half);
+          if ((CAUSAL && my_j > i) || i >= T || (STORE_DS && my_j >= T)) sacc[r] = -INFINITY;
+        }
+      }
       // P = e^{S - L}; masked entries are exactly 0.
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -439,12 +448,7 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
-          float pr = fast_exp2(fmaf(sacc[r], scale_log2, -lr[e] * kLog2e));
-          if (need_mask) {
-            const int i = ii0 + 8 * g + 4 * half + e;
-            if ((CAUSAL && my_j > i) || i >= T || (STORE_DS && my_j >= T)) pr = 0.0f;
-          }
-          sacc[r] = pr;
+          sacc[r] = fast_exp2(fmaf(sacc[r], scale_log2, -lr[e] * kLog2e));
         }
       }
 
