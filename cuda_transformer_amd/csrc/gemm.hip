@@ -351,14 +351,29 @@ void dispatch_a(int am, int bm, dim3 grid, hipStream_t st, const GemmOperand& A,
     dispatch_b<TL, kScalar, ACT>(bm, grid, st, A, B, C, ep, M, N, K, zin, Z, kchunk, ws);
 }
 
-// K splits for a GEMM whose output tiles alone cannot fill the 256 CUs: enough splits for
-// ~512 workgroups, each keeping at least 512 of K; 1 = no split.
+// K splits for a GEMM whose output tiles alone cannot fill the 256 CUs (1 = no split).  The
+// busiest CU runs ceil(tiles S / 256) workgroups of ceil(K / S) each, and the split adds a
+// round trip of S partial outputs through HBM; S in [1, 16] (at least 256 of K per split)
+// minimises the sum.  Costs are in seconds at an MFMA rate of ~0.4 TFLOP/s per CU and
+// ~5 TB/s of HBM.  E.g. the 768 x 3072 x 8192 weight gradient: 144 tiles, S = 7 (1008
+// workgroups, 98% of the CUs' time busy) where a plain "~512 workgroups" rule gives S = 4
+// (576 workgroups, three rounds for 2.25 rounds of work).
 template <class TL>
 int64_t splitk_factor(int64_t M, int64_t N, int64_t K, int64_t Z) {
   const int64_t tiles = ((M + TL::BM - 1) / TL::BM) * ((N + TL::BN - 1) / TL::BN) * Z;
   if (tiles >= 256 || K < 1024) return 1;
-  const int64_t s = std::min<int64_t>({(512 + tiles - 1) / tiles, K / 512, 16});
-  return s >= 2 ? s : 1;
+  constexpr double kCuFlops = 0.4e12, kHbmBytes = 5e12;
+  const double tile_flop_per_k = 2.0 * TL::BM * TL::BN;
+  int64_t best = 1;
+  double best_cost = 0.0;
+  for (int64_t s = 1; s <= 16 && (s == 1 || K / s >= 256); ++s) {
+    const int64_t kchunk = ((K + s - 1) / s + TL::BK - 1) / TL::BK * TL::BK;
+    const int64_t rounds = (tiles * s + 255) / 256;
+    const double cost = (double)rounds * kchunk * tile_flop_per_k / kCuFlops +
+                        (s > 1 ? 8.0 * s * M * N * Z / kHbmBytes : 0.0);
+    if (s == 1 || cost < best_cost) { best = s; best_cost = cost; }
+  }
+  return best;
 }
 
 template <class TL>
