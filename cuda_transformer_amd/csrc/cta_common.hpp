@@ -236,6 +236,9 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 // Attention operands: unit d-stride, (b, h, t) strides divisible by 4, 16-byte aligned base.
 bool attn_layout_ok(const float* p, const int64_t* s);
+// Zero n floats with a fill kernel on `st`, not hipMemsetAsync: memset nodes recorded into a
+// captured HIP graph have given wrong results on replays after the first.
+int zero_floats(float* p, int64_t n, hipStream_t st);
 // Validates (B, nh, T, hs) for the attention entry points; sets the error message on failure.
 int check_attn_sizes(int64_t B, int64_t nh, int64_t T, int64_t hs);
 

@@ -518,11 +518,7 @@ extern "C" int cta_db_calculation(const float* dy, const int64_t* dy_strides, in
   if (n == 0) return CTA_OK;
   if (!db) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
   hipStream_t st = as_stream(stream);
-  if (batch * m == 0) {
-    if (hipMemsetAsync(db, 0, n * sizeof(float), st) != hipSuccess)
-      return fail(CTA_ERR_LAUNCH, "hipMemsetAsync failed");
-    return CTA_OK;
-  }
+  if (batch * m == 0) return zero_floats(db, n, st);
   if (!dy || !dy_strides || !workspace) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
   return colsum_launch(dy, batch, m, n, dy_strides[0], dy_strides[1], dy_strides[2], db,
                        workspace, st);

@@ -83,6 +83,11 @@ unsigned elementwise_grid(int64_t n4) {
   return (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, 256 * 16));
 }
 
+__global__ __launch_bounds__(256) void zero_fill_kernel(float* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    p[i] = 0.0f;
+}
+
 // ------------------------------------------------------------------- row register path
 // A wave owns one row of length n.  VEC: n % 4 == 0 and rows 16-byte aligned, lane loads
 // float4 chunks c = lane + 64*u; otherwise lane loads scalars e = lane + 64*u.
@@ -423,6 +428,13 @@ bool row_vec_ok(const void* a, const void* b, const void* c, int n) {
 }  // namespace
 
 // Shared with the naive attention: softmax over contiguous rows (in place allowed).
+int zero_floats(float* p, int64_t n, hipStream_t st) {
+  if (n <= 0) return CTA_OK;
+  const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 1024);
+  hipLaunchKernelGGL(zero_fill_kernel, dim3(grid), dim3(256), 0, st, p, n);
+  return check_launch("zero fill");
+}
+
 int softmax_rows(const float* x, float* y, int64_t rows, int64_t n, hipStream_t st) {
   if (rows == 0 || n == 0) return CTA_OK;
   if (n > INT32_MAX || rows > ((int64_t)1 << 40)) return fail(CTA_ERR_INVALID_ARGUMENT, "softmax size out of range");
@@ -544,10 +556,8 @@ extern "C" int cta_layernorm_bwd(const float* x, const float* gamma, const float
   if (!dgamma || !dbeta) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
   hipStream_t st = as_stream(stream);
   if (rows == 0) {
-    if (hipMemsetAsync(dgamma, 0, n * sizeof(float), st) != hipSuccess ||
-        hipMemsetAsync(dbeta, 0, n * sizeof(float), st) != hipSuccess)
-      return fail(CTA_ERR_LAUNCH, "hipMemsetAsync failed");
-    return CTA_OK;
+    if (int rc = zero_floats(dgamma, n, st)) return rc;
+    return zero_floats(dbeta, n, st);
   }
   if (!x || !gamma || !mean || !rstd || !dy || !dx || !workspace)
     return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");

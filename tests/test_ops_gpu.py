@@ -322,3 +322,22 @@ def test_cuda_mlp_matches_composition(cuda, B, T, d):
     assert rel_err(f64(fused[0]), out) <= 1e-5
     for g, r in zip(fused[1:], grads):
         assert rel_err(f64(g), r) <= 1e-5
+
+
+def test_reductions_over_zero_rows_are_zero(cuda):
+    # db and dgamma/dbeta over zero rows are sums over nothing: zeros, written by a fill
+    # kernel into outputs that start out holding garbage.
+    from cuda_transformer_amd import capi
+
+    lib = capi.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    db = torch.full((7,), float("nan"), device=cuda)
+    s3 = capi.strides((0, 7, 1))
+    assert lib.cta_db_calculation(None, s3, 1, 0, 7, db.data_ptr(), None, st) == 0
+    dg = torch.full((5,), float("nan"), device=cuda)
+    dbt = torch.full((5,), 3.0, device=cuda)
+    assert lib.cta_layernorm_bwd(None, None, None, None, None, 0, 5, None, dg.data_ptr(),
+                                 dbt.data_ptr(), None, st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(db.cpu(), torch.zeros(7))
+    assert torch.equal(dg.cpu(), torch.zeros(5)) and torch.equal(dbt.cpu(), torch.zeros(5))
