@@ -85,3 +85,34 @@ def test_half_forward_rejects_row_strides_of_2_to_31():
     assert lib.cta_flash_attention_fwd_bf16(16, big, 16, ok, 16, ok, *args) == LAYOUT
     assert b"2^31" in lib.cta_last_error()
     assert lib.cta_flash_attention_fwd_f16(16, ok, 16, ok, 16, big, *args) == LAYOUT
+
+
+def test_header_is_plain_c_and_links(tmp_path):
+    # A C caller (the cgo / FFI case): the header compiles as strict C99, the library links
+    # from C, and an argument error comes back as a status code and a message.
+    import shutil
+    import subprocess
+    from pathlib import Path
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    repo = Path(__file__).resolve().parents[1]
+    lib_dir = repo / "cuda_transformer_amd"
+    src = tmp_path / "caller.c"
+    src.write_text(
+        '#include <stdio.h>\n#include "cuda_transformer_amd.h"\n'
+        "int main(void) {\n"
+        "  const int64_t s[4] = {512, 512, 64, 1};\n"
+        "  int rc = cta_flash_attention_fwd((const float*)16, s, (const float*)16, s,\n"
+        "                                   (const float*)16, s, 1, 1, 8, 64, 1, 0, 0, 0);\n"
+        '  printf("%d %s\\n", rc, cta_last_error());\n'
+        "  return rc == CTA_ERR_INVALID_ARGUMENT ? 0 : 1;\n"
+        "}\n")
+    exe = tmp_path / "caller"
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror",
+                    f"-I{repo / 'include'}", str(src), f"-L{lib_dir}", "-lcuda_transformer_amd",
+                    f"-Wl,-rpath,{lib_dir}", "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "null output pointer" in out.stdout
