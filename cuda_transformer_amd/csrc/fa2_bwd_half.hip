@@ -70,7 +70,7 @@ __global__ __launch_bounds__(256) void fa2_bwd_delta_half_kernel(const E* __rest
 // Waves per SIMD: the non-causal hs = 64 kernel is held to 168 VGPRs for a third wave (a few
 // spilled bytes; measured 3.6% faster); the causal one would spill 112 bytes and run 17% slower.
 template <class E, int HS, bool CAUSAL>
-__global__ __launch_bounds__(256, HS == 64 ? (CAUSAL ? 2 : 3) : 1) void fa2_bwd_dkdv_half_kernel(
+__global__ __launch_bounds__(256, HS == 128 ? 1 : (HS == 64 && CAUSAL ? 2 : 3)) void fa2_bwd_dkdv_half_kernel(
     const E* __restrict__ Q, const E* __restrict__ K, const E* __restrict__ V,
     const E* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
     E* __restrict__ dK, E* __restrict__ dV, E* __restrict__ dsw, int nh, int T,
@@ -82,9 +82,9 @@ __global__ __launch_bounds__(256, HS == 64 ? (CAUSAL ? 2 : 3) : 1) void fa2_bwd_
   constexpr int TP = BN + 8;         // 16-bit pitch of a transposed image row (one d)
   constexpr int XP = 32 + 8;         // 16-bit pitch of the dS transpose
   constexpr int CH = HS / 8;         // 16-byte chunks per row
-  constexpr int LOADS = BN * CH / 256;
+  constexpr int PAIRS = BN / 2 * CH; // row-pair load tasks per tensor and stage
+  constexpr int LOADS = (2 * PAIRS + 255) / 256;  // load tasks per thread
   constexpr int QS = HS / 16;        // MFMA steps over d
-  static_assert(BN * CH % 256 == 0, "stage must split evenly over 256 threads");
   // Stage image, in bytes: Q rows, dO rows, Q^T, dO^T, L log2(e), -delta.
   constexpr int B_ROWS = BN * RP * 2, B_TRS = HS * TP * 2;
   constexpr int OFF_GR = B_ROWS, OFF_QT = 2 * B_ROWS, OFF_GT = 2 * B_ROWS + B_TRS;
@@ -151,8 +151,9 @@ __global__ __launch_bounds__(256, HS == 64 ? (CAUSAL ? 2 : 3) : 1) void fa2_bwd_
   // multiple of 64, so the tensor is the same for a whole wave.
   // Rows past T (ragged last stage) are read clamped to row T - 1: their L and -delta are 0 and
   // the mask sets their P to 0, so dS = 0 there and they add nothing to dK, dV or dQ.
-  constexpr int PAIRS = BN / 2 * CH;
+  // hs = 32 has 128 tasks for 256 threads: waves 0 and 1 take them (wave-uniform).
   static_assert(PAIRS % 64 == 0, "load tensor must be wave-uniform");
+  auto task_live = [&](int u) { return 2 * PAIRS % 256 == 0 || tid + 256 * u < 2 * PAIRS; };
   uint4 st2[LOADS][2];
   float lst = 0.0f, dst = 0.0f;  // L and delta of one query row
   // Sixteen consecutive lanes take the 16 row pairs of one chunk, so a transposed store
@@ -170,7 +171,7 @@ __global__ __launch_bounds__(256, HS == 64 ? (CAUSAL ? 2 : 3) : 1) void fa2_bwd_
   for (int u = 0; u < LOADS; ++u) {
     int tensor, rp, ch;
     task_of(u, tensor, rp, ch);
-    tbase[u] = tensor == 0 ? Qb : dOb;
+    tbase[u] = tensor == 0 ? Qb : dOb;  // (unused for a dead task)
     tstride[u] = tensor == 0 ? sq.t : sdo.t;
 #pragma unroll
     for (int e = 0; e < 2; ++e) toff[u][e] = (int64_t)(2 * rp + e) * tstride[u] + 8 * ch;
@@ -180,6 +181,7 @@ __global__ __launch_bounds__(256, HS == 64 ? (CAUSAL ? 2 : 3) : 1) void fa2_bwd_
     if (r0 + BN <= T) {
 #pragma unroll
       for (int u = 0; u < LOADS; ++u) {
+        if (!task_live(u)) continue;
         const E* sb = tbase[u] + (int64_t)r0 * tstride[u];
 #pragma unroll
         for (int e = 0; e < 2; ++e) st2[u][e] = *reinterpret_cast<const uint4*>(sb + toff[u][e]);
@@ -187,6 +189,7 @@ __global__ __launch_bounds__(256, HS == 64 ? (CAUSAL ? 2 : 3) : 1) void fa2_bwd_
     } else {
 #pragma unroll
       for (int u = 0; u < LOADS; ++u) {
+        if (!task_live(u)) continue;
         int tensor, rp, ch;
         task_of(u, tensor, rp, ch);
 #pragma unroll
@@ -206,6 +209,7 @@ __global__ __launch_bounds__(256, HS == 64 ? (CAUSAL ? 2 : 3) : 1) void fa2_bwd_
     unsigned char* base = smem + buf * STAGE;
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
+      if (!task_live(u)) continue;
       int tensor, rp, ch;
       task_of(u, tensor, rp, ch);
       E* rows = reinterpret_cast<E*>(base + (tensor == 0 ? 0 : OFF_GR));
@@ -384,7 +388,7 @@ __global__ __launch_bounds__(256, HS == 64 ? (CAUSAL ? 2 : 3) : 1) void fa2_bwd_
 // 32); key stages of 64 rows go to LDS transposed ([d][key]); each wave loads its own dS tiles
 // from the workspace straight into registers, one stage ahead.
 template <class E, int HS, bool CAUSAL>
-__global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_half_kernel(
+__global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_ds_half_kernel(
     const E* __restrict__ K, const E* __restrict__ dsw, E* __restrict__ dQ,
     int nh, int T, int bh_base, int BH, int n_qtiles, RowStridesH sk, float scale) {
   constexpr int BN = 64;
@@ -393,8 +397,6 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_half_kern
   constexpr int KTP = BN + 8;  // 16-bit pitch of a K^T row (one d, every key of the stage)
   constexpr int TILE = HS * KTP;
   constexpr int CH = HS / 8;
-  constexpr int LOADS = BN * CH / 256;
-  static_assert(BN * CH % 256 == 0, "stage must split evenly over 256 threads");
   __shared__ __attribute__((aligned(16))) E smem[2 * TILE];
 
   const int tid = threadIdx.x;
@@ -428,20 +430,22 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_half_kern
   // Branch-free clamped loads: every stage issues the same loads, so the compiler counts them
   // exactly and a stage's MFMAs wait only for that stage's dS.  A thread loads rows 2 rp and
   // 2 rp + 1 of chunk ch and stores each d's pair as one 32-bit word of the K^T image.
-  static_assert(LOADS % 2 == 0, "row pairs");
-  uint4 kst[LOADS];
+  constexpr int KPAIRS = 32 * CH;              // K row-pair tasks per stage
+  constexpr int KL = (KPAIRS + 255) / 256;     // ... per thread (hs = 32: waves 0 and 1 only)
+  uint4 kst[2 * KL];
   // A wave's 64 tasks are 32 row pairs x 2 chunks: each transposed store instruction hits 64
   // distinct banks (the 32 pair positions, and the two chunks' d rows 32 banks apart).
   static_assert(BN == 64, "32 row pairs per stage");
   auto pair_of = [&](int u2, int& rp, int& ch) {
     rp = lane & 31;
     ch = 2 * (wave + 4 * u2) + (lane >> 5);
+    return KPAIRS % 256 == 0 || ch < CH;
   };
   auto gload = [&](int stage) {
 #pragma unroll
-    for (int u2 = 0; u2 < LOADS / 2; ++u2) {
+    for (int u2 = 0; u2 < KL; ++u2) {
       int rp, ch;
-      pair_of(u2, rp, ch);
+      if (!pair_of(u2, rp, ch)) continue;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int j = stage * BN + 2 * rp + e;
@@ -454,9 +458,9 @@ __global__ __launch_bounds__(256, HS == 64 ? 2 : 1) void fa2_bwd_dq_ds_half_kern
   auto lstore = [&](int buf) {
     E* kt = smem + buf * TILE;
 #pragma unroll
-    for (int u2 = 0; u2 < LOADS / 2; ++u2) {
+    for (int u2 = 0; u2 < KL; ++u2) {
       int rp, ch;
-      pair_of(u2, rp, ch);
+      if (!pair_of(u2, rp, ch)) continue;
       const uint32_t* e0 = reinterpret_cast<const uint32_t*>(&kst[2 * u2]);
       const uint32_t* e1 = reinterpret_cast<const uint32_t*>(&kst[2 * u2 + 1]);
       uint32_t* col2 = reinterpret_cast<uint32_t*>(kt + 2 * rp);
@@ -536,7 +540,10 @@ bool layout_half_ok(const void* p, const int64_t* s) {
 
 template <typename F>
 void dispatch_half(int64_t hs, int causal, F&& f) {
-  if (hs == 64) {
+  if (hs == 32) {
+    if (causal) f.template operator()<32, true>();
+    else f.template operator()<32, false>();
+  } else if (hs == 64) {
     if (causal) f.template operator()<64, true>();
     else f.template operator()<64, false>();
   } else {
@@ -546,7 +553,7 @@ void dispatch_half(int64_t hs, int causal, F&& f) {
 }
 
 int64_t bwd_half_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs, int causal) {
-  if (B <= 0 || nh <= 0 || T <= 0 || (hs != 64 && hs != 128)) return 0;
+  if (B <= 0 || nh <= 0 || T <= 0 || (hs != 32 && hs != 64 && hs != 128)) return 0;
   return B * nh * ds_tiles_per_head(T, causal != 0) * kDsTileHalf * 2;
 }
 
@@ -560,9 +567,6 @@ int bwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
              uint16_t* dv, float* delta, void* workspace, int64_t workspace_bytes, void* stream,
              const char* what) {
   if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
-  if (hs == 32)
-    return fail(CTA_ERR_UNSUPPORTED_HEAD_DIM, std::string("flash_attention_bwd with ") + what +
-                                                  " inputs supports hs=64 and hs=128");
   if (B * nh * T == 0) return CTA_OK;
   if (!layout_half_ok(q, q_strides) || !layout_half_ok(k, k_strides) ||
       !layout_half_ok(v, v_strides) || !layout_half_ok(o, o_strides) ||
@@ -594,7 +598,10 @@ int bwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
 
   const int64_t rows = B * nh * T;
   const unsigned dgrid = (unsigned)((rows * (hs / 8) + 255) / 256);
-  if (hs == 64)
+  if (hs == 32)
+    hipLaunchKernelGGL((fa2_bwd_delta_half_kernel<E, 32>), dim3(dgrid), dim3(256), 0, st, ob, gb,
+                       delta, (int)nh, (int)T, rows, rsh(o_strides), rsh(do_strides));
+  else if (hs == 64)
     hipLaunchKernelGGL((fa2_bwd_delta_half_kernel<E, 64>), dim3(dgrid), dim3(256), 0, st, ob, gb,
                        delta, (int)nh, (int)T, rows, rsh(o_strides), rsh(do_strides));
   else

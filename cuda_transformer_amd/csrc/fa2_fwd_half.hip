@@ -101,11 +101,15 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
   // transposed, the two rows' values for one d as one 32-bit word (kt_pos keeps them adjacent).
   // A wave's 64 V tasks are 32 row pairs x 2 chunks, so each transposed store instruction hits
   // 64 distinct banks: the 32 pair positions, and the two chunks' d rows 16 rows (32 banks) apart.
-  static_assert(LOADS % 2 == 0 && BN == 64, "32 row pairs per stage");
-  u32x4 kst[LOADS], vst[LOADS];
+  // hs = 32 has 128 V tasks for 256 threads: waves 0 and 1 take them (ch < CH, wave-uniform).
+  static_assert(BN == 64, "32 row pairs per stage");
+  constexpr int VPAIRS = 32 * CH;                 // V row-pair tasks per stage
+  constexpr int VL = (VPAIRS + 255) / 256;        // ... per thread
+  u32x4 kst[LOADS], vst[2 * VL];
   auto vtask = [&](int u2, int& rp, int& ch) {
     rp = lane & 31;
     ch = 2 * (wave + 4 * u2) + (lane >> 5);
+    return VPAIRS % 256 == 0 || ch < CH;
   };
   // Rows past T are read clamped to row T - 1: those keys are masked to P = 0, so their finite
   // values never reach O.  Row strides are below 2^31 (checked on the host), so an address is
@@ -118,9 +122,9 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
       kst[u] = *reinterpret_cast<const u32x4*>(Kb + 8 * (c % CH) + (uint64_t)j * (uint32_t)sk.t);
     }
 #pragma unroll
-    for (int u2 = 0; u2 < LOADS / 2; ++u2) {
+    for (int u2 = 0; u2 < VL; ++u2) {
       int rp, ch;
-      vtask(u2, rp, ch);
+      if (!vtask(u2, rp, ch)) continue;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const uint32_t j = min(stage * BN + 2 * rp + e, T - 1);
@@ -138,9 +142,9 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
       *reinterpret_cast<u32x4*>(ks + (c / CH) * KP + 8 * (c % CH)) = kst[u];
     }
 #pragma unroll
-    for (int u2 = 0; u2 < LOADS / 2; ++u2) {
+    for (int u2 = 0; u2 < VL; ++u2) {
       int rp, ch;
-      vtask(u2, rp, ch);
+      if (!vtask(u2, rp, ch)) continue;
       const u32x4 e0 = vst[2 * u2], e1 = vst[2 * u2 + 1];
       uint32_t* col2 = reinterpret_cast<uint32_t*>(vt + kt_pos(2 * rp));
 #pragma unroll
@@ -330,9 +334,6 @@ int fwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
              int64_t nh, int64_t T, int64_t hs, int causal, uint16_t* o, float* l, void* stream,
              const char* what) {
   if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
-  if (hs == 32)
-    return fail(CTA_ERR_UNSUPPORTED_HEAD_DIM, std::string("flash_attention_fwd with ") + what +
-                                                  " inputs supports hs=64 and hs=128");
   if (B * nh * T == 0) return CTA_OK;
   if (!o || !l) return fail(CTA_ERR_INVALID_ARGUMENT, "null output pointer");
   if (!attn_layout_half_ok(q, q_strides) || !attn_layout_half_ok(k, k_strides) ||
@@ -359,7 +360,8 @@ int fwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
                                             sv, scale, st);                                   \
   else launch_fwd_half<E, HS_, false>(qb, kb, vb, ob, l, (int)nh, (int)T, BH, sq, sk, sv,     \
                                       scale, st);
-  if (hs == 64) { CTA_FWD_HALF(64) }
+  if (hs == 32) { CTA_FWD_HALF(32) }
+  else if (hs == 64) { CTA_FWD_HALF(64) }
   else { CTA_FWD_HALF(128) }
 #undef CTA_FWD_HALF
   return check_launch("flash_attention_fwd (16-bit)");

@@ -381,8 +381,8 @@ std::tuple<at::Tensor, at::Tensor> flash_attention_fwd_half(const at::Tensor& Q,
   const bool bf = Q.scalar_type() == at::kBFloat16;
   TORCH_CHECK(K.scalar_type() == Q.scalar_type() && V.scalar_type() == Q.scalar_type(),
               "Q, K and V must have the same dtype (float32, bfloat16 or float16)");
-  TORCH_CHECK(hs == 64 || hs == 128,
-              "Unsupported head dimension for 16-bit inputs! Only hs=64 and hs=128 are supported.");
+  TORCH_CHECK(hs == 32 || hs == 64 || hs == 128,
+              "Unsupported head dimension! Only hs=32, hs=64, and hs=128 are supported.");
   c10::OptionalDeviceGuard guard(Q.device());
   at::Tensor O = at::empty({B, nh, T, hs}, Q.options());
   at::Tensor L = at::empty({B, nh, T}, Q.options().dtype(at::kFloat));
@@ -438,8 +438,8 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd_half(
               "Q, K, V, O and dO must have the same shape");
   TORCH_CHECK(L.dim() == 3 && L.size(0) == B && L.size(1) == nh && L.size(2) == T,
               "L must have shape (B, nh, T)");
-  TORCH_CHECK(hs == 64 || hs == 128,
-              "Unsupported head dimension for 16-bit inputs! Only hs=64 and hs=128 are supported.");
+  TORCH_CHECK(hs == 32 || hs == 64 || hs == 128,
+              "Unsupported head dimension! Only hs=32, hs=64, and hs=128 are supported.");
   c10::OptionalDeviceGuard guard(Q.device());
   at::Tensor dQ = at::empty({B, nh, T, hs}, Q.options());
   at::Tensor dK = at::empty({B, nh, T, hs}, Q.options());

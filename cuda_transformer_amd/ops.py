@@ -173,7 +173,7 @@ def _(Q, K, V, probs, dO):
 def flash_attention_fwd(Q: Tensor, K: Tensor, V: Tensor, causal: bool) -> tuple[Tensor, Tensor]:
     """FA2 forward -> (O, L), L = rowmax + ln(rowsum)  (reference ops.py:109-111).
 
-    Extension: bfloat16 or float16 Q, K, V (hs 64 or 128) run the 16-bit kernel, which returns
+    Extension: bfloat16 or float16 Q, K, V (hs 32, 64 or 128) run the 16-bit kernel, which returns
     O in the input dtype and L in float32; the reference's kernels are float32 only."""
     return _ops.flash_attention_fwd.default(Q, K, V, causal)
 
@@ -195,7 +195,7 @@ def flash_attention_bwd(Q: Tensor, K: Tensor, V: Tensor, O: Tensor, dO: Tensor, 
                         causal: bool):
     """FA2 backward -> (dQ, dK, dV)  (reference ops.py:123-125).
 
-    Extension: bfloat16 or float16 Q, K, V, O, dO with float32 L (hs 64 or 128) run the 16-bit
+    Extension: bfloat16 or float16 Q, K, V, O, dO with float32 L (hs 32, 64 or 128) run the 16-bit
     kernels and return gradients in the input dtype."""
     return _ops.flash_attention_bwd.default(Q, K, V, O, dO, L, causal)
 

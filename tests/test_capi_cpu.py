@@ -59,6 +59,9 @@ def test_workspace_queries():
     assert lib.cta_causal_self_attention_bwd_workspace(8, 33) == 8 * 33 * 33 * 4
     assert lib.cta_cuda_fma_workspace(1, 8192, 768, 3072) == 0          # fills the GPU: no split
     assert lib.cta_cuda_fma_workspace(1, 768, 8192, 3072) > 0           # 144 tiles, K = 8192
+    for hs in (32, 64, 128):  # 16-bit dS workspace: 2 KiB per stored 32x32 tile
+        assert lib.cta_flash_attention_bwd_bf16_workspace(1, 2, 64, hs, 1) == 2 * 3 * 2048
+    assert lib.cta_flash_attention_bwd_bf16_workspace(1, 2, 64, 48, 1) == 0
 
 
 def test_other_entry_points_validate_arguments():

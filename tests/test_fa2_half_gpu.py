@@ -8,7 +8,7 @@ float16).  Hence per element
     |O - O_ref| <= 2^-9 |O_ref| + 2^-9 max_j |v_j| (+ FP32 accumulation),
 bounded here by 2^-8 (|O_ref| + max|V|) for both types; L comes from FP32 scores of exact
 16-bit products and keeps an FP32-level bound of 1e-4.  Shapes follow the FP32 suite (ragged T,
-causal and full, hs 64 and 128, benchmark config 1).
+causal and full, hs 32, 64 and 128, benchmark config 1).
 """
 import numpy as np
 import pytest
@@ -32,6 +32,9 @@ SHAPES = [
     (1, 3, 1, 64, True),     # single row
     (2, 2, 1000, 64, False),
     (1, 2, 1030, 128, True),
+    (2, 4, 128, 32, False),  # hs = 32 (the reference suite's (2, 4, 128, 32) shape)
+    (2, 2, 129, 32, True),
+    (1, 3, 300, 32, True),
 ]
 
 
@@ -102,8 +105,8 @@ def test_fa2_half_deterministic(cuda):
 def test_fa2_half_errors(cuda):
     from cuda_transformer.ops import flash_attention_fwd
 
-    q = torch.randn(1, 2, 16, 32, device=cuda, dtype=torch.bfloat16)
-    with pytest.raises(RuntimeError, match="hs=64 and hs=128"):
+    q = torch.randn(1, 2, 16, 48, device=cuda, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="Only hs=32, hs=64, and hs=128 are supported"):
         flash_attention_fwd(q, q, q, False)
     q = torch.randn(1, 2, 16, 64, device=cuda, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="same dtype"):
@@ -127,6 +130,9 @@ BWD_SHAPES = [
     (1, 2, 512, 128, True),
     (1, 3, 1, 64, True),
     (2, 2, 1000, 64, False),
+    (2, 4, 128, 32, False),
+    (2, 2, 129, 32, True),
+    (1, 2, 600, 32, True),
 ]
 
 
