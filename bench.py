@@ -435,8 +435,8 @@ def _cpu_time(fn, target_s=2.0):
 
 
 def ops_workload(args):
-    """Benchmark config 4 (GPT-2-small widths, FP32): linear GEMM fwd/bwd, db, exact GELU,
-    LayerNorm and row softmax, each launched through the C ABI.  One JSON line per op with
+    """Benchmark config 4 (GPT-2-small widths, FP32): linear GEMM fwd/bwd, db, exact and
+    tanh-approximated GELU, LayerNorm and row softmax, each launched through the C ABI.  One JSON line per op with
     the kernel's roofline (MFMA TFLOP/s for GEMMs, HBM GB/s otherwise) and the CPU oracle
     (float32 numpy) timed on a bounded sample of the same op."""
     import numpy as np
@@ -537,6 +537,14 @@ def ops_workload(args):
         emit("gelu_bwd", [M, Nn],
              _time_kernel(lambda: lib.cta_gelu_bwd(vp(xg), vp(gg), vp(yg), n, st), reps),
              12.0 * n, "GB/s", _cpu_time(lambda: ew.gelu_backward(xgc, ggc)), 12.0 * n / 8, sample8)
+        # ---- tanh-approximated GELU (the form config 4 names) on the same tensor
+        emit("gelu_tanh_fwd", [M, Nn],
+             _time_kernel(lambda: lib.cta_gelu_tanh_fwd(vp(xg), vp(yg), n, st), reps),
+             8.0 * n, "GB/s", _cpu_time(lambda: ew.gelu_tanh_forward(xgc)), 8.0 * n / 8, sample8)
+        emit("gelu_tanh_bwd", [M, Nn],
+             _time_kernel(lambda: lib.cta_gelu_tanh_bwd(vp(xg), vp(gg), vp(yg), n, st), reps),
+             12.0 * n, "GB/s", _cpu_time(lambda: ew.gelu_tanh_backward(xgc, ggc)), 12.0 * n / 8,
+             sample8)
         del xg, yg, gg
 
         # ---- LayerNorm over 768 on [8192, 768], gamma = 1, beta = 0

@@ -2,8 +2,9 @@
 
 Same classes, ``apply`` signatures and saved tensors as the reference's cuda_autograd_fns/
 (cuda_flash_attention.py:4-17, cuda_linear_layer.py:4-28, cuda_gelu_layer.py:4-14,
-cuda_softmax_layer.py:4-15, cuda_causal_self_attention.py:4-35), plus ``CudaLayerNorm`` and
-``CudaMLP`` (the GPT MLP with its GELU folded into the GEMM epilogues).
+cuda_softmax_layer.py:4-15, cuda_causal_self_attention.py:4-35), plus ``CudaLayerNorm``,
+``CudaMLP`` (the GPT MLP with its GELU folded into the GEMM epilogues) and ``CudaGeluTanhLayer``
+(the tanh-approximated GELU).
 
 Deviations, each a fix:
 
@@ -19,12 +20,12 @@ import torch
 from .ops import (
     causal_self_attention_bwd, causal_self_attention_fwd, cuda_fma, cuda_fma_gelu,
     cuda_fma_gelu_grad, cuda_softmax, cuda_softmax_bwd, db_calculation, flash_attention_bwd, flash_attention_fwd, gelu_activation,
-    gelu_activation_bwd, layernorm_bwd, layernorm_fwd,
+    gelu_activation_bwd, gelu_tanh_activation, gelu_tanh_activation_bwd, layernorm_bwd, layernorm_fwd,
 )
 
 __all__ = [
     "CudaCausalSelfAttention", "CudaFlashAttention", "CudaGeluLayer", "CudaLinearLayer",
-    "CudaSoftmaxLayer", "CudaLayerNorm", "CudaMLP",
+    "CudaSoftmaxLayer", "CudaLayerNorm", "CudaMLP", "CudaGeluTanhLayer",
 ]
 
 
@@ -92,6 +93,22 @@ class CudaGeluLayer(torch.autograd.Function):
     def backward(ctx, grad_output):
         (x,) = ctx.saved_tensors
         return gelu_activation_bwd(x, grad_output.contiguous())
+
+
+class CudaGeluTanhLayer(torch.autograd.Function):
+    """tanh-approximated GELU, ``F.gelu(x, approximate="tanh")``; same saved tensor and
+    backward shape as ``CudaGeluLayer``.  No reference class (its GELU is erf-exact)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        out = gelu_tanh_activation(x)
+        ctx.save_for_backward(x)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (x,) = ctx.saved_tensors
+        return gelu_tanh_activation_bwd(x, grad_output.contiguous())
 
 
 class CudaMLP(torch.autograd.Function):

@@ -65,6 +65,8 @@ SIGNATURES = {
     "cta_db_calculation": (_int, [_p, _i64p, _i64, _i64, _i64, _p, _p, _p]),
     "cta_gelu_fwd": (_int, [_p, _p, _i64, _p]),
     "cta_gelu_bwd": (_int, [_p, _p, _p, _i64, _p]),
+    "cta_gelu_tanh_fwd": (_int, [_p, _p, _i64, _p]),
+    "cta_gelu_tanh_bwd": (_int, [_p, _p, _p, _i64, _p]),
     "cta_softmax_fwd": (_int, [_p, _p, _i64, _i64, _p]),
     "cta_softmax_bwd": (_int, [_p, _p, _p, _i64, _i64, _p]),
     "cta_layernorm_fwd": (_int, [_p, _p, _p, _i64, _i64, _f32, _p, _p, _p, _p]),

@@ -1,8 +1,10 @@
-// Bandwidth-bound kernels: exact GELU, row softmax, LayerNorm (forward and backward).
+// Bandwidth-bound kernels: exact GELU, row softmax, LayerNorm (forward and backward), and a
+// tanh-approximated GELU.
 //
 //  * GELU follows Transformer_kernels/GeLU.cuh:7-29: y = x Phi(x),
 //    dx = dy (Phi(x) + x phi(x)), phi(x) = e^{-x^2/2} / sqrt(2 pi); Phi from a Chebyshev-fitted
 //    erfc (cta_common.hpp), short enough that the kernels stay HBM-bound.
+//  * The tanh GELU has no reference kernel; it is torch's F.gelu(x, approximate="tanh").
 //  * Softmax follows softmax.cuh:25-159 (row max, sum of e^{x - max}, normalise;
 //    backward dx = p (dp - sum p dp)).
 //  * LayerNorm has no kernel in the reference; its semantics come from gpt/gpt.py:47-59:
@@ -23,11 +25,48 @@ namespace {
 // ------------------------------------------------------------------------------- GELU
 // (gelu_f / gelu_grad live in cta_common.hpp, shared with the GEMM epilogue.)
 
+// tanh-approximated GELU, torch's F.gelu(x, approximate="tanh") (the GPT-2 form; the reference
+// has no kernel for it): y = x (1 + tanh u) / 2 with u = sqrt(2/pi) (x + 0.044715 x^3).
+// With a = e^{-2|u|} in (0, 1] and r = 1 / (1 + a), (1 + tanh u) / 2 is r for u >= 0 and a r
+// for u < 0 (u has the sign of x), and (1 - tanh^2 u) / 4 = a r^2.  Neither form overflows or
+// cancels, for any x:  y = x s  and  dy/dx = s + 2 x u' a r^2,  u' = sqrt(2/pi)(1 + 3 0.044715 x^2).
+constexpr float kSqrt2OverPi = 0.7978845608028654f;
+constexpr float kGeluCubic = 0.044715f;
+__device__ __forceinline__ void gelu_tanh_parts(float x, float& s, float& ar2) {
+  // v = 2 u log2(e), so a = 2^{-|v|}
+  const float v = x * fmaf(2.0f * kLog2e * kSqrt2OverPi * kGeluCubic, x * x,
+                           2.0f * kLog2e * kSqrt2OverPi);
+  const float a = __builtin_amdgcn_exp2f(-fabsf(v));
+  const float r = __builtin_amdgcn_rcpf(1.0f + a);
+  s = x < 0.0f ? a * r : r;
+  ar2 = a * r * r;
+}
+__device__ __forceinline__ float gelu_tanh_f(float x) {
+  float s, ar2;
+  gelu_tanh_parts(x, s, ar2);
+  return x * s;
+}
+__device__ __forceinline__ float gelu_tanh_grad(float x, float g) {
+  float s, ar2;
+  gelu_tanh_parts(x, s, ar2);
+  const float du = kSqrt2OverPi * fmaf(3.0f * kGeluCubic, x * x, 1.0f);
+  return g * fmaf(2.0f * x * du, ar2, s);
+}
+
+template <bool TANH>
+__device__ __forceinline__ float gelu_act(float x) {
+  return TANH ? gelu_tanh_f(x) : gelu_f(x);
+}
+template <bool TANH>
+__device__ __forceinline__ float gelu_act_grad(float x, float g) {
+  return TANH ? gelu_tanh_grad(x, g) : gelu_grad(x, g);
+}
+
 // Each thread handles four independent float4 per iteration (index i + 256*u within a chunk of
 // 1024 float4) so that four loads are in flight before the math starts.
-__global__ __launch_bounds__(256) void gelu_fwd_kernel(const float* __restrict__ x,
-                                                       float* __restrict__ y, int64_t n4,
-                                                       int64_t n) {
+template <bool TANH>
+__device__ __forceinline__ void gelu_fwd_body(const float* __restrict__ x, float* __restrict__ y,
+                                              int64_t n4, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * 1024;
   for (int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x; base < n4; base += stride) {
     float4 v[4];
@@ -40,20 +79,21 @@ __global__ __launch_bounds__(256) void gelu_fwd_kernel(const float* __restrict__
     for (int u = 0; u < 4; ++u) {
       const int64_t i = base + 256 * u;
       if (i < n4)
-        st4(y + 4 * i, make_float4(gelu_f(v[u].x), gelu_f(v[u].y), gelu_f(v[u].z), gelu_f(v[u].w)));
+        st4(y + 4 * i, make_float4(gelu_act<TANH>(v[u].x), gelu_act<TANH>(v[u].y),
+                                   gelu_act<TANH>(v[u].z), gelu_act<TANH>(v[u].w)));
     }
   }
   // tail (n % 4 elements) handled by the first threads of block 0
   if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
     const int64_t i = 4 * n4 + threadIdx.x;
-    y[i] = gelu_f(x[i]);
+    y[i] = gelu_act<TANH>(x[i]);
   }
 }
 
-__global__ __launch_bounds__(256) void gelu_bwd_kernel(const float* __restrict__ x,
-                                                       const float* __restrict__ dy,
-                                                       float* __restrict__ dx, int64_t n4,
-                                                       int64_t n) {
+template <bool TANH>
+__device__ __forceinline__ void gelu_bwd_body(const float* __restrict__ x,
+                                              const float* __restrict__ dy,
+                                              float* __restrict__ dx, int64_t n4, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * 1024;
   for (int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x; base < n4; base += stride) {
     float4 v[4], g[4];
@@ -67,14 +107,39 @@ __global__ __launch_bounds__(256) void gelu_bwd_kernel(const float* __restrict__
     for (int u = 0; u < 4; ++u) {
       const int64_t i = base + 256 * u;
       if (i < n4)
-        st4(dx + 4 * i, make_float4(gelu_grad(v[u].x, g[u].x), gelu_grad(v[u].y, g[u].y),
-                                    gelu_grad(v[u].z, g[u].z), gelu_grad(v[u].w, g[u].w)));
+        st4(dx + 4 * i,
+            make_float4(gelu_act_grad<TANH>(v[u].x, g[u].x), gelu_act_grad<TANH>(v[u].y, g[u].y),
+                        gelu_act_grad<TANH>(v[u].z, g[u].z), gelu_act_grad<TANH>(v[u].w, g[u].w)));
     }
   }
   if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
     const int64_t i = 4 * n4 + threadIdx.x;
-    dx[i] = gelu_grad(x[i], dy[i]);
+    dx[i] = gelu_act_grad<TANH>(x[i], dy[i]);
   }
+}
+
+// One kernel name per form, so that kernel traces tell them apart.
+__global__ __launch_bounds__(256) void gelu_fwd_kernel(const float* __restrict__ x,
+                                                       float* __restrict__ y, int64_t n4,
+                                                       int64_t n) {
+  gelu_fwd_body<false>(x, y, n4, n);
+}
+__global__ __launch_bounds__(256) void gelu_bwd_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ dy,
+                                                       float* __restrict__ dx, int64_t n4,
+                                                       int64_t n) {
+  gelu_bwd_body<false>(x, dy, dx, n4, n);
+}
+__global__ __launch_bounds__(256) void gelu_tanh_fwd_kernel(const float* __restrict__ x,
+                                                            float* __restrict__ y, int64_t n4,
+                                                            int64_t n) {
+  gelu_fwd_body<true>(x, y, n4, n);
+}
+__global__ __launch_bounds__(256) void gelu_tanh_bwd_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ dy,
+                                                            float* __restrict__ dx, int64_t n4,
+                                                            int64_t n) {
+  gelu_bwd_body<true>(x, dy, dx, n4, n);
 }
 
 unsigned elementwise_grid(int64_t n4) {
@@ -481,29 +546,53 @@ int64_t layernorm_bwd_workspace_floats(int64_t rows, int64_t n) {
 
 using namespace cta;
 
-extern "C" int cta_gelu_fwd(const float* x, float* y, int64_t numel, void* stream) {
+namespace {
+template <bool TANH>
+int launch_gelu_fwd(const float* x, float* y, int64_t numel, void* stream, const char* name) {
   if (numel < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
   if (numel == 0) return CTA_OK;
   if (!x || !y) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
   if (!aligned16(x) || !aligned16(y))
-    return fail(CTA_ERR_LAYOUT, "gelu_activation needs 16-byte aligned buffers");
+    return fail(CTA_ERR_LAYOUT, std::string(name) + " needs 16-byte aligned buffers");
   const int64_t n4 = numel / 4;
-  hipLaunchKernelGGL(gelu_fwd_kernel, dim3(elementwise_grid(n4)), dim3(256), 0, as_stream(stream),
-                     x, y, n4, numel);
-  return check_launch("gelu_activation");
+  hipLaunchKernelGGL(TANH ? gelu_tanh_fwd_kernel : gelu_fwd_kernel, dim3(elementwise_grid(n4)),
+                     dim3(256), 0,
+                     as_stream(stream), x, y, n4, numel);
+  return check_launch(name);
 }
 
-extern "C" int cta_gelu_bwd(const float* x, const float* dy, float* dx, int64_t numel,
-                            void* stream) {
+template <bool TANH>
+int launch_gelu_bwd(const float* x, const float* dy, float* dx, int64_t numel, void* stream,
+                    const char* name) {
   if (numel < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
   if (numel == 0) return CTA_OK;
   if (!x || !dy || !dx) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
   if (!aligned16(x) || !aligned16(dy) || !aligned16(dx))
-    return fail(CTA_ERR_LAYOUT, "gelu_activation_bwd needs 16-byte aligned buffers");
+    return fail(CTA_ERR_LAYOUT, std::string(name) + " needs 16-byte aligned buffers");
   const int64_t n4 = numel / 4;
-  hipLaunchKernelGGL(gelu_bwd_kernel, dim3(elementwise_grid(n4)), dim3(256), 0, as_stream(stream),
-                     x, dy, dx, n4, numel);
-  return check_launch("gelu_activation_bwd");
+  hipLaunchKernelGGL(TANH ? gelu_tanh_bwd_kernel : gelu_bwd_kernel, dim3(elementwise_grid(n4)),
+                     dim3(256), 0,
+                     as_stream(stream), x, dy, dx, n4, numel);
+  return check_launch(name);
+}
+}  // namespace
+
+extern "C" int cta_gelu_fwd(const float* x, float* y, int64_t numel, void* stream) {
+  return launch_gelu_fwd<false>(x, y, numel, stream, "gelu_activation");
+}
+
+extern "C" int cta_gelu_bwd(const float* x, const float* dy, float* dx, int64_t numel,
+                            void* stream) {
+  return launch_gelu_bwd<false>(x, dy, dx, numel, stream, "gelu_activation_bwd");
+}
+
+extern "C" int cta_gelu_tanh_fwd(const float* x, float* y, int64_t numel, void* stream) {
+  return launch_gelu_fwd<true>(x, y, numel, stream, "gelu_tanh_activation");
+}
+
+extern "C" int cta_gelu_tanh_bwd(const float* x, const float* dy, float* dx, int64_t numel,
+                                 void* stream) {
+  return launch_gelu_bwd<true>(x, dy, dx, numel, stream, "gelu_tanh_activation_bwd");
 }
 
 extern "C" int cta_softmax_fwd(const float* x, float* y, int64_t rows, int64_t n, void* stream) {

@@ -212,6 +212,37 @@ at::Tensor gelu_activation_bwd(at::Tensor x, at::Tensor dy) {
   return out;
 }
 
+// ------------------------------------------------------------------ tanh GELU
+// New ops with no reference launcher: F.gelu(x, approximate="tanh") and its input gradient,
+// with the same checks and layout as gelu_activation / gelu_activation_bwd above.
+at::Tensor gelu_tanh_activation(at::Tensor x) {
+  TORCH_CHECK(x.is_cuda(), "x must be a CUDA tensor");
+  TORCH_CHECK(x.is_contiguous(), "x must be contiguous");
+  check_f32(x, "x");
+  c10::OptionalDeviceGuard guard(x.device());
+  const at::Tensor xd = dense(x);
+  at::Tensor out = at::empty(x.sizes(), x.options());
+  check_rc(cta_gelu_tanh_fwd(xd.data_ptr<float>(), out.data_ptr<float>(), x.numel(),
+                             stream_of(x)));
+  return out;
+}
+
+at::Tensor gelu_tanh_activation_bwd(at::Tensor x, at::Tensor dy) {
+  TORCH_CHECK(x.is_cuda(), "x must be a CUDA tensor");
+  TORCH_CHECK(x.is_contiguous(), "x must be contiguous");
+  TORCH_CHECK(dy.is_cuda(), "dy must be a CUDA tensor");
+  TORCH_CHECK(dy.is_contiguous(), "dy must be contiguous");
+  check_f32(x, "x");
+  check_f32(dy, "dy");
+  TORCH_CHECK(x.numel() == dy.numel(), "x and dy must have the same number of elements");
+  c10::OptionalDeviceGuard guard(x.device());
+  const at::Tensor xd = dense(x), gd = dense(dy);
+  at::Tensor out = at::empty(x.sizes(), x.options());
+  check_rc(cta_gelu_tanh_bwd(xd.data_ptr<float>(), gd.data_ptr<float>(), out.data_ptr<float>(),
+                             x.numel(), stream_of(x)));
+  return out;
+}
+
 // ------------------------------------------------------------------ softmax
 // cf. Transformer_launchers/softmax_layer.cu:22-78
 at::Tensor cuda_softmax(at::Tensor x) {
@@ -531,6 +562,8 @@ TORCH_LIBRARY(cuda_transformer, m) {
   m.def("cuda_fma_gelu_grad(Tensor dy, Tensor weights, Tensor pre) -> Tensor");
   m.def("gelu_activation(Tensor x) -> Tensor");
   m.def("gelu_activation_bwd(Tensor x, Tensor dy) -> Tensor");
+  m.def("gelu_tanh_activation(Tensor x) -> Tensor");
+  m.def("gelu_tanh_activation_bwd(Tensor x, Tensor dy) -> Tensor");
   m.def("cuda_softmax(Tensor x) -> Tensor");
   m.def("cuda_softmax_bwd(Tensor probs, Tensor dp) -> Tensor");
   m.def("causal_self_attention_fwd(Tensor qkv, int nh, bool causal) -> (Tensor, Tensor)");
@@ -554,6 +587,8 @@ TORCH_LIBRARY_IMPL(cuda_transformer, CUDA, m) {
   m.impl("cuda_fma_gelu_grad", &cuda_fma_gelu_grad);
   m.impl("gelu_activation", &gelu_activation);
   m.impl("gelu_activation_bwd", &gelu_activation_bwd);
+  m.impl("gelu_tanh_activation", &gelu_tanh_activation);
+  m.impl("gelu_tanh_activation_bwd", &gelu_tanh_activation_bwd);
   m.impl("cuda_softmax", &cuda_softmax);
   m.impl("cuda_softmax_bwd", &cuda_softmax_bwd);
   m.impl("causal_self_attention_fwd", &causal_self_attention_fwd);

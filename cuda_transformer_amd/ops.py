@@ -11,7 +11,8 @@ shape functions for FakeTensor / ``torch.compile`` tracing.  Two deviations, bot
 
 Added: ``layernorm_fwd`` / ``layernorm_bwd`` (the reference's LayerNorm is plain torch,
 gpt/gpt.py:47-59), and ``cuda_fma_gelu`` / ``cuda_fma_gelu_grad``, the GPT MLP's linear+GELU
-pairs (gpt/gpt.py:134-135 and their backward) fused into one GEMM each.
+pairs (gpt/gpt.py:134-135 and their backward) fused into one GEMM each, and
+``gelu_tanh_activation`` / ``gelu_tanh_activation_bwd``, the tanh-approximated GELU.
 """
 import torch
 from torch import Tensor
@@ -19,7 +20,7 @@ from torch import Tensor
 __all__ = [
     "cuda_fma", "db_calculation", "cuda_fma_gelu", "cuda_fma_gelu_grad",
     "cuda_softmax", "cuda_softmax_bwd",
-    "gelu_activation", "gelu_activation_bwd",
+    "gelu_activation", "gelu_activation_bwd", "gelu_tanh_activation", "gelu_tanh_activation_bwd",
     "causal_self_attention_fwd", "causal_self_attention_bwd",
     "flash_attention_fwd", "flash_attention_bwd",
     "layernorm_fwd", "layernorm_bwd",
@@ -135,6 +136,31 @@ def gelu_activation_bwd(x: Tensor, dy: Tensor) -> Tensor:
 
 
 @torch.library.register_fake("cuda_transformer::gelu_activation_bwd")
+def _(x, dy):
+    _f32(x, dy)
+    _same_device(x, dy)
+    return torch.empty_like(x)
+
+
+# ----------------------------------------------------------------- tanh GELU
+def gelu_tanh_activation(x: Tensor) -> Tensor:
+    """tanh-approximated GELU, ``F.gelu(x, approximate="tanh")``.  New op: the reference's GELU
+    is erf-exact (GeLU.cuh:7-16); this is the GPT-2 form, for models that use it."""
+    return _ops.gelu_tanh_activation.default(x)
+
+
+@torch.library.register_fake("cuda_transformer::gelu_tanh_activation")
+def _(x):
+    _f32(x)
+    return torch.empty_like(x)
+
+
+def gelu_tanh_activation_bwd(x: Tensor, dy: Tensor) -> Tensor:
+    """Input gradient of ``gelu_tanh_activation`` (torch's tanh-GELU backward)."""
+    return _ops.gelu_tanh_activation_bwd.default(x, dy)
+
+
+@torch.library.register_fake("cuda_transformer::gelu_tanh_activation_bwd")
 def _(x, dy):
     _f32(x, dy)
     _same_device(x, dy)

@@ -253,6 +253,16 @@ int cta_gelu_fwd(const float* x, float* y, int64_t numel, void* stream);
  * (gelu_activation.cu:49-77). */
 int cta_gelu_bwd(const float* x, const float* dy, float* dx, int64_t numel, void* stream);
 
+/* y = x * (1 + tanh(u)) / 2, u = sqrt(2/pi) * (x + 0.044715 x^3): torch's
+ * F.gelu(x, approximate="tanh").  No reference kernel: the reference's GELU is erf-exact
+ * (GeLU.cuh:7-16); this is the tanh-approximated GELU of the non-attention benchmark workload,
+ * for models that use the GPT-2 form.  Same buffer rules as cta_gelu_fwd. */
+int cta_gelu_tanh_fwd(const float* x, float* y, int64_t numel, void* stream);
+
+/* dx = dy * d/dx [x * (1 + tanh(u)) / 2], as torch's tanh-GELU backward.  No reference
+ * kernel (see cta_gelu_tanh_fwd). */
+int cta_gelu_tanh_bwd(const float* x, const float* dy, float* dx, int64_t numel, void* stream);
+
 /* Row softmax over `rows` rows of length n.  Replaces cuda_transformer::cuda_softmax
  * (Transformer_launchers/softmax_layer.cu:22-47). */
 int cta_softmax_fwd(const float* x, float* y, int64_t rows, int64_t n, void* stream);

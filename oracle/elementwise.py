@@ -32,6 +32,26 @@ def gelu_backward(x, dy):
     return np.asarray(dy, dtype=np.float64) * (normal_cdf(x) + x * pdf)
 
 
+SQRT_2_OVER_PI = math.sqrt(2.0 / math.pi)
+GELU_CUBIC = 0.044715
+
+
+def gelu_tanh_forward(x):
+    """y = x (1 + tanh u) / 2, u = sqrt(2/pi) (x + 0.044715 x^3): the tanh-approximated GELU of
+    the non-attention benchmark workload (torch's F.gelu(x, approximate="tanh")).  The reference
+    has no kernel for it; its GELU is erf-exact (GeLU.cuh:7-16)."""
+    x = np.asarray(x, dtype=np.float64)
+    return 0.5 * x * (1.0 + np.tanh(SQRT_2_OVER_PI * (x + GELU_CUBIC * x**3)))
+
+
+def gelu_tanh_backward(x, dy):
+    """dx = dy ((1 + tanh u) / 2 + x (1 - tanh^2 u) u' / 2), u' = sqrt(2/pi)(1 + 3 0.044715 x^2)."""
+    x = np.asarray(x, dtype=np.float64)
+    t = np.tanh(SQRT_2_OVER_PI * (x + GELU_CUBIC * x**3))
+    du = SQRT_2_OVER_PI * (1.0 + 3.0 * GELU_CUBIC * x * x)
+    return np.asarray(dy, dtype=np.float64) * (0.5 * (1.0 + t) + 0.5 * x * (1.0 - t * t) * du)
+
+
 def softmax_forward(x):
     """Row softmax over the last axis: max pass, sum of e^{x - max}, then e^{x - max} * (1/sum)
     (naive_softmax, Transformer_kernels/softmax.cuh:25-106)."""

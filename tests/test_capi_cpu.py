@@ -70,6 +70,9 @@ def test_other_entry_points_validate_arguments():
     assert lib.cta_cuda_fma(16, s3, 16, s3, 16, 1, 2, 3, 4, 5, 3, 16, None, None) == INVALID  # w_batch
     assert lib.cta_gelu_fwd(16, 16, -1, None) == INVALID
     assert lib.cta_gelu_fwd(20, 16, 8, None) == LAYOUT
+    assert lib.cta_gelu_tanh_fwd(16, 16, -1, None) == INVALID
+    assert lib.cta_gelu_tanh_bwd(16, 16, 20, 8, None) == LAYOUT
+    assert lib.cta_gelu_tanh_bwd(16, None, 16, 8, None) == INVALID
     assert lib.cta_softmax_fwd(16, 16, -1, 4, None) == INVALID
     assert lib.cta_layernorm_fwd(16, 16, 16, 4, 0, ctypes.c_float(1e-5), 16, 16, 16, None) == INVALID
     assert lib.cta_causal_self_attention_fwd(16, 1, 4, 10, 3, 1, 16, 16, None) == INVALID  # C % nh

@@ -4,7 +4,7 @@ Every op allocates through torch and launches on the current stream with no host
 synchronisation, no hipMalloc and no memset node, so a training step built from them can be
 captured once and replayed without launch overhead.  The test captures FlashAttention-2 forward
 + backward (FP32 and BF16), the GEMM (including a split-K shape, whose workspace and reduction
-kernel are captured too), bias gradient, GELU, softmax and LayerNorm forward + backward; then it
+kernel are captured too), bias gradient, GELU (both forms), softmax and LayerNorm forward + backward; then it
 replays the graph several times on fresh inputs, with eager work between replays, and requires
 every replay to equal the eager result bit for bit.
 """
@@ -23,7 +23,8 @@ def _fill(tensors, seed):
 def test_ops_replay_in_a_hip_graph(cuda):
     from cuda_transformer.ops import (cuda_fma, cuda_softmax, cuda_softmax_bwd, db_calculation,
                                       flash_attention_bwd, flash_attention_fwd, gelu_activation,
-                                      gelu_activation_bwd, layernorm_bwd, layernorm_fwd)
+                                      gelu_activation_bwd, gelu_tanh_activation,
+                                      gelu_tanh_activation_bwd, layernorm_bwd, layernorm_fwd)
 
     q, k, v, do = (torch.empty(2, 4, 257, 64, device=cuda) for _ in range(4))
     qh, kh, vh, doh = (torch.empty(1, 2, 200, 128, device=cuda, dtype=torch.bfloat16)
@@ -45,13 +46,15 @@ def test_ops_replay_in_a_hip_graph(cuda):
         yk = cuda_fma(xs.transpose(1, 2), ys, torch.zeros(96, device=cuda))
         gy = gelu_activation(y)
         dgy = gelu_activation_bwd(y, gy)
+        ty = gelu_tanh_activation(y)
+        dty = gelu_tanh_activation_bwd(y, ty)
         p = cuda_softmax(gy)
         dp = cuda_softmax_bwd(p, gy)
         db = db_calculation(dgy)
         ln, mean, rstd = layernorm_fwd(x, gamma, beta)
         lgrads = layernorm_bwd(x, gamma, mean, rstd, ln)
-        return (O, L, *grads, Oh, Lh, *grads_h, y, yk, gy, dgy, p, dp, db, ln, mean, rstd,
-                *lgrads)
+        return (O, L, *grads, Oh, Lh, *grads_h, y, yk, gy, dgy, ty, dty, p, dp, db, ln, mean,
+                rstd, *lgrads)
 
     _fill(inputs, 0)
     side = torch.cuda.Stream()  # default priority

@@ -1,4 +1,5 @@
-"""Linear, db, GELU, softmax, LayerNorm and naive attention on the GPU vs the CPU oracle.
+"""Linear, db, GELU (erf and tanh forms), softmax, LayerNorm and naive attention on the GPU vs
+the CPU oracle.
 
 Shapes follow the reference suite (test/test_linear.py:53-59, test_gelu.py:36-42,
 test_softmax.py:33-39, test_causal_self_attn.py:69-77) plus benchmark config 4 (GPT-2-small
@@ -110,6 +111,61 @@ def test_gelu_ragged_numel(cuda):
         x = seeded((1, 1, numel), numel, kind="randn")
         np.testing.assert_allclose(f64(gelu_activation(x.to(cuda))), ew.gelu_forward(f64(x)),
                                    atol=1e-6, rtol=1e-5)
+
+
+@pytest.mark.parametrize("batch,m,n", ROW_SHAPES[:5] + [(1, 8192, 3072)])
+def test_gelu_tanh(cuda, batch, m, n):
+    """The tanh-approximated GELU (config 4's GELU) against the float64 oracle, and the
+    autograd class against the two ops."""
+    from cuda_autograd_fns import CudaGeluTanhLayer
+    from cuda_transformer.ops import gelu_tanh_activation, gelu_tanh_activation_bwd
+
+    x = seeded((batch, m, n), 15, kind="rand") * 12 - 6
+    dy = seeded((batch, m, n), 16, kind="rand")
+    y = gelu_tanh_activation(x.to(cuda))
+    np.testing.assert_allclose(f64(y), ew.gelu_tanh_forward(f64(x)), atol=1e-5, rtol=1e-5)
+    dx = gelu_tanh_activation_bwd(x.to(cuda), dy.to(cuda))
+    np.testing.assert_allclose(f64(dx), ew.gelu_tanh_backward(f64(x), f64(dy)), atol=1e-5,
+                               rtol=1e-5)
+    xg = x.to(cuda).requires_grad_()
+    CudaGeluTanhLayer.apply(xg).backward(dy.to(cuda))
+    assert torch.equal(xg.grad, dx)
+
+
+def test_gelu_tanh_tails_and_ragged_numel(cuda):
+    """Large |x| (where tanh saturates and x^3 is large), signed zeros, and sizes that are not
+    a multiple of four (the scalar tail)."""
+    from cuda_transformer.ops import gelu_tanh_activation, gelu_tanh_activation_bwd
+
+    x = torch.tensor([-1e4, -100.0, -30.0, -9.0, -0.0, 0.0, 1e-30, 9.0, 30.0, 100.0, 1e4],
+                     dtype=torch.float32)
+    dy = torch.ones_like(x)
+    y, dx = gelu_tanh_activation(x.to(cuda)), gelu_tanh_activation_bwd(x.to(cuda), dy.to(cuda))
+    np.testing.assert_allclose(f64(y), ew.gelu_tanh_forward(f64(x)), atol=1e-6, rtol=1e-6)
+    np.testing.assert_allclose(f64(dx), ew.gelu_tanh_backward(f64(x), f64(dy)), atol=1e-6,
+                               rtol=1e-6)
+    for numel in (1, 3, 5, 1027):
+        x = seeded((1, 1, numel), numel, kind="randn") * 3
+        dy = seeded((1, 1, numel), numel + 1, kind="randn")
+        np.testing.assert_allclose(f64(gelu_tanh_activation(x.to(cuda))),
+                                   ew.gelu_tanh_forward(f64(x)), atol=1e-6, rtol=1e-5)
+        np.testing.assert_allclose(f64(gelu_tanh_activation_bwd(x.to(cuda), dy.to(cuda))),
+                                   ew.gelu_tanh_backward(f64(x), f64(dy)), atol=1e-6, rtol=1e-5)
+
+
+def test_gelu_tanh_through_c_abi(cuda):
+    from cuda_transformer_amd import capi
+
+    x = seeded((3, 1001), 21, kind="randn").to(cuda) * 2
+    dy = seeded((3, 1001), 22, kind="randn").to(cuda)
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    stream = torch.cuda.current_stream().cuda_stream
+    capi.call("cta_gelu_tanh_fwd", x.data_ptr(), y.data_ptr(), x.numel(), stream)
+    capi.call("cta_gelu_tanh_bwd", x.data_ptr(), dy.data_ptr(), dx.data_ptr(), x.numel(), stream)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(f64(y), ew.gelu_tanh_forward(f64(x)), atol=1e-6, rtol=1e-5)
+    np.testing.assert_allclose(f64(dx), ew.gelu_tanh_backward(f64(x), f64(dy)), atol=1e-6,
+                               rtol=1e-5)
 
 
 @pytest.mark.parametrize("batch,m,n", ROW_SHAPES + [(48, 1024, 1024)])

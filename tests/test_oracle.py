@@ -307,6 +307,33 @@ def test_gelu_matches_golden_and_closed_forms():
     np.testing.assert_allclose(ew.gelu_backward(x, np.ones_like(x)), fd, atol=1e-8)
 
 
+def test_gelu_tanh_against_torch_and_closed_forms():
+    """The tanh-GELU oracle against torch's own float64 F.gelu(approximate="tanh") and its
+    autograd, the odd-part identity y(x) - y(-x) = x, the values at 0, the distance to the
+    erf GELU, and finite differences."""
+    import torch
+    import torch.nn.functional as F
+
+    x = np.concatenate([np.linspace(-12, 12, 481), [-1e4, -30.0, -0.0, 1e-30, 30.0, 1e4]])
+    dy = np.random.default_rng(5).standard_normal(x.shape)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    yt = F.gelu(xt, approximate="tanh")
+    (dxt,) = torch.autograd.grad(yt, xt, torch.tensor(dy))
+    np.testing.assert_allclose(ew.gelu_tanh_forward(x), yt.detach().numpy(), rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(ew.gelu_tanh_backward(x, dy), dxt.numpy(), rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(ew.gelu_tanh_forward(x) - ew.gelu_tanh_forward(-x), x, rtol=1e-14,
+                               atol=1e-14)
+    assert ew.gelu_tanh_forward(0.0) == 0.0
+    assert ew.gelu_tanh_backward(0.0, 1.0) == 0.5
+    # the approximation stays within 5e-4 of the erf GELU (its published accuracy), but is not it
+    d = np.abs(ew.gelu_tanh_forward(x) - ew.gelu_forward(x))
+    assert d.max() < 5e-4 and d.max() > 1e-5
+    xs = np.linspace(-6, 6, 49)
+    h = 1e-6
+    fd = (ew.gelu_tanh_forward(xs + h) - ew.gelu_tanh_forward(xs - h)) / (2 * h)
+    np.testing.assert_allclose(ew.gelu_tanh_backward(xs, np.ones_like(xs)), fd, atol=1e-8)
+
+
 # ------------------------------------------------------------------ softmax
 @pytest.mark.parametrize("name", ["softmax_2x9x70", "softmax_1x4x1024"])
 def test_softmax_matches_golden(name):
