@@ -15,11 +15,13 @@ Pinning (tests/test_oracle.py, all CPU):
     linear.mlp_forward / mlp_backward (fc1 -> GELU -> fc2) against torch float64 autograd and a
     finite difference through both layers.
   * gelu — erf closed form at known points, finite differences for the gradient.
+  * gelu_tanh — torch's float64 F.gelu(approximate="tanh") + autograd, the identity
+    y(x) - y(-x) = x, its distance to the erf GELU, finite differences.
   * softmax — row sums, shift invariance, torch autograd, finite differences.
   * layernorm — torch.nn.functional.layer_norm + autograd, normalisation invariants.
   * naive attention — torch math of test/test_causal_self_attn.py:10-30 + autograd.
 Mutation tests plant plausible mistakes (wrong scale, dropped mask, transposed operand, missing
-delta term) in copies of the oracle and check that these checks catch them.
+delta term, a dropped or mis-differentiated tanh-GELU term) in copies of the oracle and check that these checks catch them.
 """
 from . import attention, elementwise, linear  # noqa: F401
 

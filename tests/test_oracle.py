@@ -4,7 +4,8 @@ Every oracle function is checked against (a) the committed golden fixtures, whic
 reference's own test oracle (torch CPU math + autograd, float64), (b) closed forms and
 invariants fixed by the mathematics, and (c) central finite differences for gradients.
 Mutation tests plant plausible mistakes in copies of the oracle (wrong scale, dropped causal
-mask, transposed operand, missing delta term, L in log2) and require that these checks fail.
+mask, transposed operand, missing delta term, L in log2, a dropped or mis-differentiated
+tanh-GELU term) and require that these checks fail.
 """
 from pathlib import Path
 
@@ -307,10 +308,10 @@ def test_gelu_matches_golden_and_closed_forms():
     np.testing.assert_allclose(ew.gelu_backward(x, np.ones_like(x)), fd, atol=1e-8)
 
 
-def test_gelu_tanh_against_torch_and_closed_forms():
-    """The tanh-GELU oracle against torch's own float64 F.gelu(approximate="tanh") and its
-    autograd, the odd-part identity y(x) - y(-x) = x, the values at 0, the distance to the
-    erf GELU, and finite differences."""
+def gelu_tanh_checks(fwd, bwd):
+    """The tanh-GELU checks as a list of booleans: torch's own float64
+    F.gelu(approximate="tanh") and its autograd, the odd-part identity y(x) - y(-x) = x, the
+    values at 0, the distance to the erf GELU and finite differences."""
     import torch
     import torch.nn.functional as F
 
@@ -319,19 +320,48 @@ def test_gelu_tanh_against_torch_and_closed_forms():
     xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
     yt = F.gelu(xt, approximate="tanh")
     (dxt,) = torch.autograd.grad(yt, xt, torch.tensor(dy))
-    np.testing.assert_allclose(ew.gelu_tanh_forward(x), yt.detach().numpy(), rtol=1e-13, atol=1e-15)
-    np.testing.assert_allclose(ew.gelu_tanh_backward(x, dy), dxt.numpy(), rtol=1e-12, atol=1e-14)
-    np.testing.assert_allclose(ew.gelu_tanh_forward(x) - ew.gelu_tanh_forward(-x), x, rtol=1e-14,
-                               atol=1e-14)
-    assert ew.gelu_tanh_forward(0.0) == 0.0
-    assert ew.gelu_tanh_backward(0.0, 1.0) == 0.5
-    # the approximation stays within 5e-4 of the erf GELU (its published accuracy), but is not it
-    d = np.abs(ew.gelu_tanh_forward(x) - ew.gelu_forward(x))
-    assert d.max() < 5e-4 and d.max() > 1e-5
+    d = np.abs(fwd(x) - ew.gelu_forward(x))
     xs = np.linspace(-6, 6, 49)
     h = 1e-6
-    fd = (ew.gelu_tanh_forward(xs + h) - ew.gelu_tanh_forward(xs - h)) / (2 * h)
-    np.testing.assert_allclose(ew.gelu_tanh_backward(xs, np.ones_like(xs)), fd, atol=1e-8)
+    fd = (fwd(xs + h) - fwd(xs - h)) / (2 * h)
+    return [
+        np.allclose(fwd(x), yt.detach().numpy(), rtol=1e-13, atol=1e-15),
+        np.allclose(bwd(x, dy), dxt.numpy(), rtol=1e-12, atol=1e-14),
+        np.allclose(fwd(x) - fwd(-x), x, rtol=1e-14, atol=1e-14),
+        fwd(0.0) == 0.0 and bwd(0.0, 1.0) == 0.5,
+        # the approximation stays within 5e-4 of the erf GELU (its published accuracy)
+        1e-5 < d.max() < 5e-4,
+        np.allclose(bwd(xs, np.ones_like(xs)), fd, rtol=0, atol=1e-8),
+    ]
+
+
+def test_gelu_tanh_against_torch_and_closed_forms():
+    assert all(gelu_tanh_checks(ew.gelu_tanh_forward, ew.gelu_tanh_backward))
+
+
+def _tanh_gelu(c, k):
+    return lambda x: 0.5 * np.asarray(x) * (1.0 + np.tanh(c * (np.asarray(x) + k * np.asarray(x) ** 3)))
+
+
+def _tanh_gelu_grad(c, k, three=3.0):
+    def g(x, dy):
+        x = np.asarray(x, dtype=np.float64)
+        t = np.tanh(c * (x + k * x**3))
+        return dy * (0.5 * (1 + t) + 0.5 * x * (1 - t * t) * c * (1 + three * k * x * x))
+    return g
+
+
+_C, _K = np.sqrt(2 / np.pi), 0.044715
+
+
+@pytest.mark.parametrize("fwd,bwd", [
+    (_tanh_gelu(_C, 0.0), _tanh_gelu_grad(_C, 0.0)),                    # cubic term dropped
+    (_tanh_gelu(np.sqrt(np.pi / 2), _K), _tanh_gelu_grad(np.sqrt(np.pi / 2), _K)),  # c inverted
+    (_tanh_gelu(_C, _K), _tanh_gelu_grad(_C, _K, three=1.0)),           # d/dx x^3 taken as x^2
+    (_tanh_gelu(_C, _K), lambda x, dy: dy * 0.5 * (1 + np.tanh(_C * (x + _K * x**3)))),  # product rule half
+])
+def test_gelu_tanh_checks_catch_mutants(fwd, bwd):
+    assert not all(gelu_tanh_checks(fwd, bwd))
 
 
 # ------------------------------------------------------------------ softmax
