@@ -54,6 +54,8 @@ def test_meta_shapes():
     assert ops.db_calculation(torch.empty(3, 10, 8, **m)).shape == (8,)
     assert ops.gelu_activation(x).shape == x.shape
     assert ops.gelu_activation_bwd(x, x).shape == x.shape
+    assert ops.gelu_tanh_activation(x).shape == x.shape
+    assert ops.gelu_tanh_activation_bwd(x, x).shape == x.shape
     assert ops.cuda_softmax(x).shape == x.shape
     out, probs = ops.causal_self_attention_fwd(torch.empty(2, 7, 96, **m), 4, True)
     assert out.shape == (2, 7, 32) and probs.shape == (2, 4, 7, 7)
@@ -75,3 +77,5 @@ def test_no_cpu_fallback():
         ops.flash_attention_fwd(q, q, q, True)
     with pytest.raises(NotImplementedError):
         ops.cuda_fma(torch.randn(1, 2, 3), torch.randn(3, 4), torch.randn(4))
+    with pytest.raises(NotImplementedError):
+        ops.gelu_tanh_activation(torch.randn(2, 3, 4))
