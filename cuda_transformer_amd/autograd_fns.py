@@ -19,7 +19,7 @@ import torch
 
 from .ops import (
     causal_self_attention_bwd, causal_self_attention_fwd, cuda_fma, cuda_fma_gelu,
-    cuda_fma_gelu_grad, cuda_softmax, cuda_softmax_bwd, db_calculation, flash_attention_bwd, flash_attention_fwd, gelu_activation,
+    cuda_fma_gelu_grad, cuda_fma_gelu_tanh, cuda_fma_gelu_tanh_grad, cuda_softmax, cuda_softmax_bwd, db_calculation, flash_attention_bwd, flash_attention_fwd, gelu_activation,
     gelu_activation_bwd, gelu_tanh_activation, gelu_tanh_activation_bwd, layernorm_bwd, layernorm_fwd,
 )
 
@@ -119,14 +119,18 @@ class CudaMLP(torch.autograd.Function):
     forward's fc1 GEMM writes the pre-activation and its GELU together (``cuda_fma_gelu``), and
     the backward's fc2 dx GEMM applies the GELU derivative before its store
     (``cuda_fma_gelu_grad``), so neither GELU pass re-reads the hidden tensor.
+
+    An optional sixth argument ``tanh=True`` selects the tanh-approximated GELU (the GPT-2
+    form; ``CudaGeluTanhLayer`` in the composition above).
     """
 
     @staticmethod
-    def forward(ctx, x, w1, b1, w2, b2):
+    def forward(ctx, x, w1, b1, w2, b2, tanh=False):
         torch._check(w1.dim() == 2 and w2.dim() == 2, lambda: "CudaMLP takes 2-D weights")
-        pre, h = cuda_fma_gelu(x, w1, b1)
+        pre, h = (cuda_fma_gelu_tanh if tanh else cuda_fma_gelu)(x, w1, b1)
         out = cuda_fma(h, w2, b2)
         ctx.save_for_backward(x, w1, w2, pre, h)
+        ctx.tanh = bool(tanh)
         return out
 
     @staticmethod
@@ -134,11 +138,12 @@ class CudaMLP(torch.autograd.Function):
         x, w1, w2, pre, h = ctx.saved_tensors
         dz = grad_output
         dw2, db2 = _weight_and_bias_grads(h, w2, dz)
-        dpre = cuda_fma_gelu_grad(dz, w2.unsqueeze(0).transpose(1, 2), pre)
+        dpre = (cuda_fma_gelu_tanh_grad if ctx.tanh else cuda_fma_gelu_grad)(
+            dz, w2.unsqueeze(0).transpose(1, 2), pre)
         dw1, db1 = _weight_and_bias_grads(x, w1, dpre)
         dx = cuda_fma(dpre, w1.unsqueeze(0).transpose(1, 2),
                       torch.zeros(x.shape[-1], dtype=dz.dtype, device=dz.device))
-        return dx, dw1, db1, dw2, db2
+        return dx, dw1, db1, dw2, db2, None
 
 
 class CudaSoftmaxLayer(torch.autograd.Function):

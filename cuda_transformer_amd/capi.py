@@ -61,6 +61,10 @@ SIGNATURES = {
                                  _p, _p, _p, _p]),
     "cta_cuda_fma_gelu_grad": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64, _i64,
                                       _p, _p, _p]),
+    "cta_cuda_fma_gelu_tanh": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64, _i64,
+                                      _i64, _p, _p, _p, _p]),
+    "cta_cuda_fma_gelu_tanh_grad": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64,
+                                           _i64, _p, _p, _p]),
     "cta_db_calculation_workspace": (_i64, [_i64, _i64, _i64]),
     "cta_db_calculation": (_int, [_p, _i64p, _i64, _i64, _i64, _p, _p, _p]),
     "cta_gelu_fwd": (_int, [_p, _p, _i64, _p]),

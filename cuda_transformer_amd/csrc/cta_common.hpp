@@ -224,6 +224,34 @@ __device__ __forceinline__ float gelu_grad(float x, float g) {
   return g * fmaf(x, pdf, normal_cdf(x));
 }
 
+// tanh-approximated GELU, torch's F.gelu(x, approximate="tanh") (the GPT-2 form; the reference
+// has no kernel for it): y = x (1 + tanh u) / 2 with u = sqrt(2/pi) (x + 0.044715 x^3).
+// With a = e^{-2|u|} in (0, 1] and r = 1 / (1 + a), (1 + tanh u) / 2 is r for u >= 0 and a r
+// for u < 0 (u has the sign of x), and (1 - tanh^2 u) / 4 = a r^2.  Neither form overflows or
+// cancels, for any x:  y = x s  and  dy/dx = s + 2 x u' a r^2,  u' = sqrt(2/pi)(1 + 3 0.044715 x^2).
+constexpr float kSqrt2OverPi = 0.7978845608028654f;
+constexpr float kGeluCubic = 0.044715f;
+__device__ __forceinline__ void gelu_tanh_parts(float x, float& s, float& ar2) {
+  // v = 2 u log2(e), so a = 2^{-|v|}
+  const float v = x * fmaf(2.0f * kLog2e * kSqrt2OverPi * kGeluCubic, x * x,
+                           2.0f * kLog2e * kSqrt2OverPi);
+  const float a = __builtin_amdgcn_exp2f(-fabsf(v));
+  const float r = __builtin_amdgcn_rcpf(1.0f + a);
+  s = x < 0.0f ? a * r : r;
+  ar2 = a * r * r;
+}
+__device__ __forceinline__ float gelu_tanh_f(float x) {
+  float s, ar2;
+  gelu_tanh_parts(x, s, ar2);
+  return x * s;
+}
+__device__ __forceinline__ float gelu_tanh_grad(float x, float g) {
+  float s, ar2;
+  gelu_tanh_parts(x, s, ar2);
+  const float du = kSqrt2OverPi * fmaf(3.0f * kGeluCubic, x * x, 1.0f);
+  return g * fmaf(2.0f * x * du, ar2, s);
+}
+
 // ----------------------------------------------------------------------------------
 // Host-side helpers shared by the C-ABI entry points.
 void set_error(const std::string& msg);

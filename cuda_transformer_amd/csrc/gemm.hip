@@ -2,8 +2,9 @@
 //
 //   out[z][m][n] = alpha * sum_k A[z][m][k] * B[z][k][n]  (+ bias[n])  (causal: -inf for n > m)
 //
-// optionally followed by a GELU stage in the epilogue (the GPT MLP's fc1 -> GELU forward and
-// fc2 -> GELU backward products, each one pass over the output instead of two).
+// optionally followed by a GELU stage (erf or tanh form) in the epilogue (the GPT MLP's
+// fc1 -> GELU forward and fc2 -> GELU backward products, each one pass over the output instead
+// of two).
 //
 // This one kernel backs the reference's fused_multiply_add (Transformer_kernels/
 // fused_multiply_add.cuh:10-92, launched from Transformer_launchers/linear_layer.cu:28-70),
@@ -180,8 +181,10 @@ __device__ __forceinline__ void tile_store(const f32x16 (&acc)[TL::MB][TL::NB], 
           if (ep.causal_mask && n > m) val = -INFINITY;
           const int64_t off = (int64_t)m * C.s_row + n;
           if (ACT == kActGeluGrad) val = gelu_grad(Xb[off], val);
+          if (ACT == kActGeluTanhGrad) val = gelu_tanh_grad(Xb[off], val);
           Cb[off] = val;
           if (ACT == kActGelu) Xb[off] = gelu_f(val);
+          if (ACT == kActGeluTanh) Xb[off] = gelu_tanh_f(val);
         }
       }
     }
@@ -301,8 +304,10 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float* __restric
     if (ep.causal_mask && n > m) val = -INFINITY;
     const int64_t off = zo * C.s_outer + zi * C.s_inner + (int64_t)m * C.s_row + n;
     if (ep.act == kActGeluGrad) val = gelu_grad(ep.aux[off], val);
+    if (ep.act == kActGeluTanhGrad) val = gelu_tanh_grad(ep.aux[off], val);
     C.p[off] = val;
     if (ep.act == kActGelu) ep.aux[off] = gelu_f(val);
+    if (ep.act == kActGeluTanh) ep.aux[off] = gelu_tanh_f(val);
   }
 }
 
@@ -400,6 +405,11 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
     dispatch_a<TL, kActGelu>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
   else if (act == kActGeluGrad)
     dispatch_a<TL, kActGeluGrad>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
+  else if (act == kActGeluTanh)
+    dispatch_a<TL, kActGeluTanh>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
+  else if (act == kActGeluTanhGrad)
+    dispatch_a<TL, kActGeluTanhGrad>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc,
+                                     ws);
   else
     dispatch_a<TL, kActNone>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
   if (S > 1) {
@@ -480,30 +490,65 @@ extern "C" int cta_cuda_fma(const float* x, const int64_t* x_strides, const floa
                        stream);
 }
 
+namespace {
+int fma_act(const float* x, const int64_t* x_strides, const float* w, const int64_t* w_strides,
+            const float* bias, int64_t bias_stride, int64_t batch, int64_t m, int64_t k,
+            int64_t n, int64_t w_batch, float* pre, float* out, float* workspace, void* stream,
+            int act) {
+  if (batch > 0 && m > 0 && n > 0) {
+    if (!bias || !out) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+    if (pre == out) return fail(CTA_ERR_INVALID_ARGUMENT, "pre and out must be distinct buffers");
+  }
+  const GemmEpilogue ep{1.0f, bias, bias_stride, 0, act, out};
+  return linear_launch(x, x_strides, w, w_strides, batch, m, k, n, w_batch, pre, ep, workspace,
+                       stream);
+}
+
+int fma_act_grad(const float* dy, const int64_t* dy_strides, const float* w,
+                 const int64_t* w_strides, const float* pre, int64_t batch, int64_t m, int64_t k,
+                 int64_t n, int64_t w_batch, float* dx, float* workspace, void* stream, int act) {
+  if (!pre && batch > 0 && m > 0 && n > 0) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  // Each output element reads its own pre-activation just before it is stored, so dx may
+  // alias pre.
+  const GemmEpilogue ep{1.0f, nullptr, 0, 0, act, const_cast<float*>(pre)};
+  return linear_launch(dy, dy_strides, w, w_strides, batch, m, k, n, w_batch, dx, ep, workspace,
+                       stream);
+}
+}  // namespace
+
 extern "C" int cta_cuda_fma_gelu(const float* x, const int64_t* x_strides, const float* w,
                                  const int64_t* w_strides, const float* bias,
                                  int64_t bias_stride, int64_t batch, int64_t m, int64_t k,
                                  int64_t n, int64_t w_batch, float* pre, float* out,
                                  float* workspace, void* stream) {
-  if (batch > 0 && m > 0 && n > 0) {
-    if (!bias || !out) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
-    if (pre == out) return fail(CTA_ERR_INVALID_ARGUMENT, "pre and out must be distinct buffers");
-  }
-  const GemmEpilogue ep{1.0f, bias, bias_stride, 0, kActGelu, out};
-  return linear_launch(x, x_strides, w, w_strides, batch, m, k, n, w_batch, pre, ep, workspace,
-                       stream);
+  return fma_act(x, x_strides, w, w_strides, bias, bias_stride, batch, m, k, n, w_batch, pre, out,
+                 workspace, stream, kActGelu);
 }
 
 extern "C" int cta_cuda_fma_gelu_grad(const float* dy, const int64_t* dy_strides, const float* w,
                                       const int64_t* w_strides, const float* pre, int64_t batch,
                                       int64_t m, int64_t k, int64_t n, int64_t w_batch,
                                       float* dx, float* workspace, void* stream) {
-  if (!pre && batch > 0 && m > 0 && n > 0) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
-  // Each output element reads its own pre-activation just before it is stored, so dx may
-  // alias pre.
-  const GemmEpilogue ep{1.0f, nullptr, 0, 0, kActGeluGrad, const_cast<float*>(pre)};
-  return linear_launch(dy, dy_strides, w, w_strides, batch, m, k, n, w_batch, dx, ep, workspace,
-                       stream);
+  return fma_act_grad(dy, dy_strides, w, w_strides, pre, batch, m, k, n, w_batch, dx, workspace,
+                      stream, kActGeluGrad);
+}
+
+extern "C" int cta_cuda_fma_gelu_tanh(const float* x, const int64_t* x_strides, const float* w,
+                                      const int64_t* w_strides, const float* bias,
+                                      int64_t bias_stride, int64_t batch, int64_t m, int64_t k,
+                                      int64_t n, int64_t w_batch, float* pre, float* out,
+                                      float* workspace, void* stream) {
+  return fma_act(x, x_strides, w, w_strides, bias, bias_stride, batch, m, k, n, w_batch, pre, out,
+                 workspace, stream, kActGeluTanh);
+}
+
+extern "C" int cta_cuda_fma_gelu_tanh_grad(const float* dy, const int64_t* dy_strides,
+                                           const float* w, const int64_t* w_strides,
+                                           const float* pre, int64_t batch, int64_t m, int64_t k,
+                                           int64_t n, int64_t w_batch, float* dx,
+                                           float* workspace, void* stream) {
+  return fma_act_grad(dy, dy_strides, w, w_strides, pre, batch, m, k, n, w_batch, dx, workspace,
+                      stream, kActGeluTanhGrad);
 }
 
 extern "C" int64_t cta_db_calculation_workspace(int64_t batch, int64_t m, int64_t n) {

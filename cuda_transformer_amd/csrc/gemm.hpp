@@ -22,6 +22,8 @@ enum GemmAct {
   kActNone = 0,
   kActGelu = 1,      // C = v (the pre-activation) and aux = gelu(v)
   kActGeluGrad = 2,  // C = v * gelu'(aux): aux holds the pre-activation
+  kActGeluTanh = 3,      // as kActGelu with the tanh-approximated GELU
+  kActGeluTanhGrad = 4,  // as kActGeluGrad with the tanh-approximated GELU
 };
 
 struct GemmEpilogue {
@@ -30,7 +32,7 @@ struct GemmEpilogue {
   int64_t bias_stride;
   int causal_mask;    // set entries with n > m to -inf
   int act = kActNone;
-  float* aux = nullptr;  // same (batch, m, n) layout as the output; read-only for kActGeluGrad
+  float* aux = nullptr;  // same (batch, m, n) layout as the output; read-only for the *Grad acts
 };
 
 // out[z] = alpha * A[z] B[z] (+ bias) for z in [0, Z); batch index split as (z / zin, z % zin).

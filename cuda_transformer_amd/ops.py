@@ -12,13 +12,15 @@ shape functions for FakeTensor / ``torch.compile`` tracing.  Two deviations, bot
 Added: ``layernorm_fwd`` / ``layernorm_bwd`` (the reference's LayerNorm is plain torch,
 gpt/gpt.py:47-59), and ``cuda_fma_gelu`` / ``cuda_fma_gelu_grad``, the GPT MLP's linear+GELU
 pairs (gpt/gpt.py:134-135 and their backward) fused into one GEMM each, and
-``gelu_tanh_activation`` / ``gelu_tanh_activation_bwd``, the tanh-approximated GELU.
+``gelu_tanh_activation`` / ``gelu_tanh_activation_bwd``, the tanh-approximated GELU (with its
+fused linear pair ``cuda_fma_gelu_tanh`` / ``cuda_fma_gelu_tanh_grad``).
 """
 import torch
 from torch import Tensor
 
 __all__ = [
-    "cuda_fma", "db_calculation", "cuda_fma_gelu", "cuda_fma_gelu_grad",
+    "cuda_fma", "db_calculation", "cuda_fma_gelu", "cuda_fma_gelu_grad", "cuda_fma_gelu_tanh",
+    "cuda_fma_gelu_tanh_grad",
     "cuda_softmax", "cuda_softmax_bwd",
     "gelu_activation", "gelu_activation_bwd", "gelu_tanh_activation", "gelu_tanh_activation_bwd",
     "causal_self_attention_fwd", "causal_self_attention_bwd",
@@ -77,6 +79,35 @@ def cuda_fma_gelu_grad(dy: Tensor, weights: Tensor, pre: Tensor) -> Tensor:
 
 
 @torch.library.register_fake("cuda_transformer::cuda_fma_gelu_grad")
+def _(dy, weights, pre):
+    _f32(dy, weights, pre)
+    _same_device(dy, weights, pre)
+    return torch.empty(pre.shape, dtype=dy.dtype, device=dy.device)
+
+
+def cuda_fma_gelu_tanh(x: Tensor, weights: Tensor, bias: Tensor) -> tuple[Tensor, Tensor]:
+    """As ``cuda_fma_gelu`` with the tanh-approximated GELU: bitwise equal to ``cuda_fma``
+    followed by ``gelu_tanh_activation``."""
+    return _ops.cuda_fma_gelu_tanh.default(x, weights, bias)
+
+
+@torch.library.register_fake("cuda_transformer::cuda_fma_gelu_tanh")
+def _(x, weights, bias):
+    _f32(x, weights, bias)
+    _same_device(x, weights, bias)
+    w = weights if weights.dim() == 3 else weights.unsqueeze(0)
+    shape = (x.size(0), x.size(1), w.size(2))
+    return (torch.empty(shape, dtype=x.dtype, device=x.device),
+            torch.empty(shape, dtype=x.dtype, device=x.device))
+
+
+def cuda_fma_gelu_tanh_grad(dy: Tensor, weights: Tensor, pre: Tensor) -> Tensor:
+    """As ``cuda_fma_gelu_grad`` with the tanh-approximated GELU: bitwise equal to ``cuda_fma``
+    with a zero bias followed by ``gelu_tanh_activation_bwd(pre, .)``."""
+    return _ops.cuda_fma_gelu_tanh_grad.default(dy, weights, pre)
+
+
+@torch.library.register_fake("cuda_transformer::cuda_fma_gelu_tanh_grad")
 def _(dy, weights, pre):
     _f32(dy, weights, pre)
     _same_device(dy, weights, pre)

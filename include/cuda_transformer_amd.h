@@ -61,7 +61,7 @@ int cta_flash_attention_fwd(const float* q, const int64_t* q_strides,
 
 /* Forward with BF16 Q, K, V (stored as uint16_t bit patterns) and FP32 accumulation: O dense
  * (B,nh,T,hs) in BF16, L dense (B,nh,T) in FP32, L = rowmax + ln(rowsum) as above.  hs in
- * {64, 128}.  Q/K/V strides: unit d-stride, other strides divisible by 8, 16-byte aligned
+ * {32, 64, 128}.  Q/K/V strides: unit d-stride, other strides divisible by 8, 16-byte aligned
  * base pointers (CTA_ERR_LAYOUT otherwise).  The probabilities are rounded to BF16 as the
  * P.V operand.  No counterpart in the reference's launchers: its roadmap lists reduced
  * precision (README.md:277); the semantics are those of flash_attention_fwd
@@ -105,7 +105,7 @@ int cta_flash_attention_bwd(const float* q, const int64_t* q_strides,
                             float* workspace, int64_t workspace_bytes, void* stream);
 
 /* Bytes of BF16 dS workspace for cta_flash_attention_bwd_bf16: B*nh*ceil(T/32)^2*2 KiB, or
- * about half of that when causal.  0 for empty or unsupported shapes (hs not in {64, 128}). */
+ * about half of that when causal.  0 for empty or unsupported shapes (hs not in {32, 64, 128}). */
 int64_t cta_flash_attention_bwd_bf16_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs,
                                                int causal);
 
@@ -113,7 +113,7 @@ int64_t cta_flash_attention_bwd_bf16_workspace(int64_t B, int64_t nh, int64_t T,
  * scratch of B*nh*T floats), then dK/dV storing BF16 dS tiles and dQ from them, chunked over
  * heads to fit workspace_bytes (at least one head's share of
  * cta_flash_attention_bwd_bf16_workspace(), else CTA_ERR_INVALID_ARGUMENT).  dq/dk/dv dense
- * (B,nh,T,hs) BF16.  hs in {64, 128}; strides as for cta_flash_attention_fwd_bf16.  P and dS
+ * (B,nh,T,hs) BF16.  hs in {32, 64, 128}; strides as for cta_flash_attention_fwd_bf16.  P and dS
  * are rounded to BF16 as MFMA operands; accumulation is FP32; deterministic.  No counterpart
  * in the reference's launchers (reduced precision is on its roadmap, README.md:277); the
  * semantics are those of flash_attention_bwd (flash_attn_launcher.cu:67-142). */
@@ -231,6 +231,22 @@ int cta_cuda_fma_gelu_grad(const float* dy, const int64_t* dy_strides,
                            const float* w, const int64_t* w_strides, const float* pre,
                            int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
                            float* dx, float* workspace, void* stream);
+
+/* As cta_cuda_fma_gelu with the tanh-approximated GELU: bitwise equal to cta_cuda_fma followed
+ * by cta_gelu_tanh_fwd.  No reference counterpart (the reference's GELU is erf-exact,
+ * GeLU.cuh:7-16); for MLPs that use the GPT-2 form. */
+int cta_cuda_fma_gelu_tanh(const float* x, const int64_t* x_strides,
+                           const float* w, const int64_t* w_strides,
+                           const float* bias, int64_t bias_stride,
+                           int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
+                           float* pre, float* out, float* workspace, void* stream);
+
+/* As cta_cuda_fma_gelu_grad with the tanh-approximated GELU: bitwise equal to cta_cuda_fma with
+ * a zero bias followed by cta_gelu_tanh_bwd.  No reference counterpart. */
+int cta_cuda_fma_gelu_tanh_grad(const float* dy, const int64_t* dy_strides,
+                                const float* w, const int64_t* w_strides, const float* pre,
+                                int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
+                                float* dx, float* workspace, void* stream);
 
 /* Bytes of scratch cta_db_calculation needs for a (batch, m, n) gradient. */
 int64_t cta_db_calculation_workspace(int64_t batch, int64_t m, int64_t n);

@@ -288,11 +288,26 @@ FUSED_SHAPES = [(1, 32, 64, 96), (2, 33, 17, 65), (3, 70, 129, 257), (2, 256, 38
                 (1, 64, 4096, 96)]
 
 
+def _gelu_forms(form):
+    """(fused fwd, fused grad, plain fwd, plain bwd, oracle fwd, oracle bwd) of one GELU form."""
+    from cuda_transformer import ops
+
+    if form == "erf":
+        return (ops.cuda_fma_gelu, ops.cuda_fma_gelu_grad, ops.gelu_activation,
+                ops.gelu_activation_bwd, ew.gelu_forward, ew.gelu_backward)
+    return (ops.cuda_fma_gelu_tanh, ops.cuda_fma_gelu_tanh_grad, ops.gelu_tanh_activation,
+            ops.gelu_tanh_activation_bwd, ew.gelu_tanh_forward, ew.gelu_tanh_backward)
+
+
+@pytest.mark.parametrize("form", ["erf", "tanh"])
 @pytest.mark.parametrize("B,T,d,hid", FUSED_SHAPES)
-def test_fused_linear_gelu(cuda, B, T, d, hid):
-    """cuda_fma_gelu and cuda_fma_gelu_grad: the same bits as the unfused ops, and the oracle."""
-    from cuda_transformer.ops import (cuda_fma, cuda_fma_gelu, cuda_fma_gelu_grad,
-                                      gelu_activation, gelu_activation_bwd)
+def test_fused_linear_gelu(cuda, B, T, d, hid, form):
+    """cuda_fma_gelu[_tanh] and cuda_fma_gelu[_tanh]_grad: the same bits as the unfused ops, and
+    the oracle."""
+    from cuda_transformer.ops import cuda_fma
+
+    cuda_fma_gelu, cuda_fma_gelu_grad, gelu_activation, gelu_activation_bwd, o_fwd, o_bwd = (
+        _gelu_forms(form))
 
     x = seeded((B, T, d), 50, kind="rand")
     w1 = seeded((d, hid), 51) * 0.2
@@ -304,12 +319,13 @@ def test_fused_linear_gelu(cuda, B, T, d, hid):
     assert torch.equal(pre, cuda_fma(xc, w1c, b1c))
     assert torch.equal(h, gelu_activation(pre))
     # FP32 sums of up to K = 4096 terms: relative error in norm, and a looser elementwise bound
-    pre_r, h_r, _ = lin.mlp_forward(f64(x), f64(w1), f64(b1), f64(w2), np.zeros(d))
+    pre_r = f64(x) @ f64(w1) + f64(b1)
+    h_r = o_fwd(pre_r)
     w2t = w2c.unsqueeze(0).transpose(1, 2)
     dpre = cuda_fma_gelu_grad(dzc, w2t, pre)
     unfused = gelu_activation_bwd(pre, cuda_fma(dzc, w2t, torch.zeros(hid, device=cuda)))
     assert torch.equal(dpre, unfused)
-    dpre_r = ew.gelu_backward(f64(pre), f64(dz) @ f64(w2).T)
+    dpre_r = o_bwd(f64(pre), f64(dz) @ f64(w2).T)
     for got, ref in ((pre, pre_r), (h, h_r), (dpre, dpre_r)):
         assert rel_err(f64(got), ref) <= 1e-6
         np.testing.assert_allclose(f64(got), ref, atol=1e-4, rtol=1e-4)
@@ -347,11 +363,39 @@ def test_fused_linear_gelu_through_c_abi(cuda):
                   pre.data_ptr(), pre.data_ptr(), None, stream)
 
 
+def test_fused_linear_gelu_tanh_through_c_abi(cuda):
+    from cuda_transformer.ops import cuda_fma_gelu_tanh, cuda_fma_gelu_tanh_grad
+    from cuda_transformer_amd import capi
+
+    B, T, d, hid = 2, 40, 48, 80
+    x = seeded((B, T, d), 75).to(cuda)
+    w1 = seeded((d, hid), 76).to(cuda) * 0.2
+    b1 = seeded((hid,), 77).to(cuda)
+    w2t = (seeded((hid, d), 78).to(cuda) * 0.2).t()
+    dz = seeded((B, T, d), 79).to(cuda)
+    stream = torch.cuda.current_stream().cuda_stream
+    pre = torch.empty(B, T, hid, device=cuda)
+    out = torch.empty_like(pre)
+    capi.call("cta_cuda_fma_gelu_tanh", x.data_ptr(), capi.strides(x.stride()), w1.data_ptr(),
+              capi.strides((0,) + w1.stride()), b1.data_ptr(), 1, B, T, d, hid, 1,
+              pre.data_ptr(), out.data_ptr(), None, stream)
+    dx = pre.clone()
+    capi.call("cta_cuda_fma_gelu_tanh_grad", dz.data_ptr(), capi.strides(dz.stride()),
+              w2t.data_ptr(), capi.strides((0,) + w2t.stride()), dx.data_ptr(), B, T, d, hid, 1,
+              dx.data_ptr(), None, stream)
+    torch.cuda.synchronize()
+    pre_t, out_t = cuda_fma_gelu_tanh(x, w1, b1)
+    assert torch.equal(pre, pre_t) and torch.equal(out, out_t)
+    assert torch.equal(dx, cuda_fma_gelu_tanh_grad(dz, w2t, pre_t))
+
+
+@pytest.mark.parametrize("tanh", [False, True])
 @pytest.mark.parametrize("B,T,d", [(2, 33, 48), (4, 256, 384)])
-def test_cuda_mlp_matches_composition(cuda, B, T, d):
+def test_cuda_mlp_matches_composition(cuda, B, T, d, tanh):
     """CudaMLP: output and all five gradients bitwise equal to CudaLinearLayer -> CudaGeluLayer
-    -> CudaLinearLayer, and within FP32 rounding of the oracle."""
-    from cuda_autograd_fns import CudaGeluLayer, CudaLinearLayer, CudaMLP
+    (CudaGeluTanhLayer with tanh=True) -> CudaLinearLayer, and within FP32 rounding of the
+    oracle."""
+    from cuda_autograd_fns import CudaGeluLayer, CudaGeluTanhLayer, CudaLinearLayer, CudaMLP
 
     hid = 4 * d
     params = [seeded(s, 60 + i) * 0.1 for i, s in enumerate([(d, hid), (hid,), (hid, d), (d,)])]
@@ -362,9 +406,10 @@ def test_cuda_mlp_matches_composition(cuda, B, T, d):
         xg = x.to(cuda).requires_grad_()
         ps = [p.to(cuda).requires_grad_() for p in params]
         if fused:
-            out = CudaMLP.apply(xg, *ps)
+            out = CudaMLP.apply(xg, *ps, tanh) if tanh else CudaMLP.apply(xg, *ps)
         else:
-            h = CudaGeluLayer.apply(CudaLinearLayer.apply(xg, ps[0], ps[1]))
+            act = CudaGeluTanhLayer if tanh else CudaGeluLayer
+            h = act.apply(CudaLinearLayer.apply(xg, ps[0], ps[1]))
             out = CudaLinearLayer.apply(h, ps[2], ps[3])
         out.backward(dz.to(cuda))
         return [out.detach(), xg.grad] + [p.grad for p in ps]
@@ -372,6 +417,8 @@ def test_cuda_mlp_matches_composition(cuda, B, T, d):
     fused, plain = run(True), run(False)
     for a, b in zip(fused, plain):
         assert torch.equal(a, b)
+    if tanh:
+        return  # the tanh composition's parts are each checked against the oracle above
     p64 = [f64(p) for p in params]
     pre, h, out = lin.mlp_forward(f64(x), *p64)
     grads = lin.mlp_backward(f64(x), p64[0], p64[2], pre, h, f64(dz))
