@@ -162,51 +162,57 @@ struct RowRegs {
   }
 };
 
+// Softmax rows: one wave per row, the whole row in registers.  The grid covers every row up
+// to 2^22 rows; beyond that each wave strides on by 4 gridDim.x rows.  (Several rows per wave
+// with the next row prefetched measured 5% slower at 48K rows of 1024: fewer waves in flight.)
+// x and y (p, dp and dx) may be the same buffer: a wave reads its row completely before it
+// writes it.
 template <int U, bool VEC>
-__global__ __launch_bounds__(256) void softmax_fwd_rows(const float* x,
-                                                        float* y, int64_t rows,
+__global__ __launch_bounds__(256) void softmax_fwd_rows(const float* x, float* y, int64_t rows,
                                                         int n) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  RowRegs<U, VEC> r;
-  r.load(x + row * n, n, lane, -INFINITY);
-  float mx = -INFINITY;
+  const int64_t step = (int64_t)gridDim.x * 4;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + wave_index(); row < rows; row += step) {
+    RowRegs<U, VEC> r;
+    r.load(x + row * n, n, lane, -INFINITY);
+    float mx = -INFINITY;
 #pragma unroll
-  for (int e = 0; e < U * r.W; ++e) mx = fmaxf(mx, r.v[e]);
-  mx = wave_max(mx);
-  float sum = 0.0f;
+    for (int e = 0; e < U * r.W; ++e) mx = fmaxf(mx, r.v[e]);
+    mx = wave_max(mx);
+    // e^{v - mx} = 2^{v log2(e) - mx log2(e)}: one fma and the hardware exp2 per element
+    const float off = mx * kLog2e;
+    float sum = 0.0f;
 #pragma unroll
-  for (int e = 0; e < U * r.W; ++e) {
-    const float p = expf(r.v[e] - mx);
-    r.v[e] = p;
-    sum += p;
+    for (int e = 0; e < U * r.W; ++e) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(r.v[e], kLog2e, -off));
+      r.v[e] = p;
+      sum += p;
+    }
+    sum = wave_sum(sum);
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int e = 0; e < U * r.W; ++e) r.v[e] *= inv;
+    r.store(y + row * n, n, lane);
   }
-  sum = wave_sum(sum);
-  const float inv = 1.0f / sum;
-#pragma unroll
-  for (int e = 0; e < U * r.W; ++e) r.v[e] *= inv;
-  r.store(y + row * n, n, lane);
 }
 
 template <int U, bool VEC>
-__global__ __launch_bounds__(256) void softmax_bwd_rows(const float* p,
-                                                        const float* dp,
-                                                        float* dx, int64_t rows,
-                                                        int n) {
+__global__ __launch_bounds__(256) void softmax_bwd_rows(const float* p, const float* dp,
+                                                        float* dx, int64_t rows, int n) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  RowRegs<U, VEC> a, g;
-  a.load(p + row * n, n, lane, 0.0f);
-  g.load(dp + row * n, n, lane, 0.0f);
-  float dot = 0.0f;
+  const int64_t step = (int64_t)gridDim.x * 4;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + wave_index(); row < rows; row += step) {
+    RowRegs<U, VEC> a, g;
+    a.load(p + row * n, n, lane, 0.0f);
+    g.load(dp + row * n, n, lane, 0.0f);
+    float dot = 0.0f;
 #pragma unroll
-  for (int e = 0; e < U * a.W; ++e) dot = fmaf(a.v[e], g.v[e], dot);
-  dot = wave_sum(dot);
+    for (int e = 0; e < U * a.W; ++e) dot = fmaf(a.v[e], g.v[e], dot);
+    dot = wave_sum(dot);
 #pragma unroll
-  for (int e = 0; e < U * a.W; ++e) a.v[e] = a.v[e] * (g.v[e] - dot);
-  a.store(dx + row * n, n, lane);
+    for (int e = 0; e < U * a.W; ++e) a.v[e] = a.v[e] * (g.v[e] - dot);
+    a.store(dx + row * n, n, lane);
+  }
 }
 
 // --------------------------------------------------------------- long-row block path
@@ -442,6 +448,12 @@ bool row_vec_ok(const void* a, const void* b, const void* c, int n) {
          (c == nullptr || aligned16(c));
 }
 
+// Workgroups (4 waves, one row each) for the softmax row kernels, at most 2^20 of them (the
+// kernels stride over the rest).
+dim3 softmax_grid(int64_t rows) {
+  return dim3((unsigned)std::min<int64_t>((rows + 3) / 4, (int64_t)1 << 20));
+}
+
 #define CTA_ROW_SWITCH(KERNEL, VEC, U, GRID, ST, ...)                                        \
   do {                                                                                      \
     if (VEC) {                                                                              \
@@ -479,8 +491,7 @@ int softmax_rows(const float* x, float* y, int64_t rows, int64_t n, hipStream_t 
   if (n <= kMaxRegCols) {
     const bool vec = row_vec_ok(x, y, nullptr, (int)n);
     const int u = units_for((int)n, vec);
-    const dim3 grid((unsigned)((rows + 3) / 4));
-    CTA_ROW_SWITCH(softmax_fwd_rows, vec, u, grid, st, x, y, rows, (int)n);
+    CTA_ROW_SWITCH(softmax_fwd_rows, vec, u, softmax_grid(rows), st, x, y, rows, (int)n);
   } else {
     hipLaunchKernelGGL(softmax_fwd_long, dim3((unsigned)rows), dim3(256), 0, st, x, y, (int)n);
   }
@@ -494,8 +505,7 @@ int softmax_bwd_rows_launch(const float* p, const float* dp, float* dx, int64_t 
   if (n <= kMaxRegCols) {
     const bool vec = row_vec_ok(p, dp, dx, (int)n);
     const int u = units_for((int)n, vec);
-    const dim3 grid((unsigned)((rows + 3) / 4));
-    CTA_ROW_SWITCH(softmax_bwd_rows, vec, u, grid, st, p, dp, dx, rows, (int)n);
+    CTA_ROW_SWITCH(softmax_bwd_rows, vec, u, softmax_grid(rows), st, p, dp, dx, rows, (int)n);
   } else {
     hipLaunchKernelGGL(softmax_bwd_long, dim3((unsigned)rows), dim3(256), 0, st, p, dp, dx, (int)n);
   }
