@@ -271,31 +271,32 @@ __global__ __launch_bounds__(256) void layernorm_fwd_rows(
     float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, int64_t rows,
     int n, float eps) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  using R = RowRegs<U, VEC>;
-  R r, gm, bt;
-  r.load(x + row * n, n, lane, 0.0f);
-  gm.load(gamma, n, lane, 0.0f);
-  bt.load(beta, n, lane, 0.0f);
-  float s = 0.0f;
+  const int64_t step = (int64_t)gridDim.x * 4;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + wave_index(); row < rows; row += step) {
+    using R = RowRegs<U, VEC>;
+    R r, gm, bt;
+    r.load(x + row * n, n, lane, 0.0f);
+    gm.load(gamma, n, lane, 0.0f);
+    bt.load(beta, n, lane, 0.0f);
+    float s = 0.0f;
 #pragma unroll
-  for (int e = 0; e < U * R::W; ++e) s += r.v[e];
-  const float mu = wave_sum(s) / (float)n;
-  float q = 0.0f;
+    for (int e = 0; e < U * R::W; ++e) s += r.v[e];
+    const float mu = wave_sum(s) / (float)n;
+    float q = 0.0f;
 #pragma unroll
-  for (int e = 0; e < U * R::W; ++e) {
-    const float d = (R::colof(e, lane) < n) ? r.v[e] - mu : 0.0f;
-    q = fmaf(d, d, q);
-  }
-  const float var = wave_sum(q) / (float)n;
-  const float rs = 1.0f / sqrtf(var + eps);
+    for (int e = 0; e < U * R::W; ++e) {
+      const float d = (R::colof(e, lane) < n) ? r.v[e] - mu : 0.0f;
+      q = fmaf(d, d, q);
+    }
+    const float var = wave_sum(q) / (float)n;
+    const float rs = 1.0f / sqrtf(var + eps);
 #pragma unroll
-  for (int e = 0; e < U * R::W; ++e) r.v[e] = fmaf((r.v[e] - mu) * rs, gm.v[e], bt.v[e]);
-  r.store(y + row * n, n, lane);
-  if (lane == 0) {
-    mean[row] = mu;
-    rstd[row] = rs;
+    for (int e = 0; e < U * R::W; ++e) r.v[e] = fmaf((r.v[e] - mu) * rs, gm.v[e], bt.v[e]);
+    r.store(y + row * n, n, lane);
+    if (lane == 0) {
+      mean[row] = mu;
+      rstd[row] = rs;
+    }
   }
 }
 
@@ -448,9 +449,9 @@ bool row_vec_ok(const void* a, const void* b, const void* c, int n) {
          (c == nullptr || aligned16(c));
 }
 
-// Workgroups (4 waves, one row each) for the softmax row kernels, at most 2^20 of them (the
-// kernels stride over the rest).
-dim3 softmax_grid(int64_t rows) {
+// Workgroups (4 waves, one row each) for the softmax and LayerNorm-forward row kernels, at most
+// 2^20 of them (the kernels stride over the rest).
+dim3 row_grid(int64_t rows) {
   return dim3((unsigned)std::min<int64_t>((rows + 3) / 4, (int64_t)1 << 20));
 }
 
@@ -491,7 +492,7 @@ int softmax_rows(const float* x, float* y, int64_t rows, int64_t n, hipStream_t 
   if (n <= kMaxRegCols) {
     const bool vec = row_vec_ok(x, y, nullptr, (int)n);
     const int u = units_for((int)n, vec);
-    CTA_ROW_SWITCH(softmax_fwd_rows, vec, u, softmax_grid(rows), st, x, y, rows, (int)n);
+    CTA_ROW_SWITCH(softmax_fwd_rows, vec, u, row_grid(rows), st, x, y, rows, (int)n);
   } else {
     hipLaunchKernelGGL(softmax_fwd_long, dim3((unsigned)rows), dim3(256), 0, st, x, y, (int)n);
   }
@@ -505,7 +506,7 @@ int softmax_bwd_rows_launch(const float* p, const float* dp, float* dx, int64_t 
   if (n <= kMaxRegCols) {
     const bool vec = row_vec_ok(p, dp, dx, (int)n);
     const int u = units_for((int)n, vec);
-    CTA_ROW_SWITCH(softmax_bwd_rows, vec, u, softmax_grid(rows), st, p, dp, dx, rows, (int)n);
+    CTA_ROW_SWITCH(softmax_bwd_rows, vec, u, row_grid(rows), st, p, dp, dx, rows, (int)n);
   } else {
     hipLaunchKernelGGL(softmax_bwd_long, dim3((unsigned)rows), dim3(256), 0, st, p, dp, dx, (int)n);
   }
@@ -604,8 +605,7 @@ extern "C" int cta_layernorm_fwd(const float* x, const float* gamma, const float
   if (n <= kMaxRegCols) {
     const bool vec = row_vec_ok(x, y, gamma, (int)n) && aligned16(beta);
     const int u = units_for((int)n, vec);
-    const dim3 grid((unsigned)((rows + 3) / 4));
-    CTA_ROW_SWITCH(layernorm_fwd_rows, vec, u, grid, st, x, gamma, beta, y, mean, rstd, rows,
+    CTA_ROW_SWITCH(layernorm_fwd_rows, vec, u, row_grid(rows), st, x, gamma, beta, y, mean, rstd, rows,
                    (int)n, eps);
   } else {
     hipLaunchKernelGGL(layernorm_fwd_long, dim3((unsigned)rows), dim3(256), 0, st, x, gamma, beta,

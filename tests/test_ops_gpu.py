@@ -187,6 +187,36 @@ def test_softmax(cuda, batch, m, n):
     assert torch.equal(xg.grad, dx)
 
 
+def test_row_kernels_stride_past_the_grid_cap(cuda):
+    """2^22 + 5 rows: more than the 2^20 four-row workgroups the softmax and LayerNorm-forward
+    row kernels launch, so the last 5 rows come from a wave's second pass.  Rows at both ends
+    and across the cap are checked against the oracle."""
+    from cuda_transformer.ops import cuda_softmax, cuda_softmax_bwd, layernorm_fwd
+
+    rows, n = (1 << 22) + 5, 4
+    g = torch.Generator(device=cuda).manual_seed(7)
+    x = torch.randn(1, rows, n, generator=g, device=cuda) * 2
+    dp = torch.randn(1, rows, n, generator=g, device=cuda)
+    gamma = torch.linspace(0.5, 1.5, n, device=cuda)
+    beta = torch.linspace(-0.1, 0.1, n, device=cuda)
+    p = cuda_softmax(x)
+    dx = cuda_softmax_bwd(p, dp)
+    y, mean, rstd = layernorm_fwd(x[0], gamma, beta, 1e-5)
+    idx = torch.tensor([0, 1, (1 << 22) - 1, 1 << 22, rows - 3, rows - 1], device=cuda)
+    xs, dps = f64(x[0, idx]), f64(dp[0, idx])
+    ps = ew.softmax_forward(xs)
+    np.testing.assert_allclose(f64(p[0, idx]), ps, atol=1e-6, rtol=1e-5)
+    np.testing.assert_allclose(f64(dx[0, idx]), ew.softmax_backward(f64(p[0, idx]), dps),
+                               atol=1e-6, rtol=1e-5)
+    y_r, mean_r, rstd_r = ew.layernorm_forward(xs, f64(gamma), f64(beta), 1e-5)
+    np.testing.assert_allclose(f64(y[idx]), y_r, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(f64(mean[idx]), mean_r.reshape(-1), atol=1e-6, rtol=1e-5)
+    np.testing.assert_allclose(f64(rstd[idx]), rstd_r.reshape(-1), atol=1e-6, rtol=1e-4)
+    # every row was written: each softmax row sums to one, every output is finite
+    assert torch.allclose(p.sum(-1), torch.ones(1, rows, device=cuda), atol=1e-5)
+    assert bool(torch.isfinite(y).all()) and bool(torch.isfinite(dx).all())
+
+
 @pytest.mark.parametrize("rows,n", [(64, 32), (65, 32), (70, 120), (8192, 768), (33, 384),
                                     (5, 2048), (3, 3000), (7, 65)])
 def test_layernorm(cuda, rows, n):
