@@ -13,16 +13,20 @@ Reported:
                  fwd 4*B*H*N^2*D, halved for causal; bwd 2.5x fwd; divided by the wall time of
                  exactly --steps steps bracketed by device synchronisation.
   per_kernel_ms  HIP-event durations of each kernel on its launch stream, averaged over the
-                 timed steps.
-  roofline       the dominant kernel's algorithmic FLOPs per launch / its mean duration, vs the
-                 157.3 TFLOP/s dense FP32 MFMA peak; traffic (HBM bytes per launch) from the
+                 timed steps; per_kernel_ms_flushed: the median of each kernel launched alone
+                 after 1 GiB of device memory was written (cold L2 and MALL), after the timed
+                 steps.
+  roofline       the dominant kernel's algorithmic FLOPs per launch / its mean duration in the
+                 timed steps, vs the 157.3 TFLOP/s dense FP32 MFMA peak (achieved_flushed: the
+                 same from the cache-cold launches); traffic (HBM bytes per launch) from the
                  committed rocprofv3 counter summary profiles/fa2_config2_counters.md.
-  cpu_baseline   the CPU oracle (numpy port of the reference algorithm, float32) timed on this
-                 host's cores on a bounded sample of whole heads of the same workload.
-  cpu_reference_path
-                 the reference's own CPU comparison path, torch FP32 SDPA forward + autograd
-                 backward, timed on the same host cores on 16 whole heads, with the backend torch
-                 chose and the estimated time of the full step.
+  cpu_baseline   the reference's CPU comparison path, torch FP32 SDPA forward + autograd
+                 backward (its test oracle), timed on this host's cores on whole heads of the
+                 same workload, with the backend torch chose, the CPU model and the estimated
+                 time of the full step.
+  cpu_baseline_port
+                 the CPU oracle (numpy port of the reference algorithm, float32) timed on a
+                 bounded sample of whole heads of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -66,6 +70,9 @@ def parse_args():
     p.add_argument("--seq", type=int, default=4096)
     p.add_argument("--head-dim", type=int, default=64)
     p.add_argument("--non-causal", action="store_true")
+    p.add_argument("--seqs", default="",
+                   help="fa2-sweep workload: comma-separated sequence lengths (default "
+                        "1024,2048,4096,8192,16384)")
     p.add_argument("--masks", choices=["both", "causal", "full"], default="both",
                    help="fa2-bf16 workload: which masks to time")
     p.add_argument("--gpt-mlp", choices=["fused", "reference"], default="fused",
@@ -99,6 +106,47 @@ def copy_calibration(mib):
     return 0
 
 
+# Bytes written between timed repetitions so that the next kernel starts with cold caches: well
+# above the 256 MB MALL (Infinity Cache) and the 8 x 4 MB of L2.
+FLUSH_BYTES = 1 << 30
+
+
+class CacheFlush:
+    """Writes FLUSH_BYTES of device memory (one fill kernel on the current stream), evicting the
+    L2s and the MALL before the next timed launch."""
+
+    def __init__(self, dev):
+        import torch
+
+        self.buf = torch.empty(FLUSH_BYTES // 4, device=dev)
+        self.n = 0
+
+    def __call__(self):
+        self.n += 1
+        self.buf.fill_(float(self.n & 0xFF))
+
+
+def host_info():
+    """CPU model, logical CPUs and the GPU's architecture, for the CPU-baseline records."""
+    import torch
+
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    info = {"cpu_model": model, "cpu_count": os.cpu_count()}
+    if torch.cuda.is_available():
+        props = torch.cuda.get_device_properties(0)
+        info["gpu"] = torch.cuda.get_device_name(0)
+        info["gpu_arch"] = getattr(props, "gcnArchName", "unknown")
+        info["gpu_cus"] = props.multi_processor_count
+    return info
+
+
 def attn_flops(B, H, N, D, causal):
     fwd = 4.0 * B * H * N * N * D * (0.5 if causal else 1.0)
     return fwd, 2.5 * fwd
@@ -128,7 +176,7 @@ def load_traffic(kernel: str):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(B, H, N, D, causal, target_s):
+def cpu_port_baseline(B, H, N, D, causal, target_s):
     """Time the CPU oracle (float32 numpy, BLAS-threaded) on whole heads until target_s."""
     import numpy as np
     from threadpoolctl import threadpool_info, threadpool_limits
@@ -165,11 +213,12 @@ def cpu_baseline(B, H, N, D, causal, target_s):
     }
 
 
-def cpu_reference_path(B, H, N, D, causal, heads=16):
+def cpu_reference_path(B, H, N, D, causal, step_s=2.0):
     """The reference's own CPU path, as its test suite and benchmark define correctness and the
     comparison point (test/test_flash_attention.py:10-21, benchmark/cuda_bench.py:44-68): torch
-    FP32 scaled_dot_product_attention forward + autograd backward on this host's cores, on
-    `heads` whole heads of the workload.  One warm-up step, then the median of three."""
+    FP32 scaled_dot_product_attention forward + autograd backward on this host's cores, on whole
+    heads of the workload: as many as an estimated step_s per step allows (at ~1.4 TFLOP/s), all
+    of them when that covers the workload.  One warm-up step, then the median of three."""
     import statistics
 
     import torch
@@ -179,7 +228,8 @@ def cpu_reference_path(B, H, N, D, causal, heads=16):
     prev = torch.get_num_threads()
     torch.set_num_threads(threads)
     try:
-        heads = min(heads, B * H)
+        per_head = sum(attn_flops(1, 1, N, D, causal))
+        heads = max(1, min(B * H, int(step_s * 1.4e12 / per_head)))
         gen = torch.Generator().manual_seed(0)
         q, k, v = (torch.randn(1, heads, N, D, generator=gen).requires_grad_() for _ in range(3))
         do = torch.randn(1, heads, N, D, generator=torch.Generator().manual_seed(1))
@@ -201,16 +251,19 @@ def cpu_reference_path(B, H, N, D, causal, heads=16):
         torch.set_num_threads(prev)
     fwd, bwd = attn_flops(1, heads, N, D, causal)
     return {
-        "value": (fwd + bwd) / med / 1e12,
+        "value": round((fwd + bwd) / med / 1e12, 4),
         "unit": "TFLOPS",
         "cores": threads,
-        "cpu_count": os.cpu_count(),
-        "kind": "torch-sdpa",
+        "kind": "reference",
+        "path": ("the reference's CPU comparison path: torch FP32 F.scaled_dot_product_attention "
+                 "+ autograd backward (its test oracle, test/test_flash_attention.py:32,44-50); "
+                 "the reference's CUDA kernels cannot build here"),
         "backend": backend.name,
         "sample": (f"{heads} of {B * H} heads (N={N}, D={D}, {'causal' if causal else 'full'}), "
                    f"torch {torch.__version__} F.scaled_dot_product_attention + backward, FP32, "
                    f"{threads} threads, median of 3 steps of {med:.3f} s"),
         "est_ms_per_full_step": round(med * 1e3 * B * H / heads, 1),
+        **{k_: v_ for k_, v_ in host_info().items() if k_ in ("cpu_model", "cpu_count")},
     }
 
 
@@ -218,11 +271,14 @@ def cpu_reference_path(B, H, N, D, causal, heads=16):
 BWD_WORKSPACE_CAP = 8 << 30
 
 
-def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored"):
+def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_reps=5):
     """Time `steps` FA2 steps through the C ABI on torch's current stream: fwd, then the
     backward stages of `schedule` ([delta, dkdv, dq_ds] stored; [delta, dq, dkdv] recompute;
     one combined [bwd] launch when the stored schedule needs head chunks, as the operator
-    runs it).  Returns (wall ms per step, {kernel: mean HIP-event ms}, (q, k, v, dO))."""
+    runs it).  After the timed steps, each kernel is timed again `flushed_reps` times with
+    FLUSH_BYTES written before every launch (cold L2 and MALL).  Returns (wall ms per step,
+    {kernel: mean HIP-event ms in the timed steps}, {kernel: median flushed ms},
+    (q, k, v, dO))."""
     import torch
 
     from cuda_transformer_amd import capi
@@ -306,29 +362,90 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored"):
     wall = time.perf_counter() - t0
     per_kernel = {kname: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps
                   for j, kname in enumerate(kernels)}
-    return wall * 1e3 / steps, per_kernel, (q, k, v, do)
+
+    # Cache-cold repetitions of each kernel (outside the timed region).
+    import statistics
+
+    flush = CacheFlush(dev)
+    flushed = {}
+    for kname in kernels:
+        pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                 for _ in range(flushed_reps)]
+        for a, b in pairs:
+            flush()
+            a.record(stream)
+            launch(kname)
+            b.record(stream)
+        torch.cuda.synchronize()
+        flushed[kname] = statistics.median(a.elapsed_time(b) for a, b in pairs)
+    del flush
+    return wall * 1e3 / steps, per_kernel, flushed, (q, k, v, do)
+
+
+def roofline_of(per_kernel, B, H, N, D, causal, flushed=None):
+    """Roofline object of the dominant kernel among `per_kernel` (the combined chunked "bwd"
+    launch is not a single kernel and is left out): its algorithmic work per launch over its
+    mean duration, against the FP32 MFMA or HBM peak."""
+    kernel_symbols = {"fwd": "fa2_fwd_kernel", "delta": "fa2_bwd_delta_kernel",
+                      "dq": "fa2_bwd_dq_kernel", "dkdv": "fa2_bwd_dkdv_kernel",
+                      "dq_ds": "fa2_bwd_dq_ds_kernel"}
+    dom = max((k_ for k_ in per_kernel if k_ != "bwd"), key=per_kernel.get)
+    amount, unit, bound = kernel_algorithmic(dom, B, H, N, D, causal)
+    scale, peak = (1e12, MFMA_FP32_PEAK_TFLOPS) if unit == "TFLOP/s" else (1e9, HBM_PEAK_GBPS)
+    achieved = amount / (per_kernel[dom] * 1e-3) / scale
+    out = {"kernel": kernel_symbols[dom], "bound": bound, "achieved": round(achieved, 3),
+           "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
+           "traffic": None, "algorithmic_per_launch": amount,
+           "mean_launch_ms": round(per_kernel[dom], 4)}
+    if flushed and dom in flushed:
+        af = amount / (flushed[dom] * 1e-3) / scale
+        out["achieved_flushed"] = round(af, 3)
+        out["frac_flushed"] = round(af / peak, 4)
+    return out
 
 
 def fa2_sweep(args):
-    """Benchmark config 3: non-causal B4 H32 D64, N in {1024 ... 16384}; one JSON line per N."""
+    """Benchmark config 3: non-causal B4 H32 D64, N in {1024 ... 16384} (or --seqs); one JSON
+    line per N in the layout of the reference's sweep table (README.md:38-56): forward and
+    backward TFLOPS and fraction of peak, per-kernel times (in the timed steps and cache-cold),
+    the dominant kernel's roofline, and the torch SDPA CPU path on a bounded head sample."""
     import torch
 
-    for N in (1024, 2048, 4096, 8192, 16384):
-        steps = max(2, args.steps // (N // 1024))
-        ms, per_kernel, _ = fa2_timings(4, 32, N, 64, False, steps, 1, args.bwd_schedule)
-        fwd_fl, bwd_fl = attn_flops(4, 32, N, 64, False)
+    from cuda_transformer_amd import capi
+
+    seqs = [int(x) for x in args.seqs.split(",")] if args.seqs else [1024, 2048, 4096, 8192,
+                                                                      16384]
+    B, H, D = 4, 32, 64
+    for N in seqs:
+        steps = max(2, args.steps // max(1, N // 2048))
+        ms, per_kernel, flushed, _ = fa2_timings(B, H, N, D, False, steps, 1, args.bwd_schedule)
+        fwd_fl, bwd_fl = attn_flops(B, H, N, D, False)
         bwd_ms = sum(v_ for k_, v_ in per_kernel.items() if k_ != "fwd")
-        print(json.dumps({
-            "workload": f"FA2 B4 H32 N{N} D64 non-causal", "N": N, "steps": steps,
-            "bwd_schedule": args.bwd_schedule,
+        bwd_ms_f = sum(v_ for k_, v_ in flushed.items() if k_ != "fwd")
+        ws_full = capi.lib().cta_flash_attention_bwd_workspace(B, H, N, D, 0)
+        head = capi.lib().cta_flash_attention_bwd_workspace(1, 1, N, D, 0)
+        fit = min(B * H, BWD_WORKSPACE_CAP // head)
+        chunks = -(-B * H // fit) if args.bwd_schedule == "stored" else 0
+        line = {
+            "workload": f"FA2 B{B} H{H} N{N} D{D} non-causal", "N": N, "steps": steps,
+            "dtype": "f32", "bwd_schedule": args.bwd_schedule, "bwd_head_chunks": chunks,
+            "ds_workspace_bytes": min(ws_full, BWD_WORKSPACE_CAP),
+            "ms_per_step": round(ms, 4),
             "fwd_ms": round(per_kernel["fwd"], 4), "bwd_ms": round(bwd_ms, 4),
             "fwd_tflops": round(fwd_fl / per_kernel["fwd"] / 1e9, 3),
             "bwd_tflops": round(bwd_fl / bwd_ms / 1e9, 3),
             "fwd_frac_of_peak": round(fwd_fl / per_kernel["fwd"] / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
             "bwd_frac_of_peak": round(bwd_fl / bwd_ms / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
+            "fwd_tflops_flushed": round(fwd_fl / flushed["fwd"] / 1e9, 3),
+            "bwd_tflops_flushed": round(bwd_fl / bwd_ms_f / 1e9, 3),
             "per_kernel_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
-        }), flush=True)
+            "per_kernel_ms_flushed": {k_: round(v_, 4) for k_, v_ in flushed.items()},
+            "roofline": roofline_of(per_kernel, B, H, N, D, False, flushed),
+        }
         torch.cuda.empty_cache()
+        if not args.no_cpu_baseline:
+            line["cpu_baseline"] = cpu_reference_path(B, H, N, D, False)
+        print(json.dumps(line), flush=True)
     return 0
 
 
@@ -396,10 +513,12 @@ def fa2_half_workload(args, kind):
     return 0
 
 
-def _time_kernel(fn, reps, warm_s=0.02):
+def _time_kernel(fn, reps, warm_s=0.02, flush=None):
     """Median HIP-event duration (ms) of fn's launches on torch's current stream, over at least
     20 launches, after at least warm_s of back-to-back launches: the CPU-baseline timings between
-    ops leave the GPU idle long enough for its clocks to drop."""
+    ops leave the GPU idle long enough for its clocks to drop.  With `flush` (a CacheFlush), the
+    flush runs before every timed launch, outside its event pair, so each launch starts with
+    cold L2s and MALL."""
     import statistics
 
     import torch
@@ -415,6 +534,8 @@ def _time_kernel(fn, reps, warm_s=0.02):
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(max(20, reps))]
     for a, b in evs:
+        if flush is not None:
+            flush()
         a.record(stream)
         fn()
         b.record(stream)
@@ -436,157 +557,163 @@ def _cpu_time(fn, target_s=2.0):
 
 def ops_workload(args):
     """Benchmark config 4 (GPT-2-small widths, FP32): linear GEMM fwd/bwd, db, exact and
-    tanh-approximated GELU, LayerNorm and row softmax, each launched through the C ABI.  One JSON line per op with
-    the kernel's roofline (MFMA TFLOP/s for GEMMs, HBM GB/s otherwise) and the CPU oracle
-    (float32 numpy) timed on a bounded sample of the same op."""
-    import numpy as np
+    tanh-approximated GELU, LayerNorm and row softmax, each launched through the C ABI.  One JSON
+    line per op with the kernel's roofline (MFMA TFLOP/s for GEMMs, HBM GB/s otherwise).  Each op
+    is timed cache-cold (FLUSH_BYTES written before every launch: the primary figure, "ms") and
+    back-to-back on the same buffers ("ms_unflushed"; operands under 256 MB may then be served
+    partly by the MALL).  CPU baseline: torch's own CPU kernels for the same op (the reference's
+    test oracle path: test/test_linear.py, test_gelu.py, test_softmax.py; gpt/gpt.py:47-59 for
+    LayerNorm) on 1/8 of the rows, on this host's cores."""
     import torch
-    from threadpoolctl import threadpool_limits
+    import torch.nn.functional as F
 
     from cuda_transformer_amd import capi
-    from oracle import elementwise as ew
-    from oracle import linear as lin
 
     lib = capi.lib()
     dev = torch.device("cuda", 0)
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-    reps = max(5, args.steps)
+    reps = max(20, args.steps)
     g = torch.Generator().manual_seed(0)
     cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    flush = CacheFlush(dev)
+    host = host_info()
+    aten = torch.ops.aten
 
-    def emit(name, shape, ms, amount, unit, cpu_s, cpu_amount, sample):
-        if unit == "TFLOP/s":
-            achieved, peak = amount / (ms * 1e-3) / 1e12, MFMA_FP32_PEAK_TFLOPS
-            cpu_val = cpu_amount / cpu_s / 1e12
-        else:
-            achieved, peak = amount / (ms * 1e-3) / 1e9, HBM_PEAK_GBPS
-            cpu_val = cpu_amount / cpu_s / 1e9
+    def timed(fn):
+        return _time_kernel(fn, reps, flush=flush), _time_kernel(fn, reps)
+
+    def emit(name, shape, ms_pair, amount, unit, cpu_s, cpu_amount, sample):
+        ms, ms_warm = ms_pair
+        scale, peak = (1e12, MFMA_FP32_PEAK_TFLOPS) if unit == "TFLOP/s" else (1e9, HBM_PEAK_GBPS)
+        achieved, warm = amount / (ms * 1e-3) / scale, amount / (ms_warm * 1e-3) / scale
         print(json.dumps({
-            "workload": name, "shape": shape, "ms": round(ms, 5), "value": round(achieved, 3),
-            "unit": unit,
+            "workload": name, "shape": shape, "dtype": "f32", "ms": round(ms, 5),
+            "ms_unflushed": round(ms_warm, 5), "value": round(achieved, 3), "unit": unit,
             "roofline": {"bound": "mfma" if unit == "TFLOP/s" else "hbm",
                          "achieved": round(achieved, 3), "peak": peak,
-                         "frac": round(achieved / peak, 4), "algorithmic_per_launch": amount},
-            "cpu_baseline": {"value": round(cpu_val, 4), "unit": unit, "cores": cores,
-                             "kind": "port", "sample": sample},
+                         "frac": round(achieved / peak, 4), "algorithmic_per_launch": amount,
+                         "achieved_unflushed": round(warm, 3),
+                         "frac_unflushed": round(warm / peak, 4)},
+            "cpu_baseline": {"value": round(cpu_amount / cpu_s / scale, 4), "unit": unit,
+                             "cores": cores, "kind": "reference", "sample": sample,
+                             "cpu_model": host["cpu_model"]},
         }), flush=True)
 
-    with threadpool_limits(limits=cores, user_api="blas"):
-        # ---- linear layer: X[8192,768] . W[768,3072] + b, X, W ~ N(0, 0.02^2)
-        M, K, Nn = 8192, 768, 3072
-        x = (torch.randn(1, M, K, generator=g) * 0.02).to(dev)
-        w = (torch.randn(K, Nn, generator=g) * 0.02).to(dev)
-        b = (torch.randn(Nn, generator=g) * 0.02).to(dev)
-        dy = (torch.randn(1, M, Nn, generator=g) * 0.02).to(dev)
-        out = torch.empty(1, M, Nn, device=dev)
-        dx = torch.empty(1, M, K, device=dev)
-        dw = torch.empty(1, K, Nn, device=dev)
-        zk, zn = torch.zeros(K, device=dev), torch.zeros(Nn, device=dev)
-        xs, ws = capi.strides(x.stride()), capi.strides((0, Nn, 1))
-        wts = capi.strides((0, 1, Nn))              # W^T view (1, n=3072 -> k, 768)
-        dys = capi.strides(dy.stride())
-        xts = capi.strides((M * K, 1, K))           # x^T view (1, 768, 8192)
-        fl = 2.0 * M * K * Nn
-        xc, wc, dyc = (t.cpu().numpy().reshape(t.shape[-2:]) for t in (x, w, dy))
-        rows = M // 8
-        sample = f"rows 0..{rows} of {M} (1/8), float32 numpy BLAS"
+    def cpu8(what):
+        return f"torch {torch.__version__} CPU {what}, FP32, rows 0..1/8, {cores} threads"
 
-        def scratch(m_, k_, n_):
-            nbytes = lib.cta_cuda_fma_workspace(1, m_, k_, n_)
-            return torch.empty(max(1, nbytes // 4), device=dev) if nbytes else None
+    # ---- linear layer: X[8192,768] . W[768,3072] + b, X, W ~ N(0, 0.02^2)
+    M, K, Nn = 8192, 768, 3072
+    x = (torch.randn(1, M, K, generator=g) * 0.02).to(dev)
+    w = (torch.randn(K, Nn, generator=g) * 0.02).to(dev)
+    b = (torch.randn(Nn, generator=g) * 0.02).to(dev)
+    dy = (torch.randn(1, M, Nn, generator=g) * 0.02).to(dev)
+    out = torch.empty(1, M, Nn, device=dev)
+    dx = torch.empty(1, M, K, device=dev)
+    dw = torch.empty(1, K, Nn, device=dev)
+    zk, zn = torch.zeros(K, device=dev), torch.zeros(Nn, device=dev)
+    xs, ws = capi.strides(x.stride()), capi.strides((0, Nn, 1))
+    wts = capi.strides((0, 1, Nn))              # W^T view (1, n=3072 -> k, 768)
+    dys = capi.strides(dy.stride())
+    xts = capi.strides((M * K, 1, K))           # x^T view (1, 768, 8192)
+    fl = 2.0 * M * K * Nn
+    rows = M // 8
+    xc, wc, bc, dyc = x[0, :rows].cpu(), w.cpu(), b.cpu(), dy[0, :rows].cpu()
 
-        ws_f, ws_dx, ws_dw = scratch(M, K, Nn), scratch(M, Nn, K), scratch(K, M, Nn)
-        vpo = lambda t: None if t is None else vp(t)  # noqa: E731
+    def scratch(m_, k_, n_):
+        nbytes = lib.cta_cuda_fma_workspace(1, m_, k_, n_)
+        return torch.empty(max(1, nbytes // 4), device=dev) if nbytes else None
 
-        def gemm_fwd():
-            assert lib.cta_cuda_fma(vp(x), xs, vp(w), ws, vp(b), 1, 1, M, K, Nn, 1, vp(out),
-                                    vpo(ws_f), st) == 0
-        emit("linear_fwd (cuda_fma)", [M, K, Nn], _time_kernel(gemm_fwd, reps), fl, "TFLOP/s",
-             _cpu_time(lambda: xc[:rows] @ wc + b.cpu().numpy()), fl / 8, sample)
+    ws_f, ws_dx, ws_dw = scratch(M, K, Nn), scratch(M, Nn, K), scratch(K, M, Nn)
+    vpo = lambda t: None if t is None else vp(t)  # noqa: E731
 
-        def gemm_dx():
-            assert lib.cta_cuda_fma(vp(dy), dys, vp(w), wts, vp(zk), 1, 1, M, Nn, K, 1, vp(dx),
-                                    vpo(ws_dx), st) == 0
-        emit("linear_bwd_dx (cuda_fma, W^T view)", [M, Nn, K], _time_kernel(gemm_dx, reps), fl,
-             "TFLOP/s", _cpu_time(lambda: dyc[:rows] @ wc.T), fl / 8, sample)
+    def gemm_fwd():
+        assert lib.cta_cuda_fma(vp(x), xs, vp(w), ws, vp(b), 1, 1, M, K, Nn, 1, vp(out),
+                                vpo(ws_f), st) == 0
+    emit("linear_fwd (cuda_fma)", [M, K, Nn], timed(gemm_fwd), fl, "TFLOP/s",
+         _cpu_time(lambda: torch.addmm(bc, xc, wc), 1.0), fl / 8, cpu8("addmm"))
 
-        def gemm_dw():
-            assert lib.cta_cuda_fma(vp(x), xts, vp(dy), dys, vp(zn), 1, 1, K, M, Nn, 1, vp(dw),
-                                    vpo(ws_dw), st) == 0
-        emit("linear_bwd_dw (cuda_fma, x^T view)", [K, M, Nn], _time_kernel(gemm_dw, reps), fl,
-             "TFLOP/s", _cpu_time(lambda: xc[:rows].T @ dyc[:rows]), fl / 8, sample)
+    def gemm_dx():
+        assert lib.cta_cuda_fma(vp(dy), dys, vp(w), wts, vp(zk), 1, 1, M, Nn, K, 1, vp(dx),
+                                vpo(ws_dx), st) == 0
+    emit("linear_bwd_dx (cuda_fma, W^T view)", [M, Nn, K], timed(gemm_dx), fl, "TFLOP/s",
+         _cpu_time(lambda: dyc @ wc.T, 1.0), fl / 8, cpu8("dy @ W^T"))
 
-        db = torch.empty(Nn, device=dev)
-        ws_db = torch.empty(lib.cta_db_calculation_workspace(1, M, Nn) // 4, device=dev)
+    def gemm_dw():
+        assert lib.cta_cuda_fma(vp(x), xts, vp(dy), dys, vp(zn), 1, 1, K, M, Nn, 1, vp(dw),
+                                vpo(ws_dw), st) == 0
+    emit("linear_bwd_dw (cuda_fma, x^T view)", [K, M, Nn], timed(gemm_dw), fl, "TFLOP/s",
+         _cpu_time(lambda: xc.T @ dyc, 1.0), fl / 8, cpu8("x^T @ dy"))
 
-        def dbk():
-            assert lib.cta_db_calculation(vp(dy), dys, 1, M, Nn, vp(db), vp(ws_db), st) == 0
-        emit("db_calculation", [M, Nn], _time_kernel(dbk, reps), 4.0 * M * Nn + 4 * Nn, "GB/s",
-             _cpu_time(lambda: lin.db_calculation(dyc[None, :rows])), 4.0 * rows * Nn, sample)
-        del x, w, dy, out, dx, dw
+    db = torch.empty(Nn, device=dev)
+    ws_db = torch.empty(lib.cta_db_calculation_workspace(1, M, Nn) // 4, device=dev)
 
-        # ---- exact GELU on [8192, 3072]
-        n = M * Nn
-        xg = torch.randn(n, generator=g).to(dev)
-        yg, gg = torch.empty_like(xg), torch.randn(n, generator=g).to(dev)
-        xgc, ggc = xg[: n // 8].cpu().numpy(), gg[: n // 8].cpu().numpy()
-        sample8 = "1/8 of the elements, float32 numpy oracle"
-        emit("gelu_fwd", [M, Nn], _time_kernel(lambda: lib.cta_gelu_fwd(vp(xg), vp(yg), n, st), reps),
-             8.0 * n, "GB/s", _cpu_time(lambda: ew.gelu_forward(xgc)), 8.0 * n / 8, sample8)
-        emit("gelu_bwd", [M, Nn],
-             _time_kernel(lambda: lib.cta_gelu_bwd(vp(xg), vp(gg), vp(yg), n, st), reps),
-             12.0 * n, "GB/s", _cpu_time(lambda: ew.gelu_backward(xgc, ggc)), 12.0 * n / 8, sample8)
-        # ---- tanh-approximated GELU (the form config 4 names) on the same tensor
-        emit("gelu_tanh_fwd", [M, Nn],
-             _time_kernel(lambda: lib.cta_gelu_tanh_fwd(vp(xg), vp(yg), n, st), reps),
-             8.0 * n, "GB/s", _cpu_time(lambda: ew.gelu_tanh_forward(xgc)), 8.0 * n / 8, sample8)
-        emit("gelu_tanh_bwd", [M, Nn],
-             _time_kernel(lambda: lib.cta_gelu_tanh_bwd(vp(xg), vp(gg), vp(yg), n, st), reps),
-             12.0 * n, "GB/s", _cpu_time(lambda: ew.gelu_tanh_backward(xgc, ggc)), 12.0 * n / 8,
-             sample8)
-        del xg, yg, gg
+    def dbk():
+        assert lib.cta_db_calculation(vp(dy), dys, 1, M, Nn, vp(db), vp(ws_db), st) == 0
+    emit("db_calculation", [M, Nn], timed(dbk), 4.0 * M * Nn + 4 * Nn, "GB/s",
+         _cpu_time(lambda: dyc.sum(0), 1.0), 4.0 * rows * Nn, cpu8("dy.sum(0)"))
+    del x, w, dy, out, dx, dw
 
-        # ---- LayerNorm over 768 on [8192, 768], gamma = 1, beta = 0
-        R, C = 8192, 768
-        xl = torch.randn(R, C, generator=g).to(dev)
-        gam, bet = torch.ones(C, device=dev), torch.zeros(C, device=dev)
-        yl, mean, rstd = torch.empty_like(xl), torch.empty(R, device=dev), torch.empty(R, device=dev)
-        dyl, dxl = torch.randn(R, C, generator=g).to(dev), torch.empty_like(xl)
-        dgam, dbet = torch.empty(C, device=dev), torch.empty(C, device=dev)
-        ws_ln = torch.empty(lib.cta_layernorm_bwd_workspace(R, C) // 4, device=dev)
-        xlc, dylc = xl[: R // 8].cpu().numpy(), dyl[: R // 8].cpu().numpy()
-        onec, zeroc = np.ones(C, np.float32), np.zeros(C, np.float32)
-        eps = ctypes.c_float(1e-5)
-        emit("layernorm_fwd", [R, C], _time_kernel(
-            lambda: lib.cta_layernorm_fwd(vp(xl), vp(gam), vp(bet), R, C, eps, vp(yl), vp(mean),
-                                          vp(rstd), st), reps),
-             8.0 * R * C + 8 * R, "GB/s",
-             _cpu_time(lambda: ew.layernorm_forward(xlc, onec, zeroc)), (8.0 * R * C + 8 * R) / 8,
-             sample8.replace("elements", "rows"))
-        _, mc, rc_ = ew.layernorm_forward(xlc, onec, zeroc)
-        emit("layernorm_bwd", [R, C], _time_kernel(
-            lambda: lib.cta_layernorm_bwd(vp(xl), vp(gam), vp(mean), vp(rstd), vp(dyl), R, C,
-                                          vp(dxl), vp(dgam), vp(dbet), vp(ws_ln), st), reps),
-             12.0 * R * C + 8 * R + 8 * C, "GB/s",
-             _cpu_time(lambda: ew.layernorm_backward(xlc, onec, mc, rc_, dylc)),
-             (12.0 * R * C + 8 * R) / 8, sample8.replace("elements", "rows"))
-        del xl, yl, dyl, dxl
+    # ---- exact and tanh-approximated GELU on [8192, 3072]
+    n = M * Nn
+    xg = torch.randn(n, generator=g).to(dev)
+    yg, gg = torch.empty_like(xg), torch.randn(n, generator=g).to(dev)
+    xgc, ggc = xg[: n // 8].cpu(), gg[: n // 8].cpu()
+    for approx, fwd_fn, bwd_fn, tag in (("none", lib.cta_gelu_fwd, lib.cta_gelu_bwd, ""),
+                                        ("tanh", lib.cta_gelu_tanh_fwd, lib.cta_gelu_tanh_bwd,
+                                         "_tanh")):
+        emit(f"gelu{tag}_fwd", [M, Nn], timed(lambda: fwd_fn(vp(xg), vp(yg), n, st)), 8.0 * n,
+             "GB/s", _cpu_time(lambda: F.gelu(xgc, approximate=approx), 1.0), 8.0 * n / 8,
+             cpu8(f"F.gelu(approximate={approx!r})"))
+        emit(f"gelu{tag}_bwd", [M, Nn], timed(lambda: bwd_fn(vp(xg), vp(gg), vp(yg), n, st)),
+             12.0 * n, "GB/s",
+             _cpu_time(lambda: aten.gelu_backward(ggc, xgc, approximate=approx), 1.0),
+             12.0 * n / 8, cpu8("aten.gelu_backward"))
+    del xg, yg, gg
 
-        # ---- row softmax on [4*12*1024, 1024], logits ~ N(0, 4)
-        R, C = 4 * 12 * 1024, 1024
-        xs_ = (torch.randn(R, C, generator=g) * 2).to(dev)
-        ps_, dps, dxs = torch.empty_like(xs_), torch.rand(R, C, generator=g).to(dev), torch.empty_like(xs_)
-        xsc, dpsc = xs_[: R // 8].cpu().numpy(), dps[: R // 8].cpu().numpy()
-        emit("softmax_fwd", [R, C],
-             _time_kernel(lambda: lib.cta_softmax_fwd(vp(xs_), vp(ps_), R, C, st), reps),
-             8.0 * R * C, "GB/s", _cpu_time(lambda: ew.softmax_forward(xsc)), 8.0 * R * C / 8,
-             sample8.replace("elements", "rows"))
-        psc = ew.softmax_forward(xsc).astype(np.float32)
-        emit("softmax_bwd", [R, C],
-             _time_kernel(lambda: lib.cta_softmax_bwd(vp(ps_), vp(dps), vp(dxs), R, C, st), reps),
-             12.0 * R * C, "GB/s", _cpu_time(lambda: ew.softmax_backward(psc, dpsc)),
-             12.0 * R * C / 8, sample8.replace("elements", "rows"))
+    # ---- LayerNorm over 768 on [8192, 768], gamma = 1, beta = 0
+    R, C = 8192, 768
+    xl = torch.randn(R, C, generator=g).to(dev)
+    gam, bet = torch.ones(C, device=dev), torch.zeros(C, device=dev)
+    yl, mean, rstd = torch.empty_like(xl), torch.empty(R, device=dev), torch.empty(R, device=dev)
+    dyl, dxl = torch.randn(R, C, generator=g).to(dev), torch.empty_like(xl)
+    dgam, dbet = torch.empty(C, device=dev), torch.empty(C, device=dev)
+    ws_ln = torch.empty(lib.cta_layernorm_bwd_workspace(R, C) // 4, device=dev)
+    xlc, dylc = xl[: R // 8].cpu(), dyl[: R // 8].cpu()
+    gamc, betc = gam.cpu(), bet.cpu()
+    eps = ctypes.c_float(1e-5)
+    emit("layernorm_fwd", [R, C], timed(
+        lambda: lib.cta_layernorm_fwd(vp(xl), vp(gam), vp(bet), R, C, eps, vp(yl), vp(mean),
+                                      vp(rstd), st)),
+         8.0 * R * C + 8 * R, "GB/s",
+         _cpu_time(lambda: aten.native_layer_norm(xlc, [C], gamc, betc, 1e-5), 1.0),
+         (8.0 * R * C + 8 * R) / 8, cpu8("aten.native_layer_norm"))
+    _, mc, rc_ = aten.native_layer_norm(xlc, [C], gamc, betc, 1e-5)
+    emit("layernorm_bwd", [R, C], timed(
+        lambda: lib.cta_layernorm_bwd(vp(xl), vp(gam), vp(mean), vp(rstd), vp(dyl), R, C,
+                                      vp(dxl), vp(dgam), vp(dbet), vp(ws_ln), st)),
+         12.0 * R * C + 8 * R + 8 * C, "GB/s",
+         _cpu_time(lambda: aten.native_layer_norm_backward(dylc, xlc, [C], mc, rc_, gamc, betc,
+                                                           [True, True, True]), 1.0),
+         (12.0 * R * C + 8 * R) / 8, cpu8("aten.native_layer_norm_backward"))
+    del xl, yl, dyl, dxl
+
+    # ---- row softmax on [4*12*1024, 1024], logits ~ N(0, 4)
+    R, C = 4 * 12 * 1024, 1024
+    xs_ = (torch.randn(R, C, generator=g) * 2).to(dev)
+    ps_, dps, dxs = torch.empty_like(xs_), torch.rand(R, C, generator=g).to(dev), torch.empty_like(xs_)
+    xsc, dpsc = xs_[: R // 8].cpu(), dps[: R // 8].cpu()
+    emit("softmax_fwd", [R, C], timed(lambda: lib.cta_softmax_fwd(vp(xs_), vp(ps_), R, C, st)),
+         8.0 * R * C, "GB/s", _cpu_time(lambda: F.softmax(xsc, dim=-1), 1.0), 8.0 * R * C / 8,
+         cpu8("F.softmax"))
+    psc = F.softmax(xsc, dim=-1)
+    emit("softmax_bwd", [R, C],
+         timed(lambda: lib.cta_softmax_bwd(vp(ps_), vp(dps), vp(dxs), R, C, st)),
+         12.0 * R * C, "GB/s",
+         _cpu_time(lambda: aten._softmax_backward_data(dpsc, psc, -1, torch.float32), 1.0),
+         12.0 * R * C / 8, cpu8("aten._softmax_backward_data"))
     return 0
 
 
@@ -688,8 +815,8 @@ def main():
         return fa2_half_workload(args, args.workload[4:])
     B, H, N, D = args.batch, args.heads, args.seq, args.head_dim
     causal = not args.non_causal
-    ms_step, per_kernel, (q, k, v, do) = fa2_timings(B, H, N, D, causal, args.steps, args.warmup,
-                                                     args.bwd_schedule)
+    ms_step, per_kernel, flushed, (q, k, v, do) = fa2_timings(B, H, N, D, causal, args.steps,
+                                                              args.warmup, args.bwd_schedule)
 
     fwd_fl, bwd_fl = attn_flops(B, H, N, D, causal)
     value = (fwd_fl + bwd_fl) / (ms_step * 1e-3) / 1e12
@@ -697,19 +824,8 @@ def main():
     bwd_ms = sum(v_ for k_, v_ in per_kernel.items() if k_ != "fwd")
     bwd_tf = bwd_fl / (bwd_ms * 1e-3) / 1e12
 
-    dom = max((k_ for k_ in per_kernel if k_ != "bwd"), key=per_kernel.get)
-    amount, unit, bound = kernel_algorithmic(dom, B, H, N, D, causal)
-    if unit == "TFLOP/s":
-        achieved, peak = amount / (per_kernel[dom] * 1e-3) / 1e12, MFMA_FP32_PEAK_TFLOPS
-    else:
-        achieved, peak = amount / (per_kernel[dom] * 1e-3) / 1e9, HBM_PEAK_GBPS
-    kernel_symbols = {"fwd": "fa2_fwd_kernel", "delta": "fa2_bwd_delta_kernel",
-                      "dq": "fa2_bwd_dq_kernel", "dkdv": "fa2_bwd_dkdv_kernel",
-                      "dq_ds": "fa2_bwd_dq_ds_kernel"}
-    roofline = {"kernel": kernel_symbols[dom], "bound": bound, "achieved": round(achieved, 3),
-                "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
-                "traffic": load_traffic(kernel_symbols[dom]),
-                "algorithmic_per_launch": amount}
+    roofline = roofline_of(per_kernel, B, H, N, D, causal, flushed)
+    roofline["traffic"] = load_traffic(roofline["kernel"])
 
     extra = {}
     if not args.no_autograd:
@@ -751,15 +867,17 @@ def main():
         "fwd_frac_of_peak": round(fwd_tf / MFMA_FP32_PEAK_TFLOPS, 4),
         "bwd_frac_of_peak": round(bwd_tf / MFMA_FP32_PEAK_TFLOPS, 4),
         "per_kernel_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
+        "per_kernel_ms_flushed": {k_: round(v_, 4) for k_, v_ in flushed.items()},
         "roofline": roofline,
         "reference_rtx5070_ms": REFERENCE_RTX5070_MS,
         "device": torch.cuda.get_device_name(0),
+        "host": host_info(),
         "torch": torch.__version__,
         **extra,
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(B, H, N, D, causal, args.cpu_seconds)
-        line["cpu_reference_path"] = cpu_reference_path(B, H, N, D, causal)
+        line["cpu_baseline"] = cpu_reference_path(B, H, N, D, causal)
+        line["cpu_baseline_port"] = cpu_port_baseline(B, H, N, D, causal, args.cpu_seconds)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

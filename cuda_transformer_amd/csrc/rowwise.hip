@@ -179,12 +179,14 @@ __global__ __launch_bounds__(256) void softmax_fwd_rows(const float* x, float* y
 #pragma unroll
     for (int e = 0; e < U * r.W; ++e) mx = fmaxf(mx, r.v[e]);
     mx = wave_max(mx);
-    // e^{v - mx} = 2^{v log2(e) - mx log2(e)}: one fma and the hardware exp2 per element
-    const float off = mx * kLog2e;
+    // e^{v - mx} = 2^{(v - mx) log2(e)} with the hardware exp2.  The difference is taken
+    // first: folding mx log2(e) into one rounded offset would leave that rounding error
+    // (up to 2^-25 |mx log2(e)|, about 440 at |mx| = 1e10) in every exponent, and overflow
+    // to inf for |mx| above 2.36e38.  The row max then gets exactly 2^0 at any magnitude.
     float sum = 0.0f;
 #pragma unroll
     for (int e = 0; e < U * r.W; ++e) {
-      const float p = __builtin_amdgcn_exp2f(fmaf(r.v[e], kLog2e, -off));
+      const float p = __builtin_amdgcn_exp2f((r.v[e] - mx) * kLog2e);
       r.v[e] = p;
       sum += p;
     }
@@ -228,40 +230,43 @@ __device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) 
   return r;
 }
 
-__global__ __launch_bounds__(256) void softmax_fwd_long(const float* x,
-                                                        float* y, int n) {
+__global__ __launch_bounds__(256) void softmax_fwd_long(const float* x, float* y,
+                                                        int64_t rows, int n) {
   __shared__ float red[4];
-  const int64_t row = blockIdx.x;
-  const float* xr = x + row * n;
-  float* yr = y + row * n;
-  // pass 1: online max/sum per thread, then a block-wide merge of the (max, sum) pairs
-  float m = -INFINITY, s = 0.0f;
-  for (int c = threadIdx.x; c < n; c += 256) {
-    const float v = xr[c];
-    const float mn = fmaxf(m, v);
-    s = s * expf(m - mn) + expf(v - mn);
-    m = mn;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const float* xr = x + row * n;
+    float* yr = y + row * n;
+    // pass 1: online max/sum per thread, then a block-wide merge of the (max, sum) pairs
+    float m = -INFINITY, s = 0.0f;
+    for (int c = threadIdx.x; c < n; c += 256) {
+      const float v = xr[c];
+      const float mn = fmaxf(m, v);
+      if (mn != -INFINITY) {  // masked (-inf) entries before the first finite one add nothing
+        s = s * expf(m - mn) + expf(v - mn);
+        m = mn;
+      }
+    }
+    const float gm = block_reduce(m, true, red);
+    const float part = (m == -INFINITY) ? 0.0f : s * expf(m - gm);
+    const float gs = block_reduce(part, false, red);
+    const float inv = 1.0f / gs;
+    for (int c = threadIdx.x; c < n; c += 256) yr[c] = expf(xr[c] - gm) * inv;
   }
-  const float gm = block_reduce(m, true, red);
-  const float part = (m == -INFINITY) ? 0.0f : s * expf(m - gm);
-  const float gs = block_reduce(part, false, red);
-  const float inv = 1.0f / gs;
-  for (int c = threadIdx.x; c < n; c += 256) yr[c] = expf(xr[c] - gm) * inv;
 }
 
-__global__ __launch_bounds__(256) void softmax_bwd_long(const float* p,
-                                                        const float* dp,
-                                                        float* dx, int n) {
+__global__ __launch_bounds__(256) void softmax_bwd_long(const float* p, const float* dp,
+                                                        float* dx, int64_t rows, int n) {
   __shared__ float red[4];
-  const int64_t row = blockIdx.x;
-  const float* pr = p + row * n;
-  const float* gr = dp + row * n;
-  float* xr = dx + row * n;
-  float dot = 0.0f;
-  for (int c = threadIdx.x; c < n; c += 256) dot = fmaf(pr[c], gr[c], dot);
-  dot = block_reduce(dot, false, red);
-  __syncthreads();  // every thread has read its p/dp before any in-place write lands
-  for (int c = threadIdx.x; c < n; c += 256) xr[c] = pr[c] * (gr[c] - dot);
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const float* pr = p + row * n;
+    const float* gr = dp + row * n;
+    float* xr = dx + row * n;
+    float dot = 0.0f;
+    for (int c = threadIdx.x; c < n; c += 256) dot = fmaf(pr[c], gr[c], dot);
+    dot = block_reduce(dot, false, red);
+    __syncthreads();  // every thread has read its p/dp before any in-place write lands
+    for (int c = threadIdx.x; c < n; c += 256) xr[c] = pr[c] * (gr[c] - dot);
+  }
 }
 
 // ------------------------------------------------------------------------ LayerNorm
@@ -371,46 +376,50 @@ __global__ __launch_bounds__(256) void layernorm_bwd_rows(
 // Long rows (n > 2048): one workgroup per row, three passes over the row.
 __global__ __launch_bounds__(256) void layernorm_fwd_long(
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
-    float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, int n, float eps) {
+    float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, int64_t rows,
+    int n, float eps) {
   __shared__ float red[4];
-  const int64_t row = blockIdx.x;
-  const float* xr = x + row * n;
-  float s = 0.0f;
-  for (int c = threadIdx.x; c < n; c += 256) s += xr[c];
-  const float mu = block_reduce(s, false, red) / (float)n;
-  float q = 0.0f;
-  for (int c = threadIdx.x; c < n; c += 256) {
-    const float d = xr[c] - mu;
-    q = fmaf(d, d, q);
-  }
-  const float rs = 1.0f / sqrtf(block_reduce(q, false, red) / (float)n + eps);
-  for (int c = threadIdx.x; c < n; c += 256)
-    y[row * n + c] = fmaf((xr[c] - mu) * rs, gamma[c], beta[c]);
-  if (threadIdx.x == 0) {
-    mean[row] = mu;
-    rstd[row] = rs;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const float* xr = x + row * n;
+    float s = 0.0f;
+    for (int c = threadIdx.x; c < n; c += 256) s += xr[c];
+    const float mu = block_reduce(s, false, red) / (float)n;
+    float q = 0.0f;
+    for (int c = threadIdx.x; c < n; c += 256) {
+      const float d = xr[c] - mu;
+      q = fmaf(d, d, q);
+    }
+    const float rs = 1.0f / sqrtf(block_reduce(q, false, red) / (float)n + eps);
+    for (int c = threadIdx.x; c < n; c += 256)
+      y[row * n + c] = fmaf((xr[c] - mu) * rs, gamma[c], beta[c]);
+    if (threadIdx.x == 0) {
+      mean[row] = mu;
+      rstd[row] = rs;
+    }
   }
 }
 
 __global__ __launch_bounds__(256) void layernorm_bwd_long(
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ mean,
-    const float* __restrict__ rstd, const float* __restrict__ dy, float* __restrict__ dx, int n) {
+    const float* __restrict__ rstd, const float* __restrict__ dy, float* __restrict__ dx,
+    int64_t rows, int n) {
   __shared__ float red[4];
-  const int64_t row = blockIdx.x;
-  const float mu = mean[row], rs = rstd[row];
-  float s1 = 0.0f, s2 = 0.0f;
-  for (int c = threadIdx.x; c < n; c += 256) {
-    const float xh = (x[row * n + c] - mu) * rs;
-    const float gx = dy[row * n + c] * gamma[c];
-    s1 += gx;
-    s2 = fmaf(gx, xh, s2);
-  }
-  const float m1 = block_reduce(s1, false, red) / (float)n;
-  const float m2 = block_reduce(s2, false, red) / (float)n;
-  for (int c = threadIdx.x; c < n; c += 256) {
-    const float xh = (x[row * n + c] - mu) * rs;
-    const float gx = dy[row * n + c] * gamma[c];
-    dx[row * n + c] = rs * (gx - m1 - xh * m2);
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const float mu = mean[row], rs = rstd[row];
+    float s1 = 0.0f, s2 = 0.0f;
+    for (int c = threadIdx.x; c < n; c += 256) {
+      const float xh = (x[row * n + c] - mu) * rs;
+      const float gx = dy[row * n + c] * gamma[c];
+      s1 += gx;
+      s2 = fmaf(gx, xh, s2);
+    }
+    const float m1 = block_reduce(s1, false, red) / (float)n;
+    const float m2 = block_reduce(s2, false, red) / (float)n;
+    for (int c = threadIdx.x; c < n; c += 256) {
+      const float xh = (x[row * n + c] - mu) * rs;
+      const float gx = dy[row * n + c] * gamma[c];
+      dx[row * n + c] = rs * (gx - m1 - xh * m2);
+    }
   }
 }
 
@@ -455,6 +464,11 @@ dim3 row_grid(int64_t rows) {
   return dim3((unsigned)std::min<int64_t>((rows + 3) / 4, (int64_t)1 << 20));
 }
 
+// Workgroups of the long-row kernels (one row each), at most 2^20; they stride over the rest.
+dim3 long_row_grid(int64_t rows) {
+  return dim3((unsigned)std::min<int64_t>(rows, (int64_t)1 << 20));
+}
+
 #define CTA_ROW_SWITCH(KERNEL, VEC, U, GRID, ST, ...)                                        \
   do {                                                                                      \
     if (VEC) {                                                                              \
@@ -494,7 +508,8 @@ int softmax_rows(const float* x, float* y, int64_t rows, int64_t n, hipStream_t 
     const int u = units_for((int)n, vec);
     CTA_ROW_SWITCH(softmax_fwd_rows, vec, u, row_grid(rows), st, x, y, rows, (int)n);
   } else {
-    hipLaunchKernelGGL(softmax_fwd_long, dim3((unsigned)rows), dim3(256), 0, st, x, y, (int)n);
+    hipLaunchKernelGGL(softmax_fwd_long, long_row_grid(rows), dim3(256), 0, st, x, y, rows,
+                       (int)n);
   }
   return check_launch("softmax");
 }
@@ -508,7 +523,8 @@ int softmax_bwd_rows_launch(const float* p, const float* dp, float* dx, int64_t 
     const int u = units_for((int)n, vec);
     CTA_ROW_SWITCH(softmax_bwd_rows, vec, u, row_grid(rows), st, p, dp, dx, rows, (int)n);
   } else {
-    hipLaunchKernelGGL(softmax_bwd_long, dim3((unsigned)rows), dim3(256), 0, st, p, dp, dx, (int)n);
+    hipLaunchKernelGGL(softmax_bwd_long, long_row_grid(rows), dim3(256), 0, st, p, dp, dx,
+                       rows, (int)n);
   }
   return check_launch("softmax_bwd");
 }
@@ -608,8 +624,8 @@ extern "C" int cta_layernorm_fwd(const float* x, const float* gamma, const float
     CTA_ROW_SWITCH(layernorm_fwd_rows, vec, u, row_grid(rows), st, x, gamma, beta, y, mean, rstd, rows,
                    (int)n, eps);
   } else {
-    hipLaunchKernelGGL(layernorm_fwd_long, dim3((unsigned)rows), dim3(256), 0, st, x, gamma, beta,
-                       y, mean, rstd, (int)n, eps);
+    hipLaunchKernelGGL(layernorm_fwd_long, long_row_grid(rows), dim3(256), 0, st, x, gamma,
+                       beta, y, mean, rstd, rows, (int)n, eps);
   }
   return check_launch("layernorm_fwd");
 }
@@ -644,8 +660,8 @@ extern "C" int cta_layernorm_bwd(const float* x, const float* gamma, const float
     return colsum_partials_launch(workspace, blocks, 2 * n, dgamma, dbeta, n, st,
                                   workspace + blocks * 2 * n);
   } else {
-    hipLaunchKernelGGL(layernorm_bwd_long, dim3((unsigned)rows), dim3(256), 0, st, x, gamma, mean,
-                       rstd, dy, dx, (int)n);
+    hipLaunchKernelGGL(layernorm_bwd_long, long_row_grid(rows), dim3(256), 0, st, x, gamma,
+                       mean, rstd, dy, dx, rows, (int)n);
     const int64_t chunks = (rows + kLnLongRowsPerBlock - 1) / kLnLongRowsPerBlock;
     if (chunks > 65535) return fail(CTA_ERR_INVALID_ARGUMENT, "too many rows for layernorm_bwd");
     hipLaunchKernelGGL(layernorm_colpart_long, dim3((unsigned)((n + 255) / 256), (unsigned)chunks),

@@ -18,6 +18,7 @@
 
 #include <algorithm>
 #include <array>
+#include <atomic>
 #include <cstdint>
 #include <tuple>
 
@@ -35,6 +36,15 @@ void* stream_of(const at::Tensor& t) {
 }
 
 void check_rc(int rc) { TORCH_CHECK(rc == CTA_OK, cta_last_error()); }
+
+// Which schedule the last FP32 flash_attention_bwd in this process ran: 1 stored dS, 0 recompute
+// (the allocator refused the dS workspace), -1 none yet.  Process-wide, because autograd runs
+// backward on its own device thread.  Exposed to Python as
+// cuda_transformer_amd._C.last_bwd_schedule().
+std::atomic<int>& last_bwd_schedule() {
+  static std::atomic<int> schedule{-1};
+  return schedule;
+}
 
 void check_f32(const at::Tensor& t, const char* name) {
   TORCH_CHECK(t.scalar_type() == at::kFloat, name, " must be a float32 tensor, got ",
@@ -496,8 +506,18 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd_half(
   at::Tensor delta = at::empty({B, nh, T}, Q.options().dtype(at::kFloat));
   const int64_t full = cta_flash_attention_bwd_bf16_workspace(B, nh, T, hs, causal ? 1 : 0);
   const int64_t head = cta_flash_attention_bwd_bf16_workspace(1, 1, T, hs, causal ? 1 : 0);
+  // The 16-bit backward has only the stored-dS schedule: it needs at least one head's dS tiles,
+  // even when that alone exceeds the cap (e.g. T > 2^17 non-causal), and it fails with a clear
+  // message when the allocator cannot supply them.
   const int64_t ws_bytes = std::max(head, std::min(full, kBwdWorkspaceCap));
-  at::Tensor ws = at::empty({(ws_bytes + 15) / 16 * 4}, Q.options().dtype(at::kFloat));
+  at::Tensor ws;
+  try {
+    ws = at::empty({(ws_bytes + 15) / 16 * 4}, Q.options().dtype(at::kFloat));
+  } catch (const c10::OutOfMemoryError&) {
+    TORCH_CHECK(false, "flash_attention_bwd (", Q.scalar_type(), "): cannot allocate the ",
+                ws_bytes, "-byte dS workspace (one head needs ", head,
+                " bytes at T = ", T, "); the 16-bit backward has no workspace-free schedule");
+  }
   const at::Tensor q = attn_operand_half(Q), k = attn_operand_half(K), v = attn_operand_half(V),
                    o = attn_operand_half(O), g = attn_operand_half(dO);
   const auto qs = strides_of<4>(q), ks = strides_of<4>(k), vs = strides_of<4>(v),
@@ -557,8 +577,13 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd(at::Tensor Q,
       ws = at::empty({ws_bytes / static_cast<int64_t>(sizeof(float))}, Q.options());
     } catch (const c10::OutOfMemoryError&) {
       ws_bytes = 0;
+      TORCH_WARN_ONCE(
+          "flash_attention_bwd: the dS workspace could not be allocated; running the "
+          "recompute schedule (dQ recomputes S and dP, about 20% slower, same results to "
+          "rounding)");
     }
   }
+  last_bwd_schedule().store(ws_bytes > 0 ? 1 : 0);
   check_rc(cta_flash_attention_bwd(q.data_ptr<float>(), qs.data(), k.data_ptr<float>(), ks.data(),
                                    v.data_ptr<float>(), vs.data(), o.data_ptr<float>(), os.data(),
                                    g.data_ptr<float>(), gs.data(), L.data_ptr<float>(), ls.data(),
@@ -624,9 +649,21 @@ TORCH_LIBRARY_IMPL(cuda_transformer, CUDA, m) {
 
 // Importable as cuda_transformer_amd._C (the reference imports cuda_transformer._C); importing
 // it runs the static registrations above.
+namespace {
+PyObject* py_last_bwd_schedule(PyObject*, PyObject*) {
+  const int s = cuda_transformer::last_bwd_schedule().load();
+  return PyUnicode_FromString(s == 1 ? "stored" : s == 0 ? "recompute" : "none");
+}
+PyMethodDef kMethods[] = {
+    {"last_bwd_schedule", py_last_bwd_schedule, METH_NOARGS,
+     "Backward schedule of the last FP32 flash_attention_bwd in this process: 'stored' (dK/dV "
+     "stores dS, dQ reads it), 'recompute' (the dS workspace could not be allocated) or 'none'."},
+    {nullptr, nullptr, 0, nullptr}};
+}  // namespace
+
 extern "C" PyObject* PyInit__C(void) {
   static struct PyModuleDef def = {PyModuleDef_HEAD_INIT, "_C",
                                    "gfx950 FP32 transformer kernels: torch operator library",
-                                   -1, nullptr, nullptr, nullptr, nullptr, nullptr};
+                                   -1, kMethods, nullptr, nullptr, nullptr, nullptr};
   return PyModule_Create(&def);
 }

@@ -2,10 +2,13 @@
 
 Q, K, V, dO of shape (1, 262151, 64, 128): 2,147,540,992 elements each, just past 2^31, so
 every element offset of the last heads overflows a 32-bit index.  The forward and the
-stored-dS backward (which chunks its heads under the workspace cap) run on the whole tensors
-(about 73 GB of FP32 buffers on the 288 GB MI355X); the first, middle and last heads are checked
-against the float64 oracle at the tolerances of the other FA2 tests.  Inputs are generated on
-the GPU from a fixed seed.
+stored-dS backward run on the whole tensors (about 73 GB of FP32 buffers on the 288 GB MI355X);
+the first, middle and last heads are checked against the float64 oracle at the tolerances of the
+other FA2 tests.  Inputs are generated on the GPU from a fixed seed.
+
+The FP32 dS workspace of all 262151 heads is 3.0 GiB causal and 4.0 GiB non-causal, under the
+operator's 8 GiB cap, so the backward runs in one chunk here; the head-chunked schedule is
+checked at full size by test_fa2_config3_gpu.py (N = 8192 and 16384: 4 and 16 chunks).
 """
 import numpy as np
 import pytest

@@ -187,6 +187,32 @@ def test_softmax(cuda, batch, m, n):
     assert torch.equal(xg.grad, dx)
 
 
+@pytest.mark.parametrize("n", [70, 1024, 3000])  # scalar, float4 register path, long-row path
+def test_softmax_large_magnitude_logits(cuda, n):
+    """Rows whose maximum is huge: all -1e10 (a fully masked row), a maximum of 1e10, values
+    near +-3e38, and rows that start with -inf (a mask before the first finite entry).  The
+    exponent is (x - max) log2(e), so the maximum gets exactly e^0 at any magnitude; folding
+    max log2(e) into one rounded offset would give inf or NaN on the first three."""
+    from cuda_transformer.ops import cuda_softmax
+
+    rng = np.random.default_rng(n)
+    rows = np.zeros((6, n), np.float32)
+    rows[0] = -1e10
+    rows[1] = 1e10 - rng.integers(0, 4, n).astype(np.float32) * 2048.0  # 1e10 and its neighbours
+    rows[2] = rng.choice(np.float32([3e38, 2.9e38, -3e38, 0.0]), n)
+    rows[2, 0] = 3e38
+    rows[3] = -3e38
+    rows[3, n // 2] = -2.9e38
+    rows[4] = rng.normal(0, 2, n).astype(np.float32)
+    rows[4, : n // 3] = -np.inf
+    rows[5] = rng.normal(0, 2, n).astype(np.float32) + 1e9
+    x = torch.from_numpy(rows)[None]
+    p = cuda_softmax(x.to(cuda))
+    ref = ew.softmax_forward(rows.astype(np.float64))
+    assert np.all(np.isfinite(ref))
+    np.testing.assert_allclose(f64(p)[0], ref, atol=1e-6, rtol=1e-5)
+
+
 def test_row_kernels_stride_past_the_grid_cap(cuda):
     """2^22 + 5 rows: more than the 2^20 four-row workgroups the softmax and LayerNorm-forward
     row kernels launch, so the last 5 rows come from a wave's second pass.  Rows at both ends
