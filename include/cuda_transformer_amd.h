@@ -104,6 +104,28 @@ int cta_flash_attention_bwd(const float* q, const int64_t* q_strides,
                             float* dq, float* dk, float* dv, float* delta,
                             float* workspace, int64_t workspace_bytes, void* stream);
 
+/* Largest B*nh*T that cta_flash_attention_bwd_noalloc accepts: 8,388,608 query rows, one float of
+ * delta each in a 32 MiB device array. */
+#define CTA_BWD_NOALLOC_MAX_ROWS 8388608
+
+/* Allocation-free backward: the same gradients as cta_flash_attention_bwd with workspace NULL
+ * (bitwise: the same kernels, delta then dQ recomputing S and dP then dK/dV), with no delta or
+ * workspace argument.  delta lives in a file-scope device array of the library
+ * (CTA_BWD_NOALLOC_MAX_ROWS floats, held on each GPU the library runs on until the process
+ * ends); the call allocates no memory.  B*nh*T above CTA_BWD_NOALLOC_MAX_ROWS is rejected with
+ * CTA_ERR_INVALID_ARGUMENT.  Calls that overlap on one GPU (different streams or host threads)
+ * share that array and race.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). */
+int cta_flash_attention_bwd_noalloc(const float* q, const int64_t* q_strides,
+                                    const float* k, const int64_t* k_strides,
+                                    const float* v, const int64_t* v_strides,
+                                    const float* o, const int64_t* o_strides,
+                                    const float* d_o, const int64_t* do_strides,
+                                    const float* l, const int64_t* l_strides,
+                                    int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                                    float* dq, float* dk, float* dv, void* stream);
+
 /* Bytes of BF16 dS workspace for cta_flash_attention_bwd_bf16: B*nh*ceil(T/32)^2*2 KiB, or
  * about half of that when causal.  0 for empty or unsupported shapes (hs not in {32, 64, 128}). */
 int64_t cta_flash_attention_bwd_bf16_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs,
