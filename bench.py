@@ -56,11 +56,13 @@ REFERENCE_RTX5070_MS = {"fwd": 212.73, "bwd": 1259.32}
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--workload", choices=["fa2", "fa2-sweep", "ops", "gpt", "fa2-bf16", "fa2-f16"],
+    p.add_argument("--workload", choices=["fa2", "fa2-sweep", "ops", "gpt", "gemm", "fa2-bf16",
+                                          "fa2-f16"],
                    default="fa2",
                    help="fa2: the headline step (default, one JSON line); fa2-sweep: benchmark "
                         "config 3; ops: benchmark config 4 (one JSON line per op); gpt: benchmark "
-                        "config 5 training step; fa2-bf16 / fa2-f16: the BF16 / FP16 forward and "
+                        "config 5 training step; gemm: the config-4/5 GEMMs A/B against torch's "
+                        "FP32 GEMM; fa2-bf16 / fa2-f16: the BF16 / FP16 forward and "
                         "backward at the config-2 shape, causal and full (an extension beyond "
                         "the FP32 metric)")
     p.add_argument("--steps", type=int, default=10)
@@ -106,24 +108,30 @@ def copy_calibration(mib):
     return 0
 
 
-# Bytes written between timed repetitions so that the next kernel starts with cold caches: well
-# above the 256 MB MALL (Infinity Cache) and the 8 x 4 MB of L2.
+# Bytes read between cache-cold repetitions, and the least footprint of the buffer copies that
+# rotating op timings cycle through: both well above the 256 MB MALL (Infinity Cache) and the
+# 8 x 4 MB of L2.
 FLUSH_BYTES = 1 << 30
+ROTATE_BYTES = 1 << 30
 
 
 class CacheFlush:
-    """Writes FLUSH_BYTES of device memory (one fill kernel on the current stream), evicting the
-    L2s and the MALL before the next timed launch."""
+    """Reads FLUSH_BYTES of device memory (one reduction kernel on the current stream), so the
+    L2s and the MALL hold only clean lines of this buffer when the next timed launch starts.  A
+    read, not a write: a written buffer would leave up to 256 MB of dirty lines in the MALL for
+    the timed kernel to write back (measured: +256 MB of traffic, e.g. the row softmax at 99 us
+    instead of 71 us)."""
 
     def __init__(self, dev):
         import torch
 
-        self.buf = torch.empty(FLUSH_BYTES // 4, device=dev)
-        self.n = 0
+        self.buf = torch.ones(FLUSH_BYTES // 4, device=dev)
+        self.out = torch.empty((), device=dev)
 
     def __call__(self):
-        self.n += 1
-        self.buf.fill_(float(self.n & 0xFF))
+        import torch
+
+        torch.sum(self.buf, dim=0, out=self.out)
 
 
 def host_info():
@@ -171,9 +179,9 @@ def load_traffic(kernel: str):
     path = ROOT / "profiles" / "fa2_config2_counters.md"
     if not path.exists():
         return None
-    m = re.search(rf"traffic_bytes_per_launch\[{re.escape(kernel)}\]\s*=\s*([0-9.eE+]+)",
+    m = re.search(rf"traffic_bytes_per_launch\[{re.escape(kernel)}(<[^\]]*>)?\]\s*=\s*([0-9.eE+]+)",
                   path.read_text())
-    return float(m.group(1)) if m else None
+    return float(m.group(2)) if m else None
 
 
 def cpu_port_baseline(B, H, N, D, causal, target_s):
@@ -271,12 +279,14 @@ def cpu_reference_path(B, H, N, D, causal, step_s=2.0):
 BWD_WORKSPACE_CAP = 8 << 30
 
 
-def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_reps=5):
+def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_reps=5,
+                warm_s=0.5):
     """Time `steps` FA2 steps through the C ABI on torch's current stream: fwd, then the
     backward stages of `schedule` ([delta, dkdv, dq_ds] stored; [delta, dq, dkdv] recompute;
     one combined [bwd] launch when the stored schedule needs head chunks, as the operator
-    runs it).  After the timed steps, each kernel is timed again `flushed_reps` times with
-    FLUSH_BYTES written before every launch (cold L2 and MALL).  Returns (wall ms per step,
+    runs it), after at least `warmup` untimed steps and warm_s seconds of them.  After the timed
+    steps, each kernel is timed again `flushed_reps` times with FLUSH_BYTES read before every
+    launch (cold L2 and MALL).  Returns (wall ms per step,
     {kernel: mean HIP-event ms in the timed steps}, {kernel: median flushed ms},
     (q, k, v, dO))."""
     import torch
@@ -348,8 +358,14 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_re
         if events is not None:
             events[len(kernels)].record(stream)
 
-    for _ in range(warmup):
+    # at least `warmup` steps and at least warm_s of back-to-back steps: after the host-side CPU
+    # baselines the GPU has idled and its clock must ramp up again
+    t_warm, done = time.perf_counter(), 0
+    while done < warmup or time.perf_counter() - t_warm < warm_s:
         step()
+        done += 1
+        if done % 4 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
 
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(kernels) + 1)]
@@ -379,7 +395,7 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_re
         torch.cuda.synchronize()
         flushed[kname] = statistics.median(a.elapsed_time(b) for a, b in pairs)
     del flush
-    return wall * 1e3 / steps, per_kernel, flushed, (q, k, v, do)
+    return wall * 1e3 / steps, per_kernel, flushed, (q, k, v, do), done
 
 
 def roofline_of(per_kernel, B, H, N, D, causal, flushed=None):
@@ -418,7 +434,8 @@ def fa2_sweep(args):
     B, H, D = 4, 32, 64
     for N in seqs:
         steps = max(2, args.steps // max(1, N // 2048))
-        ms, per_kernel, flushed, _ = fa2_timings(B, H, N, D, False, steps, 1, args.bwd_schedule)
+        ms, per_kernel, flushed, _, warm = fa2_timings(B, H, N, D, False, steps, args.warmup,
+                                                       args.bwd_schedule)
         fwd_fl, bwd_fl = attn_flops(B, H, N, D, False)
         bwd_ms = sum(v_ for k_, v_ in per_kernel.items() if k_ != "fwd")
         bwd_ms_f = sum(v_ for k_, v_ in flushed.items() if k_ != "fwd")
@@ -428,6 +445,7 @@ def fa2_sweep(args):
         chunks = -(-B * H // fit) if args.bwd_schedule == "stored" else 0
         line = {
             "workload": f"FA2 B{B} H{H} N{N} D{D} non-causal", "N": N, "steps": steps,
+            "warmup_steps_run": warm,
             "dtype": "f32", "bwd_schedule": args.bwd_schedule, "bwd_head_chunks": chunks,
             "ds_workspace_bytes": min(ws_full, BWD_WORKSPACE_CAP),
             "ms_per_step": round(ms, 4),
@@ -543,6 +561,40 @@ def _time_kernel(fn, reps, warm_s=0.02, flush=None):
     return statistics.median(a.elapsed_time(b) for a, b in evs)
 
 
+def _time_rotating(fn, copies, reps, warm_s=0.02):
+    """Median HIP-event duration (ms) of fn(i) over at least 20 back-to-back launches, launch i
+    on buffer copy i % copies: with copies x footprint >= ROTATE_BYTES, each launch's operands
+    were last touched copies - 1 launches earlier and have left the L2s and the MALL, and every
+    launch pays in steady state for the write-backs of the lines it dirties."""
+    import statistics
+
+    import torch
+
+    t0, i = time.perf_counter(), 0
+    while True:
+        for _ in range(2 * copies):
+            fn(i % copies)
+            i += 1
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= warm_s:
+            break
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(max(20, reps))]
+    for a, b in evs:
+        a.record(stream)
+        fn(i % copies)
+        i += 1
+        b.record(stream)
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) for a, b in evs)
+
+
+def rotation_copies(footprint_bytes):
+    """Buffer copies a rotating timing needs for footprint_bytes per launch."""
+    return max(2, -(-ROTATE_BYTES // int(footprint_bytes)))
+
+
 def _cpu_time(fn, target_s=2.0):
     """Seconds per call of a CPU function, repeated until about target_s."""
     fn()
@@ -559,11 +611,13 @@ def ops_workload(args):
     """Benchmark config 4 (GPT-2-small widths, FP32): linear GEMM fwd/bwd, db, exact and
     tanh-approximated GELU, LayerNorm and row softmax, each launched through the C ABI.  One JSON
     line per op with the kernel's roofline (MFMA TFLOP/s for GEMMs, HBM GB/s otherwise).  Each op
-    is timed cache-cold (FLUSH_BYTES written before every launch: the primary figure, "ms") and
-    back-to-back on the same buffers ("ms_unflushed"; operands under 256 MB may then be served
-    partly by the MALL).  CPU baseline: torch's own CPU kernels for the same op (the reference's
-    test oracle path: test/test_linear.py, test_gelu.py, test_softmax.py; gpt/gpt.py:47-59 for
-    LayerNorm) on 1/8 of the rows, on this host's cores."""
+    is timed cache-cold, the primary figure ("ms"): launches rotate over copies of the operands
+    totalling at least ROTATE_BYTES, so every launch reads operands that left the caches and pays
+    for its own write-backs in steady state.  Beside it, "ms_unflushed": back-to-back launches on
+    one set of buffers (operands under 256 MB may then be served partly by the MALL).  CPU
+    baseline: torch's own CPU kernels for the same op (the reference's test oracle path:
+    test/test_linear.py, test_gelu.py, test_softmax.py; gpt/gpt.py:47-59 for LayerNorm) on 1/8 of
+    the rows, on this host's cores."""
     import torch
     import torch.nn.functional as F
 
@@ -572,37 +626,57 @@ def ops_workload(args):
     lib = capi.lib()
     dev = torch.device("cuda", 0)
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    vp = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
     reps = max(20, args.steps)
     g = torch.Generator().manual_seed(0)
     cores = min(16, os.cpu_count() or 1)
     torch.set_num_threads(cores)
-    flush = CacheFlush(dev)
     host = host_info()
     aten = torch.ops.aten
 
-    def timed(fn):
-        return _time_kernel(fn, reps, flush=flush), _time_kernel(fn, reps)
+    def copies_of(*tensors):
+        """Rotation sets: the given device tensors, then clones until ROTATE_BYTES."""
+        nbytes = sum(t.numel() * t.element_size() for t in tensors if t is not None)
+        k = rotation_copies(nbytes)
+        return [tensors] + [tuple(None if t is None else t.clone() for t in tensors)
+                            for _ in range(k - 1)]
 
-    def emit(name, shape, ms_pair, amount, unit, cpu_s, cpu_amount, sample):
+    def cpu(fn):
+        return None if args.no_cpu_baseline else _cpu_time(fn, 1.0)
+
+    def timed(fn, sets):
+        return (_time_rotating(lambda i: fn(*sets[i]), len(sets), reps),
+                _time_kernel(lambda: fn(*sets[0]), reps))
+
+    def emit(name, shape, ms_pair, amount, unit, cpu_s, cpu_amount, sample, copies):
         ms, ms_warm = ms_pair
         scale, peak = (1e12, MFMA_FP32_PEAK_TFLOPS) if unit == "TFLOP/s" else (1e9, HBM_PEAK_GBPS)
         achieved, warm = amount / (ms * 1e-3) / scale, amount / (ms_warm * 1e-3) / scale
         print(json.dumps({
             "workload": name, "shape": shape, "dtype": "f32", "ms": round(ms, 5),
-            "ms_unflushed": round(ms_warm, 5), "value": round(achieved, 3), "unit": unit,
+            "ms_unflushed": round(ms_warm, 5), "rotation_copies": copies, "value": round(achieved, 3),
+            "unit": unit,
             "roofline": {"bound": "mfma" if unit == "TFLOP/s" else "hbm",
                          "achieved": round(achieved, 3), "peak": peak,
                          "frac": round(achieved / peak, 4), "algorithmic_per_launch": amount,
                          "achieved_unflushed": round(warm, 3),
                          "frac_unflushed": round(warm / peak, 4)},
-            "cpu_baseline": {"value": round(cpu_amount / cpu_s / scale, 4), "unit": unit,
-                             "cores": cores, "kind": "reference", "sample": sample,
-                             "cpu_model": host["cpu_model"]},
+            "cpu_baseline": None if cpu_s is None else {
+                "value": round(cpu_amount / cpu_s / scale, 4), "unit": unit, "cores": cores,
+                "kind": "reference", "sample": sample, "cpu_model": host["cpu_model"]},
         }), flush=True)
 
     def cpu8(what):
         return f"torch {torch.__version__} CPU {what}, FP32, rows 0..1/8, {cores} threads"
+
+    # ---- the practical HBM ceiling for a stream that reads and writes: a device-to-device copy
+    # of 256 MiB (torch's copy kernel), timed the same way as the ops below
+    src = torch.ones(1 << 26, device=dev)
+    sets = copies_of(src, torch.empty_like(src))
+    emit("device_copy (torch copy_, 256 MiB, reference ceiling)", [1 << 26],
+         timed(lambda a_, b_: b_.copy_(a_), sets), 8.0 * (1 << 26), "GB/s", None, 0.0, "",
+         len(sets))
+    del src, sets
 
     # ---- linear layer: X[8192,768] . W[768,3072] + b, X, W ~ N(0, 0.02^2)
     M, K, Nn = 8192, 768, 3072
@@ -610,10 +684,6 @@ def ops_workload(args):
     w = (torch.randn(K, Nn, generator=g) * 0.02).to(dev)
     b = (torch.randn(Nn, generator=g) * 0.02).to(dev)
     dy = (torch.randn(1, M, Nn, generator=g) * 0.02).to(dev)
-    out = torch.empty(1, M, Nn, device=dev)
-    dx = torch.empty(1, M, K, device=dev)
-    dw = torch.empty(1, K, Nn, device=dev)
-    zk, zn = torch.zeros(K, device=dev), torch.zeros(Nn, device=dev)
     xs, ws = capi.strides(x.stride()), capi.strides((0, Nn, 1))
     wts = capi.strides((0, 1, Nn))              # W^T view (1, n=3072 -> k, 768)
     dys = capi.strides(dy.stride())
@@ -621,99 +691,198 @@ def ops_workload(args):
     fl = 2.0 * M * K * Nn
     rows = M // 8
     xc, wc, bc, dyc = x[0, :rows].cpu(), w.cpu(), b.cpu(), dy[0, :rows].cpu()
+    zk, zn = torch.zeros(K, device=dev), torch.zeros(Nn, device=dev)
 
     def scratch(m_, k_, n_):
         nbytes = lib.cta_cuda_fma_workspace(1, m_, k_, n_)
         return torch.empty(max(1, nbytes // 4), device=dev) if nbytes else None
 
-    ws_f, ws_dx, ws_dw = scratch(M, K, Nn), scratch(M, Nn, K), scratch(K, M, Nn)
-    vpo = lambda t: None if t is None else vp(t)  # noqa: E731
+    def gemm_fwd(x_, w_, b_, out_, ws_):
+        assert lib.cta_cuda_fma(vp(x_), xs, vp(w_), ws, vp(b_), 1, 1, M, K, Nn, 1, vp(out_),
+                                vp(ws_), st) == 0
+    sets = copies_of(x, w, b, torch.empty(1, M, Nn, device=dev), scratch(M, K, Nn))
+    emit("linear_fwd (cuda_fma)", [M, K, Nn], timed(gemm_fwd, sets), fl, "TFLOP/s",
+         cpu(lambda: torch.addmm(bc, xc, wc)), fl / 8, cpu8("addmm"), len(sets))
 
-    def gemm_fwd():
-        assert lib.cta_cuda_fma(vp(x), xs, vp(w), ws, vp(b), 1, 1, M, K, Nn, 1, vp(out),
-                                vpo(ws_f), st) == 0
-    emit("linear_fwd (cuda_fma)", [M, K, Nn], timed(gemm_fwd), fl, "TFLOP/s",
-         _cpu_time(lambda: torch.addmm(bc, xc, wc), 1.0), fl / 8, cpu8("addmm"))
+    def gemm_dx(dy_, w_, dx_, ws_):
+        assert lib.cta_cuda_fma(vp(dy_), dys, vp(w_), wts, vp(zk), 1, 1, M, Nn, K, 1, vp(dx_),
+                                vp(ws_), st) == 0
+    sets = copies_of(dy, w, torch.empty(1, M, K, device=dev), scratch(M, Nn, K))
+    emit("linear_bwd_dx (cuda_fma, W^T view)", [M, Nn, K], timed(gemm_dx, sets), fl, "TFLOP/s",
+         cpu(lambda: dyc @ wc.T), fl / 8, cpu8("dy @ W^T"), len(sets))
 
-    def gemm_dx():
-        assert lib.cta_cuda_fma(vp(dy), dys, vp(w), wts, vp(zk), 1, 1, M, Nn, K, 1, vp(dx),
-                                vpo(ws_dx), st) == 0
-    emit("linear_bwd_dx (cuda_fma, W^T view)", [M, Nn, K], timed(gemm_dx), fl, "TFLOP/s",
-         _cpu_time(lambda: dyc @ wc.T, 1.0), fl / 8, cpu8("dy @ W^T"))
+    def gemm_dw(x_, dy_, dw_, ws_):
+        assert lib.cta_cuda_fma(vp(x_), xts, vp(dy_), dys, vp(zn), 1, 1, K, M, Nn, 1, vp(dw_),
+                                vp(ws_), st) == 0
+    sets = copies_of(x, dy, torch.empty(1, K, Nn, device=dev), scratch(K, M, Nn))
+    emit("linear_bwd_dw (cuda_fma, x^T view)", [K, M, Nn], timed(gemm_dw, sets), fl, "TFLOP/s",
+         cpu(lambda: xc.T @ dyc), fl / 8, cpu8("x^T @ dy"), len(sets))
 
-    def gemm_dw():
-        assert lib.cta_cuda_fma(vp(x), xts, vp(dy), dys, vp(zn), 1, 1, K, M, Nn, 1, vp(dw),
-                                vpo(ws_dw), st) == 0
-    emit("linear_bwd_dw (cuda_fma, x^T view)", [K, M, Nn], timed(gemm_dw), fl, "TFLOP/s",
-         _cpu_time(lambda: xc.T @ dyc, 1.0), fl / 8, cpu8("x^T @ dy"))
-
-    db = torch.empty(Nn, device=dev)
-    ws_db = torch.empty(lib.cta_db_calculation_workspace(1, M, Nn) // 4, device=dev)
-
-    def dbk():
-        assert lib.cta_db_calculation(vp(dy), dys, 1, M, Nn, vp(db), vp(ws_db), st) == 0
-    emit("db_calculation", [M, Nn], timed(dbk), 4.0 * M * Nn + 4 * Nn, "GB/s",
-         _cpu_time(lambda: dyc.sum(0), 1.0), 4.0 * rows * Nn, cpu8("dy.sum(0)"))
-    del x, w, dy, out, dx, dw
+    def dbk(dy_, db_, ws_):
+        assert lib.cta_db_calculation(vp(dy_), dys, 1, M, Nn, vp(db_), vp(ws_), st) == 0
+    sets = copies_of(dy, torch.empty(Nn, device=dev),
+                     torch.empty(lib.cta_db_calculation_workspace(1, M, Nn) // 4, device=dev))
+    emit("db_calculation", [M, Nn], timed(dbk, sets), 4.0 * M * Nn + 4 * Nn, "GB/s",
+         cpu(lambda: dyc.sum(0)), 4.0 * rows * Nn, cpu8("dy.sum(0)"), len(sets))
+    del x, w, dy, sets
 
     # ---- exact and tanh-approximated GELU on [8192, 3072]
     n = M * Nn
     xg = torch.randn(n, generator=g).to(dev)
-    yg, gg = torch.empty_like(xg), torch.randn(n, generator=g).to(dev)
+    gg = torch.randn(n, generator=g).to(dev)
     xgc, ggc = xg[: n // 8].cpu(), gg[: n // 8].cpu()
+    fsets = copies_of(xg, torch.empty_like(xg))
+    bsets = copies_of(xg, gg, torch.empty_like(xg))
     for approx, fwd_fn, bwd_fn, tag in (("none", lib.cta_gelu_fwd, lib.cta_gelu_bwd, ""),
                                         ("tanh", lib.cta_gelu_tanh_fwd, lib.cta_gelu_tanh_bwd,
                                          "_tanh")):
-        emit(f"gelu{tag}_fwd", [M, Nn], timed(lambda: fwd_fn(vp(xg), vp(yg), n, st)), 8.0 * n,
-             "GB/s", _cpu_time(lambda: F.gelu(xgc, approximate=approx), 1.0), 8.0 * n / 8,
-             cpu8(f"F.gelu(approximate={approx!r})"))
-        emit(f"gelu{tag}_bwd", [M, Nn], timed(lambda: bwd_fn(vp(xg), vp(gg), vp(yg), n, st)),
+        emit(f"gelu{tag}_fwd", [M, Nn], timed(lambda x_, y_: fwd_fn(vp(x_), vp(y_), n, st), fsets),
+             8.0 * n, "GB/s", cpu(lambda: F.gelu(xgc, approximate=approx)),
+             8.0 * n / 8, cpu8(f"F.gelu(approximate={approx!r})"), len(fsets))
+        emit(f"gelu{tag}_bwd", [M, Nn],
+             timed(lambda x_, g_, d_: bwd_fn(vp(x_), vp(g_), vp(d_), n, st), bsets),
              12.0 * n, "GB/s",
-             _cpu_time(lambda: aten.gelu_backward(ggc, xgc, approximate=approx), 1.0),
-             12.0 * n / 8, cpu8("aten.gelu_backward"))
-    del xg, yg, gg
+             cpu(lambda: aten.gelu_backward(ggc, xgc, approximate=approx)),
+             12.0 * n / 8, cpu8("aten.gelu_backward"), len(bsets))
+    del xg, gg, fsets, bsets
 
     # ---- LayerNorm over 768 on [8192, 768], gamma = 1, beta = 0
     R, C = 8192, 768
     xl = torch.randn(R, C, generator=g).to(dev)
     gam, bet = torch.ones(C, device=dev), torch.zeros(C, device=dev)
-    yl, mean, rstd = torch.empty_like(xl), torch.empty(R, device=dev), torch.empty(R, device=dev)
-    dyl, dxl = torch.randn(R, C, generator=g).to(dev), torch.empty_like(xl)
-    dgam, dbet = torch.empty(C, device=dev), torch.empty(C, device=dev)
-    ws_ln = torch.empty(lib.cta_layernorm_bwd_workspace(R, C) // 4, device=dev)
+    dyl = torch.randn(R, C, generator=g).to(dev)
     xlc, dylc = xl[: R // 8].cpu(), dyl[: R // 8].cpu()
     gamc, betc = gam.cpu(), bet.cpu()
     eps = ctypes.c_float(1e-5)
-    emit("layernorm_fwd", [R, C], timed(
-        lambda: lib.cta_layernorm_fwd(vp(xl), vp(gam), vp(bet), R, C, eps, vp(yl), vp(mean),
-                                      vp(rstd), st)),
-         8.0 * R * C + 8 * R, "GB/s",
-         _cpu_time(lambda: aten.native_layer_norm(xlc, [C], gamc, betc, 1e-5), 1.0),
-         (8.0 * R * C + 8 * R) / 8, cpu8("aten.native_layer_norm"))
+    mean, rstd = torch.empty(R, device=dev), torch.empty(R, device=dev)
+    assert lib.cta_layernorm_fwd(vp(xl), vp(gam), vp(bet), R, C, eps, vp(torch.empty_like(xl)),
+                                 vp(mean), vp(rstd), st) == 0
+
+    def ln_fwd(x_, y_, m_, r_):
+        assert lib.cta_layernorm_fwd(vp(x_), vp(gam), vp(bet), R, C, eps, vp(y_), vp(m_),
+                                     vp(r_), st) == 0
+    sets = copies_of(xl, torch.empty_like(xl), torch.empty(R, device=dev),
+                     torch.empty(R, device=dev))
+    emit("layernorm_fwd", [R, C], timed(ln_fwd, sets), 8.0 * R * C + 8 * R, "GB/s",
+         cpu(lambda: aten.native_layer_norm(xlc, [C], gamc, betc, 1e-5)),
+         (8.0 * R * C + 8 * R) / 8, cpu8("aten.native_layer_norm"), len(sets))
     _, mc, rc_ = aten.native_layer_norm(xlc, [C], gamc, betc, 1e-5)
-    emit("layernorm_bwd", [R, C], timed(
-        lambda: lib.cta_layernorm_bwd(vp(xl), vp(gam), vp(mean), vp(rstd), vp(dyl), R, C,
-                                      vp(dxl), vp(dgam), vp(dbet), vp(ws_ln), st)),
-         12.0 * R * C + 8 * R + 8 * C, "GB/s",
-         _cpu_time(lambda: aten.native_layer_norm_backward(dylc, xlc, [C], mc, rc_, gamc, betc,
-                                                           [True, True, True]), 1.0),
-         (12.0 * R * C + 8 * R) / 8, cpu8("aten.native_layer_norm_backward"))
-    del xl, yl, dyl, dxl
+
+    def ln_bwd(x_, m_, r_, dy_, dx_, dg_, db_, ws_):
+        assert lib.cta_layernorm_bwd(vp(x_), vp(gam), vp(m_), vp(r_), vp(dy_), R, C, vp(dx_),
+                                     vp(dg_), vp(db_), vp(ws_), st) == 0
+    sets = copies_of(xl, mean, rstd, dyl, torch.empty_like(xl), torch.empty(C, device=dev),
+                     torch.empty(C, device=dev),
+                     torch.empty(lib.cta_layernorm_bwd_workspace(R, C) // 4, device=dev))
+    emit("layernorm_bwd", [R, C], timed(ln_bwd, sets), 12.0 * R * C + 8 * R + 8 * C, "GB/s",
+         cpu(lambda: aten.native_layer_norm_backward(dylc, xlc, [C], mc, rc_, gamc, betc,
+                                                           [True, True, True])),
+         (12.0 * R * C + 8 * R) / 8, cpu8("aten.native_layer_norm_backward"), len(sets))
+    del xl, dyl, sets
 
     # ---- row softmax on [4*12*1024, 1024], logits ~ N(0, 4)
     R, C = 4 * 12 * 1024, 1024
     xs_ = (torch.randn(R, C, generator=g) * 2).to(dev)
-    ps_, dps, dxs = torch.empty_like(xs_), torch.rand(R, C, generator=g).to(dev), torch.empty_like(xs_)
+    dps = torch.rand(R, C, generator=g).to(dev)
     xsc, dpsc = xs_[: R // 8].cpu(), dps[: R // 8].cpu()
-    emit("softmax_fwd", [R, C], timed(lambda: lib.cta_softmax_fwd(vp(xs_), vp(ps_), R, C, st)),
-         8.0 * R * C, "GB/s", _cpu_time(lambda: F.softmax(xsc, dim=-1), 1.0), 8.0 * R * C / 8,
-         cpu8("F.softmax"))
+    sets = copies_of(xs_, torch.empty_like(xs_))
+    emit("softmax_fwd", [R, C],
+         timed(lambda x_, y_: lib.cta_softmax_fwd(vp(x_), vp(y_), R, C, st), sets),
+         8.0 * R * C, "GB/s", cpu(lambda: F.softmax(xsc, dim=-1)), 8.0 * R * C / 8,
+         cpu8("F.softmax"), len(sets))
+    ps_ = torch.empty_like(xs_)
+    assert lib.cta_softmax_fwd(vp(xs_), vp(ps_), R, C, st) == 0
+    del sets
     psc = F.softmax(xsc, dim=-1)
+    sets = copies_of(ps_, dps, torch.empty_like(xs_))
     emit("softmax_bwd", [R, C],
-         timed(lambda: lib.cta_softmax_bwd(vp(ps_), vp(dps), vp(dxs), R, C, st)),
+         timed(lambda p_, g_, d_: lib.cta_softmax_bwd(vp(p_), vp(g_), vp(d_), R, C, st), sets),
          12.0 * R * C, "GB/s",
-         _cpu_time(lambda: aten._softmax_backward_data(dpsc, psc, -1, torch.float32), 1.0),
-         12.0 * R * C / 8, cpu8("aten._softmax_backward_data"))
+         cpu(lambda: aten._softmax_backward_data(dpsc, psc, -1, torch.float32)),
+         12.0 * R * C / 8, cpu8("aten._softmax_backward_data"), len(sets))
+    return 0
+
+
+def gemm_workload(args):
+    """The FP32 GEMMs of the config-5 GPT step (6 layers, d 384, batch 64 x 256 = 16384 rows) and
+    of config 4, each timed A/B in this process against torch's own FP32 GEMM (hipBLASLt / rocBLAS
+    through torch.addmm / torch.matmul, TF32 off) on the same operands: forward x.W + b, dx =
+    dy.W^T (transposed view) and dW = x^T.dy (transposed view, split along K).  Cache-cold:
+    launches rotate over operand copies of at least ROTATE_BYTES.  One JSON line per product."""
+    import torch
+
+    from cuda_transformer_amd import capi
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    lib = capi.lib()
+    dev = torch.device("cuda", 0)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    vp = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    reps = max(20, args.steps)
+    g = torch.Generator().manual_seed(0)
+    R = 64 * 256
+    shapes = [("gpt qkv", R, 384, 1152), ("gpt proj", R, 384, 384), ("gpt fc1", R, 384, 1536),
+              ("gpt fc2", R, 1536, 384), ("gpt lm_head", R, 384, 65),
+              ("config-4 linear", 8192, 768, 3072)]
+
+    def copies_of(*tensors):
+        nbytes = sum(t.numel() * t.element_size() for t in tensors if t is not None)
+        k = rotation_copies(nbytes)
+        return [tensors] + [tuple(None if t is None else t.clone() for t in tensors)
+                            for _ in range(k - 1)]
+
+    def ws_for(m_, k_, n_):
+        nbytes = lib.cta_cuda_fma_workspace(1, m_, k_, n_)
+        return torch.empty(max(1, nbytes // 4), device=dev) if nbytes else None
+
+    for name, M, K, N in shapes:
+        x = (torch.randn(1, M, K, generator=g) * 0.02).to(dev)
+        w = (torch.randn(K, N, generator=g) * 0.02).to(dev)
+        b = (torch.randn(N, generator=g) * 0.02).to(dev)
+        dy = (torch.randn(1, M, N, generator=g) * 0.02).to(dev)
+        zk, zn = torch.zeros(K, device=dev), torch.zeros(N, device=dev)
+        s3 = capi.strides
+        products = {
+            # name: (ours(set), torch(set), operand set, m, k, n of the product)
+            "fwd": (lambda x_, w_, b_, o_, ws_: lib.cta_cuda_fma(
+                        vp(x_), s3(x_.stride()), vp(w_), s3((0, N, 1)), vp(b_), 1, 1, M, K, N, 1,
+                        vp(o_), vp(ws_), st),
+                    lambda x_, w_, b_, o_, ws_: torch.addmm(b_, x_[0], w_, out=o_[0]),
+                    (x, w, b, torch.empty(1, M, N, device=dev), ws_for(M, K, N)), M, K, N),
+            "dx": (lambda d_, w_, o_, ws_: lib.cta_cuda_fma(
+                       vp(d_), s3(d_.stride()), vp(w_), s3((0, 1, N)), vp(zk), 1, 1, M, N, K, 1,
+                       vp(o_), vp(ws_), st),
+                   lambda d_, w_, o_, ws_: torch.matmul(d_[0], w_.t(), out=o_[0]),
+                   (dy, w, torch.empty(1, M, K, device=dev), ws_for(M, N, K)), M, N, K),
+            "dW": (lambda x_, d_, o_, ws_: lib.cta_cuda_fma(
+                       vp(x_), s3((M * K, 1, K)), vp(d_), s3(d_.stride()), vp(zn), 1, 1, K, M, N, 1,
+                       vp(o_), vp(ws_), st),
+                   lambda x_, d_, o_, ws_: torch.matmul(x_[0].t(), d_[0], out=o_[0]),
+                   (x, dy, torch.empty(1, K, N, device=dev), ws_for(K, M, N)), K, M, N),
+        }
+        for pname, (ours, theirs, operands, pm, pk, pn) in products.items():
+            sets = copies_of(*operands)
+
+            def run_ours(i, ours=ours, sets=sets):
+                rc = ours(*sets[i])
+                if rc != 0:
+                    raise RuntimeError(lib.cta_last_error().decode())
+
+            t_ours = _time_rotating(run_ours, len(sets), reps)
+            t_lib = _time_rotating(lambda i, theirs=theirs, sets=sets: theirs(*sets[i]), len(sets),
+                                   reps)
+            fl = 2.0 * pm * pk * pn
+            print(json.dumps({
+                "workload": f"{name} {pname}", "m_k_n": [pm, pk, pn], "dtype": "f32",
+                "ms": round(t_ours, 5), "tflops": round(fl / t_ours / 1e9, 2),
+                "frac_of_peak": round(fl / t_ours / 1e9 / MFMA_FP32_PEAK_TFLOPS, 4),
+                "torch_ms": round(t_lib, 5), "torch_tflops": round(fl / t_lib / 1e9, 2),
+                "ours_over_torch_time": round(t_ours / t_lib, 3),
+                "splitk_workspace": operands[-1] is not None,
+            }), flush=True)
+            del sets
+        del x, w, b, dy
+        torch.cuda.empty_cache()
     return 0
 
 
@@ -811,12 +980,14 @@ def main():
         return fa2_sweep(args)
     if args.workload == "gpt":
         return gpt_workload(args)
+    if args.workload == "gemm":
+        return gemm_workload(args)
     if args.workload in ("fa2-bf16", "fa2-f16"):
         return fa2_half_workload(args, args.workload[4:])
     B, H, N, D = args.batch, args.heads, args.seq, args.head_dim
     causal = not args.non_causal
-    ms_step, per_kernel, flushed, (q, k, v, do) = fa2_timings(B, H, N, D, causal, args.steps,
-                                                              args.warmup, args.bwd_schedule)
+    ms_step, per_kernel, flushed, (q, k, v, do), warm = fa2_timings(
+        B, H, N, D, causal, args.steps, args.warmup, args.bwd_schedule)
 
     fwd_fl, bwd_fl = attn_flops(B, H, N, D, causal)
     value = (fwd_fl + bwd_fl) / (ms_step * 1e-3) / 1e12
@@ -853,6 +1024,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": warm,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -3,13 +3,15 @@
 //  * colsum_rows: per-chunk column sums of a strided (batch, m, n) tensor — the first stage of
 //    the bias gradient db[n] = sum over (batch, m) of dy (the reference reduces one column per
 //    1024-thread block with strided reads: warp_sum_kernel.cuh:13-51).  Each thread owns 4
-//    adjacent columns (dwordx4) or 1 column, walks 32 rows of its chunk with four independent
-//    accumulators, and writes one partial row.  Row pointers advance incrementally, so there is
+//    adjacent columns (dwordx4) or 1 column, walks 32 rows of its chunk eight at a time into
+//    eight independent accumulators, and writes one partial row.  Row pointers advance incrementally, so there is
 //    no division in the loop.
 //  * colsum_partials: sums a [chunks][ncols] partial matrix over its rows in a fixed order, so
-//    results are bitwise reproducible.  Given scratch, in two stages: up to 16 row groups of
-//    64-column blocks in parallel (four row phases per column, combined in LDS), then one pass
-//    over the group sums; without scratch, one workgroup per 32 columns walks every row.
+//    results are bitwise reproducible.  With float4-aligned columns, in one launch (16 row
+//    phases per float4 column group, combined in LDS).  Otherwise, given scratch, in two stages:
+//    up to 16 row groups of 64-column blocks in parallel (four row phases per column, combined
+//    in LDS), then one pass over the group sums; without scratch, one workgroup per 32 columns
+//    walks every row.
 #include "cta_common.hpp"
 #include "gemm.hpp"
 
@@ -40,34 +42,44 @@ __global__ __launch_bounds__(256) void colsum_rows_kernel(const float* __restric
       p = x + b * sb + col0 * sn;
     }
   };
-  float4 acc[4];
+  // eight rows in flight per thread, each into its own accumulator
+  float4 acc[8];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) acc[u] = zero4();
+  for (int u = 0; u < 8; ++u) acc[u] = zero4();
   auto load = [&](const float* q) -> float4 {
     if (VEC) return ld4(q);
     return make_float4(q[0], 0.f, 0.f, 0.f);
   };
   int64_t r = r0;
-  for (; r + 4 <= r1; r += 4) {
-    const float* q0 = p; advance();
-    const float* q1 = p; advance();
-    const float* q2 = p; advance();
-    const float* q3 = p; advance();
-    const float4 v0 = load(q0), v1 = load(q1), v2 = load(q2), v3 = load(q3);
-    acc[0].x += v0.x; acc[0].y += v0.y; acc[0].z += v0.z; acc[0].w += v0.w;
-    acc[1].x += v1.x; acc[1].y += v1.y; acc[1].z += v1.z; acc[1].w += v1.w;
-    acc[2].x += v2.x; acc[2].y += v2.y; acc[2].z += v2.z; acc[2].w += v2.w;
-    acc[3].x += v3.x; acc[3].y += v3.y; acc[3].z += v3.z; acc[3].w += v3.w;
+  for (; r + 8 <= r1; r += 8) {
+    const float* q[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      q[u] = p;
+      advance();
+    }
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = load(q[u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      acc[u].x += v[u].x; acc[u].y += v[u].y; acc[u].z += v[u].z; acc[u].w += v[u].w;
+    }
   }
-  for (; r < r1; ++r) {
-    const float4 v = load(p);
-    advance();
-    acc[0].x += v.x; acc[0].y += v.y; acc[0].z += v.z; acc[0].w += v.w;
+#pragma unroll
+  for (int u = 0; u < 7; ++u) {  // the last r1 - r < 8 rows; u stays a constant per copy
+    if (r + u < r1) {
+      const float4 v = load(p);
+      advance();
+      acc[u].x += v.x; acc[u].y += v.y; acc[u].z += v.z; acc[u].w += v.w;
+    }
   }
-  const float4 s = make_float4((acc[0].x + acc[1].x) + (acc[2].x + acc[3].x),
-                               (acc[0].y + acc[1].y) + (acc[2].y + acc[3].y),
-                               (acc[0].z + acc[1].z) + (acc[2].z + acc[3].z),
-                               (acc[0].w + acc[1].w) + (acc[2].w + acc[3].w));
+  auto sum8 = [&](auto get) {
+    return ((get(acc[0]) + get(acc[1])) + (get(acc[2]) + get(acc[3]))) +
+           ((get(acc[4]) + get(acc[5])) + (get(acc[6]) + get(acc[7])));
+  };
+  const float4 s = make_float4(sum8([](float4 a) { return a.x; }), sum8([](float4 a) { return a.y; }),
+                               sum8([](float4 a) { return a.z; }), sum8([](float4 a) { return a.w; }));
   float* out = part + (int64_t)blockIdx.y * N + col0;
   if (VEC) st4(out, s);
   else out[0] = s.x;
@@ -152,6 +164,50 @@ __global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restri
   }
 }
 
+// One-launch sum of a [chunks][ncols] partial matrix when ncols and the split are multiples of
+// 4 and every buffer is 16-byte aligned: a workgroup owns 16 float4 column groups, and its 16
+// row phases each add every 16th partial row in row order, 16 rows at a time with all 16 loads
+// in flight (addresses clamped to the last row, rows past it selected away, so the loads are
+// branch-free); then phase 0 adds the 16 phase sums in order.  Fixed order throughout: bitwise
+// reproducible.
+constexpr int kWideCols4 = 16;
+constexpr int kWidePhases = 16;
+constexpr int kWideBatch = 16;
+
+__global__ __launch_bounds__(kWideCols4 * kWidePhases) void colsum_wide_kernel(
+    const float* __restrict__ part, int64_t chunks, int64_t ncols, float* __restrict__ out0,
+    float* __restrict__ out1, int64_t split) {
+  __shared__ float4 red[kWidePhases][kWideCols4];
+  const int c4 = threadIdx.x % kWideCols4, ph = threadIdx.x / kWideCols4;
+  const int64_t col = ((int64_t)blockIdx.x * kWideCols4 + c4) * 4;
+  float4 acc = zero4();
+  if (col < ncols) {
+    for (int64_t base = ph; base < chunks; base += kWidePhases * kWideBatch) {
+      float4 v[kWideBatch];
+#pragma unroll
+      for (int u = 0; u < kWideBatch; ++u)
+        v[u] = ld4(part + min(base + u * kWidePhases, chunks - 1) * ncols + col);
+#pragma unroll
+      for (int u = 0; u < kWideBatch; ++u) {
+        if (base + u * kWidePhases < chunks) {
+          acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
+        }
+      }
+    }
+  }
+  red[ph][c4] = acc;
+  __syncthreads();
+  if (ph == 0 && col < ncols) {
+    float4 t = red[0][c4];
+#pragma unroll
+    for (int p = 1; p < kWidePhases; ++p) {
+      t.x += red[p][c4].x; t.y += red[p][c4].y; t.z += red[p][c4].z; t.w += red[p][c4].w;
+    }
+    if (col < split) st4(out0 + col, t);
+    else st4(out1 + (col - split), t);
+  }
+}
+
 int64_t rows_per_chunk(int64_t rows) {
   return std::max<int64_t>(kRowsPerChunk, (rows + 65534) / 65535);
 }
@@ -168,6 +224,13 @@ int64_t colsum_partials_scratch_floats(int64_t chunks, int64_t ncols) {
 
 int colsum_partials_launch(const float* part, int64_t chunks, int64_t ncols, float* out0,
                            float* out1, int64_t split, hipStream_t st, float* scratch) {
+  if (ncols % 4 == 0 && split % 4 == 0 && aligned16(part) && aligned16(out0) &&
+      aligned16(out1)) {
+    const unsigned grid = (unsigned)((ncols / 4 + kWideCols4 - 1) / kWideCols4);
+    hipLaunchKernelGGL(colsum_wide_kernel, dim3(grid), dim3(kWideCols4 * kWidePhases), 0, st,
+                       part, chunks, ncols, out0, out1, split);
+    return check_launch("column sum");
+  }
   if (scratch == nullptr) {
     const unsigned grid = (unsigned)((ncols + kTreeCols - 1) / kTreeCols);
     hipLaunchKernelGGL(colsum_tree_kernel, dim3(grid), dim3(256), 0, st, part, chunks, ncols,

@@ -115,6 +115,9 @@ def test_trace_window(tmp_path):
         w.writerow(["k", 5, 24e6, 4.8e6, 100.0, 1e6, 9e6, 0])
     win = rr.read_trace_window(d, 1, 3)
     assert win["k"]["calls"] == 3 and win["k"]["avg_ns"] == pytest.approx(2e6)
+    # two dispatches a step: step 1 is dispatches 2..3 (2, 3 ms)
+    win2 = rr.read_trace_window(d, 1, 1, {"k": 2})
+    assert win2["k"]["calls"] == 2 and win2["k"]["avg_ns"] == pytest.approx(2.5e6)
     assert win["k"]["all_calls"] == 5 and win["k"]["all_avg_ns"] == pytest.approx(4.8e6)
     (row,) = rr.build_rows(d, window=(1, 3))
     assert row.avg_ms == pytest.approx(2.0) and row.calls == 3
@@ -132,3 +135,68 @@ def test_short_name_of_mangled_kernels():
     assert short_name("_Z6foobarv") == "foobar"
     assert short_name("fa2_fwd_kernel") == "fa2_fwd_kernel"
     assert short_name("__amd_rocclr_copyBuffer") == "__amd_rocclr_copyBuffer"
+    demangled = ("void cta::(anonymous namespace)::gemm_kernel<cta::(anonymous namespace)::"
+                 "GemmTile<128, 64, 16, 2, 2>, 0, 0, 0>(cta::GemmOperand, float*)")
+    assert short_name(demangled) == "gemm_kernel<GemmTile<128, 64, 16, 2, 2>, 0, 0, 0>"
+    assert short_name("cta::(anonymous namespace)::gelu_fwd_kernel(float const*, long)") == \
+        "gelu_fwd_kernel"
+
+
+def test_theoretical_occupancy():
+    """gfx950: 512 unified VGPR+AGPR entries per lane, granule 8; 160 KiB LDS per CU; 8 slots."""
+    assert rr.theoretical_waves(256, 0, 0, 256) == (2, "vgpr")
+    assert rr.theoretical_waves(250, 0, 0, 256) == (2, "vgpr")      # 250 -> 256 allocated
+    assert rr.theoretical_waves(168, 0, 0, 256) == (3, "vgpr")
+    assert rr.theoretical_waves(128, 0, 0, 256) == (4, "vgpr")
+    assert rr.theoretical_waves(80, 48, 0, 256) == (4, "vgpr")       # 80 + 48 = 128 entries
+    assert rr.theoretical_waves(32, 0, 0, 64) == (8, "slots")
+    # 36 KiB of LDS per 4-wave workgroup: 4 workgroups per CU -> 4 waves per SIMD
+    assert rr.theoretical_waves(64, 0, 36 * 1024, 256) == (4, "lds")
+    # 64 KiB per 8-wave workgroup: 2 workgroups per CU -> 16 waves over 4 SIMDs = 4
+    assert rr.theoretical_waves(40, 0, 64 * 1024, 512) == (4, "lds")
+
+
+def test_wave_states_and_achieved_occupancy(tmp_path):
+    xcds, simds, cycles = 8, 1024, 1.0e6               # cycles per XCD
+    wave_quads = 2.5 * cycles * simds / 4              # 2.5 waves resident per SIMD on average
+    rows = [("k", "GRBM_GUI_ACTIVE", cycles * xcds), ("k", "SQ_WAVE_CYCLES", wave_quads),
+            ("k", "SQ_ACTIVE_INST_ANY", 0.4 * wave_quads), ("k", "SQ_WAIT_ANY", 0.3 * wave_quads),
+            ("k", "SQ_WAIT_INST_ANY", 0.2 * wave_quads), ("k", "SQ_ACTIVE_INST_VALU", 0.25 * wave_quads),
+            ("k", "SQ_INSTS_VALU_MFMA_MOPS_BF16", 10.0), ("k", "SQ_INSTS_VALU_MFMA_MOPS_F32", 1.0)]
+    d = _pmc(tmp_path / "ws", "w", rows)
+    (r,) = rr.build_rows(None, [d], None, rr.read_agent(d))
+    assert r.waves_achieved == pytest.approx(2.5)
+    assert r.wave_states["issue"] == pytest.approx(0.4)
+    assert r.wave_states["dep_wait"] == pytest.approx(0.3)
+    assert r.wave_states["issue_wait"] == pytest.approx(0.2)
+    assert r.wave_states["valu"] == pytest.approx(0.25)
+    assert "lds" not in r.wave_states
+    assert r.mfma_flop == pytest.approx(11.0 * 512)
+    # registers from the dispatch (VGPR_Count 128 = 256 allocated, LDS 4096 B, 256 threads)
+    assert (r.info["vgpr"], r.info["agpr"], r.info["sgpr"]) == (256, 0, 32)
+    assert (r.waves_theory, r.waves_limit) == (2, "vgpr")
+    text = rr.render([r], "T", agent=rr.read_agent(d))
+    assert "| k | 256 | 0 | 32 | 2 (vgpr) | 2.50 | 40.0% | 30.0% | 20.0% | - | 25.0% |" in text
+    assert "waves_per_simd_achieved[k] = 2.500" in text and "wave_state_dep_wait[k] = 0.3000" in text
+
+
+def test_registers_from_kernel_trace(tmp_path):
+    d = tmp_path / "kt"
+    d.mkdir()
+    cols = ["Kind", "Agent_Id", "Queue_Id", "Stream_Id", "Thread_Id", "Dispatch_Id", "Kernel_Id",
+            "Kernel_Name", "Correlation_Id", "Start_Timestamp", "End_Timestamp", "LDS_Block_Size",
+            "Scratch_Size", "VGPR_Count", "Accum_VGPR_Count", "SGPR_Count", "Workgroup_Size_X",
+            "Workgroup_Size_Y", "Workgroup_Size_Z", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z"]
+    with open(d / "x_kernel_trace.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(cols)
+        w.writerow(["KERNEL_DISPATCH", "Agent 1", 1, 0, 1, 1, 3, "kern", 1, 0, 2_000_000, 36864,
+                    20, 128, 0, 96, 256, 1, 1, 4096, 1, 1])
+    with open(d / "x_kernel_stats.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs",
+                    "MaxNs", "StdDev"])
+        w.writerow(["kern", 1, 2e6, 2e6, 100.0, 2e6, 2e6, 0])
+    (r,) = rr.build_rows(d)
+    assert r.info["vgpr"] == 256 and r.info["scratch"] == 20 and r.info["workgroup"] == 256
+    assert (r.waves_theory, r.waves_limit) == (2, "vgpr")
