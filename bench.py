@@ -80,9 +80,10 @@ def parse_args():
     p.add_argument("--gpt-mlp", choices=["fused", "reference"], default="fused",
                    help="gpt workload: fused: CudaMLP (GELU in the GEMM epilogues, the model's "
                         "default); reference: CudaLinearLayer -> CudaGeluLayer -> CudaLinearLayer")
-    p.add_argument("--bwd-schedule", choices=["stored", "recompute"], default="stored",
+    p.add_argument("--bwd-schedule", choices=["stored", "recompute", "fold"], default="stored",
                    help="stored: dK/dV writes dS and dQ reads it (what the operator runs); "
-                        "recompute: the reference's delta / dQ / dK/dV schedule")
+                        "recompute: the reference's delta / dQ / dK/dV schedule; fold: the stored "
+                        "schedule with delta computed inside the dK/dV stage (no delta launch)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="target CPU time of the bounded CPU-baseline sample")
@@ -302,7 +303,7 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_re
     dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
     delta = torch.empty(B, H, N, device=dev)
     ws_full = capi.lib().cta_flash_attention_bwd_workspace(B, H, N, D, int(causal))
-    ws_bytes = min(ws_full, BWD_WORKSPACE_CAP) if schedule == "stored" else 0
+    ws_bytes = min(ws_full, BWD_WORKSPACE_CAP) if schedule in ("stored", "fold") else 0
     ws = torch.empty(max(1, ws_bytes // 4), device=dev)
 
     stream = torch.cuda.current_stream(dev)
@@ -336,6 +337,10 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_re
         elif kernel == "dq_ds":
             rc = lib.cta_flash_attention_bwd_dq_from_ds(P["k"], s4, P["ws"], B, H, N, D, c,
                                                         P["dq"], st)
+        elif kernel == "bwd_fold":  # dK/dV with delta folded in, then dQ from dS
+            rc = lib.cta_flash_attention_bwd_fold_delta(
+                P["q"], s4, P["k"], s4, P["v"], s4, P["O"], s4, P["do"], s4, P["L"], s3, B, H, N,
+                D, c, P["dq"], P["dk"], P["dv"], P["ws"], ws_bytes, st)
         else:  # "bwd": the combined entry point, chunked over heads
             rc = lib.cta_flash_attention_bwd(P["q"], s4, P["k"], s4, P["v"], s4, P["O"], s4,
                                              P["do"], s4, P["L"], s3, B, H, N, D, c, P["dq"],
@@ -345,6 +350,8 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_re
 
     if schedule == "recompute":
         kernels = ["fwd", "delta", "dq", "dkdv"]
+    elif schedule == "fold":
+        kernels = ["fwd", "bwd_fold"]
     elif ws_full <= ws_bytes:
         kernels = ["fwd", "delta", "dkdv", "dq_ds"]
     else:
@@ -399,13 +406,13 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_re
 
 
 def roofline_of(per_kernel, B, H, N, D, causal, flushed=None):
-    """Roofline object of the dominant kernel among `per_kernel` (the combined chunked "bwd"
-    launch is not a single kernel and is left out): its algorithmic work per launch over its
-    mean duration, against the FP32 MFMA or HBM peak."""
+    """Roofline object of the dominant kernel among `per_kernel` (the combined "bwd" and
+    "bwd_fold" launches are not single kernels and are left out): its algorithmic work per
+    launch over its mean duration, against the FP32 MFMA or HBM peak."""
     kernel_symbols = {"fwd": "fa2_fwd_kernel", "delta": "fa2_bwd_delta_kernel",
                       "dq": "fa2_bwd_dq_kernel", "dkdv": "fa2_bwd_dkdv_kernel",
                       "dq_ds": "fa2_bwd_dq_ds_kernel"}
-    dom = max((k_ for k_ in per_kernel if k_ != "bwd"), key=per_kernel.get)
+    dom = max((k_ for k_ in per_kernel if k_ in kernel_symbols), key=per_kernel.get)
     amount, unit, bound = kernel_algorithmic(dom, B, H, N, D, causal)
     scale, peak = (1e12, MFMA_FP32_PEAK_TFLOPS) if unit == "TFLOP/s" else (1e9, HBM_PEAK_GBPS)
     achieved = amount / (per_kernel[dom] * 1e-3) / scale

@@ -57,6 +57,9 @@ SIGNATURES = {
                                                      _i64, _int, _p, _p, _p, _p]),
     "cta_flash_attention_bwd_dq_from_ds": (_int, [_p, _i64p, _p, _i64, _i64, _i64, _i64, _int,
                                                   _p, _p]),
+    "cta_flash_attention_bwd_fold_delta": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
+                                                  _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64,
+                                                  _int, _p, _p, _p, _p, _i64, _p]),
     "cta_cuda_fma_workspace": (_i64, [_i64, _i64, _i64, _i64]),
     "cta_cuda_fma": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p,
                             _p, _p]),

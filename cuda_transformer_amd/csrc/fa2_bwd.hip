@@ -267,21 +267,28 @@ constexpr int kDsPitch = 40;  // LDS pitch of the per-wave transpose: halves 4 r
 // to dsw (heads indexed from bh_base).  A dS tile goes to a per-wave LDS transpose buffer when
 // it is formed and out to HBM at the start of the next stage, so its stores drain behind a
 // stage of MFMAs rather than in front of the stage's vmcnt wait.
-template <int HS, bool CAUSAL, bool STORE_DS>
+//
+// FOLD: delta is not read from a delta stage's output but computed here, per query stage, from
+// the stage's dO tile and an O tile streamed beside it (delta_i = O_i . dO_i, the reference's
+// flash_attention_bwd_delta, flash_attention.cuh:175-213, folded in).  Every key tile of a head
+// recomputes it, and the stage needs a second barrier before delta is read.
+template <int HS, bool CAUSAL, bool STORE_DS, bool FOLD>
 __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
-    float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ dsw, int nh, int T,
-    int bh_base, int BH, int n_ktiles, RowStrides sq, RowStrides sk, RowStrides sv,
-    RowStrides sdo, LStrides sl, float scale, float scale_log2) {
+    const float* __restrict__ dO, const float* __restrict__ O, const float* __restrict__ Lg,
+    const float* __restrict__ delta, float* __restrict__ dK, float* __restrict__ dV,
+    float* __restrict__ dsw, int nh, int T, int bh_base, int BH, int n_ktiles, RowStrides sq,
+    RowStrides sk, RowStrides sv, RowStrides sdo, RowStrides so, LStrides sl, float scale,
+    float scale_log2) {
   constexpr int BN = DkdvTile<HS>::BN;
   constexpr int NSUB = BN / 32;
   constexpr int BM = 128;
   constexpr int H2 = HS / 2;
   constexpr int KP = HS + 4;                // LDS pitch of a Q / dO row
   constexpr int TILE = BN * KP;
-  constexpr int PIECES = (2 * TILE + 255) / 256;  // 1 KiB async copies covering Q and dO
-  constexpr int QG = PIECES * 256;          // Q tile, dO tile, tail of the last piece
+  constexpr int NT = FOLD ? 3 : 2;          // tiles per stage: Q, dO (and O when folding delta)
+  constexpr int PIECES = (NT * TILE + 255) / 256;  // 1 KiB async copies covering the tiles
+  constexpr int QG = PIECES * 256;          // the tiles and the tail of the last piece
   constexpr int RVEC = 64;                  // L and delta of a stage, padded to one wave
   constexpr int STAGE = QG + 2 * RVEC;
   constexpr int PER_WAVE = (PIECES + 3) / 4;
@@ -303,8 +310,9 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
 
   const float* Qb = Q + b * sq.b + h * sq.h;
   const float* dOb = dO + b * sdo.b + h * sdo.h;
+  const float* Ob = FOLD ? O + b * so.b + h * so.h : nullptr;
   const float* Lb = Lg + b * sl.b + h * sl.h;
-  const float* Db = delta + (int64_t)bh * T;
+  const float* Db = FOLD ? nullptr : delta + (int64_t)bh * T;
   const int nb = (T + 31) / 32;
   float* xpose = smem + 2 * STAGE + wave * NSUB * 32 * kDsPitch;  // this wave's dS buffers
   float* dsh = STORE_DS ? dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileFloats
@@ -350,20 +358,43 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
       const int pc = wave + 4 * u;
       if (pc < PIECES) {
         const int f = pc * 256 + lane * 4;  // float offset this lane fills
-        const int which = f / TILE;         // 0: Q, 1: dO, 2: tail
+        const int which = f / TILE;         // 0: Q, 1: dO, 2: O (FOLD), else tail
         const int rem = f - which * TILE;
         const int r = rem / KP, c = rem - r * KP;
         const int64_t i = min(r0 + r, T - 1);
-        const float* src = which == 0 ? Qb + i * sq.t : dOb + i * sdo.t;
+        const float* src = which == 0 ? Qb + i * sq.t
+                         : (FOLD && which == 2) ? Ob + i * so.t : dOb + i * sdo.t;
         // pad words and the tail take the row's first chunk: in bounds and never read
-        async_copy16(which < 2 && c < HS ? src + c : Qb + i * sq.t, qs + pc * 256);
+        async_copy16(which < NT && c < HS ? src + c : Qb + i * sq.t, qs + pc * 256);
       }
     }
     if (wave == 0) {  // lanes past BN fill the padding
       const int64_t i = min(r0 + lane, T - 1);
       async_copy4(Lb + i * sl.t, qs + QG);
-      async_copy4(Db + i, qs + QG + RVEC);
+      if (!FOLD) async_copy4(Db + i, qs + QG + RVEC);
     }
+  };
+  // FOLD: delta of the stage in buffer `st` from its O and dO tiles, 256 / BN lanes per row,
+  // into the stage's delta slot.  Rows past T hold row T - 1 (their P is masked to 0).
+  auto fold_delta = [&](float* st) {
+    constexpr int LPR = 256 / BN;   // lanes per row (consecutive lanes of one wave)
+    constexpr int DPL = HS / LPR;   // d values per lane
+    static_assert(256 % BN == 0 && DPL % 4 == 0, "delta split");
+    const int r = tid / LPR, seg = tid % LPR;
+    const float* orow = st + 2 * TILE + r * KP + seg * DPL;
+    const float* grow = st + TILE + r * KP + seg * DPL;
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < DPL / 4; ++c) {
+      const float4 o4 = ld4(orow + 4 * c), g4 = ld4(grow + 4 * c);
+      acc = fmaf(o4.x, g4.x, acc);
+      acc = fmaf(o4.y, g4.y, acc);
+      acc = fmaf(o4.z, g4.z, acc);
+      acc = fmaf(o4.w, g4.w, acc);
+    }
+#pragma unroll
+    for (int off = LPR / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+    if (seg == 0) st[QG + RVEC + r] = acc;
   };
   // Tiles whose every query row precedes every key row are skipped (dS = 0, nothing stored).
   auto live = [&](int ii0) { return ii0 < T && !(CAUSAL && ii0 + 31 < j0); };
@@ -400,6 +431,10 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
     const int buf = i & 1;
     if (i + 1 < n_steps) issue(stage_at(i + 1), buf ^ 1);
     if (wave_stores && i > 0) flush(stage_at(i - 1));
+    if (FOLD) {
+      fold_delta(smem + buf * STAGE);
+      __syncthreads();
+    }
     const float* qs = smem + buf * STAGE;
     const float* gs = qs + TILE;
     const float* ls = qs + QG;
@@ -679,17 +714,19 @@ void launch_dq(const float* q, const float* k, const float* v, const float* d_o,
                      scale, scale * kLog2e);
 }
 
-// dK/dV for heads [bh_base, bh_base + n_heads); with STORE_DS the dS tiles go to dsw.
-template <int HS, bool CAUSAL, bool STORE_DS>
+// dK/dV for heads [bh_base, bh_base + n_heads); with STORE_DS the dS tiles go to dsw; with
+// FOLD delta comes from O (strides so) instead of the delta array.
+template <int HS, bool CAUSAL, bool STORE_DS, bool FOLD = false>
 void launch_dkdv(const float* q, const float* k, const float* v, const float* d_o,
                  const float* l, const float* delta, float* dk, float* dv, float* dsw, int nh,
                  int T, int bh_base, int n_heads, RowStrides sq, RowStrides sk, RowStrides sv,
-                 RowStrides sdo, LStrides sl, float scale, hipStream_t st) {
+                 RowStrides sdo, LStrides sl, float scale, hipStream_t st,
+                 const float* o = nullptr, RowStrides so = {}) {
   const int n_ktiles = (T + 127) / 128;
   const int64_t items = (int64_t)(CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles) * n_heads;
-  hipLaunchKernelGGL((fa2_bwd_dkdv_kernel<HS, CAUSAL, STORE_DS>), dim3(xcd_grid(items)),
-                     dim3(256), 0, st, q, k, v, d_o, l, delta, dk, dv, dsw, nh, T, bh_base,
-                     n_heads, n_ktiles, sq, sk, sv, sdo, sl, scale, scale * kLog2e);
+  hipLaunchKernelGGL((fa2_bwd_dkdv_kernel<HS, CAUSAL, STORE_DS, FOLD>), dim3(xcd_grid(items)),
+                     dim3(256), 0, st, q, k, v, d_o, o, l, delta, dk, dv, dsw, nh, T, bh_base,
+                     n_heads, n_ktiles, sq, sk, sv, sdo, so, sl, scale, scale * kLog2e);
 }
 
 template <int HS, bool CAUSAL>
@@ -903,6 +940,49 @@ extern "C" int cta_flash_attention_bwd(const float* q, const int64_t* q_strides,
       launch_dq_ds<HS, C>(k, workspace, dq, (int)nh, (int)T, h0, n, rs(k_strides), scale, st);
     });
     if (int rc = check_launch("flash_attention_bwd")) return rc;
+  }
+  return CTA_OK;
+}
+
+extern "C" int cta_flash_attention_bwd_fold_delta(
+    const float* q, const int64_t* q_strides, const float* k, const int64_t* k_strides,
+    const float* v, const int64_t* v_strides, const float* o, const int64_t* o_strides,
+    const float* d_o, const int64_t* do_strides, const float* l, const int64_t* l_strides,
+    int64_t B, int64_t nh, int64_t T, int64_t hs, int causal, float* dq, float* dk, float* dv,
+    float* workspace, int64_t workspace_bytes, void* stream) {
+  if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
+  if (B * nh * T == 0) return CTA_OK;
+  if (!attn_layout_ok(q, q_strides) || !attn_layout_ok(k, k_strides) ||
+      !attn_layout_ok(v, v_strides) || !attn_layout_ok(o, o_strides) ||
+      !attn_layout_ok(d_o, do_strides))
+    return fail(CTA_ERR_LAYOUT,
+                "flash_attention_bwd needs unit d-stride, strides divisible by 4 and 16-byte "
+                "aligned Q/K/V/O/dO");
+  if (!l_ok(l, l_strides)) return fail(CTA_ERR_INVALID_ARGUMENT, "null L pointer");
+  const int64_t head_bytes = cta_flash_attention_bwd_workspace(1, 1, T, hs, causal);
+  if (workspace == nullptr || workspace_bytes < head_bytes)
+    return fail(CTA_ERR_INVALID_ARGUMENT,
+                "flash_attention_bwd_fold_delta needs a dS workspace of at least one head (" +
+                    std::to_string(head_bytes) + " bytes)");
+  if (!dq || !dk || !dv || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
+      !aligned16(workspace))
+    return fail(CTA_ERR_LAYOUT, "dQ/dK/dV and the workspace must be 16-byte aligned pointers");
+  const int BH = (int)(B * nh);
+  const int64_t fit = std::min<int64_t>(BH, workspace_bytes / head_bytes);
+  const int64_t n_chunks = (BH + fit - 1) / fit;
+  const int chunk = (int)((BH + n_chunks - 1) / n_chunks);
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
+  hipStream_t st = as_stream(stream);
+  for (int h0 = 0; h0 < BH; h0 += chunk) {
+    const int n = std::min(chunk, BH - h0);
+    dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
+      launch_dkdv<HS, C, true, true>(q, k, v, d_o, l, nullptr, dk, dv, workspace, (int)nh,
+                                     (int)T, h0, n, rs(q_strides), rs(k_strides), rs(v_strides),
+                                     rs(do_strides), sl, scale, st, o, rs(o_strides));
+      launch_dq_ds<HS, C>(k, workspace, dq, (int)nh, (int)T, h0, n, rs(k_strides), scale, st);
+    });
+    if (int rc = check_launch("flash_attention_bwd_fold_delta")) return rc;
   }
   return CTA_OK;
 }

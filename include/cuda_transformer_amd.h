@@ -212,6 +212,25 @@ int cta_flash_attention_bwd_dq_from_ds(const float* k, const int64_t* k_strides,
                                        int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
                                        float* dq, void* stream);
 
+/* Backward with delta folded into the dK/dV stage: no delta launch and no delta scratch.  Each
+ * dK/dV workgroup computes delta_i = O_i . dO_i for every query stage it visits from an O tile
+ * streamed beside dO, stores dS, and dQ is computed from the stored tiles as in
+ * cta_flash_attention_bwd (chunked over heads to fit workspace_bytes, which must hold at least
+ * one head's share of cta_flash_attention_bwd_workspace(), else CTA_ERR_INVALID_ARGUMENT).
+ * Same results to rounding (delta is summed in another order).  Folds the reference's
+ * flash_attention_bwd_delta launch (flash_attn_launcher.cu:107-108, flash_attention.cuh:175-213)
+ * into its flash_attention_bwd_dk_dv launch (flash_attn_launcher.cu:114,121,131); measured
+ * slower than the separate delta launch, so cta_flash_attention_bwd does not use it. */
+int cta_flash_attention_bwd_fold_delta(const float* q, const int64_t* q_strides,
+                                       const float* k, const int64_t* k_strides,
+                                       const float* v, const int64_t* v_strides,
+                                       const float* o, const int64_t* o_strides,
+                                       const float* d_o, const int64_t* do_strides,
+                                       const float* l, const int64_t* l_strides,
+                                       int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                                       float* dq, float* dk, float* dv, float* workspace,
+                                       int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------------
  * Linear layer.
  * ---------------------------------------------------------------------------- */

@@ -239,3 +239,37 @@ def test_fa2_config2_full_size(cuda):
     assert sum_dk.abs().max().item() <= 1e-3 * dk.double().abs().sum(dim=2).max().item()
     torch.testing.assert_close(dv.double().sum(dim=2), do.double().sum(dim=2), rtol=1e-6,
                                atol=1e-2)
+
+
+@pytest.mark.parametrize("B,nh,T,hs,causal", [s for s in REF_SHAPES if s[2] > 1] + [(1, 2, 600, 64, False)])
+def test_fa2_bwd_fold_delta(cuda, B, nh, T, hs, causal):
+    """The backward with delta folded into the dK/dV stage (cta_flash_attention_bwd_fold_delta)
+    against the float64 oracle, and against the stored-dS schedule of the operator (the same
+    kernels apart from how delta is summed): allclose at 1e-5.  Run with a one-head workspace as
+    well, so the head-chunked loop is exercised."""
+    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+    from cuda_transformer_amd import capi
+
+    q, k, v, do = (t.to(cuda) for t in _inputs(B, nh, T, hs, seed=700 + T + hs))
+    O, L = flash_attention_fwd(q, k, v, causal)
+    ref = flash_attention_bwd(q, k, v, O, do, L, causal)
+    s4, s3 = capi.strides(q.stride()), capi.strides(L.stride())
+    st = torch.cuda.current_stream().cuda_stream
+    full = capi.call("cta_flash_attention_bwd_workspace", B, nh, T, hs, int(causal))
+    head = capi.call("cta_flash_attention_bwd_workspace", 1, 1, T, hs, int(causal))
+    ws = torch.empty(full // 4 + 4, device=cuda)
+    refs = ora.fa2_backward(f64(q), f64(k), f64(v), f64(O), f64(do), f64(L), causal, br=64, bc=64)
+    for nbytes in (full, head):
+        out = [torch.full_like(q, float("nan")) for _ in range(3)]
+        capi.call("cta_flash_attention_bwd_fold_delta", q.data_ptr(), s4, k.data_ptr(), s4,
+                  v.data_ptr(), s4, O.data_ptr(), s4, do.data_ptr(), s4, L.data_ptr(), s3, B, nh,
+                  T, hs, int(causal), *(t.data_ptr() for t in out), ws.data_ptr(), nbytes, st)
+        torch.cuda.synchronize()
+        for got, r_op, r_or in zip(out, ref, refs):
+            torch.testing.assert_close(got, r_op, rtol=1e-5, atol=1e-5)
+            np.testing.assert_allclose(f64(got), r_or, rtol=1e-5, atol=1e-4)
+            assert_rel_err(f64(got), r_or, 1e-3)
+    with pytest.raises(capi.CtaError, match="needs a dS workspace"):
+        capi.call("cta_flash_attention_bwd_fold_delta", q.data_ptr(), s4, k.data_ptr(), s4,
+                  v.data_ptr(), s4, O.data_ptr(), s4, do.data_ptr(), s4, L.data_ptr(), s3, B, nh,
+                  T, hs, int(causal), *(t.data_ptr() for t in out), ws.data_ptr(), head - 1, st)
