@@ -64,35 +64,49 @@ __global__ __launch_bounds__(256) void fa2_bwd_delta_half_kernel(const E* __rest
 }
 
 // ------------------------------------------------------------------------------------
-// dK, dV and the stored dS tiles.  Workgroup = 128 key rows (4 waves x 32); query stages of 32
-// rows, global -> registers -> LDS, double buffered, one barrier per stage.  Heads
-// [bh_base, bh_base + BH); the dS tiles go to dsw, heads indexed from bh_base.
-// Waves per SIMD: the non-causal hs = 64 kernel is held to 168 VGPRs for a third wave (a few
-// spilled bytes; measured 3.6% faster); the causal one would spill 112 bytes and run 17% slower.
-template <class E, int HS, bool CAUSAL>
-__global__ __launch_bounds__(256, HS == 128 ? 1 : (HS == 64 && CAUSAL ? 2 : 3)) void fa2_bwd_dkdv_half_kernel(
+// dK, dV and the stored dS tiles.  Workgroup = WAVES x 32 key rows; query stages of BN rows
+// (BN / 32 sub-tiles of 32, taken in the stage walk's direction), global -> registers -> LDS,
+// double buffered, one barrier per stage.  Heads [bh_base, bh_base + BH); the dS tiles go to
+// dsw, heads indexed from bh_base.  MINW: waves per SIMD the register budget is held to.
+// hs = 32 and 64: eight waves (256 key rows) share each 64-row query stage, one workgroup per
+// CU (115 KB of LDS at hs = 64), two waves per SIMD.  A stage then holds 1024 cycles of MFMA
+// work per wave instead of 512, which hides the latency of the next stage's loads (the 4-wave,
+// 32-row kernel waited on them: 57% of its wave-cycles were dependency waits), and every
+// staged Q / dO row serves twice the keys.  Measured against four waves and 32-row stages
+// (bitwise-identical gradients at T = 4096): causal backward 1.56-1.58 vs 1.70-1.71 ms, non-
+// causal equal at config 2 and 4.5% faster at B1 H16 N8192.  Eight waves with 32-row stages
+// were 10% slower.  hs = 128 keeps four waves, one per SIMD.
+template <int HS, bool CAUSAL>
+struct DkdvHalfCfg {
+  static constexpr int WAVES = HS == 128 ? 4 : 8, BN = HS == 128 ? 32 : 64;
+  static constexpr int MINW = HS == 128 ? 1 : 2;
+};
+
+template <class E, int HS, bool CAUSAL, int WAVES, int BN, int MINW>
+__global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
     const E* __restrict__ Q, const E* __restrict__ K, const E* __restrict__ V,
     const E* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
     E* __restrict__ dK, E* __restrict__ dV, E* __restrict__ dsw, int nh, int T,
     int bh_base, int BH, int n_ktiles, RowStridesH sq, RowStridesH sk, RowStridesH sv,
     RowStridesH sdo, RowStridesH sl, float scale, float scale_log2) {
-  constexpr int BN = 32;             // query rows per stage
-  constexpr int BM = 128;            // key rows per workgroup
+  constexpr int THREADS = 64 * WAVES;
+  constexpr int NSUB = BN / 32;      // 32-row sub-tiles per query stage
+  constexpr int BM = 32 * WAVES;     // key rows per workgroup
   constexpr int RP = HS + 8;         // 16-bit pitch of a row image: conflict-free 16-byte reads
   constexpr int TP = BN + 8;         // 16-bit pitch of a transposed image row (one d)
   constexpr int XP = 32 + 8;         // 16-bit pitch of the dS transpose
   constexpr int CH = HS / 8;         // 16-byte chunks per row
   constexpr int PAIRS = BN / 2 * CH; // row-pair load tasks per tensor and stage
-  constexpr int LOADS = (2 * PAIRS + 255) / 256;  // load tasks per thread
+  constexpr int LOADS = (2 * PAIRS + THREADS - 1) / THREADS;  // load tasks per thread
   constexpr int QS = HS / 16;        // MFMA steps over d
   // Stage image, in bytes: Q rows, dO rows, Q^T, dO^T, L log2(e), -delta.
   constexpr int B_ROWS = BN * RP * 2, B_TRS = HS * TP * 2;
   constexpr int OFF_GR = B_ROWS, OFF_QT = 2 * B_ROWS, OFF_GT = 2 * B_ROWS + B_TRS;
   constexpr int OFF_L = 2 * B_ROWS + 2 * B_TRS, OFF_D = OFF_L + BN * 4;
   constexpr int STAGE = OFF_D + BN * 4;
-  constexpr int XPOSE = 32 * XP * 2;  // per wave
+  constexpr int XPOSE = NSUB * 32 * XP * 2;  // per wave: one transpose buffer per sub-tile
   static_assert(STAGE % 16 == 0 && OFF_QT % 16 == 0 && OFF_L % 16 == 0, "16-byte aligned images");
-  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * STAGE + 4 * XPOSE];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * STAGE + WAVES * XPOSE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
@@ -151,15 +165,17 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : (HS == 64 && CAUSAL ? 2 : 3)) 
   // multiple of 64, so the tensor is the same for a whole wave.
   // Rows past T (ragged last stage) are read clamped to row T - 1: their L and -delta are 0 and
   // the mask sets their P to 0, so dS = 0 there and they add nothing to dK, dV or dQ.
-  // hs = 32 has 128 tasks for 256 threads: waves 0 and 1 take them (wave-uniform).
+  // With fewer tasks than threads the first waves take them (wave-uniform).
   static_assert(PAIRS % 64 == 0, "load tensor must be wave-uniform");
-  auto task_live = [&](int u) { return 2 * PAIRS % 256 == 0 || tid + 256 * u < 2 * PAIRS; };
+  auto task_live = [&](int u) {
+    return 2 * PAIRS % THREADS == 0 || tid + THREADS * u < 2 * PAIRS;
+  };
   uint4 st2[LOADS][2];
   float lst = 0.0f, dst = 0.0f;  // L and delta of one query row
-  // Sixteen consecutive lanes take the 16 row pairs of one chunk, so a transposed store
-  // instruction spreads over 32 pair positions x 2 chunk parities (2-way at worst).
+  // BN / 2 consecutive lanes take the row pairs of one chunk, so a transposed store
+  // instruction spreads over the pair positions of one or two chunks.
   auto task_of = [&](int u, int& tensor, int& rp, int& ch) {
-    const int c = tid + 256 * u;
+    const int c = tid + THREADS * u;
     tensor = __builtin_amdgcn_readfirstlane(c / PAIRS);
     const int rem = c - tensor * PAIRS;
     rp = rem % (BN / 2);
@@ -234,17 +250,21 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : (HS == 64 && CAUSAL ? 2 : 3)) 
 
   // Tiles whose every query row precedes every key row are skipped (dS = 0, nothing stored).
   auto live = [&](int ii0) { return ii0 < T && !(CAUSAL && ii0 + 31 < j0); };
-  // The dS tile of query stage `stage`, from the transpose buffer to the workspace.
+  // The dS tiles of query stage `stage`, from the transpose buffers to the workspace.
   auto flush = [&](int stage) {
-    const int ii0 = stage * BN;
-    if (!live(ii0)) return;
-    E* gtile = dsh + ds_tile_index(ii0 / 32, j0 / 32, nb, CAUSAL) * kDsTileHalf;
-    wave_lds_fence();
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-      *reinterpret_cast<vec8_t<E>*>(gtile + 8 * (32 * (2 * s + half) + col)) =
-          ld8<E>(xw + col * XP + 16 * s + 8 * half);
-    wave_lds_fence();
+    for (int sub = 0; sub < NSUB; ++sub) {
+      const int ii0 = stage * BN + sub * 32;
+      if (!live(ii0)) continue;
+      E* gtile = dsh + ds_tile_index(ii0 / 32, j0 / 32, nb, CAUSAL) * kDsTileHalf;
+      const E* xs = xw + sub * 32 * XP;
+      wave_lds_fence();
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        *reinterpret_cast<vec8_t<E>*>(gtile + 8 * (32 * (2 * s + half) + col)) =
+            ld8<E>(xs + col * XP + 16 * s + 8 * half);
+      wave_lds_fence();
+    }
   };
 
   // Stage order: with a causal mask the first (long) pass walks its query stages downward and
@@ -270,7 +290,12 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : (HS == 64 && CAUSAL ? 2 : 3)) 
     const E* gt = reinterpret_cast<const E*>(base + OFF_GT);
     const float* ls = reinterpret_cast<const float*>(base + OFF_L);
     const float* ds = reinterpret_cast<const float*>(base + OFF_D);
-    const int ii0 = s_idx * BN;
+#pragma unroll
+    for (int k = 0; k < NSUB; ++k) {
+    // sub-tiles in the stage walk's direction, so a wave's dK / dV sums run over 32-row tiles in
+    // the same order whatever the stage height
+    const int sub = down ? NSUB - 1 - k : k;
+    const int ii0 = s_idx * BN + sub * 32;
 
     if (live(ii0)) {
       // S = Q K^T and dP = dO V^T: lane holds column my_j, rows ii0 + R(r, half).  The stage
@@ -278,7 +303,7 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : (HS == 64 && CAUSAL ? 2 : 3)) 
       f32x16 sacc = zero16(), pacc;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const float4 dv = ld4(ds + 8 * g + 4 * half);
+        const float4 dv = ld4(ds + sub * 32 + 8 * g + 4 * half);
         pacc[4 * g + 0] = dv.x;
         pacc[4 * g + 1] = dv.y;
         pacc[4 * g + 2] = dv.z;
@@ -286,10 +311,10 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : (HS == 64 && CAUSAL ? 2 : 3)) 
       }
 #pragma unroll
       for (int s = 0; s < QS; ++s)
-        sacc = Half16<E>::mfma(ld8<E>(qr + col * RP + 16 * s + 8 * half), kf[s], sacc);
+        sacc = Half16<E>::mfma(ld8<E>(qr + (sub * 32 + col) * RP + 16 * s + 8 * half), kf[s], sacc);
 #pragma unroll
       for (int s = 0; s < QS; ++s)
-        pacc = Half16<E>::mfma(ld8<E>(gr + col * RP + 16 * s + 8 * half), vf[s], pacc);
+        pacc = Half16<E>::mfma(ld8<E>(gr + (sub * 32 + col) * RP + 16 * s + 8 * half), vf[s], pacc);
 
       // P = e^{S - L}; masked entries (and, for the stored dS, key rows past T) are exactly 0.
       // The stage holds L log2(e).  Two explicit paths: left to the compiler, the masked form
@@ -297,7 +322,7 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : (HS == 64 && CAUSAL ? 2 : 3)) 
       auto exp_scores = [&]<bool MASKED>() {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const float4 lv = ld4(ls + 8 * g + 4 * half);
+          const float4 lv = ld4(ls + sub * 32 + 8 * g + 4 * half);
           const float lr[4] = {lv.x, lv.y, lv.z, lv.w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -324,7 +349,7 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : (HS == 64 && CAUSAL ? 2 : 3)) 
       for (int d = 0; d < HS / 32; ++d)
 #pragma unroll
         for (int s = 0; s < 2; ++s)
-          dvacc[d] = Half16<E>::mfma(ld8<E>(gt + (d * 32 + col) * TP + 16 * s + 8 * half), pb[s],
+          dvacc[d] = Half16<E>::mfma(ld8<E>(gt + (d * 32 + col) * TP + sub * 32 + 16 * s + 8 * half), pb[s],
                                dvacc[d]);
 
       // dS = P (dP - delta)
@@ -337,7 +362,7 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : (HS == 64 && CAUSAL ? 2 : 3)) 
       // barrier separates the write, the read in flush() and the next write.
       // Each converted pair is stored as its low and its high half (ds_write_b16 and
       // ds_write_b16_d16_hi), without unpacking it.
-      uint16_t* xw16 = reinterpret_cast<uint16_t*>(xw);
+      uint16_t* xw16 = reinterpret_cast<uint16_t*>(xw + sub * 32 * XP);
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         uint32_t pk = reinterpret_cast<const uint32_t*>(&db[r >> 3])[(r & 7) >> 1];
@@ -352,9 +377,10 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : (HS == 64 && CAUSAL ? 2 : 3)) 
       for (int d = 0; d < HS / 32; ++d)
 #pragma unroll
         for (int s = 0; s < 2; ++s)
-          dkacc[d] = Half16<E>::mfma(ld8<E>(qt + (d * 32 + col) * TP + 16 * s + 8 * half), db[s],
+          dkacc[d] = Half16<E>::mfma(ld8<E>(qt + (d * 32 + col) * TP + sub * 32 + 16 * s + 8 * half), db[s],
                                dkacc[d]);
     }
+    }  // sub-tiles
 
     if (i + 1 < n_steps) lstore(buf ^ 1);
     __syncthreads();
@@ -617,11 +643,15 @@ int bwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
   for (int h0 = 0; h0 < BH; h0 += chunk) {
     const int n = std::min(chunk, BH - h0);
     dispatch_half(hs, causal, [&]<int HS, bool C>() {
+      using Cfg = DkdvHalfCfg<HS, C>;
+      const int n_ktiles = (int)((T + 32 * Cfg::WAVES - 1) / (32 * Cfg::WAVES));
+      const int64_t kitems = (int64_t)(C ? (n_ktiles + 1) / 2 : n_ktiles) * n;
+      hipLaunchKernelGGL((fa2_bwd_dkdv_half_kernel<E, HS, C, Cfg::WAVES, Cfg::BN, Cfg::MINW>),
+                         dim3(xcd_grid(kitems)), dim3(64 * Cfg::WAVES), 0, st, qb, kb, vb, gb, l,
+                         delta, dkb, dvb, wsb, (int)nh, (int)T, h0, n, n_ktiles,
+                         rsh(q_strides), rsh(k_strides), rsh(v_strides), rsh(do_strides), sl,
+                         scale, scale * kLog2e);
       const int64_t items = (int64_t)(C ? (n_tiles + 1) / 2 : n_tiles) * n;
-      hipLaunchKernelGGL((fa2_bwd_dkdv_half_kernel<E, HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
-                         st, qb, kb, vb, gb, l, delta, dkb, dvb, wsb, (int)nh, (int)T, h0, n,
-                         n_tiles, rsh(q_strides), rsh(k_strides), rsh(v_strides),
-                         rsh(do_strides), sl, scale, scale * kLog2e);
       hipLaunchKernelGGL((fa2_bwd_dq_ds_half_kernel<E, HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
                          st, kb, wsb, dqb, (int)nh, (int)T, h0, n, n_tiles, rsh(k_strides), scale);
     });
