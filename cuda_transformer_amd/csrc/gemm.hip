@@ -19,7 +19,9 @@
 // through LDS as [m][k] and [n][k] (k contiguous, pitch BK+4), so each MFMA operand fragment is a pair of
 // conflict-free 16-byte LDS reads whatever the operand's memory order.  Global loads are
 // dwordx4 along whichever dimension is contiguous in memory (template mode), with scalar
-// loads for ragged edges and irregular strides.
+// loads for ragged edges and irregular strides.  Within a slice the instruction order is pinned
+// (sched_group_barrier): global loads and LDS stores sit between the MFMAs, and the next
+// slice's fragments are read while the current slice's last MFMAs run.
 #include "cta_common.hpp"
 #include "gemm.hpp"
 
@@ -122,38 +124,64 @@ struct TileLoader {
   }
 };
 
-// The MFMAs of one K-slice: A rows [BM][KP] then B rows [BN][KP] in LDS at `as`.
+// One wave's operand fragments of one K-slice: per MFMA tile row (A) or column (B), KC = BK / 8
+// 16-byte chunks, each feeding four MFMAs (lane half h supplies k = 2e + h of chunk element e).
 template <class TL>
-__device__ __forceinline__ void slice_mma(const float* as, f32x16 (&acc)[TL::MB][TL::NB], int wm,
-                                          int wn, int half, int col) {
-  constexpr int BM = TL::BM, BN = TL::BN, BK = TL::BK, KP = TL::KP;
-  constexpr int MB = TL::MB, NB = TL::NB, KC = BK / 8;  // KC: 16-byte chunks per lane half
+struct Frags {
+  static constexpr int KC = TL::BK / 8;
+  float4 a[TL::MB][KC], b[TL::NB][KC];
+};
+
+// Reads a slice's fragments from LDS: A rows [BM][KP] then B rows [BN][KP] at `as`.
+template <class TL>
+__device__ __forceinline__ void read_frags(const float* as, Frags<TL>& f, int wm, int wn,
+                                           int half, int col) {
+  constexpr int BM = TL::BM, BN = TL::BN, BK = TL::BK, KP = TL::KP, KC = Frags<TL>::KC;
   const float* bs = as + BM * KP;
-  float4 af[MB][KC], bf[NB][KC];
 #pragma unroll
-  for (int i = 0; i < MB; ++i) {
+  for (int i = 0; i < TL::MB; ++i) {
     const float* ap = as + (wm * (BM / TL::WM) + i * 32 + col) * KP + half * (BK / 2);
 #pragma unroll
-    for (int c = 0; c < KC; ++c) af[i][c] = ld4(ap + 4 * c);
+    for (int c = 0; c < KC; ++c) f.a[i][c] = ld4(ap + 4 * c);
   }
 #pragma unroll
-  for (int j = 0; j < NB; ++j) {
+  for (int j = 0; j < TL::NB; ++j) {
     const float* bp = bs + (wn * (BN / TL::WN) + j * 32 + col) * KP + half * (BK / 2);
 #pragma unroll
-    for (int c = 0; c < KC; ++c) bf[j][c] = ld4(bp + 4 * c);
+    for (int c = 0; c < KC; ++c) f.b[j][c] = ld4(bp + 4 * c);
   }
+}
+
+// The MFMAs of chunks [C0, C1) of a slice, in k order for every accumulator.
+template <class TL, int C0, int C1>
+__device__ __forceinline__ void mma_chunks(const Frags<TL>& f, f32x16 (&acc)[TL::MB][TL::NB]) {
 #pragma unroll
-  for (int c = 0; c < KC; ++c) {
+  for (int c = C0; c < C1; ++c)
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
+      for (int i = 0; i < TL::MB; ++i)
 #pragma unroll
-        for (int j = 0; j < NB; ++j) {
-          const float a = e == 0 ? af[i][c].x : e == 1 ? af[i][c].y : e == 2 ? af[i][c].z : af[i][c].w;
-          const float b = e == 0 ? bf[j][c].x : e == 1 ? bf[j][c].y : e == 2 ? bf[j][c].z : bf[j][c].w;
+        for (int j = 0; j < TL::NB; ++j) {
+          const float4 av = f.a[i][c], bv = f.b[j][c];
+          const float a = e == 0 ? av.x : e == 1 ? av.y : e == 2 ? av.z : av.w;
+          const float b = e == 0 ? bv.x : e == 1 ? bv.y : e == 2 ? bv.z : bv.w;
           acc[i][j] = mfma32(a, b, acc[i][j]);
         }
+}
+
+// Instruction order of a slice's first MFMAs (sched_group_barrier masks: 0x008 MFMA,
+// 0x020 global load, 0x200 LDS store): one MFMA at a time, the next slice's global loads after
+// the first NV of them and its LDS stores, two at a time, after the middle one, so both issue
+// while the MFMA pipe is busy instead of between slices.
+template <int I, int NM, int NV, int NW>
+__device__ __forceinline__ void sched_first_part() {
+  if constexpr (I < NM) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (I < NV) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    if constexpr (I >= NM / 2 && (I - NM / 2) * 2 < NW)
+      __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
+    sched_first_part<I + 1, NM, NV, NW>();
   }
 }
 
@@ -245,26 +273,53 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
   lb0.store(smem + BM * KP, tid);
   __syncthreads();
 
-  auto mma = [&](const float* as) { slice_mma<TL>(as, acc, wm, wn, half, col); };
+  // Each slice's MFMAs run in two parts around the barrier that publishes the next slice.  The
+  // first part carries the next-but-one slice's global loads and the next slice's LDS stores;
+  // right after the barrier the wave issues the next slice's fragment reads, which complete
+  // under the second part, so no wave waits on LDS latency before its MFMAs.  A buffer is
+  // rewritten only after the barrier that follows every wave's reads of it (the barrier waits
+  // for outstanding LDS reads).
+  constexpr int KC = Frags<TL>::KC;
+  static_assert(KC % 2 == 0, "a slice splits into two halves of chunks");
+  constexpr int NM1 = MB * NB * 4 * (KC / 2);  // MFMAs per part
+  constexpr int NVM = LA::LOADS + LB::LOADS;
+  constexpr int NDW = LA::LOADS * (AMODE == kVecMN ? 4 : 1) + LB::LOADS * (BMODE == kVecMN ? 4 : 1);
+  constexpr int NDR = (MB + NB) * KC;
   float* const buf0 = smem;
   float* const buf1 = smem + (BM + BN) * KP;
+  Frags<TL> f0, f1;
+  read_frags<TL>(buf0, f0, wm, wn, half, col);
   for (int t = 0; t < nk2; t += 2) {
-    // slice t from buf0; slices t+2 (set 0) and t+1 (set 1, stored below) in flight
+    // slice t in f0; slices t+2 (set 0) and t+1 (set 1, stored below) in flight
     la0.load(Ab, A.s_row, A.s_col, m0, kb + (t + 2) * BK, M, ke, tid);
     lb0.load(Bb, B.s_col, B.s_row, n0, kb + (t + 2) * BK, N, ke, tid);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(buf0);
+    mma_chunks<TL, 0, KC / 2>(f0, acc);
     la1.store(buf1, tid);
     lb1.store(buf1 + BM * KP, tid);
+    sched_first_part<0, NM1, NVM, NDW>();
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
-    // slice t+1 from buf1
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags<TL>(buf1, f1, wm, wn, half, col);
+    mma_chunks<TL, KC / 2, KC>(f0, acc);
+    __builtin_amdgcn_sched_group_barrier(0x100, NDR, 0);  // LDS reads first
+    __builtin_amdgcn_sched_group_barrier(0x008, NM1, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // slice t+1 in f1
     la1.load(Ab, A.s_row, A.s_col, m0, kb + (t + 3) * BK, M, ke, tid);
     lb1.load(Bb, B.s_col, B.s_row, n0, kb + (t + 3) * BK, N, ke, tid);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(buf1);
+    mma_chunks<TL, 0, KC / 2>(f1, acc);
     la0.store(buf0, tid);
     lb0.store(buf0 + BM * KP, tid);
+    sched_first_part<0, NM1, NVM, NDW>();
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags<TL>(buf0, f0, wm, wn, half, col);
+    mma_chunks<TL, KC / 2, KC>(f1, acc);
+    __builtin_amdgcn_sched_group_barrier(0x100, NDR, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, NM1, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   if (split_ws != nullptr) {
