@@ -77,6 +77,18 @@ template <> struct DkdvTile<32> { static constexpr int BN = 64; static constexpr
 template <> struct DkdvTile<64> { static constexpr int BN = 32; static constexpr int MINW = 2; };
 template <> struct DkdvTile<128> { static constexpr int BN = 32; static constexpr int MINW = 1; };
 
+// Instruction order of a block of MFMAs (sched_group_barrier masks: 0x008 MFMA, 0x100 LDS
+// read): N pairs of MFMAs, each pair followed by one LDS read while I < R.  Preceded by a group
+// of reads, this keeps a fixed number of operand reads in flight ahead of the MFMAs.
+template <int I, int N, int R>
+__device__ __forceinline__ void pin_mfma_pairs() {
+  if constexpr (I < N) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    if constexpr (I < R) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    pin_mfma_pairs<I + 1, N, R>();
+  }
+}
+
 // ------------------------------------------------------------------------------------
 // Stage 2: dQ.  Workgroup = 128 query rows; K/V tiles streamed through LDS.
 template <int HS, bool CAUSAL>
@@ -215,13 +227,13 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
         sacc[r] = p * (pacc[r] - dl);
       }
 
+      // K^T operand (key row R(kk, half), column d*32 + col) from a lane base pointer.
+      const float* kcol = ks + (sub * 32 + 4 * half) * KP + col;
 #pragma unroll
-      for (int d = 0; d < HS / 32; ++d) {
+      for (int kk = 0; kk < 16; ++kk) {
 #pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
-          const float a = ks[(sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col];
-          dqacc[d] = mfma32(a, sacc[kk], dqacc[d]);
-        }
+        for (int d = 0; d < HS / 32; ++d)
+          dqacc[d] = mfma32(kcol[(8 * (kk >> 2) + (kk & 3)) * KP + d * 32], sacc[kk], dqacc[d]);
       }
     }
 
@@ -490,13 +502,23 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
       // dV^T += dO^T P is issued before dS is formed, so the dS arithmetic and its transpose
       // writes overlap these MFMAs; then dK^T += Q^T dS.  One product at a time keeps at most
       // one set of LDS operands in flight.
+      //
+      // The A operand of step kk is (query row R(kk, half), column d*32 + col) of the dO or Q
+      // tile.  For HS <= 64 it is addressed from one lane base pointer plus a compile-time row
+      // offset (8 (kk/4) + kk%4), which the LDS reads carry as immediates: per-read row
+      // arithmetic held registers at the 256-VGPR limit and forced each read to wait just
+      // before its MFMA.  With the registers free, the reads are pinned several MFMA pairs
+      // ahead.  HS = 128 (one wave per SIMD) measured faster with the per-read form.
+      const float* gcol = gs + (sub * 32 + 4 * half) * KP + col;
+      const float* qcol = qs + (sub * 32 + 4 * half) * KP + col;
+      auto a_op = [&](const float* tile, const float* lane_col, int kk, int d) {
+        return HS == 128 ? tile[(sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col]
+                         : lane_col[(8 * (kk >> 2) + (kk & 3)) * KP + d * 32];
+      };
 #pragma unroll
       for (int kk = 0; kk < 16; ++kk) {
 #pragma unroll
-        for (int d = 0; d < HS / 32; ++d) {
-          const int off = (sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col;
-          dvacc[d] = mfma32(gs[off], sacc[kk], dvacc[d]);
-        }
+        for (int d = 0; d < HS / 32; ++d) dvacc[d] = mfma32(a_op(gs, gcol, kk, d), sacc[kk], dvacc[d]);
       }
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -504,6 +526,12 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
         const float dr[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) pacc[4 * g + e] = sacc[4 * g + e] * (pacc[4 * g + e] - dr[e]);
+      }
+      // L's four reads and four dO pairs ahead of the first MFMA pair, then one read (dO
+      // operands, then delta) after each pair.
+      if (HS == 64) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 4 + 4, 0);
+        pin_mfma_pairs<0, 16, 16>();
       }
 
       // Lane (col, half) holds dS[ii0 + R(r, half)][j0 + col]: into the transpose buffer as
@@ -518,10 +546,11 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
 #pragma unroll
       for (int kk = 0; kk < 16; ++kk) {
 #pragma unroll
-        for (int d = 0; d < HS / 32; ++d) {
-          const int off = (sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col;
-          dkacc[d] = mfma32(qs[off], pacc[kk], dkacc[d]);
-        }
+        for (int d = 0; d < HS / 32; ++d) dkacc[d] = mfma32(a_op(qs, qcol, kk, d), pacc[kk], dkacc[d]);
+      }
+      if (HS == 64) {  // four Q pairs ahead
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        pin_mfma_pairs<0, 16, 12>();
       }
     }
 
@@ -645,13 +674,15 @@ __global__ __launch_bounds__(256, 2) void fa2_bwd_dq_ds_kernel(
     for (int sub = 0; sub < NSUB; ++sub) {
       if (!has_tile(stage * NSUB + sub)) continue;
       // kk-major: the HS/32 accumulator chains alternate, so no MFMA waits on its predecessor
+      // K^T operand (key row R(kk, half), column d*32 + col): lane base pointer plus
+      // compile-time row offsets, carried by the LDS reads as immediates.
+      const float* kcol = ks + (sub * 32 + 4 * half) * KP + col;
 #pragma unroll
       for (int kk = 0; kk < 16; ++kk) {
 #pragma unroll
-        for (int d = 0; d < HS / 32; ++d) {
-          const float a = ks[(sub * 32 + mfma_row(kk, half)) * KP + d * 32 + col];
-          acc[d] = mfma32(a, f4_at(dr[sub][kk >> 2], kk & 3), acc[d]);
-        }
+        for (int d = 0; d < HS / 32; ++d)
+          acc[d] = mfma32(kcol[(8 * (kk >> 2) + (kk & 3)) * KP + d * 32],
+                          f4_at(dr[sub][kk >> 2], kk & 3), acc[d]);
       }
     }
   };
