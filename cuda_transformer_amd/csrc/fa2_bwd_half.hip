@@ -150,6 +150,11 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
       for (int j = 0; j < 8; ++j) { kf[s][j] = (E)0.0f; vf[s][j] = (E)0.0f; }
   }
 
+  // The k and v rows are complete before the stage loop on every path into it.  Otherwise the
+  // compiler, which cannot prove that, waits for them inside each stage, and since the
+  // counter is in order that wait also drains the next stage's loads issued just before.
+  vm_wait_all();
+
   f32x16 dkacc[HS / 32], dvacc[HS / 32];
 #pragma unroll
   for (int d = 0; d < HS / 32; ++d) { dkacc[d] = zero16(); dvacc[d] = zero16(); }
