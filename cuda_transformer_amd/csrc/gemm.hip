@@ -14,14 +14,17 @@
 // The batch index z is split as (z / zin, z % zin) with a stride per level, which lets
 // the naive attention address heads inside a packed (B, T, 3C) tensor directly.
 //
-// gfx950 design: workgroup tile 128x128 of eight 32x64 waves (4x2) or 128x64 of four 64x32
-// waves, each wave owning a block of v_mfma_f32_32x32x2_f32 tiles.  A and B tiles are staged
-// through LDS as [m][k] and [n][k] (k contiguous, pitch BK+4), so each MFMA operand fragment is a pair of
-// conflict-free 16-byte LDS reads whatever the operand's memory order.  Global loads are
-// dwordx4 along whichever dimension is contiguous in memory (template mode), with scalar
-// loads for ragged edges and irregular strides.  Within a slice the instruction order is pinned
-// (sched_group_barrier): global loads and LDS stores sit between the MFMAs, and the next
-// slice's fragments are read while the current slice's last MFMAs run.
+// gfx950 design: workgroup tile 128x128 of four 64x64 waves, or 64x128 of four 32x64 waves for
+// narrow outputs, each wave owning a block of v_mfma_f32_32x32x2_f32 tiles.  A and B tiles are
+// staged through LDS as [m][k] and [n][k] (k contiguous, pitch BK+4), so each MFMA operand
+// fragment is a pair of 16-byte LDS reads whatever the operand's memory order.  Operand loads
+// are dwordx4 buffer loads along whichever dimension is contiguous in memory (template mode),
+// with scalar loads for irregular strides; the epilogue stores through buffer stores.  Both
+// address a tile from scalar bases with fixed per-lane offsets and let the buffer's range check
+// zero (loads) or drop (stores) what lies outside the operand, so the K loop and the epilogue
+// carry no per-element address arithmetic or bounds tests.  Within a slice the instruction
+// order is pinned (sched_group_barrier): operand loads and LDS stores sit between the MFMAs, and
+// the next slice's fragments are read while the current slice's last MFMAs run.
 #include "cta_common.hpp"
 #include "gemm.hpp"
 
@@ -62,67 +65,119 @@ __device__ __forceinline__ void veck_coords(int f, int& r, int& k4) {
 
 // Loads one ROWS x BK slice of an operand into registers.  `rows` indexes m (A) or n (B); the
 // operand is row-major in (row, k) when kVecK, (k, row) when kVecMN.
+//
+// Vector modes read through buffer loads: each lane's byte offset within a slice is fixed for
+// the whole K loop, and each slice only moves the resource's base and extent (scalar work), so
+// the loop carries no per-load address arithmetic.  Reads outside the resource return zero,
+// which zeroes k past the end of the K range and slices past the last one; rows past R read
+// zero (kVecK) or in-bounds values that only feed output rows/columns never stored (kVecMN).
+// On a ragged last slice a kVecK lane whose k lies past the end moves its offset out of range.
 template <int MODE, int ROWS, int BK, int THREADS>
 struct TileLoader {
   static constexpr int LOADS = ROWS * BK / 4 / THREADS;
   static_assert(ROWS * BK % (4 * THREADS) == 0, "tile must split evenly over the workgroup");
   float4 v[LOADS];
-  bool kin[LOADS];  // vector modes: the float4 lies inside K (zeroed at store time otherwise)
-  __device__ __forceinline__ void load(const float* base, int64_t s_row, int64_t s_k, int row0,
-                                       int k0, int R, int K, int tid) {
+};
+
+template <int MODE, int ROWS, int BK, int THREADS>
+struct LoadPlan {
+  static constexpr int LOADS = TileLoader<MODE, ROWS, BK, THREADS>::LOADS;
+  const float* base;  // (row0, k0) of the tile
+  int64_t s_row, s_k;
+  int rows;           // valid rows from row0: min(ROWS, R - row0) (kVecK) or R - row0 (kVecMN)
+  int row0, kb, R, ke;
+  int voff[LOADS];    // vector modes: byte offset of the lane's float4 within a slice
+  int kq[LOADS];      // kVecK: the float4's k within a slice
+  __device__ __forceinline__ void init(const float* b, int64_t sr, int64_t sk, int r0, int k0,
+                                       int R_, int K_, int tid) {
+    s_row = sr; s_k = sk; row0 = r0; kb = k0; R = R_; ke = K_;
+    if (MODE == kVecK) {
+      base = b + (int64_t)r0 * sr + k0;
+      rows = min(ROWS, R_ - r0);
+    } else if (MODE == kVecMN) {
+      base = b + (int64_t)k0 * sk + r0;
+      rows = R_ - r0;
+    } else {
+      base = b;
+    }
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int f = tid + THREADS * u;
       if (MODE == kVecMN) {
-        // k varies fastest across lanes: each 16-lane group reads 64 contiguous bytes of one k
-        // row and the LDS transpose below writes 16 consecutive words (no bank conflicts).
-        // Branch-free: always one dwordx4 from a clamped in-bounds address (R % 4 == 0), so the
-        // wait counters stay exact.  Rows past R only feed output rows/columns that are never
-        // stored; k past K must contribute zero and is masked when the slice is stored to LDS.
         const int k = f % BK, r4 = (f / BK) * 4;
-        const int gr = row0 + r4, gk = k0 + k;
-        v[u] = ld4(base + (int64_t)min(gk, K - 1) * s_k + min(gr, R - 4));
-        kin[u] = gk < K;
-      } else if (MODE == kVecK) {
-        int r, k4;
-        veck_coords<BK>(f, r, k4);
-        const int gr = row0 + r, gk = k0 + k4;
-        v[u] = ld4(base + (int64_t)min(gr, R - 1) * s_row + min(gk, K - 4));
-        kin[u] = gk < K;  // K % 4 == 0: a float4 is wholly inside or outside
+        voff[u] = (int)(((int64_t)k * sk + r4) * 4);
+        kq[u] = k;
       } else {
         int r, k4;
         veck_coords<BK>(f, r, k4);
-        const int gr = row0 + r, gk = k0 + k4;
-        float t[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          t[e] = (gr < R && gk + e < K) ? base[(int64_t)gr * s_row + (int64_t)(gk + e) * s_k] : 0.0f;
-        v[u] = make_float4(t[0], t[1], t[2], t[3]);
-        kin[u] = true;
+        voff[u] = (int)(((int64_t)r * sr + k4) * 4);
+        kq[u] = k4;
       }
     }
   }
-  // LDS image: [row][k], pitch BK + 4.
-  __device__ __forceinline__ void store(float* lds, int tid) const {
-    constexpr int KP = BK + 4;
+  // Slice t (k from kb + t BK) into regs.
+  __device__ __forceinline__ void load(TileLoader<MODE, ROWS, BK, THREADS>& L, int t,
+                                       int tid) const {
+    const int k0 = kb + t * BK;
+    const int klim = min(BK, ke - k0);  // <= 0 past the end: nothing in range
+    if (MODE == kScalar) {
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int f = tid + THREADS * u;
-      const float4 w = kin[u] ? v[u] : zero4();
-      if (MODE == kVecMN) {
-        const int k = f % BK, r4 = (f / BK) * 4;
-        lds[(r4 + 0) * KP + k] = w.x;
-        lds[(r4 + 1) * KP + k] = w.y;
-        lds[(r4 + 2) * KP + k] = w.z;
-        lds[(r4 + 3) * KP + k] = w.w;
-      } else {
+      for (int u = 0; u < LOADS; ++u) {
+        const int f = tid + THREADS * u;
         int r, k4;
         veck_coords<BK>(f, r, k4);
-        st4(lds + r * KP + k4, w);
+        const int gr = row0 + r, gk = k0 + k4;
+        float t4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          t4[e] = (gr < R && gk + e < ke) ? base[(int64_t)gr * s_row + (int64_t)(gk + e) * s_k] : 0.0f;
+        L.v[u] = make_float4(t4[0], t4[1], t4[2], t4[3]);
       }
+      return;
+    }
+    const float* bt;
+    int nbytes;
+    if (MODE == kVecK) {
+      bt = base + (int64_t)t * BK;
+      nbytes = klim > 0 ? (int)(((int64_t)(rows - 1) * s_row + klim) * 4) : 0;
+    } else {
+      bt = base + (int64_t)t * BK * s_k;
+      nbytes = klim > 0 ? (int)(((int64_t)(klim - 1) * s_k + rows) * 4) : 0;
+    }
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(bt), (short)0, nbytes, 0x00020000);
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int vo = (MODE == kVecMN || kq[u] < klim) ? voff[u] : (int)0x80000000;
+      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, 0, 0);
+      L.v[u] = make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z),
+                           __uint_as_float(w.w));
     }
   }
 };
+
+// LDS image of a slice in regs: [row][k], pitch BK + 4.
+template <int MODE, int ROWS, int BK, int THREADS>
+__device__ __forceinline__ void store_slice(const TileLoader<MODE, ROWS, BK, THREADS>& L,
+                                            float* lds, int tid) {
+  constexpr int KP = BK + 4;
+#pragma unroll
+  for (int u = 0; u < TileLoader<MODE, ROWS, BK, THREADS>::LOADS; ++u) {
+    const int f = tid + THREADS * u;
+    const float4 w = L.v[u];
+    if (MODE == kVecMN) {
+      const int k = f % BK, r4 = (f / BK) * 4;
+      lds[(r4 + 0) * KP + k] = w.x;
+      lds[(r4 + 1) * KP + k] = w.y;
+      lds[(r4 + 2) * KP + k] = w.z;
+      lds[(r4 + 3) * KP + k] = w.w;
+    } else {
+      int r, k4;
+      veck_coords<BK>(f, r, k4);
+      st4(lds + r * KP + k4, w);
+    }
+  }
+}
 
 // One wave's operand fragments of one K-slice: per MFMA tile row (A) or column (B), KC = BK / 8
 // 16-byte chunks, each feeding four MFMAs (lane half h supplies k = 2e + h of chunk element e).
@@ -185,35 +240,48 @@ __device__ __forceinline__ void sched_first_part() {
   }
 }
 
-// The epilogue of one output tile (origin m0, n0 of batch (zo, zi)): alpha, bias, causal mask
-// and the pointwise stage ACT, stored through C.
-template <class TL, int ACT>
-__device__ __forceinline__ void tile_store(const f32x16 (&acc)[TL::MB][TL::NB], const GemmOut& C,
-                                           const GemmEpilogue& ep, int M, int N, int m0, int n0,
-                                           int zo, int zi, int wm, int wn, int half, int col) {
-  constexpr int BM = TL::BM, BN = TL::BN, MB = TL::MB, NB = TL::NB;
-  float* Cb = C.p + zo * C.s_outer + zi * C.s_inner;
-  float* Xb = ep.aux ? ep.aux + zo * C.s_outer + zi * C.s_inner : nullptr;
+// Stores a wave's block of one output tile.  RAW: the accumulators as they are (split-K
+// partials); otherwise alpha, bias, the causal mask (MASK) and the pointwise stage ACT.  `Cz`
+// and `Xz` are the batch's output and aux planes, row stride srow.  The block is stored through
+// buffer stores from its origin: a lane's column is a fixed per-lane offset (moved out of range
+// when the column lies past N), each row's offset is scalar, and rows past M fall outside the
+// resource, so the stores need no per-element bounds tests or 64-bit address arithmetic.
+template <class TL, int ACT, bool RAW, bool MASK>
+__device__ __forceinline__ void block_store(const f32x16 (&acc)[TL::MB][TL::NB], float* Cz,
+                                            float* Xz, int64_t srow, const GemmEpilogue& ep,
+                                            int M, int N, int mw, int nw, int half, int col) {
+  constexpr int MB = TL::MB, NB = TL::NB;
+  constexpr int WROWS = TL::BM / TL::WM, WCOLS = TL::BN / TL::WN;
+  float* Cb = Cz + (int64_t)mw * srow + nw;
+  float* Xb = Xz ? Xz + (int64_t)mw * srow + nw : Cb;
+  const int nbytes = (int)(((int64_t)(min(WROWS, M - mw) - 1) * srow + min(WCOLS, N - nw)) * 4);
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(Cb, (short)0, nbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(Xb, (short)0, nbytes, 0x00020000);
+  const int row_bytes = (int)(srow * 4);
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
-    const int n = n0 + wn * (BN / TL::WN) + j * 32 + col;
-    if (n >= N) continue;
-    const float bv = ep.bias ? ep.bias[(int64_t)n * ep.bias_stride] : 0.0f;
+    const int n = nw + j * 32 + col;
+    const float bv = (!RAW && ep.bias && n < N) ? ep.bias[(int64_t)n * ep.bias_stride] : 0.0f;
+    const int vo = n < N ? 4 * half * row_bytes + (j * 32 + col) * 4 : (int)0x80000000;
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * (BM / TL::WM) + i * 32 + mfma_row(r, half);
-        if (m < M) {
-          float val = fmaf(ep.alpha, acc[i][j][r], bv);
-          if (ep.causal_mask && n > m) val = -INFINITY;
-          const int64_t off = (int64_t)m * C.s_row + n;
-          if (ACT == kActGeluGrad) val = gelu_grad(Xb[off], val);
-          if (ACT == kActGeluTanhGrad) val = gelu_tanh_grad(Xb[off], val);
-          Cb[off] = val;
-          if (ACT == kActGelu) Xb[off] = gelu_f(val);
-          if (ACT == kActGeluTanh) Xb[off] = gelu_tanh_f(val);
+        const int so = (i * 32 + 8 * (r >> 2) + (r & 3)) * row_bytes;
+        float val = acc[i][j][r];
+        if (!RAW) {
+          val = fmaf(ep.alpha, val, bv);
+          if (MASK && n > mw + i * 32 + mfma_row(r, half)) val = -INFINITY;
+          if (ACT == kActGeluGrad || ACT == kActGeluTanhGrad) {
+            const float x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, vo, so, 0));
+            val = ACT == kActGeluGrad ? gelu_grad(x, val) : gelu_tanh_grad(x, val);
+          }
         }
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), rc, vo, so, 0);
+        if (!RAW && ACT == kActGelu)
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gelu_f(val)), rx, vo, so, 0);
+        if (!RAW && ACT == kActGeluTanh)
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gelu_tanh_f(val)), rx, vo, so, 0);
       }
     }
   }
@@ -232,7 +300,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
   constexpr int MB = TL::MB, NB = TL::NB;
   __shared__ __attribute__((aligned(16))) float smem[TL::LDS_FLOATS];
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_index();
   const int half = lane >> 5, col = lane & 31;
   const int wm = wave / TL::WN, wn = wave % TL::WN;
 
@@ -247,9 +315,13 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
   // A rows are m with (s_row, s_col) = (m, k); B "rows" are n with (n, k) = (s_col, s_row).
   // Global loads run two K-slices ahead of the MFMAs (two register sets, alternating), so a
   // slice's loads have two slices of MFMA work to arrive; LDS is double buffered.  Vector-mode
-  // loads clamp their addresses into the operand, so reads past K stay in bounds.
+  // reads past K, or past the last slice, return zero.
   using LA = TileLoader<AMODE, BM, BK, TL::THREADS>;
   using LB = TileLoader<BMODE, BN, BK, TL::THREADS>;
+  LoadPlan<AMODE, BM, BK, TL::THREADS> pa;
+  LoadPlan<BMODE, BN, BK, TL::THREADS> pb;
+  pa.init(Ab, A.s_row, A.s_col, m0, kb, M, ke, tid);
+  pb.init(Bb, B.s_col, B.s_row, n0, kb, N, ke, tid);
   LA la0, la1;
   LB lb0, lb1;
   const int nk = (ke - kb + BK - 1) / BK;
@@ -260,17 +332,17 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[i][j] = zero16();
 
-  // Slice count rounded up to even: slices past the end load clamped addresses whose k lies
-  // beyond ke, so they are stored as zeros and add nothing.  The loop then has no conditional
-  // loads or stores, which keeps the compiler's wait counts exact (a load issued two slices
-  // ahead is not waited for until its LDS store).
+  // Slice count rounded up to even: slices past the end read nothing in range, so they are
+  // stored as zeros and add nothing.  The loop then has no conditional loads or stores, which
+  // keeps the compiler's wait counts exact (a load issued two slices ahead is not waited for
+  // until its LDS store).
   const int nk2 = (nk + 1) & ~1;
-  la0.load(Ab, A.s_row, A.s_col, m0, kb, M, ke, tid);
-  lb0.load(Bb, B.s_col, B.s_row, n0, kb, N, ke, tid);
-  la1.load(Ab, A.s_row, A.s_col, m0, kb + BK, M, ke, tid);
-  lb1.load(Bb, B.s_col, B.s_row, n0, kb + BK, N, ke, tid);
-  la0.store(smem, tid);
-  lb0.store(smem + BM * KP, tid);
+  pa.load(la0, 0, tid);
+  pb.load(lb0, 0, tid);
+  pa.load(la1, 1, tid);
+  pb.load(lb1, 1, tid);
+  store_slice(la0, smem, tid);
+  store_slice(lb0, smem + BM * KP, tid);
   __syncthreads();
 
   // Each slice's MFMAs run in two parts around the barrier that publishes the next slice.  The
@@ -291,11 +363,11 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
   read_frags<TL>(buf0, f0, wm, wn, half, col);
   for (int t = 0; t < nk2; t += 2) {
     // slice t in f0; slices t+2 (set 0) and t+1 (set 1, stored below) in flight
-    la0.load(Ab, A.s_row, A.s_col, m0, kb + (t + 2) * BK, M, ke, tid);
-    lb0.load(Bb, B.s_col, B.s_row, n0, kb + (t + 2) * BK, N, ke, tid);
+    pa.load(la0, t + 2, tid);
+    pb.load(lb0, t + 2, tid);
     mma_chunks<TL, 0, KC / 2>(f0, acc);
-    la1.store(buf1, tid);
-    lb1.store(buf1 + BM * KP, tid);
+    store_slice(la1, buf1, tid);
+    store_slice(lb1, buf1 + BM * KP, tid);
     sched_first_part<0, NM1, NVM, NDW>();
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
@@ -306,11 +378,11 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
     __builtin_amdgcn_sched_group_barrier(0x008, NM1, 0);
     __builtin_amdgcn_sched_barrier(0);
     // slice t+1 in f1
-    la1.load(Ab, A.s_row, A.s_col, m0, kb + (t + 3) * BK, M, ke, tid);
-    lb1.load(Bb, B.s_col, B.s_row, n0, kb + (t + 3) * BK, N, ke, tid);
+    pa.load(la1, t + 3, tid);
+    pb.load(lb1, t + 3, tid);
     mma_chunks<TL, 0, KC / 2>(f1, acc);
-    la0.store(buf0, tid);
-    lb0.store(buf0 + BM * KP, tid);
+    store_slice(la0, buf0, tid);
+    store_slice(lb0, buf0 + BM * KP, tid);
     sched_first_part<0, NM1, NVM, NDW>();
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
@@ -322,23 +394,20 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  const int mw = m0 + wm * (BM / TL::WM), nw = n0 + wn * (BN / TL::WN);
+  if (mw >= M || nw >= N) return;
+  // The block's byte extent must fit the 32-bit buffer offsets; the launcher checks it.
   if (split_ws != nullptr) {
-    float* Pb = split_ws + ((int64_t)split * Z + z) * M * N;
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const int n = n0 + wn * (BN / TL::WN) + j * 32 + col;
-      if (n >= N) continue;
-#pragma unroll
-      for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm * (BM / TL::WM) + i * 32 + mfma_row(r, half);
-          if (m < M) Pb[(int64_t)m * N + n] = acc[i][j][r];
-        }
-    }
+    float* Pz = split_ws + ((int64_t)split * Z + z) * M * N;
+    block_store<TL, kActNone, true, false>(acc, Pz, nullptr, N, ep, M, N, mw, nw, half, col);
     return;
   }
-  tile_store<TL, ACT>(acc, C, ep, M, N, m0, n0, zo, zi, wm, wn, half, col);
+  float* Cz = C.p + zo * C.s_outer + zi * C.s_inner;
+  float* Xz = ep.aux ? ep.aux + zo * C.s_outer + zi * C.s_inner : nullptr;
+  if (ep.causal_mask)
+    block_store<TL, ACT, false, true>(acc, Cz, Xz, C.s_row, ep, M, N, mw, nw, half, col);
+  else
+    block_store<TL, ACT, false, false>(acc, Cz, Xz, C.s_row, ep, M, N, mw, nw, half, col);
 }
 
 // Fixed-order sum of the split-K partials plus the epilogue of gemm_kernel.
@@ -373,13 +442,20 @@ bool vec_ok(const GemmOperand& op, bool contig_is_col) {
 }
 
 // Load mode of an operand.  A: (s_row, s_col) = (m, k); B: (k, n).  `rows` is M for A and N for
-// B.  The vector modes also need the contiguous extent to be a multiple of 4 (the branch-free
-// loads clamp whole float4s) and at least 4.
+// B.  The vector modes also need the contiguous extent to be a multiple of 4 (a float4 lies
+// wholly inside or outside the operand) and at least 4.
 int pick_mode(const GemmOperand& op, bool is_a, int64_t rows, int64_t K) {
   const int64_t s_k = is_a ? op.s_col : op.s_row;
   const int64_t s_mn = is_a ? op.s_row : op.s_col;
-  if (s_k == 1 && K % 4 == 0 && K >= 4 && vec_ok(op, is_a)) return kVecK;
-  if (s_mn == 1 && rows % 4 == 0 && rows >= 4 && vec_ok(op, !is_a)) return kVecMN;
+  // The buffer loads address a slice with 32-bit byte offsets and rely on rows (kVecK) or
+  // k rows (kVecMN) not overlapping, so that reads past the valid range fall outside it.
+  constexpr int64_t kMaxBytes = (int64_t)1 << 31;
+  if (s_k == 1 && K % 4 == 0 && K >= 4 && vec_ok(op, is_a) && s_mn >= K &&
+      (255 * s_mn + 64) * 4 < kMaxBytes)
+    return kVecK;
+  if (s_mn == 1 && rows % 4 == 0 && rows >= 4 && vec_ok(op, !is_a) && s_k >= rows &&
+      (63 * s_k + rows) * 4 < kMaxBytes)
+    return kVecMN;
   return kScalar;
 }
 
@@ -445,6 +521,9 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
     return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM size out of range");
   int64_t S = splitk_factor<TL>(M, N, K, Z);
   if (S > 1 && (workspace == nullptr || workspace_floats < S * Z * M * N)) S = 1;
+  // A wave's output block is stored through 32-bit buffer offsets from its origin.
+  if ((int64_t)TL::BM * std::max<int64_t>(C.s_row, N) * 4 >= ((int64_t)1 << 31))
+    return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM output row stride too large");
   const int64_t kchunk =
       S > 1 ? ((K + S - 1) / S + TL::BK - 1) / TL::BK * TL::BK : std::max<int64_t>(K, 1);
   const dim3 grid((unsigned)((N + TL::BN - 1) / TL::BN), (unsigned)((M + TL::BM - 1) / TL::BM),
@@ -477,11 +556,12 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
 }
 
 // Tile choice, from measured sweeps of the config-4 and small-GPT shapes on an MI355X:
-// narrow outputs (N <= 768) run best with a 128x64 tile of four 64x32 waves, everything else
-// (including shapes split along K) with a 128x128 tile of eight 32x64 waves.
+// narrow outputs (N <= 768) run best with a 64x128 tile of four 32x64 waves and K-slices of 32,
+// wider ones with a 128x128 tile of four 64x64 waves, and shapes split along K with a 128x128
+// tile of eight 32x64 waves.
 using SplitTile = GemmTile<128, 128, 16, 4, 2>;
-using NarrowTile = GemmTile<128, 64, 16, 2, 2>;
-using WideTile = GemmTile<128, 128, 16, 4, 2>;
+using NarrowTile = GemmTile<64, 128, 32, 2, 2>;
+using WideTile = GemmTile<128, 128, 16, 2, 2>;
 
 }  // namespace
 
