@@ -37,6 +37,7 @@ import ctypes
 import json
 import os
 import re
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -875,9 +876,16 @@ def gemm_workload(args):
                 if rc != 0:
                     raise RuntimeError(lib.cta_last_error().decode())
 
-            t_ours = _time_rotating(run_ours, len(sets), reps)
-            t_lib = _time_rotating(lambda i, theirs=theirs, sets=sets: theirs(*sets[i]), len(sets),
-                                   reps)
+            def run_lib(i, theirs=theirs, sets=sets):
+                theirs(*sets[i])
+
+            # Five rounds, alternating which side goes first; the median of each side's rounds.
+            ts_ours, ts_lib = [], []
+            for rnd in range(5):
+                pair = ((run_ours, ts_ours), (run_lib, ts_lib))
+                for fn, acc in (pair if rnd % 2 == 0 else pair[::-1]):
+                    acc.append(_time_rotating(fn, len(sets), reps))
+            t_ours, t_lib = statistics.median(ts_ours), statistics.median(ts_lib)
             fl = 2.0 * pm * pk * pn
             print(json.dumps({
                 "workload": f"{name} {pname}", "m_k_n": [pm, pk, pn], "dtype": "f32",

@@ -252,17 +252,38 @@ __device__ __forceinline__ void block_store(const f32x16 (&acc)[TL::MB][TL::NB],
                                             int M, int N, int mw, int nw, int half, int col) {
   constexpr int MB = TL::MB, NB = TL::NB;
   constexpr int WROWS = TL::BM / TL::WM, WCOLS = TL::BN / TL::WN;
+  constexpr bool kGrad = !RAW && (ACT == kActGeluGrad || ACT == kActGeluTanhGrad);
   float* Cb = Cz + (int64_t)mw * srow + nw;
   float* Xb = Xz ? Xz + (int64_t)mw * srow + nw : Cb;
   const int nbytes = (int)(((int64_t)(min(WROWS, M - mw) - 1) * srow + min(WCOLS, N - nw)) * 4);
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(Cb, (short)0, nbytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(Xb, (short)0, nbytes, 0x00020000);
   const int row_bytes = (int)(srow * 4);
+  int vo[NB];
+  float bv[NB];
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int n = nw + j * 32 + col;
-    const float bv = (!RAW && ep.bias && n < N) ? ep.bias[(int64_t)n * ep.bias_stride] : 0.0f;
-    const int vo = n < N ? 4 * half * row_bytes + (j * 32 + col) * 4 : (int)0x80000000;
+    bv[j] = (!RAW && ep.bias && n < N) ? ep.bias[(int64_t)n * ep.bias_stride] : 0.0f;
+    vo[j] = n < N ? 4 * half * row_bytes + (j * 32 + col) * 4 : (int)0x80000000;
+  }
+  // The gradient stages read the pre-activations: all of the block's loads are issued before
+  // its first store, so their latencies overlap.  Each element's pre-activation is read before
+  // any store, so dx may alias pre.
+  float xg[kGrad ? MB : 1][kGrad ? NB : 1][16];
+  if constexpr (kGrad) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          xg[i][j][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+              rx, vo[j], (i * 32 + 8 * (r >> 2) + (r & 3)) * row_bytes, 0));
+  }
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int n = nw + j * 32 + col;
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
 #pragma unroll
@@ -270,18 +291,17 @@ __device__ __forceinline__ void block_store(const f32x16 (&acc)[TL::MB][TL::NB],
         const int so = (i * 32 + 8 * (r >> 2) + (r & 3)) * row_bytes;
         float val = acc[i][j][r];
         if (!RAW) {
-          val = fmaf(ep.alpha, val, bv);
+          val = fmaf(ep.alpha, val, bv[j]);
           if (MASK && n > mw + i * 32 + mfma_row(r, half)) val = -INFINITY;
-          if (ACT == kActGeluGrad || ACT == kActGeluTanhGrad) {
-            const float x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, vo, so, 0));
-            val = ACT == kActGeluGrad ? gelu_grad(x, val) : gelu_tanh_grad(x, val);
-          }
+          if constexpr (kGrad)
+            val = ACT == kActGeluGrad ? gelu_grad(xg[i][j][r], val)
+                                      : gelu_tanh_grad(xg[i][j][r], val);
         }
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), rc, vo, so, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), rc, vo[j], so, 0);
         if (!RAW && ACT == kActGelu)
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gelu_f(val)), rx, vo, so, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gelu_f(val)), rx, vo[j], so, 0);
         if (!RAW && ACT == kActGeluTanh)
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gelu_tanh_f(val)), rx, vo, so, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gelu_tanh_f(val)), rx, vo[j], so, 0);
       }
     }
   }
@@ -454,7 +474,7 @@ int pick_mode(const GemmOperand& op, bool is_a, int64_t rows, int64_t K) {
       (255 * s_mn + 64) * 4 < kMaxBytes)
     return kVecK;
   if (s_mn == 1 && rows % 4 == 0 && rows >= 4 && vec_ok(op, !is_a) && s_k >= rows &&
-      (63 * s_k + rows) * 4 < kMaxBytes)
+      (63 * s_k + std::max<int64_t>(rows, 256)) * 4 < kMaxBytes)
     return kVecMN;
   return kScalar;
 }

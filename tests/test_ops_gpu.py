@@ -325,6 +325,45 @@ def test_linear_split_k(cuda, B, M, K, N):
     assert rel_err(f64(out3), np.swapaxes(f64(x), 1, 2) @ f64(dyt)) <= 1e-6
 
 
+@pytest.mark.parametrize("M,K,N", [(96, 100, 68), (130, 36, 1152), (64, 1020, 388), (33, 4100, 64)])
+def test_linear_ragged_k_vector_loads(cuda, M, K, N):
+    """K not a multiple of the K-slice while both operands take 16-byte loads: the last slice's
+    lanes past K must read zeros (forward x.W, dx = dy.W^T view, dW = x^T view . dy)."""
+    from cuda_transformer.ops import cuda_fma
+
+    x = seeded((1, M, K), 41).to(cuda)
+    w = seeded((K, N), 42).to(cuda) * 0.1
+    b = seeded((N,), 43).to(cuda)
+    out = cuda_fma(x, w, b)
+    assert rel_err(f64(out), f64(x) @ f64(w) + f64(b)) <= 1e-6
+    wt = seeded((N, K), 44).to(cuda)                    # W stored (N, K): its W^T view is k-contiguous
+    out = cuda_fma(x, wt.t().unsqueeze(0), torch.zeros(N, device=cuda))
+    assert rel_err(f64(out), f64(x) @ f64(wt).T) <= 1e-6
+    dy = seeded((1, M, N), 45).to(cuda)
+    out = cuda_fma(x.transpose(1, 2), dy, torch.zeros(N, device=cuda))
+    assert rel_err(f64(out), np.swapaxes(f64(x), 1, 2) @ f64(dy)) <= 1e-6
+
+
+def test_linear_operand_strides_past_buffer_offsets(cuda):
+    """Operand views whose strides put a tile's rows more than 2 GiB apart cannot be addressed
+    with 32-bit buffer offsets; they take the scalar load path and stay exact."""
+    from cuda_transformer.ops import cuda_fma
+
+    M, K, N = 5, 64, 48
+    big = torch.zeros(M, 2_200_000, device=cuda)
+    big[:, :K] = seeded((M, K), 46).to(cuda)
+    x = big[:, :K].unsqueeze(0)                         # row stride 2.2e6 floats
+    w = seeded((K, N), 47).to(cuda)
+    b = seeded((N,), 48).to(cuda)
+    out = cuda_fma(x, w, b)
+    assert rel_err(f64(out), f64(x) @ f64(w) + f64(b)) <= 1e-6
+    wbig = torch.zeros(K, 9_000_000, device=cuda)       # W (K, N) view with k stride 9e6 floats
+    wbig[:, :N] = w
+    out2 = cuda_fma(x, wbig[:, :N], b)
+    assert torch.equal(out2, out)
+    del big, wbig
+
+
 def test_db_strided_views(cuda):
     from cuda_transformer.ops import db_calculation
 
