@@ -14,6 +14,8 @@ Deviations, each a fix:
 * ``CudaLinearLayer.backward`` allocates its zero bias on dy's device instead of the
   hard-coded 'cuda' device, and computes dW as one GEMM over the flattened (batch*m) axis
   instead of a per-batch GEMM followed by ``torch.sum(dim=0)`` (same sum, fewer bytes).
+  Its zero bias is one cached read-only tensor per (length, dtype, device) rather than a new
+  ``torch.zeros`` (a fill launch) on every backward.
 """
 import torch
 
@@ -27,6 +29,22 @@ __all__ = [
     "CudaCausalSelfAttention", "CudaFlashAttention", "CudaGeluLayer", "CudaLinearLayer",
     "CudaSoftmaxLayer", "CudaLayerNorm", "CudaMLP", "CudaGeluTanhLayer",
 ]
+
+
+_ZEROS = {}
+
+
+def _zeros(n, like):
+    """A length-n zero vector on like's device and dtype, allocated once and never written:
+    the zero bias of the backward GEMMs.  Under stream capture a first use allocates a plain
+    zeros tensor instead: memory from the graph's private pool must not outlive the graph."""
+    key = (n, like.dtype, like.device)
+    z = _ZEROS.get(key)
+    if z is None:
+        z = torch.zeros(n, dtype=like.dtype, device=like.device)
+        if not (like.is_cuda and torch.cuda.is_current_stream_capturing()):
+            _ZEROS[key] = z
+    return z
 
 
 class CudaFlashAttention(torch.autograd.Function):
@@ -60,8 +78,7 @@ class CudaLinearLayer(torch.autograd.Function):
         x, weights, _, _ = ctx.saved_tensors
         dy = grad_output
         w = weights.unsqueeze(0) if weights.dim() == 2 else weights
-        dx = cuda_fma(dy, w.transpose(1, 2),
-                      torch.zeros(x.shape[-1], dtype=dy.dtype, device=dy.device))
+        dx = cuda_fma(dy, w.transpose(1, 2), _zeros(x.shape[-1], dy))
         dw, db = _weight_and_bias_grads(x, weights, dy)
         return dx, dw, db
 
@@ -69,7 +86,7 @@ class CudaLinearLayer(torch.autograd.Function):
 def _weight_and_bias_grads(x, weights, dy):
     """dW = sum_b x[b]^T dy[b] and db = sum of dy over (batch, rows) (cuda_linear_layer.py:21-27)."""
     k, n = x.shape[-1], dy.shape[-1]
-    zero_n = torch.zeros(n, dtype=dy.dtype, device=dy.device)
+    zero_n = _zeros(n, dy)
     if weights.dim() == 2:
         # sum_b x[b]^T dy[b] == (x as (b*m, k))^T (dy as (b*m, n)): one GEMM, K = b*m
         x2 = x.reshape(1, -1, k)
@@ -141,8 +158,7 @@ class CudaMLP(torch.autograd.Function):
         dpre = (cuda_fma_gelu_tanh_grad if ctx.tanh else cuda_fma_gelu_grad)(
             dz, w2.unsqueeze(0).transpose(1, 2), pre)
         dw1, db1 = _weight_and_bias_grads(x, w1, dpre)
-        dx = cuda_fma(dpre, w1.unsqueeze(0).transpose(1, 2),
-                      torch.zeros(x.shape[-1], dtype=dz.dtype, device=dz.device))
+        dx = cuda_fma(dpre, w1.unsqueeze(0).transpose(1, 2), _zeros(x.shape[-1], dz))
         return dx, dw1, db1, dw2, db2, None
 
 

@@ -509,11 +509,12 @@ void dispatch_a(int am, int bm, dim3 grid, hipStream_t st, const GemmOperand& A,
 
 // K splits for a GEMM whose output tiles alone cannot fill the 256 CUs (1 = no split).  The
 // busiest CU runs ceil(tiles S / 256) workgroups of ceil(K / S) each, and the split adds a
-// round trip of S partial outputs through HBM; S in [1, 16] (at least 256 of K per split)
+// round trip of S partial outputs through HBM; S in [1, 32] (at least 256 of K per split)
 // minimises the sum.  Costs are in seconds at an MFMA rate of ~0.4 TFLOP/s per CU and
 // ~5 TB/s of HBM.  E.g. the 768 x 3072 x 8192 weight gradient: 144 tiles, S = 7 (1008
 // workgroups, 98% of the CUs' time busy) where a plain "~512 workgroups" rule gives S = 4
-// (576 workgroups, three rounds for 2.25 rounds of work).
+// (576 workgroups, three rounds for 2.25 rounds of work); the 384 x 384 x 16384 one: 9 tiles,
+// S = 28 (252 workgroups; capped at 16 it left 112 CUs idle and ran 27% slower).
 template <class TL>
 int64_t splitk_factor(int64_t M, int64_t N, int64_t K, int64_t Z) {
   const int64_t tiles = ((M + TL::BM - 1) / TL::BM) * ((N + TL::BN - 1) / TL::BN) * Z;
@@ -522,7 +523,7 @@ int64_t splitk_factor(int64_t M, int64_t N, int64_t K, int64_t Z) {
   const double tile_flop_per_k = 2.0 * TL::BM * TL::BN;
   int64_t best = 1;
   double best_cost = 0.0;
-  for (int64_t s = 1; s <= 16 && (s == 1 || K / s >= 256); ++s) {
+  for (int64_t s = 1; s <= 32 && (s == 1 || K / s >= 256); ++s) {
     const int64_t kchunk = ((K + s - 1) / s + TL::BK - 1) / TL::BK * TL::BK;
     const int64_t rounds = (tiles * s + 255) / 256;
     const double cost = (double)rounds * kchunk * tile_flop_per_k / kCuFlops +
