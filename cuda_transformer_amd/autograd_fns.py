@@ -3,8 +3,9 @@
 Same classes, ``apply`` signatures and saved tensors as the reference's cuda_autograd_fns/
 (cuda_flash_attention.py:4-17, cuda_linear_layer.py:4-28, cuda_gelu_layer.py:4-14,
 cuda_softmax_layer.py:4-15, cuda_causal_self_attention.py:4-35), plus ``CudaLayerNorm``,
-``CudaMLP`` (the GPT MLP with its GELU folded into the GEMM epilogues) and ``CudaGeluTanhLayer``
-(the tanh-approximated GELU).
+``CudaMLP`` (the GPT MLP with its GELU folded into the GEMM epilogues), ``CudaGeluTanhLayer``
+(the tanh-approximated GELU) and ``CudaFlashAttentionQKV`` (attention on a packed qkv projection,
+no head transposes).
 
 Deviations, each a fix:
 
@@ -21,13 +22,13 @@ import torch
 
 from .ops import (
     causal_self_attention_bwd, causal_self_attention_fwd, cuda_fma, cuda_fma_gelu,
-    cuda_fma_gelu_grad, cuda_fma_gelu_tanh, cuda_fma_gelu_tanh_grad, cuda_softmax, cuda_softmax_bwd, db_calculation, flash_attention_bwd, flash_attention_fwd, gelu_activation,
+    cuda_fma_gelu_grad, cuda_fma_gelu_tanh, cuda_fma_gelu_tanh_grad, cuda_softmax, cuda_softmax_bwd, db_calculation, flash_attention_bwd, flash_attention_fwd, flash_attention_qkv_bwd, flash_attention_qkv_fwd, gelu_activation,
     gelu_activation_bwd, gelu_tanh_activation, gelu_tanh_activation_bwd, layernorm_bwd, layernorm_fwd,
 )
 
 __all__ = [
     "CudaCausalSelfAttention", "CudaFlashAttention", "CudaGeluLayer", "CudaLinearLayer",
-    "CudaSoftmaxLayer", "CudaLayerNorm", "CudaMLP", "CudaGeluTanhLayer",
+    "CudaSoftmaxLayer", "CudaLayerNorm", "CudaMLP", "CudaGeluTanhLayer", "CudaFlashAttentionQKV",
 ]
 
 
@@ -62,6 +63,24 @@ class CudaFlashAttention(torch.autograd.Function):
         q, k, v, o, l = ctx.saved_tensors
         dq, dk, dv = flash_attention_bwd(q, k, v, o, grad_output, l, ctx.causal)
         return dq, dk, dv, None
+
+
+class CudaFlashAttentionQKV(torch.autograd.Function):
+    """(qkv (B, T, 3C), nh, causal) -> attention output (B, T, C), heads interleaved as in qkv:
+    the reference GPT's qkv.split -> head views -> flash attention -> transpose back
+    (gpt/gpt.py:104-109), with the kernels reading and writing the packed layouts in place."""
+
+    @staticmethod
+    def forward(ctx, qkv, nh, causal):
+        out, l = flash_attention_qkv_fwd(qkv, nh, causal)
+        ctx.save_for_backward(qkv, out, l)
+        ctx.nh, ctx.causal = nh, causal
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        qkv, out, l = ctx.saved_tensors
+        return flash_attention_qkv_bwd(qkv, out, grad_output, l, ctx.nh, ctx.causal), None, None
 
 
 class CudaLinearLayer(torch.autograd.Function):

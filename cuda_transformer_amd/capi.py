@@ -32,6 +32,12 @@ SIGNATURES = {
     "cta_flash_attention_bwd": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
                                        _p, _i64p, _i64, _i64, _i64, _i64, _int, _p, _p, _p, _p,
                                        _p, _i64, _p]),
+    "cta_flash_attention_fwd_strided": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64,
+                                               _i64, _int, _p, _i64p, _p, _p]),
+    "cta_flash_attention_bwd_strided": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p,
+                                               _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _int,
+                                               _p, _i64p, _p, _i64p, _p, _i64p, _p, _p, _i64,
+                                               _p]),
     "cta_flash_attention_bwd_noalloc": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p,
                                                _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _int,
                                                _p, _p, _p, _p]),

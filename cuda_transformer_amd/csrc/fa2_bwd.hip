@@ -96,7 +96,7 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
     float* __restrict__ dQ, int nh, int T, int BH, int n_qtiles, RowStrides sq, RowStrides sk,
-    RowStrides sv, RowStrides sdo, LStrides sl, float scale, float scale_log2) {
+    RowStrides sv, RowStrides sdo, LStrides sl, RowStrides sdq, float scale, float scale_log2) {
   constexpr int BN = BwdTile<HS>::BN;
   constexpr int BM = 128;
   constexpr int H2 = HS / 2;
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
   }
 
   if (my_i < T) {
-    float* op = dQ + ((int64_t)bh * T + my_i) * HS;
+    float* op = dQ + b * sdq.b + h * sdq.h + (int64_t)my_i * sdq.t;
 #pragma unroll
     for (int d = 0; d < HS / 32; ++d) {
 #pragma unroll
@@ -290,8 +290,8 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
     const float* __restrict__ dO, const float* __restrict__ O, const float* __restrict__ Lg,
     const float* __restrict__ delta, float* __restrict__ dK, float* __restrict__ dV,
     float* __restrict__ dsw, int nh, int T, int bh_base, int BH, int n_ktiles, RowStrides sq,
-    RowStrides sk, RowStrides sv, RowStrides sdo, RowStrides so, LStrides sl, float scale,
-    float scale_log2) {
+    RowStrides sk, RowStrides sv, RowStrides sdo, RowStrides so, LStrides sl, RowStrides sdk,
+    RowStrides sdv, float scale, float scale_log2) {
   constexpr int BN = DkdvTile<HS>::BN;
   constexpr int NSUB = BN / 32;
   constexpr int BM = 128;
@@ -560,8 +560,8 @@ __global__ __launch_bounds__(256, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
   if (wave_stores && n_steps > 0) flush(stage_at(n_steps - 1));
 
   if (my_j < T) {
-    float* kp = dK + ((int64_t)bh * T + my_j) * HS;
-    float* vp = dV + ((int64_t)bh * T + my_j) * HS;
+    float* kp = dK + b * sdk.b + h * sdk.h + (int64_t)my_j * sdk.t;
+    float* vp = dV + b * sdv.b + h * sdv.h + (int64_t)my_j * sdv.t;
 #pragma unroll
     for (int d = 0; d < HS / 32; ++d) {
 #pragma unroll
@@ -589,7 +589,7 @@ __device__ __forceinline__ float f4_at(const float4& v, int e) {
 template <int HS, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void fa2_bwd_dq_ds_kernel(
     const float* __restrict__ K, const float* __restrict__ dsw, float* __restrict__ dQ, int nh,
-    int T, int bh_base, int BH, int n_qtiles, RowStrides sk, float scale) {
+    int T, int bh_base, int BH, int n_qtiles, RowStrides sk, RowStrides sdq, float scale) {
   constexpr int BN = 64;
   constexpr int NSUB = BN / 32;
   constexpr int BM = 128;
@@ -708,7 +708,7 @@ __global__ __launch_bounds__(256, 2) void fa2_bwd_dq_ds_kernel(
   }
 
   if (my_i < T) {
-    float* op = dQ + ((int64_t)bh * T + my_i) * HS;
+    float* op = dQ + b * sdq.b + h * sdq.h + (int64_t)my_i * sdq.t;
 #pragma unroll
     for (int d = 0; d < HS / 32; ++d) {
 #pragma unroll
@@ -736,37 +736,39 @@ void launch_delta(const float* o, const float* d_o, float* delta, int nh, int T,
 template <int HS, bool CAUSAL>
 void launch_dq(const float* q, const float* k, const float* v, const float* d_o, const float* l,
                const float* delta, float* dq, int nh, int T, int BH, RowStrides sq,
-               RowStrides sk, RowStrides sv, RowStrides sdo, LStrides sl, float scale,
-               hipStream_t st) {
+               RowStrides sk, RowStrides sv, RowStrides sdo, LStrides sl, RowStrides sdq,
+               float scale, hipStream_t st) {
   const int n_qtiles = (T + 127) / 128;
   const int64_t items = (int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH;
   hipLaunchKernelGGL((fa2_bwd_dq_kernel<HS, CAUSAL>), dim3(xcd_grid(items)), dim3(256), 0,
                      st, q, k, v, d_o, l, delta, dq, nh, T, BH, n_qtiles, sq, sk, sv, sdo, sl,
-                     scale, scale * kLog2e);
+                     sdq, scale, scale * kLog2e);
 }
 
-// dK/dV for heads [bh_base, bh_base + n_heads); with STORE_DS the dS tiles go to dsw; with
-// FOLD delta comes from O (strides so) instead of the delta array.
+// dK/dV for heads [bh_base, bh_base + n_heads), written through strides sdk / sdv; with
+// STORE_DS the dS tiles go to dsw; with FOLD delta comes from O (strides so) instead of the
+// delta array.
 template <int HS, bool CAUSAL, bool STORE_DS, bool FOLD = false>
 void launch_dkdv(const float* q, const float* k, const float* v, const float* d_o,
                  const float* l, const float* delta, float* dk, float* dv, float* dsw, int nh,
                  int T, int bh_base, int n_heads, RowStrides sq, RowStrides sk, RowStrides sv,
-                 RowStrides sdo, LStrides sl, float scale, hipStream_t st,
-                 const float* o = nullptr, RowStrides so = {}) {
+                 RowStrides sdo, LStrides sl, RowStrides sdk, RowStrides sdv, float scale,
+                 hipStream_t st, const float* o = nullptr, RowStrides so = {}) {
   const int n_ktiles = (T + 127) / 128;
   const int64_t items = (int64_t)(CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles) * n_heads;
   hipLaunchKernelGGL((fa2_bwd_dkdv_kernel<HS, CAUSAL, STORE_DS, FOLD>), dim3(xcd_grid(items)),
                      dim3(256), 0, st, q, k, v, d_o, o, l, delta, dk, dv, dsw, nh, T, bh_base,
-                     n_heads, n_ktiles, sq, sk, sv, sdo, so, sl, scale, scale * kLog2e);
+                     n_heads, n_ktiles, sq, sk, sv, sdo, so, sl, sdk, sdv, scale,
+                     scale * kLog2e);
 }
 
 template <int HS, bool CAUSAL>
 void launch_dq_ds(const float* k, const float* dsw, float* dq, int nh, int T, int bh_base,
-                  int n_heads, RowStrides sk, float scale, hipStream_t st) {
+                  int n_heads, RowStrides sk, RowStrides sdq, float scale, hipStream_t st) {
   const int n_qtiles = (T + 127) / 128;
   const int64_t items = (int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * n_heads;
   hipLaunchKernelGGL((fa2_bwd_dq_ds_kernel<HS, CAUSAL>), dim3(xcd_grid(items)), dim3(256), 0,
-                     st, k, dsw, dq, nh, T, bh_base, n_heads, n_qtiles, sk, scale);
+                     st, k, dsw, dq, nh, T, bh_base, n_heads, n_qtiles, sk, sdq, scale);
 }
 
 // Runs f.template operator()<HS, CAUSAL>() for the runtime head size and mask flag.
@@ -817,6 +819,43 @@ int check_bwd_inputs(const float* q, const int64_t* qs, const float* k, const in
 }
 }  // namespace
 
+namespace {
+// Strides of a dense (B, nh, T, hs) output.
+RowStrides dense_out(int64_t nh, int64_t T, int64_t hs) { return {nh * T * hs, T * hs, hs}; }
+
+int bwd_dq_impl(const float* q, const int64_t* q_strides, const float* k,
+                const int64_t* k_strides, const float* v, const int64_t* v_strides,
+                const float* d_o, const int64_t* do_strides, const float* l,
+                const int64_t* l_strides, const float* delta, int64_t B, int64_t nh, int64_t T,
+                int64_t hs, int causal, float* dq, RowStrides sdq, hipStream_t st) {
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
+  const int BH = (int)(B * nh);
+  dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
+    launch_dq<HS, C>(q, k, v, d_o, l, delta, dq, (int)nh, (int)T, BH, rs(q_strides),
+                     rs(k_strides), rs(v_strides), rs(do_strides), sl, sdq, scale, st);
+  });
+  return check_launch("flash_attention_bwd_dq");
+}
+
+int bwd_dkdv_impl(const float* q, const int64_t* q_strides, const float* k,
+                  const int64_t* k_strides, const float* v, const int64_t* v_strides,
+                  const float* d_o, const int64_t* do_strides, const float* l,
+                  const int64_t* l_strides, const float* delta, int64_t B, int64_t nh, int64_t T,
+                  int64_t hs, int causal, float* dk, RowStrides sdk, float* dv, RowStrides sdv,
+                  hipStream_t st) {
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
+  const int BH = (int)(B * nh);
+  dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
+    launch_dkdv<HS, C, false>(q, k, v, d_o, l, delta, dk, dv, nullptr, (int)nh, (int)T, 0, BH,
+                              rs(q_strides), rs(k_strides), rs(v_strides), rs(do_strides), sl,
+                              sdk, sdv, scale, st);
+  });
+  return check_launch("flash_attention_bwd_dkdv");
+}
+}  // namespace
+
 extern "C" int cta_flash_attention_bwd_dq(const float* q, const int64_t* q_strides,
                                           const float* k, const int64_t* k_strides,
                                           const float* v, const int64_t* v_strides,
@@ -830,20 +869,8 @@ extern "C" int cta_flash_attention_bwd_dq(const float* q, const int64_t* q_strid
                                 l_strides, delta))
     return rc;
   if (!dq || !aligned16(dq)) return fail(CTA_ERR_LAYOUT, "dQ must be a 16-byte aligned pointer");
-  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
-  const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
-  const int BH = (int)(B * nh);
-  hipStream_t st = as_stream(stream);
-#define CTA_DQ(HS_)                                                                           \
-  if (causal) launch_dq<HS_, true>(q, k, v, d_o, l, delta, dq, (int)nh, (int)T, BH, rs(q_strides), \
-                                   rs(k_strides), rs(v_strides), rs(do_strides), sl, scale, st); \
-  else launch_dq<HS_, false>(q, k, v, d_o, l, delta, dq, (int)nh, (int)T, BH, rs(q_strides),      \
-                             rs(k_strides), rs(v_strides), rs(do_strides), sl, scale, st);
-  if (hs == 32) { CTA_DQ(32) }
-  else if (hs == 64) { CTA_DQ(64) }
-  else { CTA_DQ(128) }
-#undef CTA_DQ
-  return check_launch("flash_attention_bwd_dq");
+  return bwd_dq_impl(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l, l_strides,
+                     delta, B, nh, T, hs, causal, dq, dense_out(nh, T, hs), as_stream(stream));
 }
 
 extern "C" int cta_flash_attention_bwd_dkdv(const float* q, const int64_t* q_strides,
@@ -861,16 +888,9 @@ extern "C" int cta_flash_attention_bwd_dkdv(const float* q, const int64_t* q_str
     return rc;
   if (!dk || !dv || !aligned16(dk) || !aligned16(dv))
     return fail(CTA_ERR_LAYOUT, "dK/dV must be 16-byte aligned pointers");
-  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
-  const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
-  const int BH = (int)(B * nh);
-  hipStream_t st = as_stream(stream);
-  dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
-    launch_dkdv<HS, C, false>(q, k, v, d_o, l, delta, dk, dv, nullptr, (int)nh, (int)T, 0, BH,
-                              rs(q_strides), rs(k_strides), rs(v_strides), rs(do_strides), sl,
-                              scale, st);
-  });
-  return check_launch("flash_attention_bwd_dkdv");
+  const RowStrides dense = dense_out(nh, T, hs);
+  return bwd_dkdv_impl(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l, l_strides,
+                       delta, B, nh, T, hs, causal, dk, dense, dv, dense, as_stream(stream));
 }
 
 extern "C" int64_t cta_flash_attention_bwd_workspace(int64_t B, int64_t nh, int64_t T,
@@ -898,7 +918,8 @@ extern "C" int cta_flash_attention_bwd_dkdv_store_ds(
   dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
     launch_dkdv<HS, C, true>(q, k, v, d_o, l, delta, dk, dv, ds_workspace, (int)nh, (int)T, 0,
                              (int)(B * nh), rs(q_strides), rs(k_strides), rs(v_strides),
-                             rs(do_strides), sl, scale, st);
+                             rs(do_strides), sl, dense_out(nh, T, hs), dense_out(nh, T, hs),
+                             scale, st);
   });
   return check_launch("flash_attention_bwd_dkdv_store_ds");
 }
@@ -919,9 +940,63 @@ extern "C" int cta_flash_attention_bwd_dq_from_ds(const float* k, const int64_t*
   hipStream_t st = as_stream(stream);
   dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
     launch_dq_ds<HS, C>(k, ds_workspace, dq, (int)nh, (int)T, 0, (int)(B * nh), rs(k_strides),
-                        scale, st);
+                        dense_out(nh, T, hs), scale, st);
   });
   return check_launch("flash_attention_bwd_dq_from_ds");
+}
+
+extern "C" int cta_flash_attention_bwd_strided(
+    const float* q, const int64_t* q_strides, const float* k, const int64_t* k_strides,
+    const float* v, const int64_t* v_strides, const float* o, const int64_t* o_strides,
+    const float* d_o, const int64_t* do_strides, const float* l, const int64_t* l_strides,
+    int64_t B, int64_t nh, int64_t T, int64_t hs, int causal, float* dq,
+    const int64_t* dq_strides, float* dk, const int64_t* dk_strides, float* dv,
+    const int64_t* dv_strides, float* delta, float* workspace, int64_t workspace_bytes,
+    void* stream) {
+  if (int rc = cta_flash_attention_bwd_delta(o, o_strides, d_o, do_strides, B, nh, T, hs, delta,
+                                             stream))
+    return rc;
+  if (B * nh * T == 0) return CTA_OK;
+  if (int rc = check_bwd_inputs(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l,
+                                l_strides, delta))
+    return rc;
+  if (!attn_layout_ok(dq, dq_strides) || !attn_layout_ok(dk, dk_strides) ||
+      !attn_layout_ok(dv, dv_strides))
+    return fail(CTA_ERR_LAYOUT,
+                "flash_attention_bwd needs unit d-stride, strides divisible by 4 and 16-byte "
+                "aligned dQ/dK/dV");
+  const RowStrides sdq = rs(dq_strides), sdk = rs(dk_strides), sdv = rs(dv_strides);
+  hipStream_t st = as_stream(stream);
+  const int64_t head_bytes = cta_flash_attention_bwd_workspace(1, 1, T, hs, causal);
+  if (workspace == nullptr || head_bytes == 0 || workspace_bytes < head_bytes) {
+    // The reference's schedule: dQ recomputes S and dP.
+    if (int rc = bwd_dq_impl(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l,
+                             l_strides, delta, B, nh, T, hs, causal, dq, sdq, st))
+      return rc;
+    return bwd_dkdv_impl(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l,
+                         l_strides, delta, B, nh, T, hs, causal, dk, sdk, dv, sdv, st);
+  }
+  if (!aligned16(workspace))
+    return fail(CTA_ERR_LAYOUT, "the workspace must be a 16-byte aligned pointer");
+  // Stored-dS schedule over chunks of equal head counts that fit the workspace.
+  const int BH = (int)(B * nh);
+  const int64_t fit = std::min<int64_t>(BH, workspace_bytes / head_bytes);
+  const int64_t n_chunks = (BH + fit - 1) / fit;
+  const int chunk = (int)((BH + n_chunks - 1) / n_chunks);
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
+  const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
+  for (int h0 = 0; h0 < BH; h0 += chunk) {
+    const int n = std::min(chunk, BH - h0);
+    dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
+      launch_dkdv<HS, C, true>(q, k, v, d_o, l, delta, dk, dv, workspace, (int)nh, (int)T, h0, n,
+                               rs(q_strides), rs(k_strides), rs(v_strides), rs(do_strides), sl,
+                               sdk, sdv, scale, st);
+      launch_dq_ds<HS, C>(k, workspace, dq, (int)nh, (int)T, h0, n, rs(k_strides), sdq, scale,
+                          st);
+    });
+    if (int rc = check_launch("flash_attention_bwd")) return rc;
+  }
+  return CTA_OK;
 }
 
 extern "C" int cta_flash_attention_bwd(const float* q, const int64_t* q_strides, const float* k,
@@ -933,46 +1008,11 @@ extern "C" int cta_flash_attention_bwd(const float* q, const int64_t* q_strides,
                                        int64_t T, int64_t hs, int causal, float* dq, float* dk,
                                        float* dv, float* delta, float* workspace,
                                        int64_t workspace_bytes, void* stream) {
-  if (int rc = cta_flash_attention_bwd_delta(o, o_strides, d_o, do_strides, B, nh, T, hs, delta,
-                                             stream))
-    return rc;
-  const int64_t head_bytes = cta_flash_attention_bwd_workspace(1, 1, T, hs, causal);
-  if (workspace == nullptr || head_bytes == 0 || workspace_bytes < head_bytes) {
-    // The reference's schedule: dQ recomputes S and dP.
-    if (int rc = cta_flash_attention_bwd_dq(q, q_strides, k, k_strides, v, v_strides, d_o,
-                                            do_strides, l, l_strides, delta, B, nh, T, hs,
-                                            causal, dq, stream))
-      return rc;
-    return cta_flash_attention_bwd_dkdv(q, q_strides, k, k_strides, v, v_strides, d_o,
-                                        do_strides, l, l_strides, delta, B, nh, T, hs, causal, dk,
-                                        dv, stream);
-  }
-  if (B * nh * T == 0) return CTA_OK;
-  if (int rc = check_bwd_inputs(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l,
-                                l_strides, delta))
-    return rc;
-  if (!dq || !dk || !dv || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
-      !aligned16(workspace))
-    return fail(CTA_ERR_LAYOUT, "dQ/dK/dV and the workspace must be 16-byte aligned pointers");
-  // Stored-dS schedule over chunks of equal head counts that fit the workspace.
-  const int BH = (int)(B * nh);
-  const int64_t fit = std::min<int64_t>(BH, workspace_bytes / head_bytes);
-  const int64_t n_chunks = (BH + fit - 1) / fit;
-  const int chunk = (int)((BH + n_chunks - 1) / n_chunks);
-  const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
-  const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
-  hipStream_t st = as_stream(stream);
-  for (int h0 = 0; h0 < BH; h0 += chunk) {
-    const int n = std::min(chunk, BH - h0);
-    dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
-      launch_dkdv<HS, C, true>(q, k, v, d_o, l, delta, dk, dv, workspace, (int)nh, (int)T, h0, n,
-                               rs(q_strides), rs(k_strides), rs(v_strides), rs(do_strides), sl,
-                               scale, st);
-      launch_dq_ds<HS, C>(k, workspace, dq, (int)nh, (int)T, h0, n, rs(k_strides), scale, st);
-    });
-    if (int rc = check_launch("flash_attention_bwd")) return rc;
-  }
-  return CTA_OK;
+  const int64_t ds[4] = {nh * T * hs, T * hs, hs, 1};  // dense (B, nh, T, hs) outputs
+  return cta_flash_attention_bwd_strided(q, q_strides, k, k_strides, v, v_strides, o, o_strides,
+                                         d_o, do_strides, l, l_strides, B, nh, T, hs, causal, dq,
+                                         ds, dk, ds, dv, ds, delta, workspace, workspace_bytes,
+                                         stream);
 }
 
 extern "C" int cta_flash_attention_bwd_fold_delta(
@@ -1010,8 +1050,10 @@ extern "C" int cta_flash_attention_bwd_fold_delta(
     dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
       launch_dkdv<HS, C, true, true>(q, k, v, d_o, l, nullptr, dk, dv, workspace, (int)nh,
                                      (int)T, h0, n, rs(q_strides), rs(k_strides), rs(v_strides),
-                                     rs(do_strides), sl, scale, st, o, rs(o_strides));
-      launch_dq_ds<HS, C>(k, workspace, dq, (int)nh, (int)T, h0, n, rs(k_strides), scale, st);
+                                     rs(do_strides), sl, dense_out(nh, T, hs),
+                                     dense_out(nh, T, hs), scale, st, o, rs(o_strides));
+      launch_dq_ds<HS, C>(k, workspace, dq, (int)nh, (int)T, h0, n, rs(k_strides),
+                          dense_out(nh, T, hs), scale, st);
     });
     if (int rc = check_launch("flash_attention_bwd_fold_delta")) return rc;
   }

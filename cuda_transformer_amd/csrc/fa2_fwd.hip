@@ -43,7 +43,7 @@ template <int HS, bool CAUSAL>
 __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ L, int nh, int T, int BH, int n_qtiles,
-    RowStrides sq, RowStrides sk, RowStrides sv, float scale, float scale_log2,
+    RowStrides sq, RowStrides sk, RowStrides sv, RowStrides so, float scale, float scale_log2,
     float rescale_gap) {
   constexpr int BN = FwdTile<HS>::BN;
   constexpr int BM = 128;
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
 
   const float l_tot = sum_halves(l_run);
   if (my_i < T) {
-    float* op = O + ((int64_t)bh * T + my_i) * HS;
+    float* op = O + b * so.b + h * so.h + (int64_t)my_i * so.t;
 #pragma unroll
     for (int d = 0; d < HS / 32; ++d) {
 #pragma unroll
@@ -231,12 +231,12 @@ __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
 
 template <int HS, bool CAUSAL>
 void launch_fwd(const float* q, const float* k, const float* v, float* o, float* l, int nh,
-                int T, int BH, RowStrides sq, RowStrides sk, RowStrides sv, float scale,
-                hipStream_t stream) {
+                int T, int BH, RowStrides sq, RowStrides sk, RowStrides sv, RowStrides so,
+                float scale, hipStream_t stream) {
   const int n_qtiles = (T + 127) / 128;
   const unsigned grid = xcd_grid((int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH);
   hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL>), dim3(grid), dim3(256), 0, stream, q, k, v, o,
-                     l, nh, T, BH, n_qtiles, sq, sk, sv, scale, scale * kLog2e,
+                     l, nh, T, BH, n_qtiles, sq, sk, sv, so, scale, scale * kLog2e,
                      8.0f / (scale * kLog2e));
 }
 
@@ -261,31 +261,43 @@ int check_attn_sizes(int64_t B, int64_t nh, int64_t T, int64_t hs) {
 
 using namespace cta;
 
-extern "C" int cta_flash_attention_fwd(const float* q, const int64_t* q_strides, const float* k,
-                                       const int64_t* k_strides, const float* v,
-                                       const int64_t* v_strides, int64_t B, int64_t nh,
-                                       int64_t T, int64_t hs, int causal, float* o, float* l,
-                                       void* stream) {
+extern "C" int cta_flash_attention_fwd_strided(const float* q, const int64_t* q_strides,
+                                               const float* k, const int64_t* k_strides,
+                                               const float* v, const int64_t* v_strides,
+                                               int64_t B, int64_t nh, int64_t T, int64_t hs,
+                                               int causal, float* o, const int64_t* o_strides,
+                                               float* l, void* stream) {
   if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
   if (B * nh * T == 0) return CTA_OK;
   if (!o || !l) return fail(CTA_ERR_INVALID_ARGUMENT, "null output pointer");
   if (!attn_layout_ok(q, q_strides) || !attn_layout_ok(k, k_strides) ||
-      !attn_layout_ok(v, v_strides) || !aligned16(o))
+      !attn_layout_ok(v, v_strides) || !attn_layout_ok(o, o_strides))
     return fail(CTA_ERR_LAYOUT,
                 "flash_attention_fwd needs unit d-stride, strides divisible by 4 and 16-byte "
                 "aligned Q/K/V/O");
   const RowStrides sq{q_strides[0], q_strides[1], q_strides[2]};
   const RowStrides sk{k_strides[0], k_strides[1], k_strides[2]};
   const RowStrides sv{v_strides[0], v_strides[1], v_strides[2]};
+  const RowStrides so{o_strides[0], o_strides[1], o_strides[2]};
   const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
   const int BH = (int)(B * nh);
   hipStream_t st = as_stream(stream);
-#define CTA_FWD(HS_)                                                                        \
-  if (causal) launch_fwd<HS_, true>(q, k, v, o, l, (int)nh, (int)T, BH, sq, sk, sv, scale, st); \
-  else launch_fwd<HS_, false>(q, k, v, o, l, (int)nh, (int)T, BH, sq, sk, sv, scale, st);
+#define CTA_FWD(HS_)                                                                           \
+  if (causal) launch_fwd<HS_, true>(q, k, v, o, l, (int)nh, (int)T, BH, sq, sk, sv, so, scale, st); \
+  else launch_fwd<HS_, false>(q, k, v, o, l, (int)nh, (int)T, BH, sq, sk, sv, so, scale, st);
   if (hs == 32) { CTA_FWD(32) }
   else if (hs == 64) { CTA_FWD(64) }
   else { CTA_FWD(128) }
 #undef CTA_FWD
   return check_launch("flash_attention_fwd");
+}
+
+extern "C" int cta_flash_attention_fwd(const float* q, const int64_t* q_strides, const float* k,
+                                       const int64_t* k_strides, const float* v,
+                                       const int64_t* v_strides, int64_t B, int64_t nh,
+                                       int64_t T, int64_t hs, int causal, float* o, float* l,
+                                       void* stream) {
+  const int64_t os[4] = {nh * T * hs, T * hs, hs, 1};  // dense (B, nh, T, hs)
+  return cta_flash_attention_fwd_strided(q, q_strides, k, k_strides, v, v_strides, B, nh, T, hs,
+                                         causal, o, os, l, stream);
 }

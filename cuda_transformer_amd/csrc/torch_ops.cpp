@@ -480,6 +480,29 @@ std::tuple<at::Tensor, at::Tensor> flash_attention_fwd(at::Tensor Q, at::Tensor 
   return {O, L};
 }
 
+// Workspace for the stored-dS schedule of the FP32 backward: every head's dS tiles up to
+// kBwdWorkspaceCap (chunked over heads beyond that).  If the allocator cannot supply it, the
+// kernels run the recompute schedule, which needs no workspace (ws_bytes = 0).
+at::Tensor bwd_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs, bool causal,
+                         const at::TensorOptions& opts, int64_t& ws_bytes) {
+  ws_bytes = std::min(cta_flash_attention_bwd_workspace(B, nh, T, hs, causal ? 1 : 0),
+                      kBwdWorkspaceCap);
+  at::Tensor ws;
+  if (ws_bytes > 0) {
+    try {
+      ws = at::empty({ws_bytes / static_cast<int64_t>(sizeof(float))}, opts);
+    } catch (const c10::OutOfMemoryError&) {
+      ws_bytes = 0;
+      TORCH_WARN_ONCE(
+          "flash_attention_bwd: the dS workspace could not be allocated; running the "
+          "recompute schedule (dQ recomputes S and dP, about 20% slower, same results to "
+          "rounding)");
+    }
+  }
+  last_bwd_schedule().store(ws_bytes > 0 ? 1 : 0);
+  return ws;
+}
+
 // 16-bit backward (extension): stored-dS schedule with a 16-bit dS workspace from torch's caching
 // allocator (the same 8 GiB cap as the FP32 op; chunked over heads beyond it).
 std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd_half(
@@ -566,24 +589,8 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd(at::Tensor Q,
   const auto qs = strides_of<4>(q), ks = strides_of<4>(k), vs = strides_of<4>(v),
              os = strides_of<4>(o), gs = strides_of<4>(g);
   const auto ls = strides_of<3>(L);
-  // Workspace for the stored-dS schedule: every head's dS tiles up to kBwdWorkspaceCap
-  // (chunked over heads beyond that).  If the allocator cannot supply it, the kernels run
-  // the recompute schedule, which needs no workspace.
-  int64_t ws_bytes = std::min(cta_flash_attention_bwd_workspace(B, nh, T, hs, causal ? 1 : 0),
-                              kBwdWorkspaceCap);
-  at::Tensor ws;
-  if (ws_bytes > 0) {
-    try {
-      ws = at::empty({ws_bytes / static_cast<int64_t>(sizeof(float))}, Q.options());
-    } catch (const c10::OutOfMemoryError&) {
-      ws_bytes = 0;
-      TORCH_WARN_ONCE(
-          "flash_attention_bwd: the dS workspace could not be allocated; running the "
-          "recompute schedule (dQ recomputes S and dP, about 20% slower, same results to "
-          "rounding)");
-    }
-  }
-  last_bwd_schedule().store(ws_bytes > 0 ? 1 : 0);
+  int64_t ws_bytes = 0;
+  const at::Tensor ws = bwd_workspace(B, nh, T, hs, causal, Q.options(), ws_bytes);
   check_rc(cta_flash_attention_bwd(q.data_ptr<float>(), qs.data(), k.data_ptr<float>(), ks.data(),
                                    v.data_ptr<float>(), vs.data(), o.data_ptr<float>(), os.data(),
                                    g.data_ptr<float>(), gs.data(), L.data_ptr<float>(), ls.data(),
@@ -593,6 +600,84 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd(at::Tensor Q,
                                    ws_bytes > 0 ? ws.data_ptr<float>() : nullptr, ws_bytes,
                                    stream_of(Q)));
   return {dQ, dK, dV};
+}
+
+// ------------------------------------------------------------------ packed-qkv FlashAttention-2
+// New ops with no reference counterpart: the attention of a packed (B, T, 3C) projection
+// (C = nh * hs; Q, K, V its three column blocks, head h in columns h*hs .. h*hs + hs - 1 of
+// each), as gpt.py:104-107 slices it, with the output O in the same head-interleaved (B, T, C)
+// order and the gradient as one (B, T, 3C) tensor.  The kernels read the column blocks in place
+// and write O and dQ/dK/dV through strides, so the head transposes, the copies behind them and
+// the concatenation of dq, dk and dv disappear.  Same kernels and results as
+// flash_attention_fwd / flash_attention_bwd on the head views.
+
+// A (B, T, n) activation the kernels can address: unit last stride, strides divisible by 4,
+// 16-byte aligned.
+at::Tensor packed_operand(const at::Tensor& t) {
+  const bool ok = t.stride(2) == 1 && t.stride(0) % 4 == 0 && t.stride(1) % 4 == 0 &&
+                  (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) == 0;
+  return ok ? t : dense(t);
+}
+
+int64_t packed_head_size(const at::Tensor& qkv, int64_t nh) {
+  TORCH_CHECK(qkv.dim() == 3, "qkv must be a 3D tensor (B, T, 3C)");
+  TORCH_CHECK(qkv.is_cuda(), "qkv must be a CUDA tensor");
+  check_f32(qkv, "qkv");
+  TORCH_CHECK(nh > 0 && qkv.size(2) % (3 * nh) == 0, "qkv.size(2) must be 3 * nh * hs");
+  const int64_t hs = qkv.size(2) / (3 * nh);
+  if (hs != 32 && hs != 64 && hs != 128)
+    TORCH_CHECK(false, "Unsupported head dimension! Only hs=32, hs=64, and hs=128 are supported.");
+  return hs;
+}
+
+std::tuple<at::Tensor, at::Tensor> flash_attention_qkv_fwd(at::Tensor qkv, int64_t nh,
+                                                           bool causal) {
+  const int64_t hs = packed_head_size(qkv, nh);
+  const int64_t B = qkv.size(0), T = qkv.size(1), C = nh * hs;
+  c10::OptionalDeviceGuard guard(qkv.device());
+  at::Tensor out = at::empty({B, T, C}, qkv.options());
+  at::Tensor L = at::empty({B, nh, T}, qkv.options());
+  const at::Tensor x = packed_operand(qkv);
+  const float* p = x.data_ptr<float>();
+  const int64_t xs[4] = {x.stride(0), hs, x.stride(1), 1};  // one column block as (B, nh, T, hs)
+  const int64_t os[4] = {T * C, hs, C, 1};
+  check_rc(cta_flash_attention_fwd_strided(p, xs, p + C, xs, p + 2 * C, xs, B, nh, T, hs,
+                                           causal ? 1 : 0, out.data_ptr<float>(), os,
+                                           L.data_ptr<float>(), stream_of(qkv)));
+  return {out, L};
+}
+
+at::Tensor flash_attention_qkv_bwd(at::Tensor qkv, at::Tensor out, at::Tensor dout,
+                                   at::Tensor L, int64_t nh, bool causal) {
+  const int64_t hs = packed_head_size(qkv, nh);
+  const int64_t B = qkv.size(0), T = qkv.size(1), C = nh * hs;
+  TORCH_CHECK(out.is_cuda() && dout.is_cuda() && L.is_cuda(),
+              "out, dout and L must be CUDA tensors");
+  for (const auto* t : {&out, &dout, &L}) check_f32(*t, "input");
+  TORCH_CHECK(out.dim() == 3 && out.size(0) == B && out.size(1) == T && out.size(2) == C &&
+                  dout.sizes() == out.sizes(),
+              "out and dout must be (B, T, C)");
+  TORCH_CHECK(L.dim() == 3 && L.size(0) == B && L.size(1) == nh && L.size(2) == T,
+              "L must be (B, nh, T)");
+  c10::OptionalDeviceGuard guard(qkv.device());
+  at::Tensor dqkv = at::empty({B, T, 3 * C}, qkv.options());
+  at::Tensor delta = at::empty({B, nh, T}, qkv.options());
+  const at::Tensor x = packed_operand(qkv), o = packed_operand(out), g = packed_operand(dout);
+  const float* p = x.data_ptr<float>();
+  float* d = dqkv.data_ptr<float>();
+  const int64_t xs[4] = {x.stride(0), hs, x.stride(1), 1};
+  const int64_t os[4] = {o.stride(0), hs, o.stride(1), 1};
+  const int64_t gs[4] = {g.stride(0), hs, g.stride(1), 1};
+  const int64_t ds[4] = {T * 3 * C, hs, 3 * C, 1};
+  const auto ls = strides_of<3>(L);
+  int64_t ws_bytes = 0;
+  const at::Tensor ws = bwd_workspace(B, nh, T, hs, causal, qkv.options(), ws_bytes);
+  check_rc(cta_flash_attention_bwd_strided(
+      p, xs, p + C, xs, p + 2 * C, xs, o.data_ptr<float>(), os, g.data_ptr<float>(), gs,
+      L.data_ptr<float>(), ls.data(), B, nh, T, hs, causal ? 1 : 0, d, ds, d + C, ds, d + 2 * C,
+      ds, delta.data_ptr<float>(), ws_bytes > 0 ? ws.data_ptr<float>() : nullptr, ws_bytes,
+      stream_of(qkv)));
+  return dqkv;
 }
 
 }  // namespace
@@ -618,6 +703,10 @@ TORCH_LIBRARY(cuda_transformer, m) {
   m.def(
       "flash_attention_bwd(Tensor Q, Tensor K, Tensor V, Tensor O, Tensor dO, Tensor L, bool "
       "causal) -> (Tensor, Tensor, Tensor)");
+  m.def("flash_attention_qkv_fwd(Tensor qkv, int nh, bool causal) -> (Tensor, Tensor)");
+  m.def(
+      "flash_attention_qkv_bwd(Tensor qkv, Tensor out, Tensor dout, Tensor L, int nh, bool "
+      "causal) -> Tensor");
   m.def("layernorm_fwd(Tensor x, Tensor gamma, Tensor beta, float eps) -> (Tensor, Tensor, Tensor)");
   m.def(
       "layernorm_bwd(Tensor x, Tensor gamma, Tensor mean, Tensor rstd, Tensor dy) -> "
@@ -641,6 +730,8 @@ TORCH_LIBRARY_IMPL(cuda_transformer, CUDA, m) {
   m.impl("causal_self_attention_bwd", &causal_self_attention_bwd);
   m.impl("flash_attention_fwd", &flash_attention_fwd);
   m.impl("flash_attention_bwd", &flash_attention_bwd);
+  m.impl("flash_attention_qkv_fwd", &flash_attention_qkv_fwd);
+  m.impl("flash_attention_qkv_bwd", &flash_attention_qkv_bwd);
   m.impl("layernorm_fwd", &layernorm_fwd);
   m.impl("layernorm_bwd", &layernorm_bwd);
 }

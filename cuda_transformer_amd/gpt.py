@@ -18,8 +18,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .autograd_fns import (CudaFlashAttention, CudaGeluLayer, CudaLayerNorm, CudaLinearLayer,
-                           CudaMLP)
+from .autograd_fns import (CudaFlashAttention, CudaFlashAttentionQKV, CudaGeluLayer, CudaLayerNorm,
+                           CudaLinearLayer, CudaMLP)
 
 
 @dataclass
@@ -35,6 +35,10 @@ class GPTConfig:
     # MLP as one CudaMLP (GELU folded into the fc1 forward and fc2 dx GEMM epilogues; same
     # bits) instead of the reference's CudaLinearLayer -> CudaGeluLayer -> CudaLinearLayer.
     fused_mlp: bool = True
+    # Attention on the packed qkv projection (CudaFlashAttentionQKV: O and the qkv gradient
+    # written in the packed layouts) instead of the reference's head views, transposes and
+    # concatenation around CudaFlashAttention; same kernels, same bits.
+    packed_attention: bool = True
 
 
 class LayerNorm(nn.Module):
@@ -73,14 +77,19 @@ class CausalSelfAttention(nn.Module):
         self.out_bias = nn.Parameter(torch.zeros(d))
         nn.init.normal_(self.qkv_weight, mean=0.0, std=cfg.init_std)
         nn.init.normal_(self.out_weight, mean=0.0, std=cfg.init_std)
+        self.packed = cfg.packed_attention
 
     def forward(self, x):
         B, T, C = x.shape
         qkv = CudaLinearLayer.apply(x, self.qkv_weight, self.qkv_bias)
-        q, k, v = (t.reshape(B, T, self.num_heads, self.head_dim).transpose(1, 2)
-                   for t in qkv.chunk(3, dim=-1))
-        att, _ = CudaFlashAttention.apply(q, k, v, True)
-        att = att.transpose(1, 2).reshape(B, T, C)
+        if self.packed:
+            # heads read from and written to the packed layouts in place
+            att = CudaFlashAttentionQKV.apply(qkv, self.num_heads, True)
+        else:
+            q, k, v = (t.reshape(B, T, self.num_heads, self.head_dim).transpose(1, 2)
+                       for t in qkv.chunk(3, dim=-1))
+            att, _ = CudaFlashAttention.apply(q, k, v, True)
+            att = att.transpose(1, 2).reshape(B, T, C)
         return CudaLinearLayer.apply(att, self.out_weight, self.out_bias)
 
 

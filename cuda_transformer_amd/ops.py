@@ -25,6 +25,7 @@ __all__ = [
     "gelu_activation", "gelu_activation_bwd", "gelu_tanh_activation", "gelu_tanh_activation_bwd",
     "causal_self_attention_fwd", "causal_self_attention_bwd",
     "flash_attention_fwd", "flash_attention_bwd",
+    "flash_attention_qkv_fwd", "flash_attention_qkv_bwd",
     "layernorm_fwd", "layernorm_bwd",
 ]
 
@@ -267,6 +268,41 @@ def _(Q, K, V, O, dO, L, causal):
         _f32(Q, K, V, O, dO, L)
     _same_device(Q, K, V, O, dO, L)
     return torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
+
+
+# ----------------------------------------------------------------- packed-qkv FA2 (added)
+def flash_attention_qkv_fwd(qkv: Tensor, nh: int, causal: bool) -> tuple[Tensor, Tensor]:
+    """FA2 forward on a packed (B, T, 3C) projection -> (out (B, T, C), L (B, nh, T)).
+
+    Q, K, V are qkv's three column blocks with head h in columns h*hs .. h*hs + hs - 1 (the
+    slicing of gpt/gpt.py:104-107); out holds O in the same head-interleaved order.  The same
+    kernel as flash_attention_fwd on the head views, read and written in place (no transposes)."""
+    return _ops.flash_attention_qkv_fwd.default(qkv, nh, causal)
+
+
+@torch.library.register_fake("cuda_transformer::flash_attention_qkv_fwd")
+def _(qkv, nh, causal):
+    _f32(qkv)
+    torch._check(qkv.dim() == 3 and qkv.size(2) % (3 * nh) == 0,
+                 lambda: "qkv.size(2) must be 3 * nh * hs")
+    B, T, C = qkv.size(0), qkv.size(1), qkv.size(2) // 3
+    out = torch.empty((B, T, C), dtype=qkv.dtype, device=qkv.device)
+    L = torch.empty((B, nh, T), dtype=torch.float32, device=qkv.device)
+    return out, L
+
+
+def flash_attention_qkv_bwd(qkv: Tensor, out: Tensor, dout: Tensor, L: Tensor, nh: int,
+                            causal: bool) -> Tensor:
+    """FA2 backward of flash_attention_qkv_fwd -> d(qkv) (B, T, 3C), the gradients of the three
+    column blocks written in place of one another's concatenation."""
+    return _ops.flash_attention_qkv_bwd.default(qkv, out, dout, L, nh, causal)
+
+
+@torch.library.register_fake("cuda_transformer::flash_attention_qkv_bwd")
+def _(qkv, out, dout, L, nh, causal):
+    _f32(qkv, out, dout, L)
+    _same_device(qkv, out, dout, L)
+    return torch.empty_like(qkv, memory_format=torch.contiguous_format)
 
 
 # ----------------------------------------------------------------- LayerNorm (added)

@@ -59,6 +59,18 @@ int cta_flash_attention_fwd(const float* q, const int64_t* q_strides,
                             int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
                             float* o, float* l, void* stream);
 
+/* Forward with O written through caller strides (4 entries (b, h, t, d), the same layout rules
+ * as Q/K/V): e.g. straight into a (B, T, nh*hs) tensor, strides (T*nh*hs, hs, nh*hs, 1), which
+ * the projection after attention reads without a transpose copy.  L dense as above.  Same
+ * kernel and results as cta_flash_attention_fwd, which is this call with dense strides.  No
+ * counterpart in the reference's launchers (their outputs are always dense); for callers with
+ * packed (B, T, 3C) projections, such as the GPT harness. */
+int cta_flash_attention_fwd_strided(const float* q, const int64_t* q_strides,
+                                    const float* k, const int64_t* k_strides,
+                                    const float* v, const int64_t* v_strides,
+                                    int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                                    float* o, const int64_t* o_strides, float* l, void* stream);
+
 /* Forward with BF16 Q, K, V (stored as uint16_t bit patterns) and FP32 accumulation: O dense
  * (B,nh,T,hs) in BF16, L dense (B,nh,T) in FP32, L = rowmax + ln(rowsum) as above.  hs in
  * {32, 64, 128}.  Q/K/V strides: unit d-stride, other strides divisible by 8, 16-byte aligned
@@ -103,6 +115,23 @@ int cta_flash_attention_bwd(const float* q, const int64_t* q_strides,
                             int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
                             float* dq, float* dk, float* dv, float* delta,
                             float* workspace, int64_t workspace_bytes, void* stream);
+
+/* Backward with dQ, dK and dV written through caller strides (4 entries each, the same layout
+ * rules as Q/K/V): e.g. into the three column blocks of one (B, T, 3*nh*hs) gradient of a
+ * packed qkv projection.  Same kernels, schedules and results as cta_flash_attention_bwd,
+ * which is this call with dense output strides.  No counterpart in the reference's launchers;
+ * for callers with packed projections, such as the GPT harness. */
+int cta_flash_attention_bwd_strided(const float* q, const int64_t* q_strides,
+                                    const float* k, const int64_t* k_strides,
+                                    const float* v, const int64_t* v_strides,
+                                    const float* o, const int64_t* o_strides,
+                                    const float* d_o, const int64_t* do_strides,
+                                    const float* l, const int64_t* l_strides,
+                                    int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                                    float* dq, const int64_t* dq_strides, float* dk,
+                                    const int64_t* dk_strides, float* dv,
+                                    const int64_t* dv_strides, float* delta, float* workspace,
+                                    int64_t workspace_bytes, void* stream);
 
 /* Largest B*nh*T that cta_flash_attention_bwd_noalloc accepts: 8,388,608 query rows, one float of
  * delta each in a 32 MiB device array. */

@@ -214,6 +214,71 @@ def test_fa2_through_c_abi(cuda):
                   s4, B, nh, T, 96, 1, O.data_ptr(), L.data_ptr(), st)
 
 
+PACKED_SHAPES = [(2, 65, 3, 64, True), (1, 257, 2, 32, False), (2, 130, 2, 128, True),
+                 (4, 256, 6, 64, True), (1, 1, 2, 64, True)]
+
+
+@pytest.mark.parametrize("B,T,nh,hs,causal", PACKED_SHAPES)
+def test_fa2_packed_qkv_matches_head_views(cuda, B, T, nh, hs, causal):
+    """flash_attention_qkv_fwd/bwd on a packed (B, T, 3C) projection against the reference's
+    route (head views of qkv, flash_attention_fwd/bwd, transposes and concatenation): the same
+    kernels read the same values, so O, L and every gradient agree bit for bit."""
+    from cuda_autograd_fns import CudaFlashAttentionQKV
+    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+    from cuda_transformer_amd.ops import flash_attention_qkv_bwd, flash_attention_qkv_fwd
+
+    C = nh * hs
+    qkv = seeded((B, T, 3 * C), 91).to(cuda)
+    dout = seeded((B, T, C), 92, kind="rand").to(cuda)
+    q, k, v = (t.reshape(B, T, nh, hs).transpose(1, 2) for t in qkv.chunk(3, dim=-1))
+    O, L = flash_attention_fwd(q, k, v, causal)
+    out, L2 = flash_attention_qkv_fwd(qkv, nh, causal)
+    assert torch.equal(out, O.transpose(1, 2).reshape(B, T, C)) and torch.equal(L2, L)
+    dq, dk, dv = flash_attention_bwd(q, k, v, O, dout.reshape(B, T, nh, hs).transpose(1, 2), L,
+                                     causal)
+    ref = torch.cat([g.transpose(1, 2).reshape(B, T, C) for g in (dq, dk, dv)], dim=-1)
+    dqkv = flash_attention_qkv_bwd(qkv, out, dout, L2, nh, causal)
+    assert torch.equal(dqkv, ref)
+    x = qkv.clone().requires_grad_()
+    y = CudaFlashAttentionQKV.apply(x, nh, causal)
+    y.backward(dout)
+    assert torch.equal(y.detach(), out) and torch.equal(x.grad, ref)
+    # one head against the float64 oracle
+    qh, kh, vh = (f64(t[:1, :1]) for t in (q, k, v))
+    O_ref, _ = ora.reference_attention(qh, kh, vh, causal)
+    assert np.abs(f64(out[:1, :, :hs]).reshape(1, 1, T, hs) - O_ref).max() <= 1e-4
+
+
+def test_fa2_strided_outputs_recompute_schedule(cuda):
+    """cta_flash_attention_bwd_strided without a workspace (the reference's recompute schedule)
+    writes through the same output strides: dK, dV bitwise equal to the stored-dS schedule's,
+    dQ within rounding."""
+    from cuda_transformer_amd import capi
+    from cuda_transformer_amd.ops import flash_attention_qkv_bwd, flash_attention_qkv_fwd
+
+    lib = capi.lib()
+    B, T, nh, hs = 2, 200, 2, 64
+    C = nh * hs
+    qkv = seeded((B, T, 3 * C), 93).to(cuda)
+    dout = seeded((B, T, C), 94, kind="rand").to(cuda)
+    out, L = flash_attention_qkv_fwd(qkv, nh, True)
+    stored = flash_attention_qkv_bwd(qkv, out, dout, L, nh, True)
+    d = torch.full((B, T, 3 * C), float("nan"), device=cuda)
+    delta = torch.empty(B, nh, T, device=cuda)
+    P = lambda t, off=0: t.data_ptr() + 4 * off  # noqa: E731
+    xs = capi.strides((T * 3 * C, hs, 3 * C, 1))
+    os_ = capi.strides((T * C, hs, C, 1))
+    ls = capi.strides(L.stride())
+    rc = lib.cta_flash_attention_bwd_strided(
+        P(qkv), xs, P(qkv, C), xs, P(qkv, 2 * C), xs, P(out), os_, P(dout), os_, P(L), ls, B, nh,
+        T, hs, 1, P(d), xs, P(d, C), xs, P(d, 2 * C), xs, P(delta), None, 0,
+        torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.cta_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(d[..., C:], stored[..., C:])
+    assert (d[..., :C] - stored[..., :C]).abs().max().item() <= 1e-5
+
+
 def test_fa2_config2_full_size(cuda):
     """Benchmark config 2 (B4 H32 N4096 D64, causal) at full size: two heads against the
     float64 oracle, and on every head the size-independent invariants of the backward:
