@@ -324,8 +324,26 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
   const int half = lane >> 5, col = lane & 31;
   const int wm = wave / TL::WN, wn = wave % TL::WN;
 
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-  const int z = blockIdx.z % Z, split = blockIdx.z / Z;
+  // Without a K split: the output tiles of all batches in one row-major list (batch, m, n; n
+  // fastest), each XCD walking a contiguous run of it, so the workgroups that share an A row
+  // block run on one XCD and read it into one L2.  Split along K: tile (x, y), z = split * Z +
+  // batch.
+  int n0, m0, z, split;
+  if (split_ws == nullptr) {
+    const int ntn = (N + BN - 1) / BN, ntiles = ntn * ((M + BM - 1) / BM);
+    const int w = xcd_work_item(blockIdx.x, ntiles * Z);
+    if (w >= ntiles * Z) return;
+    z = w / ntiles;
+    const int t = w - z * ntiles;
+    n0 = (t % ntn) * BN;
+    m0 = (t / ntn) * BM;
+    split = 0;
+  } else {
+    n0 = blockIdx.x * BN;
+    m0 = blockIdx.y * BM;
+    z = blockIdx.z % Z;
+    split = blockIdx.z / Z;
+  }
   const int zo = z / zin, zi = z - zo * zin;
   const float* Ab = A.p + zo * A.s_outer + zi * A.s_inner;
   const float* Bb = B.p + zo * B.s_outer + zi * B.s_inner;
@@ -547,9 +565,13 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
     return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM output row stride too large");
   const int64_t kchunk =
       S > 1 ? ((K + S - 1) / S + TL::BK - 1) / TL::BK * TL::BK : std::max<int64_t>(K, 1);
-  const dim3 grid((unsigned)((N + TL::BN - 1) / TL::BN), (unsigned)((M + TL::BM - 1) / TL::BM),
-                  (unsigned)(Z * S));
-  if (grid.y > 65535 || grid.z > 65535) return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM grid too large");
+  const int64_t ntiles = ((N + TL::BN - 1) / TL::BN) * ((M + TL::BM - 1) / TL::BM);
+  if (ntiles * Z > INT32_MAX - kNumXcds || Z * S > 65535)
+    return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM grid too large");
+  const dim3 grid = S > 1 ? dim3((unsigned)((N + TL::BN - 1) / TL::BN),
+                                 (unsigned)((M + TL::BM - 1) / TL::BM), (unsigned)(Z * S))
+                          : dim3(xcd_grid(ntiles * Z), 1, 1);
+  if (grid.y > 65535) return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM grid too large");
   float* ws = S > 1 ? workspace : nullptr;
   const int am = pick_mode(A, true, M, K);
   const int bm = pick_mode(B, false, N, K);

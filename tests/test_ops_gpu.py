@@ -344,6 +344,22 @@ def test_linear_ragged_k_vector_loads(cuda, M, K, N):
     assert rel_err(f64(out), np.swapaxes(f64(x), 1, 2) @ f64(dy)) <= 1e-6
 
 
+@pytest.mark.parametrize("B,M,K,N", [(64, 256, 384, 1152), (3, 130, 64, 200), (9, 16, 32, 8)])
+def test_linear_batched_tiles_over_xcds(cuda, B, M, K, N):
+    """Batched products spread the tiles of all batches over the XCDs as one list: every tile of
+    every batch is computed once (batches with few tiles each, as in the GPT's layers)."""
+    from cuda_transformer.ops import cuda_fma
+
+    x = seeded((B, M, K), 51).to(cuda)
+    w = seeded((K, N), 52).to(cuda) * 0.1
+    b = seeded((N,), 53).to(cuda)
+    out = cuda_fma(x, w, b)
+    assert rel_err(f64(out), f64(x) @ f64(w) + f64(b)) <= 1e-6
+    wb = seeded((B, K, N), 54).to(cuda)                 # per-batch weights
+    out = cuda_fma(x, wb, b)
+    assert rel_err(f64(out), f64(x) @ f64(wb) + f64(b)) <= 1e-6
+
+
 def test_linear_operand_strides_past_buffer_offsets(cuda):
     """Operand views whose strides put a tile's rows more than 2 GiB apart cannot be addressed
     with 32-bit buffer offsets; they take the scalar load path and stay exact."""
