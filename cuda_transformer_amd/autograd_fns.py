@@ -14,7 +14,8 @@ Deviations, each a fix:
   scales dq and dk (test/test_causal_self_attn.py:67).
 * ``CudaLinearLayer.backward`` allocates its zero bias on dy's device instead of the
   hard-coded 'cuda' device, and computes dW as one GEMM over the flattened (batch*m) axis
-  instead of a per-batch GEMM followed by ``torch.sum(dim=0)`` (same sum, fewer bytes).
+  instead of a per-batch GEMM followed by ``torch.sum(dim=0)`` (same sum, fewer bytes).  With
+  2-D weights that GEMM also produces db (``linear_weight_bias_grad``): dy is read once.
   Its zero bias is one cached read-only tensor per (length, dtype, device) rather than a new
   ``torch.zeros`` (a fill launch) on every backward.
 """
@@ -24,6 +25,7 @@ from .ops import (
     causal_self_attention_bwd, causal_self_attention_fwd, cuda_fma, cuda_fma_gelu,
     cuda_fma_gelu_grad, cuda_fma_gelu_tanh, cuda_fma_gelu_tanh_grad, cuda_softmax, cuda_softmax_bwd, db_calculation, flash_attention_bwd, flash_attention_fwd, flash_attention_qkv_bwd, flash_attention_qkv_fwd, gelu_activation,
     gelu_activation_bwd, gelu_tanh_activation, gelu_tanh_activation_bwd, layernorm_bwd, layernorm_fwd,
+    linear_weight_bias_grad,
 )
 
 __all__ = [
@@ -104,15 +106,11 @@ class CudaLinearLayer(torch.autograd.Function):
 
 def _weight_and_bias_grads(x, weights, dy):
     """dW = sum_b x[b]^T dy[b] and db = sum of dy over (batch, rows) (cuda_linear_layer.py:21-27)."""
-    k, n = x.shape[-1], dy.shape[-1]
-    zero_n = _zeros(n, dy)
     if weights.dim() == 2:
-        # sum_b x[b]^T dy[b] == (x as (b*m, k))^T (dy as (b*m, n)): one GEMM, K = b*m
-        x2 = x.reshape(1, -1, k)
-        dy2 = dy.reshape(1, -1, n)
-        dw = cuda_fma(x2.transpose(1, 2), dy2, zero_n)[0]
-    else:
-        dw = cuda_fma(x.transpose(1, 2), dy, zero_n)
+        # sum_b x[b]^T dy[b] == (x as (b*m, k))^T (dy as (b*m, n)): one GEMM, K = b*m, which
+        # also sums dy's columns for db as it streams them
+        return linear_weight_bias_grad(x, dy)
+    dw = cuda_fma(x.transpose(1, 2), dy, _zeros(dy.shape[-1], dy))
     return dw, db_calculation(dy)
 
 

@@ -310,7 +310,10 @@ __device__ __forceinline__ void block_store(const f32x16 (&acc)[TL::MB][TL::NB],
 // split_ws == nullptr: out = alpha * A B (+ bias, mask) written through C.
 // split_ws != nullptr: blockIdx.z = s * Z + z covers K range [s*kchunk, (s+1)*kchunk) and the raw
 // partial sum goes to split_ws[s][z][m][n] (dense); gemm_splitk_reduce finishes the epilogue.
-template <class TL, int AMODE, int BMODE, int ACT>
+// CS (Z == 1, B in kVecMN mode): the workgroups of the first row of tiles also sum B's columns
+// over their K range, into ep.colsum or, split, into row s of the [S][N] block that follows
+// the partial products.
+template <class TL, int AMODE, int BMODE, int ACT, bool CS = false>
 __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOperand B,
                                                            GemmOut C, GemmEpilogue ep, int M,
                                                            int N, int K, int zin, int Z,
@@ -363,6 +366,22 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
   LA la0, la1;
   LB lb0, lb1;
   const int nk = (ke - kb + BK - 1) / BK;
+  static_assert(!CS || BMODE == kVecMN, "column sums come from n-contiguous B slices");
+
+  // CS: each lane's B float4s hold the same four columns at the same k residue in every slice,
+  // so the lane sums them as the slices pass through its registers (slices past the end are
+  // zero); the lanes of one column group are combined after the loop.
+  float4 cs[CS ? LB::LOADS : 1];
+  auto add_cs = [&](const LB& lb) {
+    if constexpr (CS) {
+#pragma unroll
+      for (int u = 0; u < LB::LOADS; ++u) {
+        cs[u].x += lb.v[u].x; cs[u].y += lb.v[u].y; cs[u].z += lb.v[u].z; cs[u].w += lb.v[u].w;
+      }
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < (CS ? LB::LOADS : 1); ++u) cs[u] = zero4();
 
   f32x16 acc[MB][NB];
 #pragma unroll
@@ -381,6 +400,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
   pb.load(lb1, 1, tid);
   store_slice(la0, smem, tid);
   store_slice(lb0, smem + BM * KP, tid);
+  add_cs(lb0);
   __syncthreads();
 
   // Each slice's MFMAs run in two parts around the barrier that publishes the next slice.  The
@@ -406,7 +426,9 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
     mma_chunks<TL, 0, KC / 2>(f0, acc);
     store_slice(la1, buf1, tid);
     store_slice(lb1, buf1 + BM * KP, tid);
+    add_cs(lb1);
     sched_first_part<0, NM1, NVM, NDW>();
+    if constexpr (CS) __builtin_amdgcn_sched_group_barrier(0x002, 4 * LB::LOADS, 0);  // sums last
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
@@ -421,7 +443,9 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
     mma_chunks<TL, 0, KC / 2>(f1, acc);
     store_slice(la0, buf0, tid);
     store_slice(lb0, buf0 + BM * KP, tid);
+    add_cs(lb0);
     sched_first_part<0, NM1, NVM, NDW>();
+    if constexpr (CS) __builtin_amdgcn_sched_group_barrier(0x002, 4 * LB::LOADS, 0);  // sums last
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
@@ -430,6 +454,30 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
     __builtin_amdgcn_sched_group_barrier(0x100, NDR, 0);
     __builtin_amdgcn_sched_group_barrier(0x008, NM1, 0);
     __builtin_amdgcn_sched_barrier(0);
+  }
+
+  if constexpr (CS) {
+    if (m0 == 0) {
+      // Lanes f with the same f / BK share a column group (BK consecutive lanes of one wave).
+      float* out = split_ws ? split_ws + (int64_t)gridDim.z * M * N + (int64_t)split * N
+                            : ep.colsum;
+#pragma unroll
+      for (int u = 0; u < LB::LOADS; ++u) {
+        float4 v = cs[u];
+#pragma unroll
+        for (int off = 1; off < BK; off <<= 1) {
+          v.x += __shfl_xor(v.x, off);
+          v.y += __shfl_xor(v.y, off);
+          v.z += __shfl_xor(v.z, off);
+          v.w += __shfl_xor(v.w, off);
+        }
+        const int f = tid + TL::THREADS * u;
+        const int n = n0 + (f / BK) * 4;
+        if (f % BK == 0 && n < N) {  // N % 4 == 0: the whole group is in range
+          out[n] = v.x; out[n + 1] = v.y; out[n + 2] = v.z; out[n + 3] = v.w;
+        }
+      }
+    }
   }
 
   const int mw = m0 + wm * (BM / TL::WM), nw = n0 + wn * (BN / TL::WN);
@@ -448,14 +496,23 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
     block_store<TL, ACT, false, false>(acc, Cz, Xz, C.s_row, ep, M, N, mw, nw, half, col);
 }
 
-// Fixed-order sum of the split-K partials plus the epilogue of gemm_kernel.
+// Fixed-order sum of the split-K partials plus the epilogue of gemm_kernel; with ep.colsum also
+// of the per-split column sums stored after them.
 __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float* __restrict__ ws, int S,
                                                           int Z, int M, int N, GemmOut C,
                                                           GemmEpilogue ep, int zin) {
   const int64_t total = (int64_t)Z * M * N;
   const int64_t plane = total;
-  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total;
+  const int64_t all = total + (ep.colsum ? N : 0);
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < all;
        e += (int64_t)gridDim.x * 256) {
+    if (e >= total) {
+      const float* p = ws + (int64_t)S * plane + (e - total);
+      float t = p[0];
+      for (int s = 1; s < S; ++s) t += p[(int64_t)s * N];
+      ep.colsum[e - total] = t;
+      continue;
+    }
     float acc = ws[e];
     for (int s = 1; s < S; ++s) acc += ws[(int64_t)s * plane + e];
     const int64_t z = e / ((int64_t)M * N);
@@ -497,11 +554,16 @@ int pick_mode(const GemmOperand& op, bool is_a, int64_t rows, int64_t K) {
   return kScalar;
 }
 
-template <class TL, int AM, int ACT>
+template <class TL, int AM, int ACT, bool CS>
 void dispatch_b(int bm, dim3 grid, hipStream_t st, const GemmOperand& A, const GemmOperand& B,
                 const GemmOut& C, const GemmEpilogue& ep, int M, int N, int K, int zin, int Z,
                 int kchunk, float* ws) {
   const dim3 block(TL::THREADS);
+  if constexpr (CS) {  // the launcher has checked bm == kVecMN
+    hipLaunchKernelGGL((gemm_kernel<TL, AM, kVecMN, ACT, true>), grid, block, 0, st, A, B, C, ep,
+                       M, N, K, zin, Z, kchunk, ws);
+    return;
+  }
   if (bm == kVecK)
     hipLaunchKernelGGL((gemm_kernel<TL, AM, kVecK, ACT>), grid, block, 0, st, A, B, C, ep, M, N,
                        K, zin, Z, kchunk, ws);
@@ -513,16 +575,16 @@ void dispatch_b(int bm, dim3 grid, hipStream_t st, const GemmOperand& A, const G
                        N, K, zin, Z, kchunk, ws);
 }
 
-template <class TL, int ACT>
+template <class TL, int ACT, bool CS = false>
 void dispatch_a(int am, int bm, dim3 grid, hipStream_t st, const GemmOperand& A,
                 const GemmOperand& B, const GemmOut& C, const GemmEpilogue& ep, int M, int N,
                 int K, int zin, int Z, int kchunk, float* ws) {
   if (am == kVecK)
-    dispatch_b<TL, kVecK, ACT>(bm, grid, st, A, B, C, ep, M, N, K, zin, Z, kchunk, ws);
+    dispatch_b<TL, kVecK, ACT, CS>(bm, grid, st, A, B, C, ep, M, N, K, zin, Z, kchunk, ws);
   else if (am == kVecMN)
-    dispatch_b<TL, kVecMN, ACT>(bm, grid, st, A, B, C, ep, M, N, K, zin, Z, kchunk, ws);
+    dispatch_b<TL, kVecMN, ACT, CS>(bm, grid, st, A, B, C, ep, M, N, K, zin, Z, kchunk, ws);
   else
-    dispatch_b<TL, kScalar, ACT>(bm, grid, st, A, B, C, ep, M, N, K, zin, Z, kchunk, ws);
+    dispatch_b<TL, kScalar, ACT, CS>(bm, grid, st, A, B, C, ep, M, N, K, zin, Z, kchunk, ws);
 }
 
 // K splits for a GEMM whose output tiles alone cannot fill the 256 CUs (1 = no split).  The
@@ -559,7 +621,8 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || Z > 65535 || zin <= 0)
     return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM size out of range");
   int64_t S = splitk_factor<TL>(M, N, K, Z);
-  if (S > 1 && (workspace == nullptr || workspace_floats < S * Z * M * N)) S = 1;
+  const int64_t cs_floats = ep.colsum ? N : 0;  // per split
+  if (S > 1 && (workspace == nullptr || workspace_floats < S * (Z * M * N + cs_floats))) S = 1;
   // A wave's output block is stored through 32-bit buffer offsets from its origin.
   if ((int64_t)TL::BM * std::max<int64_t>(C.s_row, N) * 4 >= ((int64_t)1 << 31))
     return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM output row stride too large");
@@ -578,7 +641,12 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
   // Split-K partials are stored raw; the reduction applies the epilogue's pointwise stage.
   const int act = S > 1 ? kActNone : ep.act;
   const int iM = (int)M, iN = (int)N, iK = (int)K, izin = (int)zin, iZ = (int)Z, ikc = (int)kchunk;
-  if (act == kActGelu)
+  if (ep.colsum) {
+    if (Z != 1 || bm != kVecMN || ep.act != kActNone || ep.causal_mask)
+      return fail(CTA_ERR_INVALID_ARGUMENT,
+                  "GEMM column sums need one batch, an n-contiguous B and no pointwise stage");
+    dispatch_a<TL, kActNone, true>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
+  } else if (act == kActGelu)
     dispatch_a<TL, kActGelu>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
   else if (act == kActGeluGrad)
     dispatch_a<TL, kActGeluGrad>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
@@ -590,7 +658,7 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
   else
     dispatch_a<TL, kActNone>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
   if (S > 1) {
-    const int64_t total = Z * M * N;
+    const int64_t total = Z * M * N + cs_floats;
     const unsigned rgrid = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
     hipLaunchKernelGGL(gemm_splitk_reduce, dim3(rgrid), dim3(256), 0, st, ws, (int)S, (int)Z,
                        (int)M, (int)N, C, ep, (int)zin);
@@ -608,9 +676,9 @@ using WideTile = GemmTile<128, 128, 16, 2, 2>;
 
 }  // namespace
 
-int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, int64_t Z) {
+int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, int64_t Z, bool colsum) {
   const int64_t S = splitk_factor<SplitTile>(M, N, K, Z);
-  return S > 1 ? S * Z * M * N : 0;
+  return S > 1 ? S * (Z * M * N + (colsum ? N : 0)) : 0;
 }
 
 // Launch the strided batched GEMM.  Z = number of batches, zin = inner batch extent.  With a
@@ -619,7 +687,8 @@ int gemm_launch(const GemmOperand& A, const GemmOperand& B, const GemmOut& C,
                 const GemmEpilogue& ep, int64_t M, int64_t N, int64_t K, int64_t Z, int64_t zin,
                 hipStream_t st, float* workspace, int64_t workspace_floats) {
   const int64_t S = splitk_factor<SplitTile>(M, N, K, Z);
-  if (S > 1 && workspace != nullptr && workspace_floats >= S * Z * M * N)
+  if (S > 1 && workspace != nullptr &&
+      workspace_floats >= S * (Z * M * N + (ep.colsum ? N : 0)))
     return gemm_launch_tile<SplitTile>(A, B, C, ep, M, N, K, Z, zin, st, workspace,
                                        workspace_floats);
   if (N <= 768)
@@ -745,4 +814,46 @@ extern "C" int cta_db_calculation(const float* dy, const int64_t* dy_strides, in
   if (!dy || !dy_strides || !workspace) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
   return colsum_launch(dy, batch, m, n, dy_strides[0], dy_strides[1], dy_strides[2], db,
                        workspace, st);
+}
+
+extern "C" int64_t cta_linear_weight_bias_grad_workspace(int64_t rows, int64_t k, int64_t n) {
+  if (rows <= 0 || n <= 0) return 0;
+  // k == 0: no GEMM, but db still comes from the column-sum kernels' partials
+  if (k <= 0) return colsum_workspace_floats(rows, n) * (int64_t)sizeof(float);
+  const int64_t fused = gemm_workspace_floats(k, n, rows, 1, true);
+  const int64_t apart = std::max(gemm_workspace_floats(k, n, rows, 1), colsum_workspace_floats(rows, n));
+  return std::max(fused, apart) * (int64_t)sizeof(float);
+}
+
+// dW = x^T dy as one GEMM over the rows (A = x^T through x's strides), with db = the column sums
+// of dy taken from the GEMM's own dy slices when dy is n-contiguous with n % 4 == 0; otherwise
+// the GEMM and then the column-sum kernels.
+extern "C" int cta_linear_weight_bias_grad(const float* x, const int64_t* x_strides,
+                                           const float* dy, const int64_t* dy_strides,
+                                           int64_t rows, int64_t k, int64_t n, float* dw,
+                                           float* db, float* workspace, void* stream) {
+  if (rows < 0 || k < 0 || n < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
+  if (n == 0) return CTA_OK;
+  if (!db || (k > 0 && !dw)) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  hipStream_t st = as_stream(stream);
+  if (rows == 0) {
+    if (int rc = zero_floats(db, n, st)) return rc;
+    return k > 0 ? zero_floats(dw, k * n, st) : CTA_OK;
+  }
+  if (!dy || !dy_strides || (k > 0 && (!x || !x_strides)))
+    return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  const int64_t ws_floats = cta_linear_weight_bias_grad_workspace(rows, k, n) / (int64_t)sizeof(float);
+  if (ws_floats > 0 && !workspace) return fail(CTA_ERR_INVALID_ARGUMENT, "null workspace");
+  const GemmOperand B{dy, 0, 0, dy_strides[0], dy_strides[1]};
+  const GemmOut C{dw, k * n, 0, n};
+  GemmEpilogue ep{1.0f, nullptr, 0, 0};
+  if (k > 0) {
+    const GemmOperand A{x, 0, 0, x_strides[1], x_strides[0]};
+    if (pick_mode(B, false, n, rows) == kVecMN) {
+      ep.colsum = db;
+      return gemm_launch(A, B, C, ep, k, n, rows, 1, 1, st, workspace, ws_floats);
+    }
+    if (int rc = gemm_launch(A, B, C, ep, k, n, rows, 1, 1, st, workspace, ws_floats)) return rc;
+  }
+  return colsum_launch(dy, 1, rows, n, 0, dy_strides[0], dy_strides[1], db, workspace, st);
 }

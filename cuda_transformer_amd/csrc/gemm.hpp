@@ -33,15 +33,20 @@ struct GemmEpilogue {
   int causal_mask;    // set entries with n > m to -inf
   int act = kActNone;
   float* aux = nullptr;  // same (batch, m, n) layout as the output; read-only for the *Grad acts
+  // Nullable: receives the column sums of B over K (sum_k B[k][n], n < N).  Needs Z == 1,
+  // B contiguous along n with N % 4 == 0, no pointwise stage and no mask.
+  float* colsum = nullptr;
 };
 
 // out[z] = alpha * A[z] B[z] (+ bias) for z in [0, Z); batch index split as (z / zin, z % zin).
 // With a workspace of gemm_workspace_floats(M, N, K, Z) floats, shapes with too few output
 // tiles to fill the GPU are split along K (deterministic fixed-order reduction).
+// With ep.colsum the split-K workspace also holds one row of column sums per split:
+// gemm_workspace_floats(M, N, K, Z, true) floats.
 int gemm_launch(const GemmOperand& A, const GemmOperand& B, const GemmOut& C,
                 const GemmEpilogue& ep, int64_t M, int64_t N, int64_t K, int64_t Z, int64_t zin,
                 hipStream_t st, float* workspace = nullptr, int64_t workspace_floats = 0);
-int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, int64_t Z);
+int64_t gemm_workspace_floats(int64_t M, int64_t N, int64_t K, int64_t Z, bool colsum = false);
 
 // Row softmax over `rows` dense rows of length n (x == y allowed).
 int softmax_rows(const float* x, float* y, int64_t rows, int64_t n, hipStream_t st);

@@ -210,6 +210,36 @@ at::Tensor db_calculation(at::Tensor dy) {
   return db;
 }
 
+// (dW, db) = (x^T dy, column sums of dy) over the rows of x (..., k) and dy (..., n), leading
+// dims folded into the rows: CudaLinearLayer.backward's weight product and db_calculation
+// (cuda_linear_layer.py:21-27) in one GEMM that sums dy's columns as it streams them.
+std::tuple<at::Tensor, at::Tensor> linear_weight_bias_grad(at::Tensor x, at::Tensor dy) {
+  TORCH_CHECK(x.dim() >= 1 && dy.dim() == x.dim(), "x and dy must have the same rank");
+  TORCH_CHECK(x.sizes().slice(0, x.dim() - 1) == dy.sizes().slice(0, dy.dim() - 1),
+              "x and dy must agree in every dim but the last");
+  TORCH_CHECK(x.is_cuda() && dy.is_cuda(), "x and dy must be CUDA tensors");
+  check_f32(x, "x");
+  check_f32(dy, "dy");
+  const int64_t k = x.size(-1), n = dy.size(-1);
+  int64_t rows = 1;
+  for (int64_t d = 0; d + 1 < x.dim(); ++d) rows *= x.size(d);
+  const at::Tensor x2 = x.reshape({rows, k});
+  const at::Tensor d2 = dy.reshape({rows, n});
+  c10::OptionalDeviceGuard guard(x.device());
+  at::Tensor dw = at::empty({k, n}, x.options());
+  at::Tensor db = at::empty({n}, x.options());
+  const int64_t ws_bytes = cta_linear_weight_bias_grad_workspace(rows, k, n);
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({ws_bytes / 4}, x.options());
+  const int64_t xs[2] = {x2.stride(0), x2.stride(1)};
+  const int64_t ds[2] = {d2.stride(0), d2.stride(1)};
+  check_rc(cta_linear_weight_bias_grad(x2.data_ptr<float>(), xs, d2.data_ptr<float>(), ds, rows,
+                                       k, n, dw.data_ptr<float>(), db.data_ptr<float>(),
+                                       ws_bytes > 0 ? ws.data_ptr<float>() : nullptr,
+                                       stream_of(x)));
+  return {dw, db};
+}
+
 // ------------------------------------------------------------------ GELU
 // cf. Transformer_launchers/gelu_activation.cu:22-77
 at::Tensor gelu_activation(at::Tensor x) {
@@ -685,6 +715,7 @@ at::Tensor flash_attention_qkv_bwd(at::Tensor qkv, at::Tensor out, at::Tensor do
 TORCH_LIBRARY(cuda_transformer, m) {
   m.def("cuda_fma(Tensor x, Tensor weights, Tensor bias) -> Tensor");
   m.def("db_calculation(Tensor dy) -> Tensor");
+  m.def("linear_weight_bias_grad(Tensor x, Tensor dy) -> (Tensor, Tensor)");
   m.def("cuda_fma_gelu(Tensor x, Tensor weights, Tensor bias) -> (Tensor, Tensor)");
   m.def("cuda_fma_gelu_grad(Tensor dy, Tensor weights, Tensor pre) -> Tensor");
   m.def("cuda_fma_gelu_tanh(Tensor x, Tensor weights, Tensor bias) -> (Tensor, Tensor)");
@@ -716,6 +747,7 @@ TORCH_LIBRARY(cuda_transformer, m) {
 TORCH_LIBRARY_IMPL(cuda_transformer, CUDA, m) {
   m.impl("cuda_fma", &cuda_fma);
   m.impl("db_calculation", &db_calculation);
+  m.impl("linear_weight_bias_grad", &linear_weight_bias_grad);
   m.impl("cuda_fma_gelu", &cuda_fma_gelu);
   m.impl("cuda_fma_gelu_grad", &cuda_fma_gelu_grad);
   m.impl("cuda_fma_gelu_tanh", &cuda_fma_gelu_tanh);

@@ -19,7 +19,7 @@ import torch
 from torch import Tensor
 
 __all__ = [
-    "cuda_fma", "db_calculation", "cuda_fma_gelu", "cuda_fma_gelu_grad", "cuda_fma_gelu_tanh",
+    "cuda_fma", "db_calculation", "linear_weight_bias_grad", "cuda_fma_gelu", "cuda_fma_gelu_grad", "cuda_fma_gelu_tanh",
     "cuda_fma_gelu_tanh_grad",
     "cuda_softmax", "cuda_softmax_bwd",
     "gelu_activation", "gelu_activation_bwd", "gelu_tanh_activation", "gelu_tanh_activation_bwd",
@@ -124,6 +124,25 @@ def db_calculation(dy: Tensor) -> Tensor:
 def _(dy):
     _f32(dy)
     return torch.empty(dy.size(-1), dtype=dy.dtype, device=dy.device)
+
+
+def linear_weight_bias_grad(x: Tensor, dy: Tensor):
+    """(dW, db) = (x^T dy, column sums of dy) over every row of x (..., k) and dy (..., n):
+    ``cuda_fma`` on the x^T view (zero bias) and ``db_calculation`` in one GEMM whose dy slices
+    also feed the column sums.  dW is bitwise equal to the ``cuda_fma`` route; db matches
+    ``db_calculation`` up to summation order.  No reference op (the reference makes the two
+    calls, cuda_linear_layer.py:21-27)."""
+    return _ops.linear_weight_bias_grad.default(x, dy)
+
+
+@torch.library.register_fake("cuda_transformer::linear_weight_bias_grad")
+def _(x, dy):
+    _f32(x, dy)
+    _same_device(x, dy)
+    torch._check(x.dim() == dy.dim() and x.shape[:-1] == dy.shape[:-1],
+                 lambda: "x and dy must agree in every dim but the last")
+    return (torch.empty(x.size(-1), dy.size(-1), dtype=dy.dtype, device=dy.device),
+            torch.empty(dy.size(-1), dtype=dy.dtype, device=dy.device))
 
 
 # ----------------------------------------------------------------- softmax

@@ -329,6 +329,22 @@ int cta_db_calculation(const float* dy, const int64_t* dy_strides,
                        int64_t batch, int64_t m, int64_t n,
                        float* db, float* workspace, void* stream);
 
+/* Bytes of scratch cta_linear_weight_bias_grad needs. */
+int64_t cta_linear_weight_bias_grad_workspace(int64_t rows, int64_t k, int64_t n);
+
+/* dW = x^T dy (dense (k, n)) and db = column sums of dy (n), for x (rows, k) and dy (rows, n),
+ * 2 strides each: the weight and bias gradients of CudaLinearLayer.backward with 2-D weights
+ * (cuda_autograd_fns/cuda_linear_layer.py:21-27, the batch folded into the rows).  When dy is
+ * n-contiguous with n % 4 == 0 and 16-byte aligned, db is summed inside the dW GEMM from the
+ * dy slices it already loads (no second pass over dy); otherwise db comes from the
+ * cta_db_calculation kernels.  dW is bitwise equal to cta_cuda_fma on the x^T view with a
+ * zero bias; db differs from cta_db_calculation only in summation order.  Deterministic.
+ * No single reference counterpart: it replaces the pair cuda_fma (dW) + db_calculation. */
+int cta_linear_weight_bias_grad(const float* x, const int64_t* x_strides,
+                                const float* dy, const int64_t* dy_strides,
+                                int64_t rows, int64_t k, int64_t n,
+                                float* dw, float* db, float* workspace, void* stream);
+
 /* ------------------------------------------------------------------------------
  * Elementwise / row kernels (dense inputs, as the reference launchers require).
  * ---------------------------------------------------------------------------- */

@@ -59,6 +59,15 @@ def test_workspace_queries():
     assert lib.cta_causal_self_attention_bwd_workspace(8, 33) == 8 * 33 * 33 * 4
     assert lib.cta_cuda_fma_workspace(1, 8192, 768, 3072) == 0          # fills the GPU: no split
     assert lib.cta_cuda_fma_workspace(1, 768, 8192, 3072) > 0           # 144 tiles, K = 8192
+    # weight + bias gradient: the split partials plus one row of column sums per split
+    fma_ws = lib.cta_cuda_fma_workspace(1, 768, 8192, 3072)
+    wb_ws = lib.cta_linear_weight_bias_grad_workspace(8192, 768, 3072)
+    splits = fma_ws // (768 * 3072 * 4)
+    assert splits > 1 and wb_ws == max(fma_ws + splits * 3072 * 4,
+                                      lib.cta_db_calculation_workspace(1, 8192, 3072))
+    assert lib.cta_linear_weight_bias_grad_workspace(0, 5, 5) == 0
+    # no weight columns: db alone, still through the column-sum partials
+    assert lib.cta_linear_weight_bias_grad_workspace(300, 0, 8) == lib.cta_db_calculation_workspace(1, 300, 8) > 0
     for hs in (32, 64, 128):  # 16-bit dS workspace: 2 KiB per stored 32x32 tile
         assert lib.cta_flash_attention_bwd_bf16_workspace(1, 2, 64, hs, 1) == 2 * 3 * 2048
     assert lib.cta_flash_attention_bwd_bf16_workspace(1, 2, 64, 48, 1) == 0
@@ -68,6 +77,13 @@ def test_other_entry_points_validate_arguments():
     lib = capi.lib()
     s3 = capi.strides((1, 1, 1))
     assert lib.cta_cuda_fma(16, s3, 16, s3, 16, 1, 2, 3, 4, 5, 3, 16, None, None) == INVALID  # w_batch
+    s2 = capi.strides((1, 1))
+    assert lib.cta_linear_weight_bias_grad(16, s2, 16, s2, -1, 2, 3, 16, 16, None, None) == INVALID
+    assert lib.cta_linear_weight_bias_grad(16, s2, 16, s2, 4, 2, 3, 16, None, None, None) == INVALID
+    assert lib.cta_linear_weight_bias_grad(16, s2, 16, s2, 4, 2, 0, None, None, None, None) == OK
+    # a required workspace that is missing is an error, not a launch
+    assert lib.cta_linear_weight_bias_grad(None, s2, 16, s2, 300, 0, 8, None, 16, None, None) == INVALID
+    assert lib.cta_linear_weight_bias_grad(16, s2, 16, s2, 300, 4, 8, 16, 16, None, None) == INVALID
     assert lib.cta_gelu_fwd(16, 16, -1, None) == INVALID
     assert lib.cta_gelu_fwd(20, 16, 8, None) == LAYOUT
     assert lib.cta_gelu_tanh_fwd(16, 16, -1, None) == INVALID

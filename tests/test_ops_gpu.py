@@ -393,6 +393,62 @@ def test_db_strided_views(cuda):
     assert torch.equal(db_calculation(big), db_calculation(big))
 
 
+# (rows, k, n): split-K with the SplitTile (GPT qkv / fc2 weight gradients, config 4), one
+# unsplit 128x128-tile GEMM (256 tiles), unsplit narrow tiles with ragged rows, and n % 4 != 0
+# (dy not vector-loadable: GEMM then the column-sum kernels).
+WB_SHAPES = [(16384, 384, 1152), (16384, 1536, 384), (8192, 768, 3072), (2048, 2048, 2048),
+             (333, 64, 100), (1000, 20, 36), (100, 48, 65), (5, 7, 12)]
+
+
+@pytest.mark.parametrize("rows,k,n", WB_SHAPES)
+def test_linear_weight_bias_grad(cuda, rows, k, n):
+    # dW bitwise equal to the cuda_fma route (same kernel schedule, same K split); db checked
+    # against the float64 oracle, and reproducible call to call.
+    from cuda_transformer.ops import cuda_fma
+    from cuda_transformer_amd.ops import linear_weight_bias_grad
+
+    x = seeded((rows, k), 40).to(cuda)
+    dy = seeded((rows, n), 41).to(cuda)
+    dw, db = linear_weight_bias_grad(x, dy)
+    ref_dw = cuda_fma(x.unsqueeze(0).transpose(1, 2), dy.unsqueeze(0), torch.zeros(n, device=cuda))[0]
+    assert torch.equal(dw, ref_dw)
+    _, dw_r, db_r = lin.linear_backward(f64(x)[None], np.zeros((k, n)), f64(dy)[None])
+    assert rel_err(f64(dw), dw_r) <= 1e-5
+    scale = np.abs(f64(dy)).sum(axis=0)
+    assert np.all(np.abs(f64(db) - db_r) <= 1e-6 * scale + 1e-6)
+    dw2, db2 = linear_weight_bias_grad(x, dy)
+    assert torch.equal(dw, dw2) and torch.equal(db, db2)
+
+
+def test_linear_weight_bias_grad_views_and_edges(cuda):
+    from cuda_transformer.ops import cuda_fma
+    from cuda_transformer_amd.ops import linear_weight_bias_grad
+
+    # x as a transposed view (k-contiguous A), dy rows strided past n, a 3-D batch folded into
+    # the rows, and a misaligned dy base (no vector loads: unfused path)
+    xt = seeded((96, 3000), 42).to(cuda)
+    dyb = seeded((3000, 200), 43).to(cuda)
+    cases = [(xt.t(), dyb[:, :128]), (seeded((3, 70, 40), 44).to(cuda), seeded((3, 70, 52), 45).to(cuda)),
+             (seeded((257, 33), 46).to(cuda), dyb[:257, 1:129])]
+    for x, dy in cases:
+        dw, db = linear_weight_bias_grad(x, dy)
+        x2, d2 = f64(x).reshape(-1, x.shape[-1]), f64(dy).reshape(-1, dy.shape[-1])
+        assert rel_err(f64(dw), x2.T @ d2) <= 1e-5
+        np.testing.assert_allclose(f64(db), d2.sum(axis=0), rtol=1e-5, atol=1e-4)
+        ref = cuda_fma(x.reshape(1, -1, x.shape[-1]).transpose(1, 2), dy.reshape(1, -1, dy.shape[-1]),
+                       torch.zeros(dy.shape[-1], device=cuda))[0]
+        assert torch.equal(dw, ref)
+    # zero rows: both gradients are zero; zero k: db alone
+    dw, db = linear_weight_bias_grad(torch.empty(0, 5, device=cuda), torch.empty(0, 8, device=cuda))
+    assert torch.equal(dw.cpu(), torch.zeros(5, 8)) and torch.equal(db.cpu(), torch.zeros(8))
+    dy = seeded((300, 8), 47).to(cuda)
+    dw, db = linear_weight_bias_grad(torch.empty(300, 0, device=cuda), dy)
+    assert dw.shape == (0, 8)
+    np.testing.assert_allclose(f64(db), f64(dy).sum(axis=0), rtol=1e-5, atol=1e-5)
+    with pytest.raises(RuntimeError, match="every dim but the last"):
+        linear_weight_bias_grad(torch.empty(4, 5, device=cuda), torch.empty(3, 8, device=cuda))
+
+
 # ------------------------------------------------------------ fused linear + GELU (GPT MLP)
 # (batch, rows, d, hidden); the last shape has 1 output tile and K = 4096, so it runs split-K.
 FUSED_SHAPES = [(1, 32, 64, 96), (2, 33, 17, 65), (3, 70, 129, 257), (2, 256, 384, 1536),

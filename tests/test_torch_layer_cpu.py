@@ -52,6 +52,9 @@ def test_meta_shapes():
     x = torch.empty(3, 10, 16, **m)
     assert ops.cuda_fma(x, torch.empty(16, 8, **m), torch.empty(8, **m)).shape == (3, 10, 8)
     assert ops.db_calculation(torch.empty(3, 10, 8, **m)).shape == (8,)
+    from cuda_transformer_amd.ops import linear_weight_bias_grad
+    dw, db = linear_weight_bias_grad(x, torch.empty(3, 10, 8, **m))
+    assert dw.shape == (16, 8) and db.shape == (8,)
     assert ops.gelu_activation(x).shape == x.shape
     assert ops.gelu_activation_bwd(x, x).shape == x.shape
     assert ops.gelu_tanh_activation(x).shape == x.shape
