@@ -78,6 +78,9 @@ def parse_args():
                         "1024,2048,4096,8192,16384)")
     p.add_argument("--masks", choices=["both", "causal", "full"], default="both",
                    help="fa2-bf16 workload: which masks to time")
+    p.add_argument("--gpt-adamw", choices=["fused", "foreach"], default="fused",
+                   help="gpt workload: torch AdamW implementation (fused: one multi-tensor kernel "
+                        "per step; foreach: torch's default list kernels)")
     p.add_argument("--gpt-mlp", choices=["fused", "reference"], default="fused",
                    help="gpt workload: fused: CudaMLP (GELU in the GEMM epilogues, the model's "
                         "default); reference: CudaLinearLayer -> CudaGeluLayer -> CudaLinearLayer")
@@ -914,7 +917,7 @@ def gpt_workload(args):
     model = GPT(cfg)
     init_weights_(model, seed=0)
     model.cuda()
-    opt = torch.optim.AdamW(model.parameters(), lr=6e-4)
+    opt = torch.optim.AdamW(model.parameters(), lr=6e-4, fused=args.gpt_adamw == "fused")
     batches = [synthetic_batch(cfg, batch, seed=s, device="cuda") for s in range(4)]
 
     def step(i, optimize=True):
@@ -965,7 +968,7 @@ def gpt_workload(args):
         "workload": "small-GPT training step (6L 6H d384 ctx256 vocab65, batch 64), FP32",
         "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 3),
         "fwd_bwd_ms": round(ms_fb, 3), "fwd_bwd_tokens_per_s": round(tokens / (ms_fb * 1e-3), 1),
-        "steps": args.steps, "mlp": args.gpt_mlp, "cpu_baseline": cpu,
+        "steps": args.steps, "mlp": args.gpt_mlp, "adamw": args.gpt_adamw, "cpu_baseline": cpu,
     }), flush=True)
     return 0
 

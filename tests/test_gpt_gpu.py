@@ -10,14 +10,15 @@ from oracle import gpt as ogpt
 pytestmark = pytest.mark.gpu
 
 
-def test_gpt_training_steps_match_cpu_reference(cuda):
+@pytest.mark.parametrize("fused_adamw", [False, True])  # the bench's step uses the fused AdamW
+def test_gpt_training_steps_match_cpu_reference(cuda, fused_adamw):
     cfg = GPTConfig()
     model = GPT(cfg)
     ref = ogpt.GPT(cfg)
     init_weights_(model, seed=0)
     ref.load_state_dict(model.state_dict())
     model.to(cuda)
-    opt = torch.optim.AdamW(model.parameters(), lr=6e-4)
+    opt = torch.optim.AdamW(model.parameters(), lr=6e-4, fused=fused_adamw)
     opt_ref = torch.optim.AdamW(ref.parameters(), lr=6e-4)
     torch.set_num_threads(min(16, torch.get_num_threads()))
     losses, losses_ref = [], []
