@@ -4,8 +4,8 @@ Same classes, ``apply`` signatures and saved tensors as the reference's cuda_aut
 (cuda_flash_attention.py:4-17, cuda_linear_layer.py:4-28, cuda_gelu_layer.py:4-14,
 cuda_softmax_layer.py:4-15, cuda_causal_self_attention.py:4-35), plus ``CudaLayerNorm``,
 ``CudaMLP`` (the GPT MLP with its GELU folded into the GEMM epilogues), ``CudaGeluTanhLayer``
-(the tanh-approximated GELU) and ``CudaFlashAttentionQKV`` (attention on a packed qkv projection,
-no head transposes).
+(the tanh-approximated GELU), ``CudaFlashAttentionQKV`` (attention on a packed qkv projection,
+no head transposes) and ``CudaAddLayerNorm`` (a residual add fused with the next LayerNorm).
 
 Deviations, each a fix:
 
@@ -25,12 +25,13 @@ from .ops import (
     causal_self_attention_bwd, causal_self_attention_fwd, cuda_fma, cuda_fma_gelu,
     cuda_fma_gelu_grad, cuda_fma_gelu_tanh, cuda_fma_gelu_tanh_grad, cuda_softmax, cuda_softmax_bwd, db_calculation, flash_attention_bwd, flash_attention_fwd, flash_attention_qkv_bwd, flash_attention_qkv_fwd, gelu_activation,
     gelu_activation_bwd, gelu_tanh_activation, gelu_tanh_activation_bwd, layernorm_bwd, layernorm_fwd,
-    linear_weight_bias_grad,
+    linear_weight_bias_grad, add_layernorm_bwd, add_layernorm_fwd,
 )
 
 __all__ = [
     "CudaCausalSelfAttention", "CudaFlashAttention", "CudaGeluLayer", "CudaLinearLayer",
     "CudaSoftmaxLayer", "CudaLayerNorm", "CudaMLP", "CudaGeluTanhLayer", "CudaFlashAttentionQKV",
+    "CudaAddLayerNorm",
 ]
 
 
@@ -224,6 +225,34 @@ class CudaCausalSelfAttention(torch.autograd.Function):
         sm_scale = hs ** 0.5
         grads = torch.cat([unheads(dq) / sm_scale, unheads(dk) / sm_scale, unheads(dv)], dim=-1)
         return grads, None, None
+
+
+class CudaAddLayerNorm(torch.autograd.Function):
+    """(x, f, gamma, beta, eps) -> (xsum, y) with xsum = x + f and y = LayerNorm(xsum): a pre-LN
+    block's residual add and the LayerNorm after it (gpt/gpt.py:147-150) in one pass each way.
+    The backward gets the gradient of xsum from its next use (the next residual add) and of y
+    from the sublayer, and returns their sum, LayerNorm backward included, for x and f alike:
+    the same bits as ``x + f`` then ``CudaLayerNorm`` with autograd summing the two paths, but
+    one kernel instead of two in each direction and no separate accumulation."""
+
+    @staticmethod
+    def forward(ctx, x, f, gamma, beta, eps=1e-5):
+        xsum, y, mean, rstd = add_layernorm_fwd(x, f, gamma, beta, eps)
+        ctx.save_for_backward(xsum, gamma, mean, rstd)
+        ctx.set_materialize_grads(False)
+        return xsum, y
+
+    @staticmethod
+    def backward(ctx, grad_xsum, grad_y):
+        xsum, gamma, mean, rstd = ctx.saved_tensors
+        if grad_y is None:
+            return grad_xsum, grad_xsum, None, None, None
+        if grad_xsum is None:
+            dx, dgamma, dbeta = layernorm_bwd(xsum, gamma, mean, rstd, grad_y.contiguous())
+        else:
+            dx, dgamma, dbeta = add_layernorm_bwd(xsum, gamma, mean, rstd, grad_y.contiguous(),
+                                                  grad_xsum.contiguous())
+        return dx, dx, dgamma.reshape(gamma.shape), dbeta.reshape(gamma.shape), None
 
 
 class CudaLayerNorm(torch.autograd.Function):

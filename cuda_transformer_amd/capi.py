@@ -90,6 +90,8 @@ SIGNATURES = {
     "cta_layernorm_fwd": (_int, [_p, _p, _p, _i64, _i64, _f32, _p, _p, _p, _p]),
     "cta_layernorm_bwd_workspace": (_i64, [_i64, _i64]),
     "cta_layernorm_bwd": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p]),
+    "cta_add_layernorm_fwd": (_int, [_p, _p, _p, _p, _i64, _i64, _f32, _p, _p, _p, _p, _p]),
+    "cta_add_layernorm_bwd": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p]),
     "cta_causal_self_attention_fwd": (_int, [_p, _i64, _i64, _i64, _i64, _int, _p, _p, _p]),
     "cta_causal_self_attention_bwd_workspace": (_i64, [_i64, _i64]),
     "cta_causal_self_attention_bwd": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _p, _i64p,

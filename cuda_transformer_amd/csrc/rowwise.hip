@@ -270,17 +270,33 @@ __global__ __launch_bounds__(256) void softmax_bwd_long(const float* p, const fl
 }
 
 // ------------------------------------------------------------------------ LayerNorm
-template <int U, bool VEC>
+// a + b rounded once and never fused with the multiply that produced a, so that the residual
+// variants below give the bits of a separate LayerNorm kernel followed by an add.
+__device__ __forceinline__ float add_unfused(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
+// RES: the row is x + f, stored to xsum before it is normalised (a residual add fused with the
+// LayerNorm that follows it).
+template <int U, bool VEC, bool RES = false>
 __global__ __launch_bounds__(256) void layernorm_fwd_rows(
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
     float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, int64_t rows,
-    int n, float eps) {
+    int n, float eps, const float* __restrict__ f = nullptr, float* __restrict__ xsum = nullptr) {
   const int lane = threadIdx.x & 63;
   const int64_t step = (int64_t)gridDim.x * 4;
   for (int64_t row = (int64_t)blockIdx.x * 4 + wave_index(); row < rows; row += step) {
     using R = RowRegs<U, VEC>;
     R r, gm, bt;
     r.load(x + row * n, n, lane, 0.0f);
+    if constexpr (RES) {
+      R fr;
+      fr.load(f + row * n, n, lane, 0.0f);
+#pragma unroll
+      for (int e = 0; e < U * R::W; ++e) r.v[e] += fr.v[e];
+      r.store(xsum + row * n, n, lane);
+    }
     gm.load(gamma, n, lane, 0.0f);
     bt.load(beta, n, lane, 0.0f);
     float s = 0.0f;
@@ -320,11 +336,13 @@ constexpr int ln_bwd_waves() {
   return U * RowRegs<U, VEC>::W <= 12 ? 16 : 8;
 }
 
-template <int U, bool VEC>
+// RES: dx also receives dres, the gradient reaching the LayerNorm's input by the residual path.
+template <int U, bool VEC, bool RES = false>
 __global__ __launch_bounds__((64 * ln_bwd_waves<U, VEC>())) void layernorm_bwd_rows(
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ dy, float* __restrict__ dx,
-    float* __restrict__ part, int64_t rows, int n, int rows_per_wave) {
+    float* __restrict__ part, int64_t rows, int n, int rows_per_wave,
+    const float* __restrict__ dres = nullptr) {
   using R = RowRegs<U, VEC>;
   constexpr int E = U * R::W;
   constexpr int WAVES = ln_bwd_waves<U, VEC>();
@@ -339,7 +357,7 @@ __global__ __launch_bounds__((64 * ln_bwd_waves<U, VEC>())) void layernorm_bwd_r
   const int64_t r0 = ((int64_t)blockIdx.x * WAVES + wave) * rows_per_wave;
   const int64_t r1 = min(rows, r0 + rows_per_wave);
   const float inv_n = 1.0f / (float)n;
-  auto row_grad = [&](R& xv, R& g, int64_t row) {
+  auto row_grad = [&](R& xv, R& g, const R& dr, int64_t row) {
     const float mu = mean[row], rs = rstd[row];
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
@@ -355,7 +373,10 @@ __global__ __launch_bounds__((64 * ln_bwd_waves<U, VEC>())) void layernorm_bwd_r
     }
     const float m1 = wave_sum(s1) * inv_n, m2 = wave_sum(s2) * inv_n;
 #pragma unroll
-    for (int e = 0; e < E; ++e) xv.v[e] = rs * (g.v[e] - m1 - xv.v[e] * m2);
+    for (int e = 0; e < E; ++e) {
+      xv.v[e] = rs * (g.v[e] - m1 - xv.v[e] * m2);
+      if constexpr (RES) xv.v[e] = add_unfused(xv.v[e], dr.v[e]);
+    }
     xv.store(dx + row * n, n, lane);
   };
   // two rows in flight while a row takes at most 16 registers per lane; one row beyond (two would
@@ -363,15 +384,17 @@ __global__ __launch_bounds__((64 * ln_bwd_waves<U, VEC>())) void layernorm_bwd_r
   constexpr bool PAIR = E <= 16;
   for (int64_t a = r0; a < r1; a += PAIR ? 2 : 1) {
     const bool two = PAIR && a + 1 < r1;  // wave-uniform
-    R xa, ga, xb, gb;
+    R xa, ga, xb, gb, ra, rb;
     xa.load(x + a * n, n, lane, 0.0f);
     ga.load(dy + a * n, n, lane, 0.0f);
+    if (RES) ra.load(dres + a * n, n, lane, 0.0f);
     if (two) {
       xb.load(x + (a + 1) * n, n, lane, 0.0f);
       gb.load(dy + (a + 1) * n, n, lane, 0.0f);
+      if (RES) rb.load(dres + (a + 1) * n, n, lane, 0.0f);
     }
-    row_grad(xa, ga, a);
-    if (two) row_grad(xb, gb, a + 1);
+    row_grad(xa, ga, ra, a);
+    if (two) row_grad(xb, gb, rb, a + 1);
   }
   // fixed-order tree over the waves of this workgroup
 #pragma unroll
@@ -407,16 +430,28 @@ __global__ __launch_bounds__((64 * ln_bwd_waves<U, VEC>())) void layernorm_bwd_r
   }
 }
 
-// Long rows (n > 2048): one workgroup per row, three passes over the row.
+// Long rows (n > 2048): one workgroup per row, three passes over the row.  With f the first
+// pass forms x + f and stores it to xsum, and the later passes read xsum (each thread rereads
+// the columns it wrote).
 __global__ __launch_bounds__(256) void layernorm_fwd_long(
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
     float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, int64_t rows,
-    int n, float eps) {
+    int n, float eps, const float* __restrict__ f, float* xsum) {
   __shared__ float red[4];
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     const float* xr = x + row * n;
     float s = 0.0f;
-    for (int c = threadIdx.x; c < n; c += 256) s += xr[c];
+    if (f != nullptr) {
+      float* sr = xsum + row * n;
+      for (int c = threadIdx.x; c < n; c += 256) {
+        const float v = xr[c] + f[row * n + c];
+        sr[c] = v;
+        s += v;
+      }
+      xr = sr;
+    } else {
+      for (int c = threadIdx.x; c < n; c += 256) s += xr[c];
+    }
     const float mu = block_reduce(s, false, red) / (float)n;
     float q = 0.0f;
     for (int c = threadIdx.x; c < n; c += 256) {
@@ -436,7 +471,7 @@ __global__ __launch_bounds__(256) void layernorm_fwd_long(
 __global__ __launch_bounds__(256) void layernorm_bwd_long(
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ dy, float* __restrict__ dx,
-    int64_t rows, int n) {
+    int64_t rows, int n, const float* __restrict__ dres) {
   __shared__ float red[4];
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     const float mu = mean[row], rs = rstd[row];
@@ -452,7 +487,8 @@ __global__ __launch_bounds__(256) void layernorm_bwd_long(
     for (int c = threadIdx.x; c < n; c += 256) {
       const float xh = (x[row * n + c] - mu) * rs;
       const float gx = dy[row * n + c] * gamma[c];
-      dx[row * n + c] = rs * (gx - m1 - xh * m2);
+      const float d = rs * (gx - m1 - xh * m2);
+      dx[row * n + c] = dres ? add_unfused(d, dres[row * n + c]) : d;
     }
   }
 }
@@ -657,36 +693,80 @@ extern "C" int cta_softmax_bwd(const float* probs, const float* dp, float* dx, i
   return softmax_bwd_rows_launch(probs, dp, dx, rows, n, as_stream(stream));
 }
 
-extern "C" int cta_layernorm_fwd(const float* x, const float* gamma, const float* beta,
-                                 int64_t rows, int64_t n, float eps, float* y, float* mean,
-                                 float* rstd, void* stream) {
+namespace {
+// LayerNorm forward over rows of x, or of x + f (stored to xsum) when f is given.
+int ln_fwd(const float* x, const float* f, const float* gamma, const float* beta, int64_t rows,
+           int64_t n, float eps, float* xsum, float* y, float* mean, float* rstd, void* stream) {
   if (rows < 0 || n < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
   if (rows == 0) return CTA_OK;
   if (n == 0) return fail(CTA_ERR_INVALID_ARGUMENT, "layernorm over an empty dimension");
   if (n > INT32_MAX) return fail(CTA_ERR_INVALID_ARGUMENT, "layernorm size out of range");
-  if (!x || !gamma || !beta || !y || !mean || !rstd)
+  if (!x || !gamma || !beta || !y || !mean || !rstd || (f && !xsum))
     return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
   hipStream_t st = as_stream(stream);
   if (n <= kMaxRegCols) {
-    const bool vec = row_vec_ok(x, y, gamma, (int)n) && aligned16(beta);
+    const bool vec = row_vec_ok(x, y, gamma, (int)n) && aligned16(beta) &&
+                     (!f || (aligned16(f) && aligned16(xsum)));
     const int u = units_for((int)n, vec);
-    CTA_ROW_SWITCH(layernorm_fwd_rows, vec, u, row_grid(rows), st, x, gamma, beta, y, mean, rstd, rows,
-                   (int)n, eps);
+    if (f) {
+#define CTA_ADD_LN(U_, V_)                                                                     \
+  hipLaunchKernelGGL((layernorm_fwd_rows<U_, V_, true>), row_grid(rows), dim3(256), 0, st, x,    \
+                     gamma, beta, y, mean, rstd, rows, (int)n, eps, f, xsum)
+      if (vec) {
+        switch (u) {
+          case 1: CTA_ADD_LN(1, true); break;
+          case 2: CTA_ADD_LN(2, true); break;
+          case 3: CTA_ADD_LN(3, true); break;
+          case 4: CTA_ADD_LN(4, true); break;
+          case 6: CTA_ADD_LN(6, true); break;
+          default: CTA_ADD_LN(8, true); break;
+        }
+      } else {
+        switch (u) {
+          case 1: CTA_ADD_LN(1, false); break;
+          case 2: CTA_ADD_LN(2, false); break;
+          case 4: CTA_ADD_LN(4, false); break;
+          case 8: CTA_ADD_LN(8, false); break;
+          case 16: CTA_ADD_LN(16, false); break;
+          default: CTA_ADD_LN(32, false); break;
+        }
+      }
+#undef CTA_ADD_LN
+    } else {
+      CTA_ROW_SWITCH(layernorm_fwd_rows, vec, u, row_grid(rows), st, x, gamma, beta, y, mean,
+                     rstd, rows, (int)n, eps);
+    }
   } else {
     hipLaunchKernelGGL(layernorm_fwd_long, long_row_grid(rows), dim3(256), 0, st, x, gamma,
-                       beta, y, mean, rstd, rows, (int)n, eps);
+                       beta, y, mean, rstd, rows, (int)n, eps, f, xsum);
   }
   return check_launch("layernorm_fwd");
+}
+}  // namespace
+
+extern "C" int cta_layernorm_fwd(const float* x, const float* gamma, const float* beta,
+                                 int64_t rows, int64_t n, float eps, float* y, float* mean,
+                                 float* rstd, void* stream) {
+  return ln_fwd(x, nullptr, gamma, beta, rows, n, eps, nullptr, y, mean, rstd, stream);
+}
+
+extern "C" int cta_add_layernorm_fwd(const float* x, const float* f, const float* gamma,
+                                     const float* beta, int64_t rows, int64_t n, float eps,
+                                     float* xsum, float* y, float* mean, float* rstd,
+                                     void* stream) {
+  if (rows > 0 && n > 0 && !f) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  return ln_fwd(x, f, gamma, beta, rows, n, eps, xsum, y, mean, rstd, stream);
 }
 
 extern "C" int64_t cta_layernorm_bwd_workspace(int64_t rows, int64_t n) {
   return layernorm_bwd_workspace_floats(rows, n) * (int64_t)sizeof(float);
 }
 
-extern "C" int cta_layernorm_bwd(const float* x, const float* gamma, const float* mean,
-                                 const float* rstd, const float* dy, int64_t rows, int64_t n,
-                                 float* dx, float* dgamma, float* dbeta, float* workspace,
-                                 void* stream) {
+namespace {
+// LayerNorm backward; with dres, dx also receives dres (the residual path's gradient).
+int ln_bwd(const float* x, const float* gamma, const float* mean, const float* rstd,
+           const float* dy, const float* dres, int64_t rows, int64_t n, float* dx, float* dgamma,
+           float* dbeta, float* workspace, void* stream) {
   if (rows < 0 || n < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
   if (n == 0) return CTA_OK;
   if (n > INT32_MAX) return fail(CTA_ERR_INVALID_ARGUMENT, "layernorm size out of range");
@@ -699,15 +779,22 @@ extern "C" int cta_layernorm_bwd(const float* x, const float* gamma, const float
   if (!x || !gamma || !mean || !rstd || !dy || !dx || !workspace)
     return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
   if (n <= kMaxRegCols) {
-    const bool vec = row_vec_ok(x, dy, dx, (int)n) && aligned16(gamma);
+    const bool vec = row_vec_ok(x, dy, dx, (int)n) && aligned16(gamma) && (!dres || aligned16(dres));
     const int u = units_for((int)n, vec);
     const int waves = ln_bwd_waves_for((int)n, vec);
     const int64_t blocks = ln_bwd_blocks(rows, waves);
     const int rows_per_wave = (int)((rows + blocks * waves - 1) / (blocks * waves));
 #define CTA_LN_BWD(U_, V_)                                                                     \
-  hipLaunchKernelGGL((layernorm_bwd_rows<U_, V_>), dim3((unsigned)blocks),                      \
-                     dim3(64 * ln_bwd_waves<U_, V_>()), 0, st, x, gamma, mean, rstd, dy, dx,    \
-                     workspace, rows, (int)n, rows_per_wave)
+  do {                                                                                         \
+    if (dres)                                                                                  \
+      hipLaunchKernelGGL((layernorm_bwd_rows<U_, V_, true>), dim3((unsigned)blocks),           \
+                         dim3(64 * ln_bwd_waves<U_, V_>()), 0, st, x, gamma, mean, rstd, dy,   \
+                         dx, workspace, rows, (int)n, rows_per_wave, dres);                    \
+    else                                                                                       \
+      hipLaunchKernelGGL((layernorm_bwd_rows<U_, V_>), dim3((unsigned)blocks),                 \
+                         dim3(64 * ln_bwd_waves<U_, V_>()), 0, st, x, gamma, mean, rstd, dy,   \
+                         dx, workspace, rows, (int)n, rows_per_wave);                          \
+  } while (0)
     if (vec) {
       switch (u) {
         case 1: CTA_LN_BWD(1, true); break;
@@ -733,7 +820,7 @@ extern "C" int cta_layernorm_bwd(const float* x, const float* gamma, const float
                                   workspace + blocks * 2 * n);
   } else {
     hipLaunchKernelGGL(layernorm_bwd_long, long_row_grid(rows), dim3(256), 0, st, x, gamma,
-                       mean, rstd, dy, dx, rows, (int)n);
+                       mean, rstd, dy, dx, rows, (int)n, dres);
     const int64_t chunks = (rows + kLnLongRowsPerBlock - 1) / kLnLongRowsPerBlock;
     if (chunks > 65535) return fail(CTA_ERR_INVALID_ARGUMENT, "too many rows for layernorm_bwd");
     hipLaunchKernelGGL(layernorm_colpart_long, dim3((unsigned)((n + 255) / 256), (unsigned)chunks),
@@ -744,4 +831,20 @@ extern "C" int cta_layernorm_bwd(const float* x, const float* gamma, const float
                                   workspace + chunks * 2 * n);
   }
   return check_launch("layernorm_bwd");
+}
+}  // namespace
+
+extern "C" int cta_layernorm_bwd(const float* x, const float* gamma, const float* mean,
+                                 const float* rstd, const float* dy, int64_t rows, int64_t n,
+                                 float* dx, float* dgamma, float* dbeta, float* workspace,
+                                 void* stream) {
+  return ln_bwd(x, gamma, mean, rstd, dy, nullptr, rows, n, dx, dgamma, dbeta, workspace, stream);
+}
+
+extern "C" int cta_add_layernorm_bwd(const float* xsum, const float* gamma, const float* mean,
+                                     const float* rstd, const float* dy, const float* dres,
+                                     int64_t rows, int64_t n, float* dx, float* dgamma,
+                                     float* dbeta, float* workspace, void* stream) {
+  if (rows > 0 && n > 0 && !dres) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  return ln_bwd(xsum, gamma, mean, rstd, dy, dres, rows, n, dx, dgamma, dbeta, workspace, stream);
 }

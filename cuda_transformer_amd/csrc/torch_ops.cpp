@@ -334,8 +334,10 @@ at::Tensor cuda_softmax_bwd(at::Tensor probs, at::Tensor dp) {
 }
 
 // ------------------------------------------------------------------ LayerNorm (new)
-std::tuple<at::Tensor, at::Tensor, at::Tensor> layernorm_fwd(at::Tensor x, at::Tensor gamma,
-                                                             at::Tensor beta, double eps) {
+// LayerNorm over the last dim of x, or of xsum = x + f (returned first) when f is given.
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> layernorm_fwd_impl(
+    const at::Tensor& x, const c10::optional<at::Tensor>& f, const at::Tensor& gamma,
+    const at::Tensor& beta, double eps) {
   TORCH_CHECK(x.dim() >= 1, "x must have at least one dimension");
   TORCH_CHECK(x.is_cuda(), "x must be a CUDA tensor");
   TORCH_CHECK(gamma.is_cuda(), "gamma must be a CUDA tensor");
@@ -343,26 +345,54 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> layernorm_fwd(at::Tensor x, at::T
   check_f32(x, "x");
   check_f32(gamma, "gamma");
   check_f32(beta, "beta");
+  if (f) {
+    TORCH_CHECK(f->is_cuda(), "f must be a CUDA tensor");
+    check_f32(*f, "f");
+    TORCH_CHECK(f->sizes() == x.sizes(), "f must have the shape of x");
+  }
   const int64_t n = x.size(-1);
   TORCH_CHECK(gamma.numel() == n && beta.numel() == n,
               "gamma and beta must have x.size(-1) elements");
   c10::OptionalDeviceGuard guard(x.device());
   const at::Tensor xd = dense(x), gd = dense(gamma), bd = dense(beta);
+  const at::Tensor fd = f ? dense(*f) : at::Tensor();
   const int64_t rows = n == 0 ? 0 : x.numel() / n;
   at::Tensor y = at::empty(x.sizes(), x.options());
+  at::Tensor xsum = f ? at::empty(x.sizes(), x.options()) : at::Tensor();
   auto stat_shape = x.sizes().vec();
   stat_shape.pop_back();
   at::Tensor mean = at::empty(stat_shape, x.options());
   at::Tensor rstd = at::empty(stat_shape, x.options());
-  check_rc(cta_layernorm_fwd(xd.data_ptr<float>(), gd.data_ptr<float>(), bd.data_ptr<float>(),
-                             rows, n, static_cast<float>(eps), y.data_ptr<float>(),
-                             mean.data_ptr<float>(), rstd.data_ptr<float>(), stream_of(x)));
-  return {y, mean, rstd};
+  if (f)
+    check_rc(cta_add_layernorm_fwd(xd.data_ptr<float>(), fd.data_ptr<float>(),
+                                   gd.data_ptr<float>(), bd.data_ptr<float>(), rows, n,
+                                   static_cast<float>(eps), xsum.data_ptr<float>(),
+                                   y.data_ptr<float>(), mean.data_ptr<float>(),
+                                   rstd.data_ptr<float>(), stream_of(x)));
+  else
+    check_rc(cta_layernorm_fwd(xd.data_ptr<float>(), gd.data_ptr<float>(), bd.data_ptr<float>(),
+                               rows, n, static_cast<float>(eps), y.data_ptr<float>(),
+                               mean.data_ptr<float>(), rstd.data_ptr<float>(), stream_of(x)));
+  return {xsum, y, mean, rstd};
 }
 
-std::tuple<at::Tensor, at::Tensor, at::Tensor> layernorm_bwd(at::Tensor x, at::Tensor gamma,
-                                                             at::Tensor mean, at::Tensor rstd,
-                                                             at::Tensor dy) {
+std::tuple<at::Tensor, at::Tensor, at::Tensor> layernorm_fwd(at::Tensor x, at::Tensor gamma,
+                                                             at::Tensor beta, double eps) {
+  auto r = layernorm_fwd_impl(x, c10::nullopt, gamma, beta, eps);
+  return {std::get<1>(r), std::get<2>(r), std::get<3>(r)};
+}
+
+// xsum = x + f and LayerNorm(xsum) in one pass.  New op: a pre-LN block's residual add and the
+// LayerNorm after it (gpt/gpt.py:147-150).
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> add_layernorm_fwd(
+    at::Tensor x, at::Tensor f, at::Tensor gamma, at::Tensor beta, double eps) {
+  return layernorm_fwd_impl(x, f, gamma, beta, eps);
+}
+
+// LayerNorm backward at x; with dres, dx also receives dres.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> layernorm_bwd_impl(
+    const at::Tensor& x, const at::Tensor& gamma, const at::Tensor& mean, const at::Tensor& rstd,
+    const at::Tensor& dy, const c10::optional<at::Tensor>& dres) {
   TORCH_CHECK(x.is_cuda() && gamma.is_cuda() && mean.is_cuda() && rstd.is_cuda() && dy.is_cuda(),
               "layernorm_bwd inputs must be CUDA tensors");
   check_f32(x, "x");
@@ -370,6 +400,11 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> layernorm_bwd(at::Tensor x, at::T
   check_f32(mean, "mean");
   check_f32(rstd, "rstd");
   check_f32(dy, "dy");
+  if (dres) {
+    TORCH_CHECK(dres->is_cuda(), "dres must be a CUDA tensor");
+    check_f32(*dres, "dres");
+    TORCH_CHECK(dres->sizes() == x.sizes(), "dres must have the shape of x");
+  }
   const int64_t n = x.size(-1);
   TORCH_CHECK(dy.sizes() == x.sizes(), "dy must have the shape of x");
   TORCH_CHECK(gamma.numel() == n, "gamma must have x.size(-1) elements");
@@ -378,16 +413,38 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> layernorm_bwd(at::Tensor x, at::T
   c10::OptionalDeviceGuard guard(x.device());
   const at::Tensor xd = dense(x), gd = dense(gamma), md = dense(mean), rd = dense(rstd),
                    dd = dense(dy);
+  const at::Tensor rsd = dres ? dense(*dres) : at::Tensor();
   at::Tensor dx = at::empty(x.sizes(), x.options());
   at::Tensor dgamma = at::empty({n}, x.options());
   at::Tensor dbeta = at::empty({n}, x.options());
   const int64_t ws_bytes = cta_layernorm_bwd_workspace(rows, n);
   at::Tensor ws = at::empty({std::max<int64_t>(1, ws_bytes / 4)}, x.options());
-  check_rc(cta_layernorm_bwd(xd.data_ptr<float>(), gd.data_ptr<float>(), md.data_ptr<float>(),
-                             rd.data_ptr<float>(), dd.data_ptr<float>(), rows, n,
-                             dx.data_ptr<float>(), dgamma.data_ptr<float>(),
-                             dbeta.data_ptr<float>(), ws.data_ptr<float>(), stream_of(x)));
+  if (dres)
+    check_rc(cta_add_layernorm_bwd(xd.data_ptr<float>(), gd.data_ptr<float>(),
+                                   md.data_ptr<float>(), rd.data_ptr<float>(),
+                                   dd.data_ptr<float>(), rsd.data_ptr<float>(), rows, n,
+                                   dx.data_ptr<float>(), dgamma.data_ptr<float>(),
+                                   dbeta.data_ptr<float>(), ws.data_ptr<float>(), stream_of(x)));
+  else
+    check_rc(cta_layernorm_bwd(xd.data_ptr<float>(), gd.data_ptr<float>(), md.data_ptr<float>(),
+                               rd.data_ptr<float>(), dd.data_ptr<float>(), rows, n,
+                               dx.data_ptr<float>(), dgamma.data_ptr<float>(),
+                               dbeta.data_ptr<float>(), ws.data_ptr<float>(), stream_of(x)));
   return {dx, dgamma, dbeta};
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> layernorm_bwd(at::Tensor x, at::Tensor gamma,
+                                                             at::Tensor mean, at::Tensor rstd,
+                                                             at::Tensor dy) {
+  return layernorm_bwd_impl(x, gamma, mean, rstd, dy, c10::nullopt);
+}
+
+// Backward of add_layernorm_fwd: (LayerNorm backward of dy at xsum) + dres, dgamma, dbeta.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> add_layernorm_bwd(at::Tensor xsum,
+                                                                 at::Tensor gamma,
+                                                                 at::Tensor mean, at::Tensor rstd,
+                                                                 at::Tensor dy, at::Tensor dres) {
+  return layernorm_bwd_impl(xsum, gamma, mean, rstd, dy, dres);
 }
 
 // ------------------------------------------------------------------ naive attention
@@ -739,6 +796,10 @@ TORCH_LIBRARY(cuda_transformer, m) {
       "flash_attention_qkv_bwd(Tensor qkv, Tensor out, Tensor dout, Tensor L, int nh, bool "
       "causal) -> Tensor");
   m.def("layernorm_fwd(Tensor x, Tensor gamma, Tensor beta, float eps) -> (Tensor, Tensor, Tensor)");
+  m.def("add_layernorm_fwd(Tensor x, Tensor f, Tensor gamma, Tensor beta, float eps) -> "
+        "(Tensor, Tensor, Tensor, Tensor)");
+  m.def("add_layernorm_bwd(Tensor xsum, Tensor gamma, Tensor mean, Tensor rstd, Tensor dy, "
+        "Tensor dres) -> (Tensor, Tensor, Tensor)");
   m.def(
       "layernorm_bwd(Tensor x, Tensor gamma, Tensor mean, Tensor rstd, Tensor dy) -> "
       "(Tensor, Tensor, Tensor)");
@@ -766,6 +827,8 @@ TORCH_LIBRARY_IMPL(cuda_transformer, CUDA, m) {
   m.impl("flash_attention_qkv_bwd", &flash_attention_qkv_bwd);
   m.impl("layernorm_fwd", &layernorm_fwd);
   m.impl("layernorm_bwd", &layernorm_bwd);
+  m.impl("add_layernorm_fwd", &add_layernorm_fwd);
+  m.impl("add_layernorm_bwd", &add_layernorm_bwd);
 }
 
 }  // namespace cuda_transformer

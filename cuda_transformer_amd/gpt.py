@@ -18,8 +18,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .autograd_fns import (CudaFlashAttention, CudaFlashAttentionQKV, CudaGeluLayer, CudaLayerNorm,
-                           CudaLinearLayer, CudaMLP)
+from .autograd_fns import (CudaAddLayerNorm, CudaFlashAttention, CudaFlashAttentionQKV,
+                           CudaGeluLayer, CudaLayerNorm, CudaLinearLayer, CudaMLP)
 
 
 @dataclass
@@ -39,6 +39,10 @@ class GPTConfig:
     # written in the packed layouts) instead of the reference's head views, transposes and
     # concatenation around CudaFlashAttention; same kernels, same bits.
     packed_attention: bool = True
+    # Each residual add fused with the LayerNorm that follows it (CudaAddLayerNorm: x + f and
+    # LayerNorm(x + f) in one pass; in the backward the residual gradient joins the LayerNorm
+    # gradient in the same pass) instead of separate adds; same bits.
+    fused_residual_ln: bool = True
 
 
 class LayerNorm(nn.Module):
@@ -140,14 +144,29 @@ class GPT(nn.Module):
 
     def forward(self, idx, targets=None):
         x = self.embedding(idx)
-        for block in self.mha:
-            x = block(x)
-        logits = CudaLinearLayer.apply(self.ln(x), self.lm_head_weights, self.lm_head_bias)
+        if self.cfg.fused_residual_ln and len(self.mha) > 0:
+            # the blocks' x + attn(ln1(x)), x + mlp(ln2(x)) with every add fused with the next
+            # LayerNorm: ln2 of the block, then ln1 of the next block or the final LayerNorm
+            z = self.mha[0].ln1(x)
+            for i, block in enumerate(self.mha):
+                x, z = _add_ln(x, block.attn(z), block.ln2)
+                nxt = self.mha[i + 1].ln1 if i + 1 < len(self.mha) else self.ln
+                x, z = _add_ln(x, block.mlp(z), nxt)
+        else:
+            for block in self.mha:
+                x = block(x)
+            z = self.ln(x)
+        logits = CudaLinearLayer.apply(z, self.lm_head_weights, self.lm_head_bias)
         loss = None
         if targets is not None:
             B, T, V = logits.shape
             loss = F.cross_entropy(logits.reshape(B * T, V), targets.reshape(B * T))
         return logits, loss
+
+
+def _add_ln(x, f, ln: LayerNorm):
+    """(x + f, ln(x + f)) through one CudaAddLayerNorm."""
+    return CudaAddLayerNorm.apply(x, f, ln.alpha, ln.beta, ln.epsilon)
 
 
 def init_weights_(model: nn.Module, seed: int, std: float = 0.02) -> None:

@@ -26,7 +26,7 @@ __all__ = [
     "causal_self_attention_fwd", "causal_self_attention_bwd",
     "flash_attention_fwd", "flash_attention_bwd",
     "flash_attention_qkv_fwd", "flash_attention_qkv_bwd",
-    "layernorm_fwd", "layernorm_bwd",
+    "layernorm_fwd", "layernorm_bwd", "add_layernorm_fwd", "add_layernorm_bwd",
 ]
 
 _ops = torch.ops.cuda_transformer
@@ -350,3 +350,35 @@ def _(x, gamma, mean, rstd, dy):
     n = x.size(-1)
     return (torch.empty_like(x), torch.empty(n, dtype=x.dtype, device=x.device),
             torch.empty(n, dtype=x.dtype, device=x.device))
+
+
+def add_layernorm_fwd(x: Tensor, f: Tensor, gamma: Tensor, beta: Tensor, eps: float = 1e-5):
+    """Residual add fused with the LayerNorm after it -> (xsum = x + f, LayerNorm(xsum), mean,
+    rstd): the bits of ``x + f`` followed by ``layernorm_fwd``, in one pass.  No reference op
+    (the pre-LN block's residual adds and LayerNorms, gpt/gpt.py:147-150)."""
+    return _ops.add_layernorm_fwd.default(x, f, gamma, beta, eps)
+
+
+@torch.library.register_fake("cuda_transformer::add_layernorm_fwd")
+def _(x, f, gamma, beta, eps):
+    _f32(x, f, gamma, beta)
+    _same_device(x, f, gamma, beta)
+    stat = torch.empty(x.shape[:-1], dtype=x.dtype, device=x.device)
+    return torch.empty_like(x), torch.empty_like(x), stat, torch.empty_like(stat)
+
+
+def add_layernorm_bwd(xsum: Tensor, gamma: Tensor, mean: Tensor, rstd: Tensor, dy: Tensor,
+                      dres: Tensor):
+    """Backward of ``add_layernorm_fwd`` -> (dx, dgamma, dbeta) with dx = LayerNorm backward of
+    dy at xsum plus dres, the gradient reaching xsum by the residual path (the gradient of both
+    x and f): the bits of ``layernorm_bwd`` followed by ``+ dres``."""
+    return _ops.add_layernorm_bwd.default(xsum, gamma, mean, rstd, dy, dres)
+
+
+@torch.library.register_fake("cuda_transformer::add_layernorm_bwd")
+def _(xsum, gamma, mean, rstd, dy, dres):
+    _f32(xsum, gamma, mean, rstd, dy, dres)
+    _same_device(xsum, gamma, mean, rstd, dy, dres)
+    n = xsum.size(-1)
+    return (torch.empty_like(xsum), torch.empty(n, dtype=xsum.dtype, device=xsum.device),
+            torch.empty(n, dtype=xsum.dtype, device=xsum.device))

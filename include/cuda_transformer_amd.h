@@ -391,6 +391,23 @@ int cta_layernorm_bwd(const float* x, const float* gamma, const float* mean,
                       const float* rstd, const float* dy, int64_t rows, int64_t n,
                       float* dx, float* dgamma, float* dbeta, float* workspace, void* stream);
 
+/* A residual add fused with the LayerNorm that follows it: xsum = x + f, y = LayerNorm(xsum)
+ * (mean, rstd of xsum), one pass.  Bitwise equal to an elementwise add followed by
+ * cta_layernorm_fwd.  No reference counterpart: the pre-LN block's `x + attn(...)` /
+ * `x + mlp(...)` followed by the next LayerNorm (gpt/gpt.py:147-150, 47-59). */
+int cta_add_layernorm_fwd(const float* x, const float* f, const float* gamma, const float* beta,
+                          int64_t rows, int64_t n, float eps, float* xsum, float* y,
+                          float* mean, float* rstd, void* stream);
+
+/* Backward of cta_add_layernorm_fwd: dx = LayerNorm backward of dy at xsum, plus dres (the
+ * gradient reaching xsum by the residual path); the gradient of both x and f.  dgamma, dbeta
+ * as cta_layernorm_bwd; workspace from cta_layernorm_bwd_workspace.  Bitwise equal to
+ * cta_layernorm_bwd followed by an elementwise add of dres.  No reference counterpart. */
+int cta_add_layernorm_bwd(const float* xsum, const float* gamma, const float* mean,
+                          const float* rstd, const float* dy, const float* dres, int64_t rows,
+                          int64_t n, float* dx, float* dgamma, float* dbeta, float* workspace,
+                          void* stream);
+
 /* ------------------------------------------------------------------------------
  * Materialised causal self-attention (API parity with the reference's naive path).
  * ---------------------------------------------------------------------------- */

@@ -77,6 +77,10 @@ def test_other_entry_points_validate_arguments():
     lib = capi.lib()
     s3 = capi.strides((1, 1, 1))
     assert lib.cta_cuda_fma(16, s3, 16, s3, 16, 1, 2, 3, 4, 5, 3, 16, None, None) == INVALID  # w_batch
+    # the residual LayerNorm needs its residual operand
+    assert lib.cta_add_layernorm_fwd(16, None, 16, 16, 4, 8, 1e-5, 16, 16, 16, 16, None) == INVALID
+    assert lib.cta_add_layernorm_fwd(16, 16, 16, 16, 4, 8, 1e-5, None, 16, 16, 16, None) == INVALID
+    assert lib.cta_add_layernorm_bwd(16, 16, 16, 16, 16, None, 4, 8, 16, 16, 16, 16, None) == INVALID
     s2 = capi.strides((1, 1))
     assert lib.cta_linear_weight_bias_grad(16, s2, 16, s2, -1, 2, 3, 16, 16, None, None) == INVALID
     assert lib.cta_linear_weight_bias_grad(16, s2, 16, s2, 4, 2, 3, 16, None, None, None) == INVALID

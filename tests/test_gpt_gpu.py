@@ -43,15 +43,17 @@ def test_gpt_training_steps_match_cpu_reference(cuda, fused_adamw):
         torch.testing.assert_close(p.detach().cpu(), q.detach(), rtol=1e-3, atol=1e-4, msg=name)
 
 
-def test_gpt_fused_mlp_matches_reference_composition(cuda):
-    """GPTConfig.fused_mlp (CudaMLP) against the reference's Linear -> GELU -> Linear modules:
-    the same loss and gradients, bit for bit (the embedding gradients, accumulated by torch's
-    own embedding backward, to FP32 rounding)."""
+@pytest.mark.parametrize("flag", ["fused_mlp", "fused_residual_ln"])
+def test_gpt_fusions_match_reference_composition(cuda, flag):
+    """GPTConfig.fused_mlp (CudaMLP) against the reference's Linear -> GELU -> Linear modules,
+    and GPTConfig.fused_residual_ln (CudaAddLayerNorm) against separate residual adds and
+    LayerNorms: the same loss and gradients, bit for bit (the embedding gradients, accumulated
+    by torch's own embedding backward, to FP32 rounding)."""
     cfg = GPTConfig(n_layers=2)
     idx, tgt = synthetic_batch(cfg, 8, seed=7)
     runs = []
     for fused in (True, False):
-        model = GPT(GPTConfig(n_layers=2, fused_mlp=fused))
+        model = GPT(GPTConfig(n_layers=2, **{flag: fused}))
         init_weights_(model, seed=3)
         model.to(cuda)
         _, loss = model(idx.to(cuda), tgt.to(cuda))

@@ -611,3 +611,64 @@ def test_reductions_over_zero_rows_are_zero(cuda):
     torch.cuda.synchronize()
     assert torch.equal(db.cpu(), torch.zeros(7))
     assert torch.equal(dg.cpu(), torch.zeros(5)) and torch.equal(dbt.cpu(), torch.zeros(5))
+
+
+@pytest.mark.parametrize("rows,n", [(64, 384), (33, 768), (70, 120), (9, 70), (5, 3000), (4, 2048)])
+def test_add_layernorm_matches_add_then_layernorm(cuda, rows, n):
+    # the fused residual add + LayerNorm against x + f then layernorm_fwd, and its backward
+    # against layernorm_bwd then + dres: bit for bit (register path with float4 and scalar
+    # rows, and the long-row path), and the float64 oracle
+    from cuda_transformer_amd.ops import (add_layernorm_bwd, add_layernorm_fwd, layernorm_bwd,
+                                          layernorm_fwd)
+
+    x = seeded((rows, n), 60).to(cuda)
+    f = seeded((rows, n), 61).to(cuda)
+    gamma = (1.0 + 0.1 * seeded((n,), 62)).to(cuda)
+    beta = (0.1 * seeded((n,), 63)).to(cuda)
+    dy = seeded((rows, n), 64).to(cuda)
+    dres = seeded((rows, n), 65).to(cuda)
+    xs, y, mean, rstd = add_layernorm_fwd(x, f, gamma, beta, 1e-5)
+    y2, mean2, rstd2 = layernorm_fwd(x + f, gamma, beta, 1e-5)
+    assert torch.equal(xs, x + f)
+    assert torch.equal(y, y2) and torch.equal(mean, mean2) and torch.equal(rstd, rstd2)
+    y_r, mean_r, rstd_r = ew.layernorm_forward(f64(x) + f64(f), f64(gamma), f64(beta), 1e-5)
+    np.testing.assert_allclose(f64(y), y_r, atol=2e-5, rtol=1e-5)
+    dx_r, dg_r, db_r = ew.layernorm_backward(f64(x) + f64(f), f64(gamma), mean_r, rstd_r, f64(dy))
+    dx, dg, db = add_layernorm_bwd(xs, gamma, mean, rstd, dy, dres)
+    dx2, dg2, db2 = layernorm_bwd(xs, gamma, mean, rstd, dy)
+    assert torch.equal(dx, dx2 + dres)
+    assert torch.equal(dg, dg2) and torch.equal(db, db2)
+    np.testing.assert_allclose(f64(dx), dx_r + f64(dres), atol=1e-4, rtol=1e-5)
+    np.testing.assert_allclose(f64(dg), dg_r, atol=1e-4, rtol=1e-5)
+
+
+def test_add_layernorm_autograd(cuda):
+    # CudaAddLayerNorm's gradients against x + f -> CudaLayerNorm with autograd summing the two
+    # paths, bit for bit; an unused xsum output leaves the plain LayerNorm backward
+    from cuda_autograd_fns import CudaAddLayerNorm, CudaLayerNorm
+
+    x0 = seeded((4, 16, 384), 66).to(cuda)
+    f0 = seeded((4, 16, 384), 67).to(cuda)
+    g0 = (1.0 + 0.1 * seeded((384,), 68)).to(cuda)
+    b0 = (0.1 * seeded((384,), 69)).to(cuda)
+    gy = seeded((4, 16, 384), 70).to(cuda)
+    gs = seeded((4, 16, 384), 71).to(cuda)
+    grads = []
+    for fused in (True, False):
+        x, f, g, b = (t.clone().requires_grad_() for t in (x0, f0, g0, b0))
+        if fused:
+            xs, y = CudaAddLayerNorm.apply(x, f, g, b, 1e-5)
+        else:
+            xs = x + f
+            y = CudaLayerNorm.apply(xs, g, b, 1e-5)
+        torch.autograd.backward([xs, y], [gs, gy])
+        grads.append([t.grad for t in (x, f, g, b)])
+    for a, r in zip(*grads):
+        assert torch.equal(a, r)
+    x, f, g, b = (t.clone().requires_grad_() for t in (x0, f0, g0, b0))
+    _, y = CudaAddLayerNorm.apply(x, f, g, b, 1e-5)
+    y.backward(gy)
+    xr, fr, gr, br = (t.clone().requires_grad_() for t in (x0, f0, g0, b0))
+    CudaLayerNorm.apply(xr + fr, gr, br, 1e-5).backward(gy)
+    assert torch.equal(x.grad, xr.grad) and torch.equal(f.grad, fr.grad)
+    assert torch.equal(g.grad, gr.grad) and torch.equal(b.grad, br.grad)

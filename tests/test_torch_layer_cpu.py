@@ -69,6 +69,11 @@ def test_meta_shapes():
     assert y.shape == x.shape and mean.shape == rstd.shape == (3, 10)
     dx, dg, db = ops.layernorm_bwd(x, torch.empty(16, **m), mean, rstd, x)
     assert dx.shape == x.shape and dg.shape == db.shape == (16,)
+    from cuda_transformer_amd.ops import add_layernorm_bwd, add_layernorm_fwd
+    xs, y, mean, rstd = add_layernorm_fwd(x, x, torch.empty(16, **m), torch.empty(16, **m), 1e-5)
+    assert xs.shape == y.shape == x.shape and mean.shape == rstd.shape == (3, 10)
+    dx, dg, db = add_layernorm_bwd(xs, torch.empty(16, **m), mean, rstd, x, x)
+    assert dx.shape == x.shape and dg.shape == db.shape == (16,)
 
 
 def test_fake_rejects_wrong_dtype():
