@@ -240,6 +240,30 @@ __device__ __forceinline__ void sched_first_part() {
   }
 }
 
+// Instruction order of a slice's last MFMAs: all of them in a row, or with CS the column-sum
+// adds (NA VALU instructions) one after each of the first MFMAs, where the wave would otherwise
+// wait for the matrix pipe.  (The four adds in a row just before the barrier cost the kernel
+// 2-4%; one per MFMA here, 0-2%.)
+template <int N>
+__device__ __forceinline__ void sched_interleave() {
+  if constexpr (N > 0) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+    sched_interleave<N - 1>();
+  }
+}
+
+template <bool CS, int NM, int NA>
+__device__ __forceinline__ void sched_second_part() {
+  if constexpr (CS) {
+    static_assert(NA <= NM, "one add per MFMA");
+    sched_interleave<NA>();
+    __builtin_amdgcn_sched_group_barrier(0x008, NM - NA, 0);
+  } else {
+    __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+  }
+}
+
 // Stores a wave's block of one output tile.  RAW: the accumulators as they are (split-K
 // partials); otherwise alpha, bias, the causal mask (MASK) and the pointwise stage ACT.  `Cz`
 // and `Xz` are the batch's output and aux planes, row stride srow.  The block is stored through
@@ -426,16 +450,15 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
     mma_chunks<TL, 0, KC / 2>(f0, acc);
     store_slice(la1, buf1, tid);
     store_slice(lb1, buf1 + BM * KP, tid);
-    add_cs(lb1);
     sched_first_part<0, NM1, NVM, NDW>();
-    if constexpr (CS) __builtin_amdgcn_sched_group_barrier(0x002, 4 * LB::LOADS, 0);  // sums last
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     read_frags<TL>(buf1, f1, wm, wn, half, col);
     mma_chunks<TL, KC / 2, KC>(f0, acc);
+    add_cs(lb1);
     __builtin_amdgcn_sched_group_barrier(0x100, NDR, 0);  // LDS reads first
-    __builtin_amdgcn_sched_group_barrier(0x008, NM1, 0);
+    sched_second_part<CS, NM1, 4 * LB::LOADS>();
     __builtin_amdgcn_sched_barrier(0);
     // slice t+1 in f1
     pa.load(la1, t + 3, tid);
@@ -443,16 +466,15 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_kernel(GemmOperand A, GemmOp
     mma_chunks<TL, 0, KC / 2>(f1, acc);
     store_slice(la0, buf0, tid);
     store_slice(lb0, buf0 + BM * KP, tid);
-    add_cs(lb0);
     sched_first_part<0, NM1, NVM, NDW>();
-    if constexpr (CS) __builtin_amdgcn_sched_group_barrier(0x002, 4 * LB::LOADS, 0);  // sums last
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     read_frags<TL>(buf0, f0, wm, wn, half, col);
     mma_chunks<TL, KC / 2, KC>(f1, acc);
+    add_cs(lb0);
     __builtin_amdgcn_sched_group_barrier(0x100, NDR, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, NM1, 0);
+    sched_second_part<CS, NM1, 4 * LB::LOADS>();
     __builtin_amdgcn_sched_barrier(0);
   }
 
