@@ -635,7 +635,8 @@ int64_t splitk_factor(int64_t M, int64_t N, int64_t K, int64_t Z) {
   return best;
 }
 
-template <class TL>
+// ACTS = false: a tile instantiated without the pointwise stages (ep.act must be kActNone).
+template <class TL, bool ACTS = true>
 int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& C,
                      const GemmEpilogue& ep, int64_t M, int64_t N, int64_t K, int64_t Z,
                      int64_t zin, hipStream_t st, float* workspace, int64_t workspace_floats) {
@@ -668,17 +669,22 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
       return fail(CTA_ERR_INVALID_ARGUMENT,
                   "GEMM column sums need one batch, an n-contiguous B and no pointwise stage");
     dispatch_a<TL, kActNone, true>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
-  } else if (act == kActGelu)
-    dispatch_a<TL, kActGelu>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
-  else if (act == kActGeluGrad)
-    dispatch_a<TL, kActGeluGrad>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
-  else if (act == kActGeluTanh)
-    dispatch_a<TL, kActGeluTanh>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
-  else if (act == kActGeluTanhGrad)
-    dispatch_a<TL, kActGeluTanhGrad>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc,
-                                     ws);
-  else
+  } else if constexpr (!ACTS) {
+    if (act != kActNone) return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM tile without pointwise stages");
     dispatch_a<TL, kActNone>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
+  } else {
+    if (act == kActGelu)
+      dispatch_a<TL, kActGelu>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
+    else if (act == kActGeluGrad)
+      dispatch_a<TL, kActGeluGrad>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
+    else if (act == kActGeluTanh)
+      dispatch_a<TL, kActGeluTanh>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
+    else if (act == kActGeluTanhGrad)
+      dispatch_a<TL, kActGeluTanhGrad>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc,
+                                       ws);
+    else
+      dispatch_a<TL, kActNone>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
+  }
   if (S > 1) {
     const int64_t total = Z * M * N + cs_floats;
     const unsigned rgrid = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
@@ -691,10 +697,16 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
 // Tile choice, from measured sweeps of the config-4 and small-GPT shapes on an MI355X:
 // narrow outputs (N <= 768) run best with a 64x128 tile of four 32x64 waves and K-slices of 32,
 // wider ones with a 128x128 tile of four 64x64 waves, and shapes split along K with a 128x128
-// tile of eight 32x64 waves.
+// tile of eight 32x64 waves.  When N is a multiple of 192 the same shapes with 192 columns
+// (waves of 32x96 or 64x96) measured 0-8% faster (cold, A/B in one process): 64x192 with
+// K-slices of 16 for K <= 512 and of 32 beyond, and, without a pointwise stage, 128x192 with
+// K-slices of 16 for N > 768 (with the GELU stages it was slower in the GPT step).
 using SplitTile = GemmTile<128, 128, 16, 4, 2>;
 using NarrowTile = GemmTile<64, 128, 32, 2, 2>;
+using Narrow192Tile = GemmTile<64, 192, 32, 2, 2>;
+using Narrow192ShortKTile = GemmTile<64, 192, 16, 2, 2>;
 using WideTile = GemmTile<128, 128, 16, 2, 2>;
+using Wide192Tile = GemmTile<128, 192, 16, 2, 2>;
 
 }  // namespace
 
@@ -713,8 +725,18 @@ int gemm_launch(const GemmOperand& A, const GemmOperand& B, const GemmOut& C,
       workspace_floats >= S * (Z * M * N + (ep.colsum ? N : 0)))
     return gemm_launch_tile<SplitTile>(A, B, C, ep, M, N, K, Z, zin, st, workspace,
                                        workspace_floats);
-  if (N <= 768)
+  // A product's tile never depends on its pointwise stage alone, except between the two wide
+  // tiles, which share their K-slice (hence the k pairs each MFMA sums): a fused GELU product
+  // stays bitwise equal to the plain product followed by the GELU kernel.
+  const bool n192 = N % 192 == 0;
+  if (N <= 768) {
+    if (n192 && K <= 512)
+      return gemm_launch_tile<Narrow192ShortKTile>(A, B, C, ep, M, N, K, Z, zin, st, nullptr, 0);
+    if (n192) return gemm_launch_tile<Narrow192Tile>(A, B, C, ep, M, N, K, Z, zin, st, nullptr, 0);
     return gemm_launch_tile<NarrowTile>(A, B, C, ep, M, N, K, Z, zin, st, nullptr, 0);
+  }
+  if (n192 && ep.act == kActNone)
+    return gemm_launch_tile<Wide192Tile, false>(A, B, C, ep, M, N, K, Z, zin, st, nullptr, 0);
   return gemm_launch_tile<WideTile>(A, B, C, ep, M, N, K, Z, zin, st, nullptr, 0);
 }
 

@@ -360,6 +360,27 @@ def test_linear_batched_tiles_over_xcds(cuda, B, M, K, N):
     assert rel_err(f64(out), f64(x) @ f64(wb) + f64(b)) <= 1e-6
 
 
+# (B, M, K, N) with N a multiple of 192 (the 192-column tiles): short and long K, ragged M and
+# K, one tile column, and N > 768
+@pytest.mark.parametrize("B,M,K,N", [(1, 333, 200, 576), (2, 100, 700, 192), (1, 130, 37, 384),
+                                     (1, 257, 1000, 768), (3, 70, 96, 960), (1, 200, 300, 1152)])
+def test_linear_192_column_tiles(cuda, B, M, K, N):
+    from cuda_transformer.ops import cuda_fma, cuda_fma_gelu
+
+    x = seeded((B, M, K), 50).to(cuda)
+    w = seeded((K, N), 51).to(cuda) * 0.1
+    b = seeded((N,), 52).to(cuda)
+    ref = lin.fma_forward(f64(x), f64(w), f64(b))
+    assert rel_err(f64(cuda_fma(x, w, b)), ref) <= 1e-5
+    pre, h = cuda_fma_gelu(x, w, b)
+    assert torch.equal(pre, cuda_fma(x, w, b))
+    np.testing.assert_allclose(f64(h), ew.gelu_forward(f64(pre)), atol=1e-5, rtol=1e-5)
+    # transposed operands (the linear backward's dx and dW views)
+    dy = seeded((B, M, N), 53).to(cuda)
+    dx = cuda_fma(dy, w.unsqueeze(0).transpose(1, 2), torch.zeros(K, device=cuda))
+    assert rel_err(f64(dx), f64(dy) @ f64(w).T) <= 1e-5
+
+
 def test_linear_operand_strides_past_buffer_offsets(cuda):
     """Operand views whose strides put a tile's rows more than 2 GiB apart cannot be addressed
     with 32-bit buffer offsets; they take the scalar load path and stay exact."""
