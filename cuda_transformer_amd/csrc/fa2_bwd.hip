@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
   __shared__ __attribute__((aligned(16))) float smem[2 * 2 * TILE];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_index();
   const int half = lane >> 5, col = lane & 31;
   // Head-major items over XCDs; causal items are query-tile pairs (n-1-p, p) of equal cost.
   const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
@@ -601,7 +601,7 @@ __global__ __launch_bounds__(256, 2) void fa2_bwd_dq_ds_kernel(
   __shared__ __attribute__((aligned(16))) float smem[2 * TILE];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_index();
   const int half = lane >> 5, col = lane & 31;
   // Head-major items over XCDs; causal items are query-tile pairs (n-1-p, p) of equal cost.
   const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;

@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   __shared__ __attribute__((aligned(16))) float smem[2 * (KTILE + VTILE)];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_index();
   const int half = lane >> 5, col = lane & 31;
   // Work items are head-major and spread over XCDs.  Causal: one item = the query-tile pair
   // (n-1-p, p), so every item costs n+1 tile units and the dynamic dispatch has no tail.
