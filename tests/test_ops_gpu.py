@@ -415,10 +415,12 @@ def test_db_strided_views(cuda):
 
 
 # (rows, k, n): split-K with the SplitTile (GPT qkv / fc2 weight gradients, config 4), one
-# unsplit 128x128-tile GEMM (256 tiles), unsplit narrow tiles with ragged rows, and n % 4 != 0
-# (dy not vector-loadable: GEMM then the column-sum kernels).
+# unsplit 128x128-tile GEMM (256 tiles), unsplit narrow tiles with ragged rows, the unsplit
+# 192-column tiles (64x192 with K-slices of 16 and 32, 128x192), and n % 4 != 0 (dy not
+# vector-loadable: GEMM then the column-sum kernels).
 WB_SHAPES = [(16384, 384, 1152), (16384, 1536, 384), (8192, 768, 3072), (2048, 2048, 2048),
-             (333, 64, 100), (1000, 20, 36), (100, 48, 65), (5, 7, 12)]
+             (333, 64, 100), (1000, 20, 36), (300, 64, 192), (800, 128, 384), (1000, 256, 1152),
+             (100, 48, 65), (5, 7, 12)]
 
 
 @pytest.mark.parametrize("rows,k,n", WB_SHAPES)
