@@ -173,6 +173,12 @@ __device__ __forceinline__ void async_copy16(const float* g, float* lds) {
 __device__ __forceinline__ void async_copy4(const float* g, float* lds) {
   __builtin_amdgcn_global_load_lds(static_cast<const void*>(g), (lds_void_t*)(lds), 4, 0, 0);
 }
+// The same 16-byte copy through a buffer resource: voff is the lane's byte offset in it
+// (out of range: nothing read).
+__device__ __forceinline__ void async_copy16_buffer(__amdgpu_buffer_rsrc_t rs, int voff,
+                                                    float* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds), 16, voff, 0, 0, 0);
+}
 // s_waitcnt vmcnt(0): all of this wave's vector memory operations have completed.
 __device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -263,6 +269,8 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // Attention operands: unit d-stride, (b, h, t) strides divisible by 4, 16-byte aligned base.
+// Time strides (elements) of FP32 attention operands must lie in [0, kMaxAttnTimeStride).
+constexpr int64_t kMaxAttnTimeStride = (int64_t)1 << 23;
 bool attn_layout_ok(const float* p, const int64_t* s);
 // Zero n floats with a fill kernel on `st`, not hipMemsetAsync: memset nodes recorded into a
 // captured HIP graph have given wrong results on replays after the first.

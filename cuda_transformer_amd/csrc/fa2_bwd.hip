@@ -299,10 +299,11 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
   constexpr int BM = 32 * WAVES;  // key rows per workgroup, 32 per wave
   constexpr int H2 = HS / 2;
   constexpr int KP = HS + 4;                // LDS pitch of a Q / dO row
-  constexpr int TILE = BN * KP;
+  constexpr int PPT = (BN * KP + 255) / 256;  // 1 KiB async copies per tile
+  constexpr int TILE = PPT * 256;           // a tile's LDS extent: whole copies, rows then pad
   constexpr int NT = FOLD ? 3 : 2;          // tiles per stage: Q, dO (and O when folding delta)
-  constexpr int PIECES = (NT * TILE + 255) / 256;  // 1 KiB async copies covering the tiles
-  constexpr int QG = PIECES * 256;          // the tiles and the tail of the last piece
+  constexpr int PIECES = NT * PPT;
+  constexpr int QG = PIECES * 256;
   constexpr int RVEC = 64;                  // L and delta of a stage, padded to one wave
   constexpr int STAGE = QG + 2 * RVEC;
   constexpr int PER_WAVE = (PIECES + WAVES - 1) / WAVES;
@@ -328,9 +329,27 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
   const float* Lb = Lg + b * sl.b + h * sl.h;
   const float* Db = FOLD ? nullptr : delta + (int64_t)bh * T;
   const int nb = (T + 31) / 32;
+  // Byte offset of each of this lane's copies within its tile's first row of a stage: copy pc
+  // fills floats [256 (pc % PPT), +256) of tile pc / PPT, the lane 4 of them at row f / KP,
+  // column f % KP.  Pad columns and rows past the tile are out of range (no bytes read).
+  int voff[PER_WAVE];
+#pragma unroll
+  for (int u = 0; u < PER_WAVE; ++u) {
+    const int pc = wave + WAVES * u;
+    const int which = pc / PPT;
+    const int f = (pc - which * PPT) * 256 + lane * 4;
+    const int r = f / KP, c = f - r * KP;
+    const int64_t st = which == 0 ? sq.t : (FOLD && which == 2) ? so.t : sdo.t;
+    voff[u] = pc < PIECES && r < BN && c < HS ? (int)((r * st + c) * 4) : (int)0x80000000;
+  }
   float* xpose = smem + 2 * STAGE + wave * NSUB * 32 * kDsPitch;  // this wave's dS buffers
   float* dsh = STORE_DS ? dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileFloats
                         : nullptr;
+
+  // Both stage buffers start as zeros, so the rows and pad words no copy writes are finite.
+#pragma unroll 4
+  for (int e = 4 * tid; e < 2 * STAGE; e += 4 * THREADS) st4(smem + e, zero4());
+  __syncthreads();
 
   const int n_pass = (CAUSAL && n_ktiles - 1 - p != p) ? 2 : 1;
   for (int pass = 0; pass < n_pass; ++pass) {
@@ -364,22 +383,26 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
 
   // Async copies of stage `stage` into buffer `buf`.  Piece pc covers floats
   // [256 pc, 256 pc + 256) of the Q|dO region; wave w copies pieces w, w + WAVES, ...
+  // Each tile of a stage is read through a buffer resource over its valid rows (base and
+  // extent are scalar), so the per-lane offsets above serve every stage; rows past T are out of
+  // range and keep the zeros (or an earlier stage's rows) in LDS, masked to P = 0.
   auto issue = [&](int stage, int buf) {
     float* qs = smem + buf * STAGE;
     const int r0 = stage * BN;
+    const int rows = min(BN, T - r0);
+    auto rsrc = [&](const float* base, int64_t st) {
+      return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base + (int64_t)r0 * st),
+                                               (short)0, (int)(((rows - 1) * st + HS) * 4),
+                                               0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t rq = rsrc(Qb, sq.t), rg = rsrc(dOb, sdo.t);
+    const __amdgpu_buffer_rsrc_t ro = FOLD ? rsrc(Ob, so.t) : rq;
 #pragma unroll
     for (int u = 0; u < PER_WAVE; ++u) {
       const int pc = wave + WAVES * u;
       if (pc < PIECES) {
-        const int f = pc * 256 + lane * 4;  // float offset this lane fills
-        const int which = f / TILE;         // 0: Q, 1: dO, 2: O (FOLD), else tail
-        const int rem = f - which * TILE;
-        const int r = rem / KP, c = rem - r * KP;
-        const int64_t i = min(r0 + r, T - 1);
-        const float* src = which == 0 ? Qb + i * sq.t
-                         : (FOLD && which == 2) ? Ob + i * so.t : dOb + i * sdo.t;
-        // pad words and the tail take the row's first chunk: in bounds and never read
-        async_copy16(which < NT && c < HS ? src + c : Qb + i * sq.t, qs + pc * 256);
+        const int which = pc / PPT;  // 0: Q, 1: dO, 2: O (FOLD)
+        async_copy16_buffer(which == 0 ? rq : which == 1 ? rg : ro, voff[u], qs + pc * 256);
       }
     }
     if (wave == 0) {  // lanes past BN fill the padding
@@ -827,7 +850,7 @@ extern "C" int cta_flash_attention_bwd_delta(const float* o, const int64_t* o_st
   if (!delta) return fail(CTA_ERR_INVALID_ARGUMENT, "null delta pointer");
   if (!attn_layout_ok(o, o_strides) || !attn_layout_ok(d_o, do_strides))
     return fail(CTA_ERR_LAYOUT,
-                "flash_attention_bwd needs unit d-stride, strides divisible by 4 and 16-byte "
+                "flash_attention_bwd needs unit d-stride, strides divisible by 4, time strides below 2^23 and 16-byte "
                 "aligned O/dO");
   const int64_t rows = B * nh * T;
   hipStream_t st = as_stream(stream);
@@ -844,7 +867,7 @@ int check_bwd_inputs(const float* q, const int64_t* qs, const float* k, const in
   if (!attn_layout_ok(q, qs) || !attn_layout_ok(k, ks) || !attn_layout_ok(v, vs) ||
       !attn_layout_ok(d_o, dos))
     return fail(CTA_ERR_LAYOUT,
-                "flash_attention_bwd needs unit d-stride, strides divisible by 4 and 16-byte "
+                "flash_attention_bwd needs unit d-stride, strides divisible by 4, time strides below 2^23 and 16-byte "
                 "aligned Q/K/V/dO");
   if (!l_ok(l, ls) || !delta) return fail(CTA_ERR_INVALID_ARGUMENT, "null L or delta pointer");
   return CTA_OK;
@@ -964,7 +987,7 @@ extern "C" int cta_flash_attention_bwd_dq_from_ds(const float* k, const int64_t*
   if (B * nh * T == 0) return CTA_OK;
   if (!attn_layout_ok(k, k_strides))
     return fail(CTA_ERR_LAYOUT,
-                "flash_attention_bwd needs unit d-stride, strides divisible by 4 and 16-byte "
+                "flash_attention_bwd needs unit d-stride, strides divisible by 4, time strides below 2^23 and 16-byte "
                 "aligned K");
   if (!dq || !aligned16(dq) || !ds_workspace || !aligned16(ds_workspace))
     return fail(CTA_ERR_LAYOUT, "dQ and the dS workspace must be 16-byte aligned pointers");
@@ -995,7 +1018,7 @@ extern "C" int cta_flash_attention_bwd_strided(
   if (!attn_layout_ok(dq, dq_strides) || !attn_layout_ok(dk, dk_strides) ||
       !attn_layout_ok(dv, dv_strides))
     return fail(CTA_ERR_LAYOUT,
-                "flash_attention_bwd needs unit d-stride, strides divisible by 4 and 16-byte "
+                "flash_attention_bwd needs unit d-stride, strides divisible by 4, time strides below 2^23 and 16-byte "
                 "aligned dQ/dK/dV");
   const RowStrides sdq = rs(dq_strides), sdk = rs(dk_strides), sdv = rs(dv_strides);
   hipStream_t st = as_stream(stream);
@@ -1059,7 +1082,7 @@ extern "C" int cta_flash_attention_bwd_fold_delta(
       !attn_layout_ok(v, v_strides) || !attn_layout_ok(o, o_strides) ||
       !attn_layout_ok(d_o, do_strides))
     return fail(CTA_ERR_LAYOUT,
-                "flash_attention_bwd needs unit d-stride, strides divisible by 4 and 16-byte "
+                "flash_attention_bwd needs unit d-stride, strides divisible by 4, time strides below 2^23 and 16-byte "
                 "aligned Q/K/V/O/dO");
   if (!l_ok(l, l_strides)) return fail(CTA_ERR_INVALID_ARGUMENT, "null L pointer");
   const int64_t head_bytes = cta_flash_attention_bwd_workspace(1, 1, T, hs, causal);

@@ -257,9 +257,11 @@ void launch_fwd(const float* q, const float* k, const float* v, float* o, float*
 
 }  // namespace
 
+// The kernels read 16-byte row segments (unit d-stride, strides divisible by 4, 16-byte aligned
+// base) and address a stage of up to 64 rows with 32-bit byte offsets (time stride 0 to 2^23).
 bool attn_layout_ok(const float* p, const int64_t* s) {
   return p != nullptr && s != nullptr && aligned16(p) && s[3] == 1 && s[0] % 4 == 0 &&
-         s[1] % 4 == 0 && s[2] % 4 == 0;
+         s[1] % 4 == 0 && s[2] % 4 == 0 && s[2] >= 0 && s[2] < kMaxAttnTimeStride;
 }
 
 int check_attn_sizes(int64_t B, int64_t nh, int64_t T, int64_t hs) {
@@ -288,7 +290,7 @@ extern "C" int cta_flash_attention_fwd_strided(const float* q, const int64_t* q_
   if (!attn_layout_ok(q, q_strides) || !attn_layout_ok(k, k_strides) ||
       !attn_layout_ok(v, v_strides) || !attn_layout_ok(o, o_strides))
     return fail(CTA_ERR_LAYOUT,
-                "flash_attention_fwd needs unit d-stride, strides divisible by 4 and 16-byte "
+                "flash_attention_fwd needs unit d-stride, strides divisible by 4, time strides below 2^23 and 16-byte "
                 "aligned Q/K/V/O");
   const RowStrides sq{q_strides[0], q_strides[1], q_strides[2]};
   const RowStrides sk{k_strides[0], k_strides[1], k_strides[2]};

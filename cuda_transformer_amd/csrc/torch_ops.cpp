@@ -59,11 +59,12 @@ std::array<int64_t, N> strides_of(const at::Tensor& t) {
 }
 
 // The attention kernels read 16-byte row segments: unit d-stride, strides divisible by 4,
-// 16-byte aligned base.  Anything else is passed as a dense copy.
+// 16-byte aligned base, time stride in [0, 2^23).  Anything else is passed as a dense copy.
 bool attn_layout_ok(const at::Tensor& t) {
   const auto s = strides_of<4>(t);
   return (t.size(3) == 1 || t.stride(3) == 1) && s[0] % 4 == 0 && s[1] % 4 == 0 &&
-         s[2] % 4 == 0 && (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) == 0;
+         s[2] % 4 == 0 && s[2] >= 0 && s[2] < ((int64_t)1 << 23) &&
+         (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) == 0;
 }
 
 at::Tensor attn_operand(const at::Tensor& t) {

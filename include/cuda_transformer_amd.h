@@ -45,8 +45,8 @@ const char* cta_version(void);
  * softmax scale = 1/sqrt(hs) (the reference launcher passes sqrt(hs) and the
  * kernel inverts it: flash_attn_launcher.cu:27, flash_attention.cuh:45).
  * Q/K/V/O/dO strides: 4 entries (b, h, t, d).  The kernels need d-stride 1, other
- * strides divisible by 4 and 16-byte aligned base pointers (CTA_ERR_LAYOUT
- * otherwise; the torch layer passes a dense copy in that case).
+ * strides divisible by 4, a t-stride in [0, 2^23) and 16-byte aligned base pointers
+ * (CTA_ERR_LAYOUT otherwise; the torch layer passes a dense copy in that case).
  * L strides: 3 entries (b, h, t), any values.
  * ---------------------------------------------------------------------------- */
 
