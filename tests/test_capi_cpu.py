@@ -49,6 +49,10 @@ def test_layout_checks_run_before_launch():
     assert _fwd(s=(512, 512, 64, 2)) == LAYOUT
     assert _fwd(s=(512, 512, 66, 1)) == LAYOUT
     assert b"16-byte" in capi.lib().cta_last_error()
+    # a stage of 64 rows must fit 32-bit byte offsets: time strides in [0, 2^23)
+    assert _fwd(s=(1 << 24, 1 << 24, 1 << 23, 1)) == LAYOUT
+    assert _fwd(s=(512, 512, -64, 1)) == LAYOUT
+    assert b"2^23" in capi.lib().cta_last_error()
 
 
 def test_workspace_queries():
