@@ -173,6 +173,20 @@ __device__ __forceinline__ void async_copy16(const float* g, float* lds) {
 __device__ __forceinline__ void async_copy4(const float* g, float* lds) {
   __builtin_amdgcn_global_load_lds(static_cast<const void*>(g), (lds_void_t*)(lds), 4, 0, 0);
 }
+// Buffer resource over `rows` rows (stride st floats, `width` floats used) from base; no rows:
+// an empty range.  Offsets past the range read as zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, int rows,
+                                                            int64_t st, int width) {
+  const int nbytes = rows > 0 ? (int)(((int64_t)(rows - 1) * st + width) * 4) : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, nbytes,
+                                           0x00020000);
+}
+// 16 bytes at byte offset voff of a buffer resource (zeros out of range).
+__device__ __forceinline__ float4 ld4_buffer(__amdgpu_buffer_rsrc_t rs, int voff) {
+  const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, 0);
+  return make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z),
+                     __uint_as_float(w.w));
+}
 // The same 16-byte copy through a buffer resource: voff is the lane's byte offset in it
 // (out of range: nothing read).
 __device__ __forceinline__ void async_copy16_buffer(__amdgpu_buffer_rsrc_t rs, int voff,

@@ -154,20 +154,18 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
   const int n_stages = (kv_end + BN - 1) / BN;
 
   float4 kst[LOADS], vst[LOADS];
+  // K/V rows of a stage through buffer resources over its valid rows: past T they read zero.
   auto gload = [&](int stage) {
     const int j0 = stage * BN;
+    const int rows = min(BN, T - j0);
+    const __amdgpu_buffer_rsrc_t rk = rows_rsrc(Kb + (int64_t)j0 * sk.t, rows, sk.t, HS);
+    const __amdgpu_buffer_rsrc_t rv = rows_rsrc(Vb + (int64_t)j0 * sv.t, rows, sv.t, HS);
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int f = tid + 256 * u;
       const int r = f / F4_ROW, c4 = f % F4_ROW;
-      const int j = j0 + r;
-      if (j < T) {
-        kst[u] = ld4(Kb + (int64_t)j * sk.t + 4 * c4);
-        vst[u] = ld4(Vb + (int64_t)j * sv.t + 4 * c4);
-      } else {
-        kst[u] = zero4();
-        vst[u] = zero4();
-      }
+      kst[u] = ld4_buffer(rk, (r * (int)sk.t + 4 * c4) * 4);
+      vst[u] = ld4_buffer(rv, (r * (int)sv.t + 4 * c4) * 4);
     }
   };
   auto lstore = [&](int buf) {
@@ -391,9 +389,7 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
     const int r0 = stage * BN;
     const int rows = min(BN, T - r0);
     auto rsrc = [&](const float* base, int64_t st) {
-      return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base + (int64_t)r0 * st),
-                                               (short)0, (int)(((rows - 1) * st + HS) * 4),
-                                               0x00020000);
+      return rows_rsrc(base + (int64_t)r0 * st, rows, st, HS);
     };
     const __amdgpu_buffer_rsrc_t rq = rsrc(Qb, sq.t), rg = rsrc(dOb, sdo.t);
     const __amdgpu_buffer_rsrc_t ro = FOLD ? rsrc(Ob, so.t) : rq;
@@ -656,20 +652,23 @@ __global__ __launch_bounds__(64 * WAVES, 2) void fa2_bwd_dq_ds_kernel(
   const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
   const int n_stages = (kv_end + BN - 1) / BN;
 
-  // Every stage issues the same loads, unconditionally, from clamped in-bounds addresses, and
-  // the stage count is padded to even (padded stages compute nothing).  The compiler can then
+  // Every stage issues the same loads, unconditionally (K through a buffer resource, dS from
+  // clamped in-bounds tiles), and the stage count is padded to even (padded stages compute
+  // nothing).  The compiler can then
   // count the loads in flight exactly: the MFMAs of stage s wait only for stage s's dS, not
   // for the stage s+1 loads issued ahead of them.
   float4 kst[LOADS];
+  // K rows through a buffer resource over the stage's valid rows (none for a padded stage):
+  // keys past T read as zero, as they must, since they meet finite dS columns.
   auto gload = [&](int stage) {
     const int j0 = stage * BN;
+    const int rows = min(BN, T - j0);
+    const __amdgpu_buffer_rsrc_t rk = rows_rsrc(Kb + (int64_t)j0 * sk.t, rows, sk.t, HS);
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int f = tid + THREADS * u;
       const int r = f / F4_ROW, c4 = f % F4_ROW;
-      const int j = j0 + r;
-      const float4 kv = ld4(Kb + (int64_t)min(j, T - 1) * sk.t + 4 * c4);
-      kst[u] = j < T ? kv : zero4();  // keys past T meet finite dS columns: K must be 0 there
+      kst[u] = ld4_buffer(rk, (r * (int)sk.t + 4 * c4) * 4);
     }
   };
   auto lstore = [&](int buf) {

@@ -104,20 +104,19 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   const int n_stages = (kv_end + BN - 1) / BN;
 
   float4 kst[LOADS], vst[LOADS];
+  // K/V rows of a stage through buffer resources over its valid rows (scalar base and extent;
+  // the lanes' offsets are the same every stage): rows past T read as zero.
   auto gload = [&](int stage) {
     const int j0 = stage * BN;
+    const int rows = min(BN, T - j0);
+    const __amdgpu_buffer_rsrc_t rk = rows_rsrc(Kb + (int64_t)j0 * sk.t, rows, sk.t, HS);
+    const __amdgpu_buffer_rsrc_t rv = rows_rsrc(Vb + (int64_t)j0 * sv.t, rows, sv.t, HS);
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int f = tid + THREADS * u;
       const int r = f / F4_ROW, c4 = f % F4_ROW;
-      const int j = j0 + r;
-      if (j < T) {
-        kst[u] = ld4(Kb + (int64_t)j * sk.t + 4 * c4);
-        vst[u] = ld4(Vb + (int64_t)j * sv.t + 4 * c4);
-      } else {
-        kst[u] = zero4();
-        vst[u] = zero4();
-      }
+      kst[u] = ld4_buffer(rk, (r * (int)sk.t + 4 * c4) * 4);
+      vst[u] = ld4_buffer(rv, (r * (int)sv.t + 4 * c4) * 4);
     }
   };
   auto lstore = [&](int buf) {
