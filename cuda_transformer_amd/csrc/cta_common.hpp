@@ -181,6 +181,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, i
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, nbytes,
                                            0x00020000);
 }
+// The same over rows of 16-bit elements (stride st and width in elements).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc16(const void* base, int rows,
+                                                              int64_t st, int width) {
+  const int nbytes = rows > 0 ? (int)(((int64_t)(rows - 1) * st + width) * 2) : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nbytes,
+                                           0x00020000);
+}
+// 16 raw bytes at byte offset voff of a buffer resource (zeros out of range).
+__device__ __forceinline__ u32x4 ld16_buffer(__amdgpu_buffer_rsrc_t rs, int voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, 0);
+}
 // 16 bytes at byte offset voff of a buffer resource (zeros out of range).
 __device__ __forceinline__ float4 ld4_buffer(__amdgpu_buffer_rsrc_t rs, int voff) {
   const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, 0);

@@ -472,17 +472,20 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_ds_half_ker
     ch = 2 * (wave + 4 * u2) + (lane >> 5);
     return KPAIRS % 256 == 0 || ch < CH;
   };
+  // K rows through a buffer resource over the stage's valid rows: keys past T read as zero, as
+  // they must, since they meet finite dS columns.
   auto gload = [&](int stage) {
+    const int j0 = stage * BN;
+    const __amdgpu_buffer_rsrc_t rk =
+        rows_rsrc16(Kb + (int64_t)j0 * sk.t, min(BN, T - j0), sk.t, HS);
 #pragma unroll
     for (int u2 = 0; u2 < KL; ++u2) {
       int rp, ch;
       if (!pair_of(u2, rp, ch)) continue;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        const int j = stage * BN + 2 * rp + e;
-        const uint4 kv =
-            *reinterpret_cast<const uint4*>(Kb + (int64_t)min(j, T - 1) * sk.t + 8 * ch);
-        kst[2 * u2 + e] = j < T ? kv : make_uint4(0, 0, 0, 0);  // keys past T: K must be 0
+        const u32x4 w = ld16_buffer(rk, ((2 * rp + e) * (int)sk.t + 8 * ch) * 2);
+        kst[2 * u2 + e] = make_uint4(w.x, w.y, w.z, w.w);
       }
     }
   };
@@ -566,7 +569,7 @@ RowStridesH rsh(const int64_t* s) { return RowStridesH{s[0], s[1], s[2]}; }
 
 bool layout_half_ok(const void* p, const int64_t* s) {
   return p != nullptr && s != nullptr && aligned16(p) && s[3] == 1 && s[0] % 8 == 0 &&
-         s[1] % 8 == 0 && s[2] % 8 == 0;
+         s[1] % 8 == 0 && s[2] % 8 == 0 && s[2] >= 0 && s[2] < (int64_t(1) << 24);
 }
 
 template <typename F>
@@ -603,8 +606,8 @@ int bwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
       !layout_half_ok(v, v_strides) || !layout_half_ok(o, o_strides) ||
       !layout_half_ok(d_o, do_strides))
     return fail(CTA_ERR_LAYOUT, std::string("flash_attention_bwd (") + what +
-                                    ") needs unit d-stride, strides divisible by 8 and 16-byte "
-                                    "aligned Q/K/V/O/dO");
+                                    ") needs unit d-stride, strides divisible by 8, time "
+                                    "strides below 2^24 and 16-byte aligned Q/K/V/O/dO");
   if (!l || !l_strides || !delta) return fail(CTA_ERR_INVALID_ARGUMENT, "null L or delta pointer");
   if (!dq || !dk || !dv || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
       !aligned16(workspace))

@@ -111,26 +111,27 @@ __global__ __launch_bounds__(256, 2) void fa2_fwd_half_kernel(
     ch = 2 * (wave + 4 * u2) + (lane >> 5);
     return VPAIRS % 256 == 0 || ch < CH;
   };
-  // Rows past T are read clamped to row T - 1: those keys are masked to P = 0, so their finite
-  // values never reach O.  Row strides are below 2^31 (checked on the host), so an address is
-  // one 32 x 32 -> 64-bit multiply-add.
+  // K/V rows of a stage through buffer resources over its valid rows (scalar base and extent,
+  // the same lane offsets every stage).  Rows past T read as zero: those keys are masked to
+  // P = 0, so they never reach O.  A stage's 64 rows fit 32-bit offsets (time strides below
+  // 2^23, checked on the host).
   auto gload = [&](int stage) {
+    const int j0 = stage * BN;
+    const int rows = min(BN, T - j0);
+    const __amdgpu_buffer_rsrc_t rk = rows_rsrc16(Kb + (int64_t)j0 * sk.t, rows, sk.t, HS);
+    const __amdgpu_buffer_rsrc_t rv = rows_rsrc16(Vb + (int64_t)j0 * sv.t, rows, sv.t, HS);
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int c = tid + 256 * u;
-      const uint32_t j = min(stage * BN + c / CH, T - 1);
-      kst[u] = *reinterpret_cast<const u32x4*>(Kb + 8 * (c % CH) + (uint64_t)j * (uint32_t)sk.t);
+      kst[u] = ld16_buffer(rk, ((c / CH) * (int)sk.t + 8 * (c % CH)) * 2);
     }
 #pragma unroll
     for (int u2 = 0; u2 < VL; ++u2) {
       int rp, ch;
       if (!vtask(u2, rp, ch)) continue;
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const uint32_t j = min(stage * BN + 2 * rp + e, T - 1);
-        vst[2 * u2 + e] =
-            *reinterpret_cast<const u32x4*>(Vb + 8 * ch + (uint64_t)j * (uint32_t)sv.t);
-      }
+      for (int e = 0; e < 2; ++e)
+        vst[2 * u2 + e] = ld16_buffer(rv, ((2 * rp + e) * (int)sv.t + 8 * ch) * 2);
     }
   };
   auto lstore = [&](int buf) {
@@ -321,10 +322,11 @@ void launch_fwd_half(const E* q, const E* k, const E* v, E* o, float* l, int nh,
                      k, v, o, l, nh, T, BH, n_qtiles, sq, sk, sv, scale * kLog2e);
 }
 
-// 16-bit operands: unit d-stride, (b, h, t) strides divisible by 8 elements, 16-byte aligned.
+// 16-bit operands: unit d-stride, (b, h, t) strides divisible by 8 elements, 16-byte aligned,
+// time stride in [0, 2^24) (a stage's 64 rows fit 32-bit byte offsets).
 bool attn_layout_half_ok(const void* p, const int64_t* s) {
   return p != nullptr && s != nullptr && aligned16(p) && s[3] == 1 && s[0] % 8 == 0 &&
-         s[1] % 8 == 0 && s[2] % 8 == 0;
+         s[1] % 8 == 0 && s[2] % 8 == 0 && s[2] >= 0 && s[2] < (int64_t(1) << 24);
 }
 
 // The entry points' shared body; `what` names the element type in error messages.
@@ -339,12 +341,8 @@ int fwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
   if (!attn_layout_half_ok(q, q_strides) || !attn_layout_half_ok(k, k_strides) ||
       !attn_layout_half_ok(v, v_strides) || !aligned16(o))
     return fail(CTA_ERR_LAYOUT, std::string("flash_attention_fwd (") + what +
-                                    ") needs unit d-stride, strides divisible by 8 and 16-byte "
-                                    "aligned Q/K/V/O");
-  for (const int64_t* st : {q_strides, k_strides, v_strides})
-    if (st[2] >= (int64_t(1) << 31))
-      return fail(CTA_ERR_LAYOUT, std::string("flash_attention_fwd (") + what +
-                                      ") needs row strides below 2^31 elements");
+                                    ") needs unit d-stride, strides divisible by 8, time "
+                                    "strides below 2^24 and 16-byte aligned Q/K/V/O");
   const RowStridesB sq{q_strides[0], q_strides[1], q_strides[2]};
   const RowStridesB sk{k_strides[0], k_strides[1], k_strides[2]};
   const RowStridesB sv{v_strides[0], v_strides[1], v_strides[2]};

@@ -510,7 +510,8 @@ bool is_half16(const at::Tensor& t) {
 bool attn_layout_half_ok(const at::Tensor& t) {
   const auto s = strides_of<4>(t);
   return (t.size(3) == 1 || t.stride(3) == 1) && s[0] % 8 == 0 && s[1] % 8 == 0 &&
-         s[2] % 8 == 0 && (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) == 0;
+         s[2] % 8 == 0 && s[2] >= 0 && s[2] < ((int64_t)1 << 24) &&
+         (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) == 0;
 }
 
 at::Tensor attn_operand_half(const at::Tensor& t) {

@@ -73,8 +73,8 @@ int cta_flash_attention_fwd_strided(const float* q, const int64_t* q_strides,
 
 /* Forward with BF16 Q, K, V (stored as uint16_t bit patterns) and FP32 accumulation: O dense
  * (B,nh,T,hs) in BF16, L dense (B,nh,T) in FP32, L = rowmax + ln(rowsum) as above.  hs in
- * {32, 64, 128}.  Q/K/V strides: unit d-stride, other strides divisible by 8, 16-byte aligned
- * base pointers (CTA_ERR_LAYOUT otherwise).  The probabilities are rounded to BF16 as the
+ * {32, 64, 128}.  Q/K/V strides: unit d-stride, other strides divisible by 8, a t-stride in
+ * [0, 2^24), 16-byte aligned base pointers (CTA_ERR_LAYOUT otherwise).  The probabilities are rounded to BF16 as the
  * P.V operand.  No counterpart in the reference's launchers: its roadmap lists reduced
  * precision (README.md:277); the semantics are those of flash_attention_fwd
  * (flash_attn_launcher.cu:22-65). */

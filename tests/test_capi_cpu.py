@@ -105,15 +105,17 @@ def test_other_entry_points_validate_arguments():
         capi.call("cta_flash_attention_bwd_delta", 16, st, 16, st, 1, 1, 8, 96, 16, None)
 
 
-def test_half_forward_rejects_row_strides_of_2_to_31():
-    # The 16-bit forward addresses rows with a 32-bit stride multiply; larger time strides
-    # are refused before any launch.
+def test_half_forward_rejects_time_strides_of_2_to_24():
+    # The 16-bit kernels address a stage's 64 rows with 32-bit byte offsets; larger time
+    # strides are refused before any launch.
     lib = capi.lib()
     ok = capi.strides((512, 512, 64, 1))
     big = capi.strides((1 << 32, 1 << 32, 1 << 31, 1))
     args = (1, 1, 8, 64, 1, 16, 16, None)
     assert lib.cta_flash_attention_fwd_bf16(16, big, 16, ok, 16, ok, *args) == LAYOUT
-    assert b"2^31" in lib.cta_last_error()
+    assert b"2^24" in lib.cta_last_error()
+    edge = capi.strides((1 << 24, 1 << 24, 1 << 24, 1))  # a stage's 64 rows need 32-bit offsets
+    assert lib.cta_flash_attention_fwd_bf16(16, ok, 16, edge, 16, ok, *args) == LAYOUT
     assert lib.cta_flash_attention_fwd_f16(16, ok, 16, ok, 16, big, *args) == LAYOUT
 
 
