@@ -28,6 +28,7 @@ REF_SHAPES = [
     (1, 3, 1, 64, True),     # single row
     (2, 2, 129, 32, True),
     (1, 2, 200, 128, False),
+    (1, 2, 700, 64, True),   # four-wave forward, two-wave backward (short causal heads)
 ]
 
 
