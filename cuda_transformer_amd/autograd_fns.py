@@ -22,8 +22,8 @@ Deviations, each a fix:
 import torch
 
 from .ops import (
-    causal_self_attention_bwd, causal_self_attention_fwd, cuda_fma, cuda_fma_gelu,
-    cuda_fma_gelu_grad, cuda_fma_gelu_tanh, cuda_fma_gelu_tanh_grad, cuda_softmax, cuda_softmax_bwd, db_calculation, flash_attention_bwd, flash_attention_fwd, flash_attention_qkv_bwd, flash_attention_qkv_fwd, gelu_activation,
+    causal_self_attention_bwd, causal_self_attention_fwd, cuda_fma, cuda_fma_gelu_deriv,
+    cuda_fma_gelu_tanh_deriv, cuda_fma_mul, cuda_softmax, cuda_softmax_bwd, db_calculation, flash_attention_bwd, flash_attention_fwd, flash_attention_qkv_bwd, flash_attention_qkv_fwd, gelu_activation,
     gelu_activation_bwd, gelu_tanh_activation, gelu_tanh_activation_bwd, layernorm_bwd, layernorm_fwd,
     linear_weight_bias_grad, add_layernorm_bwd, add_layernorm_fwd,
 )
@@ -151,9 +151,11 @@ class CudaMLP(torch.autograd.Function):
 
     Same values, bit for bit, as CudaLinearLayer, CudaGeluLayer and CudaLinearLayer applied in
     turn (2-D weights), in fewer passes over the (batch, m, 4 d_model) hidden tensor: the
-    forward's fc1 GEMM writes the pre-activation and its GELU together (``cuda_fma_gelu``), and
-    the backward's fc2 dx GEMM applies the GELU derivative before its store
-    (``cuda_fma_gelu_grad``), so neither GELU pass re-reads the hidden tensor.
+    forward's fc1 GEMM writes GELU(pre) and GELU'(pre) together (``cuda_fma_gelu_deriv``:
+    its epilogue already holds the normal CDF that both need), and the backward's fc2 dx GEMM
+    multiplies its product by the saved derivative before the store (``cuda_fma_mul``), so
+    neither GELU pass re-reads the hidden tensor and the backward product carries no GELU
+    arithmetic.  The saved derivative takes the place of the pre-activation (same memory).
 
     An optional sixth argument ``tanh=True`` selects the tanh-approximated GELU (the GPT-2
     form; ``CudaGeluTanhLayer`` in the composition above).
@@ -162,19 +164,17 @@ class CudaMLP(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w1, b1, w2, b2, tanh=False):
         torch._check(w1.dim() == 2 and w2.dim() == 2, lambda: "CudaMLP takes 2-D weights")
-        pre, h = (cuda_fma_gelu_tanh if tanh else cuda_fma_gelu)(x, w1, b1)
+        deriv, h = (cuda_fma_gelu_tanh_deriv if tanh else cuda_fma_gelu_deriv)(x, w1, b1)
         out = cuda_fma(h, w2, b2)
-        ctx.save_for_backward(x, w1, w2, pre, h)
-        ctx.tanh = bool(tanh)
+        ctx.save_for_backward(x, w1, w2, deriv, h)
         return out
 
     @staticmethod
     def backward(ctx, grad_output):
-        x, w1, w2, pre, h = ctx.saved_tensors
+        x, w1, w2, deriv, h = ctx.saved_tensors
         dz = grad_output
         dw2, db2 = _weight_and_bias_grads(h, w2, dz)
-        dpre = (cuda_fma_gelu_tanh_grad if ctx.tanh else cuda_fma_gelu_grad)(
-            dz, w2.unsqueeze(0).transpose(1, 2), pre)
+        dpre = cuda_fma_mul(dz, w2.unsqueeze(0).transpose(1, 2), deriv)
         dw1, db1 = _weight_and_bias_grads(x, w1, dpre)
         dx = cuda_fma(dpre, w1.unsqueeze(0).transpose(1, 2), _zeros(x.shape[-1], dz))
         return dx, dw1, db1, dw2, db2, None

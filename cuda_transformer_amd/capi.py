@@ -77,6 +77,12 @@ SIGNATURES = {
                                       _i64, _p, _p, _p, _p]),
     "cta_cuda_fma_gelu_tanh_grad": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64,
                                            _i64, _p, _p, _p]),
+    "cta_cuda_fma_gelu_deriv": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64, _i64,
+                                       _i64, _p, _p, _p, _p]),
+    "cta_cuda_fma_gelu_tanh_deriv": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64,
+                                            _i64, _i64, _p, _p, _p, _p]),
+    "cta_cuda_fma_mul": (_int, [_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p,
+                                _p]),
     "cta_db_calculation_workspace": (_i64, [_i64, _i64, _i64]),
     "cta_db_calculation": (_int, [_p, _i64p, _i64, _i64, _i64, _p, _p, _p]),
     "cta_linear_weight_bias_grad_workspace": (_i64, [_i64, _i64, _i64]),

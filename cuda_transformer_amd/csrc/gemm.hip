@@ -135,6 +135,33 @@ extern "C" int cta_cuda_fma_gelu_tanh_grad(const float* dy, const int64_t* dy_st
                       stream, kActGeluTanhGrad);
 }
 
+extern "C" int cta_cuda_fma_gelu_deriv(const float* x, const int64_t* x_strides, const float* w,
+                                       const int64_t* w_strides, const float* bias,
+                                       int64_t bias_stride, int64_t batch, int64_t m, int64_t k,
+                                       int64_t n, int64_t w_batch, float* deriv, float* out,
+                                       float* workspace, void* stream) {
+  return fma_act(x, x_strides, w, w_strides, bias, bias_stride, batch, m, k, n, w_batch, deriv,
+                 out, workspace, stream, kActGeluDeriv);
+}
+
+extern "C" int cta_cuda_fma_gelu_tanh_deriv(const float* x, const int64_t* x_strides,
+                                            const float* w, const int64_t* w_strides,
+                                            const float* bias, int64_t bias_stride,
+                                            int64_t batch, int64_t m, int64_t k, int64_t n,
+                                            int64_t w_batch, float* deriv, float* out,
+                                            float* workspace, void* stream) {
+  return fma_act(x, x_strides, w, w_strides, bias, bias_stride, batch, m, k, n, w_batch, deriv,
+                 out, workspace, stream, kActGeluTanhDeriv);
+}
+
+extern "C" int cta_cuda_fma_mul(const float* dy, const int64_t* dy_strides, const float* w,
+                                const int64_t* w_strides, const float* d, int64_t batch,
+                                int64_t m, int64_t k, int64_t n, int64_t w_batch, float* dx,
+                                float* workspace, void* stream) {
+  return fma_act_grad(dy, dy_strides, w, w_strides, d, batch, m, k, n, w_batch, dx, workspace,
+                      stream, kActMulAux);
+}
+
 extern "C" int64_t cta_db_calculation_workspace(int64_t batch, int64_t m, int64_t n) {
   if (batch <= 0 || m <= 0 || n <= 0) return 0;
   return colsum_workspace_floats(batch * m, n) * (int64_t)sizeof(float);

@@ -24,6 +24,9 @@ enum GemmAct {
   kActGeluGrad = 2,  // C = v * gelu'(aux): aux holds the pre-activation
   kActGeluTanh = 3,      // as kActGelu with the tanh-approximated GELU
   kActGeluTanhGrad = 4,  // as kActGeluGrad with the tanh-approximated GELU
+  kActGeluDeriv = 5,      // C = gelu'(v) and aux = gelu(v)
+  kActGeluTanhDeriv = 6,  // as kActGeluDeriv with the tanh-approximated GELU
+  kActMulAux = 7,         // C = v * aux: aux holds a saved gelu'(pre)
 };
 
 struct GemmEpilogue {
@@ -32,7 +35,7 @@ struct GemmEpilogue {
   int64_t bias_stride;
   int causal_mask;    // set entries with n > m to -inf
   int act = kActNone;
-  float* aux = nullptr;  // same (batch, m, n) layout as the output; read-only for the *Grad acts
+  float* aux = nullptr;  // same (batch, m, n) layout as the output; read-only for the *Grad acts and kActMulAux
   // Nullable: receives the column sums of B over K (sum_k B[k][n], n < N).  Needs Z == 1,
   // B contiguous along n with N % 4 == 0, no pointwise stage and no mask.
   float* colsum = nullptr;

@@ -282,7 +282,8 @@ __device__ __forceinline__ void block_store(const f32x16 (&acc)[TL::MB][TL::NB],
                                             int M, int N, int mw, int nw, int half, int col) {
   constexpr int MB = TL::MB, NB = TL::NB;
   constexpr int WROWS = TL::BM / TL::WM, WCOLS = TL::BN / TL::WN;
-  constexpr bool kGrad = !RAW && (ACT == kActGeluGrad || ACT == kActGeluTanhGrad);
+  constexpr bool kGrad =
+      !RAW && (ACT == kActGeluGrad || ACT == kActGeluTanhGrad || ACT == kActMulAux);
   float* Cb = Cz + (int64_t)mw * srow + nw;
   float* Xb = Xz ? Xz + (int64_t)mw * srow + nw : Cb;
   const int nbytes = (int)(((int64_t)(min(WROWS, M - mw) - 1) * srow + min(WCOLS, N - nw)) * 4);
@@ -297,9 +298,9 @@ __device__ __forceinline__ void block_store(const f32x16 (&acc)[TL::MB][TL::NB],
     bv[j] = (!RAW && ep.bias && n < N) ? ep.bias[(int64_t)n * ep.bias_stride] : 0.0f;
     vo[j] = n < N ? 4 * half * row_bytes + (j * 32 + col) * 4 : (int)0x80000000;
   }
-  // The gradient stages read the pre-activations: all of the block's loads are issued before
-  // its first store, so their latencies overlap.  Each element's pre-activation is read before
-  // any store, so dx may alias pre.
+  // The gradient stages read the pre-activations (kActMulAux: the saved derivatives): all of
+  // the block's loads are issued before its first store, so their latencies overlap.  Each
+  // element's aux value is read before any store, so dx may alias it.
   float xg[kGrad ? MB : 1][kGrad ? NB : 1][16];
   if constexpr (kGrad) {
 #pragma unroll
@@ -324,13 +325,19 @@ __device__ __forceinline__ void block_store(const f32x16 (&acc)[TL::MB][TL::NB],
           val = fmaf(ep.alpha, val, bv[j]);
           if (MASK && n > mw + i * 32 + mfma_row(r, half)) val = -INFINITY;
           if constexpr (kGrad)
-            val = ACT == kActGeluGrad ? gelu_grad(xg[i][j][r], val)
-                                      : gelu_tanh_grad(xg[i][j][r], val);
+            val = ACT == kActGeluGrad       ? gelu_grad(xg[i][j][r], val)
+                  : ACT == kActGeluTanhGrad ? gelu_tanh_grad(xg[i][j][r], val)
+                                            : val * xg[i][j][r];
         }
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), rc, vo[j], so, 0);
-        if (!RAW && ACT == kActGelu)
+        // The derivative forms store gelu'(v) (its product with g = 1.0 is exact, so a later
+        // kActMulAux stage gives gelu_grad(v, g) bit for bit) and gelu(v).
+        float cv = val;
+        if (!RAW && ACT == kActGeluDeriv) cv = gelu_grad(val, 1.0f);
+        if (!RAW && ACT == kActGeluTanhDeriv) cv = gelu_tanh_grad(val, 1.0f);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(cv), rc, vo[j], so, 0);
+        if (!RAW && (ACT == kActGelu || ACT == kActGeluDeriv))
           __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gelu_f(val)), rx, vo[j], so, 0);
-        if (!RAW && ACT == kActGeluTanh)
+        if (!RAW && (ACT == kActGeluTanh || ACT == kActGeluTanhDeriv))
           __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gelu_tanh_f(val)), rx, vo[j], so, 0);
       }
     }
@@ -552,9 +559,12 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float* __restric
     const int64_t off = zo * C.s_outer + zi * C.s_inner + (int64_t)m * C.s_row + n;
     if (ep.act == kActGeluGrad) val = gelu_grad(ep.aux[off], val);
     if (ep.act == kActGeluTanhGrad) val = gelu_tanh_grad(ep.aux[off], val);
-    C.p[off] = val;
-    if (ep.act == kActGelu) ep.aux[off] = gelu_f(val);
-    if (ep.act == kActGeluTanh) ep.aux[off] = gelu_tanh_f(val);
+    if (ep.act == kActMulAux) val = val * ep.aux[off];
+    C.p[off] = ep.act == kActGeluDeriv       ? gelu_grad(val, 1.0f)
+               : ep.act == kActGeluTanhDeriv ? gelu_tanh_grad(val, 1.0f)
+                                             : val;
+    if (ep.act == kActGelu || ep.act == kActGeluDeriv) ep.aux[off] = gelu_f(val);
+    if (ep.act == kActGeluTanh || ep.act == kActGeluTanhDeriv) ep.aux[off] = gelu_tanh_f(val);
   }
 }
 
@@ -688,6 +698,13 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
     else if (act == kActGeluTanhGrad)
       dispatch_a<TL, kActGeluTanhGrad>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc,
                                        ws);
+    else if (act == kActGeluDeriv)
+      dispatch_a<TL, kActGeluDeriv>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
+    else if (act == kActGeluTanhDeriv)
+      dispatch_a<TL, kActGeluTanhDeriv>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc,
+                                        ws);
+    else if (act == kActMulAux)
+      dispatch_a<TL, kActMulAux>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
     else
       dispatch_a<TL, kActNone>(am, bm, grid, st, A, B, C, ep, iM, iN, iK, izin, iZ, ikc, ws);
   }

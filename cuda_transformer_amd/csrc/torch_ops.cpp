@@ -130,8 +130,10 @@ at::Tensor check_linear(const at::Tensor& x, at::Tensor weights) {
 
 // (pre, out) = (x W + b, GELU(x W + b)) from one GEMM whose epilogue writes both.  New op: the
 // GPT MLP's fc1 -> GELU (gpt/gpt.py:134-135) without the second pass over pre.
+// deriv_form: the first output is GELU'(x W + b) (cta_cuda_fma_gelu_deriv) instead of pre.
 std::tuple<at::Tensor, at::Tensor> fma_gelu_impl(at::Tensor x, at::Tensor weights,
-                                                 at::Tensor bias, bool tanh_form) {
+                                                 at::Tensor bias, bool tanh_form,
+                                                 bool deriv_form = false) {
   weights = check_linear(x, weights);
   TORCH_CHECK(bias.dim() == 1, "bias must be a 1D tensor");
   TORCH_CHECK(bias.size(0) == weights.size(2), "bias.size(0) must match weights.size(2)");
@@ -146,7 +148,9 @@ std::tuple<at::Tensor, at::Tensor> fma_gelu_impl(at::Tensor x, at::Tensor weight
   const int64_t ws_bytes = cta_cuda_fma_workspace(batch, m, k, n);
   at::Tensor scratch;
   if (ws_bytes > 0) scratch = at::empty({ws_bytes / 4}, x.options());
-  check_rc((tanh_form ? cta_cuda_fma_gelu_tanh : cta_cuda_fma_gelu)(x.data_ptr<float>(), xs.data(), weights.data_ptr<float>(),
+  const auto fn = deriv_form ? (tanh_form ? cta_cuda_fma_gelu_tanh_deriv : cta_cuda_fma_gelu_deriv)
+                             : (tanh_form ? cta_cuda_fma_gelu_tanh : cta_cuda_fma_gelu);
+  check_rc(fn(x.data_ptr<float>(), xs.data(), weights.data_ptr<float>(),
                              wst.data(), bias.data_ptr<float>(), bias.stride(0), batch, m, k, n,
                              weights.size(0), pre.data_ptr<float>(), out.data_ptr<float>(),
                              ws_bytes > 0 ? scratch.data_ptr<float>() : nullptr, stream_of(x)));
@@ -155,8 +159,9 @@ std::tuple<at::Tensor, at::Tensor> fma_gelu_impl(at::Tensor x, at::Tensor weight
 
 // dx = (dy W) * GELU'(pre).  New op: CudaLinearLayer.backward's dx product of fc2 followed by
 // CudaGeluLayer.backward (cuda_linear_layer.py:19-23, cuda_gelu_layer.py:12-14) in one pass.
+// mul_form: pre holds a saved GELU'(pre) and dx = (dy W) * pre (cta_cuda_fma_mul).
 at::Tensor fma_gelu_grad_impl(at::Tensor dy, at::Tensor weights, at::Tensor pre,
-                              bool tanh_form) {
+                              bool tanh_form, bool mul_form = false) {
   weights = check_linear(dy, weights);
   const int64_t batch = dy.size(0), m = dy.size(1), k = dy.size(2), n = weights.size(2);
   TORCH_CHECK(pre.dim() == 3 && pre.size(0) == batch && pre.size(1) == m && pre.size(2) == n,
@@ -171,7 +176,9 @@ at::Tensor fma_gelu_grad_impl(at::Tensor dy, at::Tensor weights, at::Tensor pre,
   const int64_t ws_bytes = cta_cuda_fma_workspace(batch, m, k, n);
   at::Tensor scratch;
   if (ws_bytes > 0) scratch = at::empty({ws_bytes / 4}, dy.options());
-  check_rc((tanh_form ? cta_cuda_fma_gelu_tanh_grad : cta_cuda_fma_gelu_grad)(dy.data_ptr<float>(), ds.data(), weights.data_ptr<float>(),
+  const auto fn = mul_form ? cta_cuda_fma_mul
+                           : (tanh_form ? cta_cuda_fma_gelu_tanh_grad : cta_cuda_fma_gelu_grad);
+  check_rc(fn(dy.data_ptr<float>(), ds.data(), weights.data_ptr<float>(),
                                   wst.data(), pd.data_ptr<float>(), batch, m, k, n,
                                   weights.size(0), dx.data_ptr<float>(),
                                   ws_bytes > 0 ? scratch.data_ptr<float>() : nullptr,
@@ -193,6 +200,19 @@ std::tuple<at::Tensor, at::Tensor> cuda_fma_gelu_tanh(at::Tensor x, at::Tensor w
 }
 at::Tensor cuda_fma_gelu_tanh_grad(at::Tensor dy, at::Tensor weights, at::Tensor pre) {
   return fma_gelu_grad_impl(dy, weights, pre, true);
+}
+// (GELU'(x W + b), GELU(x W + b)) and its backward (dy W) * d: the derivative is evaluated in
+// the forward epilogue, which already has the normal CDF (new ops, no reference counterpart).
+std::tuple<at::Tensor, at::Tensor> cuda_fma_gelu_deriv(at::Tensor x, at::Tensor weights,
+                                                       at::Tensor bias) {
+  return fma_gelu_impl(x, weights, bias, false, true);
+}
+std::tuple<at::Tensor, at::Tensor> cuda_fma_gelu_tanh_deriv(at::Tensor x, at::Tensor weights,
+                                                            at::Tensor bias) {
+  return fma_gelu_impl(x, weights, bias, true, true);
+}
+at::Tensor cuda_fma_mul(at::Tensor dy, at::Tensor weights, at::Tensor d) {
+  return fma_gelu_grad_impl(dy, weights, d, false, true);
 }
 
 // cf. linear_layer.cu:74-97
@@ -779,6 +799,9 @@ TORCH_LIBRARY(cuda_transformer, m) {
   m.def("cuda_fma_gelu_grad(Tensor dy, Tensor weights, Tensor pre) -> Tensor");
   m.def("cuda_fma_gelu_tanh(Tensor x, Tensor weights, Tensor bias) -> (Tensor, Tensor)");
   m.def("cuda_fma_gelu_tanh_grad(Tensor dy, Tensor weights, Tensor pre) -> Tensor");
+  m.def("cuda_fma_gelu_deriv(Tensor x, Tensor weights, Tensor bias) -> (Tensor, Tensor)");
+  m.def("cuda_fma_gelu_tanh_deriv(Tensor x, Tensor weights, Tensor bias) -> (Tensor, Tensor)");
+  m.def("cuda_fma_mul(Tensor dy, Tensor weights, Tensor d) -> Tensor");
   m.def("gelu_activation(Tensor x) -> Tensor");
   m.def("gelu_activation_bwd(Tensor x, Tensor dy) -> Tensor");
   m.def("gelu_tanh_activation(Tensor x) -> Tensor");
@@ -815,6 +838,9 @@ TORCH_LIBRARY_IMPL(cuda_transformer, CUDA, m) {
   m.impl("cuda_fma_gelu_grad", &cuda_fma_gelu_grad);
   m.impl("cuda_fma_gelu_tanh", &cuda_fma_gelu_tanh);
   m.impl("cuda_fma_gelu_tanh_grad", &cuda_fma_gelu_tanh_grad);
+  m.impl("cuda_fma_gelu_deriv", &cuda_fma_gelu_deriv);
+  m.impl("cuda_fma_gelu_tanh_deriv", &cuda_fma_gelu_tanh_deriv);
+  m.impl("cuda_fma_mul", &cuda_fma_mul);
   m.impl("gelu_activation", &gelu_activation);
   m.impl("gelu_activation_bwd", &gelu_activation_bwd);
   m.impl("gelu_tanh_activation", &gelu_tanh_activation);

@@ -20,7 +20,7 @@ from torch import Tensor
 
 __all__ = [
     "cuda_fma", "db_calculation", "linear_weight_bias_grad", "cuda_fma_gelu", "cuda_fma_gelu_grad", "cuda_fma_gelu_tanh",
-    "cuda_fma_gelu_tanh_grad",
+    "cuda_fma_gelu_tanh_grad", "cuda_fma_gelu_deriv", "cuda_fma_gelu_tanh_deriv", "cuda_fma_mul",
     "cuda_softmax", "cuda_softmax_bwd",
     "gelu_activation", "gelu_activation_bwd", "gelu_tanh_activation", "gelu_tanh_activation_bwd",
     "causal_self_attention_fwd", "causal_self_attention_bwd",
@@ -113,6 +113,42 @@ def _(dy, weights, pre):
     _f32(dy, weights, pre)
     _same_device(dy, weights, pre)
     return torch.empty(pre.shape, dtype=dy.dtype, device=dy.device)
+
+
+def cuda_fma_gelu_deriv(x: Tensor, weights: Tensor, bias: Tensor) -> tuple[Tensor, Tensor]:
+    """(deriv, out) with deriv = gelu'(x @ weights + bias) and out = gelu(x @ weights + bias),
+    from one GEMM; ``cuda_fma_mul(dy, w, deriv)`` is then bitwise equal to
+    ``cuda_fma_gelu_grad(dy, w, pre)``."""
+    return _ops.cuda_fma_gelu_deriv.default(x, weights, bias)
+
+
+def cuda_fma_gelu_tanh_deriv(x: Tensor, weights: Tensor, bias: Tensor) -> tuple[Tensor, Tensor]:
+    """As ``cuda_fma_gelu_deriv`` with the tanh-approximated GELU (pairs with
+    ``cuda_fma_gelu_tanh_grad``)."""
+    return _ops.cuda_fma_gelu_tanh_deriv.default(x, weights, bias)
+
+
+def cuda_fma_mul(dy: Tensor, weights: Tensor, d: Tensor) -> Tensor:
+    """(dy @ weights) * d, from one GEMM (d of the output's shape)."""
+    return _ops.cuda_fma_mul.default(dy, weights, d)
+
+
+for _name in ("cuda_fma_gelu_deriv", "cuda_fma_gelu_tanh_deriv"):
+    @torch.library.register_fake(f"cuda_transformer::{_name}")
+    def _(x, weights, bias):
+        _f32(x, weights, bias)
+        _same_device(x, weights, bias)
+        w = weights if weights.dim() == 3 else weights.unsqueeze(0)
+        shape = (x.size(0), x.size(1), w.size(2))
+        return (torch.empty(shape, dtype=x.dtype, device=x.device),
+                torch.empty(shape, dtype=x.dtype, device=x.device))
+
+
+@torch.library.register_fake("cuda_transformer::cuda_fma_mul")
+def _(dy, weights, d):
+    _f32(dy, weights, d)
+    _same_device(dy, weights, d)
+    return torch.empty(d.shape, dtype=dy.dtype, device=dy.device)
 
 
 def db_calculation(dy: Tensor) -> Tensor:

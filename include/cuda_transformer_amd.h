@@ -320,6 +320,33 @@ int cta_cuda_fma_gelu_tanh_grad(const float* dy, const int64_t* dy_strides,
                                 int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
                                 float* dx, float* workspace, void* stream);
 
+/* deriv = GELU'(x . W + bias) and out = GELU(x . W + bias) from one GEMM, arguments and
+ * workspace as cta_cuda_fma_gelu (deriv in place of pre).  Saving the derivative instead of the
+ * pre-activation moves the GELU' evaluation out of the backward product: cta_cuda_fma_mul with
+ * this deriv is bitwise equal to cta_cuda_fma_gelu_grad with pre.  No single reference
+ * counterpart (the same composition as cta_cuda_fma_gelu). */
+int cta_cuda_fma_gelu_deriv(const float* x, const int64_t* x_strides,
+                            const float* w, const int64_t* w_strides,
+                            const float* bias, int64_t bias_stride,
+                            int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
+                            float* deriv, float* out, float* workspace, void* stream);
+
+/* As cta_cuda_fma_gelu_deriv with the tanh-approximated GELU (pairs with
+ * cta_cuda_fma_gelu_tanh_grad).  No reference counterpart. */
+int cta_cuda_fma_gelu_tanh_deriv(const float* x, const int64_t* x_strides,
+                                 const float* w, const int64_t* w_strides,
+                                 const float* bias, int64_t bias_stride,
+                                 int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
+                                 float* deriv, float* out, float* workspace, void* stream);
+
+/* dx = (dy . W) * d elementwise, d dense (batch, m, n), may alias dx; other arguments as
+ * cta_cuda_fma_gelu_grad.  With d from cta_cuda_fma_gelu_deriv it is that op's GELU backward.
+ * No single reference counterpart (the composition of cta_cuda_fma_gelu_grad). */
+int cta_cuda_fma_mul(const float* dy, const int64_t* dy_strides,
+                     const float* w, const int64_t* w_strides, const float* d,
+                     int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
+                     float* dx, float* workspace, void* stream);
+
 /* Bytes of scratch cta_db_calculation needs for a (batch, m, n) gradient. */
 int64_t cta_db_calculation_workspace(int64_t batch, int64_t m, int64_t n);
 

@@ -489,6 +489,12 @@ def _gelu_forms(form):
             ops.gelu_tanh_activation_bwd, ew.gelu_tanh_forward, ew.gelu_tanh_backward)
 
 
+def _gelu_deriv_form(form):
+    from cuda_transformer import ops
+
+    return ops.cuda_fma_gelu_deriv if form == "erf" else ops.cuda_fma_gelu_tanh_deriv
+
+
 @pytest.mark.parametrize("form", ["erf", "tanh"])
 @pytest.mark.parametrize("B,T,d,hid", FUSED_SHAPES)
 def test_fused_linear_gelu(cuda, B, T, d, hid, form):
@@ -519,6 +525,16 @@ def test_fused_linear_gelu(cuda, B, T, d, hid, form):
     for got, ref in ((pre, pre_r), (h, h_r), (dpre, dpre_r)):
         assert rel_err(f64(got), ref) <= 1e-6
         np.testing.assert_allclose(f64(got), ref, atol=1e-4, rtol=1e-4)
+    # The saved-derivative pair: GELU'(pre) from the forward epilogue, then a plain multiply in
+    # the backward one; the same bits as the pair above.
+    from cuda_transformer.ops import cuda_fma_mul
+
+    deriv, h2 = _gelu_deriv_form(form)(xc, w1c, b1c)
+    assert torch.equal(h2, h)
+    assert torch.equal(deriv, gelu_activation_bwd(pre, torch.ones_like(pre)))
+    assert torch.equal(cuda_fma_mul(dzc, w2t, deriv), dpre)
+    np.testing.assert_allclose(f64(deriv), o_bwd(pre_r, np.ones_like(pre_r)), atol=1e-4,
+                               rtol=1e-4)
 
 
 def test_fused_linear_gelu_through_c_abi(cuda):
@@ -577,6 +593,42 @@ def test_fused_linear_gelu_tanh_through_c_abi(cuda):
     pre_t, out_t = cuda_fma_gelu_tanh(x, w1, b1)
     assert torch.equal(pre, pre_t) and torch.equal(out, out_t)
     assert torch.equal(dx, cuda_fma_gelu_tanh_grad(dz, w2t, pre_t))
+
+
+@pytest.mark.parametrize("form", ["erf", "tanh"])
+def test_fused_linear_gelu_deriv_through_c_abi(cuda, form):
+    """cta_cuda_fma_gelu[_tanh]_deriv and cta_cuda_fma_mul with dx aliasing the derivative: the
+    same bits as the pre-activation pair, and the error on deriv == out."""
+    from cuda_transformer import ops
+    from cuda_transformer_amd import capi
+
+    fwd, grad = ((ops.cuda_fma_gelu, ops.cuda_fma_gelu_grad) if form == "erf"
+                 else (ops.cuda_fma_gelu_tanh, ops.cuda_fma_gelu_tanh_grad))
+    entry = "cta_cuda_fma_gelu_deriv" if form == "erf" else "cta_cuda_fma_gelu_tanh_deriv"
+    B, T, d, hid = 2, 40, 48, 80
+    x = seeded((B, T, d), 85).to(cuda)
+    w1 = seeded((d, hid), 86).to(cuda) * 0.2
+    b1 = seeded((hid,), 87).to(cuda)
+    w2t = (seeded((hid, d), 88).to(cuda) * 0.2).t()
+    dz = seeded((B, T, d), 89).to(cuda)
+    stream = torch.cuda.current_stream().cuda_stream
+    deriv = torch.empty(B, T, hid, device=cuda)
+    out = torch.empty_like(deriv)
+    capi.call(entry, x.data_ptr(), capi.strides(x.stride()), w1.data_ptr(),
+              capi.strides((0,) + w1.stride()), b1.data_ptr(), 1, B, T, d, hid, 1,
+              deriv.data_ptr(), out.data_ptr(), None, stream)
+    dx = deriv.clone()
+    capi.call("cta_cuda_fma_mul", dz.data_ptr(), capi.strides(dz.stride()), w2t.data_ptr(),
+              capi.strides((0,) + w2t.stride()), dx.data_ptr(), B, T, d, hid, 1, dx.data_ptr(),
+              None, stream)
+    torch.cuda.synchronize()
+    pre_t, out_t = fwd(x, w1, b1)
+    assert torch.equal(out, out_t)
+    assert torch.equal(dx, grad(dz, w2t, pre_t))
+    with pytest.raises(capi.CtaError, match="distinct"):
+        capi.call(entry, x.data_ptr(), capi.strides(x.stride()), w1.data_ptr(),
+                  capi.strides((0,) + w1.stride()), b1.data_ptr(), 1, B, T, d, hid, 1,
+                  out.data_ptr(), out.data_ptr(), None, stream)
 
 
 @pytest.mark.parametrize("tanh", [False, True])

@@ -62,6 +62,10 @@ def test_meta_shapes():
     pre, h = ops.cuda_fma_gelu_tanh(x, torch.empty(16, 8, **m), torch.empty(8, **m))
     assert pre.shape == h.shape == (3, 10, 8)
     assert ops.cuda_fma_gelu_tanh_grad(x, torch.empty(16, 8, **m), pre).shape == pre.shape
+    for deriv_op in (ops.cuda_fma_gelu_deriv, ops.cuda_fma_gelu_tanh_deriv):
+        d, h = deriv_op(x, torch.empty(16, 8, **m), torch.empty(8, **m))
+        assert d.shape == h.shape == (3, 10, 8)
+    assert ops.cuda_fma_mul(x, torch.empty(16, 8, **m), d).shape == d.shape
     assert ops.cuda_softmax(x).shape == x.shape
     out, probs = ops.causal_self_attention_fwd(torch.empty(2, 7, 96, **m), 4, True)
     assert out.shape == (2, 7, 32) and probs.shape == (2, 4, 7, 7)
