@@ -164,10 +164,11 @@ at::Tensor fma_gelu_grad_impl(at::Tensor dy, at::Tensor weights, at::Tensor pre,
                               bool tanh_form, bool mul_form = false) {
   weights = check_linear(dy, weights);
   const int64_t batch = dy.size(0), m = dy.size(1), k = dy.size(2), n = weights.size(2);
+  const char* name = mul_form ? "d" : "pre";
   TORCH_CHECK(pre.dim() == 3 && pre.size(0) == batch && pre.size(1) == m && pre.size(2) == n,
-              "pre must have shape (dy.size(0), dy.size(1), weights.size(-1))");
-  TORCH_CHECK(pre.is_cuda(), "pre must be a CUDA tensor");
-  check_f32(pre, "pre");
+              name, " must have shape (dy.size(0), dy.size(1), weights.size(-1))");
+  TORCH_CHECK(pre.is_cuda(), name, " must be a CUDA tensor");
+  check_f32(pre, name);
   c10::OptionalDeviceGuard guard(dy.device());
   const at::Tensor pd = pre.contiguous();
   at::Tensor dx = at::empty({batch, m, n}, dy.options());

@@ -625,6 +625,8 @@ def test_fused_linear_gelu_deriv_through_c_abi(cuda, form):
     pre_t, out_t = fwd(x, w1, b1)
     assert torch.equal(out, out_t)
     assert torch.equal(dx, grad(dz, w2t, pre_t))
+    with pytest.raises(RuntimeError, match="d must have shape"):
+        ops.cuda_fma_mul(dz, w2t, deriv[:, :5])
     with pytest.raises(capi.CtaError, match="distinct"):
         capi.call(entry, x.data_ptr(), capi.strides(x.stride()), w1.data_ptr(),
                   capi.strides((0,) + w1.stride()), b1.data_ptr(), 1, B, T, d, hid, 1,
