@@ -8,7 +8,8 @@ Same architecture and parameter layout: token + position embedding, pre-LN decod
 FlashAttention-2 on head views of the packed qkv (gpt.py:104-109), MLP 4x with exact GELU
 (gpt.py:121-137), final LayerNorm and lm_head, cross-entropy (gpt.py:166-175).  Every linear,
 attention, GELU and LayerNorm op runs on the HIP kernels through the reference's autograd
-API; the embeddings and the cross-entropy stay in torch, as in the reference.
+API; the embedding lookups and the cross-entropy stay in torch, as in the reference, while the
+token table's gradient is a GEMM on the HIP kernels (CudaEmbedding).
 """
 from __future__ import annotations
 
@@ -18,7 +19,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .autograd_fns import (CudaAddLayerNorm, CudaFlashAttention, CudaFlashAttentionQKV,
+from .autograd_fns import (CudaAddLayerNorm, CudaEmbedding, CudaFlashAttention, CudaFlashAttentionQKV,
                            CudaGeluLayer, CudaLayerNorm, CudaLinearLayer, CudaMLP)
 
 
@@ -43,6 +44,10 @@ class GPTConfig:
     # LayerNorm(x + f) in one pass; in the backward the residual gradient joins the LayerNorm
     # gradient in the same pass) instead of separate adds; same bits.
     fused_residual_ln: bool = True
+    # Token + position embedding through CudaEmbedding, whose backward issues no device-to-host
+    # read (torch's embedding backward reads the distinct-id count back and stalls the step);
+    # the token table's gradient is then summed in another order than torch's.
+    cuda_embedding: bool = True
 
 
 class LayerNorm(nn.Module):
@@ -63,8 +68,11 @@ class Embedding(nn.Module):
         super().__init__()
         self.embedding = nn.Embedding(cfg.vocab_size, cfg.d_model)
         self.positional = nn.Embedding(cfg.block_size, cfg.d_model)
+        self.cuda_embedding = cfg.cuda_embedding
 
     def forward(self, tokens):
+        if self.cuda_embedding:
+            return CudaEmbedding.apply(tokens, self.embedding.weight, self.positional.weight)
         T = tokens.shape[1]
         return self.embedding(tokens) + self.positional(torch.arange(T, device=tokens.device))
 

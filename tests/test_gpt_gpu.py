@@ -43,12 +43,13 @@ def test_gpt_training_steps_match_cpu_reference(cuda, fused_adamw):
         torch.testing.assert_close(p.detach().cpu(), q.detach(), rtol=1e-3, atol=1e-4, msg=name)
 
 
-@pytest.mark.parametrize("flag", ["fused_mlp", "fused_residual_ln"])
+@pytest.mark.parametrize("flag", ["fused_mlp", "fused_residual_ln", "cuda_embedding"])
 def test_gpt_fusions_match_reference_composition(cuda, flag):
     """GPTConfig.fused_mlp (CudaMLP) against the reference's Linear -> GELU -> Linear modules,
-    and GPTConfig.fused_residual_ln (CudaAddLayerNorm) against separate residual adds and
-    LayerNorms: the same loss and gradients, bit for bit (the embedding gradients, accumulated
-    by torch's own embedding backward, to FP32 rounding)."""
+    GPTConfig.fused_residual_ln (CudaAddLayerNorm) against separate residual adds and
+    LayerNorms, and GPTConfig.cuda_embedding (CudaEmbedding) against nn.Embedding: the same
+    loss and gradients, bit for bit (the embedding gradients, summed in different orders, to
+    FP32 rounding)."""
     cfg = GPTConfig(n_layers=2)
     idx, tgt = synthetic_batch(cfg, 8, seed=7)
     runs = []
@@ -66,3 +67,42 @@ def test_gpt_fusions_match_reference_composition(cuda, flag):
             torch.testing.assert_close(g, g_u[name], rtol=1e-6, atol=1e-7, msg=name)
         else:
             assert torch.equal(g, g_u[name]), name
+
+
+@pytest.mark.parametrize("limit", [None, 0])  # the one-hot GEMM, then torch's backward
+def test_cuda_embedding(cuda, limit, monkeypatch):
+    """CudaEmbedding: the forward equals nn.Embedding's lookups; the table gradients match a
+    float64 sum (and, through the fallback, torch's embedding backward bit for bit); re-runs are
+    bitwise equal; position rows past T get zero gradient."""
+    import torch.nn.functional as F
+
+    from cuda_transformer_amd.autograd_fns import CudaEmbedding
+
+    if limit is not None:
+        monkeypatch.setattr(CudaEmbedding, "ONEHOT_LIMIT", limit)
+    V, P, C, B, T = 65, 40, 48, 5, 33
+    g = torch.Generator().manual_seed(11)
+    tokens = torch.randint(0, V, (B, T), generator=g).to(cuda)
+    tokens[0, :7] = 3                                   # a repeated id, and ids that never occur
+    wte = torch.randn(V, C, generator=g).to(cuda).requires_grad_()
+    wpe = torch.randn(P, C, generator=g).to(cuda).requires_grad_()
+    dy = torch.randn(B, T, C, generator=g).to(cuda)
+    out = CudaEmbedding.apply(tokens, wte, wpe)
+    assert torch.equal(out, F.embedding(tokens, wte) + F.embedding(torch.arange(T, device=cuda), wpe))
+    grads = []
+    for _ in range(2):
+        wte.grad = wpe.grad = None
+        CudaEmbedding.apply(tokens, wte, wpe).backward(dy)
+        grads.append((wte.grad.clone(), wpe.grad.clone()))
+    assert all(torch.equal(a, b) for a, b in zip(grads[0], grads[1]))
+    dwte, dwpe = grads[0]
+    ids, dy64 = tokens.reshape(-1).cpu(), dy.reshape(-1, C).double().cpu()
+    ref_te = torch.zeros(V, C, dtype=torch.float64).index_add_(0, ids, dy64)
+    torch.testing.assert_close(dwte.double().cpu(), ref_te, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(dwpe[:T].double().cpu(), dy.double().sum(0).cpu(), rtol=1e-6,
+                               atol=1e-6)
+    assert torch.count_nonzero(dwpe[T:]) == 0
+    if limit == 0:
+        torch_te = torch.ops.aten.embedding_dense_backward(dy.reshape(-1, C), tokens.reshape(-1),
+                                                           V, -1, False)
+        assert torch.equal(dwte, torch_te)
