@@ -300,7 +300,7 @@ class CudaEmbedding(torch.autograd.Function):
         V, P = ctx.rows
         T, C = tokens.shape[-1], grad_output.shape[-1]
         dy = grad_output.reshape(-1, C).contiguous()
-        ids = tokens.reshape(-1)
+        ids = tokens.reshape(-1).to(torch.int64)  # int32 ids too, as nn.Embedding takes
         dwte = dwpe = None
         if ctx.needs_input_grad[1]:
             if V * ids.numel() <= CudaEmbedding.ONEHOT_LIMIT:

@@ -106,3 +106,6 @@ def test_cuda_embedding(cuda, limit, monkeypatch):
         torch_te = torch.ops.aten.embedding_dense_backward(dy.reshape(-1, C), tokens.reshape(-1),
                                                            V, -1, False)
         assert torch.equal(dwte, torch_te)
+    wte.grad = None
+    CudaEmbedding.apply(tokens.to(torch.int32), wte, wpe).backward(dy)  # int32 ids
+    assert torch.equal(wte.grad, dwte)
