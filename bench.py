@@ -968,7 +968,10 @@ def gpt_workload(args):
         "workload": "small-GPT training step (6L 6H d384 ctx256 vocab65, batch 64), FP32",
         "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 3),
         "fwd_bwd_ms": round(ms_fb, 3), "fwd_bwd_tokens_per_s": round(tokens / (ms_fb * 1e-3), 1),
-        "steps": args.steps, "mlp": args.gpt_mlp, "adamw": args.gpt_adamw, "cpu_baseline": cpu,
+        "steps": args.steps, "mlp": args.gpt_mlp, "adamw": args.gpt_adamw,
+        "model_options": {k: getattr(cfg, k) for k in ("fused_mlp", "packed_attention",
+                                                       "fused_residual_ln", "cuda_embedding")},
+        "cpu_baseline": cpu,
     }), flush=True)
     return 0
 
