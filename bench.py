@@ -24,7 +24,12 @@ Reported:
                  backward (its test oracle), timed on this host's cores on whole heads of the
                  same workload, with the backend torch chose, the CPU model and the estimated
                  time of the full step.
-  cpu_baseline_port
+  recompute      the same step with the reference's workspace-free backward schedule (delta,
+                 dQ recomputing S and dP, dK/dV without the dS store: O(N) memory), timed in
+                 the same run: per-kernel ms, fwd/bwd TFLOPS and its own roofline.  `value`
+                 stays the operator's default (stored-dS) schedule; ds_workspace_bytes states
+                 what that default allocates.
+  cpu_baseline_port (--cpu-port only)
                  the CPU oracle (numpy port of the reference algorithm, float32) timed on a
                  bounded sample of whole heads of the same workload.
 
@@ -89,6 +94,10 @@ def parse_args():
                         "recompute: the reference's delta / dQ / dK/dV schedule; fold: the stored "
                         "schedule with delta computed inside the dK/dV stage (no delta launch)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-port", action="store_true",
+                   help="also time the numpy oracle on the CPU (cpu_baseline_port, ~10 s)")
+    p.add_argument("--no-recompute", action="store_true",
+                   help="leave out the recompute-schedule object of the headline line")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="target CPU time of the bounded CPU-baseline sample")
     p.add_argument("--no-autograd", action="store_true",
@@ -179,9 +188,9 @@ def kernel_algorithmic(name, B, H, N, D, causal):
     return float(2 * B * H * N * D * 4 + B * H * N * 4), "GB/s", "hbm"
 
 
-def load_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed PMC summary, or None."""
-    path = ROOT / "profiles" / "fa2_config2_counters.md"
+def load_traffic(kernel: str, summary: str = "fa2_config2_counters.md"):
+    """HBM bytes per launch of `kernel` from a committed PMC summary under profiles/, or None."""
+    path = ROOT / "profiles" / summary
     if not path.exists():
         return None
     m = re.search(rf"traffic_bytes_per_launch\[{re.escape(kernel)}(<[^\]]*>)?\]\s*=\s*([0-9.eE+]+)",
@@ -1017,7 +1026,37 @@ def main():
     bwd_tf = bwd_fl / (bwd_ms * 1e-3) / 1e12
 
     roofline = roofline_of(per_kernel, B, H, N, D, causal, flushed)
-    roofline["traffic"] = load_traffic(roofline["kernel"])
+    is_config2 = (B, H, N, D, causal) == (4, 32, 4096, 64, True)
+    stored_summary = ("fa2_config2_counters.md" if args.bwd_schedule == "stored"
+                      else "fa2_config2_recompute_counters.md")
+    roofline["traffic"] = load_traffic(roofline["kernel"], stored_summary) if is_config2 else None
+    from cuda_transformer_amd import capi
+
+    ws_full = capi.lib().cta_flash_attention_bwd_workspace(B, H, N, D, int(causal))
+    ds_ws = min(ws_full, BWD_WORKSPACE_CAP) if args.bwd_schedule in ("stored", "fold") else 0
+
+    recompute = None
+    if args.bwd_schedule == "stored" and not args.no_recompute:
+        # The reference's O(N)-memory schedule in the same run, after the headline's timing.
+        r_ms, r_pk, r_fl, _, r_warm = fa2_timings(B, H, N, D, causal, max(3, args.steps // 2),
+                                                  args.warmup, "recompute")
+        r_bwd = sum(v_ for k_, v_ in r_pk.items() if k_ != "fwd")
+        r_roof = roofline_of(r_pk, B, H, N, D, causal, r_fl)
+        r_roof["traffic"] = (load_traffic(r_roof["kernel"], "fa2_config2_recompute_counters.md")
+                             if is_config2 else None)
+        recompute = {
+            "bwd_schedule": "recompute", "ds_workspace_bytes": 0,
+            "steps": max(3, args.steps // 2), "warmup_steps_run": r_warm,
+            "ms_per_step": round(r_ms, 4),
+            "tflops": round((fwd_fl + bwd_fl) / (r_ms * 1e-3) / 1e12, 3),
+            "fwd_tflops": round(fwd_fl / (r_pk["fwd"] * 1e-3) / 1e12, 3),
+            "bwd_tflops": round(bwd_fl / (r_bwd * 1e-3) / 1e12, 3),
+            "bwd_frac_of_peak": round(bwd_fl / (r_bwd * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4),
+            "per_kernel_ms": {k_: round(v_, 4) for k_, v_ in r_pk.items()},
+            "per_kernel_ms_flushed": {k_: round(v_, 4) for k_, v_ in r_fl.items()},
+            "roofline": r_roof,
+        }
+        torch.cuda.empty_cache()
 
     extra = {}
     if not args.no_autograd:
@@ -1062,6 +1101,8 @@ def main():
         "per_kernel_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
         "per_kernel_ms_flushed": {k_: round(v_, 4) for k_, v_ in flushed.items()},
         "roofline": roofline,
+        "ds_workspace_bytes": ds_ws,
+        "recompute": recompute,
         "reference_rtx5070_ms": REFERENCE_RTX5070_MS,
         "device": torch.cuda.get_device_name(0),
         "host": host_info(),
@@ -1070,7 +1111,8 @@ def main():
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_reference_path(B, H, N, D, causal)
-        line["cpu_baseline_port"] = cpu_port_baseline(B, H, N, D, causal, args.cpu_seconds)
+        if args.cpu_port:
+            line["cpu_baseline_port"] = cpu_port_baseline(B, H, N, D, causal, args.cpu_seconds)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

@@ -8,9 +8,12 @@
 //   dS_ij = P_ij (dP_ij - delta_i),  dV_j = sum_i P_ij dO_i,  dK_j = s sum_i dS_ij q_i,
 //   dQ_i = s sum_j dS_ij k_j,  S = s q.k, s = 1/sqrt(hs), causal mask j > i.
 // S, dP, delta and dS are FP32; P and dS are rounded to BF16 as MFMA operands, and dS is stored
-// in BF16 for the dQ stage.  The schedule is the FP32 kernels' stored-dS one: delta, then a
-// dK/dV stage that also writes every dS tile, then dQ = s dS K from the stored tiles; both
-// stages are atomics-free and deterministic.
+// in BF16 for the dQ stage.  Two schedules, as in FP32, both atomics-free and deterministic:
+//  * stored dS (given a workspace of at least one head's tiles): delta, then a dK/dV stage that
+//    also writes every dS tile, then dQ = s dS K from the stored tiles;
+//  * recompute (no workspace; the reference's schedule): delta, dK/dV without the store, and a
+//    dQ stage that recomputes S and dP from L and delta.  dK and dV are bitwise those of the
+//    stored schedule (the same kernel body); dQ differs by the rounding of its sums.
 //
 // gfx950 layout (the 16-bit forward's trick, see fa2_fwd_half.hip):
 //  * dK/dV: a wave owns 32 key rows and keeps k, v of its key row in registers as the B
@@ -82,7 +85,7 @@ struct DkdvHalfCfg {
   static constexpr int MINW = HS == 128 ? 1 : 2;
 };
 
-template <class E, int HS, bool CAUSAL, int WAVES, int BN, int MINW>
+template <class E, int HS, bool CAUSAL, int WAVES, int BN, int MINW, bool STORE>
 __global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
     const E* __restrict__ Q, const E* __restrict__ K, const E* __restrict__ V,
     const E* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
@@ -104,7 +107,8 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
   constexpr int OFF_GR = B_ROWS, OFF_QT = 2 * B_ROWS, OFF_GT = 2 * B_ROWS + B_TRS;
   constexpr int OFF_L = 2 * B_ROWS + 2 * B_TRS, OFF_D = OFF_L + BN * 4;
   constexpr int STAGE = OFF_D + BN * 4;
-  constexpr int XPOSE = NSUB * 32 * XP * 2;  // per wave: one transpose buffer per sub-tile
+  // per wave: one dS transpose buffer per sub-tile (none without the dS store)
+  constexpr int XPOSE = STORE ? NSUB * 32 * XP * 2 : 0;
   static_assert(STAGE % 16 == 0 && OFF_QT % 16 == 0 && OFF_L % 16 == 0, "16-byte aligned images");
   __shared__ __attribute__((aligned(16))) unsigned char smem[2 * STAGE + WAVES * XPOSE];
 
@@ -125,7 +129,7 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
   const float* Db = delta + (int64_t)bh * T;
   const int nb = (T + 31) / 32;
   E* xw = reinterpret_cast<E*>(smem + 2 * STAGE + wave * XPOSE);
-  E* dsh = dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileHalf;
+  E* dsh = STORE ? dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileHalf : nullptr;
 
   const int n_pass = (CAUSAL && n_ktiles - 1 - p != p) ? 2 : 1;
   for (int pass = 0; pass < n_pass; ++pass) {
@@ -161,7 +165,7 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
 
   const int q_begin = CAUSAL ? (kt * BM / BN) : 0;  // first query stage that can see these keys
   const int n_stages = (T + BN - 1) / BN;
-  const bool wave_stores = j0 < T;
+  const bool wave_stores = STORE && j0 < T;
 
   // Register-staged loads of one query stage: Q and dO rows, L log2(e) and -delta.
   // A load task is rows 2 rp and 2 rp + 1 of one 16-byte chunk ch of Q or of dO; it goes to LDS
@@ -367,14 +371,16 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
       // barrier separates the write, the read in flush() and the next write.
       // Each converted pair is stored as its low and its high half (ds_write_b16 and
       // ds_write_b16_d16_hi), without unpacking it.
-      uint16_t* xw16 = reinterpret_cast<uint16_t*>(xw + sub * 32 * XP);
+      if constexpr (STORE) {
+        uint16_t* xw16 = reinterpret_cast<uint16_t*>(xw + sub * 32 * XP);
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        uint32_t pk = reinterpret_cast<const uint32_t*>(&db[r >> 3])[(r & 7) >> 1];
-        // Opaque to the optimiser, which would otherwise convert each half again on its own.
-        asm("" : "+v"(pk));
-        xw16[mfma_row(r, half) * XP + col] = (uint16_t)pk;
-        xw16[mfma_row(r + 1, half) * XP + col] = (uint16_t)(pk >> 16);
+        for (int r = 0; r < 16; r += 2) {
+          uint32_t pk = reinterpret_cast<const uint32_t*>(&db[r >> 3])[(r & 7) >> 1];
+          // Opaque to the optimiser, which would otherwise convert each half again on its own.
+          asm("" : "+v"(pk));
+          xw16[mfma_row(r, half) * XP + col] = (uint16_t)pk;
+          xw16[mfma_row(r + 1, half) * XP + col] = (uint16_t)(pk >> 16);
+        }
       }
 
       // dK^T += Q^T dS
@@ -565,6 +571,222 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_ds_half_ker
   }  // pass: the stage loop ended on a barrier, so the next pass may refill LDS
 }
 
+// ------------------------------------------------------------------------------------
+// dQ without a workspace: the reference's dQ stage (flash_attention.cuh:216-354), which
+// recomputes S and dP from L and delta instead of reading stored dS tiles.  The 16-bit
+// forward's skeleton: workgroup = 128 query rows (4 waves x 32), key stages of 64 rows,
+// global -> registers -> LDS, double buffered, one barrier per stage; causal workgroups take
+// query-tile pairs and the second pass walks its stages downward.  A lane keeps its query
+// row's q and dO (the B operands of S^T = K Q^T and dP^T = V dO^T), L log2(e) and delta.  Each
+// stage goes to LDS as K rows (S), V rows (dP) and K^T with kt_pos (the A operand of
+// dQ^T += K^T dS^T, whose B operand is the lane's dS^T registers, as P^T is in the forward).
+template <class E, int HS, bool CAUSAL>
+__global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_half_kernel(
+    const E* __restrict__ Q, const E* __restrict__ K, const E* __restrict__ V,
+    const E* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
+    E* __restrict__ dQ, int nh, int T, int BH, int n_qtiles, RowStridesH sq, RowStridesH sk,
+    RowStridesH sv, RowStridesH sdo, RowStridesH sl, float scale, float scale_log2) {
+  constexpr int BN = 64;             // keys per stage
+  constexpr int NSUB = BN / 32;
+  constexpr int BM = 128;
+  constexpr int RP = HS + 8;         // 16-bit pitch of a K / V row image
+  constexpr int TP = BN + 8;         // 16-bit pitch of a K^T row (one d, every key of the stage)
+  constexpr int RTILE = BN * RP, TTILE = HS * TP;
+  constexpr int STAGE = 2 * RTILE + TTILE;  // K rows, V rows, K^T
+  constexpr int CH = HS / 8;         // 16-byte chunks per row
+  constexpr int QS = HS / 16;        // MFMA steps over d
+  constexpr int KPAIRS = 32 * CH;    // K row-pair tasks per stage
+  constexpr int KL = (KPAIRS + 255) / 256;
+  constexpr int VLOADS = BN * CH / 256;
+  static_assert(BN * CH % 256 == 0 && BN == 64, "stage must split evenly over 256 threads");
+  __shared__ __attribute__((aligned(16))) E smem[2 * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = wave_index();
+  const int half = lane >> 5, col = lane & 31;
+  const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+  const int w = xcd_work_item(blockIdx.x, BH * per_head);
+  if (w >= BH * per_head) return;
+  const int bh = w / per_head;
+  const int p = w - bh * per_head;
+  const int b = bh / nh, h = bh - b * nh;
+  const E* Kb = K + b * sk.b + h * sk.h;
+  const E* Vb = V + b * sv.b + h * sv.h;
+
+  const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
+  for (int pass = 0; pass < n_pass; ++pass) {
+  const int qt = CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p;
+  const int i0 = qt * BM + wave * 32;
+  const int my_i = i0 + col;
+
+  // This lane's query row: q and dO at d = 16 s + 8 half + 0..7 for step s, L log2(e), delta.
+  // Rows past T hold zeros: dO = 0 and delta = 0 make their dS 0, and their dQ is not stored.
+  vec8_t<E> qf[QS], gf[QS];
+  float lrow = 0.0f, drow = 0.0f;
+  if (my_i < T) {
+    const E* qp = Q + b * sq.b + h * sq.h + (int64_t)my_i * sq.t + 8 * half;
+    const E* gp = dO + b * sdo.b + h * sdo.h + (int64_t)my_i * sdo.t + 8 * half;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      qf[s] = ld8<E>(qp + 16 * s);
+      gf[s] = ld8<E>(gp + 16 * s);
+    }
+    lrow = Lg[b * sl.b + h * sl.h + (int64_t)my_i * sl.t] * kLog2e;
+    drow = delta[(int64_t)bh * T + my_i];
+  } else {
+#pragma unroll
+    for (int s = 0; s < QS; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { qf[s][j] = (E)0.0f; gf[s][j] = (E)0.0f; }
+  }
+  // The row loads are complete before the stage loop on every path into it (the compiler
+  // would otherwise wait for them inside each stage, draining the next stage's loads too).
+  vm_wait_all();
+
+  f32x16 acc[HS / 32];
+#pragma unroll
+  for (int d = 0; d < HS / 32; ++d) acc[d] = zero16();
+
+  const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
+  const int n_stages = (kv_end + BN - 1) / BN;
+
+  // K: a task is rows 2 rp and 2 rp + 1 of one 16-byte chunk, stored row-wise and transposed
+  // (the two rows' values for one d as one 32-bit word; a wave's 64 tasks are 32 row pairs x 2
+  // chunks, so each transposed store hits 64 distinct banks).  hs = 32 has 128 tasks: waves 0
+  // and 1 take them (wave-uniform).  V: task c = tid + 256 u is row c / CH, chunk c % CH.
+  // Rows of a stage are read through buffer resources over its valid rows; keys past T read
+  // as zero and are masked to P = 0.
+  u32x4 kst[2 * KL], vst[VLOADS];
+  auto pair_of = [&](int u2, int& rp, int& ch) {
+    rp = lane & 31;
+    ch = 2 * (wave + 4 * u2) + (lane >> 5);
+    return KPAIRS % 256 == 0 || ch < CH;
+  };
+  auto gload = [&](int stage) {
+    const int j0 = stage * BN;
+    const int rows = min(BN, T - j0);
+    const __amdgpu_buffer_rsrc_t rk = rows_rsrc16(Kb + (int64_t)j0 * sk.t, rows, sk.t, HS);
+    const __amdgpu_buffer_rsrc_t rv = rows_rsrc16(Vb + (int64_t)j0 * sv.t, rows, sv.t, HS);
+#pragma unroll
+    for (int u2 = 0; u2 < KL; ++u2) {
+      int rp, ch;
+      if (!pair_of(u2, rp, ch)) continue;
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        kst[2 * u2 + e] = ld16_buffer(rk, ((2 * rp + e) * (int)sk.t + 8 * ch) * 2);
+    }
+#pragma unroll
+    for (int u = 0; u < VLOADS; ++u) {
+      const int c = tid + 256 * u;
+      vst[u] = ld16_buffer(rv, ((c / CH) * (int)sv.t + 8 * (c % CH)) * 2);
+    }
+  };
+  auto lstore = [&](int buf) {
+    E* kr = smem + buf * STAGE;
+    E* vr = kr + RTILE;
+    E* kt = vr + RTILE;
+#pragma unroll
+    for (int u2 = 0; u2 < KL; ++u2) {
+      int rp, ch;
+      if (!pair_of(u2, rp, ch)) continue;
+      const u32x4 e0 = kst[2 * u2], e1 = kst[2 * u2 + 1];
+      *reinterpret_cast<u32x4*>(kr + (2 * rp) * RP + 8 * ch) = e0;
+      *reinterpret_cast<u32x4*>(kr + (2 * rp + 1) * RP + 8 * ch) = e1;
+      uint32_t* col2 = reinterpret_cast<uint32_t*>(kt + kt_pos(2 * rp));
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        col2[(8 * ch + 2 * t) * (TP / 2)] = pack_lo16(e0[t], e1[t]);
+        col2[(8 * ch + 2 * t + 1) * (TP / 2)] = pack_hi16(e0[t], e1[t]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < VLOADS; ++u) {
+      const int c = tid + 256 * u;
+      *reinterpret_cast<u32x4*>(vr + (c / CH) * RP + 8 * (c % CH)) = vst[u];
+    }
+  };
+
+  const bool down = CAUSAL && pass == 1;
+  auto stage_at = [&](int i) { return down ? n_stages - 1 - i : i; };
+  gload(stage_at(0));
+  lstore(0);
+  __syncthreads();
+
+  for (int i = 0; i < n_stages; ++i) {
+    const int s_idx = stage_at(i);
+    const int buf = i & 1;
+    if (i + 1 < n_stages) gload(stage_at(i + 1));
+    const E* kr = smem + buf * STAGE;
+    const E* vr = kr + RTILE;
+    const E* kt = vr + RTILE;
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub) {
+      const int jj0 = s_idx * BN + sub * 32;
+      if (jj0 >= T) continue;                 // ragged tail
+      if (CAUSAL && jj0 > i0 + 31) continue;  // tile entirely above this wave's diagonal
+
+      // S^T and dP^T - delta: lane holds query my_i, keys jj0 + R(r, half).
+      f32x16 sacc = zero16(), pacc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pacc[r] = -drow;
+      const E* krow = kr + (sub * 32 + col) * RP + 8 * half;
+      const E* vrow = vr + (sub * 32 + col) * RP + 8 * half;
+#pragma unroll
+      for (int s = 0; s < QS; ++s) sacc = Half16<E>::mfma(ld8<E>(krow + 16 * s), qf[s], sacc);
+#pragma unroll
+      for (int s = 0; s < QS; ++s) pacc = Half16<E>::mfma(ld8<E>(vrow + 16 * s), gf[s], pacc);
+
+      // P = e^{S - L}; masked keys (causal, past T) exactly 0.  Two explicit paths: left to
+      // the compiler, the masked form is if-converted into selects on every tile.
+      auto exp_scores = [&]<bool MASKED>() {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float x = fmaf(sacc[r], scale_log2, -lrow);
+          if (MASKED) {
+            const int j = jj0 + mfma_row(r, half);
+            if ((CAUSAL && j > my_i) || j >= T) x = -INFINITY;  // 2^x = 0
+          }
+          sacc[r] = fast_exp2(x);
+        }
+      };
+      if ((CAUSAL && jj0 + 31 > i0) || (jj0 + 32 > T))
+        exp_scores.template operator()<true>();
+      else
+        exp_scores.template operator()<false>();
+
+      // dS = P (dP - delta), rounded to 16 bits as the B operand of dQ^T += K^T dS^T.
+      vec8_t<E> db[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) db[r >> 3][r & 7] = (E)(sacc[r] * pacc[r]);
+#pragma unroll
+      for (int d = 0; d < HS / 32; ++d) {
+        const E* ktrow = kt + (d * 32 + col) * TP + sub * 32 + 8 * half;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) acc[d] = Half16<E>::mfma(ld8<E>(ktrow + 16 * s), db[s], acc[d]);
+      }
+    }
+
+    if (i + 1 < n_stages) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (my_i < T) {
+    E* op = dQ + ((int64_t)bh * T + my_i) * HS;
+#pragma unroll
+    for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        E q4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q4[e] = (E)(acc[d][4 * g + e] * scale);
+        *reinterpret_cast<uint2*>(op + d * 32 + 8 * g + 4 * half) =
+            *reinterpret_cast<const uint2*>(q4);
+      }
+    }
+  }
+  }  // pass: the stage loop ended on a barrier, so the next pass may refill LDS
+}
+
 RowStridesH rsh(const int64_t* s) { return RowStridesH{s[0], s[1], s[2]}; }
 
 bool layout_half_ok(const void* p, const int64_t* s) {
@@ -612,10 +834,10 @@ int bwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
   if (!dq || !dk || !dv || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
       !aligned16(workspace))
     return fail(CTA_ERR_LAYOUT, "dQ/dK/dV and the workspace must be 16-byte aligned pointers");
+  // Without a workspace that holds one head's dS tiles, the dQ stage recomputes S and dP (the
+  // reference's schedule): no O(T^2) memory at any T.
   const int64_t head_bytes = bwd_half_workspace(1, 1, T, hs, causal);
-  if (workspace == nullptr || workspace_bytes < head_bytes)
-    return fail(CTA_ERR_INVALID_ARGUMENT, std::string("flash_attention_bwd (") + what +
-                                              ") needs a dS workspace of at least one head");
+  const bool stored = workspace != nullptr && workspace_bytes >= head_bytes;
   const auto* qb = reinterpret_cast<const E*>(q);
   const auto* kb = reinterpret_cast<const E*>(k);
   const auto* vb = reinterpret_cast<const E*>(v);
@@ -643,18 +865,37 @@ int bwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
                        delta, (int)nh, (int)T, rows, rsh(o_strides), rsh(do_strides));
   if (int rc = check_launch("flash_attention_bwd (16-bit) delta")) return rc;
 
+  const int n_tiles = (int)((T + 127) / 128);
+  if (!stored) {
+    dispatch_half(hs, causal, [&]<int HS, bool C>() {
+      using Cfg = DkdvHalfCfg<HS, C>;
+      const int n_ktiles = (int)((T + 32 * Cfg::WAVES - 1) / (32 * Cfg::WAVES));
+      const int64_t kitems = (int64_t)(C ? (n_ktiles + 1) / 2 : n_ktiles) * BH;
+      hipLaunchKernelGGL(
+          (fa2_bwd_dkdv_half_kernel<E, HS, C, Cfg::WAVES, Cfg::BN, Cfg::MINW, false>),
+          dim3(xcd_grid(kitems)), dim3(64 * Cfg::WAVES), 0, st, qb, kb, vb, gb, l, delta, dkb,
+          dvb, nullptr, (int)nh, (int)T, 0, BH, n_ktiles, rsh(q_strides), rsh(k_strides),
+          rsh(v_strides), rsh(do_strides), sl, scale, scale * kLog2e);
+      const int64_t items = (int64_t)(C ? (n_tiles + 1) / 2 : n_tiles) * BH;
+      hipLaunchKernelGGL((fa2_bwd_dq_half_kernel<E, HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
+                         st, qb, kb, vb, gb, l, delta, dqb, (int)nh, (int)T, BH, n_tiles,
+                         rsh(q_strides), rsh(k_strides), rsh(v_strides), rsh(do_strides), sl,
+                         scale, scale * kLog2e);
+    });
+    return check_launch("flash_attention_bwd (16-bit, recompute)");
+  }
+
   // Chunks of equal head counts that fit the workspace.
   const int64_t fit = std::min<int64_t>(BH, workspace_bytes / head_bytes);
   const int64_t n_chunks = (BH + fit - 1) / fit;
   const int chunk = (int)((BH + n_chunks - 1) / n_chunks);
-  const int n_tiles = (int)((T + 127) / 128);
   for (int h0 = 0; h0 < BH; h0 += chunk) {
     const int n = std::min(chunk, BH - h0);
     dispatch_half(hs, causal, [&]<int HS, bool C>() {
       using Cfg = DkdvHalfCfg<HS, C>;
       const int n_ktiles = (int)((T + 32 * Cfg::WAVES - 1) / (32 * Cfg::WAVES));
       const int64_t kitems = (int64_t)(C ? (n_ktiles + 1) / 2 : n_ktiles) * n;
-      hipLaunchKernelGGL((fa2_bwd_dkdv_half_kernel<E, HS, C, Cfg::WAVES, Cfg::BN, Cfg::MINW>),
+      hipLaunchKernelGGL((fa2_bwd_dkdv_half_kernel<E, HS, C, Cfg::WAVES, Cfg::BN, Cfg::MINW, true>),
                          dim3(xcd_grid(kitems)), dim3(64 * Cfg::WAVES), 0, st, qb, kb, vb, gb, l,
                          delta, dkb, dvb, wsb, (int)nh, (int)T, h0, n, n_ktiles,
                          rsh(q_strides), rsh(k_strides), rsh(v_strides), rsh(do_strides), sl,

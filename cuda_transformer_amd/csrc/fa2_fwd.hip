@@ -99,6 +99,13 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   for (int d = 0; d < HS / 32; ++d) oacc[d] = zero16();
   float m_run = -INFINITY;  // exponent offset of row my_i (raw q.k units), lazily updated
   float l_run = 0.0f;       // this lane's partial row sum (its half of the columns)
+  // The exponents are fma(S, s log2(e), -m s log2(e)) with the offset rounded to FP32 once per
+  // rescale.  Its rounding error moves every exponent of the row by the same amount, which
+  // cancels between O and l, but grows with |m|: past 2^20 (an error above 2^-4) some row of
+  // the wave would risk overflowing or underflowing its probabilities.  Such waves form the
+  // exponents as (S - m) s log2(e) instead, exact at the row maximum at any magnitude, as the
+  // reference's expf(S - m) is (flash_attention.cuh:130-134).  Wave-uniform.
+  bool wide = false;
 
   const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
   const int n_stages = (kv_end + BN - 1) / BN;
@@ -189,11 +196,10 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
         for (int d = 0; d < HS / 32; ++d) oacc[d] *= alpha;
         m_run = m_new;
       }
-      const float mb = m_run * scale_log2;
       float psum = 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(fmaf(sacc[r], scale_log2, -mb));
+        const float p = fast_exp2((sacc[r] - m_run) * scale_log2);
         sacc[r] = p;
         psum += p;
       }

@@ -27,9 +27,23 @@
 namespace cuda_transformer {
 namespace {
 
-// Largest dS workspace the flash_attention_bwd op allocates (8 GiB of the MI355X's 288 GB);
-// longer sequences run the stored-dS schedule in chunks of heads.
-constexpr int64_t kBwdWorkspaceCap = int64_t{8} << 30;
+// Largest dS workspace the flash_attention_bwd ops allocate, in bytes: by default 8 GiB of the
+// MI355X's 288 GB; longer sequences run the stored-dS schedule in chunks of heads.  A cap below
+// one head's dS tiles (0 in particular) selects the workspace-free recompute schedule.  Settable
+// from Python with cuda_transformer_amd._C.set_bwd_workspace_cap(bytes).
+constexpr int64_t kDefaultBwdWorkspaceCap = int64_t{8} << 30;
+std::atomic<int64_t>& bwd_workspace_cap() {
+  static std::atomic<int64_t> cap{kDefaultBwdWorkspaceCap};
+  return cap;
+}
+
+// Workspace bytes the stored-dS schedule gets under the cap: whole heads only, and 0 (recompute)
+// when not even one head's tiles fit.
+int64_t capped_workspace(int64_t full, int64_t head) {
+  const int64_t cap = bwd_workspace_cap().load();
+  if (head <= 0 || cap < head) return 0;
+  return std::min(full, cap / head * head);
+}
 
 void* stream_of(const at::Tensor& t) {
   return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.get_device()).stream());
@@ -37,8 +51,8 @@ void* stream_of(const at::Tensor& t) {
 
 void check_rc(int rc) { TORCH_CHECK(rc == CTA_OK, cta_last_error()); }
 
-// Which schedule the last FP32 flash_attention_bwd in this process ran: 1 stored dS, 0 recompute
-// (the allocator refused the dS workspace), -1 none yet.  Process-wide, because autograd runs
+// Which schedule the last flash_attention_bwd in this process ran: 1 stored dS, 0 recompute
+// (the workspace cap holds less than one head, or the allocator refused it), -1 none yet.  Process-wide, because autograd runs
 // backward on its own device thread.  Exposed to Python as
 // cuda_transformer_amd._C.last_bwd_schedule().
 std::atomic<int>& last_bwd_schedule() {
@@ -590,13 +604,14 @@ std::tuple<at::Tensor, at::Tensor> flash_attention_fwd(at::Tensor Q, at::Tensor 
   return {O, L};
 }
 
-// Workspace for the stored-dS schedule of the FP32 backward: every head's dS tiles up to
-// kBwdWorkspaceCap (chunked over heads beyond that).  If the allocator cannot supply it, the
-// kernels run the recompute schedule, which needs no workspace (ws_bytes = 0).
+// Workspace for the stored-dS schedule of the FP32 backward: every head's dS tiles up to the
+// workspace cap (chunked over heads beyond that).  If the cap holds less than one head, or the
+// allocator cannot supply it, the kernels run the recompute schedule, which needs no workspace
+// (ws_bytes = 0).
 at::Tensor bwd_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs, bool causal,
                          const at::TensorOptions& opts, int64_t& ws_bytes) {
-  ws_bytes = std::min(cta_flash_attention_bwd_workspace(B, nh, T, hs, causal ? 1 : 0),
-                      kBwdWorkspaceCap);
+  ws_bytes = capped_workspace(cta_flash_attention_bwd_workspace(B, nh, T, hs, causal ? 1 : 0),
+                              cta_flash_attention_bwd_workspace(1, 1, T, hs, causal ? 1 : 0));
   at::Tensor ws;
   if (ws_bytes > 0) {
     try {
@@ -613,8 +628,8 @@ at::Tensor bwd_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs, bool caus
   return ws;
 }
 
-// 16-bit backward (extension): stored-dS schedule with a 16-bit dS workspace from torch's caching
-// allocator (the same 8 GiB cap as the FP32 op; chunked over heads beyond it).
+// 16-bit backward (extension): the FP32 op's two schedules, with a 16-bit dS workspace from
+// torch's caching allocator under the same cap (chunked over heads beyond it).
 std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd_half(
     const at::Tensor& Q, const at::Tensor& K, const at::Tensor& V, const at::Tensor& O,
     const at::Tensor& dO, const at::Tensor& L, bool causal) {
@@ -637,20 +652,23 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd_half(
   at::Tensor dV = at::empty({B, nh, T, hs}, Q.options());
   if (B * nh * T == 0) return {dQ, dK, dV};
   at::Tensor delta = at::empty({B, nh, T}, Q.options().dtype(at::kFloat));
-  const int64_t full = cta_flash_attention_bwd_bf16_workspace(B, nh, T, hs, causal ? 1 : 0);
-  const int64_t head = cta_flash_attention_bwd_bf16_workspace(1, 1, T, hs, causal ? 1 : 0);
-  // The 16-bit backward has only the stored-dS schedule: it needs at least one head's dS tiles,
-  // even when that alone exceeds the cap (e.g. T > 2^17 non-causal), and it fails with a clear
-  // message when the allocator cannot supply them.
-  const int64_t ws_bytes = std::max(head, std::min(full, kBwdWorkspaceCap));
+  // Stored-dS schedule when the cap holds at least one head's 16-bit dS tiles and the allocator
+  // supplies them; otherwise the workspace-free recompute schedule.
+  int64_t ws_bytes =
+      capped_workspace(cta_flash_attention_bwd_bf16_workspace(B, nh, T, hs, causal ? 1 : 0),
+                       cta_flash_attention_bwd_bf16_workspace(1, 1, T, hs, causal ? 1 : 0));
   at::Tensor ws;
-  try {
-    ws = at::empty({(ws_bytes + 15) / 16 * 4}, Q.options().dtype(at::kFloat));
-  } catch (const c10::OutOfMemoryError&) {
-    TORCH_CHECK(false, "flash_attention_bwd (", Q.scalar_type(), "): cannot allocate the ",
-                ws_bytes, "-byte dS workspace (one head needs ", head,
-                " bytes at T = ", T, "); the 16-bit backward has no workspace-free schedule");
+  if (ws_bytes > 0) {
+    try {
+      ws = at::empty({(ws_bytes + 15) / 16 * 4}, Q.options().dtype(at::kFloat));
+    } catch (const c10::OutOfMemoryError&) {
+      ws_bytes = 0;
+      TORCH_WARN_ONCE(
+          "flash_attention_bwd (16-bit): the dS workspace could not be allocated; running the "
+          "recompute schedule (dQ recomputes S and dP, same results to rounding)");
+    }
   }
+  last_bwd_schedule().store(ws_bytes > 0 ? 1 : 0);
   const at::Tensor q = attn_operand_half(Q), k = attn_operand_half(K), v = attn_operand_half(V),
                    o = attn_operand_half(O), g = attn_operand_half(dO);
   const auto qs = strides_of<4>(q), ks = strides_of<4>(k), vs = strides_of<4>(v),
@@ -662,7 +680,8 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd_half(
                                         u16(o), os.data(), u16(g), gs.data(),
                                         L.data_ptr<float>(), ls.data(), B, nh, T, hs,
                                         causal ? 1 : 0, w16(dQ), w16(dK), w16(dV),
-                                        delta.data_ptr<float>(), ws.data_ptr(), ws_bytes,
+                                        delta.data_ptr<float>(),
+                                        ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
                                         stream_of(Q)));
   return {dQ, dK, dV};
 }
@@ -721,10 +740,12 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> flash_attention_bwd(at::Tensor Q,
 // the concatenation of dq, dk and dv disappear.  Same kernels and results as
 // flash_attention_fwd / flash_attention_bwd on the head views.
 
-// A (B, T, n) activation the kernels can address: unit last stride, strides divisible by 4,
-// 16-byte aligned.
+// A packed (B, T, X) attention tensor read in place: unit last stride, strides divisible by 4,
+// 16-byte aligned, time stride in [0, 2^23) (the kernels' 32-bit stage offsets).  Anything else
+// is passed as a dense copy.
 at::Tensor packed_operand(const at::Tensor& t) {
   const bool ok = t.stride(2) == 1 && t.stride(0) % 4 == 0 && t.stride(1) % 4 == 0 &&
+                  t.stride(1) >= 0 && t.stride(1) < ((int64_t)1 << 23) &&
                   (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) == 0;
   return ok ? t : dense(t);
 }
@@ -869,10 +890,29 @@ PyObject* py_last_bwd_schedule(PyObject*, PyObject*) {
   const int s = cuda_transformer::last_bwd_schedule().load();
   return PyUnicode_FromString(s == 1 ? "stored" : s == 0 ? "recompute" : "none");
 }
+PyObject* py_bwd_workspace_cap(PyObject*, PyObject*) {
+  return PyLong_FromLongLong(cuda_transformer::bwd_workspace_cap().load());
+}
+PyObject* py_set_bwd_workspace_cap(PyObject*, PyObject* arg) {
+  const long long v = PyLong_AsLongLong(arg);
+  if (v == -1 && PyErr_Occurred()) return nullptr;
+  if (v < 0) {
+    PyErr_SetString(PyExc_ValueError, "the workspace cap must be a byte count >= 0");
+    return nullptr;
+  }
+  return PyLong_FromLongLong(cuda_transformer::bwd_workspace_cap().exchange(v));
+}
 PyMethodDef kMethods[] = {
     {"last_bwd_schedule", py_last_bwd_schedule, METH_NOARGS,
-     "Backward schedule of the last FP32 flash_attention_bwd in this process: 'stored' (dK/dV "
-     "stores dS, dQ reads it), 'recompute' (the dS workspace could not be allocated) or 'none'."},
+     "Backward schedule of the last flash_attention_bwd in this process: 'stored' (dK/dV "
+     "stores dS, dQ reads it), 'recompute' (no dS workspace: under the cap, or not allocatable) "
+     "or 'none'."},
+    {"bwd_workspace_cap", py_bwd_workspace_cap, METH_NOARGS,
+     "Largest dS workspace, in bytes, that flash_attention_bwd allocates (default 8 GiB)."},
+    {"set_bwd_workspace_cap", py_set_bwd_workspace_cap, METH_O,
+     "Set the dS workspace cap in bytes and return the previous one.  Heads whose dS tiles do "
+     "not all fit run in chunks; below one head (e.g. 0) the backward recomputes S and dP in "
+     "its dQ stage and allocates no workspace.  Process-wide."},
     {nullptr, nullptr, 0, nullptr}};
 }  // namespace
 

@@ -32,6 +32,24 @@ def cuda():
     return torch.device("cuda", 0)
 
 
+@pytest.fixture
+def bwd_cap():
+    """set_cap(nbytes) sets the flash_attention_bwd dS workspace cap for one test; the cap in force
+    before the test is restored afterwards (the cap is process-wide)."""
+    from cuda_transformer_amd import _C
+
+    saved = []
+
+    def set_cap(nbytes):
+        prev = _C.set_bwd_workspace_cap(nbytes)
+        if not saved:
+            saved.append(prev)
+
+    yield set_cap
+    if saved:
+        _C.set_bwd_workspace_cap(saved[0])
+
+
 def seeded(shape, seed, kind="randn", scale=1.0):
     """float32 host tensor from a fixed CPU generator (identical bits for GPU and oracle)."""
     import torch

@@ -226,3 +226,52 @@ def test_fa2_half_backward_chunked_matches_full(cuda):
     torch.cuda.synchronize()
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------- recompute schedule
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,nh,T,hs,causal", BWD_SHAPES)
+def test_fa2_half_backward_recompute_matches_oracle(cuda, bwd_cap, B, nh, T, hs, causal, dtype):
+    """The workspace-free 16-bit backward (workspace cap 0: dK/dV without the dS store, dQ
+    recomputing S and dP) against the float64 oracle with the bounds above; dK and dV bitwise
+    equal to the stored-dS schedule's (the same kernel body), dQ within the 16-bit rounding of
+    a different summation order."""
+    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+    from cuda_transformer_amd import _C
+    from conftest import rel_err
+
+    q, k, v = _half_inputs(B, nh, T, hs, seed=5000 + T + hs, dtype=dtype)
+    do = seeded((B, nh, T, hs), 9000 + T, kind="rand").to(dtype)
+    qg, kg, vg, dog = q.to(cuda), k.to(cuda), v.to(cuda), do.to(cuda)
+    O, L = flash_attention_fwd(qg, kg, vg, causal)
+    stored = flash_attention_bwd(qg, kg, vg, O, dog, L, causal)
+    bwd_cap(0)
+    grads = flash_attention_bwd(qg, kg, vg, O, dog, L, causal)
+    torch.cuda.synchronize()
+    assert _C.last_bwd_schedule() == "recompute"
+    _bwd_check([g.cpu() for g in grads], q, k, v, do, causal)
+    assert torch.equal(grads[1], stored[1]) and torch.equal(grads[2], stored[2])
+    if T > 1:
+        assert rel_err(f64(grads[0]), f64(stored[0])) <= 4e-3
+
+
+@pytest.mark.parametrize("schedule", ["stored", "recompute"])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_fa2_half_config1_as_stated(cuda, bwd_cap, dtype, causal, schedule):
+    """Benchmark config 1 (B1 H4 N256 D64) with its stated inputs, Q, K, V and dO i.i.d. N(0,1):
+    zero-mean dO, where dP - delta cancels most, through both backward schedules."""
+    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+    from cuda_transformer_amd import _C
+
+    if schedule == "recompute":
+        bwd_cap(0)
+    q, k, v = _half_inputs(1, 4, 256, 64, seed=123 + int(causal), dtype=dtype)
+    do = seeded((1, 4, 256, 64), 129, kind="randn").to(dtype)
+    qg, kg, vg = q.to(cuda), k.to(cuda), v.to(cuda)
+    O, L = flash_attention_fwd(qg, kg, vg, causal)
+    grads = flash_attention_bwd(qg, kg, vg, O, do.to(cuda), L, causal)
+    torch.cuda.synchronize()
+    assert _C.last_bwd_schedule() == schedule
+    _check(O.cpu(), L.cpu(), q, k, v, causal)
+    _bwd_check([g.cpu() for g in grads], q, k, v, do, causal)

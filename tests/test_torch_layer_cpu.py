@@ -94,3 +94,20 @@ def test_no_cpu_fallback():
         ops.cuda_fma(torch.randn(1, 2, 3), torch.randn(3, 4), torch.randn(4))
     with pytest.raises(NotImplementedError):
         ops.gelu_tanh_activation(torch.randn(2, 3, 4))
+
+
+def test_bwd_workspace_cap_setting():
+    """The dS workspace cap of flash_attention_bwd: 8 GiB by default, settable (returns the
+    previous value), byte counts only."""
+    _C = cuda_transformer_amd._C
+    assert _C.bwd_workspace_cap() == 8 << 30
+    assert _C.set_bwd_workspace_cap(0) == 8 << 30
+    try:
+        assert _C.bwd_workspace_cap() == 0
+        with pytest.raises(ValueError):
+            _C.set_bwd_workspace_cap(-5)
+        with pytest.raises(TypeError):
+            _C.set_bwd_workspace_cap("1 GiB")
+        assert _C.bwd_workspace_cap() == 0
+    finally:
+        assert _C.set_bwd_workspace_cap(8 << 30) == 0
