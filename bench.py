@@ -94,6 +94,8 @@ def parse_args():
                         "recompute: the reference's delta / dQ / dK/dV schedule; fold: the stored "
                         "schedule with delta computed inside the dK/dV stage (no delta launch)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--warm-seconds", type=float, default=1.0,
+                   help="back-to-back untimed steps before the timed ones, at least this long")
     p.add_argument("--cpu-port", action="store_true",
                    help="also time the numpy oracle on the CPU (cpu_baseline_port, ~10 s)")
     p.add_argument("--no-recompute", action="store_true",
@@ -455,7 +457,8 @@ def fa2_sweep(args):
     for N in seqs:
         steps = max(2, args.steps // max(1, N // 2048))
         ms, per_kernel, flushed, _, warm = fa2_timings(B, H, N, D, False, steps, args.warmup,
-                                                       args.bwd_schedule)
+                                                       args.bwd_schedule,
+                                                       warm_s=args.warm_seconds)
         fwd_fl, bwd_fl = attn_flops(B, H, N, D, False)
         bwd_ms = sum(v_ for k_, v_ in per_kernel.items() if k_ != "fwd")
         bwd_ms_f = sum(v_ for k_, v_ in flushed.items() if k_ != "fwd")
@@ -490,10 +493,12 @@ def fa2_sweep(args):
 def fa2_half_workload(args, kind):
     """The 16-bit FlashAttention-2 step (kind "bf16" or "f16") at the config-2 shape, causal and
     non-causal: forward (cta_flash_attention_fwd_<kind>) and backward
-    (cta_flash_attention_bwd_<kind>: delta, dK/dV storing 16-bit dS, dQ from dS), each timed
-    with HIP events on torch's current stream with inputs in HBM.  TFLOPS by the reference's
-    formula (forward 4*B*H*N^2*D, halved when causal; backward 2.5x), against the 2.5 PFLOP/s
-    dense BF16/FP16 MFMA peak.  One JSON line per mask."""
+    (cta_flash_attention_bwd_<kind>) in both schedules, recompute (no workspace: delta, dK/dV,
+    dQ recomputing S and dP) and stored dS (delta, dK/dV storing 16-bit dS, dQ from dS), each
+    timed with HIP events on torch's current stream with inputs in HBM.  `value` is the step
+    with the schedule the operator runs (recompute at hs 32 and 64, stored at hs 128).  TFLOPS
+    by the reference's formula (forward 4*B*H*N^2*D, halved when causal; backward 2.5x),
+    against the 2.5 PFLOP/s dense BF16/FP16 MFMA peak.  One JSON line per mask."""
     import torch
 
     from cuda_transformer_amd import capi
@@ -516,6 +521,7 @@ def fa2_half_workload(args, kind):
     s4, s3 = capi.strides(q.stride()), capi.strides(L.stride())
     vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     masks = {"both": (True, False), "causal": (True,), "full": (False,)}[args.masks]
+    default = "stored" if D == 128 else "recompute"
     for causal in masks:
         ws_bytes = ws_fn(B, H, N, D, int(causal))
         ws = torch.empty(ws_bytes // 4 + 4, device=dev)
@@ -525,26 +531,35 @@ def fa2_half_workload(args, kind):
                       st) != 0:
                 raise RuntimeError(lib.cta_last_error().decode())
 
-        def bwd():
+        def bwd(stored):
             if bwd_fn(vp(q), s4, vp(k), s4, vp(v), s4, vp(O), s4, vp(do), s4, vp(L), s3, B, H,
-                      N, D, int(causal), vp(dq), vp(dk), vp(dv), vp(delta), vp(ws), ws_bytes,
-                      st) != 0:
+                      N, D, int(causal), vp(dq), vp(dk), vp(dv), vp(delta),
+                      vp(ws) if stored else None, ws_bytes if stored else 0, st) != 0:
                 raise RuntimeError(lib.cta_last_error().decode())
-        fwd_ms = _time_kernel(fwd, max(10, args.steps), warm_s=0.2)
+        fwd_ms = _time_kernel(fwd, max(10, args.steps), warm_s=args.warm_seconds)
         fwd()
-        bwd_ms = _time_kernel(bwd, max(10, args.steps), warm_s=0.2)
+        bwd_ms = {sch: _time_kernel(lambda: bwd(sch == "stored"), max(10, args.steps),
+                                    warm_s=0.2)
+                  for sch in ("recompute", "stored")}
         fl, bfl = attn_flops(B, H, N, D, causal)
-        ftf, btf = fl / (fwd_ms * 1e-3) / 1e12, bfl / (bwd_ms * 1e-3) / 1e12
-        stf = (fl + bfl) / ((fwd_ms + bwd_ms) * 1e-3) / 1e12
+        ftf = fl / (fwd_ms * 1e-3) / 1e12
+        btf = {sch: bfl / (ms * 1e-3) / 1e12 for sch, ms in bwd_ms.items()}
+        stf = {sch: (fl + bfl) / ((fwd_ms + ms) * 1e-3) / 1e12 for sch, ms in bwd_ms.items()}
         print(json.dumps({
             "workload": f"FA2 {kind.upper()} fwd+bwd B{B} H{H} N{N} D{D} "
                         f"{'causal' if causal else 'non-causal'}",
-            "metric": f"FA2 {kind.upper()} fwd+bwd TFLOPS", "value": round(stf, 2), "unit": "TFLOPS",
-            "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
-            "fwd_tflops": round(ftf, 2), "bwd_tflops": round(btf, 2),
+            "metric": f"FA2 {kind.upper()} fwd+bwd TFLOPS", "value": round(stf[default], 2),
+            "unit": "TFLOPS", "bwd_schedule": default,
+            "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms[default], 4),
+            "fwd_tflops": round(ftf, 2), "bwd_tflops": round(btf[default], 2),
+            "schedules": {sch: {"bwd_ms": round(bwd_ms[sch], 4), "bwd_tflops": round(btf[sch], 2),
+                                "step_tflops": round(stf[sch], 2),
+                                "ds_workspace_bytes": ws_bytes if sch == "stored" else 0}
+                          for sch in bwd_ms},
             "dtype": f"{kind} inputs, fp32 accumulation",
-            "roofline": {"bound": "mfma", "achieved": round(stf, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(stf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "roofline": {"bound": "mfma", "achieved": round(stf[default], 2),
+                         "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(stf[default] / MFMA_BF16_PEAK_TFLOPS, 4),
                          "algorithmic_per_launch": fl + bfl},
         }), flush=True)
         del ws
@@ -1017,7 +1032,8 @@ def main():
     B, H, N, D = args.batch, args.heads, args.seq, args.head_dim
     causal = not args.non_causal
     ms_step, per_kernel, flushed, (q, k, v, do), warm = fa2_timings(
-        B, H, N, D, causal, args.steps, args.warmup, args.bwd_schedule)
+        B, H, N, D, causal, args.steps, args.warmup, args.bwd_schedule,
+        warm_s=args.warm_seconds)
 
     fwd_fl, bwd_fl = attn_flops(B, H, N, D, causal)
     value = (fwd_fl + bwd_fl) / (ms_step * 1e-3) / 1e12
@@ -1039,7 +1055,8 @@ def main():
     if args.bwd_schedule == "stored" and not args.no_recompute:
         # The reference's O(N)-memory schedule in the same run, after the headline's timing.
         r_ms, r_pk, r_fl, _, r_warm = fa2_timings(B, H, N, D, causal, max(3, args.steps // 2),
-                                                  args.warmup, "recompute")
+                                                  args.warmup, "recompute",
+                                                  warm_s=args.warm_seconds)
         r_bwd = sum(v_ for k_, v_ in r_pk.items() if k_ != "fwd")
         r_roof = roofline_of(r_pk, B, H, N, D, causal, r_fl)
         r_roof["traffic"] = (load_traffic(r_roof["kernel"], "fa2_config2_recompute_counters.md")

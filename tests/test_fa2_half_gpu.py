@@ -228,14 +228,44 @@ def test_fa2_half_backward_chunked_matches_full(cuda):
         assert torch.equal(a, b)
 
 
-# ---------------------------------------------------------------- recompute schedule
+# ---------------------------------------------------------------- the two schedules
+def _half_bwd_capi(q, k, v, O, do, L, causal, stored):
+    """The 16-bit backward through the C ABI: the stored-dS schedule (a workspace for every
+    head) or the recompute schedule (no workspace)."""
+    import ctypes
+
+    from cuda_transformer_amd import capi
+
+    lib = capi.lib()
+    kind = "bf16" if q.dtype == torch.bfloat16 else "f16"
+    fn = getattr(lib, f"cta_flash_attention_bwd_{kind}")
+    B, nh, T, hs = q.shape
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    s4, s3 = capi.strides(q.stride()), capi.strides(L.stride())
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    delta = torch.empty(B, nh, T, device=q.device)
+    nbytes, ws = 0, None
+    if stored:
+        nbytes = getattr(lib, f"cta_flash_attention_bwd_{kind}_workspace")(B, nh, T, hs,
+                                                                            int(causal))
+        ws = torch.empty(nbytes // 4 + 4, device=q.device)
+    rc = fn(P(q), s4, P(k), s4, P(v), s4, P(O), s4, P(do), s4, P(L), s3, B, nh, T, hs,
+            int(causal), P(dq), P(dk), P(dv), P(delta), P(ws) if stored else None, nbytes,
+            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, lib.cta_last_error()
+    torch.cuda.synchronize()
+    return dq, dk, dv
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("B,nh,T,hs,causal", BWD_SHAPES)
-def test_fa2_half_backward_recompute_matches_oracle(cuda, bwd_cap, B, nh, T, hs, causal, dtype):
-    """The workspace-free 16-bit backward (workspace cap 0: dK/dV without the dS store, dQ
-    recomputing S and dP) against the float64 oracle with the bounds above; dK and dV bitwise
-    equal to the stored-dS schedule's (the same kernel body), dQ within the 16-bit rounding of
-    a different summation order."""
+def test_fa2_half_backward_schedules_match_oracle(cuda, bwd_cap, B, nh, T, hs, causal, dtype):
+    """Both 16-bit schedules through the C ABI against the float64 oracle with the bounds
+    above: stored dS (a workspace) and recompute (none: dK/dV without the dS store, dQ
+    recomputing S and dP).  dK and dV are bitwise equal between them (the same kernel body),
+    dQ within the 16-bit rounding of a different summation order.  The operator runs the
+    recompute schedule at hs 32 and 64 and the stored one at hs 128 (recompute again under a
+    workspace cap of 0), with the same bits as the C ABI."""
     from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
     from cuda_transformer_amd import _C
     from conftest import rel_err
@@ -244,34 +274,40 @@ def test_fa2_half_backward_recompute_matches_oracle(cuda, bwd_cap, B, nh, T, hs,
     do = seeded((B, nh, T, hs), 9000 + T, kind="rand").to(dtype)
     qg, kg, vg, dog = q.to(cuda), k.to(cuda), v.to(cuda), do.to(cuda)
     O, L = flash_attention_fwd(qg, kg, vg, causal)
-    stored = flash_attention_bwd(qg, kg, vg, O, dog, L, causal)
-    bwd_cap(0)
-    grads = flash_attention_bwd(qg, kg, vg, O, dog, L, causal)
-    torch.cuda.synchronize()
-    assert _C.last_bwd_schedule() == "recompute"
-    _bwd_check([g.cpu() for g in grads], q, k, v, do, causal)
-    assert torch.equal(grads[1], stored[1]) and torch.equal(grads[2], stored[2])
+    stored = _half_bwd_capi(qg, kg, vg, O, dog, L, causal, stored=True)
+    recomputed = _half_bwd_capi(qg, kg, vg, O, dog, L, causal, stored=False)
+    for grads in (stored, recomputed):
+        _bwd_check([g.cpu() for g in grads], q, k, v, do, causal)
+    assert torch.equal(recomputed[1], stored[1]) and torch.equal(recomputed[2], stored[2])
     if T > 1:
-        assert rel_err(f64(grads[0]), f64(stored[0])) <= 4e-3
+        assert rel_err(f64(recomputed[0]), f64(stored[0])) <= 4e-3
+    op = flash_attention_bwd(qg, kg, vg, O, dog, L, causal)
+    torch.cuda.synchronize()
+    expect = "stored" if hs == 128 else "recompute"
+    assert _C.last_bwd_schedule() == expect
+    for a, b in zip(op, stored if expect == "stored" else recomputed):
+        assert torch.equal(a, b)
+    if hs == 128:
+        bwd_cap(0)
+        op = flash_attention_bwd(qg, kg, vg, O, dog, L, causal)
+        torch.cuda.synchronize()
+        assert _C.last_bwd_schedule() == "recompute"
+        for a, b in zip(op, recomputed):
+            assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("schedule", ["stored", "recompute"])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_fa2_half_config1_as_stated(cuda, bwd_cap, dtype, causal, schedule):
+def test_fa2_half_config1_as_stated(cuda, dtype, causal, schedule):
     """Benchmark config 1 (B1 H4 N256 D64) with its stated inputs, Q, K, V and dO i.i.d. N(0,1):
     zero-mean dO, where dP - delta cancels most, through both backward schedules."""
-    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
-    from cuda_transformer_amd import _C
+    from cuda_transformer.ops import flash_attention_fwd
 
-    if schedule == "recompute":
-        bwd_cap(0)
     q, k, v = _half_inputs(1, 4, 256, 64, seed=123 + int(causal), dtype=dtype)
     do = seeded((1, 4, 256, 64), 129, kind="randn").to(dtype)
     qg, kg, vg = q.to(cuda), k.to(cuda), v.to(cuda)
     O, L = flash_attention_fwd(qg, kg, vg, causal)
-    grads = flash_attention_bwd(qg, kg, vg, O, do.to(cuda), L, causal)
-    torch.cuda.synchronize()
-    assert _C.last_bwd_schedule() == schedule
+    grads = _half_bwd_capi(qg, kg, vg, O, do.to(cuda), L, causal, stored=schedule == "stored")
     _check(O.cpu(), L.cpu(), q, k, v, causal)
     _bwd_check([g.cpu() for g in grads], q, k, v, do, causal)
