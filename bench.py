@@ -712,6 +712,16 @@ def ops_workload(args):
          timed(lambda a_, b_: b_.copy_(a_), sets), 8.0 * (1 << 26), "GB/s", None, 0.0, "",
          len(sets))
     del src, sets
+    # ... and this library's own dwordx4 copy (cta_device_copy) at 256 MiB and at the sizes of
+    # the LayerNorm passes below (50.3 MB and 75.5 MB moved): the ceiling of a read + write
+    # stream of that length, launch ramp included
+    for nfl in (1 << 26, 8192 * 768, 8192 * 768 * 3 // 2):
+        src = torch.ones(nfl, device=dev)
+        sets = copies_of(src, torch.empty_like(src))
+        emit(f"device_copy (cta_device_copy, {nfl * 4 / 2**20:.0f} MiB)", [nfl],
+             timed(lambda a_, b_: lib.cta_device_copy(vp(a_), vp(b_), nfl, st), sets),
+             8.0 * nfl, "GB/s", None, 0.0, "", len(sets))
+        del src, sets
 
     # ---- linear layer: X[8192,768] . W[768,3072] + b, X, W ~ N(0, 0.02^2)
     M, K, Nn = 8192, 768, 3072

@@ -85,6 +85,7 @@ SIGNATURES = {
                                 _p]),
     "cta_db_calculation_workspace": (_i64, [_i64, _i64, _i64]),
     "cta_db_calculation": (_int, [_p, _i64p, _i64, _i64, _i64, _p, _p, _p]),
+    "cta_device_copy": (_int, [_p, _p, _i64, _p]),
     "cta_linear_weight_bias_grad_workspace": (_i64, [_i64, _i64, _i64]),
     "cta_linear_weight_bias_grad": (_int, [_p, _i64p, _p, _i64p, _i64, _i64, _i64, _p, _p, _p, _p]),
     "cta_gelu_fwd": (_int, [_p, _p, _i64, _p]),

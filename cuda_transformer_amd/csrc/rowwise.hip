@@ -121,6 +121,26 @@ unsigned elementwise_grid(int64_t n4) {
   return (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, 256 * 16));
 }
 
+// Plain dwordx4 copy, four float4 per thread in flight per iteration (the elementwise kernels'
+// access pattern without their arithmetic): the streaming ceiling of a read + write pass.
+__global__ __launch_bounds__(256) void device_copy_kernel(const float* __restrict__ src,
+                                                          float* __restrict__ dst, int64_t n4) {
+  const int64_t stride = (int64_t)gridDim.x * 1024;
+  for (int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x; base < n4; base += stride) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = base + 256 * u;
+      v[u] = (i < n4) ? ld4(src + 4 * i) : zero4();
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = base + 256 * u;
+      if (i < n4) st4(dst + 4 * i, v[u]);
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void zero_fill_kernel(float* __restrict__ p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
     p[i] = 0.0f;
@@ -661,6 +681,17 @@ int launch_gelu_bwd(const float* x, const float* dy, float* dx, int64_t numel, v
   return check_launch(name);
 }
 }  // namespace
+
+extern "C" int cta_device_copy(const float* src, float* dst, int64_t n, void* stream) {
+  if (n < 0) return fail(CTA_ERR_INVALID_ARGUMENT, "negative size");
+  if (n == 0) return CTA_OK;
+  if (!src || !dst) return fail(CTA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (n % 4 != 0 || !aligned16(src) || !aligned16(dst))
+    return fail(CTA_ERR_LAYOUT, "device_copy needs n % 4 == 0 and 16-byte aligned buffers");
+  hipLaunchKernelGGL(device_copy_kernel, dim3(elementwise_grid(n / 4)), dim3(256), 0,
+                     as_stream(stream), src, dst, n / 4);
+  return check_launch("device_copy");
+}
 
 extern "C" int cta_gelu_fwd(const float* x, float* y, int64_t numel, void* stream) {
   return launch_gelu_fwd<false>(x, y, numel, stream, "gelu_activation");

@@ -349,6 +349,11 @@ int cta_cuda_fma_mul(const float* dy, const int64_t* dy_strides,
                      int64_t batch, int64_t m, int64_t k, int64_t n, int64_t w_batch,
                      float* dx, float* workspace, void* stream);
 
+/* dst[0..n) = src[0..n): a plain dwordx4 device copy (16-byte aligned buffers, n % 4 == 0), a
+ * stream of one read and one write per element.  No counterpart in the reference: it is the
+ * streaming ceiling that bench.py measures beside the bandwidth-bound kernels. */
+int cta_device_copy(const float* src, float* dst, int64_t n, void* stream);
+
 /* Bytes of scratch cta_db_calculation needs for a (batch, m, n) gradient. */
 int64_t cta_db_calculation_workspace(int64_t batch, int64_t m, int64_t n);
 

@@ -749,3 +749,16 @@ def test_add_layernorm_autograd(cuda):
     CudaLayerNorm.apply(xr + fr, gr, br, 1e-5).backward(gy)
     assert torch.equal(x.grad, xr.grad) and torch.equal(f.grad, fr.grad)
     assert torch.equal(g.grad, gr.grad) and torch.equal(b.grad, br.grad)
+
+
+def test_device_copy(cuda):
+    from cuda_transformer_amd import capi
+
+    src = seeded((3 * 1024 * 1024 + 4,), 90).to(cuda)
+    dst = torch.full_like(src, float("nan"))
+    capi.call("cta_device_copy", src.data_ptr(), dst.data_ptr(), src.numel(),
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(src, dst)
+    with pytest.raises(capi.CtaError, match="n % 4 == 0"):
+        capi.call("cta_device_copy", src.data_ptr(), dst.data_ptr(), 6, 0)
