@@ -719,50 +719,106 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_half_kernel
     const E* kr = smem + buf * STAGE;
     const E* vr = kr + RTILE;
     const E* kt = vr + RTILE;
+    if constexpr (CAUSAL && HS == 64) {
+      // Both tiles' S and dP chains first (four independent MFMA chains), then their softmax
+      // and dQ products.  A/B in one process, same bits: backward +3% causal at hs 64; -2%
+      // non-causal and -5% at hs 32, which keep one tile at a time.
+      f32x16 sacc2[NSUB], pacc2[NSUB];
+      bool live2[NSUB];
 #pragma unroll
-    for (int sub = 0; sub < NSUB; ++sub) {
-      const int jj0 = s_idx * BN + sub * 32;
-      if (jj0 >= T) continue;                 // ragged tail
-      if (CAUSAL && jj0 > i0 + 31) continue;  // tile entirely above this wave's diagonal
-
-      // S^T and dP^T - delta: lane holds query my_i, keys jj0 + R(r, half).
-      f32x16 sacc = zero16(), pacc;
+      for (int sub = 0; sub < NSUB; ++sub) {
+        const int jj0 = s_idx * BN + sub * 32;
+        live2[sub] = jj0 < T && !(CAUSAL && jj0 > i0 + 31);
+        sacc2[sub] = zero16();
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pacc[r] = -drow;
-      const E* krow = kr + (sub * 32 + col) * RP + 8 * half;
-      const E* vrow = vr + (sub * 32 + col) * RP + 8 * half;
+        for (int r = 0; r < 16; ++r) pacc2[sub][r] = -drow;
+        if (!live2[sub]) continue;
+        const E* krow = kr + (sub * 32 + col) * RP + 8 * half;
+        const E* vrow = vr + (sub * 32 + col) * RP + 8 * half;
 #pragma unroll
-      for (int s = 0; s < QS; ++s) sacc = Half16<E>::mfma(ld8<E>(krow + 16 * s), qf[s], sacc);
+        for (int s = 0; s < QS; ++s)
+          sacc2[sub] = Half16<E>::mfma(ld8<E>(krow + 16 * s), qf[s], sacc2[sub]);
 #pragma unroll
-      for (int s = 0; s < QS; ++s) pacc = Half16<E>::mfma(ld8<E>(vrow + 16 * s), gf[s], pacc);
-
-      // P = e^{S - L}; masked keys (causal, past T) exactly 0.  Two explicit paths: left to
-      // the compiler, the masked form is if-converted into selects on every tile.
-      auto exp_scores = [&]<bool MASKED>() {
+        for (int s = 0; s < QS; ++s)
+          pacc2[sub] = Half16<E>::mfma(ld8<E>(vrow + 16 * s), gf[s], pacc2[sub]);
+      }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = fmaf(sacc[r], scale_log2, -lrow);
-          if (MASKED) {
-            const int j = jj0 + mfma_row(r, half);
-            if ((CAUSAL && j > my_i) || j >= T) x = -INFINITY;  // 2^x = 0
+      for (int sub = 0; sub < NSUB; ++sub) {
+        if (!live2[sub]) continue;
+        const int jj0 = s_idx * BN + sub * 32;
+        f32x16& sacc = sacc2[sub];
+        const f32x16& pacc = pacc2[sub];
+        auto exp_scores = [&]<bool MASKED>() {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float x = fmaf(sacc[r], scale_log2, -lrow);
+            if (MASKED) {
+              const int j = jj0 + mfma_row(r, half);
+              if ((CAUSAL && j > my_i) || j >= T) x = -INFINITY;
+            }
+            sacc[r] = fast_exp2(x);
           }
-          sacc[r] = fast_exp2(x);
+        };
+        if ((CAUSAL && jj0 + 31 > i0) || (jj0 + 32 > T))
+          exp_scores.template operator()<true>();
+        else
+          exp_scores.template operator()<false>();
+        vec8_t<E> db[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) db[r >> 3][r & 7] = (E)(sacc[r] * pacc[r]);
+#pragma unroll
+        for (int d = 0; d < HS / 32; ++d) {
+          const E* ktrow = kt + (d * 32 + col) * TP + sub * 32 + 8 * half;
+#pragma unroll
+          for (int s = 0; s < 2; ++s) acc[d] = Half16<E>::mfma(ld8<E>(ktrow + 16 * s), db[s], acc[d]);
         }
-      };
-      if ((CAUSAL && jj0 + 31 > i0) || (jj0 + 32 > T))
-        exp_scores.template operator()<true>();
-      else
-        exp_scores.template operator()<false>();
+      }
+    } else {
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub) {
+        const int jj0 = s_idx * BN + sub * 32;
+        if (jj0 >= T) continue;                 // ragged tail
+        if (CAUSAL && jj0 > i0 + 31) continue;  // tile entirely above this wave's diagonal
 
-      // dS = P (dP - delta), rounded to 16 bits as the B operand of dQ^T += K^T dS^T.
-      vec8_t<E> db[2];
+        // S^T and dP^T - delta: lane holds query my_i, keys jj0 + R(r, half).
+        f32x16 sacc = zero16(), pacc;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) db[r >> 3][r & 7] = (E)(sacc[r] * pacc[r]);
+        for (int r = 0; r < 16; ++r) pacc[r] = -drow;
+        const E* krow = kr + (sub * 32 + col) * RP + 8 * half;
+        const E* vrow = vr + (sub * 32 + col) * RP + 8 * half;
 #pragma unroll
-      for (int d = 0; d < HS / 32; ++d) {
-        const E* ktrow = kt + (d * 32 + col) * TP + sub * 32 + 8 * half;
+        for (int s = 0; s < QS; ++s) sacc = Half16<E>::mfma(ld8<E>(krow + 16 * s), qf[s], sacc);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) acc[d] = Half16<E>::mfma(ld8<E>(ktrow + 16 * s), db[s], acc[d]);
+        for (int s = 0; s < QS; ++s) pacc = Half16<E>::mfma(ld8<E>(vrow + 16 * s), gf[s], pacc);
+
+        // P = e^{S - L}; masked keys (causal, past T) exactly 0.  Two explicit paths: left to
+        // the compiler, the masked form is if-converted into selects on every tile.
+        auto exp_scores = [&]<bool MASKED>() {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float x = fmaf(sacc[r], scale_log2, -lrow);
+            if (MASKED) {
+              const int j = jj0 + mfma_row(r, half);
+              if ((CAUSAL && j > my_i) || j >= T) x = -INFINITY;  // 2^x = 0
+            }
+            sacc[r] = fast_exp2(x);
+          }
+        };
+        if ((CAUSAL && jj0 + 31 > i0) || (jj0 + 32 > T))
+          exp_scores.template operator()<true>();
+        else
+          exp_scores.template operator()<false>();
+
+        // dS = P (dP - delta), rounded to 16 bits as the B operand of dQ^T += K^T dS^T.
+        vec8_t<E> db[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) db[r >> 3][r & 7] = (E)(sacc[r] * pacc[r]);
+#pragma unroll
+        for (int d = 0; d < HS / 32; ++d) {
+          const E* ktrow = kt + (d * 32 + col) * TP + sub * 32 + 8 * half;
+#pragma unroll
+          for (int s = 0; s < 2; ++s) acc[d] = Half16<E>::mfma(ld8<E>(ktrow + 16 * s), db[s], acc[d]);
+        }
       }
     }
 

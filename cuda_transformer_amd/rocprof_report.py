@@ -113,7 +113,8 @@ def short_name(name: str) -> str:
     and row-length variants apart): "void cta::(anonymous namespace)::k<64, true>(float*)" ->
     "k<64, true>".  rocprofv3's truncated names (-T) are already short.  Names it cannot
     demangle (e.g. templates over __bf16, "DF16b") stay mangled; for those the last identifier
-    of the Itanium nested name is taken."""
+    of the Itanium nested name is taken, with its template arguments decoded where they are
+    integer, boolean or floating-point types and literals (so instances stay apart)."""
     if not name.startswith("_Z"):
         n = name[5:] if name.startswith("void ") else name
         n = n.replace("(anonymous namespace)::", "")
@@ -136,7 +137,40 @@ def short_name(name: str) -> str:
         n = int(name[i:j])
         last = name[j:j + n]
         i = j + n
+    if i < len(name) and name[i] == "I":
+        args = _template_args(name, i + 1)
+        if args is not None:
+            last += "<" + ", ".join(args) + ">"
     return last
+
+
+_TYPE_CODES = {"DF16b": "bf16", "DF16_": "f16", "f": "float", "d": "double", "i": "int",
+               "j": "unsigned", "b": "bool"}
+
+
+def _template_args(name: str, i: int) -> list[str] | None:
+    """Decode the Itanium template arguments starting at name[i] (after the 'I') up to the
+    closing 'E': literals L<type><value>E of integer and boolean types, and the builtin types of
+    _TYPE_CODES.  None when anything else appears."""
+    out = []
+    while i < len(name) and name[i] != "E":
+        if name[i] == "L":
+            t = name[i + 1]
+            j = name.find("E", i + 2)
+            if t not in "bijlm" or j < 0:
+                return None
+            v = name[i + 2:j].replace("n", "-")
+            out.append(("true" if v == "1" else "false") if t == "b" else v)
+            i = j + 1
+            continue
+        for code, text in _TYPE_CODES.items():
+            if name.startswith(code, i):
+                out.append(text)
+                i += len(code)
+                break
+        else:
+            return None
+    return out
 
 
 def read_kernel_stats(directory) -> dict[str, dict]:
@@ -159,7 +193,9 @@ def read_trace_window(directory, skip: int, count: int,
     each kernel, in start order, from a --kernel-trace run (``*_kernel_trace.csv``): the
     dispatches a benchmark timed, without its warm-up or later phases.  skip and count count
     steps; a kernel launched k times per step (per_step[kernel] = k, e.g. once per head chunk)
-    takes dispatches [k skip, k (skip + count)); per_step keys match kernel names by substring."""
+    takes dispatches [k skip, k (skip + count)); a per_step key names a kernel by its short name
+    or by the base identifier before its template arguments (exact match, never a substring:
+    fa2_bwd_dq_kernel does not match fa2_bwd_dq_ds_kernel<...>)."""
     per: dict[str, list[tuple[int, int]]] = {}
     with open(_one(directory, "_kernel_trace.csv")) as f:
         for r in csv.DictReader(f):
@@ -169,7 +205,8 @@ def read_trace_window(directory, skip: int, count: int,
     for k, ds in per.items():
         ds.sort()
         durs = [e - s for s, e in ds]
-        mult = next((v for key, v in (per_step or {}).items() if key in k), 1)
+        ps = per_step or {}
+        mult = ps.get(k, ps.get(k.split("<", 1)[0], 1))
         win = durs[mult * skip:mult * (skip + count)]
         if win:
             out[k] = {"calls": len(win), "avg_ns": statistics.fmean(win),

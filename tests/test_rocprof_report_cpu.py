@@ -131,7 +131,14 @@ def test_short_name_of_mangled_kernels():
 
     mangled = ("_ZN3cta12_GLOBAL__N_119fa2_fwd_bf16_kernelILi64ELb0EEEvPKDF16bS3_S3_PDF16bPfiiii"
                "NS0_11RowStridesBES6_S6_fff")
-    assert short_name(mangled) == "fa2_fwd_bf16_kernel"
+    assert short_name(mangled) == "fa2_fwd_bf16_kernel<64, false>"
+    dkdv = ("_ZN3cta12_GLOBAL__N_124fa2_bwd_dkdv_half_kernelIDF16bLi64ELb1ELi8ELi64ELi2ELb0EEEv"
+            "PKT_S4_S4_S4_PKfS6_PS2_S7_S7_iiiiiNS0_11RowStridesHES8_S8_S8_S8_ff")
+    assert short_name(dkdv) == "fa2_bwd_dkdv_half_kernel<bf16, 64, true, 8, 64, 2, false>"
+    f16 = "_ZN3cta12_GLOBAL__N_122fa2_bwd_dq_half_kernelIDF16_Li32ELb0EEEvPKT_"
+    assert short_name(f16) == "fa2_bwd_dq_half_kernel<f16, 32, false>"
+    # an argument it cannot decode leaves the bare identifier
+    assert short_name("_ZN3cta1kINS_3FooEEEvv") == "k"
     assert short_name("_Z6foobarv") == "foobar"
     assert short_name("fa2_fwd_kernel") == "fa2_fwd_kernel"
     assert short_name("__amd_rocclr_copyBuffer") == "__amd_rocclr_copyBuffer"
@@ -200,3 +207,23 @@ def test_registers_from_kernel_trace(tmp_path):
     (r,) = rr.build_rows(d)
     assert r.info["vgpr"] == 256 and r.info["scratch"] == 20 and r.info["workgroup"] == 256
     assert (r.waves_theory, r.waves_limit) == (2, "vgpr")
+
+
+def test_trace_window_per_step_matches_exact_names(tmp_path):
+    """A per-step multiplier applies to the kernel it names (short name or base identifier),
+    not to another kernel whose name contains it."""
+    from cuda_transformer_amd import rocprof_report as rr
+
+    d = tmp_path / "trace"
+    d.mkdir()
+    rows = [("fa2_bwd_dq_kernel", 0), ("fa2_bwd_dq_ds_kernel<64, true>", 0),
+            ("fa2_bwd_dq_ds_kernel<64, true>", 0)] * 4
+    with open(d / "run_kernel_trace.csv", "w") as f:
+        f.write("Kernel_Name,Start_Timestamp,End_Timestamp\n")
+        for t, (k, _) in enumerate(rows):
+            f.write(f'"{k}",{10 * t},{10 * t + 1 + t}\n')
+    win = rr.read_trace_window(d, 1, 2, {"fa2_bwd_dq_ds_kernel": 2})
+    assert win["fa2_bwd_dq_kernel"]["calls"] == 2          # not widened by the ds multiplier
+    assert win["fa2_bwd_dq_ds_kernel<64, true>"]["calls"] == 4
+    win = rr.read_trace_window(d, 1, 2, {"fa2_bwd_dq": 2})  # a substring names nothing
+    assert win["fa2_bwd_dq_kernel"]["calls"] == 2 and win["fa2_bwd_dq_ds_kernel<64, true>"]["calls"] == 2
