@@ -276,6 +276,63 @@ __device__ __forceinline__ void sched_second_part() {
 // buffer stores from its origin: a lane's column is a fixed per-lane offset (moved out of range
 // when the column lies past N), each row's offset is scalar, and rows past M fall outside the
 // resource, so the stores need no per-element bounds tests or 64-bit address arithmetic.
+// One element of the epilogue: v = alpha * acc + bias, the mask, the gradient stages (xg: the
+// aux value), then the value stored to C (cv) and, for the forward GELU stages, to aux (xv).
+template <int ACT, bool RAW, bool MASK>
+__device__ __forceinline__ void epilogue_value(float a, float bias, float xg,
+                                               const GemmEpilogue& ep, bool masked, float& cv,
+                                               float& xv) {
+  float val = a;
+  if (!RAW) {
+    val = fmaf(ep.alpha, val, bias);
+    if (MASK && masked) val = -INFINITY;
+    if constexpr (ACT == kActGeluGrad) val = gelu_grad(xg, val);
+    else if constexpr (ACT == kActGeluTanhGrad) val = gelu_tanh_grad(xg, val);
+    else if constexpr (ACT == kActMulAux) val = val * xg;
+  }
+  // The derivative forms store gelu'(v) (its product with g = 1.0 is exact, so a later
+  // kActMulAux stage gives gelu_grad(v, g) bit for bit) and gelu(v).
+  cv = val;
+  if (!RAW && ACT == kActGeluDeriv) cv = gelu_grad(val, 1.0f);
+  if (!RAW && ACT == kActGeluTanhDeriv) cv = gelu_tanh_grad(val, 1.0f);
+  xv = 0.0f;
+  if (!RAW && (ACT == kActGelu || ACT == kActGeluDeriv)) xv = gelu_f(val);
+  if (!RAW && (ACT == kActGeluTanh || ACT == kActGeluTanhDeriv)) xv = gelu_tanh_f(val);
+}
+
+// The wave's block when it spans 2^31 bytes or more (row strides of 2^22 floats and up), which
+// 32-bit buffer offsets cannot address: plain stores through 64-bit addresses with explicit
+// row and column bounds, the same values as block_store's.
+template <class TL, int ACT, bool RAW, bool MASK>
+__device__ __forceinline__ void block_store_wide(const f32x16 (&acc)[TL::MB][TL::NB], float* Cz,
+                                              float* Xz, int64_t srow, const GemmEpilogue& ep,
+                                              int M, int N, int mw, int nw, int half, int col) {
+  constexpr bool kGrad =
+      !RAW && (ACT == kActGeluGrad || ACT == kActGeluTanhGrad || ACT == kActMulAux);
+  constexpr bool kAux = !RAW && (ACT == kActGelu || ACT == kActGeluDeriv ||
+                                 ACT == kActGeluTanh || ACT == kActGeluTanhDeriv);
+#pragma unroll
+  for (int j = 0; j < TL::NB; ++j) {
+    const int n = nw + j * 32 + col;
+    if (n >= N) continue;
+    const float bias = (!RAW && ep.bias) ? ep.bias[(int64_t)n * ep.bias_stride] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TL::MB; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = mw + i * 32 + mfma_row(r, half);
+        if (m >= M) continue;
+        const int64_t at = (int64_t)m * srow + n;
+        const float xg = kGrad ? Xz[at] : 0.0f;
+        float cv, xv;
+        epilogue_value<ACT, RAW, MASK>(acc[i][j][r], bias, xg, ep, n > m, cv, xv);
+        Cz[at] = cv;
+        if (kAux) Xz[at] = xv;
+      }
+    }
+  }
+}
+
 template <class TL, int ACT, bool RAW, bool MASK>
 __device__ __forceinline__ void block_store(const f32x16 (&acc)[TL::MB][TL::NB], float* Cz,
                                             float* Xz, int64_t srow, const GemmEpilogue& ep,
@@ -284,9 +341,14 @@ __device__ __forceinline__ void block_store(const f32x16 (&acc)[TL::MB][TL::NB],
   constexpr int WROWS = TL::BM / TL::WM, WCOLS = TL::BN / TL::WN;
   constexpr bool kGrad =
       !RAW && (ACT == kActGeluGrad || ACT == kActGeluTanhGrad || ACT == kActMulAux);
+  const int64_t span = ((int64_t)(min(WROWS, M - mw) - 1) * srow + min(WCOLS, N - nw)) * 4;
+  if (span >= ((int64_t)1 << 31) || (int64_t)WROWS * srow * 4 >= ((int64_t)1 << 31)) {
+    block_store_wide<TL, ACT, RAW, MASK>(acc, Cz, Xz, srow, ep, M, N, mw, nw, half, col);
+    return;
+  }
   float* Cb = Cz + (int64_t)mw * srow + nw;
   float* Xb = Xz ? Xz + (int64_t)mw * srow + nw : Cb;
-  const int nbytes = (int)(((int64_t)(min(WROWS, M - mw) - 1) * srow + min(WCOLS, N - nw)) * 4);
+  const int nbytes = (int)span;
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(Cb, (short)0, nbytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(Xb, (short)0, nbytes, 0x00020000);
   const int row_bytes = (int)(srow * 4);
@@ -320,25 +382,13 @@ __device__ __forceinline__ void block_store(const f32x16 (&acc)[TL::MB][TL::NB],
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int so = (i * 32 + 8 * (r >> 2) + (r & 3)) * row_bytes;
-        float val = acc[i][j][r];
-        if (!RAW) {
-          val = fmaf(ep.alpha, val, bv[j]);
-          if (MASK && n > mw + i * 32 + mfma_row(r, half)) val = -INFINITY;
-          if constexpr (kGrad)
-            val = ACT == kActGeluGrad       ? gelu_grad(xg[i][j][r], val)
-                  : ACT == kActGeluTanhGrad ? gelu_tanh_grad(xg[i][j][r], val)
-                                            : val * xg[i][j][r];
-        }
-        // The derivative forms store gelu'(v) (its product with g = 1.0 is exact, so a later
-        // kActMulAux stage gives gelu_grad(v, g) bit for bit) and gelu(v).
-        float cv = val;
-        if (!RAW && ACT == kActGeluDeriv) cv = gelu_grad(val, 1.0f);
-        if (!RAW && ACT == kActGeluTanhDeriv) cv = gelu_tanh_grad(val, 1.0f);
+        float cv, xv;
+        epilogue_value<ACT, RAW, MASK>(acc[i][j][r], bv[j], kGrad ? xg[i][j][r] : 0.0f, ep,
+                                       n > mw + i * 32 + mfma_row(r, half), cv, xv);
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(cv), rc, vo[j], so, 0);
-        if (!RAW && (ACT == kActGelu || ACT == kActGeluDeriv))
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gelu_f(val)), rx, vo[j], so, 0);
-        if (!RAW && (ACT == kActGeluTanh || ACT == kActGeluTanhDeriv))
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gelu_tanh_f(val)), rx, vo[j], so, 0);
+        if (!RAW && (ACT == kActGelu || ACT == kActGeluDeriv || ACT == kActGeluTanh ||
+                     ACT == kActGeluTanhDeriv))
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(xv), rx, vo[j], so, 0);
       }
     }
   }
@@ -662,9 +712,6 @@ int gemm_launch_tile(const GemmOperand& A, const GemmOperand& B, const GemmOut& 
   int64_t S = splitk_factor<TL>(M, N, K, Z);
   const int64_t cs_floats = ep.colsum ? N : 0;  // per split
   if (S > 1 && (workspace == nullptr || workspace_floats < S * (Z * M * N + cs_floats))) S = 1;
-  // A wave's output block is stored through 32-bit buffer offsets from its origin.
-  if ((int64_t)TL::BM * std::max<int64_t>(C.s_row, N) * 4 >= ((int64_t)1 << 31))
-    return fail(CTA_ERR_INVALID_ARGUMENT, "GEMM output row stride too large");
   const int64_t kchunk =
       S > 1 ? ((K + S - 1) / S + TL::BK - 1) / TL::BK * TL::BK : std::max<int64_t>(K, 1);
   const int64_t ntiles = ((N + TL::BN - 1) / TL::BN) * ((M + TL::BM - 1) / TL::BM);

@@ -275,8 +275,8 @@ int64_t cta_cuda_fma_workspace(int64_t batch, int64_t m, int64_t k, int64_t n);
  * (broadcast, batch stride ignored) or `batch`.  Any strides: transposed views are read
  * in place.  `workspace` may be NULL; given cta_cuda_fma_workspace() bytes, shapes with few
  * output tiles and a long K are split along K with a deterministic reduction.  Outputs
- * are stored with 32-bit offsets within a 128-row block: n must stay below 2^22 (larger n
- * returns CTA_ERR_INVALID_ARGUMENT).
+ * are stored through 32-bit buffer offsets within a wave's block of rows; rows of 2^22 floats
+ * and longer, which those offsets cannot span, are stored through 64-bit addresses instead.
  * Replaces cuda_transformer::cuda_fma (Transformer_launchers/linear_layer.cu:28-70). */
 int cta_cuda_fma(const float* x, const int64_t* x_strides,
                  const float* w, const int64_t* w_strides,

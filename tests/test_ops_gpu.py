@@ -762,3 +762,26 @@ def test_device_copy(cuda):
     assert torch.equal(src, dst)
     with pytest.raises(capi.CtaError, match="n % 4 == 0"):
         capi.call("cta_device_copy", src.data_ptr(), dst.data_ptr(), 6, 0)
+
+
+def test_cuda_fma_rows_beyond_32bit_offsets(cuda):
+    """Output rows of 2^24 + 4 floats: a wave's block of rows then spans more than 2^31 bytes,
+    which the epilogue's 32-bit buffer offsets cannot address, so it stores through 64-bit
+    addresses.  x (1, 2, 4) . W (4, N) + b against the float64 product; the fused GELU epilogue
+    on the same product gives the same pre-activation bits and GELU(pre)."""
+    from cuda_transformer.ops import cuda_fma
+    from cuda_transformer_amd.ops import cuda_fma_gelu
+
+    N = (1 << 24) + 4
+    print(f"cuda_fma M2 K4 N{N}", flush=True)
+    x = seeded((1, 2, 4), 101).to(cuda)
+    w = seeded((4, N), 102).to(cuda)
+    b = seeded((N,), 103).to(cuda)
+    out = cuda_fma(x, w, b)
+    pre, act = cuda_fma_gelu(x, w, b)
+    torch.cuda.synchronize()
+    ref = f64(x)[0] @ f64(w) + f64(b)
+    np.testing.assert_allclose(f64(out)[0], ref, rtol=1e-5, atol=1e-5)
+    assert torch.equal(pre, out)
+    np.testing.assert_allclose(f64(act)[0], ew.gelu_forward(ref), rtol=1e-5, atol=1e-5)
+    del w, out, pre, act
