@@ -282,11 +282,13 @@ class CudaEmbedding(torch.autograd.Function):
     the GPU then idles while the host issues the optimizer and the next forward (about 0.45 ms
     of a 10.5 ms small-GPT step).  Here the token table's gradient is one GEMM on cuda_fma,
     onehot(tokens)^T . dy, summed in a fixed order (deterministic), when the one-hot matrix is
-    small (vocab x tokens <= ONEHOT_LIMIT floats); larger vocabularies take torch's embedding
-    backward.  The position table's gradient is dy summed over the batch (zero rows past T).
+    small and cheap (vocab x tokens <= ONEHOT_LIMIT floats and 2 vocab tokens width <=
+    ONEHOT_FLOP_LIMIT: about 40 us of GEMM, well under the stall it removes); larger vocabularies
+    take torch's embedding backward.  The position table's gradient is dy summed over the batch (zero rows past T).
     """
 
     ONEHOT_LIMIT = 1 << 26
+    ONEHOT_FLOP_LIMIT = 4e9
 
     @staticmethod
     def forward(ctx, tokens, wte, wpe):
@@ -303,7 +305,8 @@ class CudaEmbedding(torch.autograd.Function):
         ids = tokens.reshape(-1).to(torch.int64)  # int32 ids too, as nn.Embedding takes
         dwte = dwpe = None
         if ctx.needs_input_grad[1]:
-            if V * ids.numel() <= CudaEmbedding.ONEHOT_LIMIT:
+            if (V * ids.numel() <= CudaEmbedding.ONEHOT_LIMIT
+                    and 2.0 * V * ids.numel() * C <= CudaEmbedding.ONEHOT_FLOP_LIMIT):
                 onehot = torch.zeros(V, ids.numel(), dtype=dy.dtype, device=dy.device)
                 onehot.scatter_(0, ids.view(1, -1), 1.0)
                 dwte = cuda_fma(onehot.unsqueeze(0), dy, _zeros(C, dy)).view(V, C)

@@ -62,6 +62,41 @@ def test_noalloc_bwd_matches_bwd_twice(cuda):
             assert_rel_err(f64(g), r, 1e-3)
 
 
+def test_noalloc_bwd_in_a_hip_graph(cuda):
+    """One allocation-free backward captured in a HIP graph, after an eager call has resolved the
+    library's device array on this device, then replayed twice with eager work between the
+    replays: every replay equals the eager result bit for bit."""
+    from cuda_transformer.ops import flash_attention_fwd
+    from cuda_transformer_amd import capi
+
+    B, nh, T, hs, causal = 2, 4, 300, 64, True
+    q, k, v, do = _inputs(B, nh, T, hs, 700, cuda)
+    O, L = flash_attention_fwd(q, k, v, causal)
+    s4, s3 = capi.strides(q.stride()), capi.strides(L.stride())
+    grads = [torch.empty_like(q) for _ in range(3)]
+
+    def call():
+        capi.call("cta_flash_attention_bwd_noalloc", q.data_ptr(), s4, k.data_ptr(), s4,
+                  v.data_ptr(), s4, O.data_ptr(), s4, do.data_ptr(), s4, L.data_ptr(), s3, B, nh,
+                  T, hs, int(causal), *(g.data_ptr() for g in grads),
+                  torch.cuda.current_stream().cuda_stream)
+
+    call()
+    torch.cuda.synchronize()
+    eager = [g.clone() for g in grads]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for rep in range(2):
+        for g in grads:
+            g.fill_(float("nan"))
+        flash_attention_fwd(q, k, v, causal)  # eager work between the replays
+        graph.replay()
+        torch.cuda.synchronize()
+        for g, e in zip(grads, eager):
+            assert torch.equal(g, e), f"replay {rep} differs from the eager call"
+
+
 def test_noalloc_bwd_rejects_too_many_rows(cuda):
     from cuda_transformer_amd import capi
 
