@@ -34,6 +34,9 @@ SIGNATURES = {
                                        _p, _i64, _p]),
     "cta_flash_attention_fwd_strided": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64,
                                                _i64, _int, _p, _i64p, _p, _p]),
+    "cta_flash_attention_fwd_workspace": (_i64, [_i64, _i64, _i64, _i64, _int]),
+    "cta_flash_attention_fwd_ex": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64,
+                                          _int, _p, _i64p, _p, _p, _i64, _p]),
     "cta_flash_attention_bwd_strided": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p,
                                                _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _int,
                                                _p, _i64p, _p, _i64p, _p, _i64p, _p, _p, _i64,

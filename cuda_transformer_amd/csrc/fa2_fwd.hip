@@ -40,12 +40,16 @@ template <> struct FwdTile<32> { static constexpr int BN = 32; static constexpr 
 template <> struct FwdTile<64> { static constexpr int BN = 32; static constexpr int MINW = 2; };
 template <> struct FwdTile<128> { static constexpr int BN = 32; static constexpr int MINW = 1; };
 
-template <int HS, bool CAUSAL, int WAVES = 4>
+// SPLIT: each work item (query-tile pair, or tile) is run by two workgroups, part 0 and part 1,
+// each over one half of the item's K/V stages (in the item's stage order, across its passes).
+// Each writes its half's normalised O and L = m + ln l (O = 0, L = -inf where it saw no key):
+// part 0 into O / L, part 1 densely into Os / Ls; fa2_fwd_merge_kernel then combines them.
+template <int HS, bool CAUSAL, int WAVES = 4, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ L, int nh, int T, int BH, int n_qtiles,
     RowStrides sq, RowStrides sk, RowStrides sv, RowStrides so, float scale, float scale_log2,
-    float rescale_gap) {
+    float rescale_gap, float* __restrict__ Os = nullptr, float* __restrict__ Ls = nullptr) {
   constexpr int BN = FwdTile<HS>::BN;
   constexpr int THREADS = 64 * WAVES;
   constexpr int BM = 32 * WAVES;  // query rows per workgroup, 32 per wave
@@ -65,10 +69,13 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   // Work items are head-major and spread over XCDs.  Causal: one item = the query-tile pair
   // (n-1-p, p), so every item costs n+1 tile units and the dynamic dispatch has no tail.
   const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
-  const int w = xcd_work_item(blockIdx.x, BH * per_head);
-  if (w >= BH * per_head) return;
-  const int bh = w / per_head;
-  const int p = w - bh * per_head;
+  const int n_items = BH * per_head * (SPLIT ? 2 : 1);
+  const int w = xcd_work_item(blockIdx.x, n_items);
+  if (w >= n_items) return;
+  const int item = SPLIT ? w >> 1 : w;
+  const int part = SPLIT ? w & 1 : 0;  // the two parts of an item are neighbours: one XCD
+  const int bh = item / per_head;
+  const int p = item - bh * per_head;
   const int b = bh / nh, h = bh - b * nh;
 
   const float* Qb = Q + b * sq.b + h * sq.h;
@@ -76,8 +83,20 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   const float* Vb = V + b * sv.b + h * sv.h;
 
   const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
+  auto qt_of = [&](int pass) { return CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p; };
+  auto stages_of = [&](int qt) {
+    return ((CAUSAL ? min(T, (qt + 1) * BM) : T) + BN - 1) / BN;
+  };
+  // SPLIT: this part's positions [g0, g1) in the item's list of stages (pass 0's, then pass 1's).
+  int g0 = 0, g1 = 0, pos = 0;
+  if constexpr (SPLIT) {
+    int total = 0;
+    for (int pass = 0; pass < n_pass; ++pass) total += stages_of(qt_of(pass));
+    g0 = part ? (total + 1) / 2 : 0;
+    g1 = part ? total : (total + 1) / 2;
+  }
   for (int pass = 0; pass < n_pass; ++pass) {
-  const int qt = CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p;
+  const int qt = qt_of(pass);
   const int i0 = qt * BM + wave * 32;  // first query row of this wave
   const int my_i = i0 + col;           // query row owned by this lane
 
@@ -107,8 +126,11 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   // reference's expf(S - m) is (flash_attention.cuh:130-134).  Wave-uniform.
   bool wide = false;
 
-  const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
-  const int n_stages = (kv_end + BN - 1) / BN;
+  const int n_stages = stages_of(qt);
+  // the stages [i_begin, i_end) of this pass that this part runs (all of them unless SPLIT)
+  const int i_begin = SPLIT ? min(max(g0 - pos, 0), n_stages) : 0;
+  const int i_end = SPLIT ? min(max(g1 - pos, 0), n_stages) : n_stages;
+  pos += n_stages;
 
   float4 kst[LOADS], vst[LOADS];
   // K/V rows of a stage through buffer resources over its valid rows (scalar base and extent;
@@ -144,14 +166,16 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   // start), so the workgroups of a head share each K/V stage in L2.
   const bool down = CAUSAL && pass == 1;
   auto stage_at = [&](int i) { return down ? n_stages - 1 - i : i; };
-  gload(stage_at(0));
-  lstore(0);
+  if (i_begin < i_end) {  // workgroup-uniform
+    gload(stage_at(i_begin));
+    lstore(0);
+  }
   __syncthreads();
 
-  for (int i = 0; i < n_stages; ++i) {
+  for (int i = i_begin; i < i_end; ++i) {
     const int s = stage_at(i);
-    const int buf = i & 1;
-    if (i + 1 < n_stages) gload(stage_at(i + 1));
+    const int buf = (i - i_begin) & 1;
+    if (i + 1 < i_end) gload(stage_at(i + 1));
     const float* ks = smem + buf * (KTILE + VTILE);
     const float* vs = ks + KTILE;
 
@@ -215,37 +239,120 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
       }
     }
 
-    if (i + 1 < n_stages) lstore(buf ^ 1);
+    if (i + 1 < i_end) lstore(buf ^ 1);
     __syncthreads();
   }
 
   const float l_tot = sum_halves(l_run);
   if (my_i < T) {
-    float* op = O + b * so.b + h * so.h + (int64_t)my_i * so.t;
+    if constexpr (SPLIT) {
+      // A part may have seen no key of this row (l = 0): O = 0, L = -inf, which the merge
+      // weighs by e^{-inf} = 0.
+      const bool seen = l_tot > 0.0f;
+      const float inv = seen ? 1.0f / l_tot : 0.0f;
+      float* op = part ? Os + ((int64_t)bh * T + my_i) * HS
+                       : O + b * so.b + h * so.h + (int64_t)my_i * so.t;
 #pragma unroll
-    for (int d = 0; d < HS / 32; ++d) {
+      for (int d = 0; d < HS / 32; ++d) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int dc = d * 32 + 8 * g + 4 * half;
-        st4(op + dc, make_float4(oacc[d][4 * g + 0] / l_tot, oacc[d][4 * g + 1] / l_tot,
-                                 oacc[d][4 * g + 2] / l_tot, oacc[d][4 * g + 3] / l_tot));
+        for (int g = 0; g < 4; ++g) {
+          const int dc = d * 32 + 8 * g + 4 * half;
+          st4(op + dc, make_float4(oacc[d][4 * g + 0] * inv, oacc[d][4 * g + 1] * inv,
+                                   oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv));
+        }
       }
+      if (half == 0)
+        (part ? Ls : L)[(int64_t)bh * T + my_i] = seen ? m_run * scale + logf(l_tot) : -INFINITY;
+    } else {
+      float* op = O + b * so.b + h * so.h + (int64_t)my_i * so.t;
+#pragma unroll
+      for (int d = 0; d < HS / 32; ++d) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int dc = d * 32 + 8 * g + 4 * half;
+          st4(op + dc, make_float4(oacc[d][4 * g + 0] / l_tot, oacc[d][4 * g + 1] / l_tot,
+                                   oacc[d][4 * g + 2] / l_tot, oacc[d][4 * g + 3] / l_tot));
+        }
+      }
+      if (half == 0) L[(int64_t)bh * T + my_i] = m_run * scale + logf(l_tot);
     }
-    if (half == 0) L[(int64_t)bh * T + my_i] = m_run * scale + logf(l_tot);
   }
   }  // pass: the K/V loop ended on a barrier, so the next pass may refill LDS
+}
+
+// Merge of the two parts of a split forward, row by row in a fixed order (part 0, part 1):
+// L = ln(e^{L0} + e^{L1}), taken about their maximum, and O = e^{L0 - L} O0 + e^{L1 - L} O1;
+// part 0 in O / L (O through its strides), part 1 dense in Os / Ls.  HS / 4 lanes per row, one
+// float4 each.
+template <int HS>
+__global__ __launch_bounds__(256) void fa2_fwd_merge_kernel(float* __restrict__ O,
+                                                            float* __restrict__ L,
+                                                            const float* __restrict__ Os,
+                                                            const float* __restrict__ Ls, int nh,
+                                                            int T, int64_t rows, RowStrides so) {
+  constexpr int G = HS / 4;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / G;
+  if (row >= rows) return;
+  const int c4 = (int)(gid % G);
+  const int64_t bh = row / T;
+  const int t = (int)(row - bh * T);
+  const int64_t b = bh / nh, h = bh - b * nh;
+  const float l0 = L[row], l1 = Ls[row];
+  const float m = fmaxf(l0, l1);  // finite: every row sees key 0 in one of the parts
+  const float e0 = expf(l0 - m), e1 = expf(l1 - m);
+  const float inv = 1.0f / (e0 + e1);
+  const float w0 = e0 * inv, w1 = e1 * inv;
+  float* op = O + b * so.b + h * so.h + (int64_t)t * so.t + 4 * c4;
+  const float4 a = ld4(op), c = ld4(Os + row * HS + 4 * c4);
+  st4(op, make_float4(fmaf(w0, a.x, w1 * c.x), fmaf(w0, a.y, w1 * c.y), fmaf(w0, a.z, w1 * c.z),
+                      fmaf(w0, a.w, w1 * c.w)));
+  if (c4 == 0) L[row] = m + logf(e0 + e1);
+}
+
+// The forward splits each work item's K/V stages over two workgroups when its grid would hold
+// fewer than two waves per SIMD (1024 SIMDs) and a full row of keys gives each part at least
+// kSplitMinStages stages: the split doubles the waves in flight at the cost of the merge pass.
+// A/B in one process against the unsplit forward: B4 H4 N4096 causal 0.3306 -> 0.3042 ms
+// (+8.7%), B2 H4 N4096 non-causal +7.3%; at T = 256 (B64 H6, 8 stages per row) 30% slower,
+// the merge outweighing the work, hence the minimum.
+constexpr int kSimds = 1024;
+constexpr int kSplitMinStages = 16;
+
+template <int HS, bool CAUSAL>
+int fwd_waves(int T) {
+  return (HS == 64 && CAUSAL && T <= 512) ? 2 : 4;
+}
+
+template <int HS, bool CAUSAL>
+bool fwd_split(int T, int BH) {
+  const int waves = fwd_waves<HS, CAUSAL>(T);
+  const int n_qtiles = (T + 32 * waves - 1) / (32 * waves);
+  const int64_t items = (int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH;
+  return items * waves < 2 * kSimds && T / FwdTile<HS>::BN >= 2 * kSplitMinStages;
 }
 
 template <int HS, bool CAUSAL>
 void launch_fwd(const float* q, const float* k, const float* v, float* o, float* l, int nh,
                 int T, int BH, RowStrides sq, RowStrides sk, RowStrides sv, RowStrides so,
-                float scale, hipStream_t stream) {
+                float scale, hipStream_t stream, float* split_ws = nullptr) {
   auto run = [&]<int WAVES>() {
     const int n_qtiles = (T + 32 * WAVES - 1) / (32 * WAVES);
-    const unsigned grid = xcd_grid((int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH);
-    hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL, WAVES>), dim3(grid), dim3(64 * WAVES), 0,
-                       stream, q, k, v, o, l, nh, T, BH, n_qtiles, sq, sk, sv, so, scale,
-                       scale * kLog2e, 8.0f / (scale * kLog2e));
+    const int64_t items = (int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH;
+    if (split_ws != nullptr) {
+      float* Os = split_ws;
+      float* Ls = split_ws + (int64_t)BH * T * HS;
+      hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL, WAVES, true>), dim3(xcd_grid(2 * items)),
+                         dim3(64 * WAVES), 0, stream, q, k, v, o, l, nh, T, BH, n_qtiles, sq, sk,
+                         sv, so, scale, scale * kLog2e, 8.0f / (scale * kLog2e), Os, Ls);
+      const int64_t rows = (int64_t)BH * T;
+      hipLaunchKernelGGL((fa2_fwd_merge_kernel<HS>), dim3((unsigned)((rows * (HS / 4) + 255) / 256)),
+                         dim3(256), 0, stream, o, l, Os, Ls, nh, T, rows, so);
+      return;
+    }
+    hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL, WAVES>), dim3(xcd_grid(items)),
+                       dim3(64 * WAVES), 0, stream, q, k, v, o, l, nh, T, BH, n_qtiles, sq, sk,
+                       sv, so, scale, scale * kLog2e, 8.0f / (scale * kLog2e));
   };
   // Short causal heads (hs 64, T <= 512) run two waves (64 query rows) per workgroup: fewer
   // waves idle at each K/V stage's barrier along the diagonal, and the query-tile pairs balance
@@ -283,12 +390,39 @@ int check_attn_sizes(int64_t B, int64_t nh, int64_t T, int64_t hs) {
 
 using namespace cta;
 
-extern "C" int cta_flash_attention_fwd_strided(const float* q, const int64_t* q_strides,
-                                               const float* k, const int64_t* k_strides,
-                                               const float* v, const int64_t* v_strides,
-                                               int64_t B, int64_t nh, int64_t T, int64_t hs,
-                                               int causal, float* o, const int64_t* o_strides,
-                                               float* l, void* stream) {
+namespace {
+template <typename F>
+void dispatch_fwd(int64_t hs, int causal, F&& f) {
+  if (hs == 32) {
+    if (causal) f.template operator()<32, true>();
+    else f.template operator()<32, false>();
+  } else if (hs == 64) {
+    if (causal) f.template operator()<64, true>();
+    else f.template operator()<64, false>();
+  } else {
+    if (causal) f.template operator()<128, true>();
+    else f.template operator()<128, false>();
+  }
+}
+}  // namespace
+
+extern "C" int64_t cta_flash_attention_fwd_workspace(int64_t B, int64_t nh, int64_t T,
+                                                     int64_t hs, int causal) {
+  if (B <= 0 || nh <= 0 || T <= 0 || (hs != 32 && hs != 64 && hs != 128) ||
+      B * nh > ((int64_t)1 << 24) || T > ((int64_t)1 << 24))
+    return 0;
+  bool split = false;
+  dispatch_fwd(hs, causal, [&]<int HS, bool C>() { split = fwd_split<HS, C>((int)T, (int)(B * nh)); });
+  return split ? B * nh * T * (hs + 1) * (int64_t)sizeof(float) : 0;
+}
+
+extern "C" int cta_flash_attention_fwd_ex(const float* q, const int64_t* q_strides,
+                                          const float* k, const int64_t* k_strides,
+                                          const float* v, const int64_t* v_strides, int64_t B,
+                                          int64_t nh, int64_t T, int64_t hs, int causal,
+                                          float* o, const int64_t* o_strides, float* l,
+                                          void* workspace, int64_t workspace_bytes,
+                                          void* stream) {
   if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
   if (B * nh * T == 0) return CTA_OK;
   if (!o || !l) return fail(CTA_ERR_INVALID_ARGUMENT, "null output pointer");
@@ -297,21 +431,34 @@ extern "C" int cta_flash_attention_fwd_strided(const float* q, const int64_t* q_
     return fail(CTA_ERR_LAYOUT,
                 "flash_attention_fwd needs unit d-stride, strides divisible by 4, time strides below 2^23 and 16-byte "
                 "aligned Q/K/V/O");
+  const int64_t need = cta_flash_attention_fwd_workspace(B, nh, T, hs, causal);
+  float* split_ws = nullptr;
+  if (need > 0 && workspace != nullptr && workspace_bytes >= need) {
+    if (!aligned16(workspace))
+      return fail(CTA_ERR_LAYOUT, "the workspace must be a 16-byte aligned pointer");
+    split_ws = static_cast<float*>(workspace);
+  }
   const RowStrides sq{q_strides[0], q_strides[1], q_strides[2]};
   const RowStrides sk{k_strides[0], k_strides[1], k_strides[2]};
   const RowStrides sv{v_strides[0], v_strides[1], v_strides[2]};
   const RowStrides so{o_strides[0], o_strides[1], o_strides[2]};
   const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
-  const int BH = (int)(B * nh);
   hipStream_t st = as_stream(stream);
-#define CTA_FWD(HS_)                                                                           \
-  if (causal) launch_fwd<HS_, true>(q, k, v, o, l, (int)nh, (int)T, BH, sq, sk, sv, so, scale, st); \
-  else launch_fwd<HS_, false>(q, k, v, o, l, (int)nh, (int)T, BH, sq, sk, sv, so, scale, st);
-  if (hs == 32) { CTA_FWD(32) }
-  else if (hs == 64) { CTA_FWD(64) }
-  else { CTA_FWD(128) }
-#undef CTA_FWD
+  dispatch_fwd(hs, causal, [&]<int HS, bool C>() {
+    launch_fwd<HS, C>(q, k, v, o, l, (int)nh, (int)T, (int)(B * nh), sq, sk, sv, so, scale, st,
+                      split_ws);
+  });
   return check_launch("flash_attention_fwd");
+}
+
+extern "C" int cta_flash_attention_fwd_strided(const float* q, const int64_t* q_strides,
+                                               const float* k, const int64_t* k_strides,
+                                               const float* v, const int64_t* v_strides,
+                                               int64_t B, int64_t nh, int64_t T, int64_t hs,
+                                               int causal, float* o, const int64_t* o_strides,
+                                               float* l, void* stream) {
+  return cta_flash_attention_fwd_ex(q, q_strides, k, k_strides, v, v_strides, B, nh, T, hs,
+                                    causal, o, o_strides, l, nullptr, 0, stream);
 }
 
 extern "C" int cta_flash_attention_fwd(const float* q, const int64_t* q_strides, const float* k,

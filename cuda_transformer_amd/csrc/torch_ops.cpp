@@ -578,6 +578,23 @@ std::tuple<at::Tensor, at::Tensor> flash_attention_fwd_half(const at::Tensor& Q,
   return {O, L};
 }
 
+// Scratch with which the FP32 forward splits a small grid's work over twice the workgroups
+// (cta_flash_attention_fwd_workspace; none for grids that fill the GPU).  If the allocator
+// cannot supply it, the forward runs unsplit (ws_bytes = 0): same results to rounding.
+at::Tensor fwd_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs, bool causal,
+                         const at::TensorOptions& opts, int64_t& ws_bytes) {
+  ws_bytes = cta_flash_attention_fwd_workspace(B, nh, T, hs, causal ? 1 : 0);
+  at::Tensor ws;
+  if (ws_bytes > 0) {
+    try {
+      ws = at::empty({ws_bytes / static_cast<int64_t>(sizeof(float))}, opts);
+    } catch (const c10::OutOfMemoryError&) {
+      ws_bytes = 0;
+    }
+  }
+  return ws;
+}
+
 // cf. Transformer_launchers/flash_attn_launcher.cu:22-65
 std::tuple<at::Tensor, at::Tensor> flash_attention_fwd(at::Tensor Q, at::Tensor K, at::Tensor V,
                                                        bool causal) {
@@ -598,9 +615,14 @@ std::tuple<at::Tensor, at::Tensor> flash_attention_fwd(at::Tensor Q, at::Tensor 
     TORCH_CHECK(false, "Unsupported head dimension! Only hs=32, hs=64, and hs=128 are supported.");
   const at::Tensor q = attn_operand(Q), k = attn_operand(K), v = attn_operand(V);
   const auto qs = strides_of<4>(q), ks = strides_of<4>(k), vs = strides_of<4>(v);
-  check_rc(cta_flash_attention_fwd(q.data_ptr<float>(), qs.data(), k.data_ptr<float>(), ks.data(),
-                                   v.data_ptr<float>(), vs.data(), B, nh, T, hs, causal ? 1 : 0,
-                                   O.data_ptr<float>(), L.data_ptr<float>(), stream_of(Q)));
+  const int64_t os[4] = {nh * T * hs, T * hs, hs, 1};
+  int64_t ws_bytes = 0;
+  const at::Tensor ws = fwd_workspace(B, nh, T, hs, causal, Q.options(), ws_bytes);
+  check_rc(cta_flash_attention_fwd_ex(q.data_ptr<float>(), qs.data(), k.data_ptr<float>(),
+                                      ks.data(), v.data_ptr<float>(), vs.data(), B, nh, T, hs,
+                                      causal ? 1 : 0, O.data_ptr<float>(), os, L.data_ptr<float>(),
+                                      ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
+                                      stream_of(Q)));
   return {O, L};
 }
 
@@ -778,9 +800,12 @@ std::tuple<at::Tensor, at::Tensor> flash_attention_qkv_fwd(at::Tensor qkv, int64
   const float* p = x.data_ptr<float>();
   const int64_t xs[4] = {x.stride(0), hs, x.stride(1), 1};  // one column block as (B, nh, T, hs)
   const int64_t os[4] = {T * C, hs, C, 1};
-  check_rc(cta_flash_attention_fwd_strided(p, xs, p + C, xs, p + 2 * C, xs, B, nh, T, hs,
-                                           causal ? 1 : 0, out.data_ptr<float>(), os,
-                                           L.data_ptr<float>(), stream_of(qkv)));
+  int64_t ws_bytes = 0;
+  const at::Tensor ws = fwd_workspace(B, nh, T, hs, causal, qkv.options(), ws_bytes);
+  check_rc(cta_flash_attention_fwd_ex(p, xs, p + C, xs, p + 2 * C, xs, B, nh, T, hs,
+                                      causal ? 1 : 0, out.data_ptr<float>(), os,
+                                      L.data_ptr<float>(), ws_bytes > 0 ? ws.data_ptr() : nullptr,
+                                      ws_bytes, stream_of(qkv)));
   return {out, L};
 }
 

@@ -437,3 +437,56 @@ def test_fa2_forward_huge_scores(cuda, causal):
     np.testing.assert_allclose(Lg[..., h], L_ref[..., h], rtol=1e-5, atol=0)
     np.testing.assert_allclose(Og[..., n, :], O_ref[..., n, :], rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(Lg[..., n], L_ref[..., n], rtol=1e-5, atol=1e-5)
+
+
+# Grids of fewer than two waves per SIMD: the B4 H4 N4096 share of one GPU of eight, the GPT
+# step's B64 H6 T256 (two-wave tiles), hs 32 and 128, non-causal, ragged T.
+SPLIT_SHAPES = [(4, 4, 4096, 64, True), (2, 4, 4096, 64, False), (64, 6, 256, 64, True),
+                (2, 4, 2048, 32, True), (1, 4, 1030, 128, True), (1, 8, 1100, 64, False),
+                (4, 32, 1024, 64, True)]
+
+
+@pytest.mark.parametrize("B,nh,T,hs,causal", SPLIT_SHAPES)
+def test_fa2_forward_split_small_grids(cuda, B, nh, T, hs, causal):
+    """The forward with its small-grid workspace (each item's K/V range over two workgroups and
+    a fixed-order log-sum-exp merge) against the unsplit forward (within rounding), against the
+    float64 oracle on two heads, and bitwise reproducible; the torch op takes the split path.
+    Shapes that do not split (T = 256, or grids that fill the GPU) ask for no workspace and run
+    the unsplit kernel bit for bit."""
+    from cuda_transformer.ops import flash_attention_fwd
+    from cuda_transformer_amd import capi
+
+    print(f"split forward B{B} H{nh} T{T} D{hs} causal={causal}", flush=True)
+    q, k, v, _ = (t.to(cuda) for t in _inputs(B, nh, T, hs, seed=6000 + T + hs))
+    nbytes = capi.call("cta_flash_attention_fwd_workspace", B, nh, T, hs, int(causal))
+    splits = T >= 1024 and (B, nh, T) != (4, 32, 1024)
+    assert nbytes == (B * nh * T * (hs + 1) * 4 if splits else 0)
+    ws = torch.empty(max(1, nbytes // 4), device=cuda)
+    s4 = capi.strides(q.stride())
+    st = torch.cuda.current_stream().cuda_stream
+
+    def run(with_ws):
+        O = torch.full_like(q, float("nan"))
+        L = torch.full((B, nh, T), float("nan"), device=cuda)
+        capi.call("cta_flash_attention_fwd_ex", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(),
+                  s4, B, nh, T, hs, int(causal), O.data_ptr(), s4, L.data_ptr(),
+                  ws.data_ptr() if with_ws else None, nbytes if with_ws else 0, st)
+        return O, L
+
+    Os, Ls = run(True)
+    Os2, Ls2 = run(True)
+    Ou, Lu = run(False)
+    Oop, Lop = flash_attention_fwd(q, k, v, causal)
+    torch.cuda.synchronize()
+    assert torch.equal(Os, Os2) and torch.equal(Ls, Ls2)
+    assert torch.equal(Oop, Os) and torch.equal(Lop, Ls)
+    if splits:
+        torch.testing.assert_close(Os, Ou, rtol=1e-5, atol=2e-6)
+        torch.testing.assert_close(Ls, Lu, rtol=1e-6, atol=2e-6)
+    else:
+        assert torch.equal(Os, Ou) and torch.equal(Ls, Lu)
+    for b, h in ((0, 0), (B - 1, nh - 1)):
+        O_ref, L_ref = ora.reference_attention(f64(q[b:b + 1, h:h + 1]), f64(k[b:b + 1, h:h + 1]),
+                                               f64(v[b:b + 1, h:h + 1]), causal)
+        np.testing.assert_allclose(f64(Os[b:b + 1, h:h + 1]), O_ref, rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(f64(Ls[b:b + 1, h:h + 1]), L_ref, rtol=1e-5, atol=1e-5)
