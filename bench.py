@@ -319,21 +319,29 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_re
     delta = torch.empty(B, H, N, device=dev)
     ws_full = capi.lib().cta_flash_attention_bwd_workspace(B, H, N, D, int(causal))
     ws_bytes = min(ws_full, BWD_WORKSPACE_CAP) if schedule in ("stored", "fold") else 0
+    # small grids: the operator's split dK/dV stage (its partial sums after the dS tiles) and
+    # split forward, as flash_attention_fwd / flash_attention_bwd run them
+    split_bytes = (capi.lib().cta_flash_attention_bwd_split_workspace(B, H, N, D, int(causal))
+                   if schedule == "stored" and ws_bytes == ws_full else 0)
+    ws_bytes += split_bytes
     ws = torch.empty(max(1, ws_bytes // 4), device=dev)
+    fwd_ws_bytes = capi.lib().cta_flash_attention_fwd_workspace(B, H, N, D, int(causal))
+    fwd_ws = torch.empty(max(1, fwd_ws_bytes // 4), device=dev)
 
     stream = torch.cuda.current_stream(dev)
     st = ctypes.c_void_p(stream.cuda_stream)
     s4 = capi.strides(q.stride())
     s3 = capi.strides(L.stride())
     P = {name: ctypes.c_void_p(t.data_ptr()) for name, t in
-         dict(q=q, k=k, v=v, do=do, O=O, L=L, dq=dq, dk=dk, dv=dv, delta=delta, ws=ws).items()}
+         dict(q=q, k=k, v=v, do=do, O=O, L=L, dq=dq, dk=dk, dv=dv, delta=delta, ws=ws,
+              fws=fwd_ws).items()}
     lib = capi.lib()
     c = int(causal)
 
     def launch(kernel):
         if kernel == "fwd":
-            rc = lib.cta_flash_attention_fwd(P["q"], s4, P["k"], s4, P["v"], s4, B, H, N, D, c,
-                                             P["O"], P["L"], st)
+            rc = lib.cta_flash_attention_fwd_ex(P["q"], s4, P["k"], s4, P["v"], s4, B, H, N, D, c,
+                                                P["O"], s4, P["L"], P["fws"], fwd_ws_bytes, st)
         elif kernel == "delta":
             rc = lib.cta_flash_attention_bwd_delta(P["O"], s4, P["do"], s4, B, H, N, D,
                                                    P["delta"], st)
@@ -367,7 +375,7 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_re
         kernels = ["fwd", "delta", "dq", "dkdv"]
     elif schedule == "fold":
         kernels = ["fwd", "bwd_fold"]
-    elif ws_full <= ws_bytes:
+    elif ws_full <= ws_bytes and split_bytes == 0:
         kernels = ["fwd", "delta", "dkdv", "dq_ds"]
     else:
         kernels = ["fwd", "bwd"]

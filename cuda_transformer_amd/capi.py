@@ -29,6 +29,7 @@ SIGNATURES = {
     "cta_flash_attention_fwd_bf16": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64,
                                             _i64, _int, _p, _p, _p]),
     "cta_flash_attention_bwd_workspace": (_i64, [_i64, _i64, _i64, _i64, _int]),
+    "cta_flash_attention_bwd_split_workspace": (_i64, [_i64, _i64, _i64, _i64, _int]),
     "cta_flash_attention_bwd": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
                                        _p, _i64p, _i64, _i64, _i64, _i64, _int, _p, _p, _p, _p,
                                        _p, _i64, _p]),

@@ -283,14 +283,20 @@ constexpr int kDsPitch = 40;  // LDS pitch of the per-wave transpose: halves 4 r
 // the stage's dO tile and an O tile streamed beside it (delta_i = O_i . dO_i, the reference's
 // flash_attention_bwd_delta, flash_attention.cuh:175-213, folded in).  Every key tile of a head
 // recomputes it, and the stage needs a second barrier before delta is read.
-template <int HS, bool CAUSAL, bool STORE_DS, bool FOLD, int WAVES = 4>
+//
+// SPLIT: each work item (key-tile pair, or tile) is run by two workgroups, part 0 and part 1,
+// each over one half of the item's query stages (in the item's stage order, across its passes);
+// every dS tile is still stored once, by the part that forms it.  Part 0 writes its partial dK
+// and dV to dK / dV, part 1 densely to part_ws (dK, then dV, of all BH heads); zeros where a
+// part saw no query stage.  fa2_bwd_dkdv_sum_kernel then adds part 1 to part 0.
+template <int HS, bool CAUSAL, bool STORE_DS, bool FOLD, int WAVES = 4, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ O, const float* __restrict__ Lg,
     const float* __restrict__ delta, float* __restrict__ dK, float* __restrict__ dV,
     float* __restrict__ dsw, int nh, int T, int bh_base, int BH, int n_ktiles, RowStrides sq,
     RowStrides sk, RowStrides sv, RowStrides sdo, RowStrides so, LStrides sl, RowStrides sdk,
-    RowStrides sdv, float scale, float scale_log2) {
+    RowStrides sdv, float scale, float scale_log2, float* __restrict__ part_ws = nullptr) {
   constexpr int BN = DkdvTile<HS>::BN;
   constexpr int NSUB = BN / 32;
   constexpr int THREADS = 64 * WAVES;
@@ -314,10 +320,13 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
   const int half = lane >> 5, col = lane & 31;
   // Head-major items over XCDs; causal items are key-tile pairs (p, n-1-p) of equal cost.
   const int per_head = CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles;
-  const int w = xcd_work_item(blockIdx.x, BH * per_head);
-  if (w >= BH * per_head) return;
-  const int bh_local = w / per_head;
-  const int p = w - bh_local * per_head;
+  const int n_items = BH * per_head * (SPLIT ? 2 : 1);
+  const int w = xcd_work_item(blockIdx.x, n_items);
+  if (w >= n_items) return;
+  const int item = SPLIT ? w >> 1 : w;
+  const int part = SPLIT ? w & 1 : 0;  // the two parts of an item are neighbours: one XCD
+  const int bh_local = item / per_head;
+  const int p = item - bh_local * per_head;
   const int bh = bh_base + bh_local;
   const int b = bh / nh, h = bh - b * nh;
 
@@ -350,8 +359,20 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
   __syncthreads();
 
   const int n_pass = (CAUSAL && n_ktiles - 1 - p != p) ? 2 : 1;
+  auto kt_of = [&](int pass) { return CAUSAL ? (pass == 0 ? p : n_ktiles - 1 - p) : p; };
+  const int n_stages = (T + BN - 1) / BN;
+  // first query stage that can see the keys of tile kt
+  auto q_begin_of = [&](int kt) { return CAUSAL ? (kt * BM / BN) : 0; };
+  // SPLIT: this part's positions [g0, g1) in the item's list of steps (pass 0's, then pass 1's).
+  int g0 = 0, g1 = 0, pos = 0;
+  if constexpr (SPLIT) {
+    int total = 0;
+    for (int pass = 0; pass < n_pass; ++pass) total += n_stages - q_begin_of(kt_of(pass));
+    g0 = part ? (total + 1) / 2 : 0;
+    g1 = part ? total : (total + 1) / 2;
+  }
   for (int pass = 0; pass < n_pass; ++pass) {
-  const int kt = CAUSAL ? (pass == 0 ? p : n_ktiles - 1 - p) : p;
+  const int kt = kt_of(pass);
   const int j0 = kt * BM + wave * 32;  // first key row of this wave
   const int my_j = j0 + col;
 
@@ -375,8 +396,7 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
 #pragma unroll
   for (int d = 0; d < HS / 32; ++d) { dkacc[d] = zero16(); dvacc[d] = zero16(); }
 
-  const int q_begin = CAUSAL ? (kt * BM / BN) : 0;  // first query stage that can see these keys
-  const int n_stages = (T + BN - 1) / BN;
+  const int q_begin = q_begin_of(kt);
   const bool wave_stores = STORE_DS && j0 < T;
 
   // Async copies of stage `stage` into buffer `buf`.  Piece pc covers floats
@@ -453,17 +473,21 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
   // reads stage t - 4 (t counted from the item's start): the workgroups of a head share each
   // streamed Q / dO stage in L2 instead of each reading it at a different time.
   const int n_steps = n_stages - q_begin;
+  // the steps [i_begin, i_end) of this pass that this part runs (all of them unless SPLIT)
+  const int i_begin = SPLIT ? min(max(g0 - pos, 0), n_steps) : 0;
+  const int i_end = SPLIT ? min(max(g1 - pos, 0), n_steps) : n_steps;
+  pos += n_steps;
   const bool down = CAUSAL && pass == 0;
   auto stage_at = [&](int i) { return down ? n_stages - 1 - i : q_begin + i; };
-  if (n_steps > 0) issue(stage_at(0), 0);
+  if (i_begin < i_end) issue(stage_at(i_begin), 0);
   vm_wait_all();
   __syncthreads();
 
-  for (int i = 0; i < n_steps; ++i) {
+  for (int i = i_begin; i < i_end; ++i) {
     const int s = stage_at(i);
-    const int buf = i & 1;
-    if (i + 1 < n_steps) issue(stage_at(i + 1), buf ^ 1);
-    if (wave_stores && i > 0) flush(stage_at(i - 1));
+    const int buf = (i - i_begin) & 1;
+    if (i + 1 < i_end) issue(stage_at(i + 1), buf ^ 1);
+    if (wave_stores && i > i_begin) flush(stage_at(i - 1));
     if (FOLD) {
       fold_delta(smem + buf * STAGE);
       __syncthreads();
@@ -578,11 +602,15 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
     vm_wait_all();
     __syncthreads();
   }
-  if (wave_stores && n_steps > 0) flush(stage_at(n_steps - 1));
+  if (wave_stores && i_end > i_begin) flush(stage_at(i_end - 1));
 
   if (my_j < T) {
     float* kp = dK + b * sdk.b + h * sdk.h + (int64_t)my_j * sdk.t;
     float* vp = dV + b * sdv.b + h * sdv.h + (int64_t)my_j * sdv.t;
+    if (SPLIT && part) {
+      kp = part_ws + ((int64_t)bh * T + my_j) * HS;
+      vp = kp + (int64_t)(bh_base + BH) * T * HS;
+    }
 #pragma unroll
     for (int d = 0; d < HS / 32; ++d) {
 #pragma unroll
@@ -596,6 +624,31 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
     }
   }
   }  // pass: the stage loop ended on a barrier, so the next pass may refill LDS
+}
+
+// dK += part 1's dK, dV += part 1's dV, row by row in a fixed order (part 0, then part 1), after
+// a split dK/dV stage; dK / dV through their strides, part 1 dense in part_ws.  HS / 4 lanes
+// per row, one float4 each.
+template <int HS>
+__global__ __launch_bounds__(256) void fa2_bwd_dkdv_sum_kernel(float* __restrict__ dK,
+                                                               float* __restrict__ dV,
+                                                               const float* __restrict__ part_ws,
+                                                               int nh, int T, int64_t rows,
+                                                               RowStrides sdk, RowStrides sdv) {
+  constexpr int G = HS / 4;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / G;
+  if (row >= rows) return;
+  const int c4 = (int)(gid % G);
+  const int64_t bh = row / T;
+  const int t = (int)(row - bh * T);
+  const int64_t b = bh / nh, h = bh - b * nh;
+  float* kp = dK + b * sdk.b + h * sdk.h + (int64_t)t * sdk.t + 4 * c4;
+  float* vp = dV + b * sdv.b + h * sdv.h + (int64_t)t * sdv.t + 4 * c4;
+  const float4 a = ld4(kp), c = ld4(part_ws + row * HS + 4 * c4);
+  const float4 x = ld4(vp), y = ld4(part_ws + (rows + row) * HS + 4 * c4);
+  st4(kp, make_float4(a.x + c.x, a.y + c.y, a.z + c.z, a.w + c.w));
+  st4(vp, make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w));
 }
 
 // ------------------------------------------------------------------------------------
@@ -774,15 +827,28 @@ void launch_dq(const float* q, const float* k, const float* v, const float* d_o,
 // dK/dV for heads [bh_base, bh_base + n_heads), written through strides sdk / sdv; with
 // STORE_DS the dS tiles go to dsw; with FOLD delta comes from O (strides so) instead of the
 // delta array.  Four waves (128 keys) per workgroup, or two for short causal heads.
+// part_ws (heads [0, n_heads) with bh_base = 0 only): run the split form and its sum pass.
 template <int HS, bool CAUSAL, bool STORE_DS, bool FOLD = false>
 void launch_dkdv(const float* q, const float* k, const float* v, const float* d_o,
                  const float* l, const float* delta, float* dk, float* dv, float* dsw, int nh,
                  int T, int bh_base, int n_heads, RowStrides sq, RowStrides sk, RowStrides sv,
                  RowStrides sdo, LStrides sl, RowStrides sdk, RowStrides sdv, float scale,
-                 hipStream_t st, const float* o = nullptr, RowStrides so = {}) {
+                 hipStream_t st, const float* o = nullptr, RowStrides so = {},
+                 float* part_ws = nullptr) {
   auto run = [&]<int WAVES>() {
     const int n_ktiles = (T + 32 * WAVES - 1) / (32 * WAVES);
     const int64_t items = (int64_t)(CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles) * n_heads;
+    if (part_ws != nullptr) {
+      hipLaunchKernelGGL((fa2_bwd_dkdv_kernel<HS, CAUSAL, STORE_DS, FOLD, WAVES, true>),
+                         dim3(xcd_grid(2 * items)), dim3(64 * WAVES), 0, st, q, k, v, d_o, o, l,
+                         delta, dk, dv, dsw, nh, T, bh_base, n_heads, n_ktiles, sq, sk, sv, sdo,
+                         so, sl, sdk, sdv, scale, scale * kLog2e, part_ws);
+      const int64_t rows = (int64_t)n_heads * T;
+      hipLaunchKernelGGL((fa2_bwd_dkdv_sum_kernel<HS>),
+                         dim3((unsigned)((rows * (HS / 4) + 255) / 256)), dim3(256), 0, st, dk,
+                         dv, part_ws, nh, T, rows, sdk, sdv);
+      return;
+    }
     hipLaunchKernelGGL((fa2_bwd_dkdv_kernel<HS, CAUSAL, STORE_DS, FOLD, WAVES>),
                        dim3(xcd_grid(items)), dim3(64 * WAVES), 0, st, q, k, v, d_o, o, l, delta,
                        dk, dv, dsw, nh, T, bh_base, n_heads, n_ktiles, sq, sk, sv, sdo, so, sl,
@@ -823,6 +889,20 @@ void launch_dq_ds(const float* k, const float* dsw, float* dq, int nh, int T, in
     }
   }
   run.template operator()<4>();
+}
+
+// The stored-dS dK/dV stage splits each item's query stages over two workgroups when its grid
+// would hold fewer than two waves per SIMD (1024 SIMDs) and a full column of queries gives each
+// part at least kSplitMinStages stages (T >= 1024 at 32-row stages), as the forward does.
+constexpr int kSimds = 1024;
+constexpr int kSplitMinStages = 16;
+
+template <int HS, bool CAUSAL>
+bool dkdv_split(int T, int BH) {
+  const int waves = (HS == 64 && CAUSAL && T <= 1024) ? 2 : 4;
+  const int n_ktiles = (T + 32 * waves - 1) / (32 * waves);
+  const int64_t items = (int64_t)(CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles) * BH;
+  return items * waves < 2 * kSimds && T / DkdvTile<HS>::BN >= 2 * kSplitMinStages;
 }
 
 // Runs f.template operator()<HS, CAUSAL>() for the runtime head size and mask flag.
@@ -953,6 +1033,16 @@ extern "C" int64_t cta_flash_attention_bwd_workspace(int64_t B, int64_t nh, int6
   return B * nh * ds_tiles_per_head(T, causal != 0) * kDsTileFloats * (int64_t)sizeof(float);
 }
 
+extern "C" int64_t cta_flash_attention_bwd_split_workspace(int64_t B, int64_t nh, int64_t T,
+                                                           int64_t hs, int causal) {
+  if (B <= 0 || nh <= 0 || T <= 0 || (hs != 32 && hs != 64 && hs != 128) ||
+      B * nh > ((int64_t)1 << 24) || T > ((int64_t)1 << 24))
+    return 0;
+  bool split = false;
+  dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() { split = dkdv_split<HS, C>((int)T, (int)(B * nh)); });
+  return split ? 2 * B * nh * T * hs * (int64_t)sizeof(float) : 0;
+}
+
 extern "C" int cta_flash_attention_bwd_dkdv_store_ds(
     const float* q, const int64_t* q_strides, const float* k, const int64_t* k_strides,
     const float* v, const int64_t* v_strides, const float* d_o, const int64_t* do_strides,
@@ -1039,12 +1129,19 @@ extern "C" int cta_flash_attention_bwd_strided(
   const int chunk = (int)((BH + n_chunks - 1) / n_chunks);
   const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
   const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
+  // A small grid's dK/dV stage splits over twice the workgroups when the workspace also holds
+  // the split's partial sums after every head's dS tiles.
+  const int64_t ds_all = cta_flash_attention_bwd_workspace(B, nh, T, hs, causal);
+  const int64_t split = cta_flash_attention_bwd_split_workspace(B, nh, T, hs, causal);
+  float* part_ws = split > 0 && n_chunks == 1 && workspace_bytes >= ds_all + split
+                       ? workspace + ds_all / (int64_t)sizeof(float)
+                       : nullptr;
   for (int h0 = 0; h0 < BH; h0 += chunk) {
     const int n = std::min(chunk, BH - h0);
     dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
       launch_dkdv<HS, C, true>(q, k, v, d_o, l, delta, dk, dv, workspace, (int)nh, (int)T, h0, n,
                                rs(q_strides), rs(k_strides), rs(v_strides), rs(do_strides), sl,
-                               sdk, sdv, scale, st);
+                               sdk, sdv, scale, st, nullptr, {}, part_ws);
       launch_dq_ds<HS, C>(k, workspace, dq, (int)nh, (int)T, h0, n, rs(k_strides), sdq, scale,
                           st);
     });

@@ -632,8 +632,11 @@ std::tuple<at::Tensor, at::Tensor> flash_attention_fwd(at::Tensor Q, at::Tensor 
 // (ws_bytes = 0).
 at::Tensor bwd_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs, bool causal,
                          const at::TensorOptions& opts, int64_t& ws_bytes) {
-  ws_bytes = capped_workspace(cta_flash_attention_bwd_workspace(B, nh, T, hs, causal ? 1 : 0),
-                              cta_flash_attention_bwd_workspace(1, 1, T, hs, causal ? 1 : 0));
+  const int64_t full = cta_flash_attention_bwd_workspace(B, nh, T, hs, causal ? 1 : 0);
+  ws_bytes = capped_workspace(full, cta_flash_attention_bwd_workspace(1, 1, T, hs, causal ? 1 : 0));
+  // every head's dS tiles fit: room for a small grid's split dK/dV stage too
+  if (ws_bytes == full && full > 0)
+    ws_bytes += cta_flash_attention_bwd_split_workspace(B, nh, T, hs, causal ? 1 : 0);
   at::Tensor ws;
   if (ws_bytes > 0) {
     try {

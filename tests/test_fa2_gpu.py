@@ -490,3 +490,51 @@ def test_fa2_forward_split_small_grids(cuda, B, nh, T, hs, causal):
                                                f64(v[b:b + 1, h:h + 1]), causal)
         np.testing.assert_allclose(f64(Os[b:b + 1, h:h + 1]), O_ref, rtol=1e-5, atol=1e-5)
         np.testing.assert_allclose(f64(Ls[b:b + 1, h:h + 1]), L_ref, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("B,nh,T,hs,causal", [(4, 4, 4096, 64, True), (2, 4, 4096, 64, False),
+                                              (1, 4, 1030, 128, True), (2, 4, 2048, 32, True)])
+def test_fa2_bwd_split_small_grids(cuda, B, nh, T, hs, causal):
+    """The stored-dS backward with the small-grid split of its dK/dV stage (each key tile's query
+    stages over two workgroups, partial sums added in a fixed order), given the workspace for it,
+    against the same call without that room: dQ bitwise equal (the same dS tiles), dK and dV
+    within rounding; bitwise reproducible; the torch op runs the split; two heads against the
+    float64 oracle."""
+    from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+    from cuda_transformer_amd import capi
+
+    print(f"split dK/dV B{B} H{nh} T{T} D{hs} causal={causal}", flush=True)
+    q, k, v, do = (t.to(cuda) for t in _inputs(B, nh, T, hs, seed=6100 + T + hs,
+                                                do_kind="randn"))
+    O, L = flash_attention_fwd(q, k, v, causal)
+    full = capi.call("cta_flash_attention_bwd_workspace", B, nh, T, hs, int(causal))
+    extra = capi.call("cta_flash_attention_bwd_split_workspace", B, nh, T, hs, int(causal))
+    assert extra == 2 * B * nh * T * hs * 4
+    ws = torch.empty((full + extra) // 4, device=cuda)
+    s4, s3 = capi.strides(q.stride()), capi.strides(L.stride())
+    st = torch.cuda.current_stream().cuda_stream
+
+    def bwd(nbytes):
+        out = [torch.full_like(q, float("nan")) for _ in range(3)]
+        delta = torch.empty(B, nh, T, device=cuda)
+        capi.call("cta_flash_attention_bwd", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(), s4,
+                  O.data_ptr(), s4, do.data_ptr(), s4, L.data_ptr(), s3, B, nh, T, hs,
+                  int(causal), *(t.data_ptr() for t in out), delta.data_ptr(), ws.data_ptr(),
+                  nbytes, st)
+        return out
+
+    split, again, plain = bwd(full + extra), bwd(full + extra), bwd(full)
+    op = flash_attention_bwd(q, k, v, O, do, L, causal)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(split, again))
+    assert all(torch.equal(a, b) for a, b in zip(split, op))
+    assert torch.equal(split[0], plain[0])
+    for i in (1, 2):
+        torch.testing.assert_close(split[i], plain[i], rtol=1e-5, atol=1e-5)
+    for b, h in ((0, 0), (B - 1, nh - 1)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        refs = ora.fa2_backward(f64(q[sl]), f64(k[sl]), f64(v[sl]), f64(O[sl]), f64(do[sl]),
+                                f64(L[sl]), causal, br=512, bc=512)
+        for got, ref in zip(split, refs):
+            np.testing.assert_allclose(f64(got[sl]), ref, rtol=1e-5, atol=1e-4)
+            assert_rel_err(f64(got[sl]), ref, 1e-3)
