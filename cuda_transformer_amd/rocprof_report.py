@@ -39,7 +39,21 @@ wave states                 SQ_ACTIVE_INST_ANY (issuing), SQ_WAIT_ANY (waiting o
                             issued: pipe busy), SQ_WAIT_INST_LDS, and the issuing time by unit
                             (SQ_ACTIVE_INST_VALU / _LDS / _VMEM / _SCA / _MISC), each as a share
                             of SQ_WAVE_CYCLES (all in quad-cycles)
+memory / fetch latency      rocprofv3's derived metrics VmemLatency, LdsLatency and
+                            InstrFetchLatency: the in-flight instruction level (SQ_INST_LEVEL_VMEM,
+                            _LDS, SQ_IFETCH_LEVEL) accumulated every cycle over the instructions
+                            issued (SQ_INSTS_VMEM, _LDS, SQ_IFETCH), i.e. the mean cycles a
+                            vector-memory, LDS or instruction-fetch request is outstanding (one
+                            --pmc pass each)
 ==========================  =====================================================================
+
+The reference parser splits stalls into memory dependency, pipe busy, barrier and instruction
+fetch (parse_ncu_report.py:71-80).  Here: memory dependency = the dependency-wait share with the
+VMEM / LDS latencies beside it; pipe busy = the issue-wait share; instruction fetch =
+InstrFetchLatency.  gfx950's counter set has no barrier-wait counter (SQ_WAIT_ANY counts s_waitcnt
+and s_barrier waits together), and PC sampling, which would give per-reason stalls, is not
+available on the pool this was measured on; barrier waits are therefore measured with clock reads
+around the barrier in an instrumented build, not by this report.
 
 MFMA FLOPs count the FP32, BF16 and FP16 MOPS counters that were collected (512 FLOP each).
 The wave-state and occupancy figures are rocprofv3's counterparts of the reference parser's
@@ -80,6 +94,8 @@ WAVE_STATES = (("issue", "SQ_ACTIVE_INST_ANY"), ("dep_wait", "SQ_WAIT_ANY"),
                ("valu", "SQ_ACTIVE_INST_VALU"), ("lds", "SQ_ACTIVE_INST_LDS"),
                ("vmem", "SQ_ACTIVE_INST_VMEM"), ("salu", "SQ_ACTIVE_INST_SCA"),
                ("branch", "SQ_ACTIVE_INST_MISC"))
+# derived latency metrics (cycles), reported as they are
+LATENCIES = (("vmem", "VmemLatency"), ("lds", "LdsLatency"), ("ifetch", "InstrFetchLatency"))
 
 
 def _round_up(x: int, g: int) -> int:
@@ -307,6 +323,7 @@ class KernelRow:
     waves_limit: str | None = None
     waves_achieved: float | None = None
     wave_states: dict[str, float] = field(default_factory=dict)
+    latencies: dict[str, float] = field(default_factory=dict)
 
 
 def build_rows(trace=None, pmc=(), calib=None, agent=None, window=None,
@@ -378,6 +395,7 @@ def build_rows(trace=None, pmc=(), calib=None, agent=None, window=None,
                 r.intensity = r.mfma_flop / r.hbm_bytes
         if c.get("SQ_LDS_IDX_ACTIVE"):
             r.lds_conflict_rate = c.get("SQ_LDS_BANK_CONFLICT", 0.0) / c["SQ_LDS_IDX_ACTIVE"]
+        r.latencies = {key: c[ctr] for key, ctr in LATENCIES if ctr in c}
         rows.append(r)
     return rows
 
@@ -432,6 +450,15 @@ def render(rows: list[KernelRow], title: str, commands=(), calib=None, agent=Non
                 f"{pct(w.get('issue'))} | {pct(w.get('dep_wait'))} | {pct(w.get('issue_wait'))} | "
                 f"{pct(w.get('lds_issue_wait'))} | {pct(w.get('valu'))} | {pct(w.get('lds'))} | "
                 f"{pct(w.get('vmem'))} | {pct(w.get('salu'))} | {pct(w.get('branch'))} |")
+    lat = [r for r in rows if r.latencies]
+    if lat:
+        lines += ["", "Memory and instruction-fetch latency (mean cycles a request is outstanding):",
+                  "", "| kernel | VMEM latency | LDS latency | instruction-fetch latency |",
+                  "|---|---|---|---|"]
+        for r in lat:
+            lines.append(f"| {r.name} | {_fmt(r.latencies.get('vmem'), '.0f')} | "
+                         f"{_fmt(r.latencies.get('lds'), '.0f')} | "
+                         f"{_fmt(r.latencies.get('ifetch'), '.0f')} |")
     if window:
         lines += ["", "| kernel | all dispatches | mean ms over all |", "|---|---|---|"]
         lines += [f"| {r.name} | {r.info['all_calls']} | {r.info['all_avg_ms']:.4f} |"
@@ -452,6 +479,8 @@ def render(rows: list[KernelRow], title: str, commands=(), calib=None, agent=Non
             tail.append(f"waves_per_simd_achieved[{r.name}] = {r.waves_achieved:.3f}")
         for key, v in r.wave_states.items():
             tail.append(f"wave_state_{key}[{r.name}] = {v:.4f}")
+        for key, v in r.latencies.items():
+            tail.append(f"latency_{key}_cycles[{r.name}] = {v:.1f}")
     if tail:
         lines += ["", "Machine-readable:", "", "```", *tail, "```"]
     return "\n".join(lines) + "\n"

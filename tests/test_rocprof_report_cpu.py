@@ -227,3 +227,18 @@ def test_trace_window_per_step_matches_exact_names(tmp_path):
     assert win["fa2_bwd_dq_ds_kernel<64, true>"]["calls"] == 4
     win = rr.read_trace_window(d, 1, 2, {"fa2_bwd_dq": 2})  # a substring names nothing
     assert win["fa2_bwd_dq_kernel"]["calls"] == 2 and win["fa2_bwd_dq_ds_kernel<64, true>"]["calls"] == 2
+
+
+def test_latency_metrics_are_reported(tmp_path):
+    """rocprofv3's derived VmemLatency / LdsLatency / InstrFetchLatency (cycles), each from its
+    own --pmc pass, land in the latency table and the machine-readable tail as collected."""
+    lat_v = _pmc(tmp_path / "v", "v", [("k", "VmemLatency", 570.0), ("k", "VmemLatency", 590.0)])
+    lat_l = _pmc(tmp_path / "l", "l", [("k", "LdsLatency", 49.0)])
+    lat_i = _pmc(tmp_path / "i", "i", [("k", "InstrFetchLatency", 30.0), ("j", "InstrFetchLatency", 7.0)])
+    rows = rr.build_rows(pmc=[lat_v, lat_l, lat_i])
+    by = {r.name: r for r in rows}
+    assert by["k"].latencies == {"vmem": 580.0, "lds": 49.0, "ifetch": 30.0}
+    assert by["j"].latencies == {"ifetch": 7.0}
+    text = rr.render(rows, "T")
+    assert "| k | 580 | 49 | 30 |" in text and "| j | - | - | 7 |" in text
+    assert "latency_vmem_cycles[k] = 580.0" in text
