@@ -651,20 +651,44 @@ __global__ __launch_bounds__(256) void fa2_bwd_dkdv_sum_kernel(float* __restrict
   st4(vp, make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w));
 }
 
+// dQ += part 1's dQ, row by row (part 0, then part 1), after a split dQ-from-dS stage; dQ
+// through its strides, part 1 dense in part_ws.  HS / 4 lanes per row, one float4 each.
+template <int HS>
+__global__ __launch_bounds__(256) void fa2_bwd_dq_sum_kernel(float* __restrict__ dQ,
+                                                             const float* __restrict__ part_ws,
+                                                             int nh, int T, int64_t rows,
+                                                             RowStrides sdq) {
+  constexpr int G = HS / 4;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / G;
+  if (row >= rows) return;
+  const int c4 = (int)(gid % G);
+  const int64_t bh = row / T;
+  const int t = (int)(row - bh * T);
+  const int64_t b = bh / nh, h = bh - b * nh;
+  float* qp = dQ + b * sdq.b + h * sdq.h + (int64_t)t * sdq.t + 4 * c4;
+  const float4 a = ld4(qp), c = ld4(part_ws + row * HS + 4 * c4);
+  st4(qp, make_float4(a.x + c.x, a.y + c.y, a.z + c.z, a.w + c.w));
+}
+
 // ------------------------------------------------------------------------------------
 // dQ from stored dS tiles: dQ^T += K^T dS^T, one 32x32 tile per MFMA chain.  Workgroup =
 // 32 * WAVES query rows (WAVES = 4, or 2 for short causal heads).  K tiles of 64 rows go
 // global -> registers -> LDS, double
 // buffered; each wave streams its own dS tiles from the workspace straight into registers,
 // one stage ahead, as the B operand.  Heads [bh_base, bh_base + BH).
+// SPLIT (small grids, heads from 0): each item's key stages (pass 0's, then pass 1's) are
+// split over two workgroups, neighbours in the XCD order; part 0 writes dQ, part 1 its
+// partial dQ densely into part_ws, and fa2_bwd_dq_sum_kernel adds the two in that order.
 __device__ __forceinline__ float f4_at(const float4& v, int e) {
   return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
 }
 
-template <int HS, bool CAUSAL, int WAVES = 4>
+template <int HS, bool CAUSAL, int WAVES = 4, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WAVES, 2) void fa2_bwd_dq_ds_kernel(
     const float* __restrict__ K, const float* __restrict__ dsw, float* __restrict__ dQ, int nh,
-    int T, int bh_base, int BH, int n_qtiles, RowStrides sk, RowStrides sdq, float scale) {
+    int T, int bh_base, int BH, int n_qtiles, RowStrides sk, RowStrides sdq, float scale,
+    float* __restrict__ part_ws = nullptr) {
   constexpr int BN = 64;
   constexpr int NSUB = BN / 32;
   constexpr int THREADS = 64 * WAVES;
@@ -681,10 +705,13 @@ __global__ __launch_bounds__(64 * WAVES, 2) void fa2_bwd_dq_ds_kernel(
   const int half = lane >> 5, col = lane & 31;
   // Head-major items over XCDs; causal items are query-tile pairs (n-1-p, p) of equal cost.
   const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
-  const int w = xcd_work_item(blockIdx.x, BH * per_head);
-  if (w >= BH * per_head) return;
-  const int bh_local = w / per_head;
-  const int p = w - bh_local * per_head;
+  const int n_items = BH * per_head * (SPLIT ? 2 : 1);
+  const int w = xcd_work_item(blockIdx.x, n_items);
+  if (w >= n_items) return;
+  const int item = SPLIT ? w >> 1 : w;
+  const int part = SPLIT ? w & 1 : 0;
+  const int bh_local = item / per_head;
+  const int p = item - bh_local * per_head;
   const int bh = bh_base + bh_local;
   const int b = bh / nh, h = bh - b * nh;
   const float* Kb = K + b * sk.b + h * sk.h;
@@ -692,8 +719,21 @@ __global__ __launch_bounds__(64 * WAVES, 2) void fa2_bwd_dq_ds_kernel(
   const float* dsh = dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileFloats;
 
   const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
+  auto qt_of = [&](int pass) { return CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p; };
+  auto stages_of = [&](int qt) {
+    const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
+    return (kv_end + BN - 1) / BN;
+  };
+  // SPLIT: this part's positions [g0, g1) in the item's list of stages (pass 0's, then pass 1's).
+  int g0 = 0, g1 = 0, pos = 0;
+  if constexpr (SPLIT) {
+    int total = 0;
+    for (int pass = 0; pass < n_pass; ++pass) total += stages_of(qt_of(pass));
+    g0 = part ? (total + 1) / 2 : 0;
+    g1 = part ? total : (total + 1) / 2;
+  }
   for (int pass = 0; pass < n_pass; ++pass) {
-  const int qt = CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p;
+  const int qt = qt_of(pass);
   const int i0 = qt * BM + wave * 32;
   const int my_i = i0 + col;
   const int ib = i0 / 32;  // query block of this wave
@@ -702,8 +742,11 @@ __global__ __launch_bounds__(64 * WAVES, 2) void fa2_bwd_dq_ds_kernel(
 #pragma unroll
   for (int d = 0; d < HS / 32; ++d) acc[d] = zero16();
 
-  const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
-  const int n_stages = (kv_end + BN - 1) / BN;
+  const int n_stages = stages_of(qt);
+  // the stages [s_begin, s_end) of this pass that this part runs (all of them unless SPLIT)
+  const int s_begin = SPLIT ? min(max(g0 - pos, 0), n_stages) : 0;
+  const int s_end = SPLIT ? min(max(g1 - pos, 0), n_stages) : n_stages;
+  pos += n_stages;
 
   // Every stage issues the same loads, unconditionally (K through a buffer resource, dS from
   // clamped in-bounds tiles), and the stage count is padded to even (padded stages compute
@@ -749,6 +792,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void fa2_bwd_dq_ds_kernel(
     }
   };
   auto compute = [&](int stage, const float* ks, const float4 (&dr)[NSUB][4]) {
+    if (stage >= s_end) return;  // a padded stage (or, split, the other part's)
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub) {
       if (!has_tile(stage * NSUB + sub)) continue;
@@ -766,7 +810,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void fa2_bwd_dq_ds_kernel(
     }
   };
   auto step = [&](int s, const float4 (&cur)[NSUB][4], float4 (&nxt)[NSUB][4]) {
-    const int buf = s & 1;
+    const int buf = (s - s_begin) & 1;
     gload(s + 1);
     dsload(s + 1, nxt);
     compute(s, smem + buf * TILE, cur);
@@ -774,20 +818,23 @@ __global__ __launch_bounds__(64 * WAVES, 2) void fa2_bwd_dq_ds_kernel(
     __syncthreads();
   };
 
-  float4 dA[NSUB][4], dB[NSUB][4];
-  dsload(0, dA);
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  // Unrolled by two so the two dS register sets swap roles without copies.
-  const int n_stages2 = (n_stages + 1) & ~1;
-  for (int s = 0; s < n_stages2; s += 2) {
-    step(s, dA, dB);
-    step(s + 1, dB, dA);
+  if (s_end > s_begin) {
+    float4 dA[NSUB][4], dB[NSUB][4];
+    dsload(s_begin, dA);
+    gload(s_begin);
+    lstore(0);
+    __syncthreads();
+    // Unrolled by two so the two dS register sets swap roles without copies.
+    const int n_run2 = (s_end - s_begin + 1) & ~1;
+    for (int s = s_begin; s < s_begin + n_run2; s += 2) {
+      step(s, dA, dB);
+      step(s + 1, dB, dA);
+    }
   }
 
   if (my_i < T) {
     float* op = dQ + b * sdq.b + h * sdq.h + (int64_t)my_i * sdq.t;
+    if (SPLIT && part) op = part_ws + ((int64_t)bh * T + my_i) * HS;
 #pragma unroll
     for (int d = 0; d < HS / 32; ++d) {
 #pragma unroll
@@ -869,12 +916,24 @@ void launch_dkdv(const float* q, const float* k, const float* v, const float* d_
   run.template operator()<4>();
 }
 
+// part_ws (heads [0, n_heads) with bh_base = 0 only): run the split form and its sum pass.
 template <int HS, bool CAUSAL>
 void launch_dq_ds(const float* k, const float* dsw, float* dq, int nh, int T, int bh_base,
-                  int n_heads, RowStrides sk, RowStrides sdq, float scale, hipStream_t st) {
+                  int n_heads, RowStrides sk, RowStrides sdq, float scale, hipStream_t st,
+                  float* part_ws = nullptr) {
   auto run = [&]<int WAVES>() {
     const int n_qtiles = (T + 32 * WAVES - 1) / (32 * WAVES);
     const int64_t items = (int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * n_heads;
+    if (part_ws != nullptr) {
+      hipLaunchKernelGGL((fa2_bwd_dq_ds_kernel<HS, CAUSAL, WAVES, true>),
+                         dim3(xcd_grid(2 * items)), dim3(64 * WAVES), 0, st, k, dsw, dq, nh, T,
+                         bh_base, n_heads, n_qtiles, sk, sdq, scale, part_ws);
+      const int64_t rows = (int64_t)n_heads * T;
+      hipLaunchKernelGGL((fa2_bwd_dq_sum_kernel<HS>),
+                         dim3((unsigned)((rows * (HS / 4) + 255) / 256)), dim3(256), 0, st, dq,
+                         part_ws, nh, T, rows, sdq);
+      return;
+    }
     hipLaunchKernelGGL((fa2_bwd_dq_ds_kernel<HS, CAUSAL, WAVES>), dim3(xcd_grid(items)),
                        dim3(64 * WAVES), 0, st, k, dsw, dq, nh, T, bh_base, n_heads, n_qtiles, sk,
                        sdq, scale);
@@ -1129,8 +1188,9 @@ extern "C" int cta_flash_attention_bwd_strided(
   const int chunk = (int)((BH + n_chunks - 1) / n_chunks);
   const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
   const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
-  // A small grid's dK/dV stage splits over twice the workgroups when the workspace also holds
-  // the split's partial sums after every head's dS tiles.
+  // A small grid's dK/dV and dQ-from-dS stages split over twice the workgroups when the
+  // workspace also holds the split's partial sums after every head's dS tiles (dK, dV; then,
+  // once the dK/dV sum pass has read them, dQ in the same place).
   const int64_t ds_all = cta_flash_attention_bwd_workspace(B, nh, T, hs, causal);
   const int64_t split = cta_flash_attention_bwd_split_workspace(B, nh, T, hs, causal);
   float* part_ws = split > 0 && n_chunks == 1 && workspace_bytes >= ds_all + split
@@ -1143,7 +1203,7 @@ extern "C" int cta_flash_attention_bwd_strided(
                                rs(q_strides), rs(k_strides), rs(v_strides), rs(do_strides), sl,
                                sdk, sdv, scale, st, nullptr, {}, part_ws);
       launch_dq_ds<HS, C>(k, workspace, dq, (int)nh, (int)T, h0, n, rs(k_strides), sdq, scale,
-                          st);
+                          st, part_ws);
     });
     if (int rc = check_launch("flash_attention_bwd")) return rc;
   }

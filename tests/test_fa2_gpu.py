@@ -496,14 +496,14 @@ def test_fa2_forward_split_small_grids(cuda, B, nh, T, hs, causal):
                                               (1, 4, 1030, 128, True), (2, 4, 2048, 32, True)])
 def test_fa2_bwd_split_small_grids(cuda, B, nh, T, hs, causal):
     """The stored-dS backward with the small-grid split of its dK/dV stage (each key tile's query
-    stages over two workgroups, partial sums added in a fixed order), given the workspace for it,
-    against the same call without that room: dQ bitwise equal (the same dS tiles), dK and dV
-    within rounding; bitwise reproducible; the torch op runs the split; two heads against the
-    float64 oracle."""
+    stages over two workgroups) and of its dQ-from-dS stage (each query tile's key stages over
+    two workgroups), partial sums added in a fixed order, given the workspace for it, against
+    the same call without that room: dQ, dK and dV within rounding; bitwise reproducible; the
+    torch op runs the split; two heads against the float64 oracle."""
     from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
     from cuda_transformer_amd import capi
 
-    print(f"split dK/dV B{B} H{nh} T{T} D{hs} causal={causal}", flush=True)
+    print(f"split dK/dV and dQ B{B} H{nh} T{T} D{hs} causal={causal}", flush=True)
     q, k, v, do = (t.to(cuda) for t in _inputs(B, nh, T, hs, seed=6100 + T + hs,
                                                 do_kind="randn"))
     O, L = flash_attention_fwd(q, k, v, causal)
@@ -528,8 +528,7 @@ def test_fa2_bwd_split_small_grids(cuda, B, nh, T, hs, causal):
     torch.cuda.synchronize()
     assert all(torch.equal(a, b) for a, b in zip(split, again))
     assert all(torch.equal(a, b) for a, b in zip(split, op))
-    assert torch.equal(split[0], plain[0])
-    for i in (1, 2):
+    for i in (0, 1, 2):
         torch.testing.assert_close(split[i], plain[i], rtol=1e-5, atol=1e-5)
     for b, h in ((0, 0), (B - 1, nh - 1)):
         sl = (slice(b, b + 1), slice(h, h + 1))
