@@ -117,12 +117,14 @@ int cta_flash_attention_fwd_f16(const uint16_t* q, const int64_t* q_strides,
 int64_t cta_flash_attention_bwd_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs,
                                           int causal);
 
-/* Extra workspace bytes with which cta_flash_attention_bwd splits a small grid's dK/dV stage
- * (fewer than two waves per SIMD of the MI355X, T >= 1024): 2*B*nh*T*hs floats for the second
- * half's partial dK and dV, placed after every head's dS tiles; 0 when the stage does not
- * split.  Given cta_flash_attention_bwd_workspace() + this many bytes, each key tile's query
- * range is run by two workgroups whose partial sums are then added in a fixed order
- * (deterministic; equal to the unsplit stage to rounding).  No reference counterpart. */
+/* Extra workspace bytes with which cta_flash_attention_bwd splits a small grid's dK/dV and
+ * dQ-from-dS stages (fewer than two waves per SIMD of the MI355X, T >= 1024): 2*B*nh*T*hs
+ * floats for the second half's partial dK and dV, placed after every head's dS tiles, and
+ * reused for the second half's partial dQ; 0 when the stages do not split.  Given
+ * cta_flash_attention_bwd_workspace() + this many bytes, each key tile's query range (dK/dV)
+ * and each query tile's key range (dQ) is run by two workgroups whose partial sums are then
+ * added in a fixed order (deterministic; equal to the unsplit stages to rounding).  No
+ * reference counterpart. */
 int64_t cta_flash_attention_bwd_split_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs,
                                                 int causal);
 
