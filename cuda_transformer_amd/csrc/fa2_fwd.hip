@@ -40,11 +40,12 @@ template <> struct FwdTile<32> { static constexpr int BN = 32; static constexpr 
 template <> struct FwdTile<64> { static constexpr int BN = 32; static constexpr int MINW = 2; };
 template <> struct FwdTile<128> { static constexpr int BN = 32; static constexpr int MINW = 1; };
 
-// SPLIT: each work item (query-tile pair, or tile) is run by two workgroups, part 0 and part 1,
-// each over one half of the item's K/V stages (in the item's stage order, across its passes).
-// Each writes its half's normalised O and L = m + ln l (O = 0, L = -inf where it saw no key):
-// part 0 into O / L, part 1 densely into Os / Ls; fa2_fwd_merge_kernel then combines them.
-template <int HS, bool CAUSAL, int WAVES = 4, bool SPLIT = false>
+// NSPLIT > 1: each work item (query-tile pair, or tile) is run by NSPLIT workgroups, parts 0 ..
+// NSPLIT - 1, each over a contiguous share of the item's K/V stages (in the item's stage order,
+// across its passes).  Each writes its share's normalised O and L = m + ln l (O = 0, L = -inf
+// where it saw no key): part 0 into O / L, part k densely into the (k - 1)th slabs of Os / Ls;
+// fa2_fwd_merge_kernel then combines them.
+template <int HS, bool CAUSAL, int WAVES = 4, int NSPLIT = 1>
 __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ L, int nh, int T, int BH, int n_qtiles,
@@ -69,11 +70,12 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   // Work items are head-major and spread over XCDs.  Causal: one item = the query-tile pair
   // (n-1-p, p), so every item costs n+1 tile units and the dynamic dispatch has no tail.
   const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
-  const int n_items = BH * per_head * (SPLIT ? 2 : 1);
+  constexpr bool SPLIT = NSPLIT > 1;
+  const int n_items = BH * per_head * NSPLIT;
   const int w = xcd_work_item(blockIdx.x, n_items);
   if (w >= n_items) return;
-  const int item = SPLIT ? w >> 1 : w;
-  const int part = SPLIT ? w & 1 : 0;  // the two parts of an item are neighbours: one XCD
+  const int item = SPLIT ? w / NSPLIT : w;
+  const int part = SPLIT ? w - item * NSPLIT : 0;  // an item's parts are neighbours: one XCD
   const int bh = item / per_head;
   const int p = item - bh * per_head;
   const int b = bh / nh, h = bh - b * nh;
@@ -87,13 +89,14 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   auto stages_of = [&](int qt) {
     return ((CAUSAL ? min(T, (qt + 1) * BM) : T) + BN - 1) / BN;
   };
-  // SPLIT: this part's positions [g0, g1) in the item's list of stages (pass 0's, then pass 1's).
+  // SPLIT: this part's positions [g0, g1) in the item's list of stages (pass 0's, then pass
+  // 1's): boundaries at ceil(total k / NSPLIT).
   int g0 = 0, g1 = 0, pos = 0;
   if constexpr (SPLIT) {
     int total = 0;
     for (int pass = 0; pass < n_pass; ++pass) total += stages_of(qt_of(pass));
-    g0 = part ? (total + 1) / 2 : 0;
-    g1 = part ? total : (total + 1) / 2;
+    g0 = (total * part + NSPLIT - 1) / NSPLIT;
+    g1 = (total * (part + 1) + NSPLIT - 1) / NSPLIT;
   }
   for (int pass = 0; pass < n_pass; ++pass) {
   const int qt = qt_of(pass);
@@ -118,13 +121,10 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   for (int d = 0; d < HS / 32; ++d) oacc[d] = zero16();
   float m_run = -INFINITY;  // exponent offset of row my_i (raw q.k units), lazily updated
   float l_run = 0.0f;       // this lane's partial row sum (its half of the columns)
-  // The exponents are fma(S, s log2(e), -m s log2(e)) with the offset rounded to FP32 once per
-  // rescale.  Its rounding error moves every exponent of the row by the same amount, which
-  // cancels between O and l, but grows with |m|: past 2^20 (an error above 2^-4) some row of
-  // the wave would risk overflowing or underflowing its probabilities.  Such waves form the
-  // exponents as (S - m) s log2(e) instead, exact at the row maximum at any magnitude, as the
-  // reference's expf(S - m) is (flash_attention.cuh:130-134).  Wave-uniform.
-  bool wide = false;
+  // The exponents are (S - m) s log2(e): the subtraction comes first, so the row maximum gets
+  // exactly 2^0 at any score magnitude, as the reference's expf(S - m) does
+  // (flash_attention.cuh:130-134).  Folding m into one rounded offset, fma(S, c, -m c), cost the
+  // same but let the offset's rounding error (growing with |m|) overflow rows past |m| ~ 2^20.
 
   const int n_stages = stages_of(qt);
   // the stages [i_begin, i_end) of this pass that this part runs (all of them unless SPLIT)
@@ -250,7 +250,8 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
       // weighs by e^{-inf} = 0.
       const bool seen = l_tot > 0.0f;
       const float inv = seen ? 1.0f / l_tot : 0.0f;
-      float* op = part ? Os + ((int64_t)bh * T + my_i) * HS
+      const int64_t slab = (int64_t)(part - 1) * BH * T;  // part k >= 1: slab k - 1
+      float* op = part ? Os + (slab + (int64_t)bh * T + my_i) * HS
                        : O + b * so.b + h * so.h + (int64_t)my_i * so.t;
 #pragma unroll
       for (int d = 0; d < HS / 32; ++d) {
@@ -262,7 +263,8 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
         }
       }
       if (half == 0)
-        (part ? Ls : L)[(int64_t)bh * T + my_i] = seen ? m_run * scale + logf(l_tot) : -INFINITY;
+        (part ? Ls + slab : L)[(int64_t)bh * T + my_i] =
+            seen ? m_run * scale + logf(l_tot) : -INFINITY;
     } else {
       float* op = O + b * so.b + h * so.h + (int64_t)my_i * so.t;
 #pragma unroll
@@ -280,11 +282,11 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   }  // pass: the K/V loop ended on a barrier, so the next pass may refill LDS
 }
 
-// Merge of the two parts of a split forward, row by row in a fixed order (part 0, part 1):
-// L = ln(e^{L0} + e^{L1}), taken about their maximum, and O = e^{L0 - L} O0 + e^{L1 - L} O1;
-// part 0 in O / L (O through its strides), part 1 dense in Os / Ls.  HS / 4 lanes per row, one
-// float4 each.
-template <int HS>
+// Merge of the NSPLIT parts of a split forward, row by row in a fixed order (part 0, 1, ...):
+// L = ln(sum_k e^{Lk}), taken about their maximum, and O = sum_k e^{Lk - L} Ok; part 0 in
+// O / L (O through its strides), part k >= 1 dense in slab k - 1 of Os / Ls.  HS / 4 lanes per
+// row, one float4 each.
+template <int HS, int NSPLIT>
 __global__ __launch_bounds__(256) void fa2_fwd_merge_kernel(float* __restrict__ O,
                                                             float* __restrict__ L,
                                                             const float* __restrict__ Os,
@@ -298,24 +300,46 @@ __global__ __launch_bounds__(256) void fa2_fwd_merge_kernel(float* __restrict__ 
   const int64_t bh = row / T;
   const int t = (int)(row - bh * T);
   const int64_t b = bh / nh, h = bh - b * nh;
-  const float l0 = L[row], l1 = Ls[row];
-  const float m = fmaxf(l0, l1);  // finite: every row sees key 0 in one of the parts
-  const float e0 = expf(l0 - m), e1 = expf(l1 - m);
-  const float inv = 1.0f / (e0 + e1);
-  const float w0 = e0 * inv, w1 = e1 * inv;
+  float lk[NSPLIT];
+  lk[0] = L[row];
+#pragma unroll
+  for (int k = 1; k < NSPLIT; ++k) lk[k] = Ls[(int64_t)(k - 1) * rows + row];
+  float m = lk[0];  // finite: every row sees key 0 in one of the parts
+#pragma unroll
+  for (int k = 1; k < NSPLIT; ++k) m = fmaxf(m, lk[k]);
+  float e[NSPLIT], sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NSPLIT; ++k) {
+    e[k] = expf(lk[k] - m);
+    sum += e[k];
+  }
+  const float inv = 1.0f / sum;
   float* op = O + b * so.b + h * so.h + (int64_t)t * so.t + 4 * c4;
-  const float4 a = ld4(op), c = ld4(Os + row * HS + 4 * c4);
-  st4(op, make_float4(fmaf(w0, a.x, w1 * c.x), fmaf(w0, a.y, w1 * c.y), fmaf(w0, a.z, w1 * c.z),
-                      fmaf(w0, a.w, w1 * c.w)));
-  if (c4 == 0) L[row] = m + logf(e0 + e1);
+  // acc = w_{N-1} O_{N-1}, then fma in the weights of parts N-2 .. 0
+  const float wl = e[NSPLIT - 1] * inv;
+  const float4 cl = ld4(Os + ((int64_t)(NSPLIT - 2) * rows + row) * HS + 4 * c4);
+  float4 acc = make_float4(wl * cl.x, wl * cl.y, wl * cl.z, wl * cl.w);
+#pragma unroll
+  for (int k = NSPLIT - 2; k >= 1; --k) {
+    const float wk = e[k] * inv;
+    const float4 c = ld4(Os + ((int64_t)(k - 1) * rows + row) * HS + 4 * c4);
+    acc = make_float4(fmaf(wk, c.x, acc.x), fmaf(wk, c.y, acc.y), fmaf(wk, c.z, acc.z),
+                      fmaf(wk, c.w, acc.w));
+  }
+  const float w0 = e[0] * inv;
+  const float4 a = ld4(op);
+  st4(op, make_float4(fmaf(w0, a.x, acc.x), fmaf(w0, a.y, acc.y), fmaf(w0, a.z, acc.z),
+                      fmaf(w0, a.w, acc.w)));
+  if (c4 == 0) L[row] = m + logf(sum);
 }
 
-// The forward splits each work item's K/V stages over two workgroups when its grid would hold
-// fewer than two waves per SIMD (1024 SIMDs) and a full row of keys gives each part at least
-// kSplitMinStages stages: the split doubles the waves in flight at the cost of the merge pass.
-// A/B in one process against the unsplit forward: B4 H4 N4096 causal 0.3306 -> 0.3042 ms
-// (+8.7%), B2 H4 N4096 non-causal +7.3%; at T = 256 (B64 H6, 8 stages per row) 30% slower,
-// the merge outweighing the work, hence the minimum.
+// The forward splits each work item's K/V stages over NSPLIT workgroups when its grid would hold
+// fewer than two waves per SIMD (1024 SIMDs): enough parts to fill the waves per SIMD its
+// registers and LDS allow (three at hs 32 / 64, two at hs 128), each part keeping at least
+// kSplitMinStages stages; the merge pass is the cost.  A/B in one process against the unsplit
+// forward: B4 H4 N4096 causal 0.3306 -> 0.3042 ms with two parts (+8.7%), B2 H4 N4096
+// non-causal +7.3%; at T = 256 (B64 H6, 8 stages per row) two parts were 30% slower, the merge
+// outweighing the work, hence the minimum.
 constexpr int kSimds = 1024;
 constexpr int kSplitMinStages = 16;
 
@@ -324,12 +348,17 @@ int fwd_waves(int T) {
   return (HS == 64 && CAUSAL && T <= 512) ? 2 : 4;
 }
 
+// Parts per work item: 1 (no split), 2 or 3.
 template <int HS, bool CAUSAL>
-bool fwd_split(int T, int BH) {
+int fwd_nsplit(int T, int BH) {
   const int waves = fwd_waves<HS, CAUSAL>(T);
   const int n_qtiles = (T + 32 * waves - 1) / (32 * waves);
-  const int64_t items = (int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH;
-  return items * waves < 2 * kSimds && T / FwdTile<HS>::BN >= 2 * kSplitMinStages;
+  const int64_t w = (int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH * waves;
+  if (w >= 2 * kSimds) return 1;
+  const int occ = HS == 128 ? 2 : 3;  // waves per SIMD the unsplit kernel can hold
+  int n = (int)std::min<int64_t>(occ, (occ * kSimds + w - 1) / w);
+  n = std::min(n, T / FwdTile<HS>::BN / kSplitMinStages);
+  return n >= 2 ? n : 1;
 }
 
 template <int HS, bool CAUSAL>
@@ -339,15 +368,24 @@ void launch_fwd(const float* q, const float* k, const float* v, float* o, float*
   auto run = [&]<int WAVES>() {
     const int n_qtiles = (T + 32 * WAVES - 1) / (32 * WAVES);
     const int64_t items = (int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH;
-    if (split_ws != nullptr) {
+    const int nsplit = split_ws != nullptr ? fwd_nsplit<HS, CAUSAL>(T, BH) : 1;
+    auto split = [&]<int NS>() {
+      const int64_t rows = (int64_t)BH * T;
       float* Os = split_ws;
-      float* Ls = split_ws + (int64_t)BH * T * HS;
-      hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL, WAVES, true>), dim3(xcd_grid(2 * items)),
+      float* Ls = split_ws + (NS - 1) * rows * HS;
+      hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL, WAVES, NS>), dim3(xcd_grid(NS * items)),
                          dim3(64 * WAVES), 0, stream, q, k, v, o, l, nh, T, BH, n_qtiles, sq, sk,
                          sv, so, scale, scale * kLog2e, 8.0f / (scale * kLog2e), Os, Ls);
-      const int64_t rows = (int64_t)BH * T;
-      hipLaunchKernelGGL((fa2_fwd_merge_kernel<HS>), dim3((unsigned)((rows * (HS / 4) + 255) / 256)),
-                         dim3(256), 0, stream, o, l, Os, Ls, nh, T, rows, so);
+      hipLaunchKernelGGL((fa2_fwd_merge_kernel<HS, NS>),
+                         dim3((unsigned)((rows * (HS / 4) + 255) / 256)), dim3(256), 0, stream, o,
+                         l, Os, Ls, nh, T, rows, so);
+    };
+    if (nsplit == 3) {
+      split.template operator()<3>();
+      return;
+    }
+    if (nsplit == 2) {
+      split.template operator()<2>();
       return;
     }
     hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL, WAVES>), dim3(xcd_grid(items)),
@@ -411,9 +449,9 @@ extern "C" int64_t cta_flash_attention_fwd_workspace(int64_t B, int64_t nh, int6
   if (B <= 0 || nh <= 0 || T <= 0 || (hs != 32 && hs != 64 && hs != 128) ||
       B * nh > ((int64_t)1 << 24) || T > ((int64_t)1 << 24))
     return 0;
-  bool split = false;
-  dispatch_fwd(hs, causal, [&]<int HS, bool C>() { split = fwd_split<HS, C>((int)T, (int)(B * nh)); });
-  return split ? B * nh * T * (hs + 1) * (int64_t)sizeof(float) : 0;
+  int nsplit = 1;
+  dispatch_fwd(hs, causal, [&]<int HS, bool C>() { nsplit = fwd_nsplit<HS, C>((int)T, (int)(B * nh)); });
+  return (nsplit - 1) * B * nh * T * (hs + 1) * (int64_t)sizeof(float);
 }
 
 extern "C" int cta_flash_attention_fwd_ex(const float* q, const int64_t* q_strides,

@@ -71,17 +71,18 @@ int cta_flash_attention_fwd_strided(const float* q, const int64_t* q_strides,
                                     int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
                                     float* o, const int64_t* o_strides, float* l, void* stream);
 
-/* Bytes of scratch with which cta_flash_attention_fwd_ex splits the forward's work: B*nh*T*(hs+1)
- * floats when the grid would hold fewer than two waves per SIMD of the MI355X (e.g. the
- * B4 H4 N4096 D64 share of one GPU of eight), 0 when the forward does not split. */
+/* Bytes of scratch with which cta_flash_attention_fwd_ex splits the forward's work:
+ * (parts - 1)*B*nh*T*(hs+1) floats, parts = 2 or 3, when the grid would hold fewer than two
+ * waves per SIMD of the MI355X (e.g. the B4 H4 N4096 D64 share of one GPU of eight); 0 when
+ * the forward does not split. */
 int64_t cta_flash_attention_fwd_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs,
                                           int causal);
 
 /* cta_flash_attention_fwd_strided with a workspace.  Given cta_flash_attention_fwd_workspace()
- * bytes (when that is non-zero), each work item's K/V range is run by two workgroups, which
- * write the normalised partial O and L of their halves (one into O and L, one into the
- * workspace); a merge pass then combines them in a fixed order, L = ln(e^{L0} + e^{L1}),
- * O = e^{L0-L} O0 + e^{L1-L} O1.  Deterministic; equal to the unsplit forward to rounding.
+ * bytes (when that is non-zero), each work item's K/V range is run by two or three workgroups,
+ * which write the normalised partial O and L of their shares (part 0 into O and L, the others
+ * into the workspace); a merge pass then combines them in a fixed order, L = ln(sum_k e^{Lk}),
+ * O = sum_k e^{Lk-L} Ok.  Deterministic; equal to the unsplit forward to rounding.
  * Without the workspace (NULL or too small) it is cta_flash_attention_fwd_strided.  No
  * counterpart in the reference's launchers: their grid has no small-grid case to cover. */
 int cta_flash_attention_fwd_ex(const float* q, const int64_t* q_strides,

@@ -441,26 +441,27 @@ def test_fa2_forward_huge_scores(cuda, causal):
 
 # Grids of fewer than two waves per SIMD: the B4 H4 N4096 share of one GPU of eight, the GPT
 # step's B64 H6 T256 (two-wave tiles), hs 32 and 128, non-causal, ragged T.
-SPLIT_SHAPES = [(4, 4, 4096, 64, True), (2, 4, 4096, 64, False), (64, 6, 256, 64, True),
-                (2, 4, 2048, 32, True), (1, 4, 1030, 128, True), (1, 8, 1100, 64, False),
-                (4, 32, 1024, 64, True)]
+# (B, nh, T, hs, causal, parts): parts = workgroups per item (1 = no split).
+SPLIT_SHAPES = [(4, 4, 4096, 64, True, 3), (2, 4, 4096, 64, False, 3), (64, 6, 256, 64, True, 1),
+                (2, 4, 2048, 32, True, 3), (1, 4, 1030, 128, True, 2), (1, 8, 1100, 64, False, 2),
+                (4, 32, 1024, 64, True, 1), (3, 8, 4096, 64, True, 2)]
 
 
-@pytest.mark.parametrize("B,nh,T,hs,causal", SPLIT_SHAPES)
-def test_fa2_forward_split_small_grids(cuda, B, nh, T, hs, causal):
-    """The forward with its small-grid workspace (each item's K/V range over two workgroups and
-    a fixed-order log-sum-exp merge) against the unsplit forward (within rounding), against the
-    float64 oracle on two heads, and bitwise reproducible; the torch op takes the split path.
-    Shapes that do not split (T = 256, or grids that fill the GPU) ask for no workspace and run
-    the unsplit kernel bit for bit."""
+@pytest.mark.parametrize("B,nh,T,hs,causal,parts", SPLIT_SHAPES)
+def test_fa2_forward_split_small_grids(cuda, B, nh, T, hs, causal, parts):
+    """The forward with its small-grid workspace (each item's K/V range over two or three
+    workgroups and a fixed-order log-sum-exp merge) against the unsplit forward (within
+    rounding), against the float64 oracle on two heads, and bitwise reproducible; the torch op
+    takes the split path.  Shapes that do not split (T = 256, or grids that fill the GPU) ask
+    for no workspace and run the unsplit kernel bit for bit."""
     from cuda_transformer.ops import flash_attention_fwd
     from cuda_transformer_amd import capi
 
-    print(f"split forward B{B} H{nh} T{T} D{hs} causal={causal}", flush=True)
+    print(f"split forward B{B} H{nh} T{T} D{hs} causal={causal} parts={parts}", flush=True)
     q, k, v, _ = (t.to(cuda) for t in _inputs(B, nh, T, hs, seed=6000 + T + hs))
     nbytes = capi.call("cta_flash_attention_fwd_workspace", B, nh, T, hs, int(causal))
-    splits = T >= 1024 and (B, nh, T) != (4, 32, 1024)
-    assert nbytes == (B * nh * T * (hs + 1) * 4 if splits else 0)
+    splits = parts > 1
+    assert nbytes == (parts - 1) * B * nh * T * (hs + 1) * 4
     ws = torch.empty(max(1, nbytes // 4), device=cuda)
     s4 = capi.strides(q.stride())
     st = torch.cuda.current_stream().cuda_stream
