@@ -319,8 +319,8 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_re
     delta = torch.empty(B, H, N, device=dev)
     ws_full = capi.lib().cta_flash_attention_bwd_workspace(B, H, N, D, int(causal))
     ws_bytes = min(ws_full, BWD_WORKSPACE_CAP) if schedule in ("stored", "fold") else 0
-    # small grids: the operator's split dK/dV stage (its partial sums after the dS tiles) and
-    # split forward, as flash_attention_fwd / flash_attention_bwd run them
+    # small grids: the operator's split dK/dV and dQ-from-dS stages (their partial sums after
+    # the dS tiles) and split forward, as flash_attention_fwd / flash_attention_bwd run them
     split_bytes = (capi.lib().cta_flash_attention_bwd_split_workspace(B, H, N, D, int(causal))
                    if schedule == "stored" and ws_bytes == ws_full else 0)
     ws_bytes += split_bytes

@@ -578,8 +578,8 @@ std::tuple<at::Tensor, at::Tensor> flash_attention_fwd_half(const at::Tensor& Q,
   return {O, L};
 }
 
-// Scratch with which the FP32 forward splits a small grid's work over twice the workgroups
-// (cta_flash_attention_fwd_workspace; none for grids that fill the GPU).  If the allocator
+// Scratch with which the FP32 forward splits a small grid's work over two or three times the
+// workgroups (cta_flash_attention_fwd_workspace; none for grids that fill the GPU).  If the allocator
 // cannot supply it, the forward runs unsplit (ws_bytes = 0): same results to rounding.
 at::Tensor fwd_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs, bool causal,
                          const at::TensorOptions& opts, int64_t& ws_bytes) {
@@ -634,7 +634,7 @@ at::Tensor bwd_workspace(int64_t B, int64_t nh, int64_t T, int64_t hs, bool caus
                          const at::TensorOptions& opts, int64_t& ws_bytes) {
   const int64_t full = cta_flash_attention_bwd_workspace(B, nh, T, hs, causal ? 1 : 0);
   ws_bytes = capped_workspace(full, cta_flash_attention_bwd_workspace(1, 1, T, hs, causal ? 1 : 0));
-  // every head's dS tiles fit: room for a small grid's split dK/dV stage too
+  // every head's dS tiles fit: room for a small grid's split dK/dV and dQ-from-dS stages too
   if (ws_bytes == full && full > 0)
     ws_bytes += cta_flash_attention_bwd_split_workspace(B, nh, T, hs, causal ? 1 : 0);
   at::Tensor ws;
