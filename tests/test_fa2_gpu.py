@@ -346,20 +346,28 @@ def test_fa2_strided_outputs_recompute_schedule(cuda):
     assert (d[..., :C] - stored[..., :C]).abs().max().item() <= 1e-5
 
 
-@pytest.mark.parametrize("do_kind", ["randn", "rand"])
-def test_fa2_config2_full_size(cuda, do_kind):
-    """Benchmark config 2 (B4 H32 N4096 D64, causal) at full size, with dO ~ N(0,1) as the config
-    states and with the reference test's U[0,1): two heads against the float64 oracle, and on
-    every head the size-independent invariants of the backward: sum_j dK_j = 0 (rows of dS sum
-    to zero) and sum_j dV_j = sum_i dO_i (rows of P sum to 1)."""
+@pytest.mark.parametrize("do_kind,schedule,hs", [("randn", "stored", 64), ("rand", "stored", 64),
+                                                  ("randn", "recompute", 64),
+                                                  ("randn", "stored", 32), ("randn", "stored", 128)])
+def test_fa2_config2_full_size(cuda, bwd_cap, do_kind, schedule, hs):
+    """Benchmark config 2 (B4 H32 N4096 D64, causal) at full size (and at hs 32 and 128), with
+    dO ~ N(0,1) as the config states and with the reference test's U[0,1), through the
+    operator's default stored-dS schedule and (workspace cap 0) the reference's recompute
+    schedule: two heads against the float64 oracle, and on every head the size-independent
+    invariants of the backward: sum_j dK_j = 0 (rows of dS sum to zero) and
+    sum_j dV_j = sum_i dO_i (rows of P sum to 1)."""
     from cuda_transformer.ops import flash_attention_bwd, flash_attention_fwd
+    from cuda_transformer_amd import _C
 
-    B, nh, T, hs = 4, 32, 4096, 64
-    print(f"config 2: B4 H32 N4096 D64 causal dO~{do_kind}", flush=True)
+    B, nh, T = 4, 32, 4096
+    print(f"config 2: B4 H32 N4096 D{hs} causal dO~{do_kind} {schedule}", flush=True)
     q, k, v, do = (t.to(cuda) for t in _inputs(B, nh, T, hs, seed=2024, do_kind=do_kind))
     O, L = flash_attention_fwd(q, k, v, True)
+    if schedule == "recompute":
+        bwd_cap(0)
     dq, dk, dv = flash_attention_bwd(q, k, v, O, do, L, True)
     torch.cuda.synchronize()
+    assert _C.last_bwd_schedule() == schedule
     for t in (O, L, dq, dk, dv):
         assert torch.isfinite(t).all()
     for (b, h) in ((0, 0), (3, 31)):

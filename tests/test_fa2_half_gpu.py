@@ -311,3 +311,36 @@ def test_fa2_half_config1_as_stated(cuda, dtype, causal, schedule):
     grads = _half_bwd_capi(qg, kg, vg, O, do.to(cuda), L, causal, stored=schedule == "stored")
     _check(O.cpu(), L.cpu(), q, k, v, causal)
     _bwd_check([g.cpu() for g in grads], q, k, v, do, causal)
+
+
+@pytest.mark.parametrize("schedule", ["recompute", "stored"])
+def test_fa2_half_config2_full_size(cuda, schedule):
+    """The BF16 path at benchmark config 2's shape (B4 H32 N4096 D64 causal), inputs and dO
+    i.i.d. N(0,1), through both backward schedules: two heads against the float64 oracle (the
+    forward and gradient bounds above), and on every head the backward's size-independent
+    invariants, sum_j dK_j = 0 and sum_j dV_j = sum_i dO_i, within the 16-bit rounding."""
+    from cuda_transformer.ops import flash_attention_fwd
+    from conftest import rel_err
+
+    B, nh, T, hs = 4, 32, 4096, 64
+    print(f"bf16 config 2 full size, {schedule} schedule", flush=True)
+    q, k, v = _half_inputs(B, nh, T, hs, seed=2400, dtype=torch.bfloat16)
+    do = seeded((B, nh, T, hs), 2404, kind="randn").to(torch.bfloat16)
+    qg, kg, vg, dog = q.to(cuda), k.to(cuda), v.to(cuda), do.to(cuda)
+    O, L = flash_attention_fwd(qg, kg, vg, True)
+    dq, dk, dv = _half_bwd_capi(qg, kg, vg, O, dog, L, True, stored=schedule == "stored")
+    for t in (O, L, dq, dk, dv):
+        assert torch.isfinite(t).all()
+    for b, h in ((0, 0), (B - 1, nh - 1)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        qh, kh, vh, doh = (t[sl] for t in (q, k, v, do))
+        _check(O[sl].cpu(), L[sl].cpu(), qh, kh, vh, True)
+        O_ref, L_ref = ora.reference_attention(f64(qh), f64(kh), f64(vh), True)
+        refs = ora.fa2_backward(f64(qh), f64(kh), f64(vh), O_ref, f64(doh), L_ref, True,
+                                br=512, bc=512)
+        for got, ref, tol in zip((dq, dk, dv), refs, (3e-2, 3e-2, 1.5e-2)):
+            e = rel_err(f64(got[sl].cpu()), ref)
+            assert e <= tol, (schedule, b, h, e, tol)
+    dk64, dv64, do64 = dk.double(), dv.double(), dog.double()
+    assert (dk64.sum(dim=2).abs() <= 1e-2 * dk64.abs().sum(dim=2) + 1e-6).all()
+    assert ((dv64.sum(dim=2) - do64.sum(dim=2)).abs() <= 1e-2 * do64.abs().sum(dim=2)).all()
