@@ -501,8 +501,9 @@ def fa2_sweep(args):
 def fa2_half_workload(args, kind):
     """The 16-bit FlashAttention-2 step (kind "bf16" or "f16") at the config-2 shape, causal and
     non-causal: forward (cta_flash_attention_fwd_<kind>) and backward
-    (cta_flash_attention_bwd_<kind>) in both schedules, recompute (no workspace: delta, dK/dV,
-    dQ recomputing S and dP) and stored dS (delta, dK/dV storing 16-bit dS, dQ from dS), each
+    (cta_flash_attention_bwd_<kind>) in both schedules, recompute (no workspace: dQ recomputing
+    S and dP and forming delta, then dK/dV) and stored dS (delta, dK/dV storing 16-bit dS, dQ from
+    dS), each
     timed with HIP events on torch's current stream with inputs in HBM.  `value` is the step
     with the schedule the operator runs (recompute at hs 32 and 64, stored at hs 128).  TFLOPS
     by the reference's formula (forward 4*B*H*N^2*D, halved when causal; backward 2.5x),

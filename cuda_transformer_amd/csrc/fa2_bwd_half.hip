@@ -11,9 +11,10 @@
 // in BF16 for the dQ stage.  Two schedules, as in FP32, both atomics-free and deterministic:
 //  * stored dS (given a workspace of at least one head's tiles): delta, then a dK/dV stage that
 //    also writes every dS tile, then dQ = s dS K from the stored tiles;
-//  * recompute (no workspace; the reference's schedule): delta, dK/dV without the store, and a
-//    dQ stage that recomputes S and dP from L and delta.  dK and dV are bitwise those of the
-//    stored schedule (the same kernel body); dQ differs by the rounding of its sums.
+//  * recompute (no workspace; the reference's schedule): a dQ stage that recomputes S and dP
+//    from L and forms delta itself (the delta pass's sums, the same bits), then dK/dV without
+//    the store.  dK and dV are bitwise those of the stored schedule (the same kernel body); dQ
+//    differs by the rounding of its sums.
 //
 // gfx950 layout (the 16-bit forward's trick, see fa2_fwd_half.hip):
 //  * dK/dV: a wave owns 32 key rows and keeps k, v of its key row in registers as the B
@@ -580,12 +581,16 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_ds_half_ker
 // row's q and dO (the B operands of S^T = K Q^T and dP^T = V dO^T), L log2(e) and delta.  Each
 // stage goes to LDS as K rows (S), V rows (dP) and K^T with kt_pos (the A operand of
 // dQ^T += K^T dS^T, whose B operand is the lane's dS^T registers, as P^T is in the forward).
+// It also forms delta = rowsum(O dO) from its rows (the sums of fa2_bwd_delta_half_kernel in
+// the same order, so the same bits) and writes it for the dK/dV stage that runs after it:
+// the recompute schedule needs no delta launch.
 template <class E, int HS, bool CAUSAL>
 __global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_half_kernel(
     const E* __restrict__ Q, const E* __restrict__ K, const E* __restrict__ V,
-    const E* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
-    E* __restrict__ dQ, int nh, int T, int BH, int n_qtiles, RowStridesH sq, RowStridesH sk,
-    RowStridesH sv, RowStridesH sdo, RowStridesH sl, float scale, float scale_log2) {
+    const E* __restrict__ dO, const E* __restrict__ Og, const float* __restrict__ Lg,
+    float* __restrict__ delta, E* __restrict__ dQ, int nh, int T, int BH, int n_qtiles,
+    RowStridesH sq, RowStridesH sk, RowStridesH sv, RowStridesH sdo, RowStridesH so,
+    RowStridesH sl, float scale, float scale_log2) {
   constexpr int BN = 64;             // keys per stage
   constexpr int NSUB = BN / 32;
   constexpr int BM = 128;
@@ -632,13 +637,33 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_half_kernel
       gf[s] = ld8<E>(gp + 16 * s);
     }
     lrow = Lg[b * sl.b + h * sl.h + (int64_t)my_i * sl.t] * kLog2e;
-    drow = delta[(int64_t)bh * T + my_i];
+    // delta: the lane's 16-byte chunks c = 2 s + half, each an fma chain as in
+    // fa2_bwd_delta_half_kernel, then that kernel's xor tree over chunks (offsets HS/16 .. 2
+    // pair chunks s and s ^ off/2 of this lane; offset 1 pairs the two wave halves).
+    const E* op = Og + b * so.b + h * so.h + (int64_t)my_i * so.t + 8 * half;
+    float part[QS];
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      const vec8_t<E> o = ld8<E>(op + 16 * s);
+      float acc = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = fmaf((float)o[e], (float)gf[s][e], acc);
+      part[s] = acc;
+    }
+#pragma unroll
+    for (int off2 = QS / 2; off2 >= 1; off2 >>= 1)
+#pragma unroll
+      for (int s = 0; s < off2; ++s) part[s] = part[s] + part[s + off2];
+    drow = part[0];
   } else {
 #pragma unroll
     for (int s = 0; s < QS; ++s)
 #pragma unroll
       for (int j = 0; j < 8; ++j) { qf[s][j] = (E)0.0f; gf[s][j] = (E)0.0f; }
   }
+  // The cross-half step of the delta sum; every lane takes part (rows past T sum nothing).
+  drow = drow + xor32(drow);
+  if (my_i < T && half == 0) delta[(int64_t)bh * T + my_i] = drow;
   // The row loads are complete before the stage loop on every path into it (the compiler
   // would otherwise wait for them inside each stage, draining the next stage's loads too).
   vm_wait_all();
@@ -908,6 +933,27 @@ int bwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
   const int BH = (int)(B * nh);
   hipStream_t st = as_stream(stream);
 
+  const int n_tiles = (int)((T + 127) / 128);
+  if (!stored) {
+    // Recompute: dQ first (it forms delta and writes it), then dK/dV, which reads it.
+    dispatch_half(hs, causal, [&]<int HS, bool C>() {
+      const int64_t items = (int64_t)(C ? (n_tiles + 1) / 2 : n_tiles) * BH;
+      hipLaunchKernelGGL((fa2_bwd_dq_half_kernel<E, HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
+                         st, qb, kb, vb, gb, ob, l, delta, dqb, (int)nh, (int)T, BH, n_tiles,
+                         rsh(q_strides), rsh(k_strides), rsh(v_strides), rsh(do_strides),
+                         rsh(o_strides), sl, scale, scale * kLog2e);
+      using Cfg = DkdvHalfCfg<HS, C>;
+      const int n_ktiles = (int)((T + 32 * Cfg::WAVES - 1) / (32 * Cfg::WAVES));
+      const int64_t kitems = (int64_t)(C ? (n_ktiles + 1) / 2 : n_ktiles) * BH;
+      hipLaunchKernelGGL(
+          (fa2_bwd_dkdv_half_kernel<E, HS, C, Cfg::WAVES, Cfg::BN, Cfg::MINW, false>),
+          dim3(xcd_grid(kitems)), dim3(64 * Cfg::WAVES), 0, st, qb, kb, vb, gb, l, delta, dkb,
+          dvb, nullptr, (int)nh, (int)T, 0, BH, n_ktiles, rsh(q_strides), rsh(k_strides),
+          rsh(v_strides), rsh(do_strides), sl, scale, scale * kLog2e);
+    });
+    return check_launch("flash_attention_bwd (16-bit, recompute)");
+  }
+
   const int64_t rows = B * nh * T;
   const unsigned dgrid = (unsigned)((rows * (hs / 8) + 255) / 256);
   if (hs == 32)
@@ -920,26 +966,6 @@ int bwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
     hipLaunchKernelGGL((fa2_bwd_delta_half_kernel<E, 128>), dim3(dgrid), dim3(256), 0, st, ob, gb,
                        delta, (int)nh, (int)T, rows, rsh(o_strides), rsh(do_strides));
   if (int rc = check_launch("flash_attention_bwd (16-bit) delta")) return rc;
-
-  const int n_tiles = (int)((T + 127) / 128);
-  if (!stored) {
-    dispatch_half(hs, causal, [&]<int HS, bool C>() {
-      using Cfg = DkdvHalfCfg<HS, C>;
-      const int n_ktiles = (int)((T + 32 * Cfg::WAVES - 1) / (32 * Cfg::WAVES));
-      const int64_t kitems = (int64_t)(C ? (n_ktiles + 1) / 2 : n_ktiles) * BH;
-      hipLaunchKernelGGL(
-          (fa2_bwd_dkdv_half_kernel<E, HS, C, Cfg::WAVES, Cfg::BN, Cfg::MINW, false>),
-          dim3(xcd_grid(kitems)), dim3(64 * Cfg::WAVES), 0, st, qb, kb, vb, gb, l, delta, dkb,
-          dvb, nullptr, (int)nh, (int)T, 0, BH, n_ktiles, rsh(q_strides), rsh(k_strides),
-          rsh(v_strides), rsh(do_strides), sl, scale, scale * kLog2e);
-      const int64_t items = (int64_t)(C ? (n_tiles + 1) / 2 : n_tiles) * BH;
-      hipLaunchKernelGGL((fa2_bwd_dq_half_kernel<E, HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
-                         st, qb, kb, vb, gb, l, delta, dqb, (int)nh, (int)T, BH, n_tiles,
-                         rsh(q_strides), rsh(k_strides), rsh(v_strides), rsh(do_strides), sl,
-                         scale, scale * kLog2e);
-    });
-    return check_launch("flash_attention_bwd (16-bit, recompute)");
-  }
 
   // Chunks of equal head counts that fit the workspace.
   const int64_t fit = std::min<int64_t>(BH, workspace_bytes / head_bytes);

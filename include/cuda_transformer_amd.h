@@ -195,9 +195,10 @@ int64_t cta_flash_attention_bwd_bf16_workspace(int64_t B, int64_t nh, int64_t T,
 /* Backward with BF16 Q, K, V, O, dO (uint16_t bit patterns) and FP32 L: delta (FP32, caller
  * scratch of B*nh*T floats), then dK/dV storing BF16 dS tiles and dQ from them, chunked over
  * heads to fit workspace_bytes.  With no workspace, or less than one head's share of
- * cta_flash_attention_bwd_bf16_workspace(), it runs the reference's schedule instead: dK/dV
- * without the store and a dQ stage that recomputes S and dP (no O(T^2) memory; dK and dV
- * bitwise equal to the stored schedule's, dQ equal to rounding).  dq/dk/dv dense
+ * cta_flash_attention_bwd_bf16_workspace(), it runs the reference's schedule instead: a dQ
+ * stage that recomputes S and dP (and forms delta, the same bits as the delta pass), then dK/dV
+ * without the store (no O(T^2) memory; dK and dV bitwise equal to the stored schedule's, dQ
+ * equal to rounding).  dq/dk/dv dense
  * (B,nh,T,hs) BF16.  hs in {32, 64, 128}; strides as for cta_flash_attention_fwd_bf16.  P and dS
  * are rounded to BF16 as MFMA operands; accumulation is FP32; deterministic.  No counterpart
  * in the reference's launchers (reduced precision is on its roadmap, README.md:277); the
