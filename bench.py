@@ -298,7 +298,8 @@ BWD_WORKSPACE_CAP = 8 << 30
 def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_reps=5,
                 warm_s=0.5):
     """Time `steps` FA2 steps through the C ABI on torch's current stream: fwd, then the
-    backward stages of `schedule` ([delta, dkdv, dq_ds] stored; [delta, dq, dkdv] recompute;
+    backward stages of `schedule` ([delta, dkdv, dq_ds] stored; [dq forming delta, dkdv]
+    recompute;
     one combined [bwd] launch when the stored schedule needs head chunks, as the operator
     runs it), after at least `warmup` untimed steps and warm_s seconds of them.  After the timed
     steps, each kernel is timed again `flushed_reps` times with FLUSH_BYTES read before every
@@ -345,10 +346,10 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_re
         elif kernel == "delta":
             rc = lib.cta_flash_attention_bwd_delta(P["O"], s4, P["do"], s4, B, H, N, D,
                                                    P["delta"], st)
-        elif kernel == "dq":
-            rc = lib.cta_flash_attention_bwd_dq(P["q"], s4, P["k"], s4, P["v"], s4, P["do"], s4,
-                                                P["L"], s3, P["delta"], B, H, N, D, c, P["dq"],
-                                                st)
+        elif kernel == "dq":  # dQ of the reference schedule, forming delta as it goes
+            rc = lib.cta_flash_attention_bwd_dq_delta(P["q"], s4, P["k"], s4, P["v"], s4, P["O"],
+                                                      s4, P["do"], s4, P["L"], s3, B, H, N, D, c,
+                                                      P["delta"], P["dq"], st)
         elif kernel == "dkdv" and schedule == "recompute":
             rc = lib.cta_flash_attention_bwd_dkdv(P["q"], s4, P["k"], s4, P["v"], s4, P["do"],
                                                   s4, P["L"], s3, P["delta"], B, H, N, D, c,
@@ -372,7 +373,7 @@ def fa2_timings(B, H, N, D, causal, steps, warmup, schedule="stored", flushed_re
             raise RuntimeError(f"{kernel}: {lib.cta_last_error().decode()}")
 
     if schedule == "recompute":
-        kernels = ["fwd", "delta", "dq", "dkdv"]
+        kernels = ["fwd", "dq", "dkdv"]
     elif schedule == "fold":
         kernels = ["fwd", "bwd_fold"]
     elif ws_full <= ws_bytes and split_bytes == 0:

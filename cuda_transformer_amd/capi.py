@@ -59,6 +59,9 @@ SIGNATURES = {
                                              _p]),
     "cta_flash_attention_bwd_dq": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
                                           _p, _i64, _i64, _i64, _i64, _int, _p, _p]),
+    "cta_flash_attention_bwd_dq_delta": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p,
+                                                _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _int,
+                                                _p, _p, _p]),
     "cta_flash_attention_bwd_dkdv": (_int, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p,
                                             _i64p, _p, _i64, _i64, _i64, _i64, _int, _p, _p,
                                             _p]),

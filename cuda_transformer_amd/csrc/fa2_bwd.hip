@@ -91,12 +91,16 @@ __device__ __forceinline__ void pin_mfma_pairs() {
 
 // ------------------------------------------------------------------------------------
 // Stage 2: dQ.  Workgroup = 128 query rows; K/V tiles streamed through LDS.
-template <int HS, bool CAUSAL>
+// FORM_DELTA: the kernel forms delta = rowsum(O dO) from its own rows (O through strides so),
+// with fa2_bwd_delta_kernel's products and summation order (the same bits), uses it and writes
+// it for the dK/dV stage that follows; otherwise it reads delta.
+template <int HS, bool CAUSAL, bool FORM_DELTA = false>
 __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ dO, const float* __restrict__ Lg, const float* __restrict__ delta,
+    const float* __restrict__ dO, const float* __restrict__ Lg, float* __restrict__ delta,
     float* __restrict__ dQ, int nh, int T, int BH, int n_qtiles, RowStrides sq, RowStrides sk,
-    RowStrides sv, RowStrides sdo, LStrides sl, RowStrides sdq, float scale, float scale_log2) {
+    RowStrides sv, RowStrides sdo, LStrides sl, RowStrides sdq, float scale, float scale_log2,
+    const float* __restrict__ Og = nullptr, RowStrides so = {}) {
   constexpr int BN = BwdTile<HS>::BN;
   constexpr int BM = 128;
   constexpr int H2 = HS / 2;
@@ -129,6 +133,7 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
 
   float qf[H2], dof[H2];
   float l2 = 0.0f, dl = 0.0f;  // L_i * log2(e) and delta_i of this lane's row
+  float part[FORM_DELTA ? H2 / 4 : 1];  // delta's per-chunk products (FORM_DELTA)
   if (my_i < T) {
     const float* qp = Q + b * sq.b + h * sq.h + (int64_t)my_i * sq.t + half * H2;
     const float* gp = dO + b * sdo.b + h * sdo.h + (int64_t)my_i * sdo.t + half * H2;
@@ -140,10 +145,37 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
       dof[4 * c + 0] = g.x; dof[4 * c + 1] = g.y; dof[4 * c + 2] = g.z; dof[4 * c + 3] = g.w;
     }
     l2 = Lg[b * sl.b + h * sl.h + (int64_t)my_i * sl.t] * kLog2e;
-    dl = delta[(int64_t)bh * T + my_i];
+    if constexpr (FORM_DELTA) {
+      // The delta kernel's per-float4 products (chunk c = half * H2/4 + u of the row), then its
+      // xor tree over chunks: offset H2/4 pairs the two wave halves, the smaller ones chunks
+      // u and u ^ off of this lane.
+      const float* op = Og + b * so.b + h * so.h + (int64_t)my_i * so.t + half * H2;
+#pragma unroll
+      for (int c = 0; c < H2 / 4; ++c) {
+        const float4 o = ld4(op + 4 * c);
+        const float4 g = make_float4(dof[4 * c], dof[4 * c + 1], dof[4 * c + 2], dof[4 * c + 3]);
+        part[c] = o.x * g.x + o.y * g.y + o.z * g.z + o.w * g.w;
+      }
+    } else {
+      dl = delta[(int64_t)bh * T + my_i];
+    }
   } else {
 #pragma unroll
     for (int c = 0; c < H2; ++c) { qf[c] = 0.0f; dof[c] = 0.0f; }
+  }
+  if constexpr (FORM_DELTA) {
+    // Rows past T: every chunk 0 (both halves take part in the exchange).
+#pragma unroll
+    for (int c = 0; c < H2 / 4; ++c) {
+      if (my_i >= T) part[c] = 0.0f;
+      part[c] = part[c] + xor32(part[c]);
+    }
+#pragma unroll
+    for (int off = H2 / 8; off >= 1; off >>= 1)
+#pragma unroll
+      for (int c = 0; c < off; ++c) part[c] = part[c] + part[c + off];
+    dl = part[0];
+    if (my_i < T && half == 0) delta[(int64_t)bh * T + my_i] = dl;
   }
 
   f32x16 dqacc[HS / 32];
@@ -859,13 +891,20 @@ void launch_delta(const float* o, const float* d_o, float* delta, int nh, int T,
                      T, rows, so, sdo);
 }
 
+// With o != nullptr the kernel forms delta from O (strides so) and writes it into `delta`.
 template <int HS, bool CAUSAL>
 void launch_dq(const float* q, const float* k, const float* v, const float* d_o, const float* l,
-               const float* delta, float* dq, int nh, int T, int BH, RowStrides sq,
+               float* delta, float* dq, int nh, int T, int BH, RowStrides sq,
                RowStrides sk, RowStrides sv, RowStrides sdo, LStrides sl, RowStrides sdq,
-               float scale, hipStream_t st) {
+               float scale, hipStream_t st, const float* o = nullptr, RowStrides so = {}) {
   const int n_qtiles = (T + 127) / 128;
   const int64_t items = (int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH;
+  if (o != nullptr) {
+    hipLaunchKernelGGL((fa2_bwd_dq_kernel<HS, CAUSAL, true>), dim3(xcd_grid(items)), dim3(256),
+                       0, st, q, k, v, d_o, l, delta, dq, nh, T, BH, n_qtiles, sq, sk, sv, sdo,
+                       sl, sdq, scale, scale * kLog2e, o, so);
+    return;
+  }
   hipLaunchKernelGGL((fa2_bwd_dq_kernel<HS, CAUSAL>), dim3(xcd_grid(items)), dim3(256), 0,
                      st, q, k, v, d_o, l, delta, dq, nh, T, BH, n_qtiles, sq, sk, sv, sdo, sl,
                      sdq, scale, scale * kLog2e);
@@ -1016,17 +1055,19 @@ namespace {
 // Strides of a dense (B, nh, T, hs) output.
 RowStrides dense_out(int64_t nh, int64_t T, int64_t hs) { return {nh * T * hs, T * hs, hs}; }
 
+// With o != nullptr, dQ forms delta itself (from O, strides so) and writes it into `delta`.
 int bwd_dq_impl(const float* q, const int64_t* q_strides, const float* k,
                 const int64_t* k_strides, const float* v, const int64_t* v_strides,
                 const float* d_o, const int64_t* do_strides, const float* l,
-                const int64_t* l_strides, const float* delta, int64_t B, int64_t nh, int64_t T,
-                int64_t hs, int causal, float* dq, RowStrides sdq, hipStream_t st) {
+                const int64_t* l_strides, float* delta, int64_t B, int64_t nh, int64_t T,
+                int64_t hs, int causal, float* dq, RowStrides sdq, hipStream_t st,
+                const float* o = nullptr, RowStrides so = {}) {
   const float scale = 1.0f / std::sqrt(static_cast<float>(hs));
   const LStrides sl{l_strides[0], l_strides[1], l_strides[2]};
   const int BH = (int)(B * nh);
   dispatch_hs_causal(hs, causal, [&]<int HS, bool C>() {
     launch_dq<HS, C>(q, k, v, d_o, l, delta, dq, (int)nh, (int)T, BH, rs(q_strides),
-                     rs(k_strides), rs(v_strides), rs(do_strides), sl, sdq, scale, st);
+                     rs(k_strides), rs(v_strides), rs(do_strides), sl, sdq, scale, st, o, so);
   });
   return check_launch("flash_attention_bwd_dq");
 }
@@ -1062,8 +1103,31 @@ extern "C" int cta_flash_attention_bwd_dq(const float* q, const int64_t* q_strid
                                 l_strides, delta))
     return rc;
   if (!dq || !aligned16(dq)) return fail(CTA_ERR_LAYOUT, "dQ must be a 16-byte aligned pointer");
+  // (read only: without O the kernel reads delta)
   return bwd_dq_impl(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l, l_strides,
-                     delta, B, nh, T, hs, causal, dq, dense_out(nh, T, hs), as_stream(stream));
+                     const_cast<float*>(delta), B, nh, T, hs, causal, dq, dense_out(nh, T, hs),
+                     as_stream(stream));
+}
+
+extern "C" int cta_flash_attention_bwd_dq_delta(
+    const float* q, const int64_t* q_strides, const float* k, const int64_t* k_strides,
+    const float* v, const int64_t* v_strides, const float* o, const int64_t* o_strides,
+    const float* d_o, const int64_t* do_strides, const float* l, const int64_t* l_strides,
+    int64_t B, int64_t nh, int64_t T, int64_t hs, int causal, float* delta, float* dq,
+    void* stream) {
+  if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
+  if (B * nh * T == 0) return CTA_OK;
+  if (!attn_layout_ok(o, o_strides))
+    return fail(CTA_ERR_LAYOUT,
+                "flash_attention_bwd needs unit d-stride, strides divisible by 4, time strides below 2^23 and 16-byte "
+                "aligned O/dO");
+  if (int rc = check_bwd_inputs(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l,
+                                l_strides, delta))
+    return rc;
+  if (!dq || !aligned16(dq)) return fail(CTA_ERR_LAYOUT, "dQ must be a 16-byte aligned pointer");
+  return bwd_dq_impl(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l, l_strides,
+                     delta, B, nh, T, hs, causal, dq, dense_out(nh, T, hs), as_stream(stream), o,
+                     rs(o_strides));
 }
 
 extern "C" int cta_flash_attention_bwd_dkdv(const float* q, const int64_t* q_strides,
@@ -1156,9 +1220,20 @@ extern "C" int cta_flash_attention_bwd_strided(
     const int64_t* dq_strides, float* dk, const int64_t* dk_strides, float* dv,
     const int64_t* dv_strides, float* delta, float* workspace, int64_t workspace_bytes,
     void* stream) {
-  if (int rc = cta_flash_attention_bwd_delta(o, o_strides, d_o, do_strides, B, nh, T, hs, delta,
-                                             stream))
-    return rc;
+  const int64_t head_bytes = cta_flash_attention_bwd_workspace(1, 1, T, hs, causal);
+  const bool stored = workspace != nullptr && head_bytes != 0 && workspace_bytes >= head_bytes;
+  if (stored) {
+    if (int rc = cta_flash_attention_bwd_delta(o, o_strides, d_o, do_strides, B, nh, T, hs,
+                                               delta, stream))
+      return rc;
+  } else {
+    // the recompute schedule's dQ stage forms delta itself: the delta pass's checks only
+    if (int rc = check_attn_sizes(B, nh, T, hs)) return rc;
+    if (B * nh * T > 0 && (!attn_layout_ok(o, o_strides) || !attn_layout_ok(d_o, do_strides)))
+      return fail(CTA_ERR_LAYOUT,
+                  "flash_attention_bwd needs unit d-stride, strides divisible by 4, time strides below 2^23 and 16-byte "
+                  "aligned O/dO");
+  }
   if (B * nh * T == 0) return CTA_OK;
   if (int rc = check_bwd_inputs(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l,
                                 l_strides, delta))
@@ -1170,11 +1245,12 @@ extern "C" int cta_flash_attention_bwd_strided(
                 "aligned dQ/dK/dV");
   const RowStrides sdq = rs(dq_strides), sdk = rs(dk_strides), sdv = rs(dv_strides);
   hipStream_t st = as_stream(stream);
-  const int64_t head_bytes = cta_flash_attention_bwd_workspace(1, 1, T, hs, causal);
-  if (workspace == nullptr || head_bytes == 0 || workspace_bytes < head_bytes) {
-    // The reference's schedule: dQ recomputes S and dP.
+  if (!stored) {
+    // The reference's schedule: dQ recomputes S and dP, and forms delta for dK/dV on the way
+    // (no delta launch).
     if (int rc = bwd_dq_impl(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l,
-                             l_strides, delta, B, nh, T, hs, causal, dq, sdq, st))
+                             l_strides, delta, B, nh, T, hs, causal, dq, sdq, st, o,
+                             rs(o_strides)))
       return rc;
     return bwd_dkdv_impl(q, q_strides, k, k_strides, v, v_strides, d_o, do_strides, l,
                          l_strides, delta, B, nh, T, hs, causal, dk, sdk, dv, sdv, st);

@@ -4,8 +4,8 @@
 // caller.  Callers that cannot allocate device memory at all (code under HIP graph capture,
 // tight serving loops, harnesses that forbid hipMalloc) call cta_flash_attention_bwd_noalloc
 // instead: delta lives in the file-scope device array `scratch` below, and the backward runs
-// the reference's schedule (delta, dQ recomputing S and dP, dK/dV), which needs no other
-// scratch.  The kernels are those of cta_flash_attention_bwd with a NULL workspace, so the
+// the reference's schedule (dQ recomputing S and dP and forming delta, then dK/dV), which needs
+// no other scratch.  The kernels are those of cta_flash_attention_bwd with a NULL workspace, so the
 // results are bitwise identical to that call.
 //
 // The array is part of this library's code object: every GPU the library runs on holds its own
@@ -13,8 +13,8 @@
 // (on the host that name is a stand-in, not a device address); it passes the device address
 // hipGetSymbolAddress returns, resolved once per device on the first call with that device
 // current.  Every call on one GPU shares that GPU's copy: calls that overlap on one GPU (two
-// streams, or two host threads) race on delta.  Nothing in it needs to start at zero: the
-// delta kernel writes every entry the later kernels read, in stream order.
+// streams, or two host threads) race on delta.  Nothing in it needs to start at zero: the dQ
+// kernel writes every entry the dK/dV kernel reads, in stream order.
 #include "cta_common.hpp"
 
 #include <mutex>

@@ -243,6 +243,20 @@ int cta_flash_attention_bwd_dq(const float* q, const int64_t* q_strides,
                                int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
                                float* dq, void* stream);
 
+/* Stages 1 and 2 in one launch: dQ as cta_flash_attention_bwd_dq, forming delta itself from O
+ * and dO (the same bits as cta_flash_attention_bwd_delta) and writing it to `delta` (dense
+ * (B,nh,T)) for the dK/dV stage.  Replaces the flash_attention_bwd_delta and
+ * flash_attention_bwd_dq launches (flash_attn_launcher.cu:107-108,111,118,125) of the
+ * reference's schedule; cta_flash_attention_bwd runs it when it has no dS workspace. */
+int cta_flash_attention_bwd_dq_delta(const float* q, const int64_t* q_strides,
+                                     const float* k, const int64_t* k_strides,
+                                     const float* v, const int64_t* v_strides,
+                                     const float* o, const int64_t* o_strides,
+                                     const float* d_o, const int64_t* do_strides,
+                                     const float* l, const int64_t* l_strides,
+                                     int64_t B, int64_t nh, int64_t T, int64_t hs, int causal,
+                                     float* delta, float* dq, void* stream);
+
 /* Stage 3: dK and dV.  Replaces the flash_attention_bwd_dk_dv launch
  * (flash_attn_launcher.cu:114,121,131). */
 int cta_flash_attention_bwd_dkdv(const float* q, const int64_t* q_strides,

@@ -281,6 +281,47 @@ def test_fa2_through_c_abi(cuda):
                   s4, B, nh, T, 96, 1, O.data_ptr(), L.data_ptr(), st)
 
 
+@pytest.mark.parametrize("B,nh,T,hs,causal", [(1, 2, 97, 64, True), (2, 3, 300, 32, False),
+                                              (1, 2, 513, 128, True), (1, 1, 1, 64, True),
+                                              (2, 2, 1000, 64, False)])
+def test_fa2_dq_forms_delta(cuda, B, nh, T, hs, causal):
+    """The reference schedule's dQ stage with delta formed inside it
+    (cta_flash_attention_bwd_dq_delta, what cta_flash_attention_bwd runs without a workspace)
+    against the delta pass followed by the plain dQ stage: delta and dQ bitwise equal, O read
+    through a strided view; the combined backward's delta output is those bits too."""
+    from cuda_transformer.ops import flash_attention_fwd
+    from cuda_transformer_amd import capi
+
+    q, k, v, do = (t.to(cuda) for t in _inputs(B, nh, T, hs, seed=880 + T + hs, do_kind="randn"))
+    O, L = flash_attention_fwd(q, k, v, causal)
+    Ob = torch.zeros(B, nh, T, hs + 8, device=cuda)
+    Ob[..., :hs] = O
+    Ov = Ob[..., :hs]  # strided O (time stride hs + 8)
+    st = torch.cuda.current_stream().cuda_stream
+    s4, s3, so = capi.strides(q.stride()), capi.strides(L.stride()), capi.strides(Ov.stride())
+    delta_a = torch.full((B, nh, T), float("nan"), device=cuda)
+    dq_a = torch.full_like(q, float("nan"))
+    capi.call("cta_flash_attention_bwd_delta", Ov.data_ptr(), so, do.data_ptr(), s4, B, nh, T, hs,
+              delta_a.data_ptr(), st)
+    capi.call("cta_flash_attention_bwd_dq", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(), s4,
+              do.data_ptr(), s4, L.data_ptr(), s3, delta_a.data_ptr(), B, nh, T, hs, int(causal),
+              dq_a.data_ptr(), st)
+    delta_b = torch.full((B, nh, T), float("nan"), device=cuda)
+    dq_b = torch.full_like(q, float("nan"))
+    capi.call("cta_flash_attention_bwd_dq_delta", q.data_ptr(), s4, k.data_ptr(), s4,
+              v.data_ptr(), s4, Ov.data_ptr(), so, do.data_ptr(), s4, L.data_ptr(), s3, B, nh, T,
+              hs, int(causal), delta_b.data_ptr(), dq_b.data_ptr(), st)
+    out = [torch.empty_like(q) for _ in range(3)] + [torch.full((B, nh, T), float("nan"),
+                                                                device=cuda)]
+    capi.call("cta_flash_attention_bwd", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(), s4,
+              Ov.data_ptr(), so, do.data_ptr(), s4, L.data_ptr(), s3, B, nh, T, hs, int(causal),
+              *(t.data_ptr() for t in out), None, 0, st)
+    torch.cuda.synchronize()
+    assert torch.equal(delta_b, delta_a) and torch.equal(out[3], delta_a)
+    assert torch.equal(dq_b, dq_a) and torch.equal(out[0], dq_a)
+    np.testing.assert_allclose(f64(delta_a), (f64(O) * f64(do)).sum(-1), rtol=1e-5, atol=1e-5)
+
+
 PACKED_SHAPES = [(2, 65, 3, 64, True), (1, 257, 2, 32, False), (2, 130, 2, 128, True),
                  (4, 256, 6, 64, True), (1, 1, 2, 64, True)]
 
