@@ -44,6 +44,19 @@ __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast
 __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
 __device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
 
+// Streaming (non-temporal) 16-byte load and store, for data touched once per pass whose total
+// far exceeds the caches (the stored dS tiles): the access carries the `nt` bit, so it does not
+// displace the reused K/V/Q rows from L2.
+typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld4_stream(const float* p) {
+  const nt_f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const nt_f32x4*>(p));
+  return make_float4(x[0], x[1], x[2], x[3]);
+}
+__device__ __forceinline__ void st4_stream(float* p, float4 v) {
+  const nt_f32x4 x = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(x, reinterpret_cast<nt_f32x4*>(p));
+}
+
 // 16-bit MFMA (gfx950 v_mfma_f32_32x32x16_bf16 / _f16), checked on an MI355X for BF16 and
 // shared by the FP16 form:
 //   A (32 x 16): lane l supplies A[l % 32][8 (l/32) + j], j = 0..7
@@ -71,6 +84,15 @@ using vec8_t = typename Half16<E>::vec8;
 template <class E>
 __device__ __forceinline__ vec8_t<E> ld8(const E* p) {
   return *reinterpret_cast<const vec8_t<E>*>(p);
+}
+// Streaming forms of the 16-byte 16-bit vector access, for the stored dS tiles.
+template <class E>
+__device__ __forceinline__ vec8_t<E> ld8_stream(const E* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const vec8_t<E>*>(p));
+}
+template <class E>
+__device__ __forceinline__ void st8_stream(E* p, vec8_t<E> v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<vec8_t<E>*>(p));
 }
 // A 32x32 score tile in registers (lane l: rows R(r, l/32)) is the B operand of two 16-deep
 // BF16 MFMA steps: step s takes registers 8s .. 8s+7, i.e. rows 16 s + 8 (j/4) + 4 h + j%4 of

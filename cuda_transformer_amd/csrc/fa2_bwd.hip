@@ -494,7 +494,7 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
       wave_lds_fence();
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        st4(gt + 256 * g + 4 * lane, ld4(xw + col * kDsPitch + 8 * g + 4 * half));
+        st4_stream(gt + 256 * g + 4 * lane, ld4(xw + col * kDsPitch + 8 * g + 4 * half));
       wave_lds_fence();
     }
   };
@@ -820,7 +820,9 @@ __global__ __launch_bounds__(64 * WAVES, 2) void fa2_bwd_dq_ds_kernel(
       const int jbc = min(stage * NSUB + sub, CAUSAL ? ibc : nb - 1);
       const float* src = dsh + ds_tile_index(ibc, jbc, nb, CAUSAL) * kDsTileFloats + 4 * lane;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) dr[sub][g] = ld4(src + 256 * g);
+      for (int g = 0; g < 4; ++g) {
+        dr[sub][g] = ld4_stream(src + 256 * g);
+      }
     }
   };
   auto compute = [&](int stage, const float* ks, const float4 (&dr)[NSUB][4]) {

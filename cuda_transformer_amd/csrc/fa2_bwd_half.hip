@@ -271,8 +271,7 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
       wave_lds_fence();
 #pragma unroll
       for (int s = 0; s < 2; ++s)
-        *reinterpret_cast<vec8_t<E>*>(gtile + 8 * (32 * (2 * s + half) + col)) =
-            ld8<E>(xs + col * XP + 16 * s + 8 * half);
+        st8_stream<E>(gtile + 8 * (32 * (2 * s + half) + col), ld8<E>(xs + col * XP + 16 * s + 8 * half));
       wave_lds_fence();
     }
   };
@@ -520,7 +519,7 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_ds_half_ker
       const int jbc = min(stage * NSUB + sub, CAUSAL ? ibc : nb - 1);
       const E* src = dsh + ds_tile_index(ibc, jbc, nb, CAUSAL) * kDsTileHalf;
 #pragma unroll
-      for (int s = 0; s < 2; ++s) dr[sub][s] = ld8<E>(src + 8 * (32 * (2 * s + half) + col));
+      for (int s = 0; s < 2; ++s) dr[sub][s] = ld8_stream<E>(src + 8 * (32 * (2 * s + half) + col));
     }
   };
   auto compute = [&](int stage, const E* kt, const vec8_t<E> (&dr)[NSUB][2]) {
