@@ -173,6 +173,37 @@ inline unsigned xcd_grid(int64_t total) {
   return (unsigned)(kNumXcds * ((total + kNumXcds - 1) / kNumXcds));
 }
 
+// Causal attention tiles cost unequal amounts (a query tile's keys, or a key tile's queries,
+// grow along the diagonal).  The kernels pair tile p with tile n-1-p so every work item costs
+// the same, or, where lpt_heads() says so, run single tiles longest first per XCD: XCD x takes
+// heads [x h, (x+1) h) (h = lpt_heads) and walks their tiles tile-major, head-minor, so rank 0
+// (the longest tile) of each of its heads comes first.  Grid = BH * n_tiles workgroups.
+__device__ __forceinline__ void lpt_tile(int hw_id, int heads_per_xcd, int& bh, int& rank) {
+  const int x = hw_id % kNumXcds, slot = hw_id / kNumXcds;
+  rank = slot / heads_per_xcd;
+  bh = x * heads_per_xcd + (slot - rank * heads_per_xcd);
+}
+
+// Heads per XCD for longest-first tiles, or 0 for pairs.  Equal pairs end a grid in a partial
+// round when their count is not a multiple of the resident workgroups, and a grid of fewer
+// pairs than resident slots leaves SIMDs at one wave.  Longest-first tiles win when each XCD
+// runs at least two and a half rounds of them (the dispatcher ends on the shortest), or when
+// all of an XCD's tiles are resident at once with two-wave workgroups or one workgroup per CU
+// (the makespan is the longest tile, n units, against n + 1 for a pair, with more SIMDs busy).
+// Between one and two and a half rounds, or with several four-wave tiles on one CU, the
+// unequal tiles that share a CU cost more than that, and pairs stay.  `waves` per workgroup,
+// `occ` waves per SIMD the kernel holds; BH must split evenly over the XCDs.
+constexpr int kNumSimds = 1024;
+inline int lpt_heads(int64_t BH, int n_tiles, int waves, int occ) {
+  if (BH % kNumXcds != 0 || n_tiles < 2) return 0;
+  const int64_t tiles = BH / kNumXcds * n_tiles;                       // per XCD
+  const int64_t slots = (int64_t)occ * (kNumSimds / kNumXcds) / waves;  // resident per XCD
+  const int64_t cus = kNumSimds / kNumXcds / 4;
+  const bool many = 2 * tiles >= 5 * slots;
+  const bool one_round = tiles <= slots && (waves == 2 || tiles <= cus);
+  return many || one_round ? (int)(BH / kNumXcds) : 0;
+}
+
 // Stored dS tiles of the backward (FA2, FP32 and BF16).  Tile (ib, jb) covers query rows
 // 32*ib.. and key rows 32*jb.. of one head; causal heads keep the tiles with jb <= ib only,
 // packed row by row.

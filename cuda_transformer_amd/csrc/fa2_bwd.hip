@@ -100,7 +100,7 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
     const float* __restrict__ dO, const float* __restrict__ Lg, float* __restrict__ delta,
     float* __restrict__ dQ, int nh, int T, int BH, int n_qtiles, RowStrides sq, RowStrides sk,
     RowStrides sv, RowStrides sdo, LStrides sl, RowStrides sdq, float scale, float scale_log2,
-    const float* __restrict__ Og = nullptr, RowStrides so = {}) {
+    const float* __restrict__ Og = nullptr, RowStrides so = {}, int heads_per_xcd = 0) {
   constexpr int BN = BwdTile<HS>::BN;
   constexpr int BM = 128;
   constexpr int H2 = HS / 2;
@@ -114,20 +114,30 @@ __global__ __launch_bounds__(256, BwdTile<HS>::MINW) void fa2_bwd_dq_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
   const int half = lane >> 5, col = lane & 31;
-  // Head-major items over XCDs; causal items are query-tile pairs (n-1-p, p) of equal cost.
-  const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
-  const int w = xcd_work_item(blockIdx.x, BH * per_head);
-  if (w >= BH * per_head) return;
-  const int bh = w / per_head;
-  const int p = w - bh * per_head;
+  // Head-major items over XCDs; causal items are query-tile pairs (n-1-p, p) of equal cost, or
+  // (heads_per_xcd > 0) single query tiles longest first per XCD (lpt_tile).
+  int bh, qa, qb = -1;  // the item's query tiles, in pass order (qb < 0: one pass)
+  if (CAUSAL && heads_per_xcd > 0) {
+    int rank;
+    lpt_tile(blockIdx.x, heads_per_xcd, bh, rank);
+    qa = n_qtiles - 1 - rank;
+  } else {
+    const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+    const int w = xcd_work_item(blockIdx.x, BH * per_head);
+    if (w >= BH * per_head) return;
+    bh = w / per_head;
+    const int p = w - bh * per_head;
+    qa = CAUSAL ? n_qtiles - 1 - p : p;
+    if (CAUSAL && n_qtiles - 1 - p != p) qb = p;
+  }
   const int b = bh / nh, h = bh - b * nh;
 
   const float* Kb = K + b * sk.b + h * sk.h;
   const float* Vb = V + b * sv.b + h * sv.h;
 
-  const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
+  const int n_pass = qb >= 0 ? 2 : 1;
   for (int pass = 0; pass < n_pass; ++pass) {
-  const int qt = CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p;
+  const int qt = pass == 0 ? qa : qb;
   const int i0 = qt * BM + wave * 32;
   const int my_i = i0 + col;
 
@@ -328,7 +338,8 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
     const float* __restrict__ delta, float* __restrict__ dK, float* __restrict__ dV,
     float* __restrict__ dsw, int nh, int T, int bh_base, int BH, int n_ktiles, RowStrides sq,
     RowStrides sk, RowStrides sv, RowStrides sdo, RowStrides so, LStrides sl, RowStrides sdk,
-    RowStrides sdv, float scale, float scale_log2, float* __restrict__ part_ws = nullptr) {
+    RowStrides sdv, float scale, float scale_log2, float* __restrict__ part_ws = nullptr,
+    int heads_per_xcd = 0) {
   constexpr int BN = DkdvTile<HS>::BN;
   constexpr int NSUB = BN / 32;
   constexpr int THREADS = 64 * WAVES;
@@ -350,15 +361,24 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
   const int half = lane >> 5, col = lane & 31;
-  // Head-major items over XCDs; causal items are key-tile pairs (p, n-1-p) of equal cost.
-  const int per_head = CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles;
-  const int n_items = BH * per_head * (SPLIT ? 2 : 1);
-  const int w = xcd_work_item(blockIdx.x, n_items);
-  if (w >= n_items) return;
-  const int item = SPLIT ? w >> 1 : w;
-  const int part = SPLIT ? w & 1 : 0;  // the two parts of an item are neighbours: one XCD
-  const int bh_local = item / per_head;
-  const int p = item - bh_local * per_head;
+  // Head-major items over XCDs; causal items are key-tile pairs (p, n-1-p) of equal cost, or
+  // (heads_per_xcd > 0, unsplit) single key tiles longest first per XCD (lpt_tile).
+  int bh_local, part = 0;
+  int ka, kb = -1;  // the item's key tiles, in pass order (kb < 0: one pass)
+  if (CAUSAL && !SPLIT && heads_per_xcd > 0) {
+    lpt_tile(blockIdx.x, heads_per_xcd, bh_local, ka);  // key tile 0 is the longest
+  } else {
+    const int per_head = CAUSAL ? (n_ktiles + 1) / 2 : n_ktiles;
+    const int n_items = BH * per_head * (SPLIT ? 2 : 1);
+    const int w = xcd_work_item(blockIdx.x, n_items);
+    if (w >= n_items) return;
+    const int item = SPLIT ? w >> 1 : w;
+    part = SPLIT ? w & 1 : 0;  // the two parts of an item are neighbours: one XCD
+    bh_local = item / per_head;
+    const int p = item - bh_local * per_head;
+    ka = p;
+    if (CAUSAL && n_ktiles - 1 - p != p) kb = n_ktiles - 1 - p;
+  }
   const int bh = bh_base + bh_local;
   const int b = bh / nh, h = bh - b * nh;
 
@@ -390,8 +410,8 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
   for (int e = 4 * tid; e < 2 * STAGE; e += 4 * THREADS) st4(smem + e, zero4());
   __syncthreads();
 
-  const int n_pass = (CAUSAL && n_ktiles - 1 - p != p) ? 2 : 1;
-  auto kt_of = [&](int pass) { return CAUSAL ? (pass == 0 ? p : n_ktiles - 1 - p) : p; };
+  const int n_pass = kb >= 0 ? 2 : 1;
+  auto kt_of = [&](int pass) { return pass == 0 ? ka : kb; };
   const int n_stages = (T + BN - 1) / BN;
   // first query stage that can see the keys of tile kt
   auto q_begin_of = [&](int kt) { return CAUSAL ? (kt * BM / BN) : 0; };
@@ -509,7 +529,8 @@ __global__ __launch_bounds__(64 * WAVES, DkdvTile<HS>::MINW) void fa2_bwd_dkdv_k
   const int i_begin = SPLIT ? min(max(g0 - pos, 0), n_steps) : 0;
   const int i_end = SPLIT ? min(max(g1 - pos, 0), n_steps) : n_steps;
   pos += n_steps;
-  const bool down = CAUSAL && pass == 0;
+  // (the long tile of a pair walks down: a property of the tile, so single tiles match pairs)
+  const bool down = CAUSAL && kt <= n_ktiles - 1 - kt;
   auto stage_at = [&](int i) { return down ? n_stages - 1 - i : q_begin + i; };
   if (i_begin < i_end) issue(stage_at(i_begin), 0);
   vm_wait_all();
@@ -720,7 +741,7 @@ template <int HS, bool CAUSAL, int WAVES = 4, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WAVES, 2) void fa2_bwd_dq_ds_kernel(
     const float* __restrict__ K, const float* __restrict__ dsw, float* __restrict__ dQ, int nh,
     int T, int bh_base, int BH, int n_qtiles, RowStrides sk, RowStrides sdq, float scale,
-    float* __restrict__ part_ws = nullptr) {
+    float* __restrict__ part_ws = nullptr, int heads_per_xcd = 0) {
   constexpr int BN = 64;
   constexpr int NSUB = BN / 32;
   constexpr int THREADS = 64 * WAVES;
@@ -735,23 +756,34 @@ __global__ __launch_bounds__(64 * WAVES, 2) void fa2_bwd_dq_ds_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
   const int half = lane >> 5, col = lane & 31;
-  // Head-major items over XCDs; causal items are query-tile pairs (n-1-p, p) of equal cost.
-  const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
-  const int n_items = BH * per_head * (SPLIT ? 2 : 1);
-  const int w = xcd_work_item(blockIdx.x, n_items);
-  if (w >= n_items) return;
-  const int item = SPLIT ? w >> 1 : w;
-  const int part = SPLIT ? w & 1 : 0;
-  const int bh_local = item / per_head;
-  const int p = item - bh_local * per_head;
+  // Head-major items over XCDs; causal items are query-tile pairs (n-1-p, p) of equal cost, or
+  // (heads_per_xcd > 0, unsplit) single query tiles longest first per XCD (lpt_tile).
+  int bh_local, part = 0;
+  int qa, qb = -1;  // the item's query tiles, in pass order (qb < 0: one pass)
+  if (CAUSAL && !SPLIT && heads_per_xcd > 0) {
+    int rank;
+    lpt_tile(blockIdx.x, heads_per_xcd, bh_local, rank);
+    qa = n_qtiles - 1 - rank;
+  } else {
+    const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+    const int n_items = BH * per_head * (SPLIT ? 2 : 1);
+    const int w = xcd_work_item(blockIdx.x, n_items);
+    if (w >= n_items) return;
+    const int item = SPLIT ? w >> 1 : w;
+    part = SPLIT ? w & 1 : 0;
+    bh_local = item / per_head;
+    const int p = item - bh_local * per_head;
+    qa = CAUSAL ? n_qtiles - 1 - p : p;
+    if (CAUSAL && n_qtiles - 1 - p != p) qb = p;
+  }
   const int bh = bh_base + bh_local;
   const int b = bh / nh, h = bh - b * nh;
   const float* Kb = K + b * sk.b + h * sk.h;
   const int nb = (T + 31) / 32;
   const float* dsh = dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileFloats;
 
-  const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
-  auto qt_of = [&](int pass) { return CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p; };
+  const int n_pass = qb >= 0 ? 2 : 1;
+  auto qt_of = [&](int pass) { return pass == 0 ? qa : qb; };
   auto stages_of = [&](int qt) {
     const int kv_end = CAUSAL ? min(T, (qt + 1) * BM) : T;
     return (kv_end + BN - 1) / BN;
@@ -901,15 +933,17 @@ void launch_dq(const float* q, const float* k, const float* v, const float* d_o,
                float scale, hipStream_t st, const float* o = nullptr, RowStrides so = {}) {
   const int n_qtiles = (T + 127) / 128;
   const int64_t items = (int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH;
+  const int lpt = CAUSAL ? lpt_heads(BH, n_qtiles, 4, BwdTile<HS>::MINW) : 0;
+  const dim3 grid(lpt > 0 ? (unsigned)(BH * n_qtiles) : xcd_grid(items));
   if (o != nullptr) {
-    hipLaunchKernelGGL((fa2_bwd_dq_kernel<HS, CAUSAL, true>), dim3(xcd_grid(items)), dim3(256),
-                       0, st, q, k, v, d_o, l, delta, dq, nh, T, BH, n_qtiles, sq, sk, sv, sdo,
-                       sl, sdq, scale, scale * kLog2e, o, so);
+    hipLaunchKernelGGL((fa2_bwd_dq_kernel<HS, CAUSAL, true>), grid, dim3(256), 0, st, q, k, v,
+                       d_o, l, delta, dq, nh, T, BH, n_qtiles, sq, sk, sv, sdo, sl, sdq, scale,
+                       scale * kLog2e, o, so, lpt);
     return;
   }
-  hipLaunchKernelGGL((fa2_bwd_dq_kernel<HS, CAUSAL>), dim3(xcd_grid(items)), dim3(256), 0,
-                     st, q, k, v, d_o, l, delta, dq, nh, T, BH, n_qtiles, sq, sk, sv, sdo, sl,
-                     sdq, scale, scale * kLog2e);
+  hipLaunchKernelGGL((fa2_bwd_dq_kernel<HS, CAUSAL>), grid, dim3(256), 0, st, q, k, v, d_o, l,
+                     delta, dq, nh, T, BH, n_qtiles, sq, sk, sv, sdo, sl, sdq, scale,
+                     scale * kLog2e, nullptr, RowStrides{}, lpt);
 }
 
 // dK/dV for heads [bh_base, bh_base + n_heads), written through strides sdk / sdv; with
@@ -937,10 +971,12 @@ void launch_dkdv(const float* q, const float* k, const float* v, const float* d_
                          dv, part_ws, nh, T, rows, sdk, sdv);
       return;
     }
+    const int lpt = CAUSAL ? lpt_heads(n_heads, n_ktiles, WAVES, DkdvTile<HS>::MINW) : 0;
     hipLaunchKernelGGL((fa2_bwd_dkdv_kernel<HS, CAUSAL, STORE_DS, FOLD, WAVES>),
-                       dim3(xcd_grid(items)), dim3(64 * WAVES), 0, st, q, k, v, d_o, o, l, delta,
-                       dk, dv, dsw, nh, T, bh_base, n_heads, n_ktiles, sq, sk, sv, sdo, so, sl,
-                       sdk, sdv, scale, scale * kLog2e);
+                       dim3(lpt > 0 ? (unsigned)(n_heads * n_ktiles) : xcd_grid(items)),
+                       dim3(64 * WAVES), 0, st, q, k, v, d_o, o, l, delta, dk, dv, dsw, nh, T,
+                       bh_base, n_heads, n_ktiles, sq, sk, sv, sdo, so, sl, sdk, sdv, scale,
+                       scale * kLog2e, nullptr, lpt);
   };
   // Short causal heads (hs 64, T <= 1024) run two waves (64 keys) per workgroup: the half-empty
   // diagonal blocks idle fewer waves at each stage's barrier and the pairs balance over more,
@@ -975,9 +1011,11 @@ void launch_dq_ds(const float* k, const float* dsw, float* dq, int nh, int T, in
                          part_ws, nh, T, rows, sdq);
       return;
     }
-    hipLaunchKernelGGL((fa2_bwd_dq_ds_kernel<HS, CAUSAL, WAVES>), dim3(xcd_grid(items)),
+    const int lpt = CAUSAL ? lpt_heads(n_heads, n_qtiles, WAVES, 2) : 0;
+    hipLaunchKernelGGL((fa2_bwd_dq_ds_kernel<HS, CAUSAL, WAVES>),
+                       dim3(lpt > 0 ? (unsigned)(n_heads * n_qtiles) : xcd_grid(items)),
                        dim3(64 * WAVES), 0, st, k, dsw, dq, nh, T, bh_base, n_heads, n_qtiles, sk,
-                       sdq, scale);
+                       sdq, scale, nullptr, lpt);
   };
   // Short causal heads (hs 64, T <= 1024): two waves (64 query rows) per workgroup, as in the
   // dK/dV stage.  A/B in one process, bitwise-equal dQ: +11.5% at T = 256, +10% at 512, +5% at

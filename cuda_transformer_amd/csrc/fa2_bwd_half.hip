@@ -427,7 +427,8 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
 template <class E, int HS, bool CAUSAL>
 __global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_ds_half_kernel(
     const E* __restrict__ K, const E* __restrict__ dsw, E* __restrict__ dQ,
-    int nh, int T, int bh_base, int BH, int n_qtiles, RowStridesH sk, float scale) {
+    int nh, int T, int bh_base, int BH, int n_qtiles, RowStridesH sk, float scale,
+    int heads_per_xcd = 0) {
   constexpr int BN = 64;
   constexpr int NSUB = BN / 32;
   constexpr int BM = 128;
@@ -439,20 +440,30 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_ds_half_ker
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
   const int half = lane >> 5, col = lane & 31;
-  const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
-  const int w = xcd_work_item(blockIdx.x, BH * per_head);
-  if (w >= BH * per_head) return;
-  const int bh_local = w / per_head;
-  const int p = w - bh_local * per_head;
+  // query-tile pairs (n-1-p, p), or (heads_per_xcd > 0) single tiles longest first (lpt_tile)
+  int bh_local, qa, qb = -1;
+  if (CAUSAL && heads_per_xcd > 0) {
+    int rank;
+    lpt_tile(blockIdx.x, heads_per_xcd, bh_local, rank);
+    qa = n_qtiles - 1 - rank;
+  } else {
+    const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+    const int w = xcd_work_item(blockIdx.x, BH * per_head);
+    if (w >= BH * per_head) return;
+    bh_local = w / per_head;
+    const int p = w - bh_local * per_head;
+    qa = CAUSAL ? n_qtiles - 1 - p : p;
+    if (CAUSAL && n_qtiles - 1 - p != p) qb = p;
+  }
   const int bh = bh_base + bh_local;
   const int b = bh / nh, h = bh - b * nh;
   const E* Kb = K + b * sk.b + h * sk.h;
   const int nb = (T + 31) / 32;
   const E* dsh = dsw + (int64_t)bh_local * ds_tiles_per_head(T, CAUSAL) * kDsTileHalf;
 
-  const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
+  const int n_pass = qb >= 0 ? 2 : 1;
   for (int pass = 0; pass < n_pass; ++pass) {
-  const int qt = CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p;
+  const int qt = pass == 0 ? qa : qb;
   const int i0 = qt * BM + wave * 32;
   const int my_i = i0 + col;
   const int ib = i0 / 32;
@@ -589,7 +600,7 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_half_kernel
     const E* __restrict__ dO, const E* __restrict__ Og, const float* __restrict__ Lg,
     float* __restrict__ delta, E* __restrict__ dQ, int nh, int T, int BH, int n_qtiles,
     RowStridesH sq, RowStridesH sk, RowStridesH sv, RowStridesH sdo, RowStridesH so,
-    RowStridesH sl, float scale, float scale_log2) {
+    RowStridesH sl, float scale, float scale_log2, int heads_per_xcd = 0) {
   constexpr int BN = 64;             // keys per stage
   constexpr int NSUB = BN / 32;
   constexpr int BM = 128;
@@ -608,18 +619,28 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_half_kernel
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
   const int half = lane >> 5, col = lane & 31;
-  const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
-  const int w = xcd_work_item(blockIdx.x, BH * per_head);
-  if (w >= BH * per_head) return;
-  const int bh = w / per_head;
-  const int p = w - bh * per_head;
+  // query-tile pairs (n-1-p, p), or (heads_per_xcd > 0) single tiles longest first (lpt_tile)
+  int bh, qa, qb = -1;
+  if (CAUSAL && heads_per_xcd > 0) {
+    int rank;
+    lpt_tile(blockIdx.x, heads_per_xcd, bh, rank);
+    qa = n_qtiles - 1 - rank;
+  } else {
+    const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+    const int w = xcd_work_item(blockIdx.x, BH * per_head);
+    if (w >= BH * per_head) return;
+    bh = w / per_head;
+    const int p = w - bh * per_head;
+    qa = CAUSAL ? n_qtiles - 1 - p : p;
+    if (CAUSAL && n_qtiles - 1 - p != p) qb = p;
+  }
   const int b = bh / nh, h = bh - b * nh;
   const E* Kb = K + b * sk.b + h * sk.h;
   const E* Vb = V + b * sv.b + h * sv.h;
 
-  const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
+  const int n_pass = qb >= 0 ? 2 : 1;
   for (int pass = 0; pass < n_pass; ++pass) {
-  const int qt = CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p;
+  const int qt = pass == 0 ? qa : qb;
   const int i0 = qt * BM + wave * 32;
   const int my_i = i0 + col;
 
@@ -730,7 +751,7 @@ __global__ __launch_bounds__(256, HS == 128 ? 1 : 2) void fa2_bwd_dq_half_kernel
     }
   };
 
-  const bool down = CAUSAL && pass == 1;
+  const bool down = CAUSAL && qt < n_qtiles - 1 - qt;  // the short tile of a pair
   auto stage_at = [&](int i) { return down ? n_stages - 1 - i : i; };
   gload(stage_at(0));
   lstore(0);
@@ -937,10 +958,13 @@ int bwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
     // Recompute: dQ first (it forms delta and writes it), then dK/dV, which reads it.
     dispatch_half(hs, causal, [&]<int HS, bool C>() {
       const int64_t items = (int64_t)(C ? (n_tiles + 1) / 2 : n_tiles) * BH;
-      hipLaunchKernelGGL((fa2_bwd_dq_half_kernel<E, HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
+      // waves per SIMD the registers allow (150 / 228 / 356 VGPRs at hs 32 / 64 / 128)
+      const int lq = C ? lpt_heads(BH, n_tiles, 4, HS == 32 ? 3 : HS == 64 ? 2 : 1) : 0;
+      hipLaunchKernelGGL((fa2_bwd_dq_half_kernel<E, HS, C>),
+                         dim3(lq > 0 ? (unsigned)(BH * n_tiles) : xcd_grid(items)), dim3(256), 0,
                          st, qb, kb, vb, gb, ob, l, delta, dqb, (int)nh, (int)T, BH, n_tiles,
                          rsh(q_strides), rsh(k_strides), rsh(v_strides), rsh(do_strides),
-                         rsh(o_strides), sl, scale, scale * kLog2e);
+                         rsh(o_strides), sl, scale, scale * kLog2e, lq);
       using Cfg = DkdvHalfCfg<HS, C>;
       const int n_ktiles = (int)((T + 32 * Cfg::WAVES - 1) / (32 * Cfg::WAVES));
       const int64_t kitems = (int64_t)(C ? (n_ktiles + 1) / 2 : n_ktiles) * BH;
@@ -982,8 +1006,12 @@ int bwd_half(const uint16_t* q, const int64_t* q_strides, const uint16_t* k,
                          rsh(q_strides), rsh(k_strides), rsh(v_strides), rsh(do_strides), sl,
                          scale, scale * kLog2e);
       const int64_t items = (int64_t)(C ? (n_tiles + 1) / 2 : n_tiles) * n;
-      hipLaunchKernelGGL((fa2_bwd_dq_ds_half_kernel<E, HS, C>), dim3(xcd_grid(items)), dim3(256), 0,
-                         st, kb, wsb, dqb, (int)nh, (int)T, h0, n, n_tiles, rsh(k_strides), scale);
+      // waves per SIMD (76 / 100 / 180 VGPRs at hs 32 / 64 / 128; LDS allows four)
+      const int lq = C ? lpt_heads(n, n_tiles, 4, HS == 128 ? 2 : 4) : 0;
+      hipLaunchKernelGGL((fa2_bwd_dq_ds_half_kernel<E, HS, C>),
+                         dim3(lq > 0 ? (unsigned)(n * n_tiles) : xcd_grid(items)), dim3(256), 0,
+                         st, kb, wsb, dqb, (int)nh, (int)T, h0, n, n_tiles, rsh(k_strides), scale,
+                         lq);
     });
     if (int rc = check_launch("flash_attention_bwd (16-bit)")) return rc;
   }

@@ -24,7 +24,9 @@
 //  * Workgroup ids are remapped so each XCD walks a contiguous run of a head-major work list:
 //    the workgroups resident on one XCD share a few heads' K/V in its L2.  With a causal mask a
 //    workgroup takes the query-tile pair (n-1-p, p), so all workgroups cost the same and the
-//    head-major order leaves no long tiles for the end.
+//    head-major order leaves no long tiles for the end; on grids where equal pairs would end in
+//    a partial round (or leave SIMDs at one wave) each XCD instead takes single tiles of its
+//    heads longest first (lpt_heads).
 #include "cta_common.hpp"
 
 namespace cta {
@@ -50,7 +52,8 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ L, int nh, int T, int BH, int n_qtiles,
     RowStrides sq, RowStrides sk, RowStrides sv, RowStrides so, float scale, float scale_log2,
-    float rescale_gap, float* __restrict__ Os = nullptr, float* __restrict__ Ls = nullptr) {
+    float rescale_gap, float* __restrict__ Os = nullptr, float* __restrict__ Ls = nullptr,
+    int heads_per_xcd = 0) {
   constexpr int BN = FwdTile<HS>::BN;
   constexpr int THREADS = 64 * WAVES;
   constexpr int BM = 32 * WAVES;  // query rows per workgroup, 32 per wave
@@ -69,23 +72,35 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   const int half = lane >> 5, col = lane & 31;
   // Work items are head-major and spread over XCDs.  Causal: one item = the query-tile pair
   // (n-1-p, p), so every item costs n+1 tile units and the dynamic dispatch has no tail.
-  const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+  // Causal with heads_per_xcd > 0 (unsplit): one item = one query tile, longest first per XCD
+  // (lpt_tile; grid BH * n_qtiles).
   constexpr bool SPLIT = NSPLIT > 1;
-  const int n_items = BH * per_head * NSPLIT;
-  const int w = xcd_work_item(blockIdx.x, n_items);
-  if (w >= n_items) return;
-  const int item = SPLIT ? w / NSPLIT : w;
-  const int part = SPLIT ? w - item * NSPLIT : 0;  // an item's parts are neighbours: one XCD
-  const int bh = item / per_head;
-  const int p = item - bh * per_head;
+  int bh, part = 0;
+  int qa, qb = -1;  // the item's query tiles, in pass order (qb < 0: one pass)
+  if (CAUSAL && !SPLIT && heads_per_xcd > 0) {
+    int rank;
+    lpt_tile(blockIdx.x, heads_per_xcd, bh, rank);
+    qa = n_qtiles - 1 - rank;
+  } else {
+    const int per_head = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+    const int n_items = BH * per_head * NSPLIT;
+    const int w = xcd_work_item(blockIdx.x, n_items);
+    if (w >= n_items) return;
+    const int item = SPLIT ? w / NSPLIT : w;
+    part = SPLIT ? w - item * NSPLIT : 0;  // an item's parts are neighbours: one XCD
+    bh = item / per_head;
+    const int p = item - bh * per_head;
+    qa = CAUSAL ? n_qtiles - 1 - p : p;
+    if (CAUSAL && n_qtiles - 1 - p != p) qb = p;
+  }
   const int b = bh / nh, h = bh - b * nh;
 
   const float* Qb = Q + b * sq.b + h * sq.h;
   const float* Kb = K + b * sk.b + h * sk.h;
   const float* Vb = V + b * sv.b + h * sv.h;
 
-  const int n_pass = (CAUSAL && n_qtiles - 1 - p != p) ? 2 : 1;
-  auto qt_of = [&](int pass) { return CAUSAL ? (pass == 0 ? n_qtiles - 1 - p : p) : p; };
+  const int n_pass = qb >= 0 ? 2 : 1;
+  auto qt_of = [&](int pass) { return pass == 0 ? qa : qb; };
   auto stages_of = [&](int qt) {
     return ((CAUSAL ? min(T, (qt + 1) * BM) : T) + BN - 1) / BN;
   };
@@ -163,8 +178,10 @@ __global__ __launch_bounds__(64 * WAVES, FwdTile<HS>::MINW) void fa2_fwd_kernel(
   // Stage order.  With a causal mask the second (short) pass walks the K/V stages downward
   // from its last: every workgroup of a head in its first pass reads stage t at step t, and
   // every one in its second pass reads stage 4n+3-t (n query tiles; t counted from the item's
-  // start), so the workgroups of a head share each K/V stage in L2.
-  const bool down = CAUSAL && pass == 1;
+  // start), so the workgroups of a head share each K/V stage in L2.  The direction belongs to
+  // the tile (the short one of its pair walks down), so longest-first single tiles sum in the
+  // same order as pairs and give the same bits.
+  const bool down = CAUSAL && qt < n_qtiles - 1 - qt;
   auto stage_at = [&](int i) { return down ? n_stages - 1 - i : i; };
   if (i_begin < i_end) {  // workgroup-uniform
     gload(stage_at(i_begin));
@@ -361,6 +378,13 @@ int fwd_nsplit(int T, int BH) {
   return n >= 2 ? n : 1;
 }
 
+// Longest-first tiles (lpt_heads), A/B in one process against pairs (outputs within 2e-6: the
+// pairs' short tiles walk their stages downward): B4 H32 N4096 causal +1.3%, hs 32 +2.4%,
+// B8 H16 N2048 +2.5%, B64 H6 T256 +9%, B16 H8 T512 +29%; at 1.33 rounds (B1 H16 N8192,
+// B8 H32 T512) -2.5% / -3%, with 64 four-wave tiles on 32 CUs (B4 H4 N4096) -25%, which the
+// rule keeps on pairs.  The split forward, where it applies, beats both (B2 H8 N1024: 0.060 ms
+// split, 0.084 ms longest-first), so a split launch keeps the pairs.
+
 template <int HS, bool CAUSAL>
 void launch_fwd(const float* q, const float* k, const float* v, float* o, float* l, int nh,
                 int T, int BH, RowStrides sq, RowStrides sk, RowStrides sv, RowStrides so,
@@ -388,9 +412,12 @@ void launch_fwd(const float* q, const float* k, const float* v, float* o, float*
       split.template operator()<2>();
       return;
     }
-    hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL, WAVES>), dim3(xcd_grid(items)),
+    const int lpt = CAUSAL ? lpt_heads(BH, n_qtiles, WAVES, HS == 128 ? 1 : 3) : 0;
+    hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL, WAVES>),
+                       dim3(lpt > 0 ? (unsigned)(BH * n_qtiles) : xcd_grid(items)),
                        dim3(64 * WAVES), 0, stream, q, k, v, o, l, nh, T, BH, n_qtiles, sq, sk,
-                       sv, so, scale, scale * kLog2e, 8.0f / (scale * kLog2e));
+                       sv, so, scale, scale * kLog2e, 8.0f / (scale * kLog2e), nullptr, nullptr,
+                       lpt);
   };
   // Short causal heads (hs 64, T <= 512) run two waves (64 query rows) per workgroup: fewer
   // waves idle at each K/V stage's barrier along the diagonal, and the query-tile pairs balance

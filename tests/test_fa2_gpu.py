@@ -322,6 +322,56 @@ def test_fa2_dq_forms_delta(cuda, B, nh, T, hs, causal):
     np.testing.assert_allclose(f64(delta_a), (f64(O) * f64(do)).sum(-1), rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("B,nh,T,hs", [(2, 8, 1024, 64), (8, 16, 2048, 64), (2, 8, 512, 128)])
+def test_fa2_longest_first_tiles_match_pairs(cuda, B, nh, T, hs):
+    """Causal grids whose head count splits evenly over the 8 XCDs run single tiles longest
+    first where that pays (every tile resident at once, or at least 2.5 rounds of them); other
+    head counts run tile pairs (n-1-p, p).  Each tile keeps its stage order either way, so both
+    give the same bits: the full batch (longest first) against its first 7 heads run alone
+    (pairs), forward and both backward schedules, FP32 and BF16, through the C ABI."""
+    from cuda_transformer_amd import capi
+
+    q, k, v, do = (t.to(cuda) for t in _inputs(B, nh, T, hs, seed=4242, do_kind="randn"))
+    st = torch.cuda.current_stream().cuda_stream
+
+    def run(q, k, v, do):
+        b, h = q.shape[:2]
+        s4 = capi.strides(q.stride())
+        O, L = torch.empty_like(q), torch.empty(b, h, T, device=cuda)
+        capi.call("cta_flash_attention_fwd", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(), s4,
+                  b, h, T, hs, 1, O.data_ptr(), L.data_ptr(), st)
+        s3 = capi.strides(L.stride())
+        outs = [O, L]
+        ws_bytes = capi.call("cta_flash_attention_bwd_workspace", b, h, T, hs, 1)
+        ws = torch.empty(ws_bytes // 4, device=cuda)
+        for wsp, nbytes in ((ws.data_ptr(), ws_bytes), (None, 0)):  # stored dS, recompute
+            g = [torch.empty_like(q) for _ in range(3)] + [torch.empty(b, h, T, device=cuda)]
+            capi.call("cta_flash_attention_bwd", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(),
+                      s4, O.data_ptr(), s4, do.data_ptr(), s4, L.data_ptr(), s3, b, h, T, hs, 1,
+                      *(t.data_ptr() for t in g), wsp, nbytes, st)
+            outs += g[:3]
+        qh, kh, vh, doh = (t.to(torch.bfloat16) for t in (q, k, v, do))
+        Oh, Lh = torch.empty_like(qh), torch.empty(b, h, T, device=cuda)
+        capi.call("cta_flash_attention_fwd_bf16", qh.data_ptr(), s4, kh.data_ptr(), s4,
+                  vh.data_ptr(), s4, b, h, T, hs, 1, Oh.data_ptr(), Lh.data_ptr(), st)
+        outs += [Oh, Lh]
+        wsh_bytes = capi.call("cta_flash_attention_bwd_bf16_workspace", b, h, T, hs, 1)
+        wsh = torch.empty(wsh_bytes // 4 + 4, device=cuda)
+        for wsp, nbytes in ((wsh.data_ptr(), wsh_bytes), (None, 0)):
+            g = [torch.empty_like(qh) for _ in range(3)] + [torch.empty(b, h, T, device=cuda)]
+            capi.call("cta_flash_attention_bwd_bf16", qh.data_ptr(), s4, kh.data_ptr(), s4,
+                      vh.data_ptr(), s4, Oh.data_ptr(), s4, doh.data_ptr(), s4, Lh.data_ptr(), s3,
+                      b, h, T, hs, 1, *(t.data_ptr() for t in g), wsp, nbytes, st)
+            outs += g[:3]
+        return outs
+
+    full = run(q, k, v, do)
+    part = run(*(t[:1, :7].contiguous() for t in (q, k, v, do)))
+    torch.cuda.synchronize()
+    for i, (a, b_) in enumerate(zip(full, part)):
+        assert torch.equal(a[:1, :7], b_), i
+
+
 PACKED_SHAPES = [(2, 65, 3, 64, True), (1, 257, 2, 32, False), (2, 130, 2, 128, True),
                  (4, 256, 6, 64, True), (1, 1, 2, 64, True)]
 
