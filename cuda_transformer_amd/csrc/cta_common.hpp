@@ -184,24 +184,24 @@ __device__ __forceinline__ void lpt_tile(int hw_id, int heads_per_xcd, int& bh, 
   bh = x * heads_per_xcd + (slot - rank * heads_per_xcd);
 }
 
-// Heads per XCD for longest-first tiles, or 0 for pairs.  Equal pairs end a grid in a partial
-// round when their count is not a multiple of the resident workgroups, and a grid of fewer
-// pairs than resident slots leaves SIMDs at one wave.  Longest-first tiles win when each XCD
-// runs at least two and a half rounds of them (the dispatcher ends on the shortest), or when
-// all of an XCD's tiles are resident at once with two-wave workgroups or one workgroup per CU
-// (the makespan is the longest tile, n units, against n + 1 for a pair, with more SIMDs busy).
-// Between one and two and a half rounds, or with several four-wave tiles on one CU, the
-// unequal tiles that share a CU cost more than that, and pairs stay.  `waves` per workgroup,
-// `occ` waves per SIMD the kernel holds; BH must split evenly over the XCDs.
+// Heads per XCD for longest-first tiles, or 0 for pairs.  A grid of fewer pairs than resident
+// slots leaves SIMDs at one wave; when all of an XCD's single tiles fit its resident slots at
+// once, with two-wave workgroups or at most one tile per CU, they start together (so a head's
+// tiles still walk its K/V stages in step and share them in L2) and the makespan is the
+// longest tile, n units, against n + 1 for a pair, with more SIMDs busy.  Larger grids keep
+// the pairs: longest-first tiles there measured 1-2% faster in short bursts, but the tiles that
+// the dispatcher starts one by one no longer share K/V stages (L2 misses 3-4x: forward 0.65 ->
+// 2.9 GB at B4 H32 N4096), and under sustained load, which holds the chip at its power limit,
+// the gain was gone.  With several four-wave tiles on one CU the unequal tiles that share it
+// cost more than a pair.  `waves` per workgroup, `occ` waves per SIMD the kernel holds; BH must
+// split evenly over the XCDs.
 constexpr int kNumSimds = 1024;
 inline int lpt_heads(int64_t BH, int n_tiles, int waves, int occ) {
   if (BH % kNumXcds != 0 || n_tiles < 2) return 0;
   const int64_t tiles = BH / kNumXcds * n_tiles;                       // per XCD
   const int64_t slots = (int64_t)occ * (kNumSimds / kNumXcds) / waves;  // resident per XCD
   const int64_t cus = kNumSimds / kNumXcds / 4;
-  const bool many = 2 * tiles >= 5 * slots;
-  const bool one_round = tiles <= slots && (waves == 2 || tiles <= cus);
-  return many || one_round ? (int)(BH / kNumXcds) : 0;
+  return tiles <= slots && (waves == 2 || tiles <= cus) ? (int)(BH / kNumXcds) : 0;
 }
 
 // Stored dS tiles of the backward (FA2, FP32 and BF16).  Tile (ib, jb) covers query rows

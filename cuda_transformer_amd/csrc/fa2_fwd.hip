@@ -24,9 +24,9 @@
 //  * Workgroup ids are remapped so each XCD walks a contiguous run of a head-major work list:
 //    the workgroups resident on one XCD share a few heads' K/V in its L2.  With a causal mask a
 //    workgroup takes the query-tile pair (n-1-p, p), so all workgroups cost the same and the
-//    head-major order leaves no long tiles for the end; on grids where equal pairs would end in
-//    a partial round (or leave SIMDs at one wave) each XCD instead takes single tiles of its
-//    heads longest first (lpt_heads).
+//    head-major order leaves no long tiles for the end; on grids too small for the pairs to
+//    fill the resident slots each XCD instead takes single tiles of its heads longest first
+//    (lpt_heads).
 #include "cta_common.hpp"
 
 namespace cta {
@@ -378,12 +378,10 @@ int fwd_nsplit(int T, int BH) {
   return n >= 2 ? n : 1;
 }
 
-// Longest-first tiles (lpt_heads), A/B in one process against pairs (outputs within 2e-6: the
-// pairs' short tiles walk their stages downward): B4 H32 N4096 causal +1.3%, hs 32 +2.4%,
-// B8 H16 N2048 +2.5%, B64 H6 T256 +9%, B16 H8 T512 +29%; at 1.33 rounds (B1 H16 N8192,
-// B8 H32 T512) -2.5% / -3%, with 64 four-wave tiles on 32 CUs (B4 H4 N4096) -25%, which the
-// rule keeps on pairs.  The split forward, where it applies, beats both (B2 H8 N1024: 0.060 ms
-// split, 0.084 ms longest-first), so a split launch keeps the pairs.
+// Longest-first tiles (lpt_heads), A/B in one process against pairs (bitwise-equal outputs):
+// B64 H6 T256 causal +9%, B16 H8 T512 +29% (two-wave workgroups, every tile resident at once).
+// The split forward, where it applies, beats both (B2 H8 N1024: 0.060 ms split, 0.084 ms
+// longest-first), so a split launch keeps the pairs.
 
 template <int HS, bool CAUSAL>
 void launch_fwd(const float* q, const float* k, const float* v, float* o, float* l, int nh,

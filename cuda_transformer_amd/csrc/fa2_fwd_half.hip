@@ -327,10 +327,9 @@ void launch_fwd_half(const E* q, const E* k, const E* v, E* o, float* l, int nh,
                      RowStridesB sq, RowStridesB sk, RowStridesB sv, float scale,
                      hipStream_t stream) {
   const int n_qtiles = (T + 127) / 128;
-  // Longest-first tiles (lpt_heads; 109 / 161 VGPRs at hs 32 / 64: four / three waves per
-  // SIMD).  A/B in one process against pairs, bitwise-equal outputs: B4 H32 N4096 causal +5.3%
-  // at hs 64, +8.4% at hs 32, 3% slower at hs 128 (two waves per SIMD), which keeps the pairs.
-  const int lpt = CAUSAL && HS != 128 ? lpt_heads(BH, n_qtiles, 4, HS == 32 ? 4 : 3) : 0;
+  // longest-first tiles on small grids (lpt_heads); waves per SIMD the registers allow (109 /
+  // 161 / 218 VGPRs at hs 32 / 64 / 128)
+  const int lpt = CAUSAL ? lpt_heads(BH, n_qtiles, 4, HS == 32 ? 4 : HS == 64 ? 3 : 2) : 0;
   const unsigned grid = lpt > 0 ? (unsigned)(BH * n_qtiles)
                                 : xcd_grid((int64_t)(CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles) * BH);
   hipLaunchKernelGGL((fa2_fwd_half_kernel<E, HS, CAUSAL>), dim3(grid), dim3(256), 0, stream, q,
