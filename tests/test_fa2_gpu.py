@@ -327,7 +327,8 @@ def test_fa2_longest_first_tiles_match_pairs(cuda, B, nh, T, hs):
     """Small causal grids whose head count splits evenly over the 8 XCDs run single tiles
     longest first (every tile resident at once); other head counts run tile pairs (n-1-p, p).  Each tile keeps its stage order either way, so both
     give the same bits: the full batch (longest first) against its first 7 heads run alone
-    (pairs), forward and both backward schedules, FP32 and BF16, through the C ABI."""
+    (pairs), forward and both backward schedules (the stored one also over head chunks), FP32
+    and BF16, through the C ABI."""
     from cuda_transformer_amd import capi
 
     q, k, v, do = (t.to(cuda) for t in _inputs(B, nh, T, hs, seed=4242, do_kind="randn"))
@@ -343,7 +344,8 @@ def test_fa2_longest_first_tiles_match_pairs(cuda, B, nh, T, hs):
         outs = [O, L]
         ws_bytes = capi.call("cta_flash_attention_bwd_workspace", b, h, T, hs, 1)
         ws = torch.empty(ws_bytes // 4, device=cuda)
-        for wsp, nbytes in ((ws.data_ptr(), ws_bytes), (None, 0)):  # stored dS, recompute
+        # stored dS (all heads at once, then in chunks of half the heads), recompute
+        for wsp, nbytes in ((ws.data_ptr(), ws_bytes), (ws.data_ptr(), ws_bytes // 2), (None, 0)):
             g = [torch.empty_like(q) for _ in range(3)] + [torch.empty(b, h, T, device=cuda)]
             capi.call("cta_flash_attention_bwd", q.data_ptr(), s4, k.data_ptr(), s4, v.data_ptr(),
                       s4, O.data_ptr(), s4, do.data_ptr(), s4, L.data_ptr(), s3, b, h, T, hs, 1,
