@@ -299,17 +299,18 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
     const E* gt = reinterpret_cast<const E*>(base + OFF_GT);
     const float* ls = reinterpret_cast<const float*>(base + OFF_L);
     const float* ds = reinterpret_cast<const float*>(base + OFF_D);
-#pragma unroll
-    for (int k = 0; k < NSUB; ++k) {
-    // sub-tiles in the stage walk's direction, so a wave's dK / dV sums run over 32-row tiles in
-    // the same order whatever the stage height
-    const int sub = down ? NSUB - 1 - k : k;
-    const int ii0 = s_idx * BN + sub * 32;
-
-    if (live(ii0)) {
-      // S = Q K^T and dP = dO V^T: lane holds column my_j, rows ii0 + R(r, half).  The stage
-      // holds -delta, and the dP products accumulate onto it: pacc = dP - delta.
-      f32x16 sacc = zero16(), pacc;
+    // hs 128 (one wave per SIMD, nothing to hide the LDS latency behind): the A operands of
+    // dV^T += dO^T P and dK^T += Q^T dS are read before the S and dP MFMAs, so they are in
+    // registers when the exponentials finish.  A/B in one process, bitwise-equal gradients:
+    // stored-dS backward +2.3% at B4 H32 N4096 hs 128; no change at hs 32 / 64 (two waves per
+    // SIMD), which keep the reads beside their MFMAs.
+    constexpr bool PRE = HS == 128;
+    typedef vec8_t<E> AOps[HS / 32][2];
+    // S = Q K^T and dP = dO V^T of sub-tile `sub`: lane holds column my_j, rows
+    // ii0 + R(r, half).  The stage holds -delta, and the dP products accumulate onto it:
+    // pacc = dP - delta.
+    auto score = [&](int sub, f32x16& sacc, f32x16& pacc, AOps& gop, AOps& qop) {
+      sacc = zero16();
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const float4 dv = ld4(ds + sub * 32 + 8 * g + 4 * half);
@@ -318,13 +319,6 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
         pacc[4 * g + 2] = dv.z;
         pacc[4 * g + 3] = dv.w;
       }
-      // hs 128 (one wave per SIMD, nothing to hide the LDS latency behind): the A operands of
-      // dV^T += dO^T P and dK^T += Q^T dS are read here, before the S and dP MFMAs, so they are
-      // in registers when the exponentials finish.  A/B in one process, bitwise-equal gradients:
-      // stored-dS backward +2.3% at B4 H32 N4096 hs 128; no change at hs 32 / 64 (two waves per
-      // SIMD), which keep the reads beside their MFMAs.
-      constexpr bool PRE = HS == 128;
-      vec8_t<E> gop[HS / 32][2], qop[HS / 32][2];
       if constexpr (PRE) {
 #pragma unroll
         for (int d = 0; d < HS / 32; ++d)
@@ -344,7 +338,10 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * QS + 4 * (HS / 32), 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 2 * QS, 0);
       }
-
+    };
+    // P, dV, dS and dK of sub-tile `sub` (query rows ii0..) from its S and dP - delta.
+    auto finish = [&](int sub, int ii0, f32x16& sacc, const f32x16& pacc, const AOps& gop,
+                      const AOps& qop) {
       // P = e^{S - L}; masked entries (and, for the stored dS, key rows past T) are exactly 0.
       // The stage holds L log2(e).  Two explicit paths: left to the compiler, the masked form
       // is if-converted into per-element selects that every tile then pays for.
@@ -412,9 +409,21 @@ __global__ __launch_bounds__(64 * WAVES, MINW) void fa2_bwd_dkdv_half_kernel(
           dkacc[d] = Half16<E>::mfma(
               PRE ? qop[d][s] : ld8<E>(qt + (d * 32 + col) * TP + sub * 32 + 16 * s + 8 * half),
               db[s], dkacc[d]);
-    }
-    }  // sub-tiles
+    };
 
+    // Sub-tiles in the stage walk's direction, so a wave's dK / dV sums run over 32-row tiles
+    // in the same order whatever the stage height.
+#pragma unroll
+    for (int k = 0; k < NSUB; ++k) {
+      const int sub = down ? NSUB - 1 - k : k;
+      const int ii0 = s_idx * BN + sub * 32;
+      if (live(ii0)) {
+        f32x16 sacc, pacc;
+        AOps gop, qop;
+        score(sub, sacc, pacc, gop, qop);
+        finish(sub, ii0, sacc, pacc, gop, qop);
+      }
+    }  // sub-tiles
     if (i + 1 < n_steps) lstore(buf ^ 1);
     __syncthreads();
   }
