@@ -410,6 +410,10 @@ void launch_fwd(const float* q, const float* k, const float* v, float* o, float*
       split.template operator()<2>();
       return;
     }
+    // Slots counted at three waves per SIMD for hs 32 / 64 (the four-wave kernel's 160 VGPRs
+    // hold three; the two-wave one's 186 hold two, but measured, its longest-first tiles win at
+    // B64 H6 T256, 1.5 rounds of them at two waves, +9%, and lose at B8 H32 T512, 2 rounds, -3%,
+    // which the three-wave count separates).
     const int lpt = CAUSAL ? lpt_heads(BH, n_qtiles, WAVES, HS == 128 ? 1 : 3) : 0;
     hipLaunchKernelGGL((fa2_fwd_kernel<HS, CAUSAL, WAVES>),
                        dim3(lpt > 0 ? (unsigned)(BH * n_qtiles) : xcd_grid(items)),
