@@ -504,11 +504,12 @@ def fa2_half_workload(args, kind):
     non-causal: forward (cta_flash_attention_fwd_<kind>) and backward
     (cta_flash_attention_bwd_<kind>) in both schedules, recompute (no workspace: dQ recomputing
     S and dP and forming delta, then dK/dV) and stored dS (delta, dK/dV storing 16-bit dS, dQ from
-    dS), each
-    timed with HIP events on torch's current stream with inputs in HBM.  `value` is the step
-    with the schedule the operator runs (recompute at hs 32 and 64, stored at hs 128).  TFLOPS
-    by the reference's formula (forward 4*B*H*N^2*D, halved when causal; backward 2.5x),
-    against the 2.5 PFLOP/s dense BF16/FP16 MFMA peak.  One JSON line per mask."""
+    dS).  Each schedule is timed as whole steps [fwd, bwd] back to back on torch's current stream
+    with inputs in HBM, HIP events around each launch, like the FP32 headline.  `value` is the
+    wall-clock step rate with the schedule the operator runs (recompute at hs 32 and 64, stored
+    at hs 128).  TFLOPS by the reference's formula (forward 4*B*H*N^2*D, halved when causal;
+    backward 2.5x), against the 2.5 PFLOP/s dense BF16/FP16 MFMA peak.  One JSON line per
+    mask."""
     import torch
 
     from cuda_transformer_amd import capi
@@ -546,15 +547,19 @@ def fa2_half_workload(args, kind):
                       N, D, int(causal), vp(dq), vp(dk), vp(dv), vp(delta),
                       vp(ws) if stored else None, ws_bytes if stored else 0, st) != 0:
                 raise RuntimeError(lib.cta_last_error().decode())
-        fwd_ms = _time_kernel(fwd, max(10, args.steps), warm_s=args.warm_seconds)
-        fwd()
-        bwd_ms = {sch: _time_kernel(lambda: bwd(sch == "stored"), max(10, args.steps),
-                                    warm_s=0.2)
-                  for sch in ("recompute", "stored")}
+        # whole steps [fwd, bwd] per schedule, the operator's schedule first, timed as the FP32
+        # headline is: the forward runs between backwards, as in training
+        timed = {}
+        for sch in (default, "stored" if default == "recompute" else "recompute"):
+            timed[sch] = _time_steps(
+                [("fwd", fwd), ("bwd", lambda sch=sch: bwd(sch == "stored"))],
+                max(10, args.steps), args.warm_seconds)
+        fwd_ms = timed[default][1]["fwd"]
+        bwd_ms = {sch: t[1]["bwd"] for sch, t in timed.items()}
         fl, bfl = attn_flops(B, H, N, D, causal)
         ftf = fl / (fwd_ms * 1e-3) / 1e12
         btf = {sch: bfl / (ms * 1e-3) / 1e12 for sch, ms in bwd_ms.items()}
-        stf = {sch: (fl + bfl) / ((fwd_ms + ms) * 1e-3) / 1e12 for sch, ms in bwd_ms.items()}
+        stf = {sch: (fl + bfl) / (t[0] * 1e-3) / 1e12 for sch, t in timed.items()}
         print(json.dumps({
             "workload": f"FA2 {kind.upper()} fwd+bwd B{B} H{H} N{N} D{D} "
                         f"{'causal' if causal else 'non-causal'}",
@@ -562,7 +567,10 @@ def fa2_half_workload(args, kind):
             "unit": "TFLOPS", "bwd_schedule": default,
             "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms[default], 4),
             "fwd_tflops": round(ftf, 2), "bwd_tflops": round(btf[default], 2),
-            "schedules": {sch: {"bwd_ms": round(bwd_ms[sch], 4), "bwd_tflops": round(btf[sch], 2),
+            "ms_per_step": round(timed[default][0], 4),
+            "schedules": {sch: {"fwd_ms": round(timed[sch][1]["fwd"], 4),
+                                "bwd_ms": round(bwd_ms[sch], 4), "bwd_tflops": round(btf[sch], 2),
+                                "ms_per_step": round(timed[sch][0], 4),
                                 "step_tflops": round(stf[sch], 2),
                                 "ds_workspace_bytes": ws_bytes if sch == "stored" else 0}
                           for sch in bwd_ms},
@@ -604,6 +612,37 @@ def _time_kernel(fn, reps, warm_s=0.02, flush=None):
         b.record(stream)
     torch.cuda.synchronize()
     return statistics.median(a.elapsed_time(b) for a, b in evs)
+
+
+def _time_steps(kernels, steps, warm_s):
+    """Whole steps of `kernels` ([(name, fn), ...], launched in order) back to back on torch's
+    current stream: at least warm_s of untimed steps, then `steps` timed ones with HIP events
+    around each kernel.  Returns (wall-clock ms per timed step, {name: mean event ms})."""
+    import torch
+
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(2):
+            for _, fn in kernels:
+                fn()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= warm_s:
+            break
+    stream = torch.cuda.current_stream()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(kernels) + 1)]
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for e in evs:
+        for j, (_, fn) in enumerate(kernels):
+            e[j].record(stream)
+            fn()
+        e[len(kernels)].record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t1) * 1e3 / steps
+    per = {name: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps
+           for j, (name, _) in enumerate(kernels)}
+    return wall, per
 
 
 def _time_rotating(fn, copies, reps, warm_s=0.02):
